@@ -1,0 +1,223 @@
+#ifndef AIGPU_ATTENTION_H
+#define AIGPU_ATTENTION_H
+
+/*
+    aigpu_attention.h - the C ABI of the MI355X (gfx950) attention backend.
+
+    Same conventions as the reference's device boundary
+    (include/ai/gpu/DeviceABI.h in hday200202/math-utils):
+      - plain C symbols with the aigpu_ prefix; scalars, pointers and POD
+        structs only; structs go in by pointer, never by value
+        (DeviceABI.h:59-65);
+      - strings are borrowed from the backend (DeviceABI.h:79-83);
+      - the allocator frees: device memory comes from aigpu_upload /
+        aigpu_allocate and goes back through aigpu_release
+        (DeviceABI.h:89-99);
+      - every entry returns 1 on success and 0 on failure with the reason in
+        aigpu_last_error(); aigpu_available() is safe to call first
+        (DeviceABI.h:75-77);
+      - calls are serialised on one process-wide lock, as the reference
+        backend's Context::gate does (src/gpu/Kernels.hip:48-63);
+      - AiGpuCounters separate kernel time from transfer time
+        (DeviceABI.h:66-72).
+
+    The attention entries replace these CPU call sites of the reference:
+      kernels::attention     include/ai/Kernels.hpp:132-134, called at
+                             include/ai/LocalModel.hpp:2657-2659
+      norm -> RoPE -> append -> attention of attentionMixer
+                             include/ai/LocalModel.hpp:2608-2659
+      the per-token deltaStep loop of gatedDeltaNetMixer
+                             include/ai/LocalModel.hpp:2802-2830 (deltaStep at
+                             include/ai/Kernels.hpp:105-128)
+
+    Layouts. Host-side tensors keep the reference's layouts: q
+    [count][heads][qStride], k/v [count][kvHeads][dim], out
+    [count][heads][dim] (Kernels.hpp:143-154). The device KV cache is
+    head-major bf16: [kvHeads][capacity][dim] per sequence, so each KV head's
+    history is one contiguous run in HBM.
+*/
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(_WIN32)
+#define AIGPU_ABI __declspec(dllexport)
+#else
+#define AIGPU_ABI __attribute__((visibility("default")))
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of tensors crossing the boundary */
+enum { AIGPU_F32 = 0, AIGPU_BF16 = 1 };
+
+/* DeviceABI.h:66-72 */
+typedef struct AiGpuCounters {
+    uint64_t launches;
+    uint64_t hostToDeviceBytes;
+    uint64_t deviceToHostBytes;
+    double kernelSeconds;
+    double transferSeconds;
+} AiGpuCounters;
+
+/* ---- device entry points, as DeviceABI.h:75-118 ---- */
+AIGPU_ABI int aigpu_available(void);                               /* DeviceABI.h:77 */
+AIGPU_ABI const char* aigpu_device_name(void);                     /* DeviceABI.h:82 */
+AIGPU_ABI const char* aigpu_last_error(void);                      /* DeviceABI.h:83 */
+AIGPU_ABI uint64_t aigpu_total_memory(void);                       /* DeviceABI.h:85 */
+AIGPU_ABI uint64_t aigpu_free_memory(void);                        /* DeviceABI.h:86 */
+AIGPU_ABI uint64_t aigpu_allocated_bytes(void);                    /* DeviceABI.h:87 */
+AIGPU_ABI void* aigpu_upload(const void* host, uint64_t bytes);    /* DeviceABI.h:97 */
+AIGPU_ABI void aigpu_release(void* device, uint64_t bytes);        /* DeviceABI.h:98 */
+AIGPU_ABI int aigpu_download(void* host, const void* device, uint64_t bytes); /* DeviceABI.h:99 */
+AIGPU_ABI void aigpu_synchronize(void);                            /* DeviceABI.h:115 */
+AIGPU_ABI void aigpu_counters(AiGpuCounters* out);                 /* DeviceABI.h:117 */
+AIGPU_ABI void aigpu_reset_counters(void);                         /* DeviceABI.h:118 */
+
+/* New beside aigpu_upload: a zero-filled device allocation (KV caches,
+   recurrent states) released by aigpu_release, and a host->device copy into
+   an existing allocation at a byte offset. */
+AIGPU_ABI void* aigpu_allocate(uint64_t bytes);
+AIGPU_ABI int aigpu_write(void* device, uint64_t offset, const void* host, uint64_t bytes);
+
+/* ------------------------------------------------------------------------ */
+/* 1. Drop-in for kernels::attention (Kernels.hpp:132-134).                  */
+/*    Host pointers, fp32, the reference's position-major KV                 */
+/*    [pos][kvHeads][dim]; same argument list and meaning. Staged in,         */
+/*    computed in fp32 on the GPU, copied back. Replaces the call at          */
+/*    LocalModel.hpp:2657-2659 line for line.                                 */
+/* ------------------------------------------------------------------------ */
+AIGPU_ABI int aigpu_attention(const float* q, const float* keys, const float* values,
+                              float* out, uint64_t count, uint64_t start, uint64_t heads,
+                              uint64_t kvHeads, uint64_t dim, uint64_t qStride,
+                              uint64_t window);
+
+/* 2. The same computation on device pointers, with a dtype tag for q and for
+      the KV history and explicit KV element strides, so one entry serves the
+      reference's position-major layout (posStride = kvHeads*dim,
+      headStride = dim) and the head-major cache (posStride = dim,
+      headStride = capacity*dim). fp32 arithmetic; out is fp32. */
+typedef struct AiGpuAttention {
+    const void* q;            /* [count][heads][qStride], qType */
+    const void* keys;         /* kvType, element (pos, head) at pos*posStride + head*headStride */
+    const void* values;
+    float* out;               /* [count][heads][dim] */
+    uint32_t qType, kvType;
+    uint64_t count, start, heads, kvHeads, dim, qStride, window;
+    uint64_t posStride, headStride;
+    void* stream;             /* hipStream_t; NULL = default stream */
+} AiGpuAttention;
+AIGPU_ABI int aigpu_attention_device(const AiGpuAttention* args);
+
+/* ------------------------------------------------------------------------ */
+/* 3. Prefill: attentionMixer's QK-RMSNorm -> RoPE -> KV append -> causal    */
+/*    attention (LocalModel.hpp:2608-2659) for `count` new tokens at          */
+/*    positions start..start+count-1, against a head-major bf16 cache that    */
+/*    already holds positions [0, start). Flash-style kernel on fp16 MFMA     */
+/*    with fp32 accumulation. dim must be 64 or 128.                          */
+/* ------------------------------------------------------------------------ */
+typedef struct AiGpuPrefill {
+    const void* q;            /* [count][heads][qStride], inType */
+    const void* k;            /* [count][kvHeads][dim], inType */
+    const void* v;            /* [count][kvHeads][dim], inType */
+    float* out;               /* [count][heads][dim] fp32 */
+    void* keyCache;           /* bf16 [kvHeads][capacity][dim] */
+    void* valueCache;         /* bf16 [kvHeads][capacity][dim] */
+    const float* qNorm;       /* [dim] gamma, NULL = no QK-norm (LocalModel.hpp:2609-2617) */
+    const float* kNorm;       /* [dim] gamma, NULL = no QK-norm */
+    const float* rotaryFrequencies; /* [rotaryDims/2] (LocalModel.hpp:807-820); NULL = no RoPE */
+    float epsilon;            /* cfg.normEps */
+    float normOffset;         /* spec.normWeightOffset (0 for qwen3) */
+    uint32_t rotaryDims;
+    uint32_t inType;
+    uint64_t count, start, heads, kvHeads, dim, qStride, window, capacity;
+    void* stream;
+} AiGpuPrefill;
+/* device pointers throughout */
+AIGPU_ABI int aigpu_prefill_attention(const AiGpuPrefill* args);
+/* q, k, v, out, qNorm, kNorm, rotaryFrequencies are host pointers (fp32 or
+   bf16 per inType); the caches are device allocations. Staged in and out. */
+AIGPU_ABI int aigpu_prefill_attention_host(const AiGpuPrefill* args);
+
+/* ------------------------------------------------------------------------ */
+/* 4. Decode: one new token for each of `batch` sequences with ragged         */
+/*    cached lengths. The new q and k get QK-RMSNorm and RoPE at position     */
+/*    positions[b] inside the kernel ("on load"); the new k, v are appended   */
+/*    to sequence b's cache at positions[b]; attention covers positions       */
+/*    [first, positions[b]] (first from the window as Kernels.hpp:142).       */
+/*    For batch 1 this is exactly attentionMixer with count = 1. Split-K,     */
+/*    HBM-bound kernel; heads/kvHeads must be 1..8 and dim 64 or 128.         */
+/* ------------------------------------------------------------------------ */
+typedef struct AiGpuDecode {
+    const void* q;            /* [batch][heads][qStride], inType */
+    const void* k;            /* [batch][kvHeads][dim], inType */
+    const void* v;            /* [batch][kvHeads][dim], inType */
+    float* out;               /* [batch][heads][dim] fp32 */
+    void* keyCache;           /* bf16, sequence b at b*batchStride: [kvHeads][capacity][dim] */
+    void* valueCache;
+    const uint32_t* positions;/* [batch] cached length of each sequence = new token position */
+    const float* qNorm;
+    const float* kNorm;
+    const float* rotaryFrequencies;
+    float epsilon;
+    float normOffset;
+    uint32_t rotaryDims;
+    uint32_t inType;
+    uint32_t maxPosition;     /* >= every positions[b]; sizes the launch */
+    uint32_t reserved;
+    uint64_t batch, heads, kvHeads, dim, qStride, window, capacity;
+    uint64_t batchStride;     /* elements between sequences' caches; 0 = kvHeads*capacity*dim */
+    void* stream;
+} AiGpuDecode;
+AIGPU_ABI int aigpu_decode_attention(const AiGpuDecode* args);
+/* q, k, v, out, positions, qNorm, kNorm, rotaryFrequencies are host
+   pointers; the caches are device allocations. */
+AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode* args);
+
+/* ------------------------------------------------------------------------ */
+/* 5. Gated delta rule over a token range (the recurrence of                  */
+/*    gatedDeltaNetMixer, LocalModel.hpp:2802-2830): for each token t and     */
+/*    value head h (key head h / (valueHeads/keyHeads)):                      */
+/*      S *= exp(g); delta = beta*(v - S^T k); S += k delta^T; out = S^T q    */
+/*    computed as a chunked scan (WY form) with fp32 state.                   */
+/* ------------------------------------------------------------------------ */
+typedef struct AiGpuDeltaRule {
+    const void* q;            /* [count][keyHeads][keyDim], inType */
+    const void* k;            /* [count][keyHeads][keyDim], inType */
+    const void* v;            /* [count][valueHeads][valueDim], inType */
+    const float* g;           /* [count][valueHeads] log decay (used when aLog is NULL) */
+    const float* beta;        /* [count][valueHeads] (used when aLog is NULL) */
+    const float* a;           /* raw gate inputs [count][valueHeads] (used when aLog is set): */
+    const float* b;           /*   g = -exp(aLog[h])*softplus(a + dtBias[h]), beta = sigmoid(b) */
+    const float* aLog;        /* [valueHeads] (LocalModel.hpp:2820-2823) */
+    const float* dtBias;      /* [valueHeads] */
+    float* state;             /* [valueHeads][keyDim][valueDim] fp32, in/out */
+    float* out;               /* [count][valueHeads][valueDim] fp32 */
+    uint32_t inType;
+    uint32_t normalize;       /* 1: l2normalise q,k (eps 1e-6) and q *= 1/sqrt(keyDim) */
+    uint32_t chunk;           /* 64 (0 = 64) */
+    uint32_t reserved;
+    uint64_t count, keyHeads, valueHeads, keyDim, valueDim;
+    void* stream;
+} AiGpuDeltaRule;
+AIGPU_ABI int aigpu_gated_delta_rule(const AiGpuDeltaRule* args);
+/* every tensor a host pointer; state updated in place on the host */
+AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule* args);
+
+/* ------------------------------------------------------------------------ */
+/* Per-kernel timing. With profiling on, every launch is bracketed by a pair */
+/* of hipEvents on the stream it runs on; aigpu_profile_read synchronises    */
+/* and reports the summed device time and launch count of kernels whose name */
+/* contains `kernel` since the last reset.                                   */
+/* ------------------------------------------------------------------------ */
+AIGPU_ABI void aigpu_profile(int enable);
+AIGPU_ABI int aigpu_profile_read(const char* kernel, double* milliseconds, uint64_t* launches);
+AIGPU_ABI void aigpu_profile_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AIGPU_ATTENTION_H */

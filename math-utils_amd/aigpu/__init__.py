@@ -1,0 +1,291 @@
+"""aigpu - Python binding of the MI355X attention backend's C ABI
+(include/aigpu_attention.h), loaded from the in-tree libaigpu.so.
+
+The binding is thin on purpose: every call goes through an extern "C" entry
+point; PyTorch only provides device memory and the stream. Loading fails
+loudly when the HIP library is missing - there is no CPU fallback here.
+
+Host forms (numpy in, numpy out) mirror the reference's CPU call sites:
+    attention(...)          kernels::attention (Kernels.hpp:132-134)
+Device forms (torch tensors on the GPU):
+    attention_device(...)   fp32 attention over any KV layout
+    prefill(...)            attentionMixer norm -> RoPE -> append -> attention
+    decode(...)             batched ragged decode with norm/RoPE on load
+    gated_delta_rule(...)   gatedDeltaNetMixer recurrence (chunked scan)
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "libaigpu.so")
+STUB = os.path.join(HERE, "libaigpu_stub.so")
+
+F32, BF16 = 0, 1
+
+_vp, _u32, _u64, _f32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_float
+
+
+class AiGpuCounters(C.Structure):
+    _fields_ = [("launches", _u64), ("hostToDeviceBytes", _u64), ("deviceToHostBytes", _u64),
+                ("kernelSeconds", C.c_double), ("transferSeconds", C.c_double)]
+
+
+class AiGpuAttention(C.Structure):
+    _fields_ = [("q", _vp), ("keys", _vp), ("values", _vp), ("out", _vp),
+                ("qType", _u32), ("kvType", _u32),
+                ("count", _u64), ("start", _u64), ("heads", _u64), ("kvHeads", _u64),
+                ("dim", _u64), ("qStride", _u64), ("window", _u64),
+                ("posStride", _u64), ("headStride", _u64), ("stream", _vp)]
+
+
+class AiGpuPrefill(C.Structure):
+    _fields_ = [("q", _vp), ("k", _vp), ("v", _vp), ("out", _vp),
+                ("keyCache", _vp), ("valueCache", _vp),
+                ("qNorm", _vp), ("kNorm", _vp), ("rotaryFrequencies", _vp),
+                ("epsilon", _f32), ("normOffset", _f32), ("rotaryDims", _u32), ("inType", _u32),
+                ("count", _u64), ("start", _u64), ("heads", _u64), ("kvHeads", _u64),
+                ("dim", _u64), ("qStride", _u64), ("window", _u64), ("capacity", _u64),
+                ("stream", _vp)]
+
+
+class AiGpuDecode(C.Structure):
+    _fields_ = [("q", _vp), ("k", _vp), ("v", _vp), ("out", _vp),
+                ("keyCache", _vp), ("valueCache", _vp), ("positions", _vp),
+                ("qNorm", _vp), ("kNorm", _vp), ("rotaryFrequencies", _vp),
+                ("epsilon", _f32), ("normOffset", _f32), ("rotaryDims", _u32), ("inType", _u32),
+                ("maxPosition", _u32), ("reserved", _u32),
+                ("batch", _u64), ("heads", _u64), ("kvHeads", _u64), ("dim", _u64),
+                ("qStride", _u64), ("window", _u64), ("capacity", _u64), ("batchStride", _u64),
+                ("stream", _vp)]
+
+
+class AiGpuDeltaRule(C.Structure):
+    _fields_ = [("q", _vp), ("k", _vp), ("v", _vp), ("g", _vp), ("beta", _vp),
+                ("a", _vp), ("b", _vp), ("aLog", _vp), ("dtBias", _vp),
+                ("state", _vp), ("out", _vp),
+                ("inType", _u32), ("normalize", _u32), ("chunk", _u32), ("reserved", _u32),
+                ("count", _u64), ("keyHeads", _u64), ("valueHeads", _u64), ("keyDim", _u64),
+                ("valueDim", _u64), ("stream", _vp)]
+
+
+# every symbol include/aigpu_attention.h declares, with its signature
+SIGNATURES = {
+    "aigpu_available": (C.c_int, []),
+    "aigpu_device_name": (C.c_char_p, []),
+    "aigpu_last_error": (C.c_char_p, []),
+    "aigpu_total_memory": (_u64, []),
+    "aigpu_free_memory": (_u64, []),
+    "aigpu_allocated_bytes": (_u64, []),
+    "aigpu_upload": (_vp, [_vp, _u64]),
+    "aigpu_release": (None, [_vp, _u64]),
+    "aigpu_download": (C.c_int, [_vp, _vp, _u64]),
+    "aigpu_synchronize": (None, []),
+    "aigpu_counters": (None, [C.POINTER(AiGpuCounters)]),
+    "aigpu_reset_counters": (None, []),
+    "aigpu_allocate": (_vp, [_u64]),
+    "aigpu_write": (C.c_int, [_vp, _u64, _vp, _u64]),
+    "aigpu_attention": (C.c_int, [_vp, _vp, _vp, _vp] + [_u64] * 7),
+    "aigpu_attention_device": (C.c_int, [C.POINTER(AiGpuAttention)]),
+    "aigpu_prefill_attention": (C.c_int, [C.POINTER(AiGpuPrefill)]),
+    "aigpu_prefill_attention_host": (C.c_int, [C.POINTER(AiGpuPrefill)]),
+    "aigpu_decode_attention": (C.c_int, [C.POINTER(AiGpuDecode)]),
+    "aigpu_decode_attention_host": (C.c_int, [C.POINTER(AiGpuDecode)]),
+    "aigpu_gated_delta_rule": (C.c_int, [C.POINTER(AiGpuDeltaRule)]),
+    "aigpu_gated_delta_rule_host": (C.c_int, [C.POINTER(AiGpuDeltaRule)]),
+    "aigpu_profile": (None, [C.c_int]),
+    "aigpu_profile_read": (C.c_int, [C.c_char_p, C.POINTER(C.c_double), C.POINTER(_u64)]),
+    "aigpu_profile_reset": (None, []),
+}
+
+
+def load_library(path):
+    """Loads a backend (.so) and declares every ABI symbol on it."""
+    lib = C.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBRARY):
+            raise ImportError(f"HIP backend not built: {LIBRARY} is missing "
+                              "(run python math-utils_amd/build.py)")
+        _lib = load_library(LIBRARY)
+    return _lib
+
+
+class AiGpuError(RuntimeError):
+    pass
+
+
+def _check(ok):
+    if not ok:
+        raise AiGpuError(last_error())
+
+
+def available():
+    return bool(lib().aigpu_available())
+
+
+def device_name():
+    return lib().aigpu_device_name().decode()
+
+
+def last_error():
+    return lib().aigpu_last_error().decode()
+
+
+def require():
+    """Raises unless a gfx950 device is usable: the product has no CPU path."""
+    if not available():
+        raise AiGpuError("no usable gfx950 device: " + last_error())
+
+
+def counters():
+    c = AiGpuCounters()
+    lib().aigpu_counters(C.byref(c))
+    return {k: getattr(c, k) for k, _ in AiGpuCounters._fields_}
+
+
+def profile(enable=True):
+    lib().aigpu_profile(1 if enable else 0)
+
+
+def profile_reset():
+    lib().aigpu_profile_reset()
+
+
+def profile_read(kernel=None):
+    """(total milliseconds, launches) of kernels whose name contains `kernel`."""
+    ms, n = C.c_double(), _u64()
+    lib().aigpu_profile_read(None if kernel is None else kernel.encode(), C.byref(ms), C.byref(n))
+    return ms.value, n.value
+
+
+# ------------------------------------------------------------------ helpers
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is not None:
+        return C.c_void_p(stream)
+    import torch
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dtype_tag(t):
+    import torch
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.bfloat16:
+        return BF16
+    raise TypeError(f"unsupported dtype {t.dtype}: float32 or bfloat16")
+
+
+def _need(t, name, device=True):
+    import torch
+    if t is None:
+        return
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if device and not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+# ---------------------------------------------------------------- 1. host
+def attention(q, keys, values, count, start, heads, kv_heads, dim, q_stride, window=0):
+    """Drop-in for kernels::attention: numpy fp32 in the reference's layouts,
+    returns out [count][heads][dim]."""
+    q = np.ascontiguousarray(q, np.float32)
+    keys = np.ascontiguousarray(keys, np.float32)
+    values = np.ascontiguousarray(values, np.float32)
+    out = np.empty((count, heads, dim), np.float32)
+    _check(lib().aigpu_attention(q.ctypes.data, keys.ctypes.data, values.ctypes.data,
+                                 out.ctypes.data, count, start, heads, kv_heads, dim, q_stride,
+                                 window))
+    return out
+
+
+# -------------------------------------------------------------- 2. device
+def attention_device(q, keys, values, out, count, start, heads, kv_heads, dim, q_stride,
+                     pos_stride, head_stride, window=0, stream=None):
+    for t, n in ((q, "q"), (keys, "keys"), (values, "values"), (out, "out")):
+        _need(t, n)
+    a = AiGpuAttention(q=_ptr(q), keys=_ptr(keys), values=_ptr(values), out=_ptr(out),
+                       qType=_dtype_tag(q), kvType=_dtype_tag(keys), count=count, start=start,
+                       heads=heads, kvHeads=kv_heads, dim=dim, qStride=q_stride, window=window,
+                       posStride=pos_stride, headStride=head_stride, stream=_stream(stream))
+    _check(lib().aigpu_attention_device(C.byref(a)))
+    return out
+
+
+def prefill(q, k, v, out, key_cache, value_cache, start, heads, kv_heads, dim, q_stride=None,
+            q_norm=None, k_norm=None, eps=1e-6, norm_offset=0.0, freqs=None, rotary_dims=0,
+            window=0, capacity=None, stream=None):
+    """Device form of attentionMixer for `count` tokens at positions start.."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out"), (key_cache, "key_cache"),
+                 (value_cache, "value_cache"), (q_norm, "q_norm"), (k_norm, "k_norm"),
+                 (freqs, "freqs")):
+        _need(t, n)
+    count = q.shape[0]
+    cap = capacity if capacity is not None else key_cache.shape[-2]
+    a = AiGpuPrefill(q=_ptr(q), k=_ptr(k), v=_ptr(v), out=_ptr(out), keyCache=_ptr(key_cache),
+                     valueCache=_ptr(value_cache), qNorm=_ptr(q_norm), kNorm=_ptr(k_norm),
+                     rotaryFrequencies=_ptr(freqs), epsilon=eps, normOffset=norm_offset,
+                     rotaryDims=rotary_dims if freqs is not None else 0, inType=_dtype_tag(q),
+                     count=count, start=start, heads=heads, kvHeads=kv_heads, dim=dim,
+                     qStride=q_stride or dim, window=window, capacity=cap,
+                     stream=_stream(stream))
+    _check(lib().aigpu_prefill_attention(C.byref(a)))
+    return out
+
+
+def decode(q, k, v, out, key_cache, value_cache, positions, max_position, heads, kv_heads, dim,
+           q_stride=None, q_norm=None, k_norm=None, eps=1e-6, norm_offset=0.0, freqs=None,
+           rotary_dims=0, window=0, capacity=None, batch_stride=0, stream=None):
+    """Device form of the batched decode; positions is a uint32/int32 GPU tensor."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out"), (key_cache, "key_cache"),
+                 (value_cache, "value_cache"), (positions, "positions"), (q_norm, "q_norm"),
+                 (k_norm, "k_norm"), (freqs, "freqs")):
+        _need(t, n)
+    batch = q.shape[0]
+    cap = capacity if capacity is not None else key_cache.shape[-2]
+    a = AiGpuDecode(q=_ptr(q), k=_ptr(k), v=_ptr(v), out=_ptr(out), keyCache=_ptr(key_cache),
+                    valueCache=_ptr(value_cache), positions=_ptr(positions), qNorm=_ptr(q_norm),
+                    kNorm=_ptr(k_norm), rotaryFrequencies=_ptr(freqs), epsilon=eps,
+                    normOffset=norm_offset, rotaryDims=rotary_dims if freqs is not None else 0,
+                    inType=_dtype_tag(q), maxPosition=max_position, batch=batch, heads=heads,
+                    kvHeads=kv_heads, dim=dim, qStride=q_stride or dim, window=window,
+                    capacity=cap, batchStride=batch_stride, stream=_stream(stream))
+    _check(lib().aigpu_decode_attention(C.byref(a)))
+    return out
+
+
+def gated_delta_rule(q, k, v, state, out, g=None, beta=None, a=None, b=None, a_log=None,
+                     dt_bias=None, normalize=True, stream=None):
+    """Device form of the gatedDeltaNetMixer recurrence; state updated in place."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (state, "state"), (out, "out"), (g, "g"),
+                 (beta, "beta"), (a, "a"), (b, "b"), (a_log, "a_log"), (dt_bias, "dt_bias")):
+        _need(t, n)
+    count, key_heads, key_dim = q.shape
+    _, value_heads, value_dim = v.shape
+    args = AiGpuDeltaRule(q=_ptr(q), k=_ptr(k), v=_ptr(v), g=_ptr(g), beta=_ptr(beta),
+                          a=_ptr(a), b=_ptr(b), aLog=_ptr(a_log), dtBias=_ptr(dt_bias),
+                          state=_ptr(state), out=_ptr(out), inType=_dtype_tag(q),
+                          normalize=1 if normalize else 0, chunk=64, count=count,
+                          keyHeads=key_heads, valueHeads=value_heads, keyDim=key_dim,
+                          valueDim=value_dim, stream=_stream(stream))
+    _check(lib().aigpu_gated_delta_rule(C.byref(args)))
+    return out

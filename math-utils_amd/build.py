@@ -1,0 +1,65 @@
+"""build.py - compiles the gfx950 attention backend in-tree.
+
+    python math-utils_amd/build.py          # libaigpu.so + libaigpu_stub.so
+
+Outputs (git-ignored, shipped to the GPU box with the tree):
+    math-utils_amd/aigpu/libaigpu.so        the HIP backend (hipcc, gfx950)
+    math-utils_amd/aigpu/libaigpu_stub.so   the no-device backend (g++)
+Objects go to math-utils_amd/_build/.
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "aigpu")
+OBJ = os.path.join(HERE, "_build")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+SOURCES = ["abi.hip", "attention_f32.hip", "prefill.hip", "decode.hip", "delta_rule.hip"]
+
+# packed-fp32 instructions off; gfx950 only; only AIGPU_ABI symbols exported
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-but-set-variable",
+]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature; that note is harmless
+    noise = "'-packed-fp32-ops' is not a recognized feature for this target (ignoring feature)"
+    err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed: {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build(verbose=False, jobs=4):
+    os.makedirs(OBJ, exist_ok=True)
+
+    def compile_one(src):
+        obj = os.path.join(OBJ, src.replace(".hip", ".o"))
+        msg = _run([HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj])
+        if verbose and msg.strip():
+            print(msg, file=sys.stderr)
+        return obj
+
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(compile_one, SOURCES))
+    lib = os.path.join(OUT, "libaigpu.so")
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", lib + ".tmp"] + objs)
+    os.replace(lib + ".tmp", lib)
+
+    stub = os.path.join(OUT, "libaigpu_stub.so")
+    _run(["g++", "-std=c++17", "-O2", "-shared", "-fPIC", "-fvisibility=hidden", "-o", stub,
+          os.path.join(CSRC, "stub.cpp")])
+    return lib, stub
+
+
+if __name__ == "__main__":
+    for path in build(verbose=True):
+        print(path)

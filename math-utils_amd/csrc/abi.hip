@@ -1,0 +1,559 @@
+// abi.hip - the extern "C" entry points of include/aigpu_attention.h and the
+// process-wide Context behind them.
+//
+// Host forms stage their host tensors into device scratch, launch, and copy
+// the results back, timing kernels and transfers apart as the reference's
+// dispatch does (src/gpu/Kernels.hip:387-426). Device forms launch on the
+// caller's stream and return without synchronising.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstring>
+#include <string>
+
+#include "context.hpp"
+#include "kernels.hpp"
+
+namespace aigpu {
+
+using Clock = std::chrono::steady_clock;
+
+static double since(Clock::time_point t) {
+    return std::chrono::duration<double>(Clock::now() - t).count();
+}
+
+Context& Context::instance() {
+    static Context ctx;
+    return ctx;
+}
+
+Context::Context() {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+        (void)hipGetLastError();
+        error = "no HIP device found";
+        return;
+    }
+    if (hipSetDevice(0) != hipSuccess) {
+        error = "hipSetDevice(0) failed";
+        return;
+    }
+    hipDeviceProp_t props{};
+    if (hipGetDeviceProperties(&props, 0) != hipSuccess) {
+        error = "hipGetDeviceProperties failed";
+        return;
+    }
+    if (std::strncmp(props.gcnArchName, "gfx950", 6) != 0) {
+        error = std::string("this backend is built for gfx950, found ") + props.gcnArchName;
+        return;
+    }
+    name = props.name;
+    ok = true;
+}
+
+Context::~Context() {
+    // process teardown: the runtime reclaims device memory itself
+}
+
+void* Context::grow(ScratchSlot slot, size_t bytes) {
+    if (bytes == 0) bytes = 256;
+    if (scratchBytes[slot] >= bytes) return scratch[slot];
+    if (scratch[slot]) {
+        (void)hipDeviceSynchronize();   // the old buffer may still be in use by queued work
+        (void)hipFree(scratch[slot]);
+        allocated -= scratchBytes[slot];
+        scratch[slot] = nullptr;
+        scratchBytes[slot] = 0;
+    }
+    void* fresh = nullptr;
+    if (hipMalloc(&fresh, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        error = "hipMalloc failed for " + std::to_string(bytes) + " scratch bytes";
+        return nullptr;
+    }
+    scratch[slot] = fresh;
+    scratchBytes[slot] = bytes;
+    allocated += bytes;
+    return fresh;
+}
+
+hipEvent_t Context::takeEvent() {
+    if (!spareEvents.empty()) {
+        hipEvent_t e = spareEvents.back();
+        spareEvents.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+void Context::resolveProfile() {
+    for (Pending& rec : pending) {
+        float ms = 0.0f;
+        if (hipEventSynchronize(rec.end) == hipSuccess && hipEventElapsedTime(&ms, rec.begin, rec.end) == hipSuccess) {
+            auto& slot = totals[rec.kernel];
+            slot.first += ms;
+            slot.second += 1;
+        }
+        spareEvents.push_back(rec.begin);
+        spareEvents.push_back(rec.end);
+    }
+    pending.clear();
+}
+
+} // namespace aigpu
+
+using aigpu::Clock;
+using aigpu::Context;
+using aigpu::since;
+
+namespace {
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+size_t elem_bytes(uint32_t type) { return type == AIGPU_BF16 ? 2 : 4; }
+
+/* copies `bytes` from the host into scratch at byte offset `at`; returns the device address */
+void* stage_in(Context& ctx, char* base, size_t& at, const void* host, size_t bytes) {
+    if (!host || bytes == 0) return nullptr;
+    at = (at + 255) & ~size_t(255);
+    void* dst = base + at;
+    const Clock::time_point mark = Clock::now();
+    if (hipMemcpy(dst, host, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        ctx.error = "hipMemcpy host to device failed";
+        return nullptr;
+    }
+    ctx.stats.transferSeconds += since(mark);
+    ctx.stats.hostToDeviceBytes += bytes;
+    at += bytes;
+    return dst;
+}
+
+size_t padded(size_t bytes) { return bytes ? ((bytes + 255) & ~size_t(255)) + 256 : 0; }
+
+bool copy_out(Context& ctx, void* host, const void* dev, size_t bytes) {
+    const Clock::time_point mark = Clock::now();
+    if (hipMemcpy(host, dev, bytes, hipMemcpyDeviceToHost) != hipSuccess) {
+        (void)hipGetLastError();
+        return ctx.fail("hipMemcpy device to host failed");
+    }
+    ctx.stats.transferSeconds += since(mark);
+    ctx.stats.deviceToHostBytes += bytes;
+    return true;
+}
+
+bool finish(Context& ctx, Clock::time_point mark) {
+    const hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return ctx.fail(std::string("kernel execution failed: ") + hipGetErrorString(e));
+    ctx.stats.kernelSeconds += since(mark);
+    return true;
+}
+
+} // namespace
+
+extern "C" {
+
+AIGPU_ABI int aigpu_available(void) { return Context::instance().ok ? 1 : 0; }
+
+AIGPU_ABI const char* aigpu_device_name(void) { return Context::instance().name.c_str(); }
+
+AIGPU_ABI const char* aigpu_last_error(void) { return Context::instance().error.c_str(); }
+
+AIGPU_ABI uint64_t aigpu_total_memory(void) {
+    size_t free = 0, total = 0;
+    if (!Context::instance().ok || hipMemGetInfo(&free, &total) != hipSuccess) return 0;
+    return total;
+}
+
+AIGPU_ABI uint64_t aigpu_free_memory(void) {
+    size_t free = 0, total = 0;
+    if (!Context::instance().ok || hipMemGetInfo(&free, &total) != hipSuccess) return 0;
+    return free;
+}
+
+AIGPU_ABI uint64_t aigpu_allocated_bytes(void) { return Context::instance().allocated; }
+
+AIGPU_ABI void* aigpu_upload(const void* host, uint64_t bytes) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok || bytes == 0) return nullptr;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    void* device = nullptr;
+    if (hipMalloc(&device, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        ctx.error = "out of VRAM: hipMalloc(" + std::to_string(bytes) + ") failed";
+        return nullptr;
+    }
+    if (host && hipMemcpy(device, host, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(device);
+        ctx.error = "hipMemcpy host to device failed during upload";
+        return nullptr;
+    }
+    ctx.allocated += bytes;
+    ctx.stats.hostToDeviceBytes += host ? bytes : 0;
+    return device;
+}
+
+AIGPU_ABI void* aigpu_allocate(uint64_t bytes) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok || bytes == 0) return nullptr;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    void* device = nullptr;
+    if (hipMalloc(&device, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        ctx.error = "out of VRAM: hipMalloc(" + std::to_string(bytes) + ") failed";
+        return nullptr;
+    }
+    if (hipMemset(device, 0, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(device);
+        ctx.error = "hipMemset failed";
+        return nullptr;
+    }
+    ctx.allocated += bytes;
+    return device;
+}
+
+AIGPU_ABI void aigpu_release(void* device, uint64_t bytes) {
+    if (!device) return;
+    Context& ctx = Context::instance();
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    (void)hipFree(device);
+    ctx.allocated -= bytes;
+}
+
+AIGPU_ABI int aigpu_download(void* host, const void* device, uint64_t bytes) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok || !device || !host) return 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    return copy_out(ctx, host, device, bytes) ? 1 : 0;
+}
+
+AIGPU_ABI int aigpu_write(void* device, uint64_t offset, const void* host, uint64_t bytes) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok || !device || !host) return 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    if (hipMemcpy(static_cast<char*>(device) + offset, host, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        ctx.error = "hipMemcpy host to device failed";
+        return 0;
+    }
+    ctx.stats.hostToDeviceBytes += bytes;
+    return 1;
+}
+
+AIGPU_ABI void aigpu_synchronize(void) {
+    if (Context::instance().ok) (void)hipDeviceSynchronize();
+}
+
+AIGPU_ABI void aigpu_counters(AiGpuCounters* out) {
+    if (out) *out = Context::instance().stats;
+}
+
+AIGPU_ABI void aigpu_reset_counters(void) { Context::instance().stats = AiGpuCounters{}; }
+
+AIGPU_ABI void aigpu_profile(int enable) {
+    Context& ctx = Context::instance();
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    ctx.profiling = enable != 0;
+}
+
+AIGPU_ABI void aigpu_profile_reset(void) {
+    Context& ctx = Context::instance();
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    ctx.resolveProfile();
+    ctx.totals.clear();
+}
+
+AIGPU_ABI int aigpu_profile_read(const char* kernel, double* milliseconds, uint64_t* launches) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    ctx.resolveProfile();
+    double ms = 0.0;
+    uint64_t n = 0;
+    for (const auto& kv : ctx.totals)
+        if (!kernel || kv.first.find(kernel) != std::string::npos) {
+            ms += kv.second.first;
+            n += kv.second.second;
+        }
+    if (milliseconds) *milliseconds = ms;
+    if (launches) *launches = n;
+    return n > 0 ? 1 : 0;
+}
+
+/* ---------------------------------------------------------------- 1 + 2 */
+
+AIGPU_ABI int aigpu_attention_device(const AiGpuAttention* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("attention: null arguments"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    aigpu::AttentionF32Params p{};
+    p.q = args->q;
+    p.keys = args->keys;
+    p.values = args->values;
+    p.out = args->out;
+    p.qType = int(args->qType);
+    p.kvType = int(args->kvType);
+    p.count = args->count;
+    p.start = args->start;
+    p.heads = args->heads;
+    p.kvHeads = args->kvHeads;
+    p.dim = args->dim;
+    p.qStride = args->qStride;
+    p.window = args->window;
+    p.posStride = args->posStride;
+    p.headStride = args->headStride;
+    if (!p.q || !p.keys || !p.values || !p.out) return ctx.fail("attention: null tensor"), 0;
+    return aigpu::launch_attention_f32(p, as_stream(args->stream)) ? 1 : 0;
+}
+
+AIGPU_ABI int aigpu_attention(const float* q, const float* keys, const float* values, float* out,
+                              uint64_t count, uint64_t start, uint64_t heads, uint64_t kvHeads,
+                              uint64_t dim, uint64_t qStride, uint64_t window) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!q || !keys || !values || !out) return ctx.fail("attention: null tensor"), 0;
+    if (count == 0) return 1;
+    if (kvHeads == 0 || heads % kvHeads) return ctx.fail("attention: heads must be a multiple of kvHeads"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const size_t qBytes = ((count - 1) * heads * qStride + (heads - 1) * qStride + dim) * 4;
+    const size_t kvBytes = (start + count) * kvHeads * dim * 4;
+    const size_t outBytes = count * heads * dim * 4;
+    char* in = static_cast<char*>(ctx.grow(aigpu::SLOT_STAGE_IN, padded(qBytes) + 2 * padded(kvBytes)));
+    float* dOut = static_cast<float*>(ctx.grow(aigpu::SLOT_STAGE_OUT, outBytes));
+    if (!in || !dOut) return 0;
+    size_t at = 0;
+    const void* dq = stage_in(ctx, in, at, q, qBytes);
+    const void* dk = stage_in(ctx, in, at, keys, kvBytes);
+    const void* dv = stage_in(ctx, in, at, values, kvBytes);
+    if (!dq || !dk || !dv) return 0;
+    aigpu::AttentionF32Params p{dq, dk, dv, dOut, AIGPU_F32, AIGPU_F32, count, start, heads,
+                                kvHeads, dim, qStride, window, kvHeads * dim, dim};
+    const Clock::time_point mark = Clock::now();
+    if (!aigpu::launch_attention_f32(p, nullptr) || !finish(ctx, mark)) return 0;
+    return copy_out(ctx, out, dOut, outBytes) ? 1 : 0;
+}
+
+/* ------------------------------------------------------------------ 3 */
+
+static aigpu::PrefillParams prefill_params(const AiGpuPrefill* a) {
+    aigpu::PrefillParams p{};
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.out = a->out;
+    p.keyCache = static_cast<uint16_t*>(a->keyCache);
+    p.valueCache = static_cast<uint16_t*>(a->valueCache);
+    p.qNorm = a->qNorm;
+    p.kNorm = a->kNorm;
+    p.freqs = a->rotaryFrequencies;
+    p.eps = a->epsilon;
+    p.normOffset = a->normOffset;
+    p.rotaryDims = int(a->rotaryDims);
+    p.inType = int(a->inType);
+    p.count = a->count;
+    p.start = a->start;
+    p.heads = a->heads;
+    p.kvHeads = a->kvHeads;
+    p.dim = a->dim;
+    p.qStride = a->qStride;
+    p.window = a->window;
+    p.capacity = a->capacity;
+    return p;
+}
+
+AIGPU_ABI int aigpu_prefill_attention(const AiGpuPrefill* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("prefill: null arguments"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    return aigpu::launch_prefill(prefill_params(args), as_stream(args->stream)) ? 1 : 0;
+}
+
+AIGPU_ABI int aigpu_prefill_attention_host(const AiGpuPrefill* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args || !args->q || !args->k || !args->v || !args->out) return ctx.fail("prefill: null tensor"), 0;
+    if (args->count == 0) return 1;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const size_t es = elem_bytes(args->inType);
+    const size_t qBytes = args->count * args->heads * args->qStride * es;
+    const size_t kvBytes = args->count * args->kvHeads * args->dim * es;
+    const size_t gBytes = args->dim * 4, fBytes = (args->rotaryDims / 2) * 4;
+    const size_t outBytes = args->count * args->heads * args->dim * 4;
+    char* in = static_cast<char*>(ctx.grow(aigpu::SLOT_STAGE_IN, padded(qBytes) + 2 * padded(kvBytes) +
+                                                                       2 * padded(gBytes) + padded(fBytes)));
+    float* dOut = static_cast<float*>(ctx.grow(aigpu::SLOT_STAGE_OUT, outBytes));
+    if (!in || !dOut) return 0;
+    AiGpuPrefill dev = *args;
+    size_t at = 0;
+    dev.q = stage_in(ctx, in, at, args->q, qBytes);
+    dev.k = stage_in(ctx, in, at, args->k, kvBytes);
+    dev.v = stage_in(ctx, in, at, args->v, kvBytes);
+    dev.qNorm = static_cast<const float*>(stage_in(ctx, in, at, args->qNorm, gBytes));
+    dev.kNorm = static_cast<const float*>(stage_in(ctx, in, at, args->kNorm, gBytes));
+    dev.rotaryFrequencies = static_cast<const float*>(
+        args->rotaryFrequencies ? stage_in(ctx, in, at, args->rotaryFrequencies, fBytes) : nullptr);
+    dev.out = dOut;
+    if (!dev.q || !dev.k || !dev.v) return 0;
+    const Clock::time_point mark = Clock::now();
+    if (!aigpu::launch_prefill(prefill_params(&dev), nullptr) || !finish(ctx, mark)) return 0;
+    return copy_out(ctx, args->out, dOut, outBytes) ? 1 : 0;
+}
+
+/* ------------------------------------------------------------------ 4 */
+
+static aigpu::DecodeParams decode_params(const AiGpuDecode* a) {
+    aigpu::DecodeParams p{};
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.out = a->out;
+    p.keyCache = static_cast<uint16_t*>(a->keyCache);
+    p.valueCache = static_cast<uint16_t*>(a->valueCache);
+    p.positions = a->positions;
+    p.qNorm = a->qNorm;
+    p.kNorm = a->kNorm;
+    p.freqs = a->rotaryFrequencies;
+    p.eps = a->epsilon;
+    p.normOffset = a->normOffset;
+    p.rotaryDims = int(a->rotaryDims);
+    p.inType = int(a->inType);
+    p.maxPosition = a->maxPosition;
+    p.batch = a->batch;
+    p.heads = a->heads;
+    p.kvHeads = a->kvHeads;
+    p.dim = a->dim;
+    p.qStride = a->qStride;
+    p.window = a->window;
+    p.capacity = a->capacity;
+    p.batchStride = a->batchStride;
+    return p;
+}
+
+AIGPU_ABI int aigpu_decode_attention(const AiGpuDecode* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("decode: null arguments"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    return aigpu::launch_decode(decode_params(args), as_stream(args->stream)) ? 1 : 0;
+}
+
+AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args || !args->q || !args->k || !args->v || !args->out || !args->positions)
+        return ctx.fail("decode: null tensor"), 0;
+    if (args->batch == 0) return 1;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const size_t es = elem_bytes(args->inType);
+    const size_t qBytes = args->batch * args->heads * args->qStride * es;
+    const size_t kvBytes = args->batch * args->kvHeads * args->dim * es;
+    const size_t pBytes = args->batch * 4;
+    const size_t gBytes = args->dim * 4, fBytes = (args->rotaryDims / 2) * 4;
+    const size_t outBytes = args->batch * args->heads * args->dim * 4;
+    char* in = static_cast<char*>(ctx.grow(aigpu::SLOT_STAGE_IN, padded(qBytes) + 2 * padded(kvBytes) + padded(pBytes) +
+                                                                       2 * padded(gBytes) + padded(fBytes)));
+    float* dOut = static_cast<float*>(ctx.grow(aigpu::SLOT_STAGE_OUT, outBytes));
+    if (!in || !dOut) return 0;
+    AiGpuDecode dev = *args;
+    uint32_t maxPos = 0;
+    for (uint64_t b = 0; b < args->batch; ++b) maxPos = args->positions[b] > maxPos ? args->positions[b] : maxPos;
+    dev.maxPosition = maxPos;
+    size_t at = 0;
+    dev.q = stage_in(ctx, in, at, args->q, qBytes);
+    dev.k = stage_in(ctx, in, at, args->k, kvBytes);
+    dev.v = stage_in(ctx, in, at, args->v, kvBytes);
+    dev.positions = static_cast<const uint32_t*>(stage_in(ctx, in, at, args->positions, pBytes));
+    dev.qNorm = static_cast<const float*>(stage_in(ctx, in, at, args->qNorm, gBytes));
+    dev.kNorm = static_cast<const float*>(stage_in(ctx, in, at, args->kNorm, gBytes));
+    dev.rotaryFrequencies = static_cast<const float*>(
+        args->rotaryFrequencies ? stage_in(ctx, in, at, args->rotaryFrequencies, fBytes) : nullptr);
+    dev.out = dOut;
+    if (!dev.q || !dev.k || !dev.v || !dev.positions) return 0;
+    const Clock::time_point mark = Clock::now();
+    if (!aigpu::launch_decode(decode_params(&dev), nullptr) || !finish(ctx, mark)) return 0;
+    return copy_out(ctx, args->out, dOut, outBytes) ? 1 : 0;
+}
+
+/* ------------------------------------------------------------------ 5 */
+
+static aigpu::DeltaRuleParams delta_params(const AiGpuDeltaRule* a) {
+    aigpu::DeltaRuleParams p{};
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.g = a->g;
+    p.beta = a->beta;
+    p.a = a->a;
+    p.b = a->b;
+    p.aLog = a->aLog;
+    p.dtBias = a->dtBias;
+    p.state = a->state;
+    p.out = a->out;
+    p.inType = int(a->inType);
+    p.normalize = int(a->normalize);
+    p.chunk = int(a->chunk);
+    p.count = a->count;
+    p.keyHeads = a->keyHeads;
+    p.valueHeads = a->valueHeads;
+    p.keyDim = a->keyDim;
+    p.valueDim = a->valueDim;
+    return p;
+}
+
+AIGPU_ABI int aigpu_gated_delta_rule(const AiGpuDeltaRule* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("delta rule: null arguments"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    return aigpu::launch_delta_rule(delta_params(args), as_stream(args->stream)) ? 1 : 0;
+}
+
+AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args || !args->q || !args->k || !args->v || !args->state || !args->out)
+        return ctx.fail("delta rule: null tensor"), 0;
+    if (args->count == 0) return 1;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const size_t es = elem_bytes(args->inType);
+    const size_t qkBytes = args->count * args->keyHeads * args->keyDim * es;
+    const size_t vBytes = args->count * args->valueHeads * args->valueDim * es;
+    const size_t gateBytes = args->count * args->valueHeads * 4;
+    const size_t headBytes = args->valueHeads * 4;
+    const size_t stateBytes = args->valueHeads * args->keyDim * args->valueDim * 4;
+    const size_t outBytes = args->count * args->valueHeads * args->valueDim * 4;
+    char* in = static_cast<char*>(ctx.grow(aigpu::SLOT_STAGE_IN, 2 * padded(qkBytes) + padded(vBytes) + 2 * padded(gateBytes) +
+                                                                       2 * padded(headBytes) + padded(stateBytes)));
+    float* dOut = static_cast<float*>(ctx.grow(aigpu::SLOT_STAGE_OUT, outBytes));
+    if (!in || !dOut) return 0;
+    AiGpuDeltaRule dev = *args;
+    size_t at = 0;
+    dev.q = stage_in(ctx, in, at, args->q, qkBytes);
+    dev.k = stage_in(ctx, in, at, args->k, qkBytes);
+    dev.v = stage_in(ctx, in, at, args->v, vBytes);
+    if (args->aLog) {
+        dev.a = static_cast<const float*>(stage_in(ctx, in, at, args->a, gateBytes));
+        dev.b = static_cast<const float*>(stage_in(ctx, in, at, args->b, gateBytes));
+        dev.aLog = static_cast<const float*>(stage_in(ctx, in, at, args->aLog, headBytes));
+        dev.dtBias = static_cast<const float*>(stage_in(ctx, in, at, args->dtBias, headBytes));
+        dev.g = dev.beta = nullptr;
+    } else {
+        dev.g = static_cast<const float*>(stage_in(ctx, in, at, args->g, gateBytes));
+        dev.beta = static_cast<const float*>(stage_in(ctx, in, at, args->beta, gateBytes));
+    }
+    dev.state = static_cast<float*>(stage_in(ctx, in, at, args->state, stateBytes));
+    dev.out = dOut;
+    if (!dev.q || !dev.k || !dev.v || !dev.state) return 0;
+    const Clock::time_point mark = Clock::now();
+    if (!aigpu::launch_delta_rule(delta_params(&dev), nullptr) || !finish(ctx, mark)) return 0;
+    if (!copy_out(ctx, args->out, dOut, outBytes)) return 0;
+    return copy_out(ctx, args->state, dev.state, stateBytes) ? 1 : 0;
+}
+
+} // extern "C"

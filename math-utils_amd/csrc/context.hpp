@@ -1,0 +1,89 @@
+// context.hpp - process-wide backend state behind the C ABI.
+//
+// One device context per process, as the reference HIP backend keeps
+// (src/gpu/Kernels.hip:43-124): device selection, the last error string,
+// the allocation total, counters, growable scratch buffers and the lock every
+// entry point takes. Scratch buffers are allocated once and grown, never per
+// call: hipMalloc serialises against the device.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/aigpu_attention.h"
+
+namespace aigpu {
+
+enum ScratchSlot {
+    SLOT_STAGE_IN = 0,   // host-form staging of inputs
+    SLOT_STAGE_OUT,      // host-form staging of outputs
+    SLOT_PREFILL_Q,      // fp16 head-major q of a prefill
+    SLOT_PREFILL_K,      // fp16 head-major k history of a prefill
+    SLOT_PREFILL_V,      // fp16 head-major v history of a prefill
+    SLOT_DECODE_PARTS,   // split-K partial softmax records
+    SLOT_DELTA_WORK,     // per-chunk solve products of the delta rule
+    SLOT_COUNT
+};
+
+struct Context {
+    bool ok = false;
+    std::string name;
+    std::string error;
+    std::recursive_mutex gate;
+
+    size_t allocated = 0;
+    AiGpuCounters stats{};
+
+    void* scratch[SLOT_COUNT] = {};
+    size_t scratchBytes[SLOT_COUNT] = {};
+
+    // profiling: events bracketing each launch, resolved on read
+    bool profiling = false;
+    struct Pending { std::string kernel; hipEvent_t begin, end; };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> spareEvents;
+    std::map<std::string, std::pair<double, uint64_t>> totals;
+
+    static Context& instance();
+
+    // a scratch slot of at least `bytes`; nullptr (and error set) on failure
+    void* grow(ScratchSlot slot, size_t bytes);
+
+    bool fail(const std::string& why) {
+        error = why;
+        return false;
+    }
+
+    // records a launch: with profiling on, hipEvents bracket it on `stream`
+    template <typename Launch>
+    bool launch(const char* kernel, hipStream_t stream, Launch body) {
+        hipEvent_t a = nullptr, b = nullptr;
+        if (profiling) {
+            a = takeEvent();
+            b = takeEvent();
+            if (a) (void)hipEventRecord(a, stream);
+        }
+        body();
+        const hipError_t e = hipGetLastError();
+        if (profiling && a && b) {
+            (void)hipEventRecord(b, stream);
+            pending.push_back({kernel, a, b});
+        }
+        ++stats.launches;
+        if (e != hipSuccess) return fail(std::string("launch of ") + kernel + " failed: " + hipGetErrorString(e));
+        return true;
+    }
+
+    hipEvent_t takeEvent();
+    void resolveProfile();
+
+private:
+    Context();
+    ~Context();
+};
+
+} // namespace aigpu

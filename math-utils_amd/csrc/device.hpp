@@ -1,0 +1,93 @@
+// device.hpp - gfx950 device helpers shared by the attention kernels:
+// element conversions, wave64 reductions and the MFMA operand types.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace aigpu {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int WAVE = 64;
+constexpr float LOG2E = 1.4426950408889634f;
+
+/* bfloat16 is the top half of a float32: widening is a shift */
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+/* round to nearest even; NaN stays NaN */
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return uint16_t((u >> 16) | 0x40);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+
+/* element i of a tensor tagged F32 (0) or BF16 (1) */
+__device__ __forceinline__ float load_elem(const void* base, size_t i, int type) {
+    if (type == 0) return static_cast<const float*>(base)[i];
+    return bf16_bits_to_float(static_cast<const uint16_t*>(base)[i]);
+}
+
+/* wave64 butterflies */
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, WAVE);
+    return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, WAVE));
+    return x;
+}
+
+/* orders LDS traffic between the lanes of one wave without a workgroup barrier */
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+/*
+    QK-RMSNorm then rotate-half RoPE of one row held in LDS (`x`, dim floats),
+    done by one wave. Restates attentionMixer (LocalModel.hpp:2608-2648):
+    inv = 1/sqrt(sum(x^2)/dim + eps); x = x*inv*(gamma + offset); then for
+    j < rot/2 the pair (j, j+rot/2) turns by angle = float(pos)*freq[j],
+    computed in fp32 as the reference does. gamma == nullptr skips the norm,
+    freqs == nullptr skips the rotation.
+*/
+__device__ __forceinline__ void norm_rope_row(float* x, int dim, const float* gamma, float eps,
+                                              float offset, const float* freqs, int rot,
+                                              uint64_t pos, int lane) {
+    if (gamma) {
+        float ss = 0.0f;
+        for (int d = lane; d < dim; d += WAVE) ss += x[d] * x[d];
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / float(dim) + eps);
+        for (int d = lane; d < dim; d += WAVE) x[d] = x[d] * inv * (gamma[d] + offset);
+        wave_sync();
+    }
+    if (freqs) {
+        const int half = rot / 2;
+        const float fpos = float(pos);
+        for (int j = lane; j < half; j += WAVE) {
+            const float angle = fpos * freqs[j];
+            float sn, cs;
+            sincosf(angle, &sn, &cs);
+            const float a = x[j], b = x[j + half];
+            x[j] = a * cs - b * sn;
+            x[j + half] = b * cs + a * sn;
+        }
+        wave_sync();
+    }
+}
+
+} // namespace aigpu

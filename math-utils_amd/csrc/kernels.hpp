@@ -1,0 +1,77 @@
+// kernels.hpp - host-side launchers of the gfx950 kernels. Each takes device
+// pointers only, validates what its kernel's grid and indexing assume, and
+// launches on the given stream. The extern "C" layer (abi.hip) stages host
+// data and calls these.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace aigpu {
+
+// ---- generic fp32 attention (kernels::attention semantics) ---------------
+struct AttentionF32Params {
+    const void* q;
+    const void* keys;
+    const void* values;
+    float* out;
+    int qType, kvType;
+    uint64_t count, start, heads, kvHeads, dim, qStride, window, posStride, headStride;
+};
+bool launch_attention_f32(const AttentionF32Params& p, hipStream_t stream);
+
+// ---- prefill: norm + RoPE + append, then fp16 MFMA flash attention --------
+struct PrefillParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    float* out;
+    uint16_t* keyCache;
+    uint16_t* valueCache;
+    const float* qNorm;
+    const float* kNorm;
+    const float* freqs;
+    float eps, normOffset;
+    int rotaryDims, inType;
+    uint64_t count, start, heads, kvHeads, dim, qStride, window, capacity;
+};
+bool launch_prefill(const PrefillParams& p, hipStream_t stream);
+
+// ---- decode: norm + RoPE on load, append, split-K attention, merge --------
+struct DecodeParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    float* out;
+    uint16_t* keyCache;
+    uint16_t* valueCache;
+    const uint32_t* positions;
+    const float* qNorm;
+    const float* kNorm;
+    const float* freqs;
+    float eps, normOffset;
+    int rotaryDims, inType;
+    uint32_t maxPosition;
+    uint64_t batch, heads, kvHeads, dim, qStride, window, capacity, batchStride;
+};
+bool launch_decode(const DecodeParams& p, hipStream_t stream);
+
+// ---- gated delta rule: chunked scan --------------------------------------
+struct DeltaRuleParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* g;
+    const float* beta;
+    const float* a;
+    const float* b;
+    const float* aLog;
+    const float* dtBias;
+    float* state;
+    float* out;
+    int inType, normalize, chunk;
+    uint64_t count, keyHeads, valueHeads, keyDim, valueDim;
+};
+bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream);
+
+} // namespace aigpu

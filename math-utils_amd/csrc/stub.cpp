@@ -1,0 +1,53 @@
+// stub.cpp - the no-device backend: every entry point of
+// include/aigpu_attention.h answers "unavailable" (0 or null) and
+// aigpu_last_error() says why, as the reference's src/gpu/Stub.cpp:18-66 does
+// for DeviceABI.h. Linked in place of libaigpu.so where there is no ROCm, so
+// callers take their CPU path through the same availability check they need
+// anyway when a card is absent at run time.
+#include "../../include/aigpu_attention.h"
+
+extern "C" {
+
+namespace {
+const char NO_NAME[] = "";
+const char NO_DEVICE[] = "built without the HIP attention backend: no device";
+}
+
+AIGPU_ABI int aigpu_available(void) { return 0; }
+AIGPU_ABI const char* aigpu_device_name(void) { return NO_NAME; }
+AIGPU_ABI const char* aigpu_last_error(void) { return NO_DEVICE; }
+AIGPU_ABI uint64_t aigpu_total_memory(void) { return 0; }
+AIGPU_ABI uint64_t aigpu_free_memory(void) { return 0; }
+AIGPU_ABI uint64_t aigpu_allocated_bytes(void) { return 0; }
+AIGPU_ABI void* aigpu_upload(const void*, uint64_t) { return nullptr; }
+AIGPU_ABI void* aigpu_allocate(uint64_t) { return nullptr; }
+AIGPU_ABI void aigpu_release(void*, uint64_t) {}
+AIGPU_ABI int aigpu_download(void*, const void*, uint64_t) { return 0; }
+AIGPU_ABI int aigpu_write(void*, uint64_t, const void*, uint64_t) { return 0; }
+AIGPU_ABI void aigpu_synchronize(void) {}
+AIGPU_ABI void aigpu_counters(AiGpuCounters* out) {
+    if (out) *out = AiGpuCounters{};
+}
+AIGPU_ABI void aigpu_reset_counters(void) {}
+
+AIGPU_ABI int aigpu_attention(const float*, const float*, const float*, float*, uint64_t, uint64_t,
+                              uint64_t, uint64_t, uint64_t, uint64_t, uint64_t) {
+    return 0;
+}
+AIGPU_ABI int aigpu_attention_device(const AiGpuAttention*) { return 0; }
+AIGPU_ABI int aigpu_prefill_attention(const AiGpuPrefill*) { return 0; }
+AIGPU_ABI int aigpu_prefill_attention_host(const AiGpuPrefill*) { return 0; }
+AIGPU_ABI int aigpu_decode_attention(const AiGpuDecode*) { return 0; }
+AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode*) { return 0; }
+AIGPU_ABI int aigpu_gated_delta_rule(const AiGpuDeltaRule*) { return 0; }
+AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule*) { return 0; }
+
+AIGPU_ABI void aigpu_profile(int) {}
+AIGPU_ABI int aigpu_profile_read(const char*, double* ms, uint64_t* n) {
+    if (ms) *ms = 0.0;
+    if (n) *n = 0;
+    return 0;
+}
+AIGPU_ABI void aigpu_profile_reset(void) {}
+
+} // extern "C"

@@ -1,0 +1,539 @@
+/*
+    oracle.c - CPU restatement of the reference attention hot path.
+
+    TEST INFRASTRUCTURE ONLY: the checker the HIP backend is compared with,
+    and the CPU baseline bench.py times. The product never links it.
+    Every function names the reference file:line it restates; paths are
+    relative to the hday200202/math-utils tree.
+*/
+#define _GNU_SOURCE
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <sched.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ========================================================================= //
+    Static-split thread pool (include/ai/ThreadPool.hpp:69-124)
+
+    Persistent workers; thread i always takes slice(count, i, threads), the
+    calling thread is thread 0. The split is contiguous and static, as the
+    reference's Pool::run is, so per-thread work (and its imbalance on causal
+    attention) is the reference's.
+// ========================================================================= */
+
+typedef void (*or_body)(size_t begin, size_t end, void* ctx);
+
+typedef struct {
+    pthread_t* workers;
+    int size; /* including the caller */
+    pthread_mutex_t mutex;
+    pthread_cond_t wake, done;
+    unsigned long epoch;
+    int remaining, stopping;
+    or_body body;
+    void* ctx;
+    size_t count;
+} or_pool;
+
+static or_pool g_pool;
+static pthread_once_t g_pool_once = PTHREAD_ONCE_INIT;
+static pthread_mutex_t g_run_mutex = PTHREAD_MUTEX_INITIALIZER;
+static int g_pool_requested = 0;
+
+/* ThreadPool.hpp:69-73 */
+static void or_slice(size_t count, size_t index, size_t threads, size_t* b, size_t* e) {
+    const size_t span = (count + threads - 1) / threads;
+    size_t begin = index * span;
+    if (begin > count) begin = count;
+    size_t end = begin + span;
+    if (end > count) end = count;
+    *b = begin;
+    *e = end;
+}
+
+static void* or_worker(void* arg) {
+    const int index = (int)(intptr_t)arg;
+    unsigned long seen = 0;
+    for (;;) {
+        pthread_mutex_lock(&g_pool.mutex);
+        while (g_pool.epoch == seen && !g_pool.stopping)
+            pthread_cond_wait(&g_pool.wake, &g_pool.mutex);
+        if (g_pool.stopping) { pthread_mutex_unlock(&g_pool.mutex); return NULL; }
+        seen = g_pool.epoch;
+        or_body body = g_pool.body;
+        void* ctx = g_pool.ctx;
+        const size_t count = g_pool.count;
+        pthread_mutex_unlock(&g_pool.mutex);
+
+        size_t b, e;
+        or_slice(count, (size_t)index, (size_t)g_pool.size, &b, &e);
+        if (b < e) body(b, e, ctx);
+
+        pthread_mutex_lock(&g_pool.mutex);
+        if (--g_pool.remaining == 0) pthread_cond_signal(&g_pool.done);
+        pthread_mutex_unlock(&g_pool.mutex);
+    }
+}
+
+int or_threads(int requested) {
+    if (requested > 0) return requested;
+    cpu_set_t set;
+    if (sched_getaffinity(0, sizeof(set), &set) == 0) {
+        const int n = CPU_COUNT(&set);
+        if (n > 0) return n;
+    }
+    return 1;
+}
+
+static void or_pool_start(void) {
+    const int n = or_threads(g_pool_requested);
+    g_pool.size = n;
+    pthread_mutex_init(&g_pool.mutex, NULL);
+    pthread_cond_init(&g_pool.wake, NULL);
+    pthread_cond_init(&g_pool.done, NULL);
+    g_pool.workers = (pthread_t*)calloc((size_t)(n > 1 ? n - 1 : 1), sizeof(pthread_t));
+    for (int i = 1; i < n; ++i)
+        pthread_create(&g_pool.workers[i - 1], NULL, or_worker, (void*)(intptr_t)i);
+}
+
+/* Runs body over [0, count) on `threads` threads (<= pool size), statically. */
+static void or_pool_run(size_t count, int threads, or_body body, void* ctx) {
+    if (count == 0) return;
+    if (threads <= 1) { body(0, count, ctx); return; }
+    if (g_pool_requested == 0) g_pool_requested = threads;
+    pthread_once(&g_pool_once, or_pool_start);
+    pthread_mutex_lock(&g_run_mutex);
+    const int size = g_pool.size;
+    if (size <= 1) { pthread_mutex_unlock(&g_run_mutex); body(0, count, ctx); return; }
+    pthread_mutex_lock(&g_pool.mutex);
+    g_pool.body = body;
+    g_pool.ctx = ctx;
+    g_pool.count = count;
+    g_pool.remaining = size - 1;
+    g_pool.epoch++;
+    pthread_cond_broadcast(&g_pool.wake);
+    pthread_mutex_unlock(&g_pool.mutex);
+
+    size_t b, e;
+    or_slice(count, 0, (size_t)size, &b, &e);
+    if (b < e) body(b, e, ctx);
+
+    pthread_mutex_lock(&g_pool.mutex);
+    while (g_pool.remaining > 0) pthread_cond_wait(&g_pool.done, &g_pool.mutex);
+    pthread_mutex_unlock(&g_pool.mutex);
+    pthread_mutex_unlock(&g_run_mutex);
+}
+
+/* ========================================================================= //
+    Random (include/math/Random.hpp:15-89)
+// ========================================================================= */
+
+static inline uint64_t or_rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+
+/* Random.hpp:81-86 */
+static inline uint64_t or_splitmix64(uint64_t* x) {
+    uint64_t z = (*x += 0x9E3779B97F4A7C15ULL);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+/* Random.hpp:23-26: the four state words are consecutive splitmix64 outputs */
+void or_rng_seed(or_rng* r, uint64_t seed) {
+    for (int i = 0; i < 4; ++i) r->s[i] = or_splitmix64(&seed);
+    r->has_spare = 0;
+    r->spare = 0.0;
+}
+
+/* xoshiro256++ (Random.hpp:67-79) */
+uint64_t or_rng_next(or_rng* r) {
+    uint64_t* s = r->s;
+    const uint64_t result = or_rotl(s[0] + s[3], 23) + s[0];
+    const uint64_t t = s[1] << 17;
+    s[2] ^= s[0];
+    s[3] ^= s[1];
+    s[1] ^= s[2];
+    s[0] ^= s[3];
+    s[2] ^= t;
+    s[3] = or_rotl(s[3], 45);
+    return result;
+}
+
+/* Random.hpp:28 */
+double or_rng_u01(or_rng* r) { return (double)(or_rng_next(r) >> 11) * 0x1.0p-53; }
+
+/* Random.hpp:30 */
+double or_rng_uniform(or_rng* r, double lo, double hi) { return lo + or_rng_u01(r) * (hi - lo); }
+
+/* Random.hpp:32-39: rejection sampling against the largest multiple of span */
+int64_t or_rng_int(or_rng* r, int64_t lo, int64_t hi) {
+    const uint64_t span = (uint64_t)hi - (uint64_t)lo + 1;
+    if (span == 0) return (int64_t)or_rng_next(r);
+    const uint64_t limit = UINT64_MAX - (UINT64_MAX % span);
+    uint64_t x;
+    do { x = or_rng_next(r); } while (x >= limit);
+    return lo + (int64_t)(x % span);
+}
+
+/* Box-Muller with a cached spare (Random.hpp:41-57) */
+double or_rng_normal(or_rng* r, double mean, double stddev) {
+    if (r->has_spare) {
+        r->has_spare = 0;
+        return mean + stddev * r->spare;
+    }
+    const double u1 = 1.0 - or_rng_u01(r);
+    const double u2 = or_rng_u01(r);
+    const double rad = sqrt(-2.0 * log(u1));
+    const double theta = 2.0 * 3.14159265358979323846 * u2;
+    r->spare = rad * sin(theta);
+    r->has_spare = 1;
+    return mean + stddev * (rad * cos(theta));
+}
+
+/* LocalModel.hpp:1621-1630 */
+uint64_t or_fnv1a(const char* text) {
+    uint64_t h = 0xCBF29CE484222325ULL;
+    for (const unsigned char* c = (const unsigned char*)text; *c; ++c) {
+        h ^= *c;
+        h *= 0x100000001B3ULL;
+    }
+    return h;
+}
+
+enum { OR_FILL_CHUNK = 1 << 14 };
+
+typedef struct {
+    float* out;
+    size_t n;
+    uint64_t base;
+    double a, b;
+    int uniform;
+} or_fill_ctx;
+
+/* LocalModel.hpp:1555-1573: one generator per 2^14-element chunk */
+static void or_fill_body(size_t begin, size_t end, void* p) {
+    const or_fill_ctx* c = (const or_fill_ctx*)p;
+    for (size_t chunk = begin; chunk < end; ++chunk) {
+        or_rng r;
+        or_rng_seed(&r, c->base + (uint64_t)chunk * 0x9E3779B97F4A7C15ULL);
+        const size_t from = chunk * OR_FILL_CHUNK;
+        const size_t to = from + OR_FILL_CHUNK < c->n ? from + OR_FILL_CHUNK : c->n;
+        if (c->uniform)
+            for (size_t i = from; i < to; ++i) c->out[i] = (float)or_rng_uniform(&r, c->a, c->b);
+        else
+            for (size_t i = from; i < to; ++i) c->out[i] = (float)or_rng_normal(&r, c->a, c->b);
+    }
+}
+
+static void or_fill(float* out, size_t n, uint64_t seed, const char* name, double a, double b,
+                    int uniform, int threads) {
+    or_fill_ctx c = {out, n, seed ^ or_fnv1a(name), a, b, uniform};
+    const size_t chunks = (n + OR_FILL_CHUNK - 1) / OR_FILL_CHUNK;
+    or_pool_run(chunks, threads, or_fill_body, &c);
+}
+
+void or_fill_normal(float* out, size_t n, uint64_t seed, const char* name, double mean,
+                    double stddev, int threads) {
+    or_fill(out, n, seed, name, mean, stddev, 0, threads);
+}
+
+void or_fill_uniform(float* out, size_t n, uint64_t seed, const char* name, double lo,
+                     double hi, int threads) {
+    or_fill(out, n, seed, name, lo, hi, 1, threads);
+}
+
+/* ========================================================================= //
+    bfloat16
+// ========================================================================= */
+
+uint16_t or_bf16_from_float(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float or_bf16_to_float(uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float x;
+    memcpy(&x, &u, 4);
+    return x;
+}
+
+void or_round_to_bf16(float* x, size_t n) {
+    for (size_t i = 0; i < n; ++i) x[i] = or_bf16_to_float(or_bf16_from_float(x[i]));
+}
+
+void or_pack_bf16(const float* x, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = or_bf16_from_float(x[i]);
+}
+
+void or_unpack_bf16(const uint16_t* x, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = or_bf16_to_float(x[i]);
+}
+
+/* ========================================================================= //
+    Attention (include/ai/Kernels.hpp:39-70, 130-168)
+// ========================================================================= */
+
+enum { OR_LANES = 32 }; /* Kernels.hpp:55 */
+
+/* Kernels.hpp:57-70: 32 interleaved accumulators, summed in order, then the tail */
+float or_dot(const float* a, const float* b, size_t n) {
+    float acc[OR_LANES] = {0};
+    size_t i = 0;
+    for (; i + OR_LANES <= n; i += OR_LANES)
+        for (size_t j = 0; j < OR_LANES; ++j) acc[j] += a[i + j] * b[i + j];
+    float sum = 0.0f;
+    for (size_t j = 0; j < OR_LANES; ++j) sum += acc[j];
+    for (; i < n; ++i) sum += a[i] * b[i];
+    return sum;
+}
+
+typedef struct {
+    const float *q, *keys, *values;
+    float* out;
+    size_t count, start, heads, kvHeads, dim, qStride, posStride, headStride, window;
+    const uint32_t* rows;
+} or_attn_ctx;
+
+/* Kernels.hpp:137-162: per (token, head) task, scores row, max, exp-sum, PV */
+static void or_attn_body(size_t begin, size_t end, void* p) {
+    const or_attn_ctx* c = (const or_attn_ctx*)p;
+    const float scale = 1.0f / sqrtf((float)c->dim);
+    float* scores = (float*)malloc(sizeof(float) * (c->start + c->count + 1));
+    for (size_t task = begin; task < end; ++task) {
+        const size_t slot = task / c->heads, head = task % c->heads;
+        const size_t token = c->rows ? c->rows[slot] : slot;
+        const size_t position = c->start + token;
+        const size_t first =
+            c->window && position + 1 > c->window ? position + 1 - c->window : 0;
+        const size_t kv = head / (c->heads / c->kvHeads);
+        const float* query = c->q + (token * c->heads + head) * c->qStride;
+        float maximum = -INFINITY;
+        for (size_t j = first; j <= position; ++j) {
+            scores[j] = or_dot(query, c->keys + j * c->posStride + kv * c->headStride, c->dim) * scale;
+            if (scores[j] > maximum) maximum = scores[j];
+        }
+        float sum = 0;
+        for (size_t j = first; j <= position; ++j) {
+            scores[j] = expf(scores[j] - maximum);
+            sum += scores[j];
+        }
+        float* dst = c->out + task * c->dim;
+        for (size_t d = 0; d < c->dim; ++d) dst[d] = 0.0f;
+        const float inv = 1.0f / sum;
+        for (size_t j = first; j <= position; ++j) {
+            const float w = scores[j] * inv;
+            const float* v = c->values + j * c->posStride + kv * c->headStride;
+            for (size_t d = 0; d < c->dim; ++d) dst[d] += w * v[d];
+        }
+    }
+    free(scores);
+}
+
+void or_attention_strided(const float* q, const float* keys, const float* values, float* out,
+                          size_t count, size_t start, size_t heads, size_t kvHeads, size_t dim,
+                          size_t qStride, size_t posStride, size_t headStride, size_t window,
+                          const uint32_t* rows, size_t nrows, int threads) {
+    or_attn_ctx c = {q, keys, values, out, count, start, heads, kvHeads, dim,
+                     qStride, posStride, headStride, window, rows};
+    const size_t n = rows ? nrows : count;
+    const size_t tasks = n * heads;
+    /* Kernels.hpp:164-166: the pool only for substantial work */
+    if (threads > 1 && tasks > 1 &&
+        (double)n * (double)heads * (double)(start + (count + 1) / 2) * (double)dim >= 262144.0)
+        or_pool_run(tasks, threads, or_attn_body, &c);
+    else
+        or_attn_body(0, tasks, &c);
+}
+
+void or_attention(const float* q, const float* keys, const float* values, float* out,
+                  size_t count, size_t start, size_t heads, size_t kvHeads, size_t dim,
+                  size_t qStride, size_t window, int threads) {
+    or_attention_strided(q, keys, values, out, count, start, heads, kvHeads, dim, qStride,
+                         kvHeads * dim, dim, window, NULL, 0, threads);
+}
+
+/* ========================================================================= //
+    QK-RMSNorm and RoPE (include/ai/LocalModel.hpp:807-820, 1341-1348, 2608-2648)
+// ========================================================================= */
+
+/* LocalModel.hpp:1341-1348 */
+void or_rms_norm_row(const float* x, const float* w, float* out, size_t n, float eps,
+                     float weightOffset) {
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; ++i) sum += x[i] * x[i];
+    const float inv = 1.0f / sqrtf(sum / (float)n + eps);
+    for (size_t i = 0; i < n; ++i) out[i] = x[i] * inv * (w[i] + weightOffset);
+}
+
+/* LocalModel.hpp:807-820, with the parameter validation of :800-806 */
+int or_rotary_frequencies(float* out, size_t rotaryDims, float theta, int type, float factor,
+                          float lowFreq, float highFreq, float original) {
+    if (!isfinite(theta) || theta <= 0 || !isfinite(factor) || factor < 1) return 0;
+    if (type == 2 && (!isfinite(original) || original <= 0 || !isfinite(lowFreq) ||
+                      !isfinite(highFreq) || lowFreq <= 0 || highFreq <= lowFreq))
+        return 0;
+    for (size_t j = 0; j < rotaryDims / 2; ++j) {
+        float frequency = 1.0f / powf(theta, (float)(2 * j) / (float)rotaryDims);
+        if (type == 1) frequency /= factor;
+        if (type == 2) {
+            const float wavelength = 6.283185307179586f / frequency;
+            if (wavelength > original / lowFreq)
+                frequency /= factor;
+            else if (wavelength >= original / highFreq) {
+                const float blend = (original / wavelength - lowFreq) / (highFreq - lowFreq);
+                frequency *= (1 - blend) / factor + blend;
+            }
+        }
+        out[j] = frequency;
+    }
+    return 1;
+}
+
+/* LocalModel.hpp:2608-2618 (norm) then :2624-2643 (rotate-half RoPE, fp32 angle) */
+void or_qk_norm_rope(float* q, float* k, size_t count, size_t startPos, size_t heads,
+                     size_t kvHeads, size_t dim, size_t qStride, const float* qGamma,
+                     const float* kGamma, float eps, float weightOffset, const float* freqs,
+                     size_t rotaryDims) {
+    const size_t KW = kvHeads * dim;
+    for (size_t t = 0; t < count; ++t) {
+        if (qGamma)
+            for (size_t h = 0; h < heads; ++h) {
+                float* qh = q + t * heads * qStride + h * qStride;
+                or_rms_norm_row(qh, qGamma, qh, dim, eps, weightOffset);
+            }
+        if (kGamma)
+            for (size_t h = 0; h < kvHeads; ++h)
+                or_rms_norm_row(k + t * KW + h * dim, kGamma, k + t * KW + h * dim, dim, eps,
+                                weightOffset);
+    }
+    if (!freqs) return;
+    const size_t half = rotaryDims / 2;
+    for (size_t t = 0; t < count; ++t) {
+        for (size_t j = 0; j < half; ++j) {
+            const float angle = (float)(startPos + t) * freqs[j];
+            const float cs = cosf(angle), sn = sinf(angle);
+            for (size_t h = 0; h < heads; ++h) {
+                float* x = q + t * heads * qStride + h * qStride;
+                const float a = x[j], b = x[j + half];
+                x[j] = a * cs - b * sn;
+                x[j + half] = b * cs + a * sn;
+            }
+            for (size_t h = 0; h < kvHeads; ++h) {
+                float* x = k + t * KW + h * dim;
+                const float a = x[j], b = x[j + half];
+                x[j] = a * cs - b * sn;
+                x[j + half] = b * cs + a * sn;
+            }
+        }
+    }
+}
+
+/* ========================================================================= //
+    Gated delta rule (Kernels.hpp:102-128, LocalModel.hpp:1371-1386, 2797-2830)
+// ========================================================================= */
+
+float or_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+float or_softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+void or_l2normalise(float* v, size_t n, float eps) {
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; ++i) sum += v[i] * v[i];
+    const float inv = 1.0f / sqrtf(sum + eps);
+    for (size_t i = 0; i < n; ++i) v[i] *= inv;
+}
+
+/* Kernels.hpp:105-128: decay fused with prediction, rank-one update fused with
+   the readout (out reads the updated state) */
+void or_delta_step(float* state, const float* key, const float* query, const float* value,
+                   const float* decay, int perKeyDecay, float beta, size_t keys, size_t values,
+                   float* out, float* prediction, float* delta) {
+    for (size_t d = 0; d < values; ++d) prediction[d] = 0.0f;
+    for (size_t i = 0; i < keys; ++i) {
+        float* row = state + i * values;
+        const float a = decay[perKeyDecay ? i : 0], k = key[i];
+        for (size_t d = 0; d < values; ++d) {
+            row[d] *= a;
+            prediction[d] += row[d] * k;
+        }
+    }
+    for (size_t d = 0; d < values; ++d) delta[d] = (value[d] - prediction[d]) * beta;
+    for (size_t d = 0; d < values; ++d) out[d] = 0.0f;
+    for (size_t i = 0; i < keys; ++i) {
+        float* row = state + i * values;
+        const float k = key[i], q = query[i];
+        for (size_t d = 0; d < values; ++d) {
+            row[d] += k * delta[d];
+            out[d] += row[d] * q;
+        }
+    }
+}
+
+/* LocalModel.hpp:2820-2823 */
+void or_gdn_gates(const float* a, const float* b, const float* aLog, const float* dtBias,
+                  float* g, float* beta, size_t count, size_t valueHeads) {
+    for (size_t t = 0; t < count; ++t)
+        for (size_t h = 0; h < valueHeads; ++h) {
+            const size_t i = t * valueHeads + h;
+            const float aPlusBias = a[i] + dtBias[h];
+            g[i] = -expf(aLog[h]) * or_softplus(aPlusBias);
+            beta[i] = or_sigmoid(b[i]);
+        }
+}
+
+typedef struct {
+    const float *q, *k, *v, *g, *beta;
+    float *state, *out;
+    size_t count, keyHeads, valueHeads, KD, VD;
+    int normalize;
+} or_gdn_ctx;
+
+/* LocalModel.hpp:2802-2830, restricted to value heads [begin, end) */
+static void or_gdn_body(size_t begin, size_t end, void* p) {
+    const or_gdn_ctx* c = (const or_gdn_ctx*)p;
+    const size_t KD = c->KD, VD = c->VD, nV = c->valueHeads;
+    const size_t group = c->valueHeads / c->keyHeads;
+    float* qh = (float*)malloc(sizeof(float) * KD);
+    float* kh = (float*)malloc(sizeof(float) * KD);
+    float* kv = (float*)malloc(sizeof(float) * VD);
+    float* delta = (float*)malloc(sizeof(float) * VD);
+    const float qScale = 1.0f / sqrtf((float)KD);
+    for (size_t t = 0; t < c->count; ++t) {
+        for (size_t vHead = begin; vHead < end; ++vHead) {
+            const size_t kHead = vHead / group;
+            memcpy(qh, c->q + (t * c->keyHeads + kHead) * KD, sizeof(float) * KD);
+            memcpy(kh, c->k + (t * c->keyHeads + kHead) * KD, sizeof(float) * KD);
+            if (c->normalize) {
+                or_l2normalise(qh, KD, 1e-6f);
+                or_l2normalise(kh, KD, 1e-6f);
+                for (size_t i = 0; i < KD; ++i) qh[i] *= qScale;
+            }
+            const float decay = expf(c->g[t * nV + vHead]);
+            const float beta = c->beta[t * nV + vHead];
+            or_delta_step(c->state + vHead * KD * VD, kh, qh, c->v + (t * nV + vHead) * VD, &decay,
+                          0, beta, KD, VD, c->out + (t * nV + vHead) * VD, kv, delta);
+        }
+    }
+    free(qh);
+    free(kh);
+    free(kv);
+    free(delta);
+}
+
+void or_gated_delta_rule(const float* q, const float* k, const float* v, const float* g,
+                         const float* beta, float* state, float* out, size_t count,
+                         size_t keyHeads, size_t valueHeads, size_t KD, size_t VD,
+                         int normalize, int threads) {
+    or_gdn_ctx c = {q, k, v, g, beta, state, out, count, keyHeads, valueHeads, KD, VD, normalize};
+    if (threads > 1)
+        or_pool_run(valueHeads, threads, or_gdn_body, &c);
+    else
+        or_gdn_body(0, valueHeads, &c);
+}

@@ -1,0 +1,154 @@
+/*
+    oracle.h - CPU restatement of the reference attention hot path.
+
+    TEST INFRASTRUCTURE ONLY. Nothing in the product (math-utils_amd/) links,
+    loads or calls this code. It is the checker for the HIP backend: tests/
+    compare the GPU results with it, bench.py times it as the CPU baseline,
+    and __graft_entry__.smoke() uses it to check one small GPU invocation.
+
+    Each function cites the reference file:line it restates (paths relative to
+    the hday200202/math-utils tree). The arithmetic follows the reference's
+    order of operations: 32-accumulator dot, two-pass softmax, fp32 everywhere,
+    static contiguous split across threads.
+
+    Pinning (what checks each function, beyond retyping it):
+      or_rng_*                 known-answer stream of the published
+                               splitmix64/xoshiro256++ generators, plus the
+                               reference's own Random compiled into oracle/_ref
+      or_attention*            bit-compared against the reference's
+                               kernels::attention compiled from its own header
+                               (oracle/_ref), and against an fp64 closed form
+                               (llm-testing.cpp:106-134 restated)
+      or_delta_step            bit-compared against kernels::deltaStep (_ref),
+                               and against the four-pass restatement of
+                               llm-testing.cpp:813-851
+      or_rms_norm_row,
+      or_qk_norm_rope          closed forms and invariants: rms of normed/gamma
+                               is 1, RoPE keeps pair norms, position 0 is the
+                               identity, fp64 rotation matches
+      or_rotary_frequencies    closed form 1/theta^(2j/rot); linear and llama3
+                               scaling against llm-testing.cpp:141-145's
+                               expected values
+      or_gated_delta_rule      chunk-free recurrence equals or_delta_step
+                               applied step by step; beta=0 and decay=1 special
+                               cases; one token equals one deltaStep; l2norm
+                               closed form
+*/
+#ifndef ORACLE_H
+#define ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- seeded inputs: math::random::Random (include/math/Random.hpp:15-89) ---- */
+typedef struct or_rng {
+    uint64_t s[4];
+    double spare;
+    int has_spare;
+} or_rng;
+
+void     or_rng_seed(or_rng* r, uint64_t seed);
+uint64_t or_rng_next(or_rng* r);
+double   or_rng_u01(or_rng* r);
+double   or_rng_uniform(or_rng* r, double lo, double hi);
+int64_t  or_rng_int(or_rng* r, int64_t lo, int64_t hi);
+double   or_rng_normal(or_rng* r, double mean, double stddev);
+
+/* FNV-1a as LocalModel::stableHash (include/ai/LocalModel.hpp:1621-1630) */
+uint64_t or_fnv1a(const char* text);
+
+/* chunked, named fill as the random initialiser (LocalModel.hpp:1555-1573):
+   chunk c of 2^14 elements draws from Random(seed ^ fnv1a(name) + c*golden) */
+void or_fill_normal(float* out, size_t n, uint64_t seed, const char* name,
+                    double mean, double stddev, int threads);
+void or_fill_uniform(float* out, size_t n, uint64_t seed, const char* name,
+                     double lo, double hi, int threads);
+
+/* bfloat16 round-to-nearest-even and widening (a shift, Kernels.hpp:84-99) */
+uint16_t or_bf16_from_float(float x);
+float    or_bf16_to_float(uint16_t b);
+void     or_round_to_bf16(float* x, size_t n);                 /* in place */
+void     or_pack_bf16(const float* x, uint16_t* out, size_t n);
+void     or_unpack_bf16(const uint16_t* x, float* out, size_t n);
+
+/* ---- attention: kernels::attention (include/ai/Kernels.hpp:130-168) ---- */
+float or_dot(const float* a, const float* b, size_t n);       /* Kernels.hpp:55-70 */
+
+/* Same argument list and layouts as kernels::attention: q [count][heads][qStride],
+   keys/values position-major [pos][kvHeads][dim], out [count][heads][dim].
+   threads>1 uses a static contiguous split (ThreadPool.hpp:69-124) under the
+   same work threshold as Kernels.hpp:165. */
+void or_attention(const float* q, const float* keys, const float* values, float* out,
+                  size_t count, size_t start, size_t heads, size_t kvHeads, size_t dim,
+                  size_t qStride, size_t window, int threads);
+
+/* The same arithmetic with an explicit key/value layout (element strides per
+   position and per kv head) and an optional subset of query tokens: tokens
+   [rows[i]] for i < nrows (rows == NULL means all `count`). out is
+   [nrows][heads][dim]. Used for head-major caches and for sampled rows of
+   large problems. */
+void or_attention_strided(const float* q, const float* keys, const float* values,
+                          float* out, size_t count, size_t start, size_t heads,
+                          size_t kvHeads, size_t dim, size_t qStride,
+                          size_t posStride, size_t headStride, size_t window,
+                          const uint32_t* rows, size_t nrows, int threads);
+
+/* ---- norm and RoPE glue of LocalModel::attentionMixer ---- */
+/* rmsNormRow (LocalModel.hpp:1341-1348) */
+void or_rms_norm_row(const float* x, const float* w, float* out, size_t n, float eps,
+                     float weightOffset);
+
+/* LocalConfig rotary table (LocalModel.hpp:807-820). type 0 default, 1 linear,
+   2 llama3. Returns 0 on invalid parameters. */
+int or_rotary_frequencies(float* out, size_t rotaryDims, float theta, int type,
+                          float factor, float lowFreq, float highFreq, float original);
+
+/* attentionMixer QK-RMSNorm then RoPE, in place (LocalModel.hpp:2608-2648).
+   q [count][heads][qStride], k [count][kvHeads][dim]. qGamma/kGamma NULL skips
+   the norm; freqs NULL skips RoPE. */
+void or_qk_norm_rope(float* q, float* k, size_t count, size_t startPos, size_t heads,
+                     size_t kvHeads, size_t dim, size_t qStride, const float* qGamma,
+                     const float* kGamma, float eps, float weightOffset,
+                     const float* freqs, size_t rotaryDims);
+
+/* ---- gated delta rule ---- */
+float or_sigmoid(float x);                                   /* LocalModel.hpp:1371 */
+float or_softplus(float x);                                  /* LocalModel.hpp:1374-1376 */
+void  or_l2normalise(float* v, size_t n, float eps);         /* LocalModel.hpp:1380-1386 */
+
+/* kernels::deltaStep (Kernels.hpp:102-128) */
+void or_delta_step(float* state, const float* key, const float* query, const float* value,
+                   const float* decay, int perKeyDecay, float beta, size_t keys,
+                   size_t values, float* out, float* prediction, float* delta);
+
+/* gate computation of gatedDeltaNetMixer (LocalModel.hpp:2820-2823):
+   g = -exp(aLog[h]) * softplus(a + dtBias[h]); beta = sigmoid(b). a, b, g,
+   beta are [count][valueHeads]. */
+void or_gdn_gates(const float* a, const float* b, const float* aLog, const float* dtBias,
+                  float* g, float* beta, size_t count, size_t valueHeads);
+
+/* The recurrence loop of gatedDeltaNetMixer (LocalModel.hpp:2802-2830).
+   q,k [count][keyHeads][KD]; v [count][valueHeads][VD]; g (log decay) and
+   beta [count][valueHeads]; state [valueHeads][KD][VD] in/out; out
+   [count][valueHeads][VD]. normalize != 0 applies l2normalise to q and k and
+   scales q by 1/sqrt(KD) as the mixer does; 0 takes q,k as given.
+   threads > 1 splits value heads statically (the reference runs this loop on
+   one thread; heads are independent so the split changes no arithmetic). */
+void or_gated_delta_rule(const float* q, const float* k, const float* v, const float* g,
+                         const float* beta, float* state, float* out, size_t count,
+                         size_t keyHeads, size_t valueHeads, size_t KD, size_t VD,
+                         int normalize, int threads);
+
+/* number of threads the static pool would use given a request (<=0: all
+   online CPUs in this process's affinity mask) */
+int or_threads(int requested);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,275 @@
+"""oracle.py - numpy front end over the CPU restatement (liboracle_*.so) and,
+where it was built, the reference's own kernels (_ref/libref_*.so).
+
+TEST INFRASTRUCTURE ONLY. Imported by tests/, bench.py's cpu_baseline leg and
+__graft_entry__.smoke() as the checker; the product path never imports it.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_sz = C.c_size_t
+
+
+def _has_avx512():
+    try:
+        with open("/proc/cpuinfo") as f:
+            flags = f.read()
+        return all(x in flags for x in ("avx512f", "avx512bw", "avx512vl", "avx512dq"))
+    except OSError:
+        return False
+
+
+def _pick(stem, folder):
+    for level in (("v4", "v3") if _has_avx512() else ("v3",)):
+        path = os.path.join(folder, f"{stem}_{level}.so")
+        if os.path.exists(path):
+            return path
+    return None
+
+
+def build():
+    """Compiles the oracle (and _ref where the reference checkout exists)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+_ref = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        path = _pick("liboracle", HERE)
+        if path is None:
+            raise RuntimeError("oracle not built: run make -C oracle")
+        L = C.CDLL(path)
+        L.or_rng_seed.argtypes = [C.c_void_p, C.c_uint64]
+        L.or_rng_next.restype = C.c_uint64
+        L.or_rng_next.argtypes = [C.c_void_p]
+        L.or_rng_normal.restype = C.c_double
+        L.or_rng_normal.argtypes = [C.c_void_p, C.c_double, C.c_double]
+        L.or_rng_uniform.restype = C.c_double
+        L.or_rng_uniform.argtypes = [C.c_void_p, C.c_double, C.c_double]
+        L.or_rng_int.restype = C.c_int64
+        L.or_rng_int.argtypes = [C.c_void_p, C.c_int64, C.c_int64]
+        L.or_rng_u01.restype = C.c_double
+        L.or_rng_u01.argtypes = [C.c_void_p]
+        L.or_fnv1a.restype = C.c_uint64
+        L.or_fnv1a.argtypes = [C.c_char_p]
+        L.or_fill_normal.argtypes = [_f32p, _sz, C.c_uint64, C.c_char_p, C.c_double, C.c_double, C.c_int]
+        L.or_fill_uniform.argtypes = [_f32p, _sz, C.c_uint64, C.c_char_p, C.c_double, C.c_double, C.c_int]
+        L.or_round_to_bf16.argtypes = [_f32p, _sz]
+        L.or_pack_bf16.argtypes = [_f32p, _u16p, _sz]
+        L.or_dot.restype = C.c_float
+        L.or_dot.argtypes = [_f32p, _f32p, _sz]
+        L.or_attention.argtypes = [_f32p, _f32p, _f32p, _f32p] + [_sz] * 7 + [C.c_int]
+        L.or_attention_strided.argtypes = ([_f32p, _f32p, _f32p, _f32p] + [_sz] * 9 +
+                                           [C.c_void_p, _sz, C.c_int])
+        L.or_rms_norm_row.argtypes = [_f32p, _f32p, _f32p, _sz, C.c_float, C.c_float]
+        L.or_rotary_frequencies.restype = C.c_int
+        L.or_rotary_frequencies.argtypes = [_f32p, _sz, C.c_float, C.c_int, C.c_float,
+                                            C.c_float, C.c_float, C.c_float]
+        L.or_qk_norm_rope.argtypes = ([_f32p, _f32p] + [_sz] * 6 + [C.c_void_p, C.c_void_p,
+                                      C.c_float, C.c_float, C.c_void_p, _sz])
+        L.or_sigmoid.restype = C.c_float
+        L.or_sigmoid.argtypes = [C.c_float]
+        L.or_softplus.restype = C.c_float
+        L.or_softplus.argtypes = [C.c_float]
+        L.or_l2normalise.argtypes = [_f32p, _sz, C.c_float]
+        L.or_delta_step.argtypes = ([_f32p, _f32p, _f32p, _f32p, _f32p, C.c_int, C.c_float,
+                                     _sz, _sz, _f32p, _f32p, _f32p])
+        L.or_gdn_gates.argtypes = [_f32p] * 6 + [_sz, _sz]
+        L.or_gated_delta_rule.argtypes = [_f32p] * 7 + [_sz] * 5 + [C.c_int, C.c_int]
+        L.or_threads.restype = C.c_int
+        L.or_threads.argtypes = [C.c_int]
+        _lib = L
+    return _lib
+
+
+def ref():
+    """The reference's own kernels (oracle/_ref), or None when not built."""
+    global _ref
+    if _ref is None:
+        path = _pick("libref", os.path.join(HERE, "_ref"))
+        if path is None:
+            return None
+        R = C.CDLL(path)
+        R.ref_configure_pool.restype = C.c_int
+        R.ref_configure_pool.argtypes = [C.c_int]
+        R.ref_attention.argtypes = [_f32p] * 4 + [C.c_uint64] * 7 + [C.c_int]
+        R.ref_delta_step.argtypes = ([_f32p] * 5 + [C.c_int, C.c_float, C.c_uint64, C.c_uint64] +
+                                     [_f32p] * 3)
+        R.ref_dot.restype = C.c_float
+        R.ref_dot.argtypes = [_f32p, _f32p, C.c_uint64]
+        R.ref_random.argtypes = [C.c_uint64, C.c_int, C.c_uint64, C.c_double, C.c_double, C.c_void_p]
+        _ref = R
+    return _ref
+
+
+def threads(requested=0, cap=16):
+    n = lib().or_threads(int(requested))
+    return max(1, min(n, cap)) if requested <= 0 else n
+
+
+# ---------------------------------------------------------------- generator
+class Rng:
+    """math::random::Random restated (Random.hpp:15-89)."""
+
+    def __init__(self, seed):
+        self._buf = C.create_string_buffer(48)
+        lib().or_rng_seed(self._buf, C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF))
+
+    def next(self):
+        return lib().or_rng_next(self._buf)
+
+    def u01(self):
+        return lib().or_rng_u01(self._buf)
+
+    def normal(self, mean=0.0, sd=1.0):
+        return lib().or_rng_normal(self._buf, mean, sd)
+
+    def uniform(self, lo, hi):
+        return lib().or_rng_uniform(self._buf, lo, hi)
+
+    def randint(self, lo, hi):
+        return lib().or_rng_int(self._buf, lo, hi)
+
+
+def fill_normal(shape, seed, name, mean=0.0, sd=1.0, nthreads=0):
+    out = np.empty(int(np.prod(shape)), np.float32)
+    lib().or_fill_normal(out, out.size, C.c_uint64(seed), name.encode(), mean, sd,
+                         threads(nthreads))
+    return out.reshape(shape)
+
+
+def fill_uniform(shape, seed, name, lo, hi, nthreads=0):
+    out = np.empty(int(np.prod(shape)), np.float32)
+    lib().or_fill_uniform(out, out.size, C.c_uint64(seed), name.encode(), lo, hi,
+                          threads(nthreads))
+    return out.reshape(shape)
+
+
+def round_bf16(x):
+    y = np.ascontiguousarray(x, np.float32).copy()
+    lib().or_round_to_bf16(y.reshape(-1), y.size)
+    return y
+
+
+def pack_bf16(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_pack_bf16(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def unpack_bf16(b):
+    b = np.ascontiguousarray(b, np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+# ---------------------------------------------------------------- attention
+def attention(q, keys, values, count, start, heads, kv_heads, dim, q_stride, window=0,
+              nthreads=1):
+    """kernels::attention restated; position-major keys/values [pos][kv][dim]."""
+    q = np.ascontiguousarray(q, np.float32)
+    keys = np.ascontiguousarray(keys, np.float32)
+    values = np.ascontiguousarray(values, np.float32)
+    out = np.zeros(count * heads * dim, np.float32)
+    lib().or_attention(q.reshape(-1), keys.reshape(-1), values.reshape(-1), out, count, start,
+                       heads, kv_heads, dim, q_stride, window,
+                       threads(nthreads) if nthreads != 1 else 1)
+    return out.reshape(count, heads, dim)
+
+
+def attention_strided(q, keys, values, count, start, heads, kv_heads, dim, q_stride,
+                      pos_stride, head_stride, window=0, rows=None, nthreads=1):
+    q = np.ascontiguousarray(q, np.float32)
+    keys = np.ascontiguousarray(keys, np.float32)
+    values = np.ascontiguousarray(values, np.float32)
+    n = count if rows is None else len(rows)
+    out = np.zeros(n * heads * dim, np.float32)
+    rows_arr = None if rows is None else np.ascontiguousarray(rows, np.uint32)
+    lib().or_attention_strided(q.reshape(-1), keys.reshape(-1), values.reshape(-1), out, count,
+                               start, heads, kv_heads, dim, q_stride, pos_stride, head_stride,
+                               window,
+                               None if rows_arr is None else rows_arr.ctypes.data_as(C.c_void_p),
+                               0 if rows_arr is None else len(rows_arr),
+                               threads(nthreads) if nthreads != 1 else 1)
+    return out.reshape(n, heads, dim)
+
+
+def rotary_frequencies(rotary_dims, theta, kind=0, factor=1.0, low=1.0, high=4.0,
+                       original=0.0):
+    out = np.zeros(rotary_dims // 2, np.float32)
+    ok = lib().or_rotary_frequencies(out, rotary_dims, theta, kind, factor, low, high, original)
+    if not ok:
+        raise ValueError("invalid rotary position parameters")
+    return out
+
+
+def qk_norm_rope(q, k, count, start, heads, kv_heads, dim, q_stride, q_gamma, k_gamma, eps,
+                 freqs, rotary_dims, weight_offset=0.0):
+    """attentionMixer norm + RoPE restated; returns new (q, k) arrays."""
+    q = np.ascontiguousarray(q, np.float32).copy()
+    k = np.ascontiguousarray(k, np.float32).copy()
+    qg = None if q_gamma is None else np.ascontiguousarray(q_gamma, np.float32)
+    kg = None if k_gamma is None else np.ascontiguousarray(k_gamma, np.float32)
+    fr = None if freqs is None else np.ascontiguousarray(freqs, np.float32)
+    lib().or_qk_norm_rope(q.reshape(-1), k.reshape(-1), count, start, heads, kv_heads, dim,
+                          q_stride, None if qg is None else qg.ctypes.data_as(C.c_void_p),
+                          None if kg is None else kg.ctypes.data_as(C.c_void_p), eps,
+                          weight_offset,
+                          None if fr is None else fr.ctypes.data_as(C.c_void_p), rotary_dims)
+    return q, k
+
+
+# ------------------------------------------------------------- delta rule
+def delta_step(state, key, query, value, decay, per_key, beta):
+    """kernels::deltaStep restated; updates `state` in place, returns out."""
+    K, V = state.shape
+    out = np.zeros(V, np.float32)
+    pred = np.zeros(V, np.float32)
+    delta = np.zeros(V, np.float32)
+    lib().or_delta_step(state.reshape(-1), np.ascontiguousarray(key, np.float32),
+                        np.ascontiguousarray(query, np.float32),
+                        np.ascontiguousarray(value, np.float32),
+                        np.ascontiguousarray(decay, np.float32), int(per_key), beta, K, V, out,
+                        pred, delta)
+    return out
+
+
+def gdn_gates(a, b, a_log, dt_bias):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    g = np.zeros_like(a)
+    beta = np.zeros_like(a)
+    count, nv = a.shape
+    lib().or_gdn_gates(a.reshape(-1), b.reshape(-1), np.ascontiguousarray(a_log, np.float32),
+                       np.ascontiguousarray(dt_bias, np.float32), g.reshape(-1),
+                       beta.reshape(-1), count, nv)
+    return g, beta
+
+
+def gated_delta_rule(q, k, v, g, beta, state=None, normalize=True, nthreads=1):
+    """gatedDeltaNetMixer recurrence restated. q,k [S][Hk][KD], v [S][Hv][VD],
+    g, beta [S][Hv]. Returns (out [S][Hv][VD], final state [Hv][KD][VD])."""
+    S, Hk, KD = q.shape
+    _, Hv, VD = v.shape
+    st = (np.zeros((Hv, KD, VD), np.float32) if state is None
+          else np.ascontiguousarray(state, np.float32).copy())
+    out = np.zeros((S, Hv, VD), np.float32)
+    lib().or_gated_delta_rule(np.ascontiguousarray(q, np.float32).reshape(-1),
+                              np.ascontiguousarray(k, np.float32).reshape(-1),
+                              np.ascontiguousarray(v, np.float32).reshape(-1),
+                              np.ascontiguousarray(g, np.float32).reshape(-1),
+                              np.ascontiguousarray(beta, np.float32).reshape(-1),
+                              st.reshape(-1), out.reshape(-1), S, Hk, Hv, KD, VD,
+                              int(bool(normalize)),
+                              threads(nthreads) if nthreads != 1 else 1)
+    return out, st

@@ -1,0 +1,70 @@
+/*
+    ref_shim.cpp - C entry points over the reference's own CPU kernels.
+
+    TEST INFRASTRUCTURE ONLY. Compiled by oracle/Makefile from the reference
+    headers where they lie under $(REF) (the read-only hday200202/math-utils
+    checkout); nothing from the reference is copied into this repository. The
+    resulting oracle/_ref/libref_*.so validates the C restatement in
+    oracle.c and may serve as the CPU baseline ("kind": "reference").
+
+    Wrapped, unchanged:
+      ai::kernels::attention   include/ai/Kernels.hpp:132-168
+      ai::kernels::deltaStep   include/ai/Kernels.hpp:105-128
+      ai::kernels::Pool        include/ai/ThreadPool.hpp:33-124
+      math::random::Random     include/math/Random.hpp:15-89
+*/
+#include <sched.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "ai/Kernels.hpp"
+#include "math/Random.hpp"
+
+extern "C" {
+
+/* Restricts the reference pool to the first `n` CPUs of this process's
+   affinity mask, through the reference's own Pool::configure. Must run before
+   the first threaded call; returns the pool size afterwards. */
+int ref_configure_pool(int n) {
+    cpu_set_t set;
+    std::vector<size_t> cpus;
+    if (sched_getaffinity(0, sizeof(set), &set) == 0)
+        for (int c = 0; c < CPU_SETSIZE && (int)cpus.size() < n; ++c)
+            if (CPU_ISSET(c, &set)) cpus.push_back(size_t(c));
+    if (!cpus.empty()) ai::kernels::Pool::configure(cpus);
+    return int(ai::kernels::Pool::instance().size());
+}
+
+void ref_attention(const float* q, const float* keys, const float* values, float* out,
+                   uint64_t count, uint64_t start, uint64_t heads, uint64_t kvHeads,
+                   uint64_t dim, uint64_t qStride, uint64_t window, int threaded) {
+    ai::kernels::attention(q, keys, values, out, count, start, heads, kvHeads, dim, qStride,
+                           window, threaded != 0);
+}
+
+void ref_delta_step(float* state, const float* key, const float* query, const float* value,
+                    const float* decay, int perKeyDecay, float beta, uint64_t keys,
+                    uint64_t values, float* out, float* prediction, float* delta) {
+    ai::kernels::deltaStep(state, key, query, value, decay, perKeyDecay != 0, beta, keys, values,
+                           out, prediction, delta);
+}
+
+float ref_dot(const float* a, const float* b, uint64_t n) { return ai::kernels::dot(a, b, n); }
+
+/* Draws `n` values from Random(seed): kind 0 next() as raw bits, 1 u01,
+   2 normal(0,1), 3 randInt(lo, hi), 4 randDouble(lo, hi). */
+void ref_random(uint64_t seed, int kind, uint64_t n, double lo, double hi, void* out) {
+    math::random::Random rng(seed);
+    for (uint64_t i = 0; i < n; ++i) {
+        switch (kind) {
+        case 0: static_cast<uint64_t*>(out)[i] = rng(); break;
+        case 1: static_cast<double*>(out)[i] = rng.u01(); break;
+        case 2: static_cast<double*>(out)[i] = rng.normal(); break;
+        case 3: static_cast<int64_t*>(out)[i] = rng.randInt(int64_t(lo), int64_t(hi)); break;
+        default: static_cast<double*>(out)[i] = rng.randDouble(lo, hi); break;
+        }
+    }
+}
+
+} // extern "C"

@@ -1,0 +1,97 @@
+"""GPU parity of the fp32 attention path (the drop-in for kernels::attention)
+against the oracle and the reference kernels' golden outputs."""
+import os
+
+import numpy as np
+import pytest
+
+from common import assert_f32_parity, attention_fp64, errors
+from gpu_util import dev_bf16, dev_f32, host, say
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_kernels.npz")
+
+
+def test_cfg1_gpt2_mha_prefill_fp32(gpu):
+    """batch 1, 12 heads, head_dim 64, seq 128, N(0,1) seed 0."""
+    S, H, D = 128, 12, 64
+    q = O.fill_normal((S, H, D), 0, "q")
+    k = O.fill_normal((S, H, D), 0, "k")
+    v = O.fill_normal((S, H, D), 0, "v")
+    ref = O.attention(q, k, v, S, 0, H, H, D, D)
+    say("cfg1 aigpu_attention", S, H, D)
+    got = gpu.attention(q, k, v, S, 0, H, H, D, D)
+    assert_f32_parity(ref, got, "cfg1")
+
+
+@pytest.mark.parametrize("window", [0, 1, 7, 200])
+def test_reference_unit_case_windows(gpu, window):
+    """llm-testing.cpp:106-134: T=19 after S=11 cached, 4 heads over 2, D=48,
+    qStride 96, against the reference kernel's own outputs."""
+    g = np.load(GOLDEN)
+    T, S, H, KV, D, ST = 19, 11, 4, 2, 48, 96
+    say("llm-testing window", window)
+    got = gpu.attention(g["llm_q"], g["llm_k"], g["llm_v"], T, S, H, KV, D, ST, window)
+    assert_f32_parity(g[f"llm_out_serial_w{window}"], got, f"window {window}")
+    # the reference test's own bar against the fp64 closed form
+    ref64 = attention_fp64(g["llm_q"], g["llm_k"], g["llm_v"], T, S, H, KV, D, ST, window)
+    assert np.abs(got - ref64).max() < 2e-6
+
+
+def test_gqa_with_history_golden(gpu):
+    g = np.load(GOLDEN)
+    say("gqa history golden")
+    got = gpu.attention(g["gqa_q"], g["gqa_k"], g["gqa_v"], 5, 7, 8, 2, 64, 64)
+    assert_f32_parity(g["gqa_out"], got, "gqa")
+
+
+def test_long_context_single_token(gpu):
+    L, H, KV, D = 5000, 8, 2, 128
+    q = O.fill_normal((1, H, D), 5, "q")
+    k = O.fill_normal((L + 1, KV, D), 5, "k")
+    v = O.fill_normal((L + 1, KV, D), 5, "v")
+    ref = O.attention(q, k, v, 1, L, H, KV, D, D)
+    say("long context single token", L)
+    got = gpu.attention(q, k, v, 1, L, H, KV, D, D)
+    assert_f32_parity(ref, got, "long")
+
+
+def test_device_form_head_major_bf16_cache(gpu):
+    """one entry serves the head-major bf16 cache through explicit strides"""
+    import torch
+    cnt, start, H, KV, D, cap = 9, 40, 8, 4, 128, 64
+    qbits = O.pack_bf16(O.fill_normal((cnt, H, D), 6, "q"))
+    kbits = O.pack_bf16(O.fill_normal((KV, cap, D), 6, "k"))
+    vbits = O.pack_bf16(O.fill_normal((KV, cap, D), 6, "v"))
+    qf, kf, vf = O.unpack_bf16(qbits), O.unpack_bf16(kbits), O.unpack_bf16(vbits)
+    ref = O.attention_strided(qf.reshape(-1), kf, vf, cnt, start, H, KV, D, D, D, cap * D)
+    out = torch.zeros((cnt, H, D), dtype=torch.float32, device="cuda")
+    say("device form head-major bf16")
+    gpu.attention_device(dev_bf16(qbits), dev_bf16(kbits), dev_bf16(vbits), out, cnt, start, H, KV,
+                         D, D, D, cap * D)
+    assert_f32_parity(ref.reshape(cnt, H, D), host(out), "head-major")
+
+
+def test_empty_and_invalid(gpu):
+    q = np.zeros((1, 3, 8), np.float32)
+    kv = np.zeros((1, 2, 8), np.float32)
+    say("empty and invalid")
+    out = gpu.attention(q, kv, kv, 0, 0, 3, 1, 8, 8)
+    assert out.shape == (0, 3, 8)
+    with pytest.raises(gpu.AiGpuError):
+        gpu.attention(q, kv, kv, 1, 0, 3, 2, 8, 8)      # heads not a multiple of kvHeads
+    assert "multiple" in gpu.last_error()
+
+
+def test_counters_track_transfers(gpu):
+    gpu.lib().aigpu_reset_counters()
+    q = O.fill_normal((4, 2, 32), 7, "q")
+    k = O.fill_normal((4, 2, 32), 7, "k")
+    say("counters")
+    gpu.attention(q, k, k, 4, 0, 2, 2, 32, 32)
+    c = gpu.counters()
+    assert c["launches"] >= 1 and c["hostToDeviceBytes"] >= q.nbytes + 2 * k.nbytes
+    assert c["deviceToHostBytes"] == 4 * 2 * 32 * 4
+    assert errors(np.zeros(1), np.zeros(1))["max_abs"] == 0

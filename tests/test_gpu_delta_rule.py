@@ -1,0 +1,100 @@
+"""GPU parity of the gated delta rule (chunked scan) against the oracle's
+sequential restatement of gatedDeltaNetMixer's recurrence
+(LocalModel.hpp:2802-2830, deltaStep at Kernels.hpp:105-128)."""
+import numpy as np
+import pytest
+
+from common import assert_bf16_parity, assert_f32_parity, bf16_normal
+from gpu_util import dev_bf16, dev_f32, host, say
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def gates(S, hv, seed):
+    g = -np.log1p(np.exp(O.fill_normal((S, hv), seed, "g").astype(np.float64))).astype(np.float32)
+    beta = (1.0 / (1.0 + np.exp(-O.fill_normal((S, hv), seed, "beta").astype(np.float64)))).astype(np.float32)
+    return g, beta
+
+
+def run_gdn(gpu, S, hk, hv, kd, vd, seed, dtype="f32", state0=None, raw_gates=False):
+    import torch
+    if dtype == "bf16":
+        qb, q = bf16_normal((S, hk, kd), seed, "q")
+        kb, k = bf16_normal((S, hk, kd), seed, "k")
+        vb, v = bf16_normal((S, hv, vd), seed, "v")
+        dq, dk, dv = dev_bf16(qb), dev_bf16(kb), dev_bf16(vb)
+    else:
+        q = O.fill_normal((S, hk, kd), seed, "q")
+        k = O.fill_normal((S, hk, kd), seed, "k")
+        v = O.fill_normal((S, hv, vd), seed, "v")
+        dq, dk, dv = dev_f32(q), dev_f32(k), dev_f32(v)
+    s0 = np.zeros((hv, kd, vd), np.float32) if state0 is None else state0
+    state = dev_f32(s0)
+    out = torch.zeros((S, hv, vd), dtype=torch.float32, device="cuda")
+    say("delta rule", dict(S=S, hk=hk, hv=hv, kd=kd, vd=vd, dtype=dtype, raw=raw_gates))
+    if raw_gates:
+        a = O.fill_normal((S, hv), seed, "a")
+        b = O.fill_normal((S, hv), seed, "b")
+        alog = O.fill_normal((hv,), seed, "alog") * np.float32(0.5)
+        dt = O.fill_normal((hv,), seed, "dt")
+        g, beta = O.gdn_gates(a, b, alog, dt)
+        gpu.gated_delta_rule(dq, dk, dv, state, out, a=dev_f32(a), b=dev_f32(b), a_log=dev_f32(alog),
+                             dt_bias=dev_f32(dt))
+    else:
+        g, beta = gates(S, hv, seed)
+        gpu.gated_delta_rule(dq, dk, dv, state, out, g=dev_f32(g), beta=dev_f32(beta))
+    ref_out, ref_state = O.gated_delta_rule(q, k, v, g, beta, state=s0, nthreads=0)
+    return ref_out, host(out), ref_state, host(state)
+
+
+@pytest.mark.parametrize("S", [1, 63, 64, 65, 200])
+def test_lengths_fp32(gpu, S):
+    ro, go, rs, gs = run_gdn(gpu, S, 2, 4, 128, 128, 100 + S)
+    assert_f32_parity(ro, go, f"out S={S}")
+    assert_f32_parity(rs, gs, f"state S={S}")
+
+
+def test_raw_gates_and_initial_state(gpu):
+    s0 = O.fill_normal((4, 128, 64), 7, "s0") * np.float32(0.1)
+    ro, go, rs, gs = run_gdn(gpu, 150, 2, 4, 128, 64, 7, state0=s0, raw_gates=True)
+    assert_f32_parity(ro, go, "out raw gates")
+    assert_f32_parity(rs, gs, "state raw gates")
+
+
+def test_key_dim_64(gpu):
+    ro, go, rs, gs = run_gdn(gpu, 100, 4, 4, 64, 32, 8)
+    assert_f32_parity(ro, go, "out kd64")
+    assert_f32_parity(rs, gs, "state kd64")
+
+
+def test_chunk_continuation(gpu):
+    """a split call (state carried) equals one call: chunk continuity, the
+    kernel-level form of llm-testing.cpp:853-890"""
+    import torch
+    S, hk, hv, kd, vd = 130, 2, 4, 128, 32
+    q = O.fill_normal((S, hk, kd), 9, "q")
+    k = O.fill_normal((S, hk, kd), 9, "k")
+    v = O.fill_normal((S, hv, vd), 9, "v")
+    g, beta = gates(S, hv, 9)
+    whole_state = dev_f32(np.zeros((hv, kd, vd), np.float32))
+    whole = torch.zeros((S, hv, vd), dtype=torch.float32, device="cuda")
+    say("continuation")
+    gpu.gated_delta_rule(dev_f32(q), dev_f32(k), dev_f32(v), whole_state, whole, g=dev_f32(g), beta=dev_f32(beta))
+    split_state = dev_f32(np.zeros((hv, kd, vd), np.float32))
+    parts = []
+    for lo, hi in ((0, 64), (64, 100), (100, 130)):
+        o = torch.zeros((hi - lo, hv, vd), dtype=torch.float32, device="cuda")
+        gpu.gated_delta_rule(dev_f32(q[lo:hi]), dev_f32(k[lo:hi]), dev_f32(v[lo:hi]), split_state, o,
+                             g=dev_f32(g[lo:hi]), beta=dev_f32(beta[lo:hi]))
+        parts.append(host(o))
+    assert_f32_parity(host(whole), np.concatenate(parts), "continuation out")
+    assert_f32_parity(host(whole_state), host(split_state), "continuation state")
+
+
+def test_cfg5_qwen3_next_16k(gpu):
+    """16 qk / 32 v heads, D 128, seq 16384, chunk 64, bf16 inputs,
+    l2-normalised q/k, beta = sigmoid(N(0,1)), g = -softplus(N(0,1)), seed 4."""
+    ro, go, rs, gs = run_gdn(gpu, 16384, 16, 32, 128, 128, 4, dtype="bf16")
+    say("cfg5 out", assert_bf16_parity(ro, go, "cfg5 out"))
+    say("cfg5 state", assert_bf16_parity(rs, gs, "cfg5 state"))

@@ -1,0 +1,120 @@
+"""GPU parity of the prefill path (QK-RMSNorm -> RoPE -> KV append -> causal
+GQA flash attention on fp16 MFMA) against the oracle restatement of
+attentionMixer (LocalModel.hpp:2608-2659) + kernels::attention."""
+import numpy as np
+import pytest
+
+from common import assert_bf16_parity, bf16_normal, errors, gammas
+from gpu_util import dev_bf16, dev_f32, host, host_bits, say
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(gpu, count, start, H, KV, D, seed, norm=True, rope=True, window=0, dtype="bf16",
+             rows=None, theta=1e6, q_stride=None):
+    """Builds seeded inputs, runs the GPU prefill and the oracle; returns
+    (oracle out, gpu out, oracle-normed keys, gpu caches)."""
+    import torch
+    qs = q_stride or D
+    cap = start + count + 3
+    if dtype == "bf16":
+        qb, q = bf16_normal((count, H, qs), seed, "q")
+        kb, k = bf16_normal((count, KV, D), seed, "k")
+        vb, v = bf16_normal((count, KV, D), seed, "v")
+        dq, dk, dv = dev_bf16(qb), dev_bf16(kb), dev_bf16(vb)
+    else:
+        q = O.fill_normal((count, H, qs), seed, "q")
+        k = O.fill_normal((count, KV, D), seed, "k")
+        v = O.fill_normal((count, KV, D), seed, "v")
+        dq, dk, dv = dev_f32(q), dev_f32(k), dev_f32(v)
+    gq = gammas(D, seed, "q_norm") if norm else None
+    gk = gammas(D, seed, "k_norm") if norm else None
+    fr = O.rotary_frequencies(D, theta) if rope else None
+    # cached history [0, start): bf16 values in the head-major cache
+    hkb, hk = bf16_normal((KV, start, D), seed, "k_cache")
+    hvb, hv = bf16_normal((KV, start, D), seed, "v_cache")
+    kc = np.zeros((KV, cap, D), np.uint16)
+    vc = np.zeros((KV, cap, D), np.uint16)
+    kc[:, :start] = hkb
+    vc[:, :start] = hvb
+    key_cache, value_cache = dev_bf16(kc), dev_bf16(vc)
+
+    # oracle: norm + RoPE on fp32 (widened) inputs, then attention over history + new
+    qn, kn = O.qk_norm_rope(q, k, count, start, H, KV, D, qs, gq, gk, 1e-6, fr, D)
+    keys = np.concatenate([hk.transpose(1, 0, 2), kn], 0)
+    vals = np.concatenate([hv.transpose(1, 0, 2), v], 0)
+    ref = O.attention_strided(qn, keys, vals, count, start, H, KV, D, qs, KV * D, D, window,
+                              rows=rows, nthreads=0)
+
+    out = torch.zeros((count, H, D), dtype=torch.float32, device="cuda")
+    say("prefill", dict(count=count, start=start, H=H, KV=KV, D=D, window=window, dtype=dtype))
+    gpu.prefill(dq, dk, dv, out, key_cache, value_cache, start, H, KV, D, q_stride=qs,
+                q_norm=None if gq is None else dev_f32(gq),
+                k_norm=None if gk is None else dev_f32(gk),
+                freqs=None if fr is None else dev_f32(fr), rotary_dims=D, window=window)
+    got = host(out)
+    if rows is not None:
+        got = got[rows]
+    return ref, got, kn, v, host(key_cache), host_bits(value_cache), vb if dtype == "bf16" else None
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_small_gqa_norm_rope(gpu, D):
+    ref, got, kn, v, kc, vcb, vb = run_case(gpu, 300, 0, 8, 2, D, 40)
+    assert_bf16_parity(ref, got, f"D={D}")
+
+
+def test_cache_append_layout(gpu):
+    count, start, KV, D = 70, 25, 2, 128
+    ref, got, kn, v, kc, vcb, vb = run_case(gpu, count, start, 4, KV, D, 41)
+    assert_bf16_parity(ref, got, "history")
+    # new keys land at [kv][start + t] as bf16 of the normed, rotated key
+    new_k = kc[:, start:start + count].transpose(1, 0, 2)
+    assert np.abs(new_k - kn).max() <= np.abs(kn).max() * 2 ** -8
+    # values are appended unchanged
+    assert np.array_equal(vcb[:, start:start + count].transpose(1, 0, 2), vb)
+
+
+def test_fp32_inputs_mha_no_norm_no_rope(gpu):
+    ref, got, *_ = run_case(gpu, 129, 0, 12, 12, 64, 42, norm=False, rope=False, dtype="f32")
+    assert_bf16_parity(ref, got, "mha fp32 inputs")
+
+
+@pytest.mark.parametrize("window", [1, 33, 100])
+def test_sliding_window(gpu, window):
+    ref, got, *_ = run_case(gpu, 250, 10, 4, 2, 128, 43, window=window)
+    assert_bf16_parity(ref, got, f"window {window}")
+
+
+def test_q_stride_with_gate_halves(gpu):
+    # Qwen3.5-style q rows carry a gate after each head (qStride = 2D, LocalModel.hpp:2583)
+    ref, got, *_ = run_case(gpu, 40, 0, 4, 2, 64, 44, q_stride=128)
+    assert_bf16_parity(ref, got, "qStride 2D")
+
+
+def test_single_token_and_ragged_tiles(gpu):
+    for count in (1, 127, 128, 129):
+        ref, got, *_ = run_case(gpu, count, 0, 4, 4, 128, 45 + count)
+        assert_bf16_parity(ref, got, f"count {count}")
+
+
+def test_cfg3_qwen3_8b_prefill_8k_sampled_rows(gpu):
+    """32 q / 8 kv heads, D 128, seq 8192, QK-norm + RoPE theta 1e6,
+    N(0,1) bf16 seed 2. Full GPU run; oracle on sampled rows (every row is an
+    independent softmax, so a row subset checks the full-size kernel)."""
+    rows = list(range(0, 64)) + list(range(64, 8128, 97)) + list(range(8128, 8192))
+    ref, got, *_ = run_case(gpu, 8192, 0, 32, 8, 128, 2, rows=rows)
+    e = assert_bf16_parity(ref, got, "cfg3")
+    say("cfg3 errors", e)
+
+
+def test_rejects_unsupported_dim(gpu):
+    import torch
+    x = torch.zeros((2, 2, 96), dtype=torch.bfloat16, device="cuda")
+    kc = torch.zeros((2, 4, 96), dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros((2, 2, 96), dtype=torch.float32, device="cuda")
+    with pytest.raises(gpu.AiGpuError):
+        gpu.prefill(x, x, x, out, kc, kc, 0, 2, 2, 96)
+    assert "dim" in gpu.last_error()
+    assert errors(np.ones(2), np.ones(2))["rel_l2"] == 0

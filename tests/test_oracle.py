@@ -1,0 +1,390 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each function is checked against something other than a retyping of its own
+formula: the reference's compiled kernels (golden vectors from oracle/_ref),
+the reference's own unit tests restated (llm-testing.cpp), fp64 closed forms,
+and invariants a plausible mistake would break.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from common import attention_fp64 as _attention_fp64
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_kernels.npz")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN)
+
+
+# ------------------------------------------------------------------- RNG
+def _xoshiro_python(seed, n):
+    """splitmix64 seeding + xoshiro256++ from the published algorithms
+    (Vigna), written independently in Python."""
+    M = (1 << 64) - 1
+
+    def splitmix(x):
+        x = (x + 0x9E3779B97F4A7C15) & M
+        z = x
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        return x, z ^ (z >> 31)
+
+    s = []
+    x = seed
+    for _ in range(4):
+        x, z = splitmix(x)
+        s.append(z)
+
+    def rotl(v, k):
+        return ((v << k) | (v >> (64 - k))) & M
+
+    out = []
+    for _ in range(n):
+        out.append((rotl((s[0] + s[3]) & M, 23) + s[0]) & M)
+        t = (s[1] << 17) & M
+        s[2] ^= s[0]
+        s[3] ^= s[1]
+        s[1] ^= s[2]
+        s[0] ^= s[3]
+        s[2] ^= t
+        s[3] = rotl(s[3], 45)
+    return out
+
+
+def test_rng_matches_reference_random(golden):
+    r = O.Rng(12345)
+    assert [r.next() for _ in range(64)] == [int(x) for x in golden["rng_raw_seed12345"]]
+    r = O.Rng(7)
+    assert np.array_equal(np.array([r.normal() for _ in range(64)]), golden["rng_normal_seed7"])
+    r = O.Rng(3)
+    assert [r.randint(1024, 32768) for _ in range(32)] == list(golden["rng_randint_1024_32768_seed3"])
+    r = O.Rng(11)
+    assert np.array_equal(np.array([r.uniform(0.5, 1.5) for _ in range(16)]),
+                          golden["rng_uniform_05_15_seed11"])
+
+
+def test_rng_matches_published_xoshiro256pp():
+    r = O.Rng(2024)
+    assert [r.next() for _ in range(16)] == _xoshiro_python(2024, 16)
+
+
+def test_rng_known_answer_first_output():
+    # state {1,2,3,4} is not reachable through seeding, so check the first
+    # output's closed form on the seeded state instead: rotl(s0+s3, 23) + s0
+    M = (1 << 64) - 1
+    x = 99
+    s = []
+    for _ in range(4):
+        x = (x + 0x9E3779B97F4A7C15) & M
+        z = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        s.append(z ^ (z >> 31))
+    v = (s[0] + s[3]) & M
+    expect = ((((v << 23) | (v >> 41)) & M) + s[0]) & M
+    assert O.Rng(99).next() == expect
+
+
+def test_normal_moments_and_uniform_range():
+    x = O.fill_normal((1 << 16,), 5, "moments")
+    assert abs(x.mean()) < 0.02 and abs(x.std() - 1) < 0.02
+    u = O.fill_uniform((1 << 14,), 5, "u", 0.5, 1.5)
+    assert u.min() >= 0.5 and u.max() <= 1.5 and abs(u.mean() - 1.0) < 0.01
+
+
+def test_fill_is_chunked_and_thread_independent():
+    a = O.fill_normal((70000,), 9, "t", nthreads=1)
+    b = O.fill_normal((70000,), 9, "t", nthreads=4)
+    assert np.array_equal(a, b)
+    # chunk c draws from Random(seed ^ fnv1a(name) + c * golden)
+    base = 9 ^ O.lib().or_fnv1a(b"t")
+    r = O.Rng((base + 2 * 0x9E3779B97F4A7C15) & ((1 << 64) - 1))
+    assert a[2 * 16384] == np.float32(r.normal())
+
+
+def test_fnv1a_published_vectors():
+    assert O.lib().or_fnv1a(b"") == 0xCBF29CE484222325
+    assert O.lib().or_fnv1a(b"a") == 0xAF63DC4C8601EC8C
+    assert O.lib().or_fnv1a(b"foobar") == 0x85944171F73967E8
+
+
+def test_bf16_rounding_is_nearest_even():
+    x = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, 1.0 + 2 ** -9, -2.5, 3.0e38], np.float32)
+    got = O.round_bf16(x)
+    assert got[0] == 1.0
+    assert got[1] == 1.0                     # tie -> even
+    assert got[2] == np.float32(1.0 + 4 * 2 ** -8)  # tie -> even (up)
+    assert got[3] == 1.0
+    assert got[4] == -2.5
+    assert np.isfinite(got[5])
+
+
+# ------------------------------------------------------------- attention
+def test_attention_bitexact_vs_reference_kernels(golden):
+    T, S, H, KV, D, ST = 19, 11, 4, 2, 48, 96
+    for w in (0, 1, 7, 200):
+        serial = O.attention(golden["llm_q"], golden["llm_k"], golden["llm_v"], T, S, H, KV, D, ST, w)
+        threaded = O.attention(golden["llm_q"], golden["llm_k"], golden["llm_v"], T, S, H, KV, D, ST,
+                               w, nthreads=4)
+        assert np.array_equal(serial.reshape(-1), golden[f"llm_out_serial_w{w}"])
+        assert np.array_equal(threaded.reshape(-1), golden[f"llm_out_w{w}"])
+        assert np.array_equal(serial, threaded)
+
+
+def test_attention_matches_fp64_closed_form(golden):
+    # llm-testing.cpp:106-134: windows {0,1,7,200}, tolerance 2e-6
+    T, S, H, KV, D, ST = 19, 11, 4, 2, 48, 96
+    for w in (0, 1, 7, 200):
+        got = O.attention(golden["llm_q"], golden["llm_k"], golden["llm_v"], T, S, H, KV, D, ST, w)
+        ref = _attention_fp64(golden["llm_q"], golden["llm_k"], golden["llm_v"], T, S, H, KV, D, ST, w)
+        assert np.abs(got - ref).max() < 2e-6
+
+
+def test_attention_gqa_history_bitexact(golden):
+    got = O.attention(golden["gqa_q"], golden["gqa_k"], golden["gqa_v"], 5, 7, 8, 2, 64, 64)
+    assert np.array_equal(got, golden["gqa_out"])
+
+
+def test_attention_strided_equals_position_major():
+    cnt, start, h, kv, d = 6, 10, 4, 2, 32
+    q = O.fill_normal((cnt, h, d), 1, "q")
+    k = O.fill_normal((start + cnt, kv, d), 1, "k")
+    v = O.fill_normal((start + cnt, kv, d), 1, "v")
+    base = O.attention(q, k, v, cnt, start, h, kv, d, d)
+    kh = np.ascontiguousarray(k.transpose(1, 0, 2))   # head-major [kv][pos][d]
+    vh = np.ascontiguousarray(v.transpose(1, 0, 2))
+    got = O.attention_strided(q, kh, vh, cnt, start, h, kv, d, d, d, (start + cnt) * d)
+    assert np.array_equal(base, got)
+    rows = [0, 3, 5]
+    sub = O.attention_strided(q, k, v, cnt, start, h, kv, d, d, kv * d, d, rows=rows)
+    assert np.array_equal(sub, base[rows])
+
+
+def test_softmax_overflow_row_fixture():
+    # make_fixtures.py:117-120: the row [1, 2, 900, 3] must not overflow.
+    # One query with dim 1 and q = 1 makes the scores exactly the keys.
+    keys = np.array([1.0, 2.0, 900.0, 3.0], np.float32).reshape(4, 1, 1)
+    values = np.eye(4, dtype=np.float32).reshape(4, 1, 4)
+    # dim is 1 for the scores but the values need 4 columns: run per column
+    out = np.zeros(4)
+    for col in range(4):
+        vcol = np.ascontiguousarray(values[:, :, col:col + 1])
+        out[col] = O.attention(np.ones((1, 1, 1), np.float32), keys, vcol, 1, 3, 1, 1, 1, 1)[0, 0, 0]
+    x = np.array([1.0, 2.0, 900.0, 3.0])
+    ref = np.exp(x - x.max()) / np.exp(x - x.max()).sum()
+    assert np.all(np.isfinite(out)) and np.abs(out - ref).max() < 1e-7
+
+
+def test_causal_mask_fixture():
+    # make_fixtures.py:124-129: causal mask then softmax, position t sees 0..t
+    rng = np.random.default_rng(0)
+    d = 8
+    q = rng.standard_normal((4, 1, d)).astype(np.float32)
+    k = rng.standard_normal((4, 1, d)).astype(np.float32)
+    v = rng.standard_normal((4, 1, d)).astype(np.float32)
+    got = O.attention(q, k, v, 4, 0, 1, 1, d, d)
+    scores = (q[:, 0].astype(np.float64) @ k[:, 0].T.astype(np.float64)) / np.sqrt(d)
+    scores = np.where(np.triu(np.ones((4, 4), bool), 1), -1e10, scores)
+    p = np.exp(scores - scores.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    assert np.abs(got[:, 0] - p @ v[:, 0]).max() < 2e-6
+
+
+def test_attention_first_token_returns_its_value():
+    q = O.fill_normal((1, 2, 16), 3, "q")
+    k = O.fill_normal((1, 1, 16), 3, "k")
+    v = O.fill_normal((1, 1, 16), 3, "v")
+    out = O.attention(q, k, v, 1, 0, 2, 1, 16, 16)
+    assert np.array_equal(out[0, 0], v[0, 0]) and np.array_equal(out[0, 1], v[0, 0])
+
+
+# ------------------------------------------------------------ norm, RoPE
+def test_rotary_frequencies_closed_form():
+    f = O.rotary_frequencies(128, 1e6)
+    j = np.arange(64)
+    ref = 1.0 / np.power(1e6, 2 * j / 128.0)
+    assert np.abs(f / ref - 1).max() < 2e-6
+    assert f[0] == 1.0
+
+
+def test_rotary_scaling_matches_reference_tests():
+    # llm-testing.cpp:141-142: linear factor 4 gives 0.25 for the first pair
+    f = O.rotary_frequencies(64, 10000.0, kind=1, factor=4)
+    assert abs(f[0] - 0.25) < 1e-7
+    # llm-testing.cpp:143-144: llama3 keeps the highest frequency, shrinks the lowest
+    f = O.rotary_frequencies(128, 500000.0, kind=2, factor=8, low=1, high=4, original=8192)
+    assert f[0] == 1.0 and f[-1] < 1e-6
+    with pytest.raises(ValueError):      # llm-testing.cpp:149-150
+        O.rotary_frequencies(64, 10000.0, kind=1, factor=0)
+
+
+def test_rms_norm_closed_form_and_invariant():
+    x = O.fill_normal((3, 96), 4, "x") * np.float32(3.0)
+    gamma = O.fill_uniform((96,), 4, "g", 0.5, 1.5)
+    out = np.zeros(96, np.float32)
+    for row in x:
+        O.lib().or_rms_norm_row(np.ascontiguousarray(row), gamma, out, 96, 1e-6, 0.0)
+        ref = row.astype(np.float64) / np.sqrt(np.mean(row.astype(np.float64) ** 2) + 1e-6) * gamma
+        assert np.abs(out - ref).max() < 1e-5
+        assert abs(np.sqrt(np.mean((out / gamma) ** 2)) - 1.0) < 1e-5
+
+
+def test_qk_norm_rope_invariants():
+    cnt, h, kv, d = 5, 4, 2, 64
+    q = O.fill_normal((cnt, h, d), 6, "q")
+    k = O.fill_normal((cnt, kv, d), 6, "k")
+    fr = O.rotary_frequencies(d, 1e6)
+    # RoPE alone preserves every pair's norm and is the identity at position 0
+    q2, k2 = O.qk_norm_rope(q, k, cnt, 0, h, kv, d, d, None, None, 1e-6, fr, d)
+    assert np.array_equal(q2[0], q[0]) and np.array_equal(k2[0], k[0])
+    half = d // 2
+    n0 = q[..., :half] ** 2 + q[..., half:] ** 2
+    n1 = q2[..., :half] ** 2 + q2[..., half:] ** 2
+    assert np.abs(n1 - n0).max() < 1e-5
+    # matches an fp64 rotation at a large position
+    start = 8000
+    q3, _ = O.qk_norm_rope(q, k, cnt, start, h, kv, d, d, None, None, 1e-6, fr, d)
+    ang = (np.arange(start, start + cnt, dtype=np.float32)[:, None] * fr[None, :]).astype(np.float32)
+    c, s = np.cos(ang.astype(np.float64)), np.sin(ang.astype(np.float64))
+    a, b = q[..., :half].astype(np.float64), q[..., half:].astype(np.float64)
+    ref = np.concatenate([a * c[:, None] - b * s[:, None], b * c[:, None] + a * s[:, None]], -1)
+    assert np.abs(q3 - ref).max() < 1e-5
+
+
+def test_qk_norm_then_rope_order():
+    # norm first, then rotate (LocalModel.hpp:2608-2643): the rotated row keeps rms(x/gamma)=1
+    cnt, h, kv, d = 2, 2, 1, 32
+    q = O.fill_normal((cnt, h, d), 8, "q") * np.float32(4)
+    k = O.fill_normal((cnt, kv, d), 8, "k")
+    ones = np.ones(d, np.float32)
+    fr = O.rotary_frequencies(d, 1e6)
+    q2, _ = O.qk_norm_rope(q, k, cnt, 3, h, kv, d, d, ones, ones, 1e-6, fr, d)
+    assert np.abs(np.sqrt(np.mean(q2.astype(np.float64) ** 2, -1)) - 1).max() < 1e-5
+
+
+# ----------------------------------------------------------- delta rule
+def _four_pass(state, key, query, value, decay, per_key, beta):
+    """llm-testing.cpp:830-841: the independent four-pass update."""
+    K, V = state.shape
+    state *= (decay[:, None] if per_key else decay[0])
+    kv = np.zeros(V, np.float32)
+    for i in range(K):
+        kv += state[i] * key[i]
+    delta = (value - kv) * np.float32(beta)
+    for i in range(K):
+        state[i] += key[i] * delta
+    out = np.zeros(V, np.float32)
+    for i in range(K):
+        out += state[i] * query[i]
+    return out
+
+
+@pytest.mark.parametrize("dims", [(3, 7), (32, 64), (128, 128)])
+@pytest.mark.parametrize("per_key", [False, True])
+def test_delta_step_matches_four_pass(dims, per_key):
+    # llm-testing.cpp:813-851: 37 tokens, beta 0.35, decay .8+.02*(i%7), tol 1e-6
+    K, V = dims
+    actual = (np.sin(np.arange(K * V, dtype=np.float32) * np.float32(0.3)) * np.float32(0.01)).reshape(K, V)
+    expected = actual.copy()
+    worst = 0.0
+    for t in range(37):
+        i = np.arange(K, dtype=np.float32)
+        key = (np.sin((i + t) * np.float32(0.7)) / np.float32(np.sqrt(K))).astype(np.float32)
+        query = (np.cos((i + t) * np.float32(0.4)) / np.float32(K)).astype(np.float32)
+        decay = (np.float32(0.8) + (np.arange(K) % 7).astype(np.float32) * np.float32(0.02)).astype(np.float32)
+        value = np.sin((np.arange(V, dtype=np.float32) + t) * np.float32(0.17)).astype(np.float32)
+        ref = _four_pass(expected, key, query, value, decay, per_key, 0.35)
+        got = O.delta_step(actual, key, query, value, decay, per_key, 0.35)
+        worst = max(worst, np.abs(actual - expected).max(), np.abs(got - ref).max())
+    assert worst < 1e-6
+
+
+@pytest.mark.parametrize("tag", ["delta_32x64_scalar", "delta_32x64_channel", "delta_128x128_scalar"])
+def test_delta_step_bitexact_vs_reference_kernel(golden, tag):
+    state = golden[tag + "_state0"].copy()
+    per_key = "channel" in tag
+    for t in range(golden[tag + "_keys"].shape[0]):
+        out = O.delta_step(state, golden[tag + "_keys"][t], golden[tag + "_queries"][t],
+                           golden[tag + "_values"][t], golden[tag + "_decays"][t], per_key,
+                           float(golden[tag + "_betas"][t]))
+        assert np.array_equal(out, golden[tag + "_outs"][t])
+    assert np.array_equal(state, golden[tag + "_state"])
+
+
+def _gdn_inputs(S, hk, hv, kd, vd, seed):
+    q = O.fill_normal((S, hk, kd), seed, "q")
+    k = O.fill_normal((S, hk, kd), seed, "k")
+    v = O.fill_normal((S, hv, vd), seed, "v")
+    g = -np.log1p(np.exp(O.fill_normal((S, hv), seed, "g"))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-O.fill_normal((S, hv), seed, "beta")))).astype(np.float32)
+    return q, k, v, g, beta
+
+
+def test_gated_delta_rule_is_repeated_delta_step():
+    S, hk, hv, kd, vd = 7, 2, 4, 16, 8
+    q, k, v, g, beta = _gdn_inputs(S, hk, hv, kd, vd, 12)
+    out, st = O.gated_delta_rule(q, k, v, g, beta)
+    state = np.zeros((hv, kd, vd), np.float32)
+    for t in range(S):
+        for h in range(hv):
+            kh = h // (hv // hk)
+            qq = q[t, kh].astype(np.float64)
+            kk = k[t, kh].astype(np.float64)
+            qq = (qq / np.sqrt((qq ** 2).sum() + 1e-6)) / np.sqrt(kd)
+            kk = kk / np.sqrt((kk ** 2).sum() + 1e-6)
+            s64 = state[h].astype(np.float64) * np.exp(np.float64(g[t, h]))
+            delta = beta[t, h] * (v[t, h] - s64.T @ kk)
+            s64 += np.outer(kk, delta)
+            assert np.abs(out[t, h] - s64.T @ qq).max() < 1e-5
+            state[h] = s64
+    assert np.abs(st - state).max() < 1e-5
+
+
+def test_gated_delta_rule_special_cases():
+    S, hk, hv, kd, vd = 5, 1, 2, 8, 4
+    q, k, v, g, beta = _gdn_inputs(S, hk, hv, kd, vd, 13)
+    s0 = O.fill_normal((hv, kd, vd), 13, "s0")
+    # beta = 0: the state only decays, by exp(sum g)
+    _, st = O.gated_delta_rule(q, k, v, g, np.zeros_like(beta), state=s0)
+    decay = np.exp(g.astype(np.float64).sum(0))
+    assert np.abs(st - s0 * decay[:, None, None]).max() < 1e-5
+    # g = 0, beta = 1 with a unit key: the key's row projection becomes v exactly
+    _, st = O.gated_delta_rule(q[:1], k[:1], v[:1], np.zeros_like(g[:1]), np.ones_like(beta[:1]), state=s0)
+    kk = k[0, 0].astype(np.float64)
+    kk /= np.sqrt((kk ** 2).sum() + 1e-6)
+    assert np.abs(st[0].T @ kk - v[0, 0]).max() < 1e-4
+    # one token equals one deltaStep on normalised inputs
+    out1, st1 = O.gated_delta_rule(q[:1], k[:1], v[:1], g[:1], beta[:1], state=s0)
+    s = s0[1].copy()
+    qq = q[0, 0].copy()
+    kk = k[0, 0].copy()
+    O.lib().or_l2normalise(qq, kd, 1e-6)
+    O.lib().or_l2normalise(kk, kd, 1e-6)
+    qq *= np.float32(1 / np.sqrt(np.float32(kd)))
+    o = O.delta_step(s, kk, qq, v[0, 1], np.array([np.exp(g[0, 1])], np.float32), False, float(beta[0, 1]))
+    assert np.array_equal(o, out1[0, 1]) and np.array_equal(s, st1[1])
+
+
+def test_gdn_gates_closed_form():
+    a = O.fill_normal((6, 3), 14, "a")
+    b = O.fill_normal((6, 3), 14, "b")
+    alog = O.fill_normal((3,), 14, "alog")
+    dt = O.fill_normal((3,), 14, "dt")
+    g, beta = O.gdn_gates(a, b, alog, dt)
+    x = a.astype(np.float64) + dt
+    ref_g = -np.exp(alog.astype(np.float64)) * np.log1p(np.exp(x))
+    assert np.abs(g - ref_g).max() < 1e-5
+    assert np.abs(beta - 1 / (1 + np.exp(-b.astype(np.float64)))).max() < 1e-6
+    # softplus switches to the identity above 20 (LocalModel.hpp:1374-1376)
+    assert O.lib().or_softplus(25.0) == 25.0
+
+
+def test_gated_delta_rule_threads_do_not_change_results():
+    q, k, v, g, beta = _gdn_inputs(20, 2, 4, 16, 16, 15)
+    a = O.gated_delta_rule(q, k, v, g, beta, nthreads=1)
+    b = O.gated_delta_rule(q, k, v, g, beta, nthreads=4)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
