@@ -1,0 +1,401 @@
+#!/usr/bin/env python3
+"""bench.py - throughput of the MI355X attention hot path against its roofline,
+with the reference's CPU path timed beside it.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|delta|all]
+
+A step is one call of the hot path over one batch of synthetic, HBM-resident
+input. The headline workload (config.workload) is configs[2] of BASELINE.json,
+the Qwen3-8B-shaped causal GQA prefill at 8k (32 q / 8 kv heads, head_dim
+128, QK-RMSNorm + RoPE theta 1e6, bf16 in, fp32 accumulate): `value` is its
+whole-step TFLOP/s (norm/RoPE/append + flash attention) with the algorithmic
+count 2*D*Hq*S*(S+1). `decode` carries configs[3] (Qwen3-30B-A3B batched
+ragged decode, KV GB/s with 2048*sum(L_b+1) bytes) in the same form, and
+`others` the remaining configurations.
+
+`roofline` is for the dominant kernel of the step: algorithmic flops (or
+bytes) per launch over its average duration, from hipEvents the backend
+records around every launch on the stream it runs on. `cpu_baseline` is the
+reference's own kernels::attention / deltaStep (compiled from its headers into
+oracle/_ref, "reference"), or the C restatement ("port") where that library
+is absent, timed on the host's cores on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "math-utils_amd"))
+
+PEAK_MFMA_F16 = 2516.6      # TFLOP/s, dense bf16/fp16 MFMA (MI355X spec)
+PEAK_MFMA_F32 = 157.3       # TFLOP/s, fp32
+PEAK_HBM = 8000.0           # GB/s
+CPU_THREADS_CAP = 16        # the GPU box's CPU share for one GPU
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "all"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU time of each baseline sample")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run a 1 GiB device copy first (scales HBM counters in profiles)")
+    return ap.parse_args()
+
+
+# ------------------------------------------------------------ synthetic data
+class Xoshiro:
+    """math::random::Random's randInt (Random.hpp:23-39, 67-86): only used to
+    draw configs[3]'s sequence lengths exactly as the configuration states."""
+    M = (1 << 64) - 1
+
+    def __init__(self, seed):
+        self.s = []
+        x = seed
+        for _ in range(4):
+            x = (x + 0x9E3779B97F4A7C15) & self.M
+            z = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & self.M
+            z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & self.M
+            self.s.append(z ^ (z >> 31))
+
+    def next(self):
+        s, M = self.s, self.M
+        rotl = lambda v, k: ((v << k) | (v >> (64 - k))) & M  # noqa: E731
+        r = (rotl((s[0] + s[3]) & M, 23) + s[0]) & M
+        t = (s[1] << 17) & M
+        s[2] ^= s[0]
+        s[3] ^= s[1]
+        s[1] ^= s[2]
+        s[0] ^= s[3]
+        s[2] ^= t
+        s[3] = rotl(s[3], 45)
+        return r
+
+    def randint(self, lo, hi):
+        span = hi - lo + 1
+        limit = self.M - (self.M % span)
+        while True:
+            x = self.next()
+            if x < limit:
+                return lo + x % span
+
+
+def rotary_table(dim, theta):
+    import numpy as np
+    j = np.arange(dim // 2, dtype=np.float32)
+    return (np.float32(1.0) / np.power(np.float32(theta), np.float32(2) * j / np.float32(dim))).astype(np.float32)
+
+
+def randn(shape, gen, dtype):
+    import torch
+    return torch.randn(shape, generator=gen, device="cuda", dtype=torch.float32).to(dtype)
+
+
+def gammas(dim, gen):
+    import torch
+    return (torch.rand((dim,), generator=gen, device="cuda") + 0.5).contiguous()
+
+
+# ------------------------------------------------------------------ timing
+def time_steps(step, steps, warmup, kernel):
+    """warmup, then K timed steps between synchronisations; returns step ms and
+    the named kernel's average launch ms from the backend's hipEvents"""
+    import torch
+    import aigpu
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    aigpu.profile_reset()
+    aigpu.profile(True)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    aigpu.profile(False)
+    step_ms = t0.elapsed_time(t1) / steps
+    k_ms, n = aigpu.profile_read(kernel)
+    all_ms, _ = aigpu.profile_read(None)
+    return step_ms, (k_ms / n if n else float("nan")), all_ms / steps
+
+
+def cpu_lib():
+    """(library, kind): the reference's compiled kernels when present."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as O
+    ref = O.ref()
+    threads = O.threads(0, cap=CPU_THREADS_CAP)
+    if ref is not None:
+        ref.ref_configure_pool(threads)
+        return O, ref, "reference", threads
+    return O, None, "port", threads
+
+
+# --------------------------------------------------------------- workloads
+def prefill_workload(args, cpu):
+    import numpy as np
+    import torch
+    import aigpu
+    S, H, KV, D = 8192, 32, 8, 128
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    q = randn((S, H, D), gen, torch.bfloat16)
+    k = randn((S, KV, D), gen, torch.bfloat16)
+    v = randn((S, KV, D), gen, torch.bfloat16)
+    gq, gk = gammas(D, gen), gammas(D, gen)
+    fr = torch.from_numpy(rotary_table(D, 1e6)).cuda()
+    kc = torch.empty((KV, S, D), dtype=torch.bfloat16, device="cuda")
+    vc = torch.empty_like(kc)
+    out = torch.empty((S, H, D), dtype=torch.float32, device="cuda")
+
+    def step():
+        aigpu.prefill(q, k, v, out, kc, vc, 0, H, KV, D, q_norm=gq, k_norm=gk, freqs=fr,
+                      rotary_dims=D)
+
+    flops = 2.0 * D * H * S * (S + 1)
+    step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "prefill_flash_kernel")
+    res = {
+        "workload": "configs[2] qwen3-8b causal GQA prefill S=8192 32q/8kv D=128 bf16, QK-norm+RoPE",
+        "value": flops / (step_ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": step_ms,
+        "roofline": {"kernel": "prefill_flash_kernel", "bound": "mfma",
+                     "achieved": flops / (k_ms * 1e-3) / 1e12, "peak": PEAK_MFMA_F16,
+                     "unit": "TFLOP/s", "frac": flops / (k_ms * 1e-3) / 1e12 / PEAK_MFMA_F16,
+                     "traffic": None, "kernel_ms": k_ms, "flops_per_launch": flops},
+    }
+    if cpu is not None:
+        O, ref, kind, threads = cpu
+        qh = q[-64:].float().cpu().numpy()
+        kh = k.float().cpu().numpy()
+        vh = v.float().cpu().numpy()
+
+        def run(n):
+            start = S - n
+            qq = np.ascontiguousarray(np.resize(qh, (n, H, D)), np.float32)
+            o = np.zeros(n * H * D, np.float32)
+            t = time.perf_counter()
+            if ref is not None:
+                ref.ref_attention(qq.reshape(-1), kh.reshape(-1), vh.reshape(-1), o, n, start, H, KV, D,
+                                  D, 0, 1)
+            else:
+                O.attention(qq, kh, vh, n, start, H, KV, D, D, nthreads=threads)
+            dt = time.perf_counter() - t
+            return 4.0 * D * H * sum(start + i + 1 for i in range(n)), dt
+
+        f0, t0 = run(32)
+        n = int(min(S, max(32, 32 * args.cpu_seconds / max(t0, 1e-3))))
+        f1, t1 = run(n)
+        res["cpu_baseline"] = {"value": f1 / t1 / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": kind,
+                               "sample": f"kernels::attention over the last {n} of the 8192 query rows "
+                                         f"(full causal history, {f1 / 1e9:.1f} GFLOP in {t1:.1f} s, "
+                                         f"fp32, static-split pool)"}
+    return res
+
+
+def decode_workload(args, cpu):
+    import numpy as np
+    import torch
+    import aigpu
+    B, H, KV, D = 32, 32, 4, 128
+    r = Xoshiro(3)
+    lengths = [r.randint(1024, 32768) for _ in range(B)]
+    cap = max(lengths) + 1
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    q = randn((B, H, D), gen, torch.bfloat16)
+    k = randn((B, KV, D), gen, torch.bfloat16)
+    v = randn((B, KV, D), gen, torch.bfloat16)
+    gq, gk = gammas(D, gen), gammas(D, gen)
+    fr = torch.from_numpy(rotary_table(D, 1e6)).cuda()
+    kc = randn((B, KV, cap, D), gen, torch.bfloat16)
+    vc = randn((B, KV, cap, D), gen, torch.bfloat16)
+    pos = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    out = torch.empty((B, H, D), dtype=torch.float32, device="cuda")
+
+    def step():
+        aigpu.decode(q, k, v, out, kc, vc, pos, max(lengths), H, KV, D, q_norm=gq, k_norm=gk, freqs=fr,
+                     rotary_dims=D)
+
+    nbytes = 2048.0 * sum(L + 1 for L in lengths)
+    step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "decode_split_kernel")
+    res = {
+        "workload": "configs[3] qwen3-30b-a3b batched ragged GQA decode B=32 L~U[1k,32k] 32q/4kv D=128 bf16 KV",
+        "value": nbytes / (step_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": step_ms,
+        "kv_bytes": nbytes,
+        "roofline": {"kernel": "decode_split_kernel", "bound": "hbm",
+                     "achieved": nbytes / (k_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
+                     "frac": nbytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
+                     "kernel_ms": k_ms, "bytes_per_launch": nbytes},
+    }
+    if cpu is not None:
+        O, ref, kind, threads = cpu
+        qh = q.float().cpu().numpy()
+        done_bytes, spent, seqs = 0.0, 0.0, 0
+        for b in range(B):
+            L = lengths[b]
+            keys = np.ascontiguousarray(kc[b, :, :L + 1].float().cpu().numpy().transpose(1, 0, 2))
+            vals = np.ascontiguousarray(vc[b, :, :L + 1].float().cpu().numpy().transpose(1, 0, 2))
+            o = np.zeros(H * D, np.float32)
+            t = time.perf_counter()
+            if ref is not None:
+                ref.ref_attention(np.ascontiguousarray(qh[b]).reshape(-1), keys.reshape(-1), vals.reshape(-1),
+                                  o, 1, L, H, KV, D, D, 0, 1)
+            else:
+                O.attention(qh[b:b + 1], keys, vals, 1, L, H, KV, D, D, nthreads=threads)
+            spent += time.perf_counter() - t
+            done_bytes += 2048.0 * (L + 1)
+            seqs += 1
+            if spent > args.cpu_seconds:
+                break
+        res["cpu_baseline"] = {"value": done_bytes / spent / 1e9, "unit": "GB/s", "cores": threads,
+                               "kind": kind,
+                               "sample": f"kernels::attention for {seqs} of the 32 sequences, one call each "
+                                         f"(count=1, start=L_b) as the reference decodes, fp32 "
+                                         f"position-major KV; GB/s on the same bf16 KV byte count"}
+    return res
+
+
+def delta_workload(args, cpu):
+    import numpy as np
+    import torch
+    import aigpu
+    S, HK, HV, KD, VD = 16384, 16, 32, 128, 128
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    q = randn((S, HK, KD), gen, torch.bfloat16)
+    k = randn((S, HK, KD), gen, torch.bfloat16)
+    v = randn((S, HV, VD), gen, torch.bfloat16)
+    g = -torch.nn.functional.softplus(torch.randn((S, HV), generator=gen, device="cuda"))
+    beta = torch.sigmoid(torch.randn((S, HV), generator=gen, device="cuda"))
+    state = torch.zeros((HV, KD, VD), dtype=torch.float32, device="cuda")
+    out = torch.empty((S, HV, VD), dtype=torch.float32, device="cuda")
+
+    def step():
+        state.zero_()
+        aigpu.gated_delta_rule(q, k, v, state, out, g=g, beta=beta)
+
+    nbytes = 543162368.0
+    step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "delta_scan_kernel")
+    flops = S * HV * (7.0 * KD * VD + 4.0 * VD)
+    res = {
+        "workload": "configs[4] qwen3-next gated delta rule S=16384 16qk/32v heads D=128 chunk 64 bf16 in, fp32 state",
+        "value": nbytes / (step_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": step_ms,
+        "recurrence_tflops": flops / (step_ms * 1e-3) / 1e12,
+        "roofline": {"kernel": "delta_scan_kernel", "bound": "hbm",
+                     "achieved": nbytes / (launched_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
+                     "frac": nbytes / (launched_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
+                     "kernel_ms": k_ms, "all_kernels_ms": launched_ms, "bytes_per_step": nbytes},
+    }
+    if cpu is not None:
+        O, ref, kind, threads = cpu
+        n = 2048
+        qh = q[:n].float().cpu().numpy()
+        kh = k[:n].float().cpu().numpy()
+        vh = v[:n].float().cpu().numpy()
+        gh = g[:n].cpu().numpy()
+        bh = beta[:n].cpu().numpy()
+        t = time.perf_counter()
+        O.gated_delta_rule(qh, kh, vh, gh, bh, nthreads=1)
+        dt = time.perf_counter() - t
+        res["cpu_baseline"] = {"value": nbytes * n / S / dt / 1e9, "unit": "GB/s", "cores": 1,
+                               "kind": "port",
+                               "sample": f"gatedDeltaNetMixer recurrence over the first {n} of 16384 tokens, "
+                                         f"single-threaded as the reference runs it ({dt:.1f} s), "
+                                         f"C restatement of deltaStep"}
+    return res
+
+
+def small_workloads(args):
+    """launch-latency-bound, reported as measured"""
+    import torch
+    import aigpu
+    out = []
+    # Qwen3-0.6B decode at 4096
+    H, KV, D, L = 16, 8, 128, 4096
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    q = randn((1, H, D), gen, torch.bfloat16)
+    k = randn((1, KV, D), gen, torch.bfloat16)
+    v = randn((1, KV, D), gen, torch.bfloat16)
+    kc = randn((1, KV, L + 1, D), gen, torch.bfloat16)
+    vc = randn((1, KV, L + 1, D), gen, torch.bfloat16)
+    gq, gk = gammas(D, gen), gammas(D, gen)
+    fr = torch.from_numpy(rotary_table(D, 1e6)).cuda()
+    pos = torch.tensor([L], dtype=torch.int32, device="cuda")
+    o = torch.empty((1, H, D), dtype=torch.float32, device="cuda")
+    step_ms, k_ms, _ = time_steps(lambda: aigpu.decode(q, k, v, o, kc, vc, pos, L, H, KV, D, q_norm=gq,
+                                                       k_norm=gk, freqs=fr, rotary_dims=D),
+                                  max(args.steps, 50), args.warmup, "decode_split_kernel")
+    nbytes = 2.0 * (L + 1) * KV * D * 2
+    out.append({"workload": "configs[1] qwen3-0.6b decode L=4096 16q/8kv D=128", "unit": "GB/s",
+                "value": nbytes / (step_ms * 1e-3) / 1e9, "ms_per_step": step_ms,
+                "kernel_ms": k_ms, "kernel_frac_of_hbm": nbytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM})
+    # GPT-2 MHA prefill fp32 through the exact fp32 path (device form)
+    S, H, D = 128, 12, 64
+    qf = torch.randn((S, H, D), generator=gen, device="cuda")
+    kf = torch.randn((S, H, D), generator=gen, device="cuda")
+    vf = torch.randn((S, H, D), generator=gen, device="cuda")
+    of = torch.empty((S, H, D), dtype=torch.float32, device="cuda")
+    step_ms, k_ms, _ = time_steps(lambda: aigpu.attention_device(qf, kf, vf, of, S, 0, H, H, D, D, H * D, D),
+                                  max(args.steps, 50), args.warmup, "attention_f32_kernel")
+    flops = 4.0 * D * H * S * (S + 1) / 2
+    out.append({"workload": "configs[0] gpt2-small MHA prefill fp32 S=128 12 heads D=64", "unit": "TFLOP/s",
+                "value": flops / (step_ms * 1e-3) / 1e12, "ms_per_step": step_ms, "kernel_ms": k_ms,
+                "kernel_frac_of_fp32": flops / (k_ms * 1e-3) / 1e12 / PEAK_MFMA_F32})
+    return out
+
+
+def calibrate_copy():
+    """one 1 GiB device-to-device copy: the HBM counters of this known-size
+    kernel scale the FETCH_SIZE/WRITE_SIZE readings of the attention kernels"""
+    import torch
+    a = torch.empty((1 << 28,), dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(each GPU box has one MI355X); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import aigpu
+    aigpu.require()
+    if args.calibrate_copy:
+        calibrate_copy()
+    cpu = None if args.no_cpu else cpu_lib()
+    head = None
+    extra = {}
+    if args.workload in ("prefill", "all"):
+        head = prefill_workload(args, cpu)
+    if args.workload in ("decode", "all"):
+        extra["decode"] = decode_workload(args, cpu)
+    if args.workload in ("delta", "all"):
+        extra["delta_rule"] = delta_workload(args, cpu)
+    if args.workload == "all":
+        extra["others"] = small_workloads(args)
+    if head is None:   # a single non-prefill workload becomes the line
+        head = extra.pop("decode", None) or extra.pop("delta_rule")
+    line = {
+        "metric": "attn TFLOP/s (prefill) & KV GB/s (decode) as % roofline, 1 MI355X vs host CPU",
+        "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (torch seeded N(0,1) at each configuration's shape)",
+        "config": {"workload": head["workload"], "device": aigpu.device_name()},
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+    }
+    line.update(extra)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
