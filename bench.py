@@ -223,12 +223,12 @@ def decode_workload(args, cpu):
                      rotary_dims=D)
 
     nbytes = 2048.0 * sum(L + 1 for L in lengths)
-    step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "decode_split_kernel")
+    step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "decode_attention_kernel")
     res = {
         "workload": "configs[3] qwen3-30b-a3b batched ragged GQA decode B=32 L~U[1k,32k] 32q/4kv D=128 bf16 KV",
         "value": nbytes / (step_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": step_ms,
         "kv_bytes": nbytes,
-        "roofline": {"kernel": "decode_split_kernel", "bound": "hbm",
+        "roofline": {"kernel": "decode_attention_kernel", "bound": "hbm",
                      "achieved": nbytes / (k_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
                      "frac": nbytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
                      "kernel_ms": k_ms, "bytes_per_launch": nbytes},
@@ -329,7 +329,7 @@ def small_workloads(args):
     o = torch.empty((1, H, D), dtype=torch.float32, device="cuda")
     step_ms, k_ms, _ = time_steps(lambda: aigpu.decode(q, k, v, o, kc, vc, pos, L, H, KV, D, q_norm=gq,
                                                        k_norm=gk, freqs=fr, rotary_dims=D),
-                                  max(args.steps, 50), args.warmup, "decode_split_kernel")
+                                  max(args.steps, 50), args.warmup, "decode_attention_kernel")
     nbytes = 2.0 * (L + 1) * KV * D * 2
     out.append({"workload": "configs[1] qwen3-0.6b decode L=4096 16q/8kv D=128", "unit": "GB/s",
                 "value": nbytes / (step_ms * 1e-3) / 1e9, "ms_per_step": step_ms,

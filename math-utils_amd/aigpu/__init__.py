@@ -101,7 +101,15 @@ SIGNATURES = {
 
 
 def load_library(path):
-    """Loads a backend (.so) and declares every ABI symbol on it."""
+    """Loads a backend (.so) and declares every ABI symbol on it.
+
+    PyTorch ships its own libamdhip64.so.7 under the same soname as ROCm's;
+    whichever is loaded first serves the whole process. torch is imported
+    first (when installed) so that both sides always share torch's runtime."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)

@@ -77,6 +77,17 @@ void* Context::grow(ScratchSlot slot, size_t bytes) {
     return fresh;
 }
 
+void* Context::growZeroed(ScratchSlot slot, size_t bytes) {
+    const bool fresh = scratchBytes[slot] < (bytes ? bytes : 256);
+    void* p = grow(slot, bytes);
+    if (p && fresh && hipMemset(p, 0, scratchBytes[slot]) != hipSuccess) {
+        (void)hipGetLastError();
+        error = "hipMemset of scratch failed";
+        return nullptr;
+    }
+    return p;
+}
+
 hipEvent_t Context::takeEvent() {
     if (!spareEvents.empty()) {
         hipEvent_t e = spareEvents.back();

@@ -25,6 +25,7 @@ enum ScratchSlot {
     SLOT_PREFILL_K,      // fp16 head-major k history of a prefill
     SLOT_PREFILL_V,      // fp16 head-major v history of a prefill
     SLOT_DECODE_PARTS,   // split-K partial softmax records
+    SLOT_DECODE_QUERIES, // prepared decode queries and new-token scores
     SLOT_DELTA_WORK,     // per-chunk solve products of the delta rule
     SLOT_COUNT
 };
@@ -52,6 +53,9 @@ struct Context {
 
     // a scratch slot of at least `bytes`; nullptr (and error set) on failure
     void* grow(ScratchSlot slot, size_t bytes);
+    // the same, zero-filled whenever it is (re)allocated; kernels that use it
+    // must leave it zero again
+    void* growZeroed(ScratchSlot slot, size_t bytes);
 
     bool fail(const std::string& why) {
         error = why;

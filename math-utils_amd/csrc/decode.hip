@@ -1,24 +1,36 @@
 // decode.hip - batched single-token GQA decode for gfx950, HBM-bound.
 //
-// decode_split_kernel: one workgroup per (sequence b, kv head, chunk of CH
-// positions); its 4 waves split the chunk into slabs of 64 positions.
+// One persistent launch walks a flattened work list of (sequence b, kv head,
+// chunk of CH positions) items; each workgroup takes items blockIdx.x,
+// blockIdx.x + gridDim.x, ... so ragged lengths leave no empty workgroups.
+// Per item, 4 waves split the chunk into slabs of 32 positions, software-
+// pipelined: a wave's next slab is requested before the current one computes,
+// and its first slab before the item's queries are prepared.
 //   - the G query heads of the kv head get QK-RMSNorm and RoPE at position
 //     positions[b] on load (attentionMixer, LocalModel.hpp:2608-2648);
-//   - the workgroup whose chunk ends at the new token also normalises and
-//     rotates the new k, appends k and v to the bf16 cache at positions[b]
-//     (LocalModel.hpp:2650-2655) and folds the new token in from registers,
-//     so no workgroup reads the slot being written;
-//   - scores: v_mfma_f32_16x16x32_bf16 with K rows (straight from HBM, 16-byte
-//     loads, each K byte read once for all G heads) as A and q as B, q split
+//   - the item whose chunk ends at the new token also normalises and rotates
+//     the new k, appends k and v to the bf16 cache at positions[b]
+//     (LocalModel.hpp:2650-2655) and folds the new token in from LDS, so no
+//     workgroup reads the slot being written;
+//   - scores: v_mfma_f32_16x16x32_bf16 with K rows (16-byte loads straight
+//     from HBM, each K byte read once for all G heads) as A and q as B, q split
 //     into a bf16 high part (columns 0-7) and the bf16 residual (columns 8-15)
 //     so the two halves add back to ~16 significant bits;
-//   - P.V: v_mfma_f32_16x16x4f32, fp32 P against widened bf16 V rows, with
-//     the output columns permuted so each lane loads 16 contiguous bytes of a
-//     V row;
-//   - online softmax inside a wave, a cross-wave merge in LDS, then one
-//     partial (m, l, acc) record per chunk.
-// decode_merge_kernel combines a sequence's chunk records (the split-K merge
-// algebra of the reference's Metal decoder, src/gpu/Kernels.metal:318-345).
+//   - P.V: v_mfma_f32_16x16x32_bf16 with P split like q (bf16 high part in
+//     rows 0-7, residual in rows 8-15) against V: V rows arrive as whole
+//     1 KB-per-instruction nontemporal loads, pass through LDS, and come back
+//     through ds_read_b64_tr_b16 as the k-contiguous B operand;
+//   - online softmax inside a wave, a cross-wave merge in LDS; a sequence
+//     that fits one chunk writes its output directly, otherwise each chunk
+//     leaves a (m, l, acc) record.
+// decode_merge_kernel then combines the records of multi-chunk sequences -
+// the split-K algebra of the reference's Metal decoder
+// (src/gpu/Kernels.metal:318-345). A kernel boundary, not an in-kernel
+// device-scope fence, publishes the records: on gfx950 such a fence writes
+// back and invalidates the XCD's whole L2, which costs far more than a launch.
+//
+// Calls that share the backend's scratch (the records) must not run
+// concurrently on different streams.
 #include "context.hpp"
 #include "device.hpp"
 #include "kernels.hpp"
@@ -30,280 +42,462 @@ namespace aigpu {
 namespace {
 
 constexpr int MAXG = 8;          // query heads per kv head handled by one workgroup
-constexpr int SLAB = 64;         // positions per wave step
+constexpr int SLAB = 32;         // positions per wave step
+constexpr int MAXB = 1024;       // sequences per launch (larger batches are split)
 
 struct DecodeArgs {
     DecodeParams p;
     float* parts;                // [batch][kvHeads][maxChunks][RS]
-    uint32_t chunkLen;           // CH
+    uint32_t* qrec;              // [batch][kvHeads][QREC] prepared queries and new token
+    uint32_t chunkLen;           // CH, a multiple of 4 * SLAB
     uint32_t maxChunks;
     float scaleLog2;
 };
 
 __host__ __device__ constexpr int record_floats(int D) { return 2 * MAXG + MAXG * D; }
 
-__device__ __forceinline__ void chunk_range(const DecodeParams& p, uint32_t L, uint32_t& first,
-                                            uint32_t& nChunks, uint32_t CH) {
-    first = (p.window && uint64_t(L) + 1 > p.window) ? uint32_t(uint64_t(L) + 1 - p.window) : 0u;
-    nChunks = (L + 1 - first + CH - 1) / CH;
+/* per (sequence, kv head), written by decode_prep_kernel: q as the score
+   MFMA's B operand (D/32 blocks x 64 lanes x 16 bytes), the new token's scores
+   snew[MAXG] and its value row vnew[D] in fp32 */
+__host__ __device__ constexpr int qrec_words(int D) { return (D / 32) * 64 * 4 + MAXG + D; }
+
+__device__ __forceinline__ uint32_t first_position(const DecodeParams& p, uint32_t L) {
+    return (p.window && uint64_t(L) + 1 > p.window) ? uint32_t(uint64_t(L) + 1 - p.window) : 0u;
 }
 
+typedef __bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
+
+/* x from lane (lane ^ 8) of the same 16-lane row: a DPP row rotate by 8 */
+__device__ __forceinline__ float row_rotate8(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));
+}
+
+/* ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4
+   of the 8-byte rows addressed by lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12 */
+__device__ __forceinline__ bf16x4 read_tr16(const uint16_t* lds) {
+    typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(lds));
+}
+
+/* V slabs in LDS: rows of D halfs, RPL rows per 1 KB DMA block; the 16-byte
+   column block x of row r sits at x ^ v_swizzle(r) */
+__device__ __forceinline__ int v_swizzle(int r) { return 2 * (r & 3); }
+
 template <int D>
-__global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
-    constexpr int DB = D / 32;   // 32-deep d blocks of the score MFMA
-    constexpr int TPL = D / 16;  // value columns each lane carries in the P.V tiles
-    constexpr int RS = record_floats(D);
+__device__ __forceinline__ int v_offset(int r, int x) {
+    return r * D + 8 * (x ^ v_swizzle(r));
+}
+
+/* s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding) */
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+/* Once per (sequence b, kv head): QK-RMSNorm and RoPE of the G query rows and
+   of the new key at position positions[b] (attentionMixer, LocalModel.hpp:
+   2608-2648), the new key and value appended to the bf16 cache
+   (LocalModel.hpp:2650-2655), the new token's scores, and q packed as the
+   score MFMA's B operand (bf16 high part in columns 0-7, residual in 8-15). */
+template <int D>
+__global__ __launch_bounds__(256) void decode_prep_kernel(DecodeArgs a) {
+    constexpr int DB = D / 32;
+    typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
     const DecodeParams& p = a.p;
-    const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const uint32_t G = uint32_t(p.heads / p.kvHeads);
+    const uint32_t KVH = uint32_t(p.kvHeads), G = uint32_t(p.heads / p.kvHeads);
+    const uint32_t b = blockIdx.x / KVH, kvh = blockIdx.x % KVH;
     const uint32_t L = p.positions[b];
-    if (L > p.maxPosition) return;  // outside the launch's bounds: the merge marks it NaN
-    uint32_t first, nChunks;
-    chunk_range(p, L, first, nChunks, a.chunkLen);
-    if (chunk >= nChunks) return;  // uniform over the workgroup
-    const uint32_t lo = first + chunk * a.chunkLen;
-    const uint32_t hi = (lo + a.chunkLen < L + 1) ? lo + a.chunkLen : L + 1;
-    const bool hasNew = hi == L + 1;
-    const uint32_t cachedHi = hi < L ? hi : L;   // cached positions are [lo, cachedHi)
-
-    __shared__ float qs[MAXG][D];
-    __shared__ float rowbuf[4][D];
-    __shared__ float knew[D], vnew[D];
-    __shared__ float snew[MAXG];
-    __shared__ float wm[4][MAXG], wl[4][MAXG];
-    __shared__ float wacc[4][MAXG][D];
-
+    if (L > p.maxPosition) return;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    __shared__ float rows[MAXG + 1][D];   // normed, rotated q rows (scaled) and the new key
     const size_t cacheBase = size_t(b) * p.batchStride + size_t(kvh) * p.capacity * D;
-    const uint16_t* kc = p.keyCache + cacheBase;
-    const uint16_t* vc = p.valueCache + cacheBase;
+    uint32_t* rec = a.qrec + (size_t(b) * KVH + kvh) * qrec_words(D);
+    float* snew = reinterpret_cast<float*>(rec + DB * 64 * 4);
+    float* vnew = snew + MAXG;
 
-    // ---- queries (and the new key/value) through norm + RoPE, in fp32 ----
-    const uint32_t nrows = G + (hasNew ? 1u : 0u);
-    for (uint32_t r = w; r < nrows; r += 4) {
-        float* x = rowbuf[w];
-        if (r < G) {
-            const size_t src = (size_t(b) * p.heads + size_t(kvh) * G + r) * p.qStride;
-            for (int d = lane; d < D; d += WAVE) x[d] = load_elem(p.q, src + d, p.inType);
-            wave_sync();
-            norm_rope_row(x, D, p.qNorm, p.eps, p.normOffset, p.freqs, p.rotaryDims, L, lane);
-            for (int d = lane; d < D; d += WAVE) qs[r][d] = x[d] * a.scaleLog2;
-        } else {
-            const size_t src = (size_t(b) * p.kvHeads + kvh) * D;
-            for (int d = lane; d < D; d += WAVE) x[d] = load_elem(p.k, src + d, p.inType);
-            wave_sync();
-            norm_rope_row(x, D, p.kNorm, p.eps, p.normOffset, p.freqs, p.rotaryDims, L, lane);
+    for (uint32_t r = w; r <= G; r += 4) {
+        float* x = rows[r];
+        const bool isKey = r == G;
+        const size_t src = isKey ? (size_t(b) * p.kvHeads + kvh) * D
+                                 : (size_t(b) * p.heads + size_t(kvh) * G + r) * p.qStride;
+        for (int d = lane; d < D; d += WAVE) x[d] = load_elem(isKey ? p.k : p.q, src + d, p.inType);
+        wave_sync();
+        norm_rope_row(x, D, isKey ? p.kNorm : p.qNorm, p.eps, p.normOffset, p.freqs, p.rotaryDims, L, lane);
+        if (isKey) {
             uint16_t* kdst = p.keyCache + cacheBase + size_t(L) * D;
             uint16_t* vdst = p.valueCache + cacheBase + size_t(L) * D;
             for (int d = lane; d < D; d += WAVE) {
-                knew[d] = x[d];
                 kdst[d] = float_to_bf16_bits(x[d]);
-                const float vv = load_elem(p.v, src + d, p.inType);
-                vnew[d] = vv;
+                const float vv = load_elem(p.v, (size_t(b) * p.kvHeads + kvh) * D + d, p.inType);
                 vdst[d] = float_to_bf16_bits(vv);
+                vnew[d] = vv;
             }
+        } else {
+            for (int d = lane; d < D; d += WAVE) x[d] *= a.scaleLog2;
         }
         wave_sync();
     }
     __syncthreads();
-    if (hasNew && w == 0) {
-        for (uint32_t h = 0; h < G; ++h) {
-            float part = 0.0f;
-            for (int d = lane; d < D; d += WAVE) part += qs[h][d] * knew[d];
-            part = wave_sum(part);
-            if (lane == 0) snew[h] = part;
-        }
+    for (uint32_t h = w; h < G; h += 4) {
+        float part = 0.0f;
+        for (int d = lane; d < D; d += WAVE) part += rows[h][d] * rows[G][d];
+        part = wave_sum(part);
+        if (lane == 0) snew[h] = part;
     }
-
-    // ---- q as the B operand: column j < 8 is head j's bf16 high part, column
-    //      8 + j its bf16 residual; heads >= G are zero ----
-    const int g = lane >> 4, c16 = lane & 15;
-    typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
-    bf16x8 qb[DB];
-    {
+    if (w == 0) {
+        const int g = lane >> 4, c16 = lane & 15;
         const uint32_t h = c16 & 7;
         const bool residual = c16 >= 8;
-#pragma unroll
         for (int db = 0; db < DB; ++db) {
             u16x8 bits;
-#pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const float x = h < G ? qs[h][32 * db + 8 * g + s] : 0.0f;
+                const float x = h < G ? rows[h][32 * db + 8 * g + s] : 0.0f;
                 const uint16_t top = float_to_bf16_bits(x);
                 bits[s] = residual ? float_to_bf16_bits(x - bf16_bits_to_float(top)) : top;
             }
-            qb[db] = __builtin_bit_cast(bf16x8, bits);
-        }
-    }
-
-    // ---- slabs ----
-    float m = -INFINITY, lsum = 0.0f;   // per lane: head c16 & 7
-    floatx4 acc[TPL];
-#pragma unroll
-    for (int t = 0; t < TPL; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    for (uint32_t p0 = lo + SLAB * w; p0 < cachedHi; p0 += 4 * SLAB) {
-        const uint32_t lastRow = cachedHi - 1;
-        u32x4 kr[4][DB];
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            uint32_t row = p0 + 16 * rb + c16;
-            if (row > lastRow) row = lastRow;
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-                kr[rb][db] = *reinterpret_cast<const u32x4*>(kc + size_t(row) * D + 32 * db + 8 * g);
-        }
-        typedef uint32_t vchunk __attribute__((ext_vector_type(TPL / 2)));
-        vchunk vr[4][4];
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t row = p0 + 16 * rb + 4 * g + i;
-                if (row > lastRow) row = lastRow;
-                vr[rb][i] = *reinterpret_cast<const vchunk*>(vc + size_t(row) * D + TPL * c16);
-            }
-
-        floatx4 sc[4];
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            sc[rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-                sc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[rb][db]),
-                                                                 qb[db], sc[rb], 0, 0, 0);
-        }
-
-        float sv[4][4];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float x = sc[rb][i];
-                x += __shfl_xor(x, 8, WAVE);   // high part + residual
-                const uint32_t pos = p0 + 16 * rb + 4 * g + i;
-                x = pos < cachedHi ? x : -INFINITY;
-                sv[rb][i] = x;
-                mx = fmaxf(mx, x);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
-        const float mn = fmaxf(m, mx);
-        const float base = mn == -INFINITY ? 0.0f : mn;
-        const float alpha = exp2f(m - base);
-        float ps = 0.0f;
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                sv[rb][i] = exp2f(sv[rb][i] - base);
-                ps += sv[rb][i];
-            }
-        lsum = lsum * alpha + ps;
-        m = mn;
-
-        // accumulator rows are heads 4g + r: fetch their rescale factors
-        float ar[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r, WAVE);
-#pragma unroll
-        for (int t = 0; t < TPL; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[t][r] *= ar[r];
-
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                for (int t = 0; t < TPL; ++t) {
-                    const uint32_t word = vr[rb][i][t / 2];
-                    const float vf = (t & 1) ? __uint_as_float(word & 0xFFFF0000u) : __uint_as_float(word << 16);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[rb][i], vf, acc[t], 0, 0, 0);
-                }
-            }
-    }
-
-    // ---- per-wave state to LDS ----
-    lsum += __shfl_xor(lsum, 16, WAVE);
-    lsum += __shfl_xor(lsum, 32, WAVE);
-    if (g == 0 && c16 < MAXG) {
-        wm[w][c16] = m;
-        wl[w][c16] = lsum;
-    }
-    if (g < 2) {
-#pragma unroll
-        for (int t = 0; t < TPL; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) wacc[w][4 * g + r][TPL * c16 + t] = acc[t][r];
-    }
-    __syncthreads();
-
-    // ---- merge the waves (and the new token) into this chunk's record ----
-    float* rec = a.parts + ((size_t(b) * p.kvHeads + kvh) * a.maxChunks + chunk) * RS;
-    for (uint32_t idx = tid; idx < G * D; idx += 256) {
-        const uint32_t h = idx / D, d = idx % D;
-        float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
-        if (hasNew) M = fmaxf(M, snew[h]);
-        float lt = 0.0f, at = 0.0f;
-#pragma unroll
-        for (int ww = 0; ww < 4; ++ww) {
-            const float f = wm[ww][h] == -INFINITY ? 0.0f : exp2f(wm[ww][h] - M);
-            lt += wl[ww][h] * f;
-            at += wacc[ww][h][d] * f;
-        }
-        if (hasNew) {
-            const float f = exp2f(snew[h] - M);
-            lt += f;
-            at += f * vnew[d];
-        }
-        rec[2 * MAXG + h * D + d] = at;
-        if (d == 0) {
-            rec[h] = M;
-            rec[MAXG + h] = lt;
+            reinterpret_cast<u32x4*>(rec)[db * 64 + lane] = __builtin_bit_cast(u32x4, bits);
         }
     }
 }
 
 template <int D>
-__global__ __launch_bounds__(128) void decode_merge_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) {
+    constexpr int DB = D / 32;   // 32-deep d blocks of the score MFMA
+    constexpr int CT = D / 16;   // 16-column tiles of the P.V product
+    constexpr int LPR = D / 8;   // lanes covering one V row with 16-byte loads
+    constexpr int RPL = WAVE / LPR;                 // V rows per load instruction
+    constexpr int VLOADS = SLAB / RPL;              // V load instructions per slab
+    constexpr int VSLAB = SLAB * D;                 // halfs of one V slab in LDS
     constexpr int RS = record_floats(D);
+    static_assert(2 * MAXG * D * 4 <= 2 * VSLAB * 2, "per-wave state must fit in the wave's V slabs");
+    typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
     const DecodeParams& p = a.p;
-    const uint32_t hq = blockIdx.x, b = blockIdx.y;
+    const uint32_t B = uint32_t(p.batch), KVH = uint32_t(p.kvHeads);
     const uint32_t G = uint32_t(p.heads / p.kvHeads);
-    const uint32_t kvh = hq / G, h = hq % G;
-    const uint32_t L = p.positions[b];
-    const int d = threadIdx.x;
-    if (d >= D) return;
-    if (L > p.maxPosition) {   // a position the caller's maxPosition did not cover
-        p.out[(size_t(b) * p.heads + hq) * D + d] = __builtin_nanf("");
-        return;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+
+    __shared__ uint32_t pre[MAXB + 1];
+    __shared__ float wm[4][MAXG], wl[4][MAXG];
+    __shared__ __attribute__((aligned(16))) uint16_t vbuf[4 * 2 * VSLAB];   // per-wave V slabs (x2)
+
+    // ---- chunk counts -> prefix over the batch (the work list) ----
+    for (uint32_t i = tid; i < B; i += 256) {
+        const uint32_t L = p.positions[i];
+        pre[i + 1] = L > p.maxPosition ? 0u : (L + 1 - first_position(p, L) + a.chunkLen - 1) / a.chunkLen;
     }
-    uint32_t first, nChunks;
-    chunk_range(p, L, first, nChunks, a.chunkLen);
-    const float* recs = a.parts + (size_t(b) * p.kvHeads + kvh) * a.maxChunks * RS;
-    float M = -INFINITY;
-    for (uint32_t c = 0; c < nChunks; ++c) M = fmaxf(M, recs[size_t(c) * RS + h]);
-    float lt = 0.0f, at = 0.0f;
-    for (uint32_t c = 0; c < nChunks; ++c) {
-        const float* r = recs + size_t(c) * RS;
-        const float f = exp2f(r[h] - M);
-        lt += r[MAXG + h] * f;
-        at += r[2 * MAXG + h * D + d] * f;
+    if (tid == 0) pre[0] = 0;
+    __syncthreads();
+    if (w == 0) {
+        uint32_t carry = 0;
+        for (uint32_t base = 0; base < B; base += 64) {
+            const uint32_t i = base + lane;
+            uint32_t x = i < B ? pre[i + 1] : 0u;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t y = __shfl_up(x, off, WAVE);
+                if (lane >= off) x += y;
+            }
+            x += carry;
+            if (i < B) pre[i + 1] = x;
+            carry = __shfl(x, 63, WAVE);
+        }
     }
-    p.out[(size_t(b) * p.heads + hq) * D + d] = at / lt;
+    __syncthreads();
+    const uint32_t items = pre[B] * KVH;
+    uint16_t* vw = vbuf + w * (2 * VSLAB);
+
+    for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
+        const uint32_t kvh = item % KVH, j = item / KVH;
+        uint32_t lo_b = 0, hi_b = B;   // pre[lo_b] <= j < pre[hi_b]
+        while (hi_b - lo_b > 1) {
+            const uint32_t mid = (lo_b + hi_b) / 2;
+            if (pre[mid] <= j) lo_b = mid;
+            else hi_b = mid;
+        }
+        const uint32_t b = lo_b, chunk = j - pre[b], nChunks = pre[b + 1] - pre[b];
+        const uint32_t L = p.positions[b];
+        const uint32_t first = first_position(p, L);
+        const uint32_t lo = first + chunk * a.chunkLen;
+        const uint32_t hi = (lo + a.chunkLen < L + 1) ? lo + a.chunkLen : L + 1;
+        const bool hasNew = hi == L + 1;
+        const uint32_t cachedHi = hi < L ? hi : L;   // cached positions are [lo, cachedHi)
+        const uint32_t lastRow = cachedHi ? cachedHi - 1 : 0;
+        const size_t cacheBase = size_t(b) * p.batchStride + size_t(kvh) * p.capacity * D;
+        const uint16_t* kc = p.keyCache + cacheBase;
+        const uint16_t* vc = p.valueCache + cacheBase;
+
+        // a slab's loads: K rows into registers as MFMA A operands (row =
+        // lane % 16); V rows straight into LDS slab `half` by DMA, 1 KB per
+        // instruction, each lane's 16-byte column block XOR-swizzled by its row
+        // so the transposed reads below are bank-conflict free
+        auto issue = [&](uint32_t p0, u32x4 (&kr)[2][DB], int half) {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                uint32_t row = p0 + 16 * rb + c16;
+                if (row > lastRow) row = lastRow;
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+                    kr[rb][db] = *reinterpret_cast<const u32x4*>(kc + size_t(row) * D + 32 * db + 8 * g);
+            }
+            uint16_t* vs = vw + half * VSLAB;
+#pragma unroll
+            for (int jj = 0; jj < VLOADS; ++jj) {
+                const int r = jj * RPL + lane / LPR;                 // row within the slab
+                const int cb = (lane % LPR) ^ v_swizzle(r);          // 16-byte column block
+                uint32_t row = p0 + r;
+                if (row > lastRow) row = lastRow;
+                __builtin_amdgcn_global_load_lds(vc + size_t(row) * D + 8 * cb,
+                                                 (__attribute__((address_space(3))) void*)(vs + jj * RPL * D),
+                                                 16, 0, 0);
+            }
+        };
+
+        __syncthreads();   // LDS of the previous item is free
+
+        // this wave's first slab is requested before the queries are prepared
+        u32x4 krA[2][DB], krB[2][DB];
+        uint32_t pA = lo + SLAB * w;
+        if (pA < cachedHi) issue(pA, krA, 0);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- the prepared q operand (written by decode_prep_kernel) ----
+        const uint32_t* qr = a.qrec + (size_t(b) * KVH + kvh) * qrec_words(D);
+        bf16x8 qb[DB];
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+            qb[db] = __builtin_bit_cast(bf16x8, reinterpret_cast<const u32x4*>(qr)[db * 64 + lane]);
+        const float* snewG = reinterpret_cast<const float*>(qr + DB * 64 * 4);
+        const float* vnewG = snewG + MAXG;
+
+        float m = -INFINITY, lsum = 0.0f;   // per lane: head c16 & 7
+        floatx4 acc[CT];                    // rows 0-7: P_hi.V, rows 8-15: P_lo.V
+#pragma unroll
+        for (int t = 0; t < CT; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+        // one slab: scores, online softmax, P.V; `half` picks the LDS V buffer
+        auto compute = [&](uint32_t p0, const u32x4 (&kr)[2][DB], int half, bool nextInFlight) {
+            const uint16_t* vs = vw + half * VSLAB;
+            floatx4 sc[2];
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                sc[rb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+                    sc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[rb][db]),
+                                                                     qb[db], sc[rb], 0, 0, 0);
+            }
+            float sv[2][4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float x = sc[rb][i];
+                    x += row_rotate8(x);   // high part + residual (columns j and j^8)
+                    const uint32_t pos = p0 + 16 * rb + 4 * g + i;
+                    x = pos < cachedHi ? x : -INFINITY;
+                    sv[rb][i] = x;
+                    mx = fmaxf(mx, x);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+            const float mn = fmaxf(m, mx);
+            const float base = mn == -INFINITY ? 0.0f : mn;
+            const float alpha = exp2f(m - base);
+            float ps = 0.0f;
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    sv[rb][i] = exp2f(sv[rb][i] - base);
+                    ps += sv[rb][i];
+                }
+            lsum = lsum * alpha + ps;
+            m = mn;
+
+            // accumulator rows 4g + r hold head (4g + r) & 7: rescale them
+            float ar[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, (4 * g + r) & 7, WAVE);
+#pragma unroll
+            for (int t = 0; t < CT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[t][r] *= ar[r];
+
+            // P as the A operand: row j < 8 is head j's bf16 high part, row 8 + j
+            // its residual; the k slots of lane group g are positions
+            // 4g + (s & 3) + 16 (s >> 2), exactly the scores this lane holds
+            u16x8 bits;
+#pragma unroll
+            for (int s8 = 0; s8 < 8; ++s8) {
+                const float pv = sv[s8 >> 2][s8 & 3];
+                const uint16_t top = float_to_bf16_bits(pv);
+                bits[s8] = c16 >= 8 ? float_to_bf16_bits(pv - bf16_bits_to_float(top)) : top;
+            }
+            const bf16x8 pa = __builtin_bit_cast(bf16x8, bits);
+
+            // the slab's V DMA has landed: only the next slab's loads may be pending
+            if (nextInFlight) wait_vmcnt<2 * DB + VLOADS>();
+            else wait_vmcnt<0>();
+            wave_sync();
+#pragma unroll
+            for (int t = 0; t < CT; ++t) {
+                // transposed reads: lane c16 of group g gets column 16t + c16 at
+                // positions 4g + 0..3, then 16 + 4g + 0..3
+                const int r0 = 4 * g + (c16 >> 2), r1 = r0 + 16;
+                const int x = 2 * t + ((c16 >> 1) & 1), sub = 4 * (c16 & 1);
+                const bf16x4 lo4 = read_tr16(vs + v_offset<D>(r0, x) + sub);
+                const bf16x4 hi4 = read_tr16(vs + v_offset<D>(r1, x) + sub);
+                const bf16x8 vb = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, acc[t], 0, 0, 0);
+            }
+        };
+
+        // ---- slabs, software-pipelined: the next slab's loads are in flight
+        //      while the current one computes (two register/LDS buffers) ----
+        while (pA < cachedHi) {
+            const uint32_t pB = pA + 4 * SLAB;
+            if (pB < cachedHi) issue(pB, krB, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(pA, krA, 0, pB < cachedHi);
+            if (pB >= cachedHi) break;
+            const uint32_t pC = pB + 4 * SLAB;
+            wave_sync();   // slab A's LDS reads are done before its buffer refills
+            if (pC < cachedHi) issue(pC, krA, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(pB, krB, 1, pC < cachedHi);
+            wave_sync();
+            pA = pC;
+        }
+
+        // ---- per-wave state to LDS (each wave inside its own V slabs) ----
+        lsum += __shfl_xor(lsum, 16, WAVE);
+        lsum += __shfl_xor(lsum, 32, WAVE);
+        if (g == 0 && c16 < MAXG) {
+            wm[w][c16] = m;
+            wl[w][c16] = lsum;
+        }
+        wave_sync();   // the last slab's LDS reads are done before the slabs are reused
+        float* waccw = reinterpret_cast<float*>(vw);   // [16][D]: rows h and 8 + h add up
+#pragma unroll
+        for (int t = 0; t < CT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) waccw[(4 * g + r) * D + 16 * t + c16] = acc[t][r];
+        __syncthreads();
+
+        // ---- the waves (and the new token) merged: this chunk's (M, l, acc);
+        //      a one-chunk sequence is finished here ----
+        float* rec = a.parts + ((size_t(b) * KVH + kvh) * a.maxChunks + chunk) * RS;
+        float* outRow = p.out + (size_t(b) * p.heads + size_t(kvh) * G) * D;
+        for (uint32_t idx = tid; idx < G * D; idx += 256) {
+            const uint32_t h = idx / D, d = idx % D;
+            const float sn = hasNew ? snewG[h] : -INFINITY;
+            float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+            M = fmaxf(M, sn);
+            float lt = 0.0f, at = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < 4; ++ww) {
+                const float f = wm[ww][h] == -INFINITY ? 0.0f : exp2f(wm[ww][h] - M);
+                const float* wa = reinterpret_cast<const float*>(vbuf + ww * (2 * VSLAB));
+                lt += wl[ww][h] * f;
+                at += (wa[h * D + d] + wa[(8 + h) * D + d]) * f;
+            }
+            if (hasNew) {
+                const float f = exp2f(sn - M);
+                lt += f;
+                at += f * vnewG[d];
+            }
+            if (nChunks == 1) {
+                outRow[h * D + d] = at / lt;
+            } else {
+                rec[2 * MAXG + h * D + d] = at;
+                if (d == 0) {
+                    rec[h] = M;
+                    rec[MAXG + h] = lt;
+                }
+            }
+        }
+    }
+
+    // sequences whose position exceeds the launch's maxPosition are marked NaN
+    for (uint32_t i = blockIdx.x; i < B; i += gridDim.x) {
+        if (p.positions[i] <= p.maxPosition) continue;
+        for (uint32_t idx = tid; idx < p.heads * D; idx += 256)
+            p.out[size_t(i) * p.heads * D + idx] = __builtin_nanf("");
+    }
 }
 
-uint32_t decode_chunk_len() {
-    static uint32_t len = [] {
-        const char* env = std::getenv("AIGPU_DECODE_CHUNK");
-        long v = env ? std::atol(env) : 512;
-        if (v < 256) v = 256;
-        v = v / 256 * 256;
-        return uint32_t(v);
-    }();
-    return len;
+/* combines the chunk records of every (sequence, kv head) with more than one
+   chunk; one workgroup per (sequence, kv head). The per-chunk weights
+   exp2(m_c - M) are staged in LDS so the accumulator loads are independent. */
+template <int D>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
+    constexpr int RS = record_floats(D);
+    constexpr int TILE = 256;   // chunks whose weights sit in LDS at once
+    __shared__ float wts[TILE][MAXG];
+    __shared__ float Mh[MAXG], Lh[MAXG];
+    const DecodeParams& p = a.p;
+    const uint32_t KVH = uint32_t(p.kvHeads), G = uint32_t(p.heads / p.kvHeads);
+    const uint32_t b = blockIdx.x / KVH, kvh = blockIdx.x % KVH;
+    const uint32_t L = p.positions[b];
+    if (L > p.maxPosition) return;
+    const uint32_t nChunks = (L + 1 - first_position(p, L) + a.chunkLen - 1) / a.chunkLen;
+    if (nChunks < 2) return;   // written by the attention kernel itself
+    const float* recs = a.parts + (size_t(b) * KVH + kvh) * a.maxChunks * RS;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+    for (uint32_t h = w; h < G; h += 4) {   // per head: max, then weighted sum of l
+        float mx = -INFINITY;
+        for (uint32_t c = lane; c < nChunks; c += WAVE) mx = fmaxf(mx, recs[size_t(c) * RS + h]);
+        mx = wave_max(mx);
+        float lt = 0.0f;
+        for (uint32_t c = lane; c < nChunks; c += WAVE) {
+            const float* r = recs + size_t(c) * RS;
+            lt += r[MAXG + h] * exp2f(r[h] - mx);
+        }
+        lt = wave_sum(lt);
+        if (lane == 0) {
+            Mh[h] = mx;
+            Lh[h] = lt;
+        }
+    }
+    __syncthreads();
+
+    float acc[(MAXG * D + 255) / 256] = {};
+    for (uint32_t c0 = 0; c0 < nChunks; c0 += TILE) {
+        const uint32_t nc = nChunks - c0 < TILE ? nChunks - c0 : TILE;
+        __syncthreads();
+        for (uint32_t idx = tid; idx < nc * G; idx += 256) {
+            const uint32_t c = idx / G, h = idx % G;
+            wts[c][h] = exp2f(recs[size_t(c0 + c) * RS + h] - Mh[h]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < (MAXG * D + 255) / 256; ++k) {
+            const uint32_t idx = tid + 256 * k;
+            if (idx >= G * D) break;
+            const uint32_t h = idx / D;
+            const float* col = recs + size_t(c0) * RS + 2 * MAXG + idx;
+            float s = 0.0f;
+#pragma unroll 8
+            for (uint32_t c = 0; c < nc; ++c) s += col[size_t(c) * RS] * wts[c][h];
+            acc[k] += s;
+        }
+    }
+    float* outRow = p.out + (size_t(b) * p.heads + size_t(kvh) * G) * D;
+#pragma unroll
+    for (int k = 0; k < (MAXG * D + 255) / 256; ++k) {
+        const uint32_t idx = tid + 256 * k;
+        if (idx < G * D) outRow[idx] = acc[k] / Lh[idx / D];
+    }
+}
+
+uint32_t env_u32(const char* name, uint32_t fallback) {
+    const char* env = std::getenv(name);
+    return env ? uint32_t(std::atol(env)) : fallback;
 }
 
 } // namespace
@@ -322,37 +516,60 @@ bool launch_decode(const DecodeParams& p, hipStream_t stream) {
     if (p.batch == 0) return true;
     if (uint64_t(p.maxPosition) + 1 > p.capacity)
         return ctx.fail("decode: maxPosition + 1 exceeds the cache capacity");
-    if (p.batch > 65535 || p.kvHeads > 65535) return ctx.fail("decode: batch or kvHeads too large");
+    if (p.kvHeads > 65535) return ctx.fail("decode: kvHeads too large");
 
-    DecodeArgs a{};
-    a.p = p;
-    if (a.p.batchStride == 0) a.p.batchStride = p.kvHeads * p.capacity * p.dim;
-    a.chunkLen = decode_chunk_len();
-    a.maxChunks = (p.maxPosition + 1 + a.chunkLen - 1) / a.chunkLen;
-    a.scaleLog2 = LOG2E / sqrtf(float(p.dim));
+    static const uint32_t chunkEnv = env_u32("AIGPU_DECODE_CHUNK", 1024);
+    static const uint32_t gridEnv = env_u32("AIGPU_DECODE_GRID", 512);
+    const uint32_t chunkLen = chunkEnv < 4 * SLAB ? 4 * SLAB : chunkEnv / (4 * SLAB) * (4 * SLAB);
+    const uint32_t maxChunks = (p.maxPosition + 1 + chunkLen - 1) / chunkLen;
+    const uint64_t slice = p.batch < MAXB ? p.batch : MAXB;
     const size_t rs = size_t(record_floats(int(p.dim)));
-    a.parts = static_cast<float*>(
-        ctx.grow(SLOT_DECODE_PARTS, p.batch * p.kvHeads * a.maxChunks * rs * sizeof(float)));
-    if (!a.parts) return false;
+    float* parts = static_cast<float*>(ctx.grow(SLOT_DECODE_PARTS, slice * p.kvHeads * maxChunks * rs * sizeof(float)));
+    if (!parts) return false;
+    uint32_t* qrec = static_cast<uint32_t*>(
+        ctx.grow(SLOT_DECODE_QUERIES, slice * p.kvHeads * size_t(qrec_words(int(p.dim))) * 4));
+    if (!qrec) return false;
 
-    const dim3 grid(a.maxChunks, unsigned(p.kvHeads), unsigned(p.batch));
-    const dim3 mgrid(unsigned(p.heads), unsigned(p.batch));
-    if (p.dim == 128) {
-        if (!ctx.launch("decode_split_kernel", stream, [&] {
-                hipLaunchKernelGGL(decode_split_kernel<128>, grid, dim3(256), 0, stream, a);
-            }))
-            return false;
-        return ctx.launch("decode_merge_kernel", stream, [&] {
-            hipLaunchKernelGGL(decode_merge_kernel<128>, mgrid, dim3(128), 0, stream, a);
-        });
+    const uint64_t batchStride = p.batchStride ? p.batchStride : p.kvHeads * p.capacity * p.dim;
+    for (uint64_t b0 = 0; b0 < p.batch; b0 += slice) {
+        DecodeArgs a{};
+        a.p = p;
+        a.p.batch = (p.batch - b0 < slice) ? p.batch - b0 : slice;
+        a.p.batchStride = batchStride;
+        const size_t es = p.inType == 1 ? 2 : 4;
+        a.p.q = static_cast<const char*>(p.q) + b0 * p.heads * p.qStride * es;
+        a.p.k = static_cast<const char*>(p.k) + b0 * p.kvHeads * p.dim * es;
+        a.p.v = static_cast<const char*>(p.v) + b0 * p.kvHeads * p.dim * es;
+        a.p.out = p.out + b0 * p.heads * p.dim;
+        a.p.keyCache = p.keyCache + b0 * batchStride;
+        a.p.valueCache = p.valueCache + b0 * batchStride;
+        a.p.positions = p.positions + b0;
+        a.parts = parts;
+        a.qrec = qrec;
+        a.chunkLen = chunkLen;
+        a.maxChunks = maxChunks;
+        a.scaleLog2 = LOG2E / sqrtf(float(p.dim));
+        const uint64_t upper = a.p.batch * p.kvHeads * maxChunks;
+        const unsigned grid = unsigned(upper < gridEnv ? upper : gridEnv);
+        const unsigned mgrid = unsigned(a.p.batch * p.kvHeads);
+        const bool ok = p.dim == 128
+            ? ctx.launch("decode_prep_kernel", stream, [&] {
+                  hipLaunchKernelGGL(decode_prep_kernel<128>, dim3(mgrid), dim3(256), 0, stream, a);
+              }) && ctx.launch("decode_attention_kernel", stream, [&] {
+                  hipLaunchKernelGGL(decode_attention_kernel<128>, dim3(grid), dim3(256), 0, stream, a);
+              }) && (maxChunks < 2 || ctx.launch("decode_merge_kernel", stream, [&] {
+                  hipLaunchKernelGGL(decode_merge_kernel<128>, dim3(mgrid), dim3(256), 0, stream, a);
+              }))
+            : ctx.launch("decode_prep_kernel", stream, [&] {
+                  hipLaunchKernelGGL(decode_prep_kernel<64>, dim3(mgrid), dim3(256), 0, stream, a);
+              }) && ctx.launch("decode_attention_kernel", stream, [&] {
+                  hipLaunchKernelGGL(decode_attention_kernel<64>, dim3(grid), dim3(256), 0, stream, a);
+              }) && (maxChunks < 2 || ctx.launch("decode_merge_kernel", stream, [&] {
+                  hipLaunchKernelGGL(decode_merge_kernel<64>, dim3(mgrid), dim3(256), 0, stream, a);
+              }));
+        if (!ok) return false;
     }
-    if (!ctx.launch("decode_split_kernel", stream, [&] {
-            hipLaunchKernelGGL(decode_split_kernel<64>, grid, dim3(256), 0, stream, a);
-        }))
-        return false;
-    return ctx.launch("decode_merge_kernel", stream, [&] {
-        hipLaunchKernelGGL(decode_merge_kernel<64>, mgrid, dim3(128), 0, stream, a);
-    });
+    return true;
 }
 
 } // namespace aigpu
