@@ -50,6 +50,13 @@ def build(verbose=False, jobs=4):
 
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         objs = list(pool.map(compile_one, SOURCES))
+    # a kernel template whose host stub was silently not emitted would only
+    # fail at load time on the GPU box: refuse to link it
+    for obj in objs:
+        syms = subprocess.run(["nm", "-u", obj], capture_output=True, text=True, check=True).stdout
+        missing = [l.split()[-1] for l in syms.splitlines() if "__device_stub__" in l]
+        if missing:
+            raise RuntimeError(f"{obj}: kernel stubs not emitted: {missing}")
     lib = os.path.join(OUT, "libaigpu.so")
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", lib + ".tmp"] + objs)
     os.replace(lib + ".tmp", lib)

@@ -80,12 +80,13 @@ __device__ __forceinline__ bf16x4 read_tr16(const uint16_t* lds) {
 }
 
 /* V slabs in LDS: rows of D halfs, RPL rows per 1 KB DMA block; the 16-byte
-   column block x of row r sits at x ^ v_swizzle(r) */
-__device__ __forceinline__ int v_swizzle(int r) { return 2 * (r & 3); }
+   column block x of row r sits at x ^ v_swizzle(r), so the 8 rows x 32 bytes a
+   32-lane transposed read touches hit distinct banks */
+__device__ __forceinline__ int v_swizzle(int r, int D) { return D == 128 ? 2 * (r & 7) : 2 * ((r >> 1) & 3); }
 
 template <int D>
 __device__ __forceinline__ int v_offset(int r, int x) {
-    return r * D + 8 * (x ^ v_swizzle(r));
+    return r * D + 8 * (x ^ v_swizzle(r, D));
 }
 
 /* s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding) */
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) 
 #pragma unroll
             for (int jj = 0; jj < VLOADS; ++jj) {
                 const int r = jj * RPL + lane / LPR;                 // row within the slab
-                const int cb = (lane % LPR) ^ v_swizzle(r);          // 16-byte column block
+                const int cb = (lane % LPR) ^ v_swizzle(r, D);          // 16-byte column block
                 uint32_t row = p0 + r;
                 if (row > lastRow) row = lastRow;
                 __builtin_amdgcn_global_load_lds(vc + size_t(row) * D + 8 * cb,
@@ -518,9 +519,18 @@ bool launch_decode(const DecodeParams& p, hipStream_t stream) {
         return ctx.fail("decode: maxPosition + 1 exceeds the cache capacity");
     if (p.kvHeads > 65535) return ctx.fail("decode: kvHeads too large");
 
-    static const uint32_t chunkEnv = env_u32("AIGPU_DECODE_CHUNK", 1024);
+    // chunk length: the longest of 2048/1024/512/256 positions that still gives
+    // every resident workgroup (2 per CU) two items; AIGPU_DECODE_CHUNK overrides
+    static const uint32_t chunkEnv = env_u32("AIGPU_DECODE_CHUNK", 0);
     static const uint32_t gridEnv = env_u32("AIGPU_DECODE_GRID", 512);
-    const uint32_t chunkLen = chunkEnv < 4 * SLAB ? 4 * SLAB : chunkEnv / (4 * SLAB) * (4 * SLAB);
+    uint32_t chunkLen = 2048;
+    if (chunkEnv) {
+        chunkLen = chunkEnv < 4 * SLAB ? 4 * SLAB : chunkEnv / (4 * SLAB) * (4 * SLAB);
+    } else {
+        const uint64_t bs = p.batch < MAXB ? p.batch : MAXB;
+        while (chunkLen > 256 && bs * p.kvHeads * ((uint64_t(p.maxPosition) + chunkLen) / chunkLen) < 2ull * gridEnv)
+            chunkLen /= 2;
+    }
     const uint32_t maxChunks = (p.maxPosition + 1 + chunkLen - 1) / chunkLen;
     const uint64_t slice = p.batch < MAXB ? p.batch : MAXB;
     const size_t rs = size_t(record_floats(int(p.dim)));

@@ -15,20 +15,23 @@
 // them near 5e-4, inside the 2e-3 bound, at the same MFMA rate. The KV cache
 // itself stays bf16.
 //
-// Flash kernel layout (one workgroup = 4 waves = 128 query rows of one head,
-// one wave = 32 rows; key tiles of 64):
-//   S^T = K Q^T     A = K rows (LDS), B = Q^T (registers, loaded once)
+// Flash kernel layout (one workgroup = 8 waves = 256 query rows of one head,
+// one wave = 32 rows; key tiles of 64, DMA'd into LDS one tile ahead):
+//   S^T = K Q^T     A = K rows (LDS), B = Q^T (registers, loaded once, already
+//                   scaled by log2(e)/sqrt(D) so the softmax is exp2 of it)
 //                   -> each lane owns one query (lane % 32) and 16 keys, so
 //                      the row max/sum need one exchange with lane ^ 32
-//   O^T += V^T P^T  A = V^T (LDS, stored transposed), B = P^T straight from
-//                      the S^T accumulators -> the softmax rescale of O is
-//                      lane-local
+//   O^T += V^T P^T  A = V^T read straight from row-major V through
+//                      ds_read_b64_tr_b16, B = P^T straight from the S^T
+//                      accumulators -> the softmax rescale of O is lane-local
 // The K tile rows are stored permuted so that accumulator register r of the
 // S^T tile holds key 16*(lane/32) + r, which makes each lane's 8-key slice of
-// P^T contiguous in Vt.
+// P^T 8 consecutive keys.
 #include "context.hpp"
 #include "device.hpp"
 #include "kernels.hpp"
+
+#include <cstdlib>
 
 namespace aigpu {
 
@@ -36,91 +39,166 @@ namespace {
 
 constexpr int PREP_MAX_DIM = 256;
 
+/* grid.y = kv head; each kv head's history [0, start) is one contiguous run */
 __global__ __launch_bounds__(256) void prefill_history_kernel(
     const uint16_t* __restrict__ keyCache, const uint16_t* __restrict__ valueCache,
-    _Float16* __restrict__ kh, _Float16* __restrict__ vh, uint64_t kvHeads, uint64_t start,
-    uint64_t capacity, uint64_t dim, uint64_t T) {
-    const uint64_t per = start * dim, total = kvHeads * per;
-    for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-         i += uint64_t(gridDim.x) * blockDim.x) {
-        const uint64_t kv = i / per, rem = i % per;
-        const uint64_t src = kv * capacity * dim + rem, dst = kv * T * dim + rem;
-        kh[dst] = _Float16(bf16_bits_to_float(keyCache[src]));
-        vh[dst] = _Float16(bf16_bits_to_float(valueCache[src]));
+    _Float16* __restrict__ kh, _Float16* __restrict__ vh, uint32_t per, uint64_t capacity,
+    uint64_t dim, uint64_t T) {
+    const uint64_t kv = blockIdx.y;
+    const uint16_t* ks = keyCache + kv * capacity * dim;
+    const uint16_t* vs = valueCache + kv * capacity * dim;
+    _Float16* kd = kh + kv * T * dim;
+    _Float16* vd = vh + kv * T * dim;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < per; i += gridDim.x * blockDim.x) {
+        kd[i] = _Float16(bf16_bits_to_float(ks[i]));
+        vd[i] = _Float16(bf16_bits_to_float(vs[i]));
     }
 }
 
-/* one wave per (token, head-row); rows [0, heads) are queries, the rest KV heads */
+/* one workgroup per token: the token's q, k, v rows are staged in LDS with all
+   loads in flight at once, its RoPE cos/sin are computed once for every row,
+   then one wave per row normalises, rotates and writes */
 __global__ __launch_bounds__(256) void prefill_prep_kernel(PrefillParams p, _Float16* __restrict__ qh,
                                                            _Float16* __restrict__ kh,
-                                                           _Float16* __restrict__ vh, uint64_t T) {
-    __shared__ float rows[4][PREP_MAX_DIM];
-    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-    const uint64_t perToken = p.heads + p.kvHeads;
-    const uint64_t r = uint64_t(blockIdx.x) * 4 + w;
-    if (r >= p.count * perToken) return;
-    const uint64_t t = r / perToken, h = r % perToken;
-    const uint64_t pos = p.start + t;
-    const int dim = int(p.dim);
-    float* x = rows[w];
+                                                           _Float16* __restrict__ vh, uint64_t T,
+                                                           float qScale) {
+    extern __shared__ float tok[];   // [heads + 2 kvHeads][dim]
+    __shared__ float cs[PREP_MAX_DIM / 2], sn[PREP_MAX_DIM / 2];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
+    const uint64_t t = blockIdx.x, pos = p.start + t;
+    const int dim = int(p.dim), half = p.rotaryDims / 2;
+    const uint64_t H = p.heads, KVH = p.kvHeads;
 
-    if (h < p.heads) {
-        const uint64_t src = (t * p.heads + h) * p.qStride;
-        for (int d = lane; d < dim; d += WAVE) x[d] = load_elem(p.q, src + d, p.inType);
-        wave_sync();
-        norm_rope_row(x, dim, p.qNorm, p.eps, p.normOffset, p.freqs, p.rotaryDims, pos, lane);
-        _Float16* dst = qh + (h * p.count + t) * p.dim;
-        for (int d = lane; d < dim; d += WAVE) dst[d] = _Float16(x[d]);
-    } else {
-        const uint64_t kv = h - p.heads;
-        const uint64_t src = (t * p.kvHeads + kv) * p.dim;
-        for (int d = lane; d < dim; d += WAVE) x[d] = load_elem(p.k, src + d, p.inType);
-        wave_sync();
-        norm_rope_row(x, dim, p.kNorm, p.eps, p.normOffset, p.freqs, p.rotaryDims, pos, lane);
-        const uint64_t work = (kv * T + pos) * p.dim;
-        const uint64_t cache = (kv * p.capacity + pos) * p.dim;
-        for (int d = lane; d < dim; d += WAVE) {
-            kh[work + d] = _Float16(x[d]);
-            p.keyCache[cache + d] = float_to_bf16_bits(x[d]);
-            const float vv = load_elem(p.v, src + d, p.inType);
-            vh[work + d] = _Float16(vv);
-            p.valueCache[cache + d] = float_to_bf16_bits(vv);
+    const uint32_t shift = __builtin_ctz(uint32_t(p.dim));   // dim is 64 or 128
+    const uint32_t nq = uint32_t(H) << shift, nk = uint32_t(KVH) << shift;
+    const size_t qrow = t * H * p.qStride, krow = t * nk;
+    for (uint32_t i = tid; i < nq + 2 * nk; i += 256) {
+        float x;
+        if (i < nq) x = load_elem(p.q, qrow + size_t(i >> shift) * p.qStride + (i & (uint32_t(p.dim) - 1)), p.inType);
+        else if (i < nq + nk) x = load_elem(p.k, krow + (i - nq), p.inType);
+        else x = load_elem(p.v, krow + (i - nq - nk), p.inType);
+        tok[i] = x;
+    }
+    if (p.freqs) {
+        const float fpos = float(pos);   // the reference's fp32 angle (LocalModel.hpp:2632)
+        for (int j = tid; j < half; j += 256) sincosf(fpos * p.freqs[j], &sn[j], &cs[j]);
+    }
+    __syncthreads();
+
+    for (uint64_t h = w; h < H + 2 * KVH; h += 4) {
+        float* x = tok + h * p.dim;
+        const bool isQuery = h < H, isKey = !isQuery && h < H + KVH;
+        if (isQuery || isKey) {
+            const float* gamma = isQuery ? p.qNorm : p.kNorm;
+            if (gamma) {   // rmsNormRow (LocalModel.hpp:1341-1348)
+                float ss = 0.0f;
+                for (int d = lane; d < dim; d += WAVE) ss += x[d] * x[d];
+                ss = wave_sum(ss);
+                const float inv = 1.0f / sqrtf(ss / float(dim) + p.eps);
+                for (int d = lane; d < dim; d += WAVE) x[d] = x[d] * inv * (gamma[d] + p.normOffset);
+                wave_sync();
+            }
+            if (p.freqs) {   // rotate-half pairs (LocalModel.hpp:2636-2641)
+                for (int j = lane; j < half; j += WAVE) {
+                    const float a = x[j], b = x[j + half];
+                    x[j] = a * cs[j] - b * sn[j];
+                    x[j + half] = b * cs[j] + a * sn[j];
+                }
+                wave_sync();
+            }
+        }
+        if (isQuery) {
+            _Float16* dst = qh + (h * p.count + t) * p.dim;
+            for (int d = lane; d < dim; d += WAVE) dst[d] = _Float16(x[d] * qScale);
+        } else {
+            const uint64_t kv = isKey ? h - H : h - H - KVH;
+            const uint64_t work = (kv * T + pos) * p.dim;
+            const uint64_t cache = (kv * p.capacity + pos) * p.dim;
+            _Float16* wdst = isKey ? kh : vh;
+            uint16_t* cdst = isKey ? p.keyCache : p.valueCache;
+            for (int d = lane; d < dim; d += WAVE) {
+                wdst[work + d] = _Float16(x[d]);
+                cdst[cache + d] = float_to_bf16_bits(x[d]);
+            }
         }
     }
 }
 
 struct FlashArgs {
-    const _Float16* qh;  // [heads][count][D]
+    const _Float16* qh;  // [heads][count][D], pre-scaled by log2(e)/sqrt(D)
     const _Float16* kh;  // [kvHeads][T][D]
     const _Float16* vh;  // [kvHeads][T][D]
     float* out;          // [count][heads][D]
     uint32_t count, start, heads, kvHeads, window, T, nQT, xcdRemap;
-    float scaleLog2;
 };
 
-/* LDS row of key k (0..31) inside a 32-key block: the inverse of the A-row to
-   key map pi(i) = 16*((i>>2)&1) + 4*(i>>3) + (i&3) */
-__device__ __forceinline__ int key_to_lds_row(int k) {
-    return 8 * ((k >> 2) & 3) + 4 * (k >> 4) + (k & 3);
+typedef __fp16 fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+/* the S^T MFMA's A row i of a 32-key block is key pi(i) = 16((i>>2)&1) +
+   4(i>>3) + (i&3): accumulator register r of lane group g then holds key
+   16g + r, so each lane's P^T slice is 8 consecutive keys */
+__device__ __forceinline__ int key_of_row(int i) { return 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3); }
+
+/* ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4
+   of the 8-byte rows addressed by lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12 */
+__device__ __forceinline__ half8 read_tr16x2(const _Float16* a0, const _Float16* a1) {
+    typedef __attribute__((address_space(3))) fp16x4 lds_fp16x4;
+    const fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4*)(a0));
+    const fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4*)(a1));
+    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+    const u32x2v l2 = __builtin_bit_cast(u32x2v, lo), h2 = __builtin_bit_cast(u32x2v, hi);
+    return __builtin_bit_cast(half8, u32x4{l2[0], l2[1], h2[0], h2[1]});
 }
 
-template <int D>
-__global__ __launch_bounds__(256, 2) void prefill_flash_kernel(FlashArgs a) {
-    constexpr int BM = 128, BN = 64;
-    constexpr int DB = D / 16;        // 16-wide d blocks of the S^T product
-    constexpr int DT = D / 32;        // 32-wide d tiles of the O^T accumulator
-    constexpr int KSTR = D + 8;       // halfs per K row in LDS
-    constexpr int VSTR = BN + 8;      // halfs per V^T row in LDS
-    constexpr int KCH = D / 8;        // 16-byte chunks per K row
-    constexpr int KLOADS = BN * KCH / 256;
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[BN * KSTR];
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * VSTR];
+/* LDS swizzles: the K tile's 16-byte block c of row i sits at c ^ kswz(i),
+   the V tile's block c of row r at c ^ vswz(r, D) */
+__device__ __forceinline__ int kswz(int i, int D) { return (i / (128 / D)) % (D / 8); }
+__device__ __forceinline__ int vswz(int r, int D) { return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
 
-    uint32_t bid = blockIdx.x;
-    if (a.xcdRemap) bid = (bid % 8) * (gridDim.x / 8) + bid / 8;
-    const uint32_t head = bid % a.heads;
-    const uint32_t qt = a.nQT - 1 - bid / a.heads;   // longest rows first
-    const uint32_t kvh = head / (a.heads / a.kvHeads);
+/* s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding) */
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+/*
+    Flash attention, one workgroup = 8 waves = 256 query rows of one head, one
+    wave = 32 rows; key tiles of 64, double-buffered in LDS and filled by DMA
+    (global_load_lds, 1 KB per wave instruction) one tile ahead.
+
+    LDS K tile: row i holds key pi(i % 32) + 32 (i / 32); the 16-byte column
+    block c of row i sits at c ^ kswz(i, D), so the 16 rows an A-operand read
+    touches hit distinct banks. LDS V tile: natural rows; block c of row r at
+    c ^ vswz(r), so the 4 rows x 64 bytes a 32-lane transposed read touches hit
+    distinct banks.
+*/
+template <int D, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void prefill_flash_kernel(FlashArgs a) {
+    constexpr int BM = 32 * WAVES, BN = 64;
+    constexpr int DB = D / 16;            // 16-deep d blocks of the S^T product
+    constexpr int DT = D / 32;            // 32-row d tiles of the O^T accumulator
+    constexpr int CPR = D / 8;            // 16-byte blocks per row
+    constexpr int RPB = WAVE / CPR;       // rows per 1 KB DMA block
+    constexpr int NBLK = BN / RPB;        // DMA blocks per tile (K or V)
+    constexpr int BPW = NBLK / WAVES;     // DMA blocks per wave per tile (K or V)
+    constexpr int TILE = BN * D;          // halfs per K or V tile
+    static_assert(NBLK % WAVES == 0, "DMA blocks must split evenly over the waves");
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][TILE];
+    __shared__ __attribute__((aligned(16))) _Float16 Vs[2][TILE];
+
+    // Workgroups are dealt round-robin over the 8 XCDs (blockIdx % 8), each
+    // with its own L2. The logical order groups a kv head's query heads, and
+    // contiguous logical ranges land on one XCD, so the G query heads sharing a
+    // kv head walk the same K/V tiles from the same L2 at the same time;
+    // within a kv head, the longest query tiles go first.
+    const uint32_t G = a.heads / a.kvHeads;
+    uint32_t lg = blockIdx.x;
+    if (a.xcdRemap) lg = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;
+    const uint32_t kvh = lg / (G * a.nQT);
+    const uint32_t rest = lg % (G * a.nQT);
+    const uint32_t head = kvh * G + rest % G;
+    const uint32_t qt = a.nQT - 1 - rest / G;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, c = lane & 31;
 
     const uint32_t q0 = qt * BM;
@@ -154,122 +232,130 @@ __global__ __launch_bounds__(256, 2) void prefill_flash_kernel(FlashArgs a) {
     uint32_t kbeg = 0;
     if (a.window && a.start + q0 + 1 > a.window) kbeg = a.start + q0 + 1 - a.window;
     kbeg = kbeg / BN * BN;
+    const uint32_t ntiles = (kend - kbeg + BN - 1) / BN;
 
     const _Float16* kbase = a.kh + size_t(kvh) * a.T * D;
     const _Float16* vbase = a.vh + size_t(kvh) * a.T * D;
-    const int vkq = tid & 15, vdq = tid >> 4;   // V^T staging: keys 4*vkq.., d 8*vdq..
-    u32x4 kreg[KLOADS];
-    u32x4 vreg[4];
 
-    auto gload = [&](uint32_t k0) {
+    auto issue = [&](uint32_t k0, int bf) {
 #pragma unroll
-        for (int i = 0; i < KLOADS; ++i) {
-            const int cidx = tid + 256 * i, row = cidx / KCH, col = cidx % KCH;
-            uint32_t src = k0 + row;
-            if (src > a.T - 1) src = a.T - 1;
-            kreg[i] = *reinterpret_cast<const u32x4*>(kbase + size_t(src) * D + col * 8);
+        for (int n = 0; n < BPW; ++n) {
+            const int blk = w * BPW + n;
+            const int i = blk * RPB + lane / CPR, pos = lane % CPR;
+            uint32_t key = k0 + (i & ~31) + key_of_row(i & 31);
+            if (key > a.T - 1) key = a.T - 1;
+            __builtin_amdgcn_global_load_lds(kbase + size_t(key) * D + 8 * (pos ^ kswz(i, D)),
+                                             (__attribute__((address_space(3))) void*)(&Ks[bf][blk * 512]),
+                                             16, 0, 0);
         }
-        if (vdq < D / 8) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t src = k0 + 4 * vkq + i;
-                if (src > a.T - 1) src = a.T - 1;
-                vreg[i] = *reinterpret_cast<const u32x4*>(vbase + size_t(src) * D + vdq * 8);
-            }
-        }
-    };
-    auto lstore = [&]() {
-#pragma unroll
-        for (int i = 0; i < KLOADS; ++i) {
-            const int cidx = tid + 256 * i, row = cidx / KCH, col = cidx % KCH;
-            const int lrow = (row & ~31) + key_to_lds_row(row & 31);
-            *reinterpret_cast<u32x4*>(&Ks[lrow * KSTR + col * 8]) = kreg[i];
-        }
-        if (vdq < D / 8) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                // dword e of each key row holds d = 8*vdq + 2e (low half) and +1 (high half)
-                u32x2 even, odd;
-                even[0] = (vreg[0][e] & 0xFFFFu) | (vreg[1][e] << 16);
-                even[1] = (vreg[2][e] & 0xFFFFu) | (vreg[3][e] << 16);
-                odd[0] = (vreg[0][e] >> 16) | (vreg[1][e] & 0xFFFF0000u);
-                odd[1] = (vreg[2][e] >> 16) | (vreg[3][e] & 0xFFFF0000u);
-                const int d = 8 * vdq + 2 * e;
-                *reinterpret_cast<u32x2*>(&Vt[d * VSTR + 4 * vkq]) = even;
-                *reinterpret_cast<u32x2*>(&Vt[(d + 1) * VSTR + 4 * vkq]) = odd;
-            }
+        for (int n = 0; n < BPW; ++n) {
+            const int blk = w * BPW + n;
+            const int r = blk * RPB + lane / CPR, pos = lane % CPR;
+            uint32_t key = k0 + r;
+            if (key > a.T - 1) key = a.T - 1;
+            __builtin_amdgcn_global_load_lds(vbase + size_t(key) * D + 8 * (pos ^ vswz(r, D)),
+                                             (__attribute__((address_space(3))) void*)(&Vs[bf][blk * 512]),
+                                             16, 0, 0);
         }
     };
 
-    if (kbeg < kend) gload(kbeg);
-    for (uint32_t k0 = kbeg; k0 < kend; k0 += BN) {
-        __syncthreads();
-        lstore();
-        __syncthreads();
-        if (k0 + BN < kend) gload(k0 + BN);
+    if (ntiles) issue(kbeg, 0);
+    for (uint32_t it = 0; it < ntiles; ++it) {
+        const uint32_t k0 = kbeg + it * BN;
+        const int bf = it & 1;
+        if (it + 1 < ntiles) {
+            issue(k0 + BN, bf ^ 1);
+            wait_vmcnt<2 * BPW>();   // this thread's DMA for tile `it` has landed
+        } else {
+            wait_vmcnt<0>();
+        }
+        __syncthreads();             // ... and every other thread's
 
         bool active = waveActive && k0 <= wPosLast;
         if (a.window && uint64_t(k0) + BN - 1 + a.window < uint64_t(wPosFirst) + 1) active = false;
-        if (!active) continue;
-
-        floatx16 s[2];
+        if (active) {
+            const _Float16* ks = Ks[bf];
+            const _Float16* vs = Vs[bf];
+            floatx16 s[2];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
+                for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
+                const int i = 32 * kb + c;
 #pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                const half8 ka = *reinterpret_cast<const half8*>(&Ks[(32 * kb + c) * KSTR + 16 * db + 8 * g]);
-                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[db], s[kb], 0, 0, 0);
-            }
-        }
-
-        const bool needMask = (k0 + BN - 1 > wPosFirst) ||
-                              (a.window && uint64_t(k0) + a.window < uint64_t(wPosLast) + 1);
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float x = s[kb][r] * a.scaleLog2;
-                if (needMask) {
-                    const uint32_t key = k0 + 32 * kb + 16 * g + r;
-                    if (key > P || (a.window && uint64_t(key) + a.window <= P)) x = -INFINITY;
+                for (int db = 0; db < DB; ++db) {
+                    const half8 ka = *reinterpret_cast<const half8*>(ks + i * D + 8 * ((2 * db + g) ^ kswz(i, D)));
+                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[db], s[kb], 0, 0, 0);
                 }
-                s[kb][r] = x;
-                mx = fmaxf(mx, x);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
-        const float mn = fmaxf(m, mx);
-        const float base = mn == -INFINITY ? 0.0f : mn;
-        const float alpha = exp2f(m - base);
-        float ps = 0.0f;
-        half8 pk[2][2];
+
+            const bool needMask = (k0 + BN - 1 > wPosFirst) ||
+                                  (a.window && uint64_t(k0) + a.window < uint64_t(wPosLast) + 1);
+            if (needMask) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+                for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float pv = exp2f(s[kb][8 * h + j] - base);
-                    ps += pv;
-                    pk[kb][h][j] = _Float16(pv);
-                }
-        lsum = lsum * alpha + ps;
-        m = mn;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+                    for (int r = 0; r < 16; ++r) {
+                        const uint32_t key = k0 + 32 * kb + 16 * g + r;
+                        if (key > P || (a.window && uint64_t(key) + a.window <= P)) s[kb][r] = -INFINITY;
+                    }
+            }
+            float mx = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const half8 va = *reinterpret_cast<const half8*>(
-                        &Vt[(32 * dt + c) * VSTR + 32 * kb + 16 * g + 8 * h]);
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pk[kb][h], o[dt], 0, 0, 0);
-                }
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+            // lazy rescale: the running max only moves when a tile exceeds it by
+            // more than 2^8, so P = exp2(s - m) <= 256 stays exact enough in fp16
+            // and most tiles skip rescaling O
+            const bool grow = mx > m + 8.0f;
+            const float mn = grow ? mx : m;
+            const float alpha = grow ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
+            const bool rescale = __any(grow);
+            const float base = mn == -INFINITY ? 0.0f : mn;
+            float ps = 0.0f;
+            half8 pk[2][2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float pv = __builtin_amdgcn_exp2f(s[kb][8 * h + j] - base);
+                        ps += pv;
+                        pk[kb][h][j] = _Float16(pv);
+                    }
+            lsum = lsum * alpha + ps;
+            m = mn;
+
+            const int q16 = lane & 15, half16 = (lane >> 4) & 1;
+            if (rescale) {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                // V^T rows d = 32dt + lane % 32 with keys 32kb + 16g + 8h + 0..7:
+                // lane q16 of each 16-lane group addresses row P0 + q16/4,
+                // columns dbase + 4 (q16 % 4)
+                const int dbase = 32 * dt + 16 * half16 + 4 * (q16 & 3);
+                const int cb = dbase >> 3, sub = dbase & 7;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int r0 = 32 * kb + 16 * g + 8 * h + (q16 >> 2), r1 = r0 + 4;
+                        const half8 va = read_tr16x2(vs + r0 * D + 8 * (cb ^ vswz(r0, D)) + sub,
+                                                     vs + r1 * D + 8 * (cb ^ vswz(r1, D)) + sub);
+                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pk[kb][h], o[dt], 0, 0, 0);
+                    }
+            }
         }
+        __syncthreads();             // buffer `bf` may be refilled by the next issue
     }
 
     lsum += __shfl_xor(lsum, 32, WAVE);
@@ -302,7 +388,9 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     if (p.count == 0) return true;
     const uint64_t T = p.start + p.count;
     if (p.capacity < T) return ctx.fail("prefill: cache capacity below start + count");
-    if (T >= (1ull << 31) || p.heads * p.count >= (1ull << 31))
+    if ((p.heads + 2 * p.kvHeads) * p.dim * sizeof(float) > 96 * 1024)
+        return ctx.fail("prefill: one token's q, k, v rows exceed 96 KB of LDS");
+    if (T * p.dim >= (1ull << 31) || p.heads * p.count >= (1ull << 31) || p.kvHeads > 65535)
         return ctx.fail("prefill: sequence too long");
 
     _Float16* qh = static_cast<_Float16*>(ctx.grow(SLOT_PREFILL_Q, p.heads * p.count * p.dim * 2));
@@ -311,21 +399,20 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     if (!qh || !kh || !vh) return false;
 
     if (p.start > 0) {
-        const uint64_t total = p.kvHeads * p.start * p.dim;
-        uint64_t blocks = (total + 255) / 256;
-        if (blocks > 65536) blocks = 65536;
+        const uint32_t per = uint32_t(p.start * p.dim);
+        const uint32_t blocks = (per + 255) / 256 < 4096 ? (per + 255) / 256 : 4096;
         if (!ctx.launch("prefill_history_kernel", stream, [&] {
-                hipLaunchKernelGGL(prefill_history_kernel, dim3(unsigned(blocks)), dim3(256), 0, stream,
-                                   p.keyCache, p.valueCache, kh, vh, p.kvHeads, p.start, p.capacity,
-                                   p.dim, T);
+                hipLaunchKernelGGL(prefill_history_kernel, dim3(blocks, unsigned(p.kvHeads)), dim3(256), 0,
+                                   stream, p.keyCache, p.valueCache, kh, vh, per, p.capacity, p.dim, T);
             }))
             return false;
     }
 
-    const uint64_t rows = p.count * (p.heads + p.kvHeads);
+    const float qScale = LOG2E / sqrtf(float(p.dim));
     if (!ctx.launch("prefill_prep_kernel", stream, [&] {
-            hipLaunchKernelGGL(prefill_prep_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, stream,
-                               p, qh, kh, vh, T);
+            hipLaunchKernelGGL(prefill_prep_kernel, dim3(unsigned(p.count)), dim3(256),
+                               (p.heads + 2 * p.kvHeads) * p.dim * sizeof(float), stream, p, qh, kh, vh, T,
+                               qScale);
         }))
         return false;
 
@@ -340,16 +427,19 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     a.kvHeads = uint32_t(p.kvHeads);
     a.window = uint32_t(p.window > 0xFFFFFFFFull ? 0 : p.window);
     a.T = uint32_t(T);
-    a.nQT = uint32_t((p.count + 127) / 128);
-    a.scaleLog2 = LOG2E / sqrtf(float(p.dim));
+    static const int waves = [] {
+        const char* env = std::getenv("AIGPU_PREFILL_WAVES");
+        return env && std::atoi(env) == 8 ? 8 : 4;
+    }();
+    a.nQT = uint32_t((p.count + 32 * waves - 1) / (32 * waves));
     const uint64_t blocks = uint64_t(a.nQT) * p.heads;
     a.xcdRemap = (blocks % 8 == 0) ? 1u : 0u;
-    if (p.dim == 128)
-        return ctx.launch("prefill_flash_kernel", stream, [&] {
-            hipLaunchKernelGGL(prefill_flash_kernel<128>, dim3(unsigned(blocks)), dim3(256), 0, stream, a);
-        });
     return ctx.launch("prefill_flash_kernel", stream, [&] {
-        hipLaunchKernelGGL(prefill_flash_kernel<64>, dim3(unsigned(blocks)), dim3(256), 0, stream, a);
+        const dim3 grid{unsigned(blocks)}, block{unsigned(64 * waves)};
+        if (p.dim == 128 && waves == 8) hipLaunchKernelGGL((prefill_flash_kernel<128, 8>), grid, block, 0, stream, a);
+        else if (p.dim == 128) hipLaunchKernelGGL((prefill_flash_kernel<128, 4>), grid, block, 0, stream, a);
+        else if (waves == 8) hipLaunchKernelGGL((prefill_flash_kernel<64, 8>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((prefill_flash_kernel<64, 4>), grid, block, 0, stream, a);
     });
 }
 
