@@ -124,6 +124,156 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(PrefillParams p, _Flo
     }
 }
 
+/* 8 consecutive input elements, widened to fp32 (16 B of bf16 or 32 B of f32) */
+template <bool F32>
+__device__ __forceinline__ void load8(const void* base, size_t i, float (&x)[8]) {
+    if (F32) {
+        const floatx4* s = reinterpret_cast<const floatx4*>(static_cast<const float*>(base) + i);
+        const floatx4 a = s[0], b = s[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[4 + e] = b[e]; }
+    } else {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[2 * e] = __uint_as_float(w[e] << 16);
+            x[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+        }
+    }
+}
+
+__device__ __forceinline__ void store8_f16(_Float16* dst, const float (&x)[8], float scale) {
+    half8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = _Float16(x[e] * scale);
+    *reinterpret_cast<half8*>(dst) = h;
+}
+
+__device__ __forceinline__ void store8_bf16(uint16_t* dst, const float (&x)[8]) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        w[e] = uint32_t(float_to_bf16_bits(x[2 * e])) | (uint32_t(float_to_bf16_bits(x[2 * e + 1])) << 16);
+    *reinterpret_cast<u32x4*>(dst) = w;
+}
+
+/*
+    The same work as prefill_prep_kernel with every row held in registers:
+    one workgroup per token, D/8 lanes per row, 8 consecutive elements per
+    lane (one 16-byte load of bf16). The RMS sum is a butterfly over the
+    row's lanes; the rotate-half partner of element e (e +- rot/2) sits in
+    lane +- rot/16 at the same slot, which needs rot % 16 == 0. Rows are taken
+    four at a time with all four loads issued before any arithmetic.
+*/
+template <int D, bool F32>
+__global__ __launch_bounds__(256) void prefill_prep_vec_kernel(PrefillParams p, _Float16* __restrict__ qh,
+                                                               _Float16* __restrict__ kh,
+                                                               _Float16* __restrict__ vh, uint32_t T,
+                                                               float qScale) {
+    constexpr int LPR = D / 8, RPP = 256 / LPR, UNROLL = 4;
+    __shared__ float cs[D / 2], sn[D / 2];
+    const int tid = threadIdx.x, sub = tid % LPR, lane = tid % WAVE;
+    const uint32_t t = blockIdx.x, pos = uint32_t(p.start) + t;
+    const uint32_t H = uint32_t(p.heads), KVH = uint32_t(p.kvHeads), rows = H + 2 * KVH;
+    const int half = p.freqs ? p.rotaryDims / 2 : 0;
+    if (tid < half) {
+        const float fpos = float(pos);   // the reference's fp32 angle (LocalModel.hpp:2632)
+        sincosf(fpos * p.freqs[tid], &sn[tid], &cs[tid]);
+    }
+    __syncthreads();
+    // rotate-half partner lane and the sign of its term, per element slot
+    const int e0 = 8 * sub, shiftL = half / 8;
+    const bool lowHalf = e0 < half, highHalf = !lowHalf && e0 < 2 * half;
+    const int partner = lowHalf ? lane + shiftL : (highHalf ? lane - shiftL : lane);
+    float c8[8], s8[8];
+    if (lowHalf || highHalf) {
+        const int j0 = lowHalf ? e0 : e0 - half;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            c8[e] = cs[j0 + e];
+            s8[e] = lowHalf ? -sn[j0 + e] : sn[j0 + e];
+        }
+    }
+
+    for (uint32_t r0 = tid / LPR; r0 < rows; r0 += UNROLL * RPP) {
+        float x[UNROLL][8];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const uint32_t r = r0 + u * RPP;
+            if (r >= rows) continue;
+            if (r < H) load8<F32>(p.q, (size_t(t) * H + r) * p.qStride + e0, x[u]);
+            else if (r < H + KVH) load8<F32>(p.k, (size_t(t) * KVH + (r - H)) * D + e0, x[u]);
+            else load8<F32>(p.v, (size_t(t) * KVH + (r - H - KVH)) * D + e0, x[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const uint32_t r = r0 + u * RPP;
+            if (r >= rows) continue;   // uniform over the row's LPR lanes
+            float (&v)[8] = x[u];
+            if (r < H + KVH) {
+                const float* gamma = r < H ? p.qNorm : p.kNorm;
+                if (gamma) {   // rmsNormRow (LocalModel.hpp:1341-1348)
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+#pragma unroll
+                    for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o, WAVE);
+                    const float inv = 1.0f / sqrtf(ss / float(D) + p.eps);
+                    const floatx4* g = reinterpret_cast<const floatx4*>(gamma + e0);
+                    const floatx4 g0 = g[0], g1 = g[1];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[e] = v[e] * inv * (g0[e] + p.normOffset);
+                        v[4 + e] = v[4 + e] * inv * (g1[e] + p.normOffset);
+                    }
+                }
+                if (half) {   // rotate-half pairs (LocalModel.hpp:2636-2641)
+                    float o8[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o8[e] = __shfl(v[e], partner, WAVE);
+                    if (lowHalf || highHalf) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[e] = v[e] * c8[e] + o8[e] * s8[e];
+                    }
+                }
+            }
+            if (r < H) {
+                store8_f16(qh + (size_t(r) * p.count + t) * D + e0, v, qScale);
+            } else {
+                const bool isKey = r < H + KVH;
+                const uint32_t kv = isKey ? r - H : r - H - KVH;
+                store8_f16((isKey ? kh : vh) + (size_t(kv) * T + pos) * D + e0, v, 1.0f);
+                store8_bf16((isKey ? p.keyCache : p.valueCache) + (size_t(kv) * p.capacity + pos) * D + e0, v);
+            }
+        }
+    }
+}
+
+/* prefill_history_kernel with 8 elements (16 B) per lane and step */
+__global__ __launch_bounds__(256) void prefill_history_vec_kernel(
+    const uint16_t* __restrict__ keyCache, const uint16_t* __restrict__ valueCache,
+    _Float16* __restrict__ kh, _Float16* __restrict__ vh, uint32_t per8, uint64_t capacity,
+    uint32_t dim, uint32_t T) {
+    const uint32_t kv = blockIdx.y;
+    const u32x4* ks = reinterpret_cast<const u32x4*>(keyCache + kv * capacity * dim);
+    const u32x4* vs = reinterpret_cast<const u32x4*>(valueCache + kv * capacity * dim);
+    half8* kd = reinterpret_cast<half8*>(kh + size_t(kv) * T * dim);
+    half8* vd = reinterpret_cast<half8*>(vh + size_t(kv) * T * dim);
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < per8; i += gridDim.x * blockDim.x) {
+        const u32x4 a = ks[i], b = vs[i];
+        half8 x, y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[2 * e] = _Float16(__uint_as_float(a[e] << 16));
+            x[2 * e + 1] = _Float16(__uint_as_float(a[e] & 0xFFFF0000u));
+            y[2 * e] = _Float16(__uint_as_float(b[e] << 16));
+            y[2 * e + 1] = _Float16(__uint_as_float(b[e] & 0xFFFF0000u));
+        }
+        kd[i] = x;
+        vd[i] = y;
+    }
+}
+
 struct FlashArgs {
     const _Float16* qh;  // [heads][count][D], pre-scaled by log2(e)/sqrt(D)
     const _Float16* kh;  // [kvHeads][T][D]
@@ -398,21 +548,51 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     _Float16* vh = static_cast<_Float16*>(ctx.grow(SLOT_PREFILL_V, p.kvHeads * T * p.dim * 2));
     if (!qh || !kh || !vh) return false;
 
+    // the register-row kernels need 16-byte aligned rows and rot % 16 == 0
+    const size_t inAlign = p.inType == 0 ? 4 : 8;   // elements per 16 bytes
+    auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    const bool vec = aligned(p.q) && aligned(p.k) && aligned(p.v) && aligned(p.keyCache) &&
+                     aligned(p.valueCache) && (p.qStride % inAlign) == 0 &&
+                     (!p.qNorm || aligned(p.qNorm)) && (!p.kNorm || aligned(p.kNorm)) &&
+                     (!p.freqs || (p.rotaryDims % 16) == 0);
+
     if (p.start > 0) {
         const uint32_t per = uint32_t(p.start * p.dim);
-        const uint32_t blocks = (per + 255) / 256 < 4096 ? (per + 255) / 256 : 4096;
+        const uint32_t per8 = per / 8;   // dim is a multiple of 8
+        const uint32_t work = vec ? per8 : per;
+        const uint32_t blocks = (work + 255) / 256 < 4096 ? (work + 255) / 256 : 4096;
         if (!ctx.launch("prefill_history_kernel", stream, [&] {
-                hipLaunchKernelGGL(prefill_history_kernel, dim3(blocks, unsigned(p.kvHeads)), dim3(256), 0,
-                                   stream, p.keyCache, p.valueCache, kh, vh, per, p.capacity, p.dim, T);
+                const dim3 grid{blocks, unsigned(p.kvHeads)};
+                if (vec)
+                    hipLaunchKernelGGL(prefill_history_vec_kernel, grid, dim3(256), 0, stream, p.keyCache,
+                                       p.valueCache, kh, vh, per8, p.capacity, uint32_t(p.dim), uint32_t(T));
+                else
+                    hipLaunchKernelGGL(prefill_history_kernel, grid, dim3(256), 0, stream, p.keyCache,
+                                       p.valueCache, kh, vh, per, p.capacity, p.dim, T);
             }))
             return false;
     }
 
     const float qScale = LOG2E / sqrtf(float(p.dim));
     if (!ctx.launch("prefill_prep_kernel", stream, [&] {
-            hipLaunchKernelGGL(prefill_prep_kernel, dim3(unsigned(p.count)), dim3(256),
-                               (p.heads + 2 * p.kvHeads) * p.dim * sizeof(float), stream, p, qh, kh, vh, T,
-                               qScale);
+            const dim3 grid{unsigned(p.count)}, block{256};
+            const uint32_t t32 = uint32_t(T);
+            if (!vec)
+                hipLaunchKernelGGL(prefill_prep_kernel, grid, block,
+                                   (p.heads + 2 * p.kvHeads) * p.dim * sizeof(float), stream, p, qh, kh, vh, T,
+                                   qScale);
+            else if (p.dim == 128 && p.inType == 1)
+                hipLaunchKernelGGL((prefill_prep_vec_kernel<128, false>), grid, block, 0, stream, p, qh, kh, vh,
+                                   t32, qScale);
+            else if (p.dim == 128)
+                hipLaunchKernelGGL((prefill_prep_vec_kernel<128, true>), grid, block, 0, stream, p, qh, kh, vh,
+                                   t32, qScale);
+            else if (p.inType == 1)
+                hipLaunchKernelGGL((prefill_prep_vec_kernel<64, false>), grid, block, 0, stream, p, qh, kh, vh,
+                                   t32, qScale);
+            else
+                hipLaunchKernelGGL((prefill_prep_vec_kernel<64, true>), grid, block, 0, stream, p, qh, kh, vh,
+                                   t32, qScale);
         }))
         return false;
 

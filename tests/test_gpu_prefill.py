@@ -12,7 +12,7 @@ pytestmark = pytest.mark.gpu
 
 
 def run_case(gpu, count, start, H, KV, D, seed, norm=True, rope=True, window=0, dtype="bf16",
-             rows=None, theta=1e6, q_stride=None):
+             rows=None, theta=1e6, q_stride=None, rot=None):
     """Builds seeded inputs, runs the GPU prefill and the oracle; returns
     (oracle out, gpu out, oracle-normed keys, gpu caches)."""
     import torch
@@ -30,7 +30,8 @@ def run_case(gpu, count, start, H, KV, D, seed, norm=True, rope=True, window=0, 
         dq, dk, dv = dev_f32(q), dev_f32(k), dev_f32(v)
     gq = gammas(D, seed, "q_norm") if norm else None
     gk = gammas(D, seed, "k_norm") if norm else None
-    fr = O.rotary_frequencies(D, theta) if rope else None
+    rot = rot or D
+    fr = O.rotary_frequencies(rot, theta) if rope else None
     # cached history [0, start): bf16 values in the head-major cache
     hkb, hk = bf16_normal((KV, start, D), seed, "k_cache")
     hvb, hv = bf16_normal((KV, start, D), seed, "v_cache")
@@ -41,7 +42,7 @@ def run_case(gpu, count, start, H, KV, D, seed, norm=True, rope=True, window=0, 
     key_cache, value_cache = dev_bf16(kc), dev_bf16(vc)
 
     # oracle: norm + RoPE on fp32 (widened) inputs, then attention over history + new
-    qn, kn = O.qk_norm_rope(q, k, count, start, H, KV, D, qs, gq, gk, 1e-6, fr, D)
+    qn, kn = O.qk_norm_rope(q, k, count, start, H, KV, D, qs, gq, gk, 1e-6, fr, rot)
     keys = np.concatenate([hk.transpose(1, 0, 2), kn], 0)
     vals = np.concatenate([hv.transpose(1, 0, 2), v], 0)
     ref = O.attention_strided(qn, keys, vals, count, start, H, KV, D, qs, KV * D, D, window,
@@ -52,7 +53,7 @@ def run_case(gpu, count, start, H, KV, D, seed, norm=True, rope=True, window=0, 
     gpu.prefill(dq, dk, dv, out, key_cache, value_cache, start, H, KV, D, q_stride=qs,
                 q_norm=None if gq is None else dev_f32(gq),
                 k_norm=None if gk is None else dev_f32(gk),
-                freqs=None if fr is None else dev_f32(fr), rotary_dims=D, window=window)
+                freqs=None if fr is None else dev_f32(fr), rotary_dims=rot, window=window)
     got = host(out)
     if rows is not None:
         got = got[rows]
@@ -91,6 +92,26 @@ def test_q_stride_with_gate_halves(gpu):
     # Qwen3.5-style q rows carry a gate after each head (qStride = 2D, LocalModel.hpp:2583)
     ref, got, *_ = run_case(gpu, 40, 0, 4, 2, 64, 44, q_stride=128)
     assert_bf16_parity(ref, got, "qStride 2D")
+
+
+@pytest.mark.parametrize("rot", [32, 24])
+def test_partial_rotary(gpu, rot):
+    # rot % 16 == 0 takes the register-row prep kernel, other even widths the
+    # LDS-row one
+    ref, got, *_ = run_case(gpu, 90, 7, 4, 2, 128, 46, rot=rot)
+    assert_bf16_parity(ref, got, f"rotary {rot} of 128")
+
+
+@pytest.mark.parametrize("qs", [72, 68])
+def test_q_stride_alignment(gpu, qs):
+    # a 16-byte multiple row stride (72 bf16) and one that is not (68)
+    ref, got, *_ = run_case(gpu, 60, 5, 4, 2, 64, 47, q_stride=qs)
+    assert_bf16_parity(ref, got, f"qStride {qs}")
+
+
+def test_fp32_inputs_gqa_norm_rope_history(gpu):
+    ref, got, *_ = run_case(gpu, 70, 30, 8, 2, 128, 48, dtype="f32")
+    assert_bf16_parity(ref, got, "fp32 inputs with history")
 
 
 def test_single_token_and_ragged_tiles(gpu):
