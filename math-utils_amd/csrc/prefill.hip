@@ -32,6 +32,7 @@
 #include "kernels.hpp"
 
 #include <cstdlib>
+#include <type_traits>
 
 namespace aigpu {
 
@@ -312,19 +313,42 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+/* s_waitcnt lgkmcnt(0) (vmcnt and expcnt left alone), then s_barrier. Unlike
+   __syncthreads() it carries no workgroup release fence, which on gfx950 waits
+   for every outstanding vector-memory operation (vmcnt(0)) and so would also
+   wait for the DMA of tiles prefetched for later iterations; DMA completion is
+   ordered by the explicit vmcnt waits instead. The signal fences keep the
+   compiler from moving LDS accesses across the barrier. */
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 /*
-    Flash attention, one workgroup = 8 waves = 256 query rows of one head, one
-    wave = 32 rows; key tiles of 64, double-buffered in LDS and filled by DMA
-    (global_load_lds, 1 KB per wave instruction) one tile ahead.
+    Flash attention, one workgroup = WAVES waves of 32 query rows of one
+    head; key tiles of 64 keys staged in LDS by DMA (global_load_lds, 1 KB
+    per wave instruction) in STAGES stages, STAGES - 1 tiles ahead of the one
+    being computed. One barrier per tile: past it, tile `it` has landed for
+    every wave and every wave has finished tile it - 1, whose stage is then
+    refilled. Per tile a wave runs S^T = K Q^T (16 MFMAs for D = 128), the
+    online softmax, and O^T += V^T P^T (16 MFMAs).
+
+    Every wave computes every tile of the workgroup's key range; keys past a
+    row's position (or outside its window) are masked, so such tiles add
+    exactly nothing, and the loop stays single-path.
 
     LDS K tile: row i holds key pi(i % 32) + 32 (i / 32); the 16-byte column
     block c of row i sits at c ^ kswz(i, D), so the 16 rows an A-operand read
-    touches hit distinct banks. LDS V tile: natural rows; block c of row r at
-    c ^ vswz(r), so the 4 rows x 64 bytes a 32-lane transposed read touches hit
-    distinct banks.
+    touches hit distinct banks (a fragment-major layout reads linearly but
+    makes each DMA instruction gather 32 rows x 32 bytes, which costs more
+    than it saves). LDS V tile: natural rows; block c of row r at c ^ vswz(r),
+    so the 4 rows x 64 bytes a 32-lane transposed read touches hit distinct
+    banks.
 */
-template <int D, int WAVES>
-__global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void prefill_flash_kernel(FlashArgs a) {
+template <int D, int WAVES, int STAGES>
+__global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_kernel(FlashArgs a) {
     constexpr int BM = 32 * WAVES, BN = 64;
     constexpr int DB = D / 16;            // 16-deep d blocks of the S^T product
     constexpr int DT = D / 32;            // 32-row d tiles of the O^T accumulator
@@ -333,9 +357,30 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void prefill_flash_kernel(Fl
     constexpr int NBLK = BN / RPB;        // DMA blocks per tile (K or V)
     constexpr int BPW = NBLK / WAVES;     // DMA blocks per wave per tile (K or V)
     constexpr int TILE = BN * D;          // halfs per K or V tile
+    constexpr int AHEAD = STAGES - 1;     // DMA distance in tiles
+    constexpr int PER = 2 * BPW;          // DMA instructions per wave per tile
     static_assert(NBLK % WAVES == 0, "DMA blocks must split evenly over the waves");
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][TILE];
-    __shared__ __attribute__((aligned(16))) _Float16 Vs[2][TILE];
+    static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 LDS stages");
+    // One LDS object per stage and operand, always indexed by a compile-time
+    // stage: the compiler then tells a read of stage j from the DMA still in
+    // flight into the other stages and waits on stage j's DMA only.
+    // V first: its stages sit below 64 KB, inside the 16-bit offset of a DS
+    // instruction, so every V read is a per-d-tile lane address plus an
+    // immediate; K needs one lane address per stage
+    __shared__ __attribute__((aligned(16))) _Float16 V0[TILE], V1[TILE], V2[TILE], V3[TILE];
+    __shared__ __attribute__((aligned(16))) _Float16 K0[TILE], K1[TILE], K2[TILE], K3[TILE];
+    auto kbuf = [&](auto j) __attribute__((always_inline)) -> _Float16* {
+        if constexpr (decltype(j)::value == 0) return K0;
+        else if constexpr (decltype(j)::value == 1) return K1;
+        else if constexpr (decltype(j)::value == 2) return K2;
+        else return K3;
+    };
+    auto vbuf = [&](auto j) __attribute__((always_inline)) -> _Float16* {
+        if constexpr (decltype(j)::value == 0) return V0;
+        else if constexpr (decltype(j)::value == 1) return V1;
+        else if constexpr (decltype(j)::value == 2) return V2;
+        else return V3;
+    };
 
     // Workgroups are dealt round-robin over the 8 XCDs (blockIdx % 8), each
     // with its own L2. The logical order groups a kv head's query heads, and
@@ -356,7 +401,6 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void prefill_flash_kernel(Fl
     const uint32_t tq = wq0 + c;
     const bool rowValid = tq < a.count;
     const uint32_t P = a.start + tq;
-    const bool waveActive = wq0 < a.count;
     const uint32_t wLast = (wq0 + 31 < a.count ? wq0 + 31 : a.count - 1);
     const uint32_t wPosFirst = a.start + wq0, wPosLast = a.start + wLast;
 
@@ -368,6 +412,11 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void prefill_flash_kernel(Fl
             if (rowValid) qreg[db] = *reinterpret_cast<const half8*>(qrow + 16 * db + 8 * g);
             else qreg[db] = half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
+        // Q lands before any DMA is issued, so the vmcnt waits in the loop
+        // only ever count DMA
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        wait_vmcnt<0>();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
 
     floatx16 o[DT];
@@ -377,6 +426,8 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void prefill_flash_kernel(Fl
         for (int r = 0; r < 16; ++r) o[dt][r] = 0.0f;
     float m = -INFINITY, lsum = 0.0f;
 
+    // key tiles [kbeg, kend) cover every row of the workgroup; count >= 1, so
+    // there is at least one
     const uint32_t tileLast = (q0 + BM < a.count ? q0 + BM : a.count) - 1;
     const uint32_t kend = a.start + tileLast + 1;
     uint32_t kbeg = 0;
@@ -387,125 +438,205 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void prefill_flash_kernel(Fl
     const _Float16* kbase = a.kh + size_t(kvh) * a.T * D;
     const _Float16* vbase = a.vh + size_t(kvh) * a.T * D;
 
-    auto issue = [&](uint32_t k0, int bf) {
+    // per-lane element offsets of this wave's DMA block n inside one tile,
+    // recomputed at each issue (a few integer ops) rather than held in
+    // registers across the loop; a tile that runs past the last key clamps
+    // its rows to T - 1 instead
+    auto dma_offsets = [&](int n, uint32_t& ko, uint32_t& vo) __attribute__((always_inline)) {
+        const int blk = w * BPW + n;
+        const int i = blk * RPB + lane / CPR, pos = lane % CPR;
+        ko = uint32_t(((i & ~31) + key_of_row(i & 31)) * D + 8 * (pos ^ kswz(i, D)));
+        vo = uint32_t(i * D + 8 * (pos ^ vswz(i, D)));
+    };
+    auto issue = [&](uint32_t k0, auto bf) __attribute__((always_inline)) {
+        _Float16* kd = kbuf(bf);
+        _Float16* vd = vbuf(bf);
+        const _Float16* kt = kbase + size_t(k0) * D;
+        const _Float16* vt = vbase + size_t(k0) * D;
+        const bool tail = k0 + BN > a.T;
+        uint32_t koff[BPW], voff[BPW];
+#pragma unroll
+        for (int n = 0; n < BPW; ++n) dma_offsets(n, koff[n], voff[n]);
 #pragma unroll
         for (int n = 0; n < BPW; ++n) {
-            const int blk = w * BPW + n;
-            const int i = blk * RPB + lane / CPR, pos = lane % CPR;
-            uint32_t key = k0 + (i & ~31) + key_of_row(i & 31);
-            if (key > a.T - 1) key = a.T - 1;
-            __builtin_amdgcn_global_load_lds(kbase + size_t(key) * D + 8 * (pos ^ kswz(i, D)),
-                                             (__attribute__((address_space(3))) void*)(&Ks[bf][blk * 512]),
+            uint32_t off = koff[n];
+            if (tail) {
+                const uint32_t key = k0 + off / D;
+                if (key > a.T - 1) off = (a.T - 1 - k0) * D + off % D;
+            }
+            __builtin_amdgcn_global_load_lds(kt + off,
+                                             (__attribute__((address_space(3))) void*)(kd + (w * BPW + n) * 512),
                                              16, 0, 0);
         }
 #pragma unroll
         for (int n = 0; n < BPW; ++n) {
-            const int blk = w * BPW + n;
-            const int r = blk * RPB + lane / CPR, pos = lane % CPR;
-            uint32_t key = k0 + r;
-            if (key > a.T - 1) key = a.T - 1;
-            __builtin_amdgcn_global_load_lds(vbase + size_t(key) * D + 8 * (pos ^ vswz(r, D)),
-                                             (__attribute__((address_space(3))) void*)(&Vs[bf][blk * 512]),
+            uint32_t off = voff[n];
+            if (tail) {
+                const uint32_t key = k0 + off / D;
+                if (key > a.T - 1) off = (a.T - 1 - k0) * D + off % D;
+            }
+            __builtin_amdgcn_global_load_lds(vt + off,
+                                             (__attribute__((address_space(3))) void*)(vd + (w * BPW + n) * 512),
                                              16, 0, 0);
         }
     };
 
-    if (ntiles) issue(kbeg, 0);
-    for (uint32_t it = 0; it < ntiles; ++it) {
-        const uint32_t k0 = kbeg + it * BN;
-        const int bf = it & 1;
-        if (it + 1 < ntiles) {
-            issue(k0 + BN, bf ^ 1);
-            wait_vmcnt<2 * BPW>();   // this thread's DMA for tile `it` has landed
-        } else {
-            wait_vmcnt<0>();
+    // V^T rows d = 32dt + lane % 32 with keys 32kb + 16g + 8h + 0..7: lane
+    // q16 of each 16-lane group addresses row 32kb + 16g + 8h + q16/4 (and the
+    // row 4 below), columns 32dt + 16 (lane / 16 % 2) + 4 (q16 % 4). The
+    // swizzle depends on the row only through q16 / 4 (kb, h and the +4 keep
+    // row % 4), so each d tile needs one lane address and kb, h are immediates.
+    int vaddr[DT];
+    {
+        const int q16 = lane & 15, half16 = (lane >> 4) & 1, rl = 16 * g + (q16 >> 2);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const int dbase = 32 * dt + 16 * half16 + 4 * (q16 & 3);
+            vaddr[dt] = rl * D + 8 * ((dbase >> 3) ^ vswz(rl, D)) + (dbase & 7);
         }
-        __syncthreads();             // ... and every other thread's
+    }
+    static_assert(D == 128 || D == 64, "vswz keeps row % 4 (D 128) or row % 4 / 2 (D 64)");
+    // K A-operand rows 32 kb + c, 16-byte block 2 db + g at (2 db + g) ^
+    // kswz(row); kswz depends on the row only through c, so kb is an immediate
+    int kaddr[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) kaddr[db] = c * D + 8 * ((2 * db + g) ^ kswz(c, D));
+    // Each step passes the lane addresses through an empty asm: the compiler
+    // then cannot hoist (stage base + lane address) out of the loop into one
+    // register per stage and d tile, and folds each stage base, a link-time
+    // constant, into the DS offset instead.
+    auto opaque_addresses = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) asm volatile("" : "+v"(vaddr[dt]));
+#pragma unroll
+        for (int db = 0; db < DB; ++db) asm volatile("" : "+v"(kaddr[db]));
+    };
+    // wait for tile `it` (stage J), barrier, refill the stage of tile it - 1
+    // with tile it + STAGES - 1
+    auto sync = [&](uint32_t it, auto J) __attribute__((always_inline)) {
+        constexpr int bf = decltype(J)::value;
+        const uint32_t after = ntiles - 1 - it;   // tiles issued after `it`: min(AHEAD - 1, after)
+        if (AHEAD >= 3 && after >= 2) wait_vmcnt<(AHEAD >= 3 ? 2 : 0) * PER>();
+        else if (AHEAD >= 2 && after >= 1) wait_vmcnt<(AHEAD >= 2 ? 1 : 0) * PER>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        opaque_addresses();
+        if (it + AHEAD < ntiles)
+            issue(kbeg + (it + AHEAD) * BN, std::integral_constant<int, (bf + AHEAD) % STAGES>{});
+    };
 
-        bool active = waveActive && k0 <= wPosLast;
-        if (a.window && uint64_t(k0) + BN - 1 + a.window < uint64_t(wPosFirst) + 1) active = false;
-        if (active) {
-            const _Float16* ks = Ks[bf];
-            const _Float16* vs = Vs[bf];
-            floatx16 s[2];
+    // S^T = K Q^T for the tile in stage J (keys from k0), masked
+    auto scores = [&](uint32_t k0, auto J, floatx16 (&s)[2]) __attribute__((always_inline)) {
+        const _Float16* ks = kbuf(J);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
-                const int i = 32 * kb + c;
+            for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
 #pragma unroll
-                for (int db = 0; db < DB; ++db) {
-                    const half8 ka = *reinterpret_cast<const half8*>(ks + i * D + 8 * ((2 * db + g) ^ kswz(i, D)));
-                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[db], s[kb], 0, 0, 0);
+            for (int db = 0; db < DB; ++db) {
+                const half8 ka = *reinterpret_cast<const half8*>(ks + kaddr[db] + 32 * kb * D);
+                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[db], s[kb], 0, 0, 0);
+            }
+        }
+        const bool needMask = (k0 + BN - 1 > wPosFirst) ||
+                              (a.window && uint64_t(k0) + a.window < uint64_t(wPosLast) + 1);
+        if (needMask) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t key = k0 + 32 * kb + 16 * g + r;
+                    if (key > P || (a.window && uint64_t(key) + a.window <= P)) s[kb][r] = -INFINITY;
                 }
-            }
-
-            const bool needMask = (k0 + BN - 1 > wPosFirst) ||
-                                  (a.window && uint64_t(k0) + a.window < uint64_t(wPosLast) + 1);
-            if (needMask) {
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const uint32_t key = k0 + 32 * kb + 16 * g + r;
-                        if (key > P || (a.window && uint64_t(key) + a.window <= P)) s[kb][r] = -INFINITY;
-                    }
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
-            // lazy rescale: the running max only moves when a tile exceeds it by
-            // more than 2^8, so P = exp2(s - m) <= 256 stays exact enough in fp16
-            // and most tiles skip rescaling O
-            const bool grow = mx > m + 8.0f;
-            const float mn = grow ? mx : m;
-            const float alpha = grow ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
-            const bool rescale = __any(grow);
-            const float base = mn == -INFINITY ? 0.0f : mn;
-            float ps = 0.0f;
-            half8 pk[2][2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const float pv = __builtin_amdgcn_exp2f(s[kb][8 * h + j] - base);
-                        ps += pv;
-                        pk[kb][h][j] = _Float16(pv);
-                    }
-            lsum = lsum * alpha + ps;
-            m = mn;
-
-            const int q16 = lane & 15, half16 = (lane >> 4) & 1;
-            if (rescale) {
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-            }
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                // V^T rows d = 32dt + lane % 32 with keys 32kb + 16g + 8h + 0..7:
-                // lane q16 of each 16-lane group addresses row P0 + q16/4,
-                // columns dbase + 4 (q16 % 4)
-                const int dbase = 32 * dt + 16 * half16 + 4 * (q16 & 3);
-                const int cb = dbase >> 3, sub = dbase & 7;
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const int r0 = 32 * kb + 16 * g + 8 * h + (q16 >> 2), r1 = r0 + 4;
-                        const half8 va = read_tr16x2(vs + r0 * D + 8 * (cb ^ vswz(r0, D)) + sub,
-                                                     vs + r1 * D + 8 * (cb ^ vswz(r1, D)) + sub);
-                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pk[kb][h], o[dt], 0, 0, 0);
-                    }
-            }
         }
-        __syncthreads();             // buffer `bf` may be refilled by the next issue
+    };
+
+    // online softmax of one tile: P^T (fp16) into pk, running max and sum,
+    // and O moved to the new running max
+    auto softmax = [&](floatx16 (&s)[2], half8 (&pk)[2][2]) __attribute__((always_inline)) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+        {   // lanes l and l ^ 32 hold the two key halves of one query
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+            mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        // lazy rescale: the running max only moves when a tile exceeds it by
+        // more than 2^8, so P = exp2(s - m) <= 256 stays exact enough in fp16
+        // and most tiles skip rescaling O
+        const bool grow = mx > m + 8.0f;
+        const float mn = grow ? mx : m;
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
+        const float base = mn == -INFINITY ? 0.0f : mn;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) pk[kb][h][j] = _Float16(__builtin_amdgcn_exp2f(s[kb][8 * h + j] - base));
+        // the row sum adds the fp16 P that the P.V product uses, in fp32
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        float ps[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 8; j += 2)
+                    ps[kb] = __builtin_amdgcn_fdot2(h2{pk[kb][h][j], pk[kb][h][j + 1]}, h2{1, 1}, ps[kb], false);
+        lsum = lsum * alpha + (ps[0] + ps[1]);
+        m = mn;
+        if (__any(grow)) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+        }
+    };
+
+    // O^T += V^T P^T for the tile in stage J
+    auto pv = [&](auto J, const half8 (&pk)[2][2]) __attribute__((always_inline)) {
+        const _Float16* vs = vbuf(J);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const _Float16* a0 = vs + vaddr[dt] + (32 * kb + 8 * h) * D;
+                    const half8 va = read_tr16x2(a0, a0 + 4 * D);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pk[kb][h], o[dt], 0, 0, 0);
+                }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    issue(kbeg, S0{});
+    if constexpr (AHEAD > 1)
+        if (ntiles > 1) issue(kbeg + BN, S1{});
+    if constexpr (AHEAD > 2)
+        if (ntiles > 2) issue(kbeg + 2 * BN, S2{});
+
+    // step `it` in stage it % STAGES: S, softmax, O += P V for one tile
+    auto step = [&](uint32_t it, auto J) __attribute__((always_inline)) -> bool {
+        if (it >= ntiles) return false;
+        floatx16 s[2];
+        half8 pk[2][2];
+        sync(it, J);
+        scores(kbeg + it * BN, J, s);
+        softmax(s, pk);
+        pv(J, pk);
+        return true;
+    };
+    for (uint32_t it = 0;; it += STAGES) {
+        if (!step(it, S0{})) break;
+        if (!step(it + 1, S1{})) break;
+        if constexpr (STAGES > 2)
+            if (!step(it + 2, S2{})) break;
+        if constexpr (STAGES > 3)
+            if (!step(it + 3, std::integral_constant<int, 3>{})) break;
     }
 
     lsum += __shfl_xor(lsum, 32, WAVE);
@@ -607,19 +738,28 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     a.kvHeads = uint32_t(p.kvHeads);
     a.window = uint32_t(p.window > 0xFFFFFFFFull ? 0 : p.window);
     a.T = uint32_t(T);
+    // AIGPU_PREFILL_WAVES / AIGPU_PREFILL_STAGES pick the tiling (tuning);
+    // 4-wave workgroups run two per CU and take two stages
     static const int waves = [] {
         const char* env = std::getenv("AIGPU_PREFILL_WAVES");
-        return env && std::atoi(env) == 8 ? 8 : 4;
+        return env && std::atoi(env) == 4 ? 4 : 8;
+    }();
+    static const int stages = [] {
+        const char* env = std::getenv("AIGPU_PREFILL_STAGES");
+        const int n = env ? std::atoi(env) : 3;
+        return waves == 4 ? 2 : (n >= 2 && n <= 4 ? n : 3);
     }();
     a.nQT = uint32_t((p.count + 32 * waves - 1) / (32 * waves));
     const uint64_t blocks = uint64_t(a.nQT) * p.heads;
     a.xcdRemap = (blocks % 8 == 0) ? 1u : 0u;
     return ctx.launch("prefill_flash_kernel", stream, [&] {
         const dim3 grid{unsigned(blocks)}, block{unsigned(64 * waves)};
-        if (p.dim == 128 && waves == 8) hipLaunchKernelGGL((prefill_flash_kernel<128, 8>), grid, block, 0, stream, a);
-        else if (p.dim == 128) hipLaunchKernelGGL((prefill_flash_kernel<128, 4>), grid, block, 0, stream, a);
-        else if (waves == 8) hipLaunchKernelGGL((prefill_flash_kernel<64, 8>), grid, block, 0, stream, a);
-        else hipLaunchKernelGGL((prefill_flash_kernel<64, 4>), grid, block, 0, stream, a);
+#define AIGPU_FLASH(DD, WV, ST) \
+    if (p.dim == DD && waves == WV && stages == ST) \
+        hipLaunchKernelGGL((prefill_flash_kernel<DD, WV, ST>), grid, block, 0, stream, a)
+        AIGPU_FLASH(128, 8, 2); AIGPU_FLASH(128, 8, 3); AIGPU_FLASH(128, 8, 4); AIGPU_FLASH(128, 4, 2);
+        AIGPU_FLASH(64, 8, 2); AIGPU_FLASH(64, 8, 3); AIGPU_FLASH(64, 8, 4); AIGPU_FLASH(64, 4, 2);
+#undef AIGPU_FLASH
     });
 }
 
