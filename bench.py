@@ -35,6 +35,13 @@ PEAK_MFMA_F32 = 157.3       # TFLOP/s, fp32
 PEAK_HBM = 8000.0           # GB/s
 CPU_THREADS_CAP = 16        # the GPU box's CPU share for one GPU
 
+# HBM bytes per launch of prefill_flash_kernel<128, 8, 3> on configs[2]:
+# rocprofv3 FETCH_SIZE and WRITE_SIZE passes, each scaled by what the same
+# counter reads for a 1 GiB device copy (fetch x2.000, write x1.000):
+# 148.4 MB read + 134.2 MB written (profiles/prefill_flash_kernel_cfg3_hbm_traffic.md).
+# Re-measure when the kernel changes.
+PREFILL_FLASH_TRAFFIC = 282.6e6
+
 
 def parse():
     ap = argparse.ArgumentParser()
@@ -169,11 +176,13 @@ def prefill_workload(args, cpu):
     step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "prefill_flash_kernel")
     res = {
         "workload": "configs[2] qwen3-8b causal GQA prefill S=8192 32q/8kv D=128 bf16, QK-norm+RoPE",
+        # bf16 in; the flash MFMAs take fp16 operands (3 more mantissa bits) and accumulate in fp32
+        "dtype": "fp16",
         "value": flops / (step_ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": step_ms,
         "roofline": {"kernel": "prefill_flash_kernel", "bound": "mfma",
                      "achieved": flops / (k_ms * 1e-3) / 1e12, "peak": PEAK_MFMA_F16,
                      "unit": "TFLOP/s", "frac": flops / (k_ms * 1e-3) / 1e12 / PEAK_MFMA_F16,
-                     "traffic": None, "kernel_ms": k_ms, "flops_per_launch": flops},
+                     "traffic": PREFILL_FLASH_TRAFFIC, "kernel_ms": k_ms, "flops_per_launch": flops},
     }
     if cpu is not None:
         O, ref, kind, threads = cpu
@@ -231,6 +240,7 @@ def decode_workload(args, cpu):
     step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "decode_attention_kernel")
     res = {
         "workload": "configs[3] qwen3-30b-a3b batched ragged GQA decode B=32 L~U[1k,32k] 32q/4kv D=128 bf16 KV",
+        "dtype": "bf16",
         "value": nbytes / (step_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": step_ms,
         "kv_bytes": nbytes,
         "roofline": {"kernel": "decode_attention_kernel", "bound": "hbm",
@@ -289,6 +299,7 @@ def delta_workload(args, cpu):
     flops = S * HV * (7.0 * KD * VD + 4.0 * VD)
     res = {
         "workload": "configs[4] qwen3-next gated delta rule S=16384 16qk/32v heads D=128 chunk 64 bf16 in, fp32 state",
+        "dtype": "f32",
         "value": nbytes / (step_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": step_ms,
         "recurrence_tflops": flops / (step_ms * 1e-3) / 1e12,
         "roofline": {"kernel": "delta_scan_kernel", "bound": "hbm",
@@ -297,21 +308,26 @@ def delta_workload(args, cpu):
                      "kernel_ms": k_ms, "all_kernels_ms": launched_ms, "bytes_per_step": nbytes},
     }
     if cpu is not None:
+        # the whole workload: the mixer's token loop around the reference's own
+        # deltaStep (oracle/_ref), single-threaded as gatedDeltaNetMixer runs
+        # it; the C restatement where the reference library is absent
         O, ref, kind, threads = cpu
-        n = 2048
-        qh = q[:n].float().cpu().numpy()
-        kh = k[:n].float().cpu().numpy()
-        vh = v[:n].float().cpu().numpy()
-        gh = g[:n].cpu().numpy()
-        bh = beta[:n].cpu().numpy()
+        qh = q.float().cpu().numpy()
+        kh = k.float().cpu().numpy()
+        vh = v.float().cpu().numpy()
+        gh = g.cpu().numpy()
+        bh = beta.cpu().numpy()
         t = time.perf_counter()
-        O.gated_delta_rule(qh, kh, vh, gh, bh, nthreads=1)
+        if ref is not None:
+            O.ref_gated_delta_rule(qh, kh, vh, gh, bh)
+            what = "the reference's kernels::deltaStep driven token by token (restated l2norm/q-scale glue)"
+        else:
+            O.gated_delta_rule(qh, kh, vh, gh, bh, nthreads=1)
+            what = "the C restatement of deltaStep"
         dt = time.perf_counter() - t
-        res["cpu_baseline"] = {"value": nbytes * n / S / dt / 1e9, "unit": "GB/s", "cores": 1,
-                               "kind": "port",
-                               "sample": f"gatedDeltaNetMixer recurrence over the first {n} of 16384 tokens, "
-                                         f"single-threaded as the reference runs it ({dt:.1f} s), "
-                                         f"C restatement of deltaStep"}
+        res["cpu_baseline"] = {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
+                               "sample": f"all 16384 tokens x 32 value heads, single-threaded as "
+                                         f"gatedDeltaNetMixer runs it ({dt:.1f} s): {what}"}
     return res
 
 
@@ -392,7 +408,7 @@ def main():
         "metric": "attn TFLOP/s (prefill) & KV GB/s (decode) as % roofline, 1 MI355X vs host CPU",
         "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "scaling": "weak", "vs_baseline": None, "dtype": head["dtype"],
         "data": "synthetic (torch seeded N(0,1) at each configuration's shape)",
         "config": {"workload": head["workload"], "device": aigpu.device_name()},
         "roofline": head["roofline"],

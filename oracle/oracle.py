@@ -108,8 +108,29 @@ def ref():
         R.ref_dot.restype = C.c_float
         R.ref_dot.argtypes = [_f32p, _f32p, C.c_uint64]
         R.ref_random.argtypes = [C.c_uint64, C.c_int, C.c_uint64, C.c_double, C.c_double, C.c_void_p]
+        R.ref_gated_delta_rule.argtypes = [_f32p] * 7 + [C.c_uint64] * 5 + [C.c_int]
         _ref = R
     return _ref
+
+
+def ref_gated_delta_rule(q, k, v, g, beta, state=None, normalize=True):
+    """The mixer's token loop around the reference's own deltaStep
+    (oracle/ref_shim.cpp); None when oracle/_ref is not built."""
+    R = ref()
+    if R is None:
+        return None
+    S, Hk, KD = q.shape
+    _, Hv, VD = v.shape
+    st = (np.zeros((Hv, KD, VD), np.float32) if state is None
+          else np.ascontiguousarray(state, np.float32).copy())
+    out = np.zeros((S, Hv, VD), np.float32)
+    R.ref_gated_delta_rule(np.ascontiguousarray(q, np.float32).reshape(-1),
+                           np.ascontiguousarray(k, np.float32).reshape(-1),
+                           np.ascontiguousarray(v, np.float32).reshape(-1),
+                           np.ascontiguousarray(g, np.float32).reshape(-1),
+                           np.ascontiguousarray(beta, np.float32).reshape(-1),
+                           st.reshape(-1), out.reshape(-1), S, Hk, Hv, KD, VD, int(bool(normalize)))
+    return out, st
 
 
 def threads(requested=0, cap=16):

@@ -9,13 +9,16 @@
 
     Wrapped, unchanged:
       ai::kernels::attention   include/ai/Kernels.hpp:132-168
-      ai::kernels::deltaStep   include/ai/Kernels.hpp:105-128
+      ai::kernels::deltaStep   include/ai/Kernels.hpp:105-128 (also driven by
+                               ref_gated_delta_rule, the mixer's token loop)
       ai::kernels::Pool        include/ai/ThreadPool.hpp:33-124
       math::random::Random     include/math/Random.hpp:15-89
 */
 #include <sched.h>
 
+#include <cmath>
 #include <cstdint>
+#include <cstring>
 #include <vector>
 
 #include "ai/Kernels.hpp"
@@ -51,6 +54,41 @@ void ref_delta_step(float* state, const float* key, const float* query, const fl
 }
 
 float ref_dot(const float* a, const float* b, uint64_t n) { return ai::kernels::dot(a, b, n); }
+
+/* gatedDeltaNetMixer's per-token loop (LocalModel.hpp:2802-2830) around the
+   reference's own deltaStep, single-threaded as the mixer runs it. The l2
+   normalisation with eps inside the square root (LocalModel.hpp:1380-1386)
+   and the 1/sqrt(KD) q scale (:2817-2818) are restated here: LocalModel.hpp
+   does not compile with this toolchain. g is the log decay, beta the gate. */
+void ref_gated_delta_rule(const float* q, const float* k, const float* v, const float* g,
+                          const float* beta, float* state, float* out, uint64_t count,
+                          uint64_t keyHeads, uint64_t valueHeads, uint64_t KD, uint64_t VD,
+                          int normalize) {
+    std::vector<float> qh(KD), kh(KD), prediction(VD), delta(VD);
+    const uint64_t group = valueHeads / keyHeads;
+    const float qScale = 1.0f / std::sqrt(float(KD));
+    auto l2 = [](float* x, uint64_t n) {
+        float sum = 0.0f;
+        for (uint64_t i = 0; i < n; ++i) sum += x[i] * x[i];
+        const float inv = 1.0f / std::sqrt(sum + 1e-6f);
+        for (uint64_t i = 0; i < n; ++i) x[i] *= inv;
+    };
+    for (uint64_t t = 0; t < count; ++t)
+        for (uint64_t h = 0; h < valueHeads; ++h) {
+            const uint64_t kHead = h / group;
+            std::memcpy(qh.data(), q + (t * keyHeads + kHead) * KD, sizeof(float) * KD);
+            std::memcpy(kh.data(), k + (t * keyHeads + kHead) * KD, sizeof(float) * KD);
+            if (normalize) {
+                l2(qh.data(), KD);
+                l2(kh.data(), KD);
+                for (uint64_t i = 0; i < KD; ++i) qh[i] *= qScale;
+            }
+            const float decay = std::exp(g[t * valueHeads + h]);
+            ai::kernels::deltaStep(state + h * KD * VD, kh.data(), qh.data(), v + (t * valueHeads + h) * VD,
+                                   &decay, false, beta[t * valueHeads + h], KD, VD,
+                                   out + (t * valueHeads + h) * VD, prediction.data(), delta.data());
+        }
+}
 
 /* Draws `n` values from Random(seed): kind 0 next() as raw bits, 1 u01,
    2 normal(0,1), 3 randInt(lo, hi), 4 randDouble(lo, hi). */

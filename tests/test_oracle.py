@@ -324,6 +324,18 @@ def _gdn_inputs(S, hk, hv, kd, vd, seed):
     return q, k, v, g, beta
 
 
+def test_gated_delta_rule_matches_reference_delta_step_loop():
+    """the restated mixer loop equals the reference's own deltaStep driven
+    token by token (oracle/_ref), bit for bit, over 300 tokens"""
+    if O.ref() is None:
+        pytest.skip("oracle/_ref not built (reference checkout absent)")
+    q, k, v, g, beta = _gdn_inputs(300, 2, 4, 64, 32, 13)
+    s0 = O.fill_normal((4, 64, 32), 13, "s0")
+    ro, rs = O.ref_gated_delta_rule(q, k, v, g, beta, state=s0)
+    po, ps = O.gated_delta_rule(q, k, v, g, beta, state=s0)
+    assert np.array_equal(ro, po) and np.array_equal(rs, ps)
+
+
 def test_gated_delta_rule_is_repeated_delta_step():
     S, hk, hv, kd, vd = 7, 2, 4, 16, 8
     q, k, v, g, beta = _gdn_inputs(S, hk, hv, kd, vd, 12)
