@@ -58,11 +58,14 @@ def build(verbose=False, jobs=4):
         if missing:
             raise RuntimeError(f"{obj}: kernel stubs not emitted: {missing}")
     lib = os.path.join(OUT, "libaigpu.so")
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", lib + ".tmp"] + objs)
+    # -Bsymbolic: the library's own calls bind to its own symbols even when the
+    # host executable defines the same device-management entry points (the
+    # reference's HIP backend does)
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-Bsymbolic", "-o", lib + ".tmp"] + objs)
     os.replace(lib + ".tmp", lib)
 
     stub = os.path.join(OUT, "libaigpu_stub.so")
-    _run(["g++", "-std=c++17", "-O2", "-shared", "-fPIC", "-fvisibility=hidden", "-o", stub,
+    _run(["g++", "-std=c++17", "-O2", "-shared", "-fPIC", "-fvisibility=hidden", "-Wl,-Bsymbolic", "-o", stub,
           os.path.join(CSRC, "stub.cpp")])
     return lib, stub
 

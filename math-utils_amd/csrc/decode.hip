@@ -1,17 +1,20 @@
 // decode.hip - batched single-token GQA decode for gfx950, HBM-bound.
 //
-// One persistent launch walks a flattened work list of (sequence b, kv head,
-// chunk of CH positions) items; each workgroup takes items blockIdx.x,
-// blockIdx.x + gridDim.x, ... so ragged lengths leave no empty workgroups.
+// Three launches:
+//   decode_prep_kernel       per (sequence b, kv head): QK-RMSNorm and RoPE at
+//                            position positions[b] for the G query heads and the
+//                            new k (attentionMixer, LocalModel.hpp:2608-2648),
+//                            the new k and v appended to the bf16 cache at
+//                            positions[b] (LocalModel.hpp:2650-2655), and q
+//                            written as the score MFMA's B operand;
+//   decode_attention_kernel  one persistent launch over a flattened work list of
+//                            (sequence, kv head, chunk of CH positions) items;
+//                            workgroup i takes items i, i + gridDim.x, ... so
+//                            ragged lengths leave no empty workgroups;
+//   decode_merge_kernel      combines the (m, l, acc) records of sequences that
+//                            span several chunks.
 // Per item, 4 waves split the chunk into slabs of 32 positions, software-
-// pipelined: a wave's next slab is requested before the current one computes,
-// and its first slab before the item's queries are prepared.
-//   - the G query heads of the kv head get QK-RMSNorm and RoPE at position
-//     positions[b] on load (attentionMixer, LocalModel.hpp:2608-2648);
-//   - the item whose chunk ends at the new token also normalises and rotates
-//     the new k, appends k and v to the bf16 cache at positions[b]
-//     (LocalModel.hpp:2650-2655) and folds the new token in from LDS, so no
-//     workgroup reads the slot being written;
+// pipelined: a wave's next slab is requested before the current one computes.
 //   - scores: v_mfma_f32_16x16x32_bf16 with K rows (16-byte loads straight
 //     from HBM, each K byte read once for all G heads) as A and q as B, q split
 //     into a bf16 high part (columns 0-7) and the bf16 residual (columns 8-15)
@@ -22,12 +25,12 @@
 //     through ds_read_b64_tr_b16 as the k-contiguous B operand;
 //   - online softmax inside a wave, a cross-wave merge in LDS; a sequence
 //     that fits one chunk writes its output directly, otherwise each chunk
-//     leaves a (m, l, acc) record.
-// decode_merge_kernel then combines the records of multi-chunk sequences -
-// the split-K algebra of the reference's Metal decoder
-// (src/gpu/Kernels.metal:318-345). A kernel boundary, not an in-kernel
-// device-scope fence, publishes the records: on gfx950 such a fence writes
-// back and invalidates the XCD's whole L2, which costs far more than a launch.
+//     leaves a (m, l, acc) record, combined by decode_merge_kernel with the
+//     split-K algebra of the reference's Metal decoder
+//     (src/gpu/Kernels.metal:318-345).
+// A kernel boundary, not an in-kernel device-scope fence, publishes the
+// records: on gfx950 such a fence writes back and invalidates the XCD's whole
+// L2, which costs far more than a launch.
 //
 // Calls that share the backend's scratch (the records) must not run
 // concurrently on different streams.

@@ -29,10 +29,12 @@
       or_rotary_frequencies    closed form 1/theta^(2j/rot); linear and llama3
                                scaling against llm-testing.cpp:141-145's
                                expected values
-      or_gated_delta_rule      chunk-free recurrence equals or_delta_step
-                               applied step by step; beta=0 and decay=1 special
-                               cases; one token equals one deltaStep; l2norm
-                               closed form
+      or_gated_delta_rule      bit-compared against the reference's deltaStep
+                               driven token by token (ref_gated_delta_rule in
+                               oracle/_ref); equals or_delta_step applied step
+                               by step; beta=0 and decay=1 special cases; one
+                               token equals one deltaStep; l2norm closed form
+      or_gdn_gates             closed form of softplus / sigmoid
 */
 #ifndef ORACLE_H
 #define ORACLE_H
