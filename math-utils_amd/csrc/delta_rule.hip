@@ -245,8 +245,13 @@ __global__ __launch_bounds__(256) void delta_solve_kernel(DeltaArgs a) {
     rec[2 * CH * CH + tid] = sc[tid];
 }
 
+/*
+    The scan on v_mfma_f32_16x16x4f32 for fp32 inputs, whose parity bound
+    (1e-5) a split into 16-bit parts does not meet: the fp16 residual of values
+    below 2^-3 is subnormal, and bf16 parts carry 8 bits each.
+*/
 template <int KD, bool F32>
-__global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
+__global__ __launch_bounds__(256) void delta_scan_f32_kernel(DeltaArgs a) {
     constexpr int KS = KD + 1;
     constexpr int EPL = F32 ? 4 : 8;                 // elements per 16-byte load
     constexpr int KQL = CH * KD / (256 * EPL);       // 16-byte loads per thread for k (and q)
@@ -434,6 +439,267 @@ __global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
     }
 }
 
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __fp16 fp16x4v __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+/* fp32 -> bf16 high part and bf16 residual (round to nearest even): hi + lo
+   carries ~16 significant bits over fp32's whole exponent range */
+__device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
+    hi = __bf16(x);
+    lo = __bf16(x - float(hi));
+}
+
+/* ds_read_b64_tr_b16 pair: lane i of each 16-lane group receives column
+   `base + i` of rows P0..P0+7 when lane L addresses row P0 + L/4 (and +4),
+   columns base + 4 (L % 4) .. +3 */
+__device__ __forceinline__ bf16x8 tr_pair(const __bf16* a0, const __bf16* a1) {
+    typedef __attribute__((address_space(3))) fp16x4v lds_x4;
+    const fp16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_x4*)(a0));
+    const fp16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_x4*)(a1));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+    return __builtin_bit_cast(bf16x8, u32x4{l2[0], l2[1], h2[0], h2[1]});
+}
+
+__device__ __forceinline__ floatx4 mfma_bf(const bf16x8& a, const bf16x8& b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+/*
+    The scan for bf16 inputs: value head h, value columns col0 .. col0+15,
+    chunk by chunk, on v_mfma_f32_16x16x32_bf16. Raw q/k rows are exact in
+    bf16; every fp32 operand (S, T, QKm, R, U, W) is split into a bf16 high
+    part and the bf16 residual, and each product takes hi*hi + hi*lo + lo*hi
+    (or hi*hi + hi*lo against an exact raw row) with fp32 accumulation, ~2^-16
+    relative. Per chunk:
+      R  = diag(beta) (V - diag(gamma kinv) K_raw S)       rows i, cols c
+      U  = T R
+      O  = diag(gamma qinv) Q_raw S + QKm U
+      S' = e^{gc_last} S + K_raw^T W,  W = diag(kinv e^{gc_last - gc}) U
+    S stays in registers as each wave's fp32 accumulators (wave w owns key
+    rows 16 (w + 4t) + 0..15) across all chunks; LDS holds its transposed
+    split as the next chunk's B operand. Matrices sit in LDS row-major with 16
+    bytes of padding per row (A-operand reads of 16 rows x 16 bytes hit
+    distinct banks); B operands are stored transposed, so every operand read
+    is one 16-byte LDS load; K^T comes from row-major K through transposed
+    reads.
+*/
+template <int KD>
+__global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
+    constexpr int KQL = CH * KD / (256 * 8);         // 16-byte loads per thread for k (and q)
+    constexpr int KH = KD + 8;                       // elements per K/Q row in LDS
+    constexpr int CHH = CH + 8;                      // elements per row of CH-wide matrices
+    constexpr int MT = KD / 64;                      // 16-row state tiles per wave
+    __shared__ __attribute__((aligned(16))) __bf16 Kb[CH * KH];       // raw k rows
+    __shared__ __attribute__((aligned(16))) __bf16 Qb[CH * KH];       // raw q rows
+    __shared__ __attribute__((aligned(16))) __bf16 Tb[2][CH * CHH];   // T, hi / lo
+    __shared__ __attribute__((aligned(16))) __bf16 Mb[2][CH * CHH];   // QKm, hi / lo
+    __shared__ __attribute__((aligned(16))) __bf16 St[2][NB * KH];    // S^T [col][key]
+    __shared__ __attribute__((aligned(16))) __bf16 Rt[2][NB * CHH];   // R^T [col][token]
+    __shared__ __attribute__((aligned(16))) __bf16 Ut[2][NB * CHH];   // U^T
+    __shared__ __attribute__((aligned(16))) __bf16 Wt[2][NB * CHH];   // W^T
+    __shared__ float vs[CH * NS];
+    __shared__ float sc[SC];                         // gc, beta, kinv, qinv
+    __shared__ float kdk[CH];                        // kinv_i exp(gc_last - gc_i)
+
+    const DeltaRuleParams& p = a.p;
+    // keep a head's column blocks on one XCD: they read the same records
+    uint32_t bid = blockIdx.x;
+    const uint32_t nb = gridDim.x, nCol = uint32_t(p.valueDim / NB);
+    if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
+    const uint32_t h = bid / nCol, cb = bid % nCol;
+    const uint32_t kh = uint32_t(h / (p.valueHeads / p.keyHeads));
+    const uint32_t col0 = cb * NB;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c16 = lane & 15;
+    const size_t VD = p.valueDim, Hv = p.valueHeads;
+    const bool vec = a.vec != 0;
+
+    // C-layout tile (rows row0 + 4g + r, column c16) -> transposed split [col][row]
+    auto put_t = [&](__bf16* dhi, __bf16* dlo, int stride, int row0, const floatx4& x) {
+        bf16x4 hv, lv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            __bf16 hi, lo;
+            split_bf16(x[r], hi, lo);
+            hv[r] = hi;
+            lv[r] = lo;
+        }
+        *reinterpret_cast<bf16x4*>(&dhi[c16 * stride + row0 + 4 * g]) = hv;
+        *reinterpret_cast<bf16x4*>(&dlo[c16 * stride + row0 + 4 * g]) = lv;
+    };
+
+    // S: wave w's tiles mt = w + 4t hold key rows 16 mt + 4g + r, column c16
+    float* state = p.state + size_t(h) * KD * VD;
+    floatx4 sacc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            sacc[t][r] = state[size_t(16 * (w + 4 * t) + 4 * g + r) * VD + col0 + c16];
+    auto publish_state = [&]() {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) put_t(St[0], St[1], KH, 16 * (w + 4 * t), sacc[t]);
+    };
+    publish_state();
+
+    // registers holding the next chunk's inputs while the current one computes
+    u32x4 kst[KQL], qst[KQL];
+    floatx4 tst[4], mst[4];
+    u32x2 vst;
+    float sst;
+    auto stage = [&](uint32_t chunk) {
+        const uint64_t t0 = uint64_t(chunk) * CH;
+        const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
+#pragma unroll
+        for (int i = 0; i < KQL; ++i) {
+            const int e = (tid + 256 * i) * 8, r = e / KD, col = e % KD;
+            const size_t src = ((t0 + r) * p.keyHeads + kh) * KD + col;
+            kst[i] = uint32_t(r) < n ? load_raw16<false>(p.k, src, vec) : u32x4{0, 0, 0, 0};
+            qst[i] = uint32_t(r) < n ? load_raw16<false>(p.q, src, vec) : u32x4{0, 0, 0, 0};
+        }
+        const float* rec = a.work + (size_t(h) * a.nChunks + chunk) * WORK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            tst[i] = *reinterpret_cast<const floatx4*>(rec + 4 * (tid + 256 * i));
+            mst[i] = *reinterpret_cast<const floatx4*>(rec + CH * CH + 4 * (tid + 256 * i));
+        }
+        sst = rec[2 * CH * CH + tid];
+        const int r = tid >> 2, c4 = 4 * (tid & 3);
+        vst = u32x2{0, 0};
+        if (uint32_t(r) < n) {
+            const uint16_t* vb = static_cast<const uint16_t*>(p.v) + ((t0 + r) * Hv + h) * VD + col0 + c4;
+            vst = vec ? *reinterpret_cast<const u32x2*>(vb)
+                      : u32x2{uint32_t(vb[0]) | (uint32_t(vb[1]) << 16), uint32_t(vb[2]) | (uint32_t(vb[3]) << 16)};
+        }
+    };
+    auto commit = [&]() {
+#pragma unroll
+        for (int i = 0; i < KQL; ++i) {   // raw bf16 rows go in as they are
+            const int e = (tid + 256 * i) * 8, r = e / KD, col = e % KD;
+            *reinterpret_cast<u32x4*>(&Kb[r * KH + col]) = kst[i];
+            *reinterpret_cast<u32x4*>(&Qb[r * KH + col]) = qst[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = 4 * (tid + 256 * i), r = idx / CH, col = idx % CH;
+            bf16x4 th, tl, mh, ml;
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                __bf16 hi, lo;
+                split_bf16(tst[i][x], hi, lo);
+                th[x] = hi;
+                tl[x] = lo;
+                split_bf16(mst[i][x], hi, lo);
+                mh[x] = hi;
+                ml[x] = lo;
+            }
+            *reinterpret_cast<bf16x4*>(&Tb[0][r * CHH + col]) = th;
+            *reinterpret_cast<bf16x4*>(&Tb[1][r * CHH + col]) = tl;
+            *reinterpret_cast<bf16x4*>(&Mb[0][r * CHH + col]) = mh;
+            *reinterpret_cast<bf16x4*>(&Mb[1][r * CHH + col]) = ml;
+        }
+        sc[tid] = sst;
+        const int r = tid >> 2, c4 = 4 * (tid & 3);
+        const u32x4 v4{vst[0], vst[1], 0, 0};
+#pragma unroll
+        for (int x = 0; x < 4; ++x) vs[r * NS + c4 + x] = raw_elem<false>(v4, x);
+    };
+    // acc += X[rows 16w .. +15][k] Y[k][cols], k in [0, K): X row-major (one
+    // exact part, or hi/lo when X1 is given), Y transposed split [col][k]
+    auto gemm = [&](floatx4 acc, const __bf16* X0, const __bf16* X1, int XS, const __bf16* Y0, const __bf16* Y1,
+                    int YS, int K) {
+#pragma unroll
+        for (int kb = 0; kb < K / 32; ++kb) {
+            const int xo = (16 * w + c16) * XS + 32 * kb + 8 * g, yo = c16 * YS + 32 * kb + 8 * g;
+            const bf16x8 xh = *reinterpret_cast<const bf16x8*>(X0 + xo);
+            const bf16x8 yh = *reinterpret_cast<const bf16x8*>(Y0 + yo);
+            acc = mfma_bf(xh, yh, acc);
+            acc = mfma_bf(xh, *reinterpret_cast<const bf16x8*>(Y1 + yo), acc);
+            if (X1) acc = mfma_bf(*reinterpret_cast<const bf16x8*>(X1 + xo), yh, acc);
+        }
+        return acc;
+    };
+
+    stage(0);
+    commit();
+    for (uint32_t chunk = 0; chunk < a.nChunks; ++chunk) {
+        const uint64_t t0 = uint64_t(chunk) * CH;
+        const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
+        __syncthreads();   // the chunk's inputs and S^T are in LDS
+        if (chunk + 1 < a.nChunks) stage(chunk + 1);
+        const float* gcs = sc;
+        const float* bs = sc + CH;
+        const float* kinv = sc + 2 * CH;
+        const float* qinv = sc + 3 * CH;
+        const float gLast = gcs[CH - 1];
+        if (tid < CH) kdk[tid] = kinv[tid] * expf(gLast - gcs[tid]);
+
+        // R = beta (V - gamma kinv (K_raw S))
+        floatx4 acc = gemm(floatx4{0.0f, 0.0f, 0.0f, 0.0f}, Kb, nullptr, KH, St[0], St[1], KH, KD);
+        {
+            floatx4 rv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * w + 4 * g + r;
+                rv[r] = bs[i] * (vs[i * NS + c16] - expf(gcs[i]) * (kinv[i] * acc[r]));
+            }
+            put_t(Rt[0], Rt[1], CHH, 16 * w, rv);
+        }
+        __syncthreads();
+
+        // U = T R, and W = diag(kdk) U for the state update
+        const floatx4 u = gemm(floatx4{0.0f, 0.0f, 0.0f, 0.0f}, Tb[0], Tb[1], CHH, Rt[0], Rt[1], CHH, CH);
+        put_t(Ut[0], Ut[1], CHH, 16 * w, u);
+        {
+            floatx4 wv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) wv[r] = kdk[16 * w + 4 * g + r] * u[r];
+            put_t(Wt[0], Wt[1], CHH, 16 * w, wv);
+        }
+        __syncthreads();
+
+        // O = gamma qinv (Q_raw S) + QKm U
+        acc = gemm(floatx4{0.0f, 0.0f, 0.0f, 0.0f}, Qb, nullptr, KH, St[0], St[1], KH, KD);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = 16 * w + 4 * g + r;
+            acc[r] *= expf(gcs[i]) * qinv[i];
+        }
+        acc = gemm(acc, Mb[0], Mb[1], CHH, Ut[0], Ut[1], CHH, CH);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t i = 16 * w + 4 * g + r;
+            if (i < n) p.out[((t0 + i) * Hv + h) * VD + col0 + c16] = acc[r];
+        }
+
+        // S' = e^{gc_last} S + K_raw^T W: A = K^T rows d (transposed reads of
+        // row-major K), B = W^T [col][token]
+        const float eLast = expf(gLast);
+        const int q16 = lane & 15;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int d0 = 16 * (w + 4 * t);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sacc[t][r] *= eLast;
+#pragma unroll
+            for (int ib = 0; ib < CH / 32; ++ib) {
+                const int row = 32 * ib + 8 * g + (q16 >> 2), col = d0 + 4 * (q16 & 3);
+                const bf16x8 kt = tr_pair(&Kb[row * KH + col], &Kb[(row + 4) * KH + col]);
+                const int yo = c16 * CHH + 32 * ib + 8 * g;
+                sacc[t] = mfma_bf(kt, *reinterpret_cast<const bf16x8*>(&Wt[0][yo]), sacc[t]);
+                sacc[t] = mfma_bf(kt, *reinterpret_cast<const bf16x8*>(&Wt[1][yo]), sacc[t]);
+            }
+        }
+        __syncthreads();   // every read of this chunk's LDS is done
+        publish_state();
+        if (chunk + 1 < a.nChunks) commit();
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            state[size_t(16 * (w + 4 * t) + 4 * g + r) * VD + col0 + c16] = sacc[t][r];
+}
+
 } // namespace
 
 bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream) {
@@ -465,7 +731,8 @@ bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream) {
             }))                                                                                               \
             return false;                                                                                     \
         return ctx.launch("delta_scan_kernel", stream, [&] {                                                  \
-            hipLaunchKernelGGL((delta_scan_kernel<KD, F>), dim3(scanBlocks), dim3(256), 0, stream, a);       \
+            if (F) hipLaunchKernelGGL((delta_scan_f32_kernel<KD, true>), dim3(scanBlocks), dim3(256), 0, stream, a); \
+            else hipLaunchKernelGGL((delta_scan_kernel<KD>), dim3(scanBlocks), dim3(256), 0, stream, a);     \
         });                                                                                                   \
     }
     AIGPU_DELTA(128, false)

@@ -55,6 +55,21 @@ def test_lengths_fp32(gpu, S):
     assert_f32_parity(rs, gs, f"state S={S}")
 
 
+# bf16 inputs take the bf16 hi/residual split kernel; fp32 inputs the fp32 one
+@pytest.mark.parametrize("S", [1, 63, 64, 65, 200])
+def test_lengths_bf16(gpu, S):
+    ro, go, rs, gs = run_gdn(gpu, S, 2, 4, 128, 128, 200 + S, dtype="bf16")
+    assert_bf16_parity(ro, go, f"out S={S}")
+    assert_bf16_parity(rs, gs, f"state S={S}")
+
+
+def test_bf16_raw_gates_initial_state_kd64(gpu):
+    s0 = O.fill_normal((4, 64, 48), 17, "s0") * np.float32(0.1)
+    ro, go, rs, gs = run_gdn(gpu, 300, 2, 4, 64, 48, 17, dtype="bf16", state0=s0, raw_gates=True)
+    assert_bf16_parity(ro, go, "out bf16 kd64")
+    assert_bf16_parity(rs, gs, "state bf16 kd64")
+
+
 def test_raw_gates_and_initial_state(gpu):
     s0 = O.fill_normal((4, 128, 64), 7, "s0") * np.float32(0.1)
     ro, go, rs, gs = run_gdn(gpu, 150, 2, 4, 128, 64, 7, state0=s0, raw_gates=True)
