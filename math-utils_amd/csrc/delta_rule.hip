@@ -34,6 +34,8 @@
 #include "device.hpp"
 #include "kernels.hpp"
 
+#include <type_traits>
+
 namespace aigpu {
 
 namespace {
@@ -108,25 +110,34 @@ __device__ __forceinline__ void chunk_gates(const DeltaRuleParams& p, uint64_t t
     beta = bt;
 }
 
+/*
+    Per (key head, chunk): the raw products K K^T and Q K^T of the chunk's rows
+    (exact bf16 products on v_mfma_f32_16x16x32_bf16 for bf16 inputs, fp32
+    MFMA for fp32 inputs) scaled by the inverse l2 norms, held in registers;
+    then for each of the G value heads that share the key head, its gates,
+    the decayed masks A and QKm and T = (I + A)^-1, written to that value
+    head's record.
+*/
 template <int KD, bool F32>
-__global__ __launch_bounds__(256) void delta_solve_kernel(DeltaArgs a) {
-    constexpr int KS = KD + 1;
+__global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs a) {
     constexpr int PE = KD / 4;              // elements of a row per thread
     constexpr int EPL = F32 ? 4 : 8;        // elements per 16-byte load
-    __shared__ float ks[CH * KS];
-    __shared__ float qs[CH * KS];
+    constexpr int KH = F32 ? KD + 1 : KD + 8;   // LDS row stride in elements
+    using Raw = std::conditional_t<F32, float, __bf16>;
+    __shared__ __attribute__((aligned(16))) Raw ks[CH * KH];   // raw k rows
+    __shared__ __attribute__((aligned(16))) Raw qs[CH * KH];   // raw q rows
     __shared__ float Am[CH * CS];
     __shared__ float Tm[CH * CS];
     __shared__ float Xs[4][16 * 17];
-    __shared__ float sc[SC];                // gc, beta, kinv, qinv
+    __shared__ float nrm[2 * CH];           // kinv, qinv
+    __shared__ float gsc[2 * CH];           // gc, beta of the current value head
 
     const DeltaRuleParams& p = a.p;
-    const uint32_t chunk = blockIdx.x, h = blockIdx.y;
-    const uint32_t kh = uint32_t(h / (p.valueHeads / p.keyHeads));
+    const uint32_t chunk = blockIdx.x, kh = blockIdx.y;
+    const uint32_t G = uint32_t(p.valueHeads / p.keyHeads);
     const uint64_t t0 = uint64_t(chunk) * CH;
     const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c16 = lane & 15;
-    float* rec = a.work + (size_t(h) * a.nChunks + chunk) * WORK;
 
     // rows: thread -> (row tid / 4, quarter tid % 4); l2 norms over the 4
     // threads of a row (LocalModel.hpp:2814-2818, l2normalise at :1380-1386)
@@ -158,91 +169,130 @@ __global__ __launch_bounds__(256) void delta_solve_kernel(DeltaArgs a) {
             qinv = (1.0f / sqrtf(qss + 1e-6f)) * (1.0f / sqrtf(float(KD)));
         }
 #pragma unroll
-        for (int i = 0; i < PE / EPL; ++i)
+        for (int i = 0; i < PE / EPL; ++i) {
+            const int col = qq * PE + i * EPL;
+            if (F32) {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                ks[r * KS + qq * PE + i * EPL + e] = raw_elem<F32>(kr[i], e) * kinv;
-                qs[r * KS + qq * PE + i * EPL + e] = raw_elem<F32>(qr[i], e) * qinv;
+                for (int e = 0; e < EPL; ++e) {
+                    reinterpret_cast<float*>(ks)[r * KH + col + e] = raw_elem<true>(kr[i], e);
+                    reinterpret_cast<float*>(qs)[r * KH + col + e] = raw_elem<true>(qr[i], e);
+                }
+            } else {
+                *reinterpret_cast<u32x4*>(&ks[r * KH + col]) = kr[i];
+                *reinterpret_cast<u32x4*>(&qs[r * KH + col]) = qr[i];
             }
+        }
         if (qq == 0) {
-            sc[2 * CH + r] = kinv;
-            sc[3 * CH + r] = qinv;
+            nrm[r] = kinv;
+            nrm[CH + r] = qinv;
         }
     }
-    if (w == 0) {
-        float gc, bt;
-        chunk_gates(p, t0, n, h, lane, gc, bt);
-        sc[lane] = gc;
-        sc[CH + lane] = bt;
-    }
-    // T starts as zero above the diagonal blocks
+    // T is zero above its diagonal blocks for every value head
     for (int idx = tid; idx < CH * CH; idx += 256) {
         const int i = idx / CH, j = idx % CH;
         if ((j >> 4) > (i >> 4)) Tm[i * CS + j] = 0.0f;
     }
     __syncthreads();
 
-    // KK^T and QK^T: wave w owns rows 16w..16w+15
-    float* qkm = rec + CH * CH;
+    // K K^T and Q K^T of the normalised rows: wave w owns rows 16w..16w+15
+    floatx4 kk[4], qk[4];
+#pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
-        floatx4 kk = {0.0f, 0.0f, 0.0f, 0.0f}, qk = {0.0f, 0.0f, 0.0f, 0.0f};
+        floatx4 x = {0.0f, 0.0f, 0.0f, 0.0f}, y = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (F32) {
+            const float* kf = reinterpret_cast<const float*>(ks);
+            const float* qf = reinterpret_cast<const float*>(qs);
 #pragma unroll 8
-        for (int s = 0; s < KD / 4; ++s) {
-            const float kj = ks[(16 * ct + c16) * KS + 4 * s + g];
-            kk = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[(16 * w + c16) * KS + 4 * s + g], kj, kk, 0, 0, 0);
-            qk = __builtin_amdgcn_mfma_f32_16x16x4f32(qs[(16 * w + c16) * KS + 4 * s + g], kj, qk, 0, 0, 0);
+            for (int s = 0; s < KD / 4; ++s) {
+                const float kj = kf[(16 * ct + c16) * KH + 4 * s + g];
+                x = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[(16 * w + c16) * KH + 4 * s + g], kj, x, 0, 0, 0);
+                y = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[(16 * w + c16) * KH + 4 * s + g], kj, y, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < KD / 32; ++kb) {
+                const bf16x8 kj = *reinterpret_cast<const bf16x8*>(&ks[(16 * ct + c16) * KH + 32 * kb + 8 * g]);
+                x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    *reinterpret_cast<const bf16x8*>(&ks[(16 * w + c16) * KH + 32 * kb + 8 * g]), kj, x, 0, 0, 0);
+                y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    *reinterpret_cast<const bf16x8*>(&qs[(16 * w + c16) * KH + 32 * kb + 8 * g]), kj, y, 0, 0, 0);
+            }
         }
+        const int j = 16 * ct + c16;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int i = 16 * w + 4 * g + r, j = 16 * ct + c16;
-            const float dec = j <= i ? expf(sc[i] - sc[j]) : 0.0f;
-            Am[i * CS + j] = j < i ? sc[CH + i] * dec * kk[r] : 0.0f;
-            qkm[i * CH + j] = dec * qk[r];
+            const int i = 16 * w + 4 * g + r;
+            kk[ct][r] = x[r] * (nrm[i] * nrm[j]);
+            qk[ct][r] = y[r] * (nrm[CH + i] * nrm[j]);
         }
     }
-    __syncthreads();
 
-    // T = (I + A)^-1. Diagonal blocks: wave w inverts block w by forward
-    // substitution, lane = column within the block.
-    {
-        const int b0 = 16 * w;
-        for (int i = 0; i < 16; ++i) {
-            if (lane < 16) {
-                float acc = 0.0f;
-                for (int mm = lane; mm < i; ++mm) acc = fmaf(Am[(b0 + i) * CS + b0 + mm], Tm[(b0 + mm) * CS + b0 + lane], acc);
-                Tm[(b0 + i) * CS + b0 + lane] = lane < i ? -acc : (lane == i ? 1.0f : 0.0f);
-            }
-            wave_sync();
+    for (uint32_t m = 0; m < G; ++m) {
+        const uint32_t h = kh * G + m;
+        float* rec = a.work + (size_t(h) * a.nChunks + chunk) * WORK;
+        if (w == 0) {
+            float gc, bt;
+            chunk_gates(p, t0, n, h, lane, gc, bt);
+            gsc[lane] = gc;
+            gsc[CH + lane] = bt;
         }
-    }
-    // Off-diagonal block (I, J): T_IJ = -T_II sum_{M=J}^{I-1} A_IM T_MJ; the
-    // blocks of one block row are independent, one wave each.
-    for (int I = 1; I < 4; ++I) {
         __syncthreads();
-        if (w < I) {
-            const int J = w;
-            floatx4 x = {0.0f, 0.0f, 0.0f, 0.0f};
-            for (int M = J; M < I; ++M)
+
+        float* qkm = rec + CH * CH;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * w + 4 * g + r, j = 16 * ct + c16;
+                const float dec = j <= i ? expf(gsc[i] - gsc[j]) : 0.0f;
+                Am[i * CS + j] = j < i ? gsc[CH + i] * dec * kk[ct][r] : 0.0f;
+                qkm[i * CH + j] = dec * qk[ct][r];
+            }
+        __syncthreads();
+
+        // T = (I + A)^-1. Diagonal blocks: wave w inverts block w by forward
+        // substitution, lane = column within the block.
+        {
+            const int b0 = 16 * w;
+            for (int i = 0; i < 16; ++i) {
+                if (lane < 16) {
+                    float acc = 0.0f;
+                    for (int mm = lane; mm < i; ++mm) acc = fmaf(Am[(b0 + i) * CS + b0 + mm], Tm[(b0 + mm) * CS + b0 + lane], acc);
+                    Tm[(b0 + i) * CS + b0 + lane] = lane < i ? -acc : (lane == i ? 1.0f : 0.0f);
+                }
+                wave_sync();
+            }
+        }
+        // Off-diagonal block (I, J): T_IJ = -T_II sum_{M=J}^{I-1} A_IM T_MJ; the
+        // blocks of one block row are independent, one wave each.
+        for (int I = 1; I < 4; ++I) {
+            __syncthreads();
+            if (w < I) {
+                const int J = w;
+                floatx4 x = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int M = J; M < I; ++M)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        x = __builtin_amdgcn_mfma_f32_16x16x4f32(Am[(16 * I + c16) * CS + 16 * M + 4 * s + g],
+                                                                 Tm[(16 * M + 4 * s + g) * CS + 16 * J + c16], x, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) Xs[w][(4 * g + r) * 17 + c16] = x[r];
+                wave_sync();
+                floatx4 y = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
-                    x = __builtin_amdgcn_mfma_f32_16x16x4f32(Am[(16 * I + c16) * CS + 16 * M + 4 * s + g],
-                                                             Tm[(16 * M + 4 * s + g) * CS + 16 * J + c16], x, 0, 0, 0);
+                    y = __builtin_amdgcn_mfma_f32_16x16x4f32(Tm[(16 * I + c16) * CS + 16 * I + 4 * s + g],
+                                                             Xs[w][(4 * s + g) * 17 + c16], y, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) Xs[w][(4 * g + r) * 17 + c16] = x[r];
-            wave_sync();
-            floatx4 y = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-                y = __builtin_amdgcn_mfma_f32_16x16x4f32(Tm[(16 * I + c16) * CS + 16 * I + 4 * s + g],
-                                                         Xs[w][(4 * s + g) * 17 + c16], y, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) Tm[(16 * I + 4 * g + r) * CS + 16 * J + c16] = -y[r];
+                for (int r = 0; r < 4; ++r) Tm[(16 * I + 4 * g + r) * CS + 16 * J + c16] = -y[r];
+            }
         }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    for (int idx = tid; idx < CH * CH; idx += 256) rec[idx] = Tm[(idx / CH) * CS + idx % CH];
-    rec[2 * CH * CH + tid] = sc[tid];
+        for (int idx = tid; idx < CH * CH; idx += 256) rec[idx] = Tm[(idx / CH) * CS + idx % CH];
+        rec[2 * CH * CH + tid] = tid < 2 * CH ? gsc[tid] : nrm[tid - 2 * CH];
+        __syncthreads();   // gsc, Am and Tm are rewritten for the next value head
+    }
 }
 
 /*
@@ -722,7 +772,7 @@ bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream) {
     auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     a.vec = aligned(p.q) && aligned(p.k) && aligned(p.v) ? 1u : 0u;
 
-    const dim3 sgrid(a.nChunks, unsigned(p.valueHeads));
+    const dim3 sgrid(a.nChunks, unsigned(p.keyHeads));
     const unsigned scanBlocks = unsigned(p.valueHeads * (p.valueDim / NB));
 #define AIGPU_DELTA(KD, F)                                                                                    \
     if (p.keyDim == KD && (p.inType == 0) == F) {                                                             \
