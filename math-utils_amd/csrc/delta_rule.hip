@@ -300,8 +300,9 @@ __global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs
     (1e-5) a split into 16-bit parts does not meet: the fp16 residual of values
     below 2^-3 is subnormal, and bf16 parts carry 8 bits each.
 */
-template <int KD, bool F32>
+template <int KD, bool VEC>
 __global__ __launch_bounds__(256) void delta_scan_f32_kernel(DeltaArgs a) {
+    constexpr bool F32 = true;
     constexpr int KS = KD + 1;
     constexpr int EPL = F32 ? 4 : 8;                 // elements per 16-byte load
     constexpr int KQL = CH * KD / (256 * EPL);       // 16-byte loads per thread for k (and q)
@@ -324,7 +325,7 @@ __global__ __launch_bounds__(256) void delta_scan_f32_kernel(DeltaArgs a) {
     const uint32_t col0 = cb * NB;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c16 = lane & 15;
     const size_t VD = p.valueDim, Hv = p.valueHeads;
-    const bool vec = a.vec != 0;
+    constexpr bool vec = VEC;
 
     float* state = p.state + size_t(h) * KD * VD;
     for (int idx = tid; idx < KD * NB; idx += 256) {
@@ -335,17 +336,24 @@ __global__ __launch_bounds__(256) void delta_scan_f32_kernel(DeltaArgs a) {
     // registers holding the next chunk's inputs while the current one computes
     u32x4 kst[KQL], qst[KQL];
     floatx4 tst[4], mst[4];
-    u32x4 vst;      // 4 value columns of one row (bf16: 8 bytes used)
+    u32x4 vst;      // 4 value columns of one row
     float sst;
+    uint32_t stagedN = 0;
+    // Loads are unconditional (rows past the chunk's end read its last row)
+    // and those rows are zeroed at the commit: a load guarded by a condition
+    // makes the compiler load into a temporary and copy, and the copy waits
+    // for the load, which would serialise the prefetch.
     auto stage = [&](uint32_t chunk) {
         const uint64_t t0 = uint64_t(chunk) * CH;
         const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
+        stagedN = n;
 #pragma unroll
         for (int i = 0; i < KQL; ++i) {
             const int e = (tid + 256 * i) * EPL, r = e / KD, col = e % KD;
-            const size_t src = ((t0 + r) * p.keyHeads + kh) * KD + col;
-            kst[i] = uint32_t(r) < n ? load_raw16<F32>(p.k, src, vec) : u32x4{0, 0, 0, 0};
-            qst[i] = uint32_t(r) < n ? load_raw16<F32>(p.q, src, vec) : u32x4{0, 0, 0, 0};
+            const uint32_t rr = uint32_t(r) < n ? uint32_t(r) : n - 1;
+            const size_t src = ((t0 + rr) * p.keyHeads + kh) * KD + col;
+            kst[i] = load_raw16<F32>(p.k, src, vec);
+            qst[i] = load_raw16<F32>(p.q, src, vec);
         }
         const float* rec = a.work + (size_t(h) * a.nChunks + chunk) * WORK;
 #pragma unroll
@@ -356,35 +364,21 @@ __global__ __launch_bounds__(256) void delta_scan_f32_kernel(DeltaArgs a) {
         sst = rec[2 * CH * CH + tid];
         {
             const int r = tid >> 2, c4 = 4 * (tid & 3);
-            vst = u32x4{0, 0, 0, 0};
-            if (uint32_t(r) < n) {
-                const size_t src = ((t0 + r) * Hv + h) * VD + col0 + c4;
-                if (F32) {
-                    vst = vec ? *reinterpret_cast<const u32x4*>(static_cast<const float*>(p.v) + src)
-                              : u32x4{__float_as_uint(static_cast<const float*>(p.v)[src]),
-                                      __float_as_uint(static_cast<const float*>(p.v)[src + 1]),
-                                      __float_as_uint(static_cast<const float*>(p.v)[src + 2]),
-                                      __float_as_uint(static_cast<const float*>(p.v)[src + 3])};
-                } else {
-                    const uint16_t* vb = static_cast<const uint16_t*>(p.v) + src;
-                    if (vec) {
-                        const u32x2 x = *reinterpret_cast<const u32x2*>(vb);
-                        vst = u32x4{x[0], x[1], 0, 0};
-                    } else {
-                        vst = u32x4{uint32_t(vb[0]) | (uint32_t(vb[1]) << 16), uint32_t(vb[2]) | (uint32_t(vb[3]) << 16), 0, 0};
-                    }
-                }
-            }
+            const uint32_t rr = uint32_t(r) < n ? uint32_t(r) : n - 1;
+            const float* vf = static_cast<const float*>(p.v) + ((t0 + rr) * Hv + h) * VD + col0 + c4;
+            if (vec) vst = *reinterpret_cast<const u32x4*>(vf);
+            else vst = u32x4{__float_as_uint(vf[0]), __float_as_uint(vf[1]), __float_as_uint(vf[2]), __float_as_uint(vf[3])};
         }
     };
     auto commit = [&]() {
 #pragma unroll
         for (int i = 0; i < KQL; ++i) {
             const int e = (tid + 256 * i) * EPL, r = e / KD, col = e % KD;
+            const bool ok = uint32_t(r) < stagedN;
 #pragma unroll
             for (int x = 0; x < EPL; ++x) {
-                ks[r * KS + col + x] = raw_elem<F32>(kst[i], x);
-                qs[r * KS + col + x] = raw_elem<F32>(qst[i], x);
+                ks[r * KS + col + x] = ok ? raw_elem<F32>(kst[i], x) : 0.0f;
+                qs[r * KS + col + x] = ok ? raw_elem<F32>(qst[i], x) : 0.0f;
             }
         }
 #pragma unroll
@@ -397,8 +391,9 @@ __global__ __launch_bounds__(256) void delta_scan_f32_kernel(DeltaArgs a) {
             }
         sc[tid] = sst;
         const int r = tid >> 2, c4 = 4 * (tid & 3);
+        const bool ok = uint32_t(r) < stagedN;
 #pragma unroll
-        for (int x = 0; x < 4; ++x) vs[r * NS + c4 + x] = F32 ? __uint_as_float(vst[x]) : raw_elem<false>(vst, x);
+        for (int x = 0; x < 4; ++x) vs[r * NS + c4 + x] = ok ? __uint_as_float(vst[x]) : 0.0f;
     };
 
     stage(0);
@@ -453,11 +448,7 @@ __global__ __launch_bounds__(256) void delta_scan_f32_kernel(DeltaArgs a) {
         for (int s = 0; s < CH / 4; ++s)
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Qm[(16 * w + c16) * CS + 4 * s + g],
                                                        Vn[(4 * s + g) * NS + c16], acc, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t i = 16 * w + 4 * g + r;
-            if (i < n) p.out[((t0 + i) * Hv + h) * VD + col0 + c16] = acc[r];
-        }
+        const floatx4 oacc = acc;   // stored after the commit below
 
         // S' = gamma_last S + sum_i k_raw_i (kinv_i exp(gc_last - gc_i)) U_i
         constexpr int MT = KD / 64;   // key-dim tiles per wave
@@ -481,6 +472,16 @@ __global__ __launch_bounds__(256) void delta_scan_f32_kernel(DeltaArgs a) {
             for (int r = 0; r < 4; ++r) Ss[(16 * mt + 4 * g + r) * NS + c16] = sn[t][r];
         }
         if (chunk + 1 < a.nChunks) commit();
+        // The output leaves after the commit: stores count in vmcnt with the
+        // staged loads, so the commit's wait for those loads would otherwise
+        // also wait out the latency of this chunk's stores.
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t i = 16 * w + 4 * g + r;
+            if (i < n) p.out[((t0 + i) * Hv + h) * VD + col0 + c16] = oacc[r];
+        }
     }
     __syncthreads();
     for (int idx = tid; idx < KD * NB; idx += 256) {
@@ -533,7 +534,7 @@ __device__ __forceinline__ floatx4 mfma_bf(const bf16x8& a, const bf16x8& b, con
     is one 16-byte LDS load; K^T comes from row-major K through transposed
     reads.
 */
-template <int KD>
+template <int KD, bool VEC>
 __global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
     constexpr int KQL = CH * KD / (256 * 8);         // 16-byte loads per thread for k (and q)
     constexpr int KH = KD + 8;                       // elements per K/Q row in LDS
@@ -561,7 +562,7 @@ __global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
     const uint32_t col0 = cb * NB;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c16 = lane & 15;
     const size_t VD = p.valueDim, Hv = p.valueHeads;
-    const bool vec = a.vec != 0;
+    constexpr bool vec = VEC;
 
     // C-layout tile (rows row0 + 4g + r, column c16) -> transposed split [col][row]
     auto put_t = [&](__bf16* dhi, __bf16* dlo, int stride, int row0, const floatx4& x) {
@@ -596,15 +597,22 @@ __global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
     floatx4 tst[4], mst[4];
     u32x2 vst;
     float sst;
+    uint32_t stagedN = 0;
+    // Loads are unconditional (rows past the chunk's end read its last row)
+    // and those rows are zeroed at the commit: a load guarded by a condition
+    // makes the compiler load into a temporary and copy, and the copy waits
+    // for the load, which would serialise the prefetch.
     auto stage = [&](uint32_t chunk) {
         const uint64_t t0 = uint64_t(chunk) * CH;
         const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
+        stagedN = n;
 #pragma unroll
         for (int i = 0; i < KQL; ++i) {
             const int e = (tid + 256 * i) * 8, r = e / KD, col = e % KD;
-            const size_t src = ((t0 + r) * p.keyHeads + kh) * KD + col;
-            kst[i] = uint32_t(r) < n ? load_raw16<false>(p.k, src, vec) : u32x4{0, 0, 0, 0};
-            qst[i] = uint32_t(r) < n ? load_raw16<false>(p.q, src, vec) : u32x4{0, 0, 0, 0};
+            const uint32_t rr = uint32_t(r) < n ? uint32_t(r) : n - 1;
+            const size_t src = ((t0 + rr) * p.keyHeads + kh) * KD + col;
+            kst[i] = load_raw16<false>(p.k, src, vec);
+            qst[i] = load_raw16<false>(p.q, src, vec);
         }
         const float* rec = a.work + (size_t(h) * a.nChunks + chunk) * WORK;
 #pragma unroll
@@ -614,19 +622,18 @@ __global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
         }
         sst = rec[2 * CH * CH + tid];
         const int r = tid >> 2, c4 = 4 * (tid & 3);
-        vst = u32x2{0, 0};
-        if (uint32_t(r) < n) {
-            const uint16_t* vb = static_cast<const uint16_t*>(p.v) + ((t0 + r) * Hv + h) * VD + col0 + c4;
-            vst = vec ? *reinterpret_cast<const u32x2*>(vb)
-                      : u32x2{uint32_t(vb[0]) | (uint32_t(vb[1]) << 16), uint32_t(vb[2]) | (uint32_t(vb[3]) << 16)};
-        }
+        const uint32_t rr = uint32_t(r) < n ? uint32_t(r) : n - 1;
+        const uint16_t* vb = static_cast<const uint16_t*>(p.v) + ((t0 + rr) * Hv + h) * VD + col0 + c4;
+        if (vec) vst = *reinterpret_cast<const u32x2*>(vb);
+        else vst = u32x2{uint32_t(vb[0]) | (uint32_t(vb[1]) << 16), uint32_t(vb[2]) | (uint32_t(vb[3]) << 16)};
     };
     auto commit = [&]() {
 #pragma unroll
         for (int i = 0; i < KQL; ++i) {   // raw bf16 rows go in as they are
             const int e = (tid + 256 * i) * 8, r = e / KD, col = e % KD;
-            *reinterpret_cast<u32x4*>(&Kb[r * KH + col]) = kst[i];
-            *reinterpret_cast<u32x4*>(&Qb[r * KH + col]) = qst[i];
+            const bool ok = uint32_t(r) < stagedN;
+            *reinterpret_cast<u32x4*>(&Kb[r * KH + col]) = ok ? kst[i] : u32x4{0, 0, 0, 0};
+            *reinterpret_cast<u32x4*>(&Qb[r * KH + col]) = ok ? qst[i] : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -649,7 +656,8 @@ __global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
         }
         sc[tid] = sst;
         const int r = tid >> 2, c4 = 4 * (tid & 3);
-        const u32x4 v4{vst[0], vst[1], 0, 0};
+        const bool ok = uint32_t(r) < stagedN;
+        const u32x4 v4{ok ? vst[0] : 0u, ok ? vst[1] : 0u, 0, 0};
 #pragma unroll
         for (int x = 0; x < 4; ++x) vs[r * NS + c4 + x] = raw_elem<false>(v4, x);
     };
@@ -715,11 +723,7 @@ __global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
             acc[r] *= expf(gcs[i]) * qinv[i];
         }
         acc = gemm(acc, Mb[0], Mb[1], CHH, Ut[0], Ut[1], CHH, CH);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t i = 16 * w + 4 * g + r;
-            if (i < n) p.out[((t0 + i) * Hv + h) * VD + col0 + c16] = acc[r];
-        }
+        const floatx4 oacc = acc;   // stored after the commit below
 
         // S' = e^{gc_last} S + K_raw^T W: A = K^T rows d (transposed reads of
         // row-major K), B = W^T [col][token]
@@ -742,6 +746,16 @@ __global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
         __syncthreads();   // every read of this chunk's LDS is done
         publish_state();
         if (chunk + 1 < a.nChunks) commit();
+        // The output leaves after the commit: stores count in vmcnt with the
+        // staged loads, so the commit's wait for those loads would otherwise
+        // also wait out the latency of this chunk's stores.
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t i = 16 * w + 4 * g + r;
+            if (i < n) p.out[((t0 + i) * Hv + h) * VD + col0 + c16] = oacc[r];
+        }
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t)
@@ -781,8 +795,11 @@ bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream) {
             }))                                                                                               \
             return false;                                                                                     \
         return ctx.launch("delta_scan_kernel", stream, [&] {                                                  \
-            if (F) hipLaunchKernelGGL((delta_scan_f32_kernel<KD, true>), dim3(scanBlocks), dim3(256), 0, stream, a); \
-            else hipLaunchKernelGGL((delta_scan_kernel<KD>), dim3(scanBlocks), dim3(256), 0, stream, a);     \
+            const dim3 grid{scanBlocks}, block{256};                                                         \
+            if (F && a.vec) hipLaunchKernelGGL((delta_scan_f32_kernel<KD, true>), grid, block, 0, stream, a);    \
+            else if (F) hipLaunchKernelGGL((delta_scan_f32_kernel<KD, false>), grid, block, 0, stream, a);        \
+            else if (a.vec) hipLaunchKernelGGL((delta_scan_kernel<KD, true>), grid, block, 0, stream, a);         \
+            else hipLaunchKernelGGL((delta_scan_kernel<KD, false>), grid, block, 0, stream, a);                    \
         });                                                                                                   \
     }
     AIGPU_DELTA(128, false)
