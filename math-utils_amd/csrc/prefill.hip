@@ -170,7 +170,8 @@ template <int D, bool F32>
 __global__ __launch_bounds__(256) void prefill_prep_vec_kernel(PrefillParams p, _Float16* __restrict__ qh,
                                                                _Float16* __restrict__ kh,
                                                                _Float16* __restrict__ vh, uint32_t T,
-                                                               float qScale) {
+                                                               float qScale, uint32_t firstRow,
+                                                               float* __restrict__ rope) {
     constexpr int LPR = D / 8, RPP = 256 / LPR, UNROLL = 4;
     __shared__ float cs[D / 2], sn[D / 2];
     const int tid = threadIdx.x, sub = tid % LPR, lane = tid % WAVE;
@@ -180,6 +181,10 @@ __global__ __launch_bounds__(256) void prefill_prep_vec_kernel(PrefillParams p, 
     if (tid < half) {
         const float fpos = float(pos);   // the reference's fp32 angle (LocalModel.hpp:2632)
         sincosf(fpos * p.freqs[tid], &sn[tid], &cs[tid]);
+        if (rope) {   // the token's cos/sin row for the flash kernel's own q rotation
+            rope[size_t(t) * 2 * half + tid] = cs[tid];
+            rope[size_t(t) * 2 * half + half + tid] = sn[tid];
+        }
     }
     __syncthreads();
     // rotate-half partner lane and the sign of its term, per element slot
@@ -196,7 +201,7 @@ __global__ __launch_bounds__(256) void prefill_prep_vec_kernel(PrefillParams p, 
         }
     }
 
-    for (uint32_t r0 = tid / LPR; r0 < rows; r0 += UNROLL * RPP) {
+    for (uint32_t r0 = firstRow + tid / LPR; r0 < rows; r0 += UNROLL * RPP) {
         float x[UNROLL][8];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
@@ -281,6 +286,13 @@ struct FlashArgs {
     const _Float16* vh;  // [kvHeads][T][D]
     float* out;          // [count][heads][D]
     uint32_t count, start, heads, kvHeads, window, T, nQT, xcdRemap;
+    // fused Q: the raw q rows are normed, rotated and scaled on load instead
+    // of read from qh
+    const void* qraw;    // [count][heads][qStride], inType
+    const float* qNorm;  // [D] gamma or null
+    const float* rope;   // [count][2][half] cos, sin of each token, or null
+    float eps, normOffset, qScale;
+    uint32_t qStride, inType, half, fuseQ;
 };
 
 typedef __fp16 fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
@@ -405,7 +417,86 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     const uint32_t wPosFirst = a.start + wq0, wPosLast = a.start + wLast;
 
     half8 qreg[DB];
-    {
+    if (a.fuseQ) {
+        // this lane's half of its query row: elements 16 db + 8g + j. QK-RMSNorm
+        // over the row (the other half is in lane ^ 32), RoPE pairs (e, e + half)
+        // within the lane (half % 16 == 0), then the log2(e)/sqrt(D) scale
+        // (attentionMixer, LocalModel.hpp:2608-2648)
+        float x[DB][8];
+        const size_t row = (size_t(rowValid ? tq : 0) * a.heads + head) * a.qStride;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            if (a.inType == 0) {
+                const floatx4* src = reinterpret_cast<const floatx4*>(static_cast<const float*>(a.qraw) + row + 16 * db + 8 * g);
+                const floatx4 lo = src[0], hi = src[1];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[db][j] = lo[j];
+                    x[db][4 + j] = hi[j];
+                }
+            } else {
+                const u32x4 wv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qraw) + row + 16 * db + 8 * g);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[db][2 * j] = __uint_as_float(wv[j] << 16);
+                    x[db][2 * j + 1] = __uint_as_float(wv[j] & 0xFFFF0000u);
+                }
+            }
+        }
+        if (a.qNorm) {   // rmsNormRow (LocalModel.hpp:1341-1348)
+            float ss = 0.0f;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) ss += x[db][j] * x[db][j];
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+            ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+            const float inv = 1.0f / sqrtf(ss / float(D) + a.eps);
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const floatx4* gm = reinterpret_cast<const floatx4*>(a.qNorm + 16 * db + 8 * g);
+                const floatx4 g0 = gm[0], g1 = gm[1];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[db][j] = x[db][j] * inv * (g0[j] + a.normOffset);
+                    x[db][4 + j] = x[db][4 + j] * inv * (g1[j] + a.normOffset);
+                }
+            }
+        }
+        if (a.rope) {   // rotate-half pairs (LocalModel.hpp:2636-2641)
+            const float* cs = a.rope + size_t(rowValid ? tq : 0) * 2 * a.half;
+            const int hb = int(a.half) / 16;   // partner block offset
+#pragma unroll
+            for (int db = 0; db < DB / 2; ++db) {
+                if (db < hb) {
+                    const floatx4* cp = reinterpret_cast<const floatx4*>(cs + 16 * db + 8 * g);
+                    const floatx4* sp = reinterpret_cast<const floatx4*>(cs + a.half + 16 * db + 8 * g);
+                    const floatx4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float cj = j < 4 ? c0[j] : c1[j - 4], sj = j < 4 ? s0[j] : s1[j - 4];
+                        const float lo = x[db][j];
+                        float hi = 0.0f;
+#pragma unroll
+                        for (int pb = 0; pb < DB; ++pb)
+                            if (pb == db + hb) hi = x[pb][j];
+                        const float nlo = lo * cj - hi * sj, nhi = hi * cj + lo * sj;
+                        x[db][j] = nlo;
+#pragma unroll
+                        for (int pb = 0; pb < DB; ++pb)
+                            if (pb == db + hb) x[pb][j] = nhi;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qreg[db][j] = rowValid ? _Float16(x[db][j] * a.qScale) : _Float16(0.0f);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        wait_vmcnt<0>();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    } else {
         const _Float16* qrow = a.qh + (size_t(head) * a.count + (rowValid ? tq : 0)) * D;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
@@ -674,10 +765,9 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     if (T * p.dim >= (1ull << 31) || p.heads * p.count >= (1ull << 31) || p.kvHeads > 65535)
         return ctx.fail("prefill: sequence too long");
 
-    _Float16* qh = static_cast<_Float16*>(ctx.grow(SLOT_PREFILL_Q, p.heads * p.count * p.dim * 2));
     _Float16* kh = static_cast<_Float16*>(ctx.grow(SLOT_PREFILL_K, p.kvHeads * T * p.dim * 2));
     _Float16* vh = static_cast<_Float16*>(ctx.grow(SLOT_PREFILL_V, p.kvHeads * T * p.dim * 2));
-    if (!qh || !kh || !vh) return false;
+    if (!kh || !vh) return false;
 
     // the register-row kernels need 16-byte aligned rows and rot % 16 == 0
     const size_t inAlign = p.inType == 0 ? 4 : 8;   // elements per 16 bytes
@@ -686,6 +776,20 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
                      aligned(p.valueCache) && (p.qStride % inAlign) == 0 &&
                      (!p.qNorm || aligned(p.qNorm)) && (!p.kNorm || aligned(p.kNorm)) &&
                      (!p.freqs || (p.rotaryDims % 16) == 0);
+    // the flash kernel normalises and rotates its own q rows when each lane's
+    // RoPE partners are in the lane itself (rot / 2 a multiple of 16); prep
+    // then handles only k and v, plus a cos/sin table for the q rotation
+    const bool fuseQ = vec && p.qStride < (1ull << 32) && (!p.freqs || (p.rotaryDims % 32) == 0);
+    _Float16* qh = nullptr;
+    float* rope = nullptr;
+    if (!fuseQ) {
+        qh = static_cast<_Float16*>(ctx.grow(SLOT_PREFILL_Q, p.heads * p.count * p.dim * 2));
+        if (!qh) return false;
+    } else if (p.freqs) {
+        rope = static_cast<float*>(ctx.grow(SLOT_PREFILL_Q, p.count * size_t(p.rotaryDims) * sizeof(float)));
+        if (!rope) return false;
+    }
+    const uint32_t firstRow = fuseQ ? uint32_t(p.heads) : 0u;
 
     if (p.start > 0) {
         const uint32_t per = uint32_t(p.start * p.dim);
@@ -714,16 +818,16 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
                                    qScale);
             else if (p.dim == 128 && p.inType == 1)
                 hipLaunchKernelGGL((prefill_prep_vec_kernel<128, false>), grid, block, 0, stream, p, qh, kh, vh,
-                                   t32, qScale);
+                                   t32, qScale, firstRow, rope);
             else if (p.dim == 128)
                 hipLaunchKernelGGL((prefill_prep_vec_kernel<128, true>), grid, block, 0, stream, p, qh, kh, vh,
-                                   t32, qScale);
+                                   t32, qScale, firstRow, rope);
             else if (p.inType == 1)
                 hipLaunchKernelGGL((prefill_prep_vec_kernel<64, false>), grid, block, 0, stream, p, qh, kh, vh,
-                                   t32, qScale);
+                                   t32, qScale, firstRow, rope);
             else
                 hipLaunchKernelGGL((prefill_prep_vec_kernel<64, true>), grid, block, 0, stream, p, qh, kh, vh,
-                                   t32, qScale);
+                                   t32, qScale, firstRow, rope);
         }))
         return false;
 
@@ -738,6 +842,16 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     a.kvHeads = uint32_t(p.kvHeads);
     a.window = uint32_t(p.window > 0xFFFFFFFFull ? 0 : p.window);
     a.T = uint32_t(T);
+    a.fuseQ = fuseQ ? 1u : 0u;
+    a.qraw = p.q;
+    a.qNorm = p.qNorm;
+    a.rope = rope;
+    a.eps = p.eps;
+    a.normOffset = p.normOffset;
+    a.qScale = qScale;
+    a.qStride = uint32_t(p.qStride);
+    a.inType = uint32_t(p.inType);
+    a.half = p.freqs ? uint32_t(p.rotaryDims / 2) : 0u;
     // AIGPU_PREFILL_WAVES / AIGPU_PREFILL_STAGES pick the tiling (tuning);
     // 4-wave workgroups run two per CU and take two stages
     static const int waves = [] {
