@@ -38,9 +38,9 @@ CPU_THREADS_CAP = 16        # the GPU box's CPU share for one GPU
 # HBM bytes per launch of prefill_flash_kernel<128, 8, 3> on configs[2]:
 # rocprofv3 FETCH_SIZE and WRITE_SIZE passes, each scaled by what the same
 # counter reads for a 1 GiB device copy (fetch x2.000, write x1.000):
-# 148.4 MB read + 134.2 MB written (profiles/prefill_flash_kernel_cfg3_hbm_traffic.md).
+# 183.8 MB read + 134.3 MB written (profiles/prefill_flash_kernel_cfg3_hbm_traffic.md).
 # Re-measure when the kernel changes.
-PREFILL_FLASH_TRAFFIC = 282.6e6
+PREFILL_FLASH_TRAFFIC = 318.0e6
 
 
 def parse():
