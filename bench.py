@@ -46,8 +46,10 @@ PREFILL_FLASH_TRAFFIC = 318.0e6
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    # the GPU's clock ramps over the first ~15 ms of sustained work: a short
+    # warm-up times the ramp rather than the kernels
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
