@@ -45,11 +45,18 @@ constexpr int CS = CH + 1;               // LDS row stride of CH x CH matrices
 constexpr int NB = 16;                   // value columns per scan workgroup
 constexpr int NS = NB + 1;
 constexpr int SC = 4 * CH;               // gc, beta, kinv, qinv per chunk
-constexpr int WORK = 2 * CH * CH + SC;   // floats per (head, chunk) record
+constexpr int WORK = 2 * CH * CH + SC;   // floats per (head, chunk) record, fp32 form
+// the split form, laid out as the DMA scan's LDS image: T hi, T lo, QKm hi,
+// QKm lo ([64][64] bf16 each, 16-byte block b of row r at b ^ (r % 8)), then
+// 512 floats: beta, gamma kinv, gamma qinv, kinv exp(gc_last - gc),
+// exp(gc_last) (64 copies), zeros
+constexpr int SPLIT_MAT = CH * CH / 2;          // floats per bf16 [64][64] matrix
+constexpr int SPLIT_SC = 512;
+constexpr int WORK_SPLIT = 4 * SPLIT_MAT + SPLIT_SC;
 
 struct DeltaArgs {
     DeltaRuleParams p;
-    float* work;       // [valueHeads][nChunks][WORK]: T, QKm, gc, beta, kinv, qinv
+    float* work;       // [valueHeads][nChunks][record]: fp32 or split form
     uint32_t nChunks;
     uint32_t vec;      // q, k, v 16-byte aligned: vector loads
 };
@@ -118,8 +125,9 @@ __device__ __forceinline__ void chunk_gates(const DeltaRuleParams& p, uint64_t t
     the decayed masks A and QKm and T = (I + A)^-1, written to that value
     head's record.
 */
-template <int KD, bool F32>
+template <int KD, bool F32, bool SPLIT>
 __global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs a) {
+    static_assert(!(F32 && SPLIT), "the split form serves bf16 inputs");
     constexpr int PE = KD / 4;              // elements of a row per thread
     constexpr int EPL = F32 ? 4 : 8;        // elements per 16-byte load
     constexpr int KH = F32 ? KD + 1 : KD + 8;   // LDS row stride in elements
@@ -229,7 +237,7 @@ __global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs
 
     for (uint32_t m = 0; m < G; ++m) {
         const uint32_t h = kh * G + m;
-        float* rec = a.work + (size_t(h) * a.nChunks + chunk) * WORK;
+        float* rec = a.work + (size_t(h) * a.nChunks + chunk) * (SPLIT ? WORK_SPLIT : WORK);
         if (w == 0) {
             float gc, bt;
             chunk_gates(p, t0, n, h, lane, gc, bt);
@@ -239,6 +247,7 @@ __global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs
         __syncthreads();
 
         float* qkm = rec + CH * CH;
+        floatx4 qkv[4];   // this value head's QKm, written once T is done (split form)
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
@@ -246,7 +255,8 @@ __global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs
                 const int i = 16 * w + 4 * g + r, j = 16 * ct + c16;
                 const float dec = j <= i ? expf(gsc[i] - gsc[j]) : 0.0f;
                 Am[i * CS + j] = j < i ? gsc[CH + i] * dec * kk[ct][r] : 0.0f;
-                qkm[i * CH + j] = dec * qk[ct][r];
+                if constexpr (SPLIT) qkv[ct][r] = dec * qk[ct][r];
+                else qkm[i * CH + j] = dec * qk[ct][r];
             }
         __syncthreads();
 
@@ -289,8 +299,54 @@ __global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs
         }
         __syncthreads();
 
-        for (int idx = tid; idx < CH * CH; idx += 256) rec[idx] = Tm[(idx / CH) * CS + idx % CH];
-        rec[2 * CH * CH + tid] = tid < 2 * CH ? gsc[tid] : nrm[tid - 2 * CH];
+        if constexpr (!SPLIT) {
+            for (int idx = tid; idx < CH * CH; idx += 256) rec[idx] = Tm[(idx / CH) * CS + idx % CH];
+            rec[2 * CH * CH + tid] = tid < 2 * CH ? gsc[tid] : nrm[tid - 2 * CH];
+        } else {
+            // QKm into Am (free now that T is done), then both matrices split
+            // into bf16 hi/lo rows, 16 bytes per store, in the scan's LDS image
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) Am[(16 * w + 4 * g + r) * CS + 16 * ct + c16] = qkv[ct][r];
+            __syncthreads();
+            uint16_t* out16 = reinterpret_cast<uint16_t*>(rec);
+#pragma unroll
+            for (int it = 0; it < 2; ++it) {
+                const int idx = tid + 256 * it, r = idx >> 3, b = idx & 7;
+                const int dst = r * CH + 8 * (b ^ (r & 7));
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    const float* src = (m == 0 ? Tm : Am) + r * CS + 8 * b;
+                    u32x4 hi, lo;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x0 = src[2 * e], x1 = src[2 * e + 1];
+                        const uint16_t h0 = float_to_bf16_bits(x0), h1 = float_to_bf16_bits(x1);
+                        const uint16_t l0 = float_to_bf16_bits(x0 - bf16_bits_to_float(h0));
+                        const uint16_t l1 = float_to_bf16_bits(x1 - bf16_bits_to_float(h1));
+                        hi[e] = uint32_t(h0) | (uint32_t(h1) << 16);
+                        lo[e] = uint32_t(l0) | (uint32_t(l1) << 16);
+                    }
+                    *reinterpret_cast<u32x4*>(out16 + (2 * m) * CH * CH + dst) = hi;
+                    *reinterpret_cast<u32x4*>(out16 + (2 * m + 1) * CH * CH + dst) = lo;
+                }
+            }
+            // per-row scalars of the scan: rows past the sequence's end have
+            // beta 0, so they add nothing to U, O or the state
+            float* sc = rec + 4 * SPLIT_MAT;
+            const float gLast = gsc[CH - 1];
+            for (int idx = tid; idx < SPLIT_SC; idx += 256) {
+                const int i = idx & (CH - 1), part = idx >> 6;
+                float x = 0.0f;
+                if (part == 0) x = gsc[CH + i];
+                else if (part == 1) x = expf(gsc[i]) * nrm[i];
+                else if (part == 2) x = expf(gsc[i]) * nrm[CH + i];
+                else if (part == 3) x = nrm[i] * expf(gLast - gsc[i]);
+                else if (part == 4) x = expf(gLast);
+                sc[idx] = x;
+            }
+        }
         __syncthreads();   // gsc, Am and Tm are rewritten for the next value head
     }
 }
@@ -764,6 +820,309 @@ __global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
             state[size_t(16 * (w + 4 * t) + 4 * g + r) * VD + col0 + c16] = sacc[t][r];
 }
 
+__device__ __forceinline__ void wait_vmcnt_all() { __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (15 << 8)); }
+
+/* s_waitcnt vmcnt(N) alone (N < 64) */
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+/* workgroup barrier that waits for this wave's LDS traffic only: the DMA in
+   flight for a later chunk keeps going */
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+/* One 1 KB DMA block: each lane's 16 bytes from `src` into LDS at
+   lds + 16 * lane. Written as asm so the compiler's wait analysis does not
+   track it (it cannot tell the double-buffered stages apart and would wait for
+   all DMA before reading any of them); the scan orders its DMA with explicit
+   vmcnt waits and barriers. One wait state separates the M0 write from the
+   DMA that reads it; nothing else in the scan uses M0. */
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   // M0 is reserved, and clobbered on purpose
+__device__ __forceinline__ void dma_block(const void* src, const void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)lds)));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+/*
+    The scan for 16-byte aligned bf16 inputs with every chunk input DMA'd into
+    LDS: nothing is staged in registers or converted on the scan's path.
+      - raw k and q rows come straight from the input tensors, 16-byte block b
+        of row r stored at b ^ (r % (KD / 8)), so A-operand reads of 16 rows
+        hit distinct banks;
+      - T and QKm come from the solve kernel already split into bf16 hi/lo in
+        this kernel's LDS layout, with the per-row scalars;
+      - the value block [64][16] bf16.
+    k, T, v and the scalars are double-buffered and fetched a chunk ahead; q
+    and QKm, read only by the output product at the end of a chunk, have one
+    buffer and are fetched at the chunk's start. Per chunk, with three
+    barriers:
+      R  = diag(beta) (V - diag(gamma kinv) K_raw S)
+      U  = T R,  W = diag(kinv e^{gc_last - gc}) U
+      S' = e^{gc_last} S + K_raw^T W
+      O  = diag(gamma qinv) Q_raw S + QKm U
+    S is each wave's fp32 accumulators (wave w owns key rows 16 (w + 4t) +
+    0..15); its transposed hi/lo split, the B operand of the R and O products,
+    is double-buffered by chunk parity so S' is published while O still reads
+    S. Every product takes hi*hi + hi*lo (+ lo*hi) with fp32 accumulation.
+*/
+template <int KD>
+__global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
+    constexpr int KBLK = KD / 8;                     // 16-byte blocks per k/q row
+    constexpr int RPI = 1024 / (2 * KD);             // k/q rows per 1 KB DMA block
+    constexpr int KI = CH / RPI / 4;                 // k (or q) DMA blocks per wave
+    constexpr int TI = 4;                            // T (or QKm) hi+lo blocks per wave: 16 KB / 4
+    constexpr int KTVS = KI + TI + 1;                // DMA blocks per wave for k, T, v + scalars
+    constexpr int KST = KD + 8;                      // S^T row stride (elements)
+    constexpr int CHH = CH + 8;                      // R^T, U^T, W^T row stride
+    constexpr int MT = KD / 64;                      // 16-row state tiles per wave
+    static_assert(KI * 4 * RPI == CH, "k rows split evenly over the waves");
+    __shared__ __attribute__((aligned(16))) __bf16 Kb[2][CH * KD];        // raw k rows, swizzled
+    __shared__ __attribute__((aligned(16))) __bf16 Tb[2][2 * CH * CH];    // T hi, lo (solve's image)
+    __shared__ __attribute__((aligned(16))) float Ax[2][1024];           // v [64][16] bf16, then scalars
+    __shared__ __attribute__((aligned(16))) __bf16 Qb[CH * KD];           // raw q rows, swizzled
+    __shared__ __attribute__((aligned(16))) __bf16 Mb[2 * CH * CH];       // QKm hi, lo
+    __shared__ __attribute__((aligned(16))) __bf16 St[2][2][NB * KST];    // [parity][hi/lo] S^T [col][key]
+    __shared__ __attribute__((aligned(16))) __bf16 Rt[2][NB * CHH];       // R^T hi, lo
+    __shared__ __attribute__((aligned(16))) __bf16 Ut[2][NB * CHH];       // U^T
+    __shared__ __attribute__((aligned(16))) __bf16 Wt[2][NB * CHH];       // W^T
+
+    const DeltaRuleParams& p = a.p;
+    // keep a head's column blocks on one XCD: they read the same records
+    uint32_t bid = blockIdx.x;
+    const uint32_t nb = gridDim.x, nCol = uint32_t(p.valueDim / NB);
+    if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
+    const uint32_t h = bid / nCol, cb = bid % nCol;
+    const uint32_t kh = uint32_t(h / (p.valueHeads / p.keyHeads));
+    const uint32_t col0 = cb * NB;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c16 = lane & 15;
+    const size_t VD = p.valueDim, Hv = p.valueHeads;
+    const uint32_t nChunks = a.nChunks;
+
+    auto chunk_rows = [&](uint32_t chunk) -> uint32_t {
+        const uint64_t t0 = uint64_t(chunk) * CH;
+        return uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
+    };
+    auto record = [&](uint32_t chunk) -> const float* {
+        return a.work + (size_t(h) * nChunks + chunk) * WORK_SPLIT;
+    };
+    // k or q rows of `chunk` into a swizzled [64][KD] buffer; rows past the
+    // end repeat the last row (their beta is 0)
+    auto dma_rows = [&](const void* base, uint32_t chunk, __bf16* dst) __attribute__((always_inline)) {
+        const uint64_t t0 = uint64_t(chunk) * CH;
+        const uint32_t n = chunk_rows(chunk);
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            const int blk = w * KI + j, row = RPI * blk + lane / KBLK, pb = lane % KBLK;
+            const int lb = pb ^ (row % KBLK);
+            const uint32_t rr = uint32_t(row) < n ? uint32_t(row) : n - 1;
+            const uint16_t* src = static_cast<const uint16_t*>(base) + ((t0 + rr) * p.keyHeads + kh) * KD + 8 * lb;
+            dma_block(src, dst + blk * 512);
+        }
+    };
+    auto dma_mat = [&](const float* rec, __bf16* dst) __attribute__((always_inline)) {   // hi + lo, 16 KB
+#pragma unroll
+        for (int j = 0; j < TI; ++j) {
+            const int blk = w * TI + j;
+            dma_block(reinterpret_cast<const uint8_t*>(rec) + blk * 1024 + 16 * lane, dst + blk * 512);
+        }
+    };
+    auto issue_ktvs = [&](uint32_t chunk, int buf) __attribute__((always_inline)) {
+        dma_rows(p.k, chunk, Kb[buf]);
+        const float* rec = record(chunk);
+        dma_mat(rec, Tb[buf]);
+        if (w < 2) {   // value block: 32 rows of 32 bytes per DMA block
+            const uint64_t t0 = uint64_t(chunk) * CH;
+            const uint32_t n = chunk_rows(chunk);
+            const int row = 32 * w + lane / 2;
+            const uint32_t rr = uint32_t(row) < n ? uint32_t(row) : n - 1;
+            const uint16_t* src = static_cast<const uint16_t*>(p.v) + ((t0 + rr) * Hv + h) * VD + col0 + 8 * (lane & 1);
+            dma_block(src, reinterpret_cast<uint8_t*>(Ax[buf]) + 1024 * w);
+        } else {       // scalars
+            dma_block(reinterpret_cast<const uint8_t*>(rec + 4 * SPLIT_MAT) + 1024 * (w - 2) + 16 * lane,
+                      reinterpret_cast<uint8_t*>(Ax[buf]) + 2048 + 1024 * (w - 2));
+        }
+    };
+    auto issue_qm = [&](uint32_t chunk) __attribute__((always_inline)) {
+        dma_rows(p.q, chunk, Qb);
+        dma_mat(record(chunk) + 2 * SPLIT_MAT, Mb);
+    };
+
+    // C-layout tile (rows row0 + 4g + r, column c16) -> transposed split [col][row]
+    auto put_t = [&](__bf16* dhi, __bf16* dlo, int stride, int row0, const floatx4& x) __attribute__((always_inline)) {
+        bf16x4 hv, lv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            __bf16 hi, lo;
+            split_bf16(x[r], hi, lo);
+            hv[r] = hi;
+            lv[r] = lo;
+        }
+        *reinterpret_cast<bf16x4*>(&dhi[c16 * stride + row0 + 4 * g]) = hv;
+        *reinterpret_cast<bf16x4*>(&dlo[c16 * stride + row0 + 4 * g]) = lv;
+    };
+    // A operand from a swizzled k/q buffer: rows 16w + c16, k-block kb
+    auto rows_a = [&](const __bf16* X, int kb) __attribute__((always_inline)) -> bf16x8 {
+        const int r = 16 * w + c16, lb = 4 * kb + g;
+        return *reinterpret_cast<const bf16x8*>(X + r * KD + 8 * (lb ^ (r % KBLK)));
+    };
+    // A operand from a [64][64] split matrix in the solve's image
+    auto mat_a = [&](const __bf16* X, int kb) __attribute__((always_inline)) -> bf16x8 {
+        const int r = 16 * w + c16, lb = 4 * kb + g;
+        return *reinterpret_cast<const bf16x8*>(X + r * CH + 8 * (lb ^ (r & 7)));
+    };
+
+    // S: wave w's tiles mt = w + 4t hold key rows 16 mt + 4g + r, column c16
+    float* state = p.state + size_t(h) * KD * VD;
+    floatx4 sacc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            sacc[t][r] = state[size_t(16 * (w + 4 * t) + 4 * g + r) * VD + col0 + c16];
+    auto publish_state = [&](int par) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) put_t(St[par][0], St[par][1], KST, 16 * (w + 4 * t), sacc[t]);
+    };
+    publish_state(0);
+    issue_ktvs(0, 0);
+
+    floatx4 oacc = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto store_out = [&](uint32_t chunk) __attribute__((always_inline)) {
+        const uint64_t t0 = uint64_t(chunk) * CH;
+        const uint32_t n = chunk_rows(chunk);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t i = 16 * w + 4 * g + r;
+            if (i < n) p.out[((t0 + i) * Hv + h) * VD + col0 + c16] = oacc[r];
+        }
+    };
+
+    for (uint32_t chunk = 0; chunk < nChunks; ++chunk) {
+        const int par = chunk & 1;
+        // this chunk's k, T, v and scalars have landed (and every earlier
+        // store has left); every read of the other buffers is done
+        wait_vmcnt_all();
+        __syncthreads();
+        issue_qm(chunk);
+        issue_ktvs(chunk + 1 < nChunks ? chunk + 1 : chunk, par ^ 1);   // the last chunk reloads itself
+        if (chunk > 0) store_out(chunk - 1);
+
+        const __bf16* K = Kb[par];
+        const __bf16* T = Tb[par];
+        const __bf16* vb = reinterpret_cast<const __bf16*>(Ax[par]);
+        const float* sc = Ax[par] + 512;
+        const float* beta = sc;
+        const float* gkinv = sc + CH;
+        const float* gqinv = sc + 2 * CH;
+        const float* kdk = sc + 3 * CH;
+        const float eLast = sc[4 * CH];
+        const __bf16* S0 = St[par][0];
+        const __bf16* S1 = St[par][1];
+
+        // R = beta (V - gamma kinv (K_raw S))
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < KD / 32; ++kb) {
+            const bf16x8 x = rows_a(K, kb);
+            const int yo = c16 * KST + 32 * kb + 8 * g;
+            acc = mfma_bf(x, *reinterpret_cast<const bf16x8*>(S0 + yo), acc);
+            acc = mfma_bf(x, *reinterpret_cast<const bf16x8*>(S1 + yo), acc);
+        }
+        {
+            floatx4 rv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * w + 4 * g + r;
+                rv[r] = beta[i] * (float(vb[i * NB + c16]) - gkinv[i] * acc[r]);
+            }
+            put_t(Rt[0], Rt[1], CHH, 16 * w, rv);
+        }
+        lds_barrier();
+
+        // U = T R, W = diag(kdk) U
+        floatx4 u = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < CH / 32; ++kb) {
+            const bf16x8 th = mat_a(T, kb), tl = mat_a(T + CH * CH, kb);
+            const int yo = c16 * CHH + 32 * kb + 8 * g;
+            const bf16x8 rh = *reinterpret_cast<const bf16x8*>(&Rt[0][yo]);
+            u = mfma_bf(th, rh, u);
+            u = mfma_bf(th, *reinterpret_cast<const bf16x8*>(&Rt[1][yo]), u);
+            u = mfma_bf(tl, rh, u);
+        }
+        put_t(Ut[0], Ut[1], CHH, 16 * w, u);
+        {
+            floatx4 wv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) wv[r] = kdk[16 * w + 4 * g + r] * u[r];
+            put_t(Wt[0], Wt[1], CHH, 16 * w, wv);
+        }
+        wait_vmcnt<KTVS>();   // this wave's q and QKm blocks have landed
+        lds_barrier();
+
+        // S' = e^{gc_last} S + K_raw^T W: A = K^T rows d through transposed
+        // reads of the swizzled rows, B = W^T [col][token]
+        const int q16 = lane & 15;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int d0 = 16 * (w + 4 * t);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sacc[t][r] *= eLast;
+#pragma unroll
+            for (int ib = 0; ib < CH / 32; ++ib) {
+                const int row = 32 * ib + 8 * g + (q16 >> 2), col = d0 + 4 * (q16 & 3);
+                const int cb8 = col >> 3, co = col & 7;
+                const bf16x8 kt = tr_pair(K + row * KD + 8 * (cb8 ^ (row % KBLK)) + co,
+                                          K + (row + 4) * KD + 8 * (cb8 ^ ((row + 4) % KBLK)) + co);
+                const int yo = c16 * CHH + 32 * ib + 8 * g;
+                sacc[t] = mfma_bf(kt, *reinterpret_cast<const bf16x8*>(&Wt[0][yo]), sacc[t]);
+                sacc[t] = mfma_bf(kt, *reinterpret_cast<const bf16x8*>(&Wt[1][yo]), sacc[t]);
+            }
+        }
+        publish_state(par ^ 1);
+
+        // O = gamma qinv (Q_raw S) + QKm U
+        acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < KD / 32; ++kb) {
+            const bf16x8 x = rows_a(Qb, kb);
+            const int yo = c16 * KST + 32 * kb + 8 * g;
+            acc = mfma_bf(x, *reinterpret_cast<const bf16x8*>(S0 + yo), acc);
+            acc = mfma_bf(x, *reinterpret_cast<const bf16x8*>(S1 + yo), acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] *= gqinv[16 * w + 4 * g + r];
+#pragma unroll
+        for (int kb = 0; kb < CH / 32; ++kb) {
+            const bf16x8 mh = mat_a(Mb, kb), ml = mat_a(Mb + CH * CH, kb);
+            const int yo = c16 * CHH + 32 * kb + 8 * g;
+            const bf16x8 uh = *reinterpret_cast<const bf16x8*>(&Ut[0][yo]);
+            acc = mfma_bf(mh, uh, acc);
+            acc = mfma_bf(mh, *reinterpret_cast<const bf16x8*>(&Ut[1][yo]), acc);
+            acc = mfma_bf(ml, uh, acc);
+        }
+        oacc = acc;
+    }
+    store_out(nChunks - 1);
+    wait_vmcnt_all();   // the last chunk's reload must land before the LDS is released
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            state[size_t(16 * (w + 4 * t) + 4 * g + r) * VD + col0 + c16] = sacc[t][r];
+}
+
 } // namespace
 
 bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream) {
@@ -781,31 +1140,42 @@ bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream) {
     a.p = p;
     a.nChunks = uint32_t((p.count + CH - 1) / CH);
     if (a.nChunks > 65535u * 1024u) return ctx.fail("delta rule: sequence too long");
-    a.work = static_cast<float*>(ctx.grow(SLOT_DELTA_WORK, size_t(p.valueHeads) * a.nChunks * WORK * sizeof(float)));
-    if (!a.work) return false;
     auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     a.vec = aligned(p.q) && aligned(p.k) && aligned(p.v) ? 1u : 0u;
+    // bf16 inputs on 16-byte boundaries take the DMA scan, whose records are
+    // the split form; fp32 and unaligned bf16 inputs take the register-staged
+    // scans over fp32 records
+    const bool dma = p.inType == 1 && a.vec;
+    const size_t rec = dma ? WORK_SPLIT : WORK;
+    a.work = static_cast<float*>(ctx.grow(SLOT_DELTA_WORK, size_t(p.valueHeads) * a.nChunks * rec * sizeof(float)));
+    if (!a.work) return false;
 
     const dim3 sgrid(a.nChunks, unsigned(p.keyHeads));
-    const unsigned scanBlocks = unsigned(p.valueHeads * (p.valueDim / NB));
-#define AIGPU_DELTA(KD, F)                                                                                    \
-    if (p.keyDim == KD && (p.inType == 0) == F) {                                                             \
-        if (!ctx.launch("delta_solve_kernel", stream, [&] {                                                   \
-                hipLaunchKernelGGL((delta_solve_kernel<KD, F>), sgrid, dim3(256), 0, stream, a);             \
-            }))                                                                                               \
-            return false;                                                                                     \
-        return ctx.launch("delta_scan_kernel", stream, [&] {                                                  \
-            const dim3 grid{scanBlocks}, block{256};                                                         \
-            if (F && a.vec) hipLaunchKernelGGL((delta_scan_f32_kernel<KD, true>), grid, block, 0, stream, a);    \
-            else if (F) hipLaunchKernelGGL((delta_scan_f32_kernel<KD, false>), grid, block, 0, stream, a);        \
-            else if (a.vec) hipLaunchKernelGGL((delta_scan_kernel<KD, true>), grid, block, 0, stream, a);         \
-            else hipLaunchKernelGGL((delta_scan_kernel<KD, false>), grid, block, 0, stream, a);                    \
-        });                                                                                                   \
+    const dim3 grid{unsigned(p.valueHeads * (p.valueDim / NB))}, block{256};
+#define AIGPU_DELTA(KD)                                                                                        \
+    if (p.keyDim == KD) {                                                                                      \
+        if (!ctx.launch("delta_solve_kernel", stream, [&] {                                                    \
+                if (p.inType == 0)                                                                             \
+                    hipLaunchKernelGGL((delta_solve_kernel<KD, true, false>), sgrid, dim3(256), 0, stream, a);  \
+                else if (dma)                                                                                  \
+                    hipLaunchKernelGGL((delta_solve_kernel<KD, false, true>), sgrid, dim3(256), 0, stream, a);  \
+                else                                                                                           \
+                    hipLaunchKernelGGL((delta_solve_kernel<KD, false, false>), sgrid, dim3(256), 0, stream, a); \
+            }))                                                                                                \
+            return false;                                                                                      \
+        return ctx.launch("delta_scan_kernel", stream, [&] {                                                   \
+            if (p.inType == 0 && a.vec)                                                                        \
+                hipLaunchKernelGGL((delta_scan_f32_kernel<KD, true>), grid, block, 0, stream, a);              \
+            else if (p.inType == 0)                                                                            \
+                hipLaunchKernelGGL((delta_scan_f32_kernel<KD, false>), grid, block, 0, stream, a);             \
+            else if (dma)                                                                                      \
+                hipLaunchKernelGGL((delta_scan_dma_kernel<KD>), grid, block, 0, stream, a);                    \
+            else                                                                                               \
+                hipLaunchKernelGGL((delta_scan_kernel<KD, false>), grid, block, 0, stream, a);                 \
+        });                                                                                                    \
     }
-    AIGPU_DELTA(128, false)
-    AIGPU_DELTA(128, true)
-    AIGPU_DELTA(64, false)
-    AIGPU_DELTA(64, true)
+    AIGPU_DELTA(128)
+    AIGPU_DELTA(64)
 #undef AIGPU_DELTA
     return ctx.fail("delta rule: unsupported configuration");
 }

@@ -17,13 +17,24 @@ def gates(S, hv, seed):
     return g, beta
 
 
-def run_gdn(gpu, S, hk, hv, kd, vd, seed, dtype="f32", state0=None, raw_gates=False):
+def misaligned(t):
+    """the same values in a view that starts 2 bytes past a 16-byte boundary"""
+    import torch
+    flat = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    flat[1:].copy_(t.reshape(-1))
+    return flat[1:].view(t.shape)
+
+
+def run_gdn(gpu, S, hk, hv, kd, vd, seed, dtype="f32", state0=None, raw_gates=False, unaligned=False):
     import torch
     if dtype == "bf16":
         qb, q = bf16_normal((S, hk, kd), seed, "q")
         kb, k = bf16_normal((S, hk, kd), seed, "k")
         vb, v = bf16_normal((S, hv, vd), seed, "v")
         dq, dk, dv = dev_bf16(qb), dev_bf16(kb), dev_bf16(vb)
+        if unaligned:   # the register-staged scan instead of the DMA scan
+            dq, dk, dv = misaligned(dq), misaligned(dk), misaligned(dv)
+            assert dq.data_ptr() % 16 == 2
     else:
         q = O.fill_normal((S, hk, kd), seed, "q")
         k = O.fill_normal((S, hk, kd), seed, "k")
@@ -61,6 +72,13 @@ def test_lengths_bf16(gpu, S):
     ro, go, rs, gs = run_gdn(gpu, S, 2, 4, 128, 128, 200 + S, dtype="bf16")
     assert_bf16_parity(ro, go, f"out S={S}")
     assert_bf16_parity(rs, gs, f"state S={S}")
+
+
+@pytest.mark.parametrize("kd", [128, 64])
+def test_bf16_unaligned_inputs(gpu, kd):
+    ro, go, rs, gs = run_gdn(gpu, 130, 2, 4, kd, 32, 300 + kd, dtype="bf16", unaligned=True)
+    assert_bf16_parity(ro, go, f"out bf16 unaligned kd{kd}")
+    assert_bf16_parity(rs, gs, f"state bf16 unaligned kd{kd}")
 
 
 def test_bf16_raw_gates_initial_state_kd64(gpu):
