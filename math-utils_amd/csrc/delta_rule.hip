@@ -863,18 +863,18 @@ __device__ __forceinline__ void dma_block(const void* src, const void* lds) {
       - T and QKm come from the solve kernel already split into bf16 hi/lo in
         this kernel's LDS layout, with the per-row scalars;
       - the value block [64][16] bf16.
-    k, T, v and the scalars are double-buffered and fetched a chunk ahead; q
-    and QKm, read only by the output product at the end of a chunk, have one
-    buffer and are fetched at the chunk's start. Per chunk, with three
-    barriers:
-      R  = diag(beta) (V - diag(gamma kinv) K_raw S)
+    Every input is double-buffered and fetched a whole chunk ahead, so each
+    chunk waits once, at its start, for DMA issued a chunk earlier. Per chunk,
+    with three barriers:
+      R  = diag(beta) (V - diag(gamma kinv) K_raw S),  and Q_raw S
       U  = T R,  W = diag(kinv e^{gc_last - gc}) U
       S' = e^{gc_last} S + K_raw^T W
-      O  = diag(gamma qinv) Q_raw S + QKm U
+      O  = diag(gamma qinv) (Q_raw S) + QKm U
     S is each wave's fp32 accumulators (wave w owns key rows 16 (w + 4t) +
-    0..15); its transposed hi/lo split, the B operand of the R and O products,
-    is double-buffered by chunk parity so S' is published while O still reads
-    S. Every product takes hi*hi + hi*lo (+ lo*hi) with fp32 accumulation.
+    0..15); its transposed hi/lo split is the B operand of both first-phase
+    products, so once they are done (the barrier after R) S' can be published
+    over it. Every product takes hi*hi + hi*lo (+ lo*hi) with fp32
+    accumulation.
 */
 template <int KD>
 __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
@@ -882,7 +882,7 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
     constexpr int RPI = 1024 / (2 * KD);             // k/q rows per 1 KB DMA block
     constexpr int KI = CH / RPI / 4;                 // k (or q) DMA blocks per wave
     constexpr int TI = 4;                            // T (or QKm) hi+lo blocks per wave: 16 KB / 4
-    constexpr int KTVS = KI + TI + 1;                // DMA blocks per wave for k, T, v + scalars
+
     constexpr int KST = KD + 8;                      // S^T row stride (elements)
     constexpr int CHH = CH + 8;                      // R^T, U^T, W^T row stride
     constexpr int MT = KD / 64;                      // 16-row state tiles per wave
@@ -890,9 +890,9 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
     __shared__ __attribute__((aligned(16))) __bf16 Kb[2][CH * KD];        // raw k rows, swizzled
     __shared__ __attribute__((aligned(16))) __bf16 Tb[2][2 * CH * CH];    // T hi, lo (solve's image)
     __shared__ __attribute__((aligned(16))) float Ax[2][1024];           // v [64][16] bf16, then scalars
-    __shared__ __attribute__((aligned(16))) __bf16 Qb[CH * KD];           // raw q rows, swizzled
-    __shared__ __attribute__((aligned(16))) __bf16 Mb[2 * CH * CH];       // QKm hi, lo
-    __shared__ __attribute__((aligned(16))) __bf16 St[2][2][NB * KST];    // [parity][hi/lo] S^T [col][key]
+    __shared__ __attribute__((aligned(16))) __bf16 Qb[2][CH * KD];        // raw q rows, swizzled
+    __shared__ __attribute__((aligned(16))) __bf16 Mb[2][2 * CH * CH];    // QKm hi, lo
+    __shared__ __attribute__((aligned(16))) __bf16 St[2][NB * KST];       // [hi/lo] S^T [col][key]
     __shared__ __attribute__((aligned(16))) __bf16 Rt[2][NB * CHH];       // R^T hi, lo
     __shared__ __attribute__((aligned(16))) __bf16 Ut[2][NB * CHH];       // U^T
     __shared__ __attribute__((aligned(16))) __bf16 Wt[2][NB * CHH];       // W^T
@@ -937,10 +937,12 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
             dma_block(reinterpret_cast<const uint8_t*>(rec) + blk * 1024 + 16 * lane, dst + blk * 512);
         }
     };
-    auto issue_ktvs = [&](uint32_t chunk, int buf) __attribute__((always_inline)) {
+    auto issue = [&](uint32_t chunk, int buf) __attribute__((always_inline)) {
         dma_rows(p.k, chunk, Kb[buf]);
+        dma_rows(p.q, chunk, Qb[buf]);
         const float* rec = record(chunk);
         dma_mat(rec, Tb[buf]);
+        dma_mat(rec + 2 * SPLIT_MAT, Mb[buf]);
         if (w < 2) {   // value block: 32 rows of 32 bytes per DMA block
             const uint64_t t0 = uint64_t(chunk) * CH;
             const uint32_t n = chunk_rows(chunk);
@@ -952,10 +954,6 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
             dma_block(reinterpret_cast<const uint8_t*>(rec + 4 * SPLIT_MAT) + 1024 * (w - 2) + 16 * lane,
                       reinterpret_cast<uint8_t*>(Ax[buf]) + 2048 + 1024 * (w - 2));
         }
-    };
-    auto issue_qm = [&](uint32_t chunk) __attribute__((always_inline)) {
-        dma_rows(p.q, chunk, Qb);
-        dma_mat(record(chunk) + 2 * SPLIT_MAT, Mb);
     };
 
     // C-layout tile (rows row0 + 4g + r, column c16) -> transposed split [col][row]
@@ -990,12 +988,12 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             sacc[t][r] = state[size_t(16 * (w + 4 * t) + 4 * g + r) * VD + col0 + c16];
-    auto publish_state = [&](int par) __attribute__((always_inline)) {
+    auto publish_state = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < MT; ++t) put_t(St[par][0], St[par][1], KST, 16 * (w + 4 * t), sacc[t]);
+        for (int t = 0; t < MT; ++t) put_t(St[0], St[1], KST, 16 * (w + 4 * t), sacc[t]);
     };
-    publish_state(0);
-    issue_ktvs(0, 0);
+    publish_state();
+    issue(0, 0);
 
     floatx4 oacc = {0.0f, 0.0f, 0.0f, 0.0f};
     auto store_out = [&](uint32_t chunk) __attribute__((always_inline)) {
@@ -1010,16 +1008,17 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
 
     for (uint32_t chunk = 0; chunk < nChunks; ++chunk) {
         const int par = chunk & 1;
-        // this chunk's k, T, v and scalars have landed (and every earlier
-        // store has left); every read of the other buffers is done
+        // this chunk's inputs have landed (and every earlier store has left);
+        // every read of the other buffers is done
         wait_vmcnt_all();
         __syncthreads();
-        issue_qm(chunk);
-        issue_ktvs(chunk + 1 < nChunks ? chunk + 1 : chunk, par ^ 1);   // the last chunk reloads itself
+        issue(chunk + 1 < nChunks ? chunk + 1 : chunk, par ^ 1);   // the last chunk reloads itself
         if (chunk > 0) store_out(chunk - 1);
 
         const __bf16* K = Kb[par];
+        const __bf16* Q = Qb[par];
         const __bf16* T = Tb[par];
+        const __bf16* M = Mb[par];
         const __bf16* vb = reinterpret_cast<const __bf16*>(Ax[par]);
         const float* sc = Ax[par] + 512;
         const float* beta = sc;
@@ -1027,17 +1026,18 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
         const float* gqinv = sc + 2 * CH;
         const float* kdk = sc + 3 * CH;
         const float eLast = sc[4 * CH];
-        const __bf16* S0 = St[par][0];
-        const __bf16* S1 = St[par][1];
-
-        // R = beta (V - gamma kinv (K_raw S))
-        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        // R = beta (V - gamma kinv (K_raw S)), and Q_raw S for the output
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, qs = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int kb = 0; kb < KD / 32; ++kb) {
-            const bf16x8 x = rows_a(K, kb);
+            const bf16x8 x = rows_a(K, kb), xq = rows_a(Q, kb);
             const int yo = c16 * KST + 32 * kb + 8 * g;
-            acc = mfma_bf(x, *reinterpret_cast<const bf16x8*>(S0 + yo), acc);
-            acc = mfma_bf(x, *reinterpret_cast<const bf16x8*>(S1 + yo), acc);
+            const bf16x8 sh = *reinterpret_cast<const bf16x8*>(&St[0][yo]);
+            const bf16x8 sl = *reinterpret_cast<const bf16x8*>(&St[1][yo]);
+            acc = mfma_bf(x, sh, acc);
+            qs = mfma_bf(xq, sh, qs);
+            acc = mfma_bf(x, sl, acc);
+            qs = mfma_bf(xq, sl, qs);
         }
         {
             floatx4 rv;
@@ -1068,7 +1068,6 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
             for (int r = 0; r < 4; ++r) wv[r] = kdk[16 * w + 4 * g + r] * u[r];
             put_t(Wt[0], Wt[1], CHH, 16 * w, wv);
         }
-        wait_vmcnt<KTVS>();   // this wave's q and QKm blocks have landed
         lds_barrier();
 
         // S' = e^{gc_last} S + K_raw^T W: A = K^T rows d through transposed
@@ -1090,22 +1089,14 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
                 sacc[t] = mfma_bf(kt, *reinterpret_cast<const bf16x8*>(&Wt[1][yo]), sacc[t]);
             }
         }
-        publish_state(par ^ 1);
+        publish_state();   // every read of S^T was before the barrier after R
 
         // O = gamma qinv (Q_raw S) + QKm U
-        acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kb = 0; kb < KD / 32; ++kb) {
-            const bf16x8 x = rows_a(Qb, kb);
-            const int yo = c16 * KST + 32 * kb + 8 * g;
-            acc = mfma_bf(x, *reinterpret_cast<const bf16x8*>(S0 + yo), acc);
-            acc = mfma_bf(x, *reinterpret_cast<const bf16x8*>(S1 + yo), acc);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] *= gqinv[16 * w + 4 * g + r];
+        for (int r = 0; r < 4; ++r) acc[r] = qs[r] * gqinv[16 * w + 4 * g + r];
 #pragma unroll
         for (int kb = 0; kb < CH / 32; ++kb) {
-            const bf16x8 mh = mat_a(Mb, kb), ml = mat_a(Mb + CH * CH, kb);
+            const bf16x8 mh = mat_a(M, kb), ml = mat_a(M + CH * CH, kb);
             const int yo = c16 * CHH + 32 * kb + 8 * g;
             const bf16x8 uh = *reinterpret_cast<const bf16x8*>(&Ut[0][yo]);
             acc = mfma_bf(mh, uh, acc);
