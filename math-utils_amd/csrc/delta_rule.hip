@@ -846,13 +846,21 @@ __device__ __forceinline__ void lds_barrier() {
    DMA that reads it; nothing else in the scan uses M0. */
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"   // M0 is reserved, and clobbered on purpose
-__device__ __forceinline__ void dma_block(const void* src, const void* lds) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-        uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)lds)));
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0)
+__device__ __forceinline__ void dma_block(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds)
+                 : "memory", "m0");
+}
+/* the same from a uniform base plus a 32-bit per-lane byte offset */
+__device__ __forceinline__ void dma_block(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "s"(lds)
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
+
+/* LDS byte address of a __shared__ object */
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
 
 /*
     The scan for 16-byte aligned bf16 inputs with every chunk input DMA'd into
@@ -905,7 +913,8 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
     const uint32_t h = bid / nCol, cb = bid % nCol;
     const uint32_t kh = uint32_t(h / (p.valueHeads / p.keyHeads));
     const uint32_t col0 = cb * NB;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c16 = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: DMA targets are scalar
     const size_t VD = p.valueDim, Hv = p.valueHeads;
     const uint32_t nChunks = a.nChunks;
 
@@ -916,43 +925,59 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
     auto record = [&](uint32_t chunk) -> const float* {
         return a.work + (size_t(h) * nChunks + chunk) * WORK_SPLIT;
     };
-    // k or q rows of `chunk` into a swizzled [64][KD] buffer; rows past the
-    // end repeat the last row (their beta is 0)
-    auto dma_rows = [&](const void* base, uint32_t chunk, __bf16* dst) __attribute__((always_inline)) {
+    // DMA targets: LDS byte addresses of each buffer (uniform)
+    const uint32_t ldsK = lds_address(Kb), ldsQ = lds_address(Qb), ldsT = lds_address(Tb);
+    const uint32_t ldsM = lds_address(Mb), ldsA = lds_address(Ax);
+    constexpr uint32_t KBUF = CH * KD * 2, TBUF = 2 * CH * CH * 2, ABUF = 4096;   // bytes per buffer
+    // per-lane byte offsets of this wave's DMA blocks within a chunk: k/q
+    // rows (block j: rows RPI (w KI + j) + lane / KBLK, swizzled; rows past a
+    // partial chunk's end repeat its last row, whose beta is 0), the split
+    // matrices and scalars of a record, the value rows
+    const uint32_t rowBytes = uint32_t(p.keyHeads * KD * 2);
+    int kqRow[KI];
+    uint32_t kqCol[KI];
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+        kqRow[j] = RPI * (w * KI + j) + lane / KBLK;
+        kqCol[j] = kh * KD * 2 + 16 * ((lane % KBLK) ^ (kqRow[j] % KBLK));
+    }
+    const uint32_t matOff = uint32_t(w * TI * 1024 + 16 * lane);
+    const uint32_t vRowBytes = uint32_t(Hv * VD * 2);
+    const int vRow = 32 * w + lane / 2;
+
+    // The next chunk's DMA is spread over the current chunk's phases, a block
+    // or two between MFMAs: a wave that issues it all at once stalls on the
+    // memory pipeline's queue before its next LDS read.
+    struct Next {
+        const uint8_t *k, *q, *rec, *v;
+        uint32_t n;
+        int buf;
+    };
+    auto next_of = [&](uint32_t chunk, int buf) __attribute__((always_inline)) {
         const uint64_t t0 = uint64_t(chunk) * CH;
-        const uint32_t n = chunk_rows(chunk);
-#pragma unroll
-        for (int j = 0; j < KI; ++j) {
-            const int blk = w * KI + j, row = RPI * blk + lane / KBLK, pb = lane % KBLK;
-            const int lb = pb ^ (row % KBLK);
-            const uint32_t rr = uint32_t(row) < n ? uint32_t(row) : n - 1;
-            const uint16_t* src = static_cast<const uint16_t*>(base) + ((t0 + rr) * p.keyHeads + kh) * KD + 8 * lb;
-            dma_block(src, dst + blk * 512);
-        }
+        return Next{static_cast<const uint8_t*>(p.k) + t0 * rowBytes, static_cast<const uint8_t*>(p.q) + t0 * rowBytes,
+                    reinterpret_cast<const uint8_t*>(record(chunk)),
+                    static_cast<const uint8_t*>(p.v) + ((t0 * Hv + h) * VD + col0) * 2, chunk_rows(chunk), buf};
     };
-    auto dma_mat = [&](const float* rec, __bf16* dst) __attribute__((always_inline)) {   // hi + lo, 16 KB
-#pragma unroll
-        for (int j = 0; j < TI; ++j) {
-            const int blk = w * TI + j;
-            dma_block(reinterpret_cast<const uint8_t*>(rec) + blk * 1024 + 16 * lane, dst + blk * 512);
-        }
+    auto dma_rows_j = [&](const Next& nx, int j) __attribute__((always_inline)) {   // k and q block j
+        const uint32_t rr = uint32_t(kqRow[j]) < nx.n ? uint32_t(kqRow[j]) : nx.n - 1;
+        const uint32_t off = rr * rowBytes + kqCol[j];
+        dma_block(nx.k, off, ldsK + nx.buf * KBUF + (w * KI + j) * 1024);
+        dma_block(nx.q, off, ldsQ + nx.buf * KBUF + (w * KI + j) * 1024);
     };
-    auto issue = [&](uint32_t chunk, int buf) __attribute__((always_inline)) {
-        dma_rows(p.k, chunk, Kb[buf]);
-        dma_rows(p.q, chunk, Qb[buf]);
-        const float* rec = record(chunk);
-        dma_mat(rec, Tb[buf]);
-        dma_mat(rec + 2 * SPLIT_MAT, Mb[buf]);
+    auto dma_t_j = [&](const Next& nx, int j) __attribute__((always_inline)) {
+        dma_block(nx.rec + j * 1024, matOff, ldsT + nx.buf * TBUF + (w * TI + j) * 1024);
+    };
+    auto dma_m_j = [&](const Next& nx, int j) __attribute__((always_inline)) {
+        dma_block(nx.rec + 2 * SPLIT_MAT * 4 + j * 1024, matOff, ldsM + nx.buf * TBUF + (w * TI + j) * 1024);
+    };
+    auto dma_aux = [&](const Next& nx) __attribute__((always_inline)) {
         if (w < 2) {   // value block: 32 rows of 32 bytes per DMA block
-            const uint64_t t0 = uint64_t(chunk) * CH;
-            const uint32_t n = chunk_rows(chunk);
-            const int row = 32 * w + lane / 2;
-            const uint32_t rr = uint32_t(row) < n ? uint32_t(row) : n - 1;
-            const uint16_t* src = static_cast<const uint16_t*>(p.v) + ((t0 + rr) * Hv + h) * VD + col0 + 8 * (lane & 1);
-            dma_block(src, reinterpret_cast<uint8_t*>(Ax[buf]) + 1024 * w);
+            const uint32_t rr = uint32_t(vRow) < nx.n ? uint32_t(vRow) : nx.n - 1;
+            dma_block(nx.v, rr * vRowBytes + 16 * (lane & 1), ldsA + nx.buf * ABUF + 1024 * w);
         } else {       // scalars
-            dma_block(reinterpret_cast<const uint8_t*>(rec + 4 * SPLIT_MAT) + 1024 * (w - 2) + 16 * lane,
-                      reinterpret_cast<uint8_t*>(Ax[buf]) + 2048 + 1024 * (w - 2));
+            dma_block(nx.rec + 4 * SPLIT_MAT * 4, uint32_t(1024 * (w - 2) + 16 * lane),
+                      ldsA + nx.buf * ABUF + 2048 + 1024 * (w - 2));
         }
     };
 
@@ -993,17 +1018,34 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
         for (int t = 0; t < MT; ++t) put_t(St[0], St[1], KST, 16 * (w + 4 * t), sacc[t]);
     };
     publish_state();
-    issue(0, 0);
+    {
+        const Next first = next_of(0, 0);
+#pragma unroll
+        for (int j = 0; j < KI; ++j) dma_rows_j(first, j);
+#pragma unroll
+        for (int j = 0; j < TI; ++j) {
+            dma_t_j(first, j);
+            dma_m_j(first, j);
+        }
+        dma_aux(first);
+    }
 
-    floatx4 oacc = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto store_out = [&](uint32_t chunk) __attribute__((always_inline)) {
+    // The wave's 16 output rows leave as one 16-byte store per lane (row
+    // 16w + lane / 4, columns 4 (lane % 4) ..): the C-layout tile goes
+    // through the wave's own kilobyte of the R^T buffer, which no wave uses
+    // between the barrier after U and the next chunk's R phase.
+    const uint32_t oOff = uint32_t(16 * w + lane / 4) * uint32_t(Hv * VD * 4) + 16 * (lane & 3);
+    float* stage = reinterpret_cast<float*>(Rt[0]) + 256 * w;
+    static_assert(2 * NB * CHH * 2 >= 4 * 1024, "R^T holds four waves' output tiles");
+    auto store_out = [&](uint32_t chunk, const floatx4& o) __attribute__((always_inline)) {
         const uint64_t t0 = uint64_t(chunk) * CH;
         const uint32_t n = chunk_rows(chunk);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t i = 16 * w + 4 * g + r;
-            if (i < n) p.out[((t0 + i) * Hv + h) * VD + col0 + c16] = oacc[r];
-        }
+        for (int r = 0; r < 4; ++r) stage[(4 * g + r) * NB + c16] = o[r];
+        wave_sync();
+        const floatx4 v4 = *reinterpret_cast<const floatx4*>(stage + 4 * lane);
+        uint8_t* ob = reinterpret_cast<uint8_t*>(p.out + (t0 * Hv + h) * VD + col0);
+        if (uint32_t(16 * w + lane / 4) < n) *reinterpret_cast<floatx4*>(ob + oOff) = v4;
     };
 
     for (uint32_t chunk = 0; chunk < nChunks; ++chunk) {
@@ -1012,8 +1054,7 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
         // every read of the other buffers is done
         wait_vmcnt_all();
         __syncthreads();
-        issue(chunk + 1 < nChunks ? chunk + 1 : chunk, par ^ 1);   // the last chunk reloads itself
-        if (chunk > 0) store_out(chunk - 1);
+        const Next nx = next_of(chunk + 1 < nChunks ? chunk + 1 : chunk, par ^ 1);   // the last chunk reloads itself
 
         const __bf16* K = Kb[par];
         const __bf16* Q = Qb[par];
@@ -1028,8 +1069,10 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
         const float eLast = sc[4 * CH];
         // R = beta (V - gamma kinv (K_raw S)), and Q_raw S for the output
         floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, qs = {0.0f, 0.0f, 0.0f, 0.0f};
+        static_assert(KI == KD / 32, "one k/q DMA block per first-phase step");
 #pragma unroll
         for (int kb = 0; kb < KD / 32; ++kb) {
+            dma_rows_j(nx, kb);
             const bf16x8 x = rows_a(K, kb), xq = rows_a(Q, kb);
             const int yo = c16 * KST + 32 * kb + 8 * g;
             const bf16x8 sh = *reinterpret_cast<const bf16x8*>(&St[0][yo]);
@@ -1054,6 +1097,10 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
         floatx4 u = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int kb = 0; kb < CH / 32; ++kb) {
+            dma_t_j(nx, 2 * kb);
+            dma_t_j(nx, 2 * kb + 1);
+            dma_m_j(nx, 2 * kb);
+            dma_m_j(nx, 2 * kb + 1);
             const bf16x8 th = mat_a(T, kb), tl = mat_a(T + CH * CH, kb);
             const int yo = c16 * CHH + 32 * kb + 8 * g;
             const bf16x8 rh = *reinterpret_cast<const bf16x8*>(&Rt[0][yo]);
@@ -1061,6 +1108,7 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
             u = mfma_bf(th, *reinterpret_cast<const bf16x8*>(&Rt[1][yo]), u);
             u = mfma_bf(tl, rh, u);
         }
+        dma_aux(nx);
         put_t(Ut[0], Ut[1], CHH, 16 * w, u);
         {
             floatx4 wv;
@@ -1103,9 +1151,8 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
             acc = mfma_bf(mh, *reinterpret_cast<const bf16x8*>(&Ut[1][yo]), acc);
             acc = mfma_bf(ml, uh, acc);
         }
-        oacc = acc;
+        store_out(chunk, acc);
     }
-    store_out(nChunks - 1);
     wait_vmcnt_all();   // the last chunk's reload must land before the LDS is released
 #pragma unroll
     for (int t = 0; t < MT; ++t)
@@ -1136,7 +1183,9 @@ bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream) {
     // bf16 inputs on 16-byte boundaries take the DMA scan, whose records are
     // the split form; fp32 and unaligned bf16 inputs take the register-staged
     // scans over fp32 records
-    const bool dma = p.inType == 1 && a.vec;
+    // (its per-lane DMA and store offsets within a chunk are 32-bit)
+    const bool dma = p.inType == 1 && a.vec && uint64_t(CH) * p.keyHeads * p.keyDim * 2 < (1ull << 31) &&
+                     uint64_t(CH) * p.valueHeads * p.valueDim * 4 < (1ull << 31);
     const size_t rec = dma ? WORK_SPLIT : WORK;
     a.work = static_cast<float*>(ctx.grow(SLOT_DELTA_WORK, size_t(p.valueHeads) * a.nChunks * rec * sizeof(float)));
     if (!a.work) return false;
