@@ -261,16 +261,23 @@ __global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs
         __syncthreads();
 
         // T = (I + A)^-1. Diagonal blocks: wave w inverts block w by forward
-        // substitution, lane = column within the block.
+        // substitution, T[i][j] = [i == j] - sum_{m < i} A[i][m] T[m][j], with
+        // column j = lane % 16 of every row in registers and each A row read
+        // as a broadcast; terms with m < j are exact zeros (T[m][j] = 0), so
+        // the sum is the one over j <= m < i.
         {
-            const int b0 = 16 * w;
+            const int b0 = 16 * w, j = lane & 15;
+            float t[16];
+#pragma unroll
             for (int i = 0; i < 16; ++i) {
-                if (lane < 16) {
-                    float acc = 0.0f;
-                    for (int mm = lane; mm < i; ++mm) acc = fmaf(Am[(b0 + i) * CS + b0 + mm], Tm[(b0 + mm) * CS + b0 + lane], acc);
-                    Tm[(b0 + i) * CS + b0 + lane] = lane < i ? -acc : (lane == i ? 1.0f : 0.0f);
-                }
-                wave_sync();
+                float acc = i == j ? 1.0f : 0.0f;
+#pragma unroll
+                for (int m = 0; m < i; ++m) acc = fmaf(-Am[(b0 + i) * CS + b0 + m], t[m], acc);
+                t[i] = acc;
+            }
+            if (lane < 16) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) Tm[(b0 + i) * CS + b0 + j] = t[i];
             }
         }
         // Off-diagonal block (I, J): T_IJ = -T_II sum_{M=J}^{I-1} A_IM T_MJ; the
