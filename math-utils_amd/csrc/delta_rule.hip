@@ -15,18 +15,21 @@
 // overflows however strongly the gates decay.
 //
 // Two launches:
-//   delta_solve_kernel  parallel over (head, chunk): l2 norms, KK^T, QK^T,
-//                       the decayed masks and T = (I + A)^-1 (blocked: four
-//                       16 x 16 diagonal blocks by forward substitution, the
-//                       rest by block products); writes T, QKm, gc, beta and
-//                       the per-row inverse norms to a workspace
-//   delta_scan_kernel   per (head, 16 value columns): walks the chunks in
-//                       order carrying S (fp32, in LDS), U = T R, outputs
-//                       and the state update on v_mfma_f32_16x16x4f32. It
-//                       reads the raw q/k rows and applies the inverse norms
-//                       as row scales of the products (k_i = k_raw_i kinv_i
-//                       enters every product linearly), and it loads chunk
-//                       c + 1 into registers while it computes chunk c.
+//   delta_solve_kernel  parallel over (key head, chunk): l2 norms, KK^T, QK^T,
+//                       then per value head the decayed masks and
+//                       T = (I + A)^-1 (blocked: four 16 x 16 diagonal blocks
+//                       by forward substitution, the rest by block products);
+//                       writes a record per (value head, chunk): T, QKm and
+//                       per-row scalars, fp32 or split into bf16 hi/lo
+//   delta_scan_*        per (value head, 16 value columns): walks the chunks
+//                       in order carrying S in registers. The DMA scan (bf16
+//                       inputs on 16-byte boundaries) takes every chunk input
+//                       into LDS by DMA a chunk ahead; the register-staged
+//                       scans (unaligned bf16, fp32) load the next chunk into
+//                       registers while the current one computes. They read
+//                       the raw q/k rows and apply the inverse norms as row
+//                       scales of the products (k_i = k_raw_i kinv_i enters
+//                       every product linearly).
 // State columns evolve independently (Kernels.hpp:113-125 touches column d
 // only through delta[d]), which is what lets one head split over 16-column
 // workgroups.
