@@ -207,6 +207,49 @@ AIGPU_ABI int aigpu_gated_delta_rule(const AiGpuDeltaRule* args);
 AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule* args);
 
 /* ------------------------------------------------------------------------ */
+/* 6. The Gated DeltaNet steps either side of the recurrence                 */
+/*    (gatedDeltaNetMixer, LocalModel.hpp:2724-2844). No reference kernel    */
+/*    exists for them: the mixer runs them inline on the host.               */
+/* ------------------------------------------------------------------------ */
+/* causalConvolution + SiLU (LocalModel.hpp:2678-2708) over the projection    */
+/* rows, with the linFusedQKVZ de-interleave (:2739-2776) when `fused` is     */
+/* set, writing the recurrence's dense inputs. The window carries the last   */
+/* kernelSize-1 inputs between calls (LocalCache::convWindow), as fp32.      */
+typedef struct AiGpuGdnConv {
+    const void* in;           /* fused == 0: [count][CW] rows q | k | v (CW = 2 keyHeads keyDim
+                                 + valueHeads valueDim); fused: [count][keyHeads][2 keyDim +
+                                 2 G valueDim] (per key head q, k, its G value heads' v, their z) */
+    const void* ba;           /* fused: [count][keyHeads][2 G], the G heads' b then their a */
+    const float* kernel;      /* [CW][kernelSize] (LocalLayer::linConv) */
+    float* window;            /* [kernelSize-1][CW] fp32, read then replaced */
+    void* q;                  /* out [count][keyHeads][keyDim], outType */
+    void* k;                  /* out [count][keyHeads][keyDim], outType */
+    void* v;                  /* out [count][valueHeads][valueDim], outType */
+    void* z;                  /* fused: out [count][valueHeads][valueDim], outType (not convolved) */
+    float* a;                 /* fused: out [count][valueHeads] fp32 */
+    float* b;                 /* fused: out [count][valueHeads] fp32 */
+    uint32_t inType, outType; /* AIGPU_F32 / AIGPU_BF16 */
+    uint32_t fused, reserved;
+    uint64_t count, keyHeads, valueHeads, keyDim, valueDim, kernelSize;
+    void* stream;
+} AiGpuGdnConv;
+AIGPU_ABI int aigpu_gdn_conv(const AiGpuGdnConv* args);
+
+/* rmsNormRow of each (token, value head) row of the recurrence output, its  */
+/* weight stored directly, then times SiLU(z) (LocalModel.hpp:2833-2841)     */
+typedef struct AiGpuGdnGatedNorm {
+    const float* x;           /* [count][valueHeads][valueDim] fp32 */
+    const void* z;            /* [count][valueHeads][valueDim], zType */
+    const float* gamma;       /* [valueDim] (LocalLayer::linNorm) */
+    void* out;                /* [count][valueHeads][valueDim], outType */
+    float epsilon;            /* LocalConfig::normEps */
+    uint32_t zType, outType, reserved;
+    uint64_t count, valueHeads, valueDim;
+    void* stream;
+} AiGpuGdnGatedNorm;
+AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm* args);
+
+/* ------------------------------------------------------------------------ */
 /* Per-kernel timing. With profiling on, every launch is bracketed by a pair */
 /* of hipEvents on the stream it runs on; aigpu_profile_read synchronises    */
 /* and reports the summed device time and launch count of kernels whose name */

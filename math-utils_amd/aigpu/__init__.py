@@ -70,6 +70,20 @@ class AiGpuDeltaRule(C.Structure):
                 ("valueDim", _u64), ("stream", _vp)]
 
 
+class AiGpuGdnConv(C.Structure):
+    _fields_ = [("in_", _vp), ("ba", _vp), ("kernel", _vp), ("window", _vp), ("q", _vp), ("k", _vp),
+                ("v", _vp), ("z", _vp), ("a", _vp), ("b", _vp),
+                ("inType", _u32), ("outType", _u32), ("fused", _u32), ("reserved", _u32),
+                ("count", _u64), ("keyHeads", _u64), ("valueHeads", _u64), ("keyDim", _u64),
+                ("valueDim", _u64), ("kernelSize", _u64), ("stream", _vp)]
+
+
+class AiGpuGdnGatedNorm(C.Structure):
+    _fields_ = [("x", _vp), ("z", _vp), ("gamma", _vp), ("out", _vp), ("epsilon", C.c_float),
+                ("zType", _u32), ("outType", _u32), ("reserved", _u32),
+                ("count", _u64), ("valueHeads", _u64), ("valueDim", _u64), ("stream", _vp)]
+
+
 # every symbol include/aigpu_attention.h declares, with its signature
 SIGNATURES = {
     "aigpu_available": (C.c_int, []),
@@ -92,6 +106,8 @@ SIGNATURES = {
     "aigpu_prefill_attention_host": (C.c_int, [C.POINTER(AiGpuPrefill)]),
     "aigpu_decode_attention": (C.c_int, [C.POINTER(AiGpuDecode)]),
     "aigpu_decode_attention_host": (C.c_int, [C.POINTER(AiGpuDecode)]),
+    "aigpu_gdn_conv": (C.c_int, [C.POINTER(AiGpuGdnConv)]),
+    "aigpu_gdn_gated_norm": (C.c_int, [C.POINTER(AiGpuGdnGatedNorm)]),
     "aigpu_gated_delta_rule": (C.c_int, [C.POINTER(AiGpuDeltaRule)]),
     "aigpu_gated_delta_rule_host": (C.c_int, [C.POINTER(AiGpuDeltaRule)]),
     "aigpu_profile": (None, [C.c_int]),
@@ -296,4 +312,35 @@ def gated_delta_rule(q, k, v, state, out, g=None, beta=None, a=None, b=None, a_l
                           keyHeads=key_heads, valueHeads=value_heads, keyDim=key_dim,
                           valueDim=value_dim, stream=_stream(stream))
     _check(lib().aigpu_gated_delta_rule(C.byref(args)))
+    return out
+
+
+def gdn_conv(x, kernel, window, q, k, v, key_heads, value_heads, key_dim, value_dim, ba=None, z=None,
+             a=None, b=None, stream=None):
+    """Device form of gatedDeltaNetMixer's de-interleave + causalConvolution:
+    x [count][CW] (plain) or [count][key_heads][2 KD + 2 G VD] with ba (fused);
+    writes q, k, v (and z, a, b when fused); window [K-1][CW] fp32 updated."""
+    fused = ba is not None
+    for t, n in ((x, "x"), (kernel, "kernel"), (window, "window"), (q, "q"), (k, "k"), (v, "v"),
+                 (ba, "ba"), (z, "z"), (a, "a"), (b, "b")):
+        _need(t, n)
+    args = AiGpuGdnConv(in_=_ptr(x), ba=_ptr(ba), kernel=_ptr(kernel), window=_ptr(window), q=_ptr(q),
+                        k=_ptr(k), v=_ptr(v), z=_ptr(z), a=_ptr(a), b=_ptr(b), inType=_dtype_tag(x),
+                        outType=_dtype_tag(q), fused=1 if fused else 0, count=x.shape[0],
+                        keyHeads=key_heads, valueHeads=value_heads, keyDim=key_dim, valueDim=value_dim,
+                        kernelSize=kernel.shape[1], stream=_stream(stream))
+    _check(lib().aigpu_gdn_conv(C.byref(args)))
+    return q, k, v
+
+
+def gdn_gated_norm(x, z, gamma, out, eps=1e-6, stream=None):
+    """Device form of the gated norm after the recurrence: x, z, out
+    [count][value_heads][value_dim]."""
+    for t, n in ((x, "x"), (z, "z"), (gamma, "gamma"), (out, "out")):
+        _need(t, n)
+    count, value_heads, value_dim = x.shape
+    args = AiGpuGdnGatedNorm(x=_ptr(x), z=_ptr(z), gamma=_ptr(gamma), out=_ptr(out), epsilon=eps,
+                             zType=_dtype_tag(z), outType=_dtype_tag(out), count=count,
+                             valueHeads=value_heads, valueDim=value_dim, stream=_stream(stream))
+    _check(lib().aigpu_gdn_gated_norm(C.byref(args)))
     return out

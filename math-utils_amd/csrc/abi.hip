@@ -568,3 +568,50 @@ AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule* args) {
 }
 
 } // extern "C"
+
+AIGPU_ABI int aigpu_gdn_conv(const AiGpuGdnConv* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("gdn conv: null arguments"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    aigpu::GdnConvParams p{};
+    p.in = args->in;
+    p.ba = args->ba;
+    p.kernel = args->kernel;
+    p.window = args->window;
+    p.q = args->q;
+    p.k = args->k;
+    p.v = args->v;
+    p.z = args->z;
+    p.a = args->a;
+    p.b = args->b;
+    p.inType = args->inType == AIGPU_BF16 ? 1 : (args->inType == AIGPU_F32 ? 0 : 2);
+    p.outType = args->outType == AIGPU_BF16 ? 1 : (args->outType == AIGPU_F32 ? 0 : 2);
+    p.fused = args->fused ? 1 : 0;
+    p.count = args->count;
+    p.keyHeads = args->keyHeads;
+    p.valueHeads = args->valueHeads;
+    p.keyDim = args->keyDim;
+    p.valueDim = args->valueDim;
+    p.kernelSize = args->kernelSize;
+    return aigpu::launch_gdn_conv(p, as_stream(args->stream)) ? 1 : 0;
+}
+
+AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("gdn gated norm: null arguments"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    aigpu::GdnGatedNormParams p{};
+    p.x = args->x;
+    p.z = args->z;
+    p.gamma = args->gamma;
+    p.out = args->out;
+    p.eps = args->epsilon;
+    p.zType = args->zType == AIGPU_BF16 ? 1 : (args->zType == AIGPU_F32 ? 0 : 2);
+    p.outType = args->outType == AIGPU_BF16 ? 1 : (args->outType == AIGPU_F32 ? 0 : 2);
+    p.count = args->count;
+    p.valueHeads = args->valueHeads;
+    p.valueDim = args->valueDim;
+    return aigpu::launch_gdn_gated_norm(p, as_stream(args->stream)) ? 1 : 0;
+}

@@ -74,4 +74,32 @@ struct DeltaRuleParams {
 };
 bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream);
 
+// ---- Gated DeltaNet neighbours: de-interleave + causal conv, gated norm --
+struct GdnConvParams {
+    const void* in;       // plain [count][CW] or fused [count][keyHeads][2KD + 2G VD]
+    const void* ba;       // fused: [count][keyHeads][2G]
+    const float* kernel;  // [CW][kernelSize]
+    float* window;        // [kernelSize - 1][CW], in/out
+    void* q;
+    void* k;
+    void* v;
+    void* z;              // fused: [count][valueHeads][valueDim]
+    float* a;             // fused: [count][valueHeads]
+    float* b;
+    uint32_t inType, outType, fused;
+    uint64_t count, keyHeads, valueHeads, keyDim, valueDim, kernelSize;
+};
+bool launch_gdn_conv(const GdnConvParams& p, hipStream_t stream);
+
+struct GdnGatedNormParams {
+    const float* x;       // [count][valueHeads][valueDim]
+    const void* z;
+    const float* gamma;   // [valueDim]
+    void* out;
+    float eps;
+    uint32_t zType, outType;
+    uint64_t count, valueHeads, valueDim;
+};
+bool launch_gdn_gated_norm(const GdnGatedNormParams& p, hipStream_t stream);
+
 } // namespace aigpu

@@ -41,6 +41,8 @@ AIGPU_ABI int aigpu_decode_attention(const AiGpuDecode*) { return 0; }
 AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode*) { return 0; }
 AIGPU_ABI int aigpu_gated_delta_rule(const AiGpuDeltaRule*) { return 0; }
 AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule*) { return 0; }
+AIGPU_ABI int aigpu_gdn_conv(const AiGpuGdnConv*) { return 0; }
+AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm*) { return 0; }
 
 AIGPU_ABI void aigpu_profile(int) {}
 AIGPU_ABI int aigpu_profile_read(const char*, double* ms, uint64_t* n) {

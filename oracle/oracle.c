@@ -537,3 +537,77 @@ void or_gated_delta_rule(const float* q, const float* k, const float* v, const f
     else
         or_gdn_body(0, valueHeads, &c);
 }
+
+
+/* ========================================================================= //
+    Gated DeltaNet neighbours of the recurrence (include/ai/LocalModel.hpp)
+// ========================================================================= */
+
+/* siluOf, LocalModel.hpp:1369 */
+float or_silu(float x) { return x / (1.0f + expf(-x)); }
+
+/* causalConvolution, LocalModel.hpp:2678-2708: channel c of token t mixes
+   inputs t-K+1 .. t with kernel[c][0..K-1] (tap K-1 the current token),
+   reaching back into `window` ([K-1][CW], its last row the most recent input)
+   for t-K+1+j < 0, then SiLU. The window then holds the last K-1 inputs of
+   window ++ in. */
+void or_gdn_conv(const float* in, size_t count, size_t CW, size_t K, const float* kernel,
+                 float* window, float* out) {
+    for (size_t t = 0; t < count; ++t)
+        for (size_t c = 0; c < CW; ++c) {
+            float acc = 0.0f;
+            for (size_t j = 0; j < K; ++j) {
+                const long at = (long)t - (long)(K - 1) + (long)j;
+                const float xv = at >= 0 ? in[(size_t)at * CW + c] : window[(size_t)((long)K - 1 + at) * CW + c];
+                acc += kernel[c * K + j] * xv;
+            }
+            out[t * CW + c] = or_silu(acc);
+        }
+    if (K < 2) return;
+    float* next = (float*)malloc((K - 1) * CW * sizeof(float));
+    for (size_t i = 0; i < K - 1; ++i) {
+        const long at = (long)count - (long)(K - 1) + (long)i;
+        const float* src = at >= 0 ? &in[(size_t)at * CW] : &window[(size_t)((long)K - 1 + at) * CW];
+        memcpy(&next[i * CW], src, CW * sizeof(float));
+    }
+    memcpy(window, next, (K - 1) * CW * sizeof(float));
+    free(next);
+}
+
+/* the linFusedQKVZ de-interleave of gatedDeltaNetMixer, LocalModel.hpp:2739-2776.
+   fused [count][nK][2 KD + 2 G VD]: per key head its q, its k, its G value
+   heads' v, then the same heads' z; ba [count][nK][2 G]: the G heads' b,
+   then their a. Out: qkv [count][CW] (all q, all k, all v), z [count][nV][VD],
+   b, a [count][nV]. */
+void or_gdn_deinterleave(const float* fused, const float* ba, size_t count, size_t nK, size_t nV,
+                         size_t KD, size_t VD, float* qkv, float* z, float* b, float* a) {
+    const size_t G = nV / nK, KW = nK * KD, VW = nV * VD, CW = 2 * KW + VW;
+    const size_t stride = 2 * KD + 2 * G * VD, baStride = 2 * G;
+    for (size_t t = 0; t < count; ++t)
+        for (size_t kh = 0; kh < nK; ++kh) {
+            const float* head = &fused[(t * nK + kh) * stride];
+            const float* pair = &ba[(t * nK + kh) * baStride];
+            memcpy(&qkv[t * CW + kh * KD], head, KD * sizeof(float));
+            memcpy(&qkv[t * CW + KW + kh * KD], head + KD, KD * sizeof(float));
+            for (size_t j = 0; j < G; ++j) {
+                const size_t vh = kh * G + j;
+                const float* vSrc = head + 2 * KD + j * VD;
+                const float* zSrc = vSrc + G * VD;
+                memcpy(&qkv[t * CW + 2 * KW + vh * VD], vSrc, VD * sizeof(float));
+                memcpy(&z[t * VW + vh * VD], zSrc, VD * sizeof(float));
+                b[t * nV + vh] = pair[j];
+                a[t * nV + vh] = pair[G + j];
+            }
+        }
+}
+
+/* the gated norm after the recurrence, LocalModel.hpp:2833-2841: per token
+   and value head, rmsNormRow(x, gamma, VD, eps) (weight stored directly,
+   offset 0), then times siluOf(z) elementwise. x, z, out [count][nV][VD]. */
+void or_gdn_gated_norm(const float* x, const float* z, const float* gamma, float eps, float* out,
+                       size_t count, size_t nV, size_t VD) {
+    for (size_t r = 0; r < count * nV; ++r) {
+        or_rms_norm_row(&x[r * VD], gamma, &out[r * VD], VD, eps, 0.0f);
+        for (size_t d = 0; d < VD; ++d) out[r * VD + d] *= or_silu(z[r * VD + d]);
+    }
+}

@@ -35,6 +35,22 @@
                                by step; beta=0 and decay=1 special cases; one
                                token equals one deltaStep; l2norm closed form
       or_gdn_gates             closed form of softplus / sigmoid
+      or_gdn_conv              the reference's header (LocalModel.hpp) needs
+                               <format>, absent from this image's libstdc++,
+                               so it cannot be compiled into oracle/_ref.
+                               Pinned by: an fp64 per-channel convolution with
+                               asymmetric taps and a nonzero carried window;
+                               a one-hot current tap reduces to SiLU(x); and
+                               window continuity, token-by-token calls equal
+                               one call (llm-testing.cpp:853-890 checks the
+                               same of the reference's window)
+      or_gdn_deinterleave      round trip: the fused rows are built per key
+                               head by concatenation as the reference's comment
+                               states (q, k, the group's v, the group's z; b
+                               then a), and come back as the plain layout
+      or_gdn_gated_norm,
+      or_silu                  fp64 closed form; a constant row normalises to
+                               sign * gamma; SiLU(0) = 0 and SiLU(x) -> x
 */
 #ifndef ORACLE_H
 #define ORACLE_H
@@ -144,6 +160,19 @@ void or_gated_delta_rule(const float* q, const float* k, const float* v, const f
                          const float* beta, float* state, float* out, size_t count,
                          size_t keyHeads, size_t valueHeads, size_t KD, size_t VD,
                          int normalize, int threads);
+
+/* ---- Gated DeltaNet neighbours ---- */
+float or_silu(float x);                                      /* LocalModel.hpp:1369 */
+/* causalConvolution (LocalModel.hpp:2678-2708): in, out [count][CW]; kernel
+   [CW][K]; window [K-1][CW] read, then replaced by the last K-1 inputs */
+void or_gdn_conv(const float* in, size_t count, size_t CW, size_t K, const float* kernel,
+                 float* window, float* out);
+/* the linFusedQKVZ de-interleave (LocalModel.hpp:2739-2776) */
+void or_gdn_deinterleave(const float* fused, const float* ba, size_t count, size_t nK, size_t nV,
+                         size_t KD, size_t VD, float* qkv, float* z, float* b, float* a);
+/* rmsNormRow then x SiLU(z) per (token, value head) (LocalModel.hpp:2833-2841) */
+void or_gdn_gated_norm(const float* x, const float* z, const float* gamma, float eps, float* out,
+                       size_t count, size_t nV, size_t VD);
 
 /* number of threads the static pool would use given a request (<=0: all
    online CPUs in this process's affinity mask) */

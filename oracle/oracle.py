@@ -86,6 +86,11 @@ def lib():
                                      _sz, _sz, _f32p, _f32p, _f32p])
         L.or_gdn_gates.argtypes = [_f32p] * 6 + [_sz, _sz]
         L.or_gated_delta_rule.argtypes = [_f32p] * 7 + [_sz] * 5 + [C.c_int, C.c_int]
+        L.or_silu.restype = C.c_float
+        L.or_silu.argtypes = [C.c_float]
+        L.or_gdn_conv.argtypes = [_f32p, _sz, _sz, _sz, _f32p, _f32p, _f32p]
+        L.or_gdn_deinterleave.argtypes = [_f32p, _f32p] + [_sz] * 5 + [_f32p] * 4
+        L.or_gdn_gated_norm.argtypes = [_f32p, _f32p, _f32p, C.c_float, _f32p, _sz, _sz, _sz]
         L.or_threads.restype = C.c_int
         L.or_threads.argtypes = [C.c_int]
         _lib = L
@@ -294,3 +299,48 @@ def gated_delta_rule(q, k, v, g, beta, state=None, normalize=True, nthreads=1):
                               int(bool(normalize)),
                               threads(nthreads) if nthreads != 1 else 1)
     return out, st
+
+
+# ---------------------------------------------------------------- GDN neighbours
+def silu(x):
+    return lib().or_silu(float(x))
+
+
+def gdn_conv(x, kernel, window):
+    """causalConvolution (LocalModel.hpp:2678-2708) restated: x [count][CW],
+    kernel [CW][K], window [K-1][CW]; returns (out, new window)."""
+    x = np.ascontiguousarray(x, np.float32)
+    kernel = np.ascontiguousarray(kernel, np.float32)
+    win = np.ascontiguousarray(window, np.float32).copy()
+    count, CW = x.shape
+    K = kernel.shape[1]
+    out = np.empty((count, CW), np.float32)
+    lib().or_gdn_conv(x.reshape(-1), count, CW, K, kernel.reshape(-1), win.reshape(-1), out.reshape(-1))
+    return out, win
+
+
+def gdn_deinterleave(fused, ba, nK, nV, KD, VD):
+    """the linFusedQKVZ de-interleave (LocalModel.hpp:2739-2776) restated;
+    returns (qkv [count][CW], z [count][nV][VD], b, a [count][nV])."""
+    fused = np.ascontiguousarray(fused, np.float32)
+    ba = np.ascontiguousarray(ba, np.float32)
+    count = fused.shape[0]
+    CW = 2 * nK * KD + nV * VD
+    qkv = np.empty((count, CW), np.float32)
+    z = np.empty((count, nV, VD), np.float32)
+    b = np.empty((count, nV), np.float32)
+    a = np.empty((count, nV), np.float32)
+    lib().or_gdn_deinterleave(fused.reshape(-1), ba.reshape(-1), count, nK, nV, KD, VD, qkv.reshape(-1),
+                              z.reshape(-1), b.reshape(-1), a.reshape(-1))
+    return qkv, z, b, a
+
+
+def gdn_gated_norm(x, z, gamma, eps=1e-6):
+    """rmsNormRow then x SiLU(z) per (token, value head) (LocalModel.hpp:2833-2841)."""
+    x = np.ascontiguousarray(x, np.float32)
+    z = np.ascontiguousarray(z, np.float32)
+    gamma = np.ascontiguousarray(gamma, np.float32)
+    count, nV, VD = x.shape
+    out = np.empty_like(x)
+    lib().or_gdn_gated_norm(x.reshape(-1), z.reshape(-1), gamma, eps, out.reshape(-1), count, nV, VD)
+    return out

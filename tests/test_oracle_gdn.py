@@ -1,0 +1,139 @@
+"""Pins the oracle's restatement of the Gated DeltaNet neighbours of the
+recurrence (LocalModel.hpp:2678-2708 causalConvolution, :2739-2776 the fused
+qkvz de-interleave, :2833-2841 the gated norm).
+
+The reference's LocalModel.hpp needs <format>, which this image's libstdc++
+lacks, so these functions cannot be compiled into oracle/_ref; they are pinned
+by fp64 closed forms, special cases and the reference's own chunk-continuity
+property (llm-testing.cpp:853-890) instead.
+"""
+import numpy as np
+
+from oracle import oracle as O
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _conv_fp64(x, kernel, window):
+    """per-channel causal convolution written independently: the history is
+    the carried window followed by the inputs, and output t weights history
+    rows t .. t+K-1 (the last one the current token) by taps 0 .. K-1"""
+    hist = np.concatenate([window.astype(np.float64), x.astype(np.float64)])
+    K = kernel.shape[1]
+    count = x.shape[0]
+    acc = np.stack([(hist[t:t + K] * kernel.T.astype(np.float64)).sum(axis=0) for t in range(count)])
+    return acc / (1.0 + np.exp(-acc))
+
+
+def test_conv_matches_fp64_with_window_and_asymmetric_taps():
+    r = _rng(1)
+    count, CW, K = 37, 24, 4
+    x = r.standard_normal((count, CW)).astype(np.float32)
+    kernel = r.standard_normal((CW, K)).astype(np.float32)
+    window = r.standard_normal((K - 1, CW)).astype(np.float32)
+    out, nw = O.gdn_conv(x, kernel, window)
+    ref = _conv_fp64(x, kernel, window)
+    assert np.max(np.abs(out - ref)) < 2e-6 * max(1.0, np.max(np.abs(ref)))
+    np.testing.assert_array_equal(nw, x[-(K - 1):])
+    # a reversed tap order is a plausible mistake; it must not pass
+    bad = _conv_fp64(x, kernel[:, ::-1], window)
+    assert np.max(np.abs(out - bad)) > 1e-2
+
+
+def test_conv_one_hot_current_tap_is_silu():
+    r = _rng(2)
+    count, CW, K = 9, 16, 4
+    x = r.standard_normal((count, CW)).astype(np.float32) * 4
+    kernel = np.zeros((CW, K), np.float32)
+    kernel[:, K - 1] = 1.0
+    out, _ = O.gdn_conv(x, kernel, np.full((K - 1, CW), 7.0, np.float32))
+    xd = x.astype(np.float64)
+    np.testing.assert_allclose(out, xd / (1.0 + np.exp(-xd)), rtol=2e-6, atol=1e-7)
+
+
+def test_conv_window_continuity_token_by_token():
+    """one call over the prompt equals one call per token with the window
+    carried (the property llm-testing.cpp:853-890 checks of the reference)"""
+    r = _rng(3)
+    count, CW, K = 11, 20, 4
+    x = r.standard_normal((count, CW)).astype(np.float32)
+    kernel = r.standard_normal((CW, K)).astype(np.float32)
+    w0 = r.standard_normal((K - 1, CW)).astype(np.float32)
+    whole, wend = O.gdn_conv(x, kernel, w0)
+    w = w0
+    parts = []
+    for t in range(count):
+        o, w = O.gdn_conv(x[t:t + 1], kernel, w)
+        parts.append(o)
+    np.testing.assert_array_equal(np.concatenate(parts), whole)
+    np.testing.assert_array_equal(w, wend)
+
+
+def test_conv_short_call_shifts_window():
+    r = _rng(4)
+    CW, K = 8, 4
+    w0 = r.standard_normal((K - 1, CW)).astype(np.float32)
+    x = r.standard_normal((1, CW)).astype(np.float32)
+    _, nw = O.gdn_conv(x, r.standard_normal((CW, K)).astype(np.float32), w0)
+    np.testing.assert_array_equal(nw, np.concatenate([w0[1:], x]))
+
+
+def _fuse(q, k, v, z, b, a):
+    """the fused projection rows as the reference's comment lays them out:
+    per key head its q, then its k, then its group's v, then the same group's
+    z; the ba rows: the group's b, then its a"""
+    count, nK, KD = q.shape
+    nV = v.shape[1]
+    G = nV // nK
+    rows, pairs = [], []
+    for kh in range(nK):
+        grp = slice(kh * G, (kh + 1) * G)
+        rows.append(np.concatenate([q[:, kh], k[:, kh], v[:, grp].reshape(count, -1),
+                                    z[:, grp].reshape(count, -1)], axis=1))
+        pairs.append(np.concatenate([b[:, grp], a[:, grp]], axis=1))
+    return np.stack(rows, axis=1), np.stack(pairs, axis=1)
+
+
+def test_deinterleave_round_trip():
+    r = _rng(5)
+    count, nK, nV, KD, VD = 3, 2, 6, 4, 5
+    q = r.standard_normal((count, nK, KD)).astype(np.float32)
+    k = r.standard_normal((count, nK, KD)).astype(np.float32)
+    v = r.standard_normal((count, nV, VD)).astype(np.float32)
+    z = r.standard_normal((count, nV, VD)).astype(np.float32)
+    b = r.standard_normal((count, nV)).astype(np.float32)
+    a = r.standard_normal((count, nV)).astype(np.float32)
+    fused, ba = _fuse(q, k, v, z, b, a)
+    qkv, z2, b2, a2 = O.gdn_deinterleave(fused, ba, nK, nV, KD, VD)
+    KW = nK * KD
+    np.testing.assert_array_equal(qkv[:, :KW], q.reshape(count, -1))
+    np.testing.assert_array_equal(qkv[:, KW:2 * KW], k.reshape(count, -1))
+    np.testing.assert_array_equal(qkv[:, 2 * KW:], v.reshape(count, -1))
+    np.testing.assert_array_equal(z2, z)
+    np.testing.assert_array_equal(b2, b)
+    np.testing.assert_array_equal(a2, a)
+
+
+def test_gated_norm_fp64_and_constant_row():
+    r = _rng(6)
+    count, nV, VD = 4, 3, 32
+    x = r.standard_normal((count, nV, VD)).astype(np.float32)
+    z = r.standard_normal((count, nV, VD)).astype(np.float32) * 3
+    gamma = r.uniform(0.5, 1.5, VD).astype(np.float32)
+    out = O.gdn_gated_norm(x, z, gamma, 1e-6)
+    xd, zd = x.astype(np.float64), z.astype(np.float64)
+    ref = xd / np.sqrt((xd * xd).mean(-1, keepdims=True) + 1e-6) * gamma * (zd / (1 + np.exp(-zd)))
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+    # a constant row normalises to sign * gamma (eps negligible)
+    c = np.full((1, 1, VD), -2.5, np.float32)
+    zz = np.full((1, 1, VD), 30.0, np.float32)   # SiLU(30) = 30 to fp32 precision
+    out = O.gdn_gated_norm(c, zz, gamma, 1e-12)
+    np.testing.assert_allclose(out[0, 0], -gamma * 30.0, rtol=1e-6)
+
+
+def test_silu_special_values():
+    assert O.silu(0.0) == 0.0
+    assert abs(O.silu(40.0) - 40.0) < 1e-5
+    assert abs(O.silu(-40.0)) < 1e-15
