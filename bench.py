@@ -2,7 +2,7 @@
 """bench.py - throughput of the MI355X attention hot path against its roofline,
 with the reference's CPU path timed beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|delta|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|delta|gdn|all]
 
 A step is one call of the hot path over one batch of synthetic, HBM-resident
 input. The headline workload (config.workload) is configs[2] of BASELINE.json,
@@ -50,7 +50,7 @@ def parse():
     # the GPU's clock ramps over the first ~15 ms of sustained work: a short
     # warm-up times the ramp rather than the kernels
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "all"])
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of each baseline sample")
@@ -333,6 +333,80 @@ def delta_workload(args, cpu):
     return res
 
 
+def gdn_workload(args, cpu):
+    """the steps either side of the recurrence at configs[4]'s shapes: the fused
+    qkvz de-interleave + causal conv (K 4) + SiLU, then the gated norm"""
+    import numpy as np
+    import torch
+    import aigpu
+    S, HK, HV, KD, VD, K = 16384, 16, 32, 128, 128, 4
+    G = HV // HK
+    CW = 2 * HK * KD + HV * VD
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    fused = randn((S, HK, 2 * KD + 2 * G * VD), gen, torch.bfloat16)
+    ba = randn((S, HK, 2 * G), gen, torch.bfloat16)
+    kernel = torch.randn((CW, K), generator=gen, device="cuda") * 0.5
+    window = torch.zeros((K - 1, CW), dtype=torch.float32, device="cuda")
+    q = torch.empty((S, HK, KD), dtype=torch.bfloat16, device="cuda")
+    k = torch.empty_like(q)
+    v = torch.empty((S, HV, VD), dtype=torch.bfloat16, device="cuda")
+    z = torch.empty_like(v)
+    a = torch.empty((S, HV), dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    core = randn((S, HV, VD), gen, torch.float32)
+    gamma = torch.rand((VD,), generator=gen, device="cuda") + 0.5
+    normed = torch.empty((S, HV, VD), dtype=torch.bfloat16, device="cuda")
+
+    def step():
+        aigpu.gdn_conv(fused, kernel, window, q, k, v, HK, HV, KD, VD, ba=ba, z=z, a=a, b=b)
+        aigpu.gdn_gated_norm(core, z, gamma, normed)
+
+    conv_bytes = (S * HK * (2 * KD + 2 * G * VD) * 2 + S * HK * 2 * G * 2 + CW * K * 4 + 2 * (K - 1) * CW * 4 +
+                  S * CW * 2 + S * HV * VD * 2 + 2 * S * HV * 4)
+    norm_bytes = S * HV * VD * (4 + 2 + 2) + VD * 4
+    step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "gdn_conv_kernel")
+    aigpu.profile_reset()
+    aigpu.profile(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    aigpu.profile(False)
+    n_ms, n = aigpu.profile_read("gdn_gated_norm_kernel")
+    n_ms = n_ms / n if n else float("nan")
+    res = {
+        "workload": "configs[4] shapes: fused qkvz de-interleave + causal conv K=4 + SiLU (bf16 in/out), "
+                    "gated RMSNorm x SiLU(z) (fp32 x, bf16 z/out); S=16384 16k/32v heads D=128",
+        "dtype": "bf16", "unit": "GB/s", "ms_per_step": step_ms,
+        "value": (conv_bytes + norm_bytes) / (step_ms * 1e-3) / 1e9,
+        "roofline": {"kernel": "gdn_conv_kernel", "bound": "hbm",
+                     "achieved": conv_bytes / (k_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
+                     "frac": conv_bytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
+                     "kernel_ms": k_ms, "bytes_per_launch": float(conv_bytes)},
+        "gated_norm": {"kernel": "gdn_gated_norm_kernel", "bound": "hbm", "kernel_ms": n_ms,
+                       "achieved": norm_bytes / (n_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
+                       "frac": norm_bytes / (n_ms * 1e-3) / 1e9 / PEAK_HBM, "bytes_per_launch": float(norm_bytes)},
+    }
+    if cpu is not None:
+        # the C restatement (the reference's header cannot be compiled here),
+        # single-threaded as the mixer runs these loops, on the first 512 tokens
+        O = cpu[0]
+        n = 512
+        fh = fused[:n].float().cpu().numpy()
+        bh = ba[:n].float().cpu().numpy()
+        kh = kernel.cpu().numpy()
+        ch = core[:n].cpu().numpy()
+        gh = gamma.cpu().numpy()
+        t = time.perf_counter()
+        qkv, zh, _, _ = O.gdn_deinterleave(fh, bh, HK, HV, KD, VD)
+        O.gdn_conv(qkv, kh, np.zeros((K - 1, CW), np.float32))
+        O.gdn_gated_norm(ch, zh, gh, 1e-6)
+        dt = time.perf_counter() - t
+        res["cpu_baseline"] = {"value": (conv_bytes + norm_bytes) * n / S / dt / 1e9, "unit": "GB/s", "cores": 1,
+                               "kind": "port", "sample": f"the first {n} of 16384 tokens, fp32, single-threaded "
+                                                         f"({dt:.2f} s): the C restatement"}
+    return res
+
+
 def small_workloads(args):
     """configs[0] and configs[1]: launch-latency-bound, reported as measured"""
     import torch
@@ -402,10 +476,12 @@ def main():
         extra["decode"] = decode_workload(args, cpu)
     if args.workload in ("delta", "all"):
         extra["delta_rule"] = delta_workload(args, cpu)
+    if args.workload in ("gdn", "all"):
+        extra["gdn_neighbours"] = gdn_workload(args, cpu)
     if args.workload == "all":
         extra["others"] = small_workloads(args)
     if head is None:   # a single non-prefill workload becomes the line
-        head = extra.pop("decode", None) or extra.pop("delta_rule")
+        head = extra.pop("decode", None) or extra.pop("delta_rule", None) or extra.pop("gdn_neighbours")
     line = {
         "metric": "attn TFLOP/s (prefill) & KV GB/s (decode) as % roofline, 1 MI355X vs host CPU",
         "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,

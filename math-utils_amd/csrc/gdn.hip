@@ -25,102 +25,136 @@ constexpr int UNROLL = 8;  // tokens whose loads a thread has in flight together
 
 __device__ __forceinline__ float silu_of(float x) { return x / (1.0f + expf(-x)); }   // LocalModel.hpp:1369
 
-/* 4 consecutive elements at element index i of an fp32 (T = false) or bf16
+/* N (4 or 8) consecutive elements at element index i of an fp32 or bf16
    tensor, as fp32 */
-template <bool BF16>
-__device__ __forceinline__ floatx4 load4(const void* base, size_t i) {
+template <bool BF16, int N>
+__device__ __forceinline__ void loadN(const void* base, size_t i, float (&x)[N]) {
     if constexpr (BF16) {
-        const u32x2 w = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(base) + i);
-        return floatx4{__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xFFFF0000u),
-                       __uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xFFFF0000u)};
+        if constexpr (N == 8) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[2 * e] = __uint_as_float(w[e] << 16);
+                x[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+            }
+        } else {
+            const u32x2 w = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(base) + i);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                x[2 * e] = __uint_as_float(w[e] << 16);
+                x[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+            }
+        }
     } else {
-        return *reinterpret_cast<const floatx4*>(static_cast<const float*>(base) + i);
+#pragma unroll
+        for (int h = 0; h < N / 4; ++h) {
+            const floatx4 v = *reinterpret_cast<const floatx4*>(static_cast<const float*>(base) + i + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[4 * h + e] = v[e];
+        }
     }
 }
 
-template <bool BF16>
-__device__ __forceinline__ void store4(void* base, size_t i, const floatx4& x) {
+template <bool BF16, int N>
+__device__ __forceinline__ void storeN(void* base, size_t i, const float (&x)[N]) {
     if constexpr (BF16) {
-        u32x2 w;
-        w[0] = uint32_t(float_to_bf16_bits(x[0])) | (uint32_t(float_to_bf16_bits(x[1])) << 16);
-        w[1] = uint32_t(float_to_bf16_bits(x[2])) | (uint32_t(float_to_bf16_bits(x[3])) << 16);
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(base) + i) = w;
+        uint32_t w[N / 2];
+#pragma unroll
+        for (int e = 0; e < N / 2; ++e)
+            w[e] = uint32_t(float_to_bf16_bits(x[2 * e])) | (uint32_t(float_to_bf16_bits(x[2 * e + 1])) << 16);
+        if constexpr (N == 8)
+            *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i) = u32x4{w[0], w[1], w[2], w[3]};
+        else
+            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(base) + i) = u32x2{w[0], w[1]};
     } else {
-        *reinterpret_cast<floatx4*>(static_cast<float*>(base) + i) = x;
+#pragma unroll
+        for (int h = 0; h < N / 4; ++h)
+            *reinterpret_cast<floatx4*>(static_cast<float*>(base) + i + 4 * h) =
+                floatx4{x[4 * h], x[4 * h + 1], x[4 * h + 2], x[4 * h + 3]};
     }
 }
 
 struct ConvArgs {
     GdnConvParams p;
-    uint32_t KW, VW, CW, quads;   // quads: 4-channel groups of CW (+ VW for z when fused)
+    uint32_t KW, VW, CW, groups;   // groups: 8-channel groups of CW (+ VW for z, + b/a heads, fused)
 };
 
 /* element index, within the input rows, of convolution channel c (q | k | v
    order) of token t; the fused layout holds per key head q, k, the group's v
-   and the group's z (LocalModel.hpp:2739-2776) */
+   and the group's z (LocalModel.hpp:2739-2776). Split into a per-channel
+   offset and a per-token row start. */
 template <bool FUSED>
-__device__ __forceinline__ size_t in_index(const ConvArgs& a, uint64_t t, uint32_t c) {
+__device__ __forceinline__ size_t channel_offset(const ConvArgs& a, uint32_t c) {
     const GdnConvParams& p = a.p;
-    if constexpr (!FUSED) return t * a.CW + c;
+    if constexpr (!FUSED) return c;
     const uint32_t KD = uint32_t(p.keyDim), VD = uint32_t(p.valueDim);
     const uint32_t G = uint32_t(p.valueHeads / p.keyHeads);
     const size_t stride = 2 * KD + 2 * size_t(G) * VD;
-    uint32_t kh, off;
-    if (c < a.KW) {
-        kh = c / KD;
-        off = c % KD;
-    } else if (c < 2 * a.KW) {
-        kh = (c - a.KW) / KD;
-        off = KD + (c - a.KW) % KD;
-    } else {
-        const uint32_t vc = c - 2 * a.KW, vh = vc / VD;
-        kh = vh / G;
-        off = 2 * KD + (vh % G) * VD + vc % VD;
-    }
-    return (t * p.keyHeads + kh) * stride + off;
+    if (c < a.KW) return (c / KD) * stride + c % KD;
+    if (c < 2 * a.KW) return ((c - a.KW) / KD) * stride + KD + (c - a.KW) % KD;
+    const uint32_t vc = c - 2 * a.KW, vh = vc / VD;
+    return (vh / G) * stride + 2 * KD + (vh % G) * VD + vc % VD;
+}
+template <bool FUSED>
+__device__ __forceinline__ size_t row_elems(const ConvArgs& a) {
+    const GdnConvParams& p = a.p;
+    if constexpr (!FUSED) return a.CW;
+    return p.keyHeads * (2 * p.keyDim + 2 * (p.valueHeads / p.keyHeads) * p.valueDim);
 }
 
 /*
-    Thread = 4 consecutive channels x TB consecutive tokens. The K-1 previous
-    inputs of each channel stay in registers as the thread walks its tokens,
-    so every input is read once (plus a K-1 row halo per block); the first
-    block reads its halo from the carried window. Channel quads past CW copy
-    the fused layout's z rows; one more range de-interleaves b and a.
+    Thread = 8 consecutive channels x TB consecutive tokens (one 16-byte bf16
+    load per token). The K-1 previous inputs of each channel stay in registers
+    as the thread walks its tokens, so every input is read once (plus a K-1
+    row halo per block); the first block reads its halo from the carried
+    window. KT is the kernel size when fixed at compile time (4, the models'
+    value), 0 for any size up to MAXK. Channel groups past CW copy the fused
+    layout's z rows; one more range de-interleaves b and a.
 */
-template <bool IN_BF16, bool OUT_BF16, bool FUSED>
+template <bool IN_BF16, bool OUT_BF16, bool FUSED, int KT>
 __global__ __launch_bounds__(256) void gdn_conv_kernel(ConvArgs a) {
+    constexpr int CPT = 8;
+    constexpr int KM = KT ? KT : MAXK;   // register taps
     const GdnConvParams& p = a.p;
-    const uint32_t quad = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t grp = blockIdx.x * 256 + threadIdx.x;
     const uint64_t t0 = uint64_t(blockIdx.y) * TB;
-    const uint32_t K = uint32_t(p.kernelSize);
+    const uint32_t K = KT ? uint32_t(KT) : uint32_t(p.kernelSize);
     const uint64_t tEnd = t0 + TB < p.count ? t0 + TB : p.count;
-    if (quad < a.CW / 4) {
-        const uint32_t c = 4 * quad;
-        float w[4][MAXK];
+    const size_t rowE = row_elems<FUSED>(a);
+    if (grp < a.CW / CPT) {
+        const uint32_t c = CPT * grp;
+        const size_t off = channel_offset<FUSED>(a, c);
+        float w[CPT][KM];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
+        for (int e = 0; e < CPT; ++e)
 #pragma unroll
-            for (int j = 0; j < MAXK; ++j) w[e][j] = uint32_t(j) < K ? p.kernel[(c + e) * K + j] : 0.0f;
+            for (int j = 0; j < KM; ++j) w[e][j] = uint32_t(j) < K ? p.kernel[(c + e) * K + j] : 0.0f;
+        float wcur[CPT];   // the current token's tap, K - 1
+#pragma unroll
+        for (int e = 0; e < CPT; ++e) {
+            wcur[e] = w[e][0];
+#pragma unroll
+            for (int j = 1; j < KM; ++j)
+                if (uint32_t(j) == K - 1) wcur[e] = w[e][j];
+        }
         // hist[j]: input of token t - (K-1) + j, j < K-1, before token t
-        floatx4 hist[MAXK - 1];
+        float hist[KM > 1 ? KM - 1 : 1][CPT];
 #pragma unroll
-        for (int j = 0; j < MAXK - 1; ++j) {
-            hist[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < KM - 1; ++j) {
+#pragma unroll
+            for (int e = 0; e < CPT; ++e) hist[j][e] = 0.0f;
             if (uint32_t(j) < K - 1) {
                 const int64_t at = int64_t(t0) - int64_t(K - 1) + j;
-                if (at >= 0) hist[j] = load4<IN_BF16>(p.in, in_index<FUSED>(a, uint64_t(at), c));
-                else hist[j] = *reinterpret_cast<const floatx4*>(p.window + size_t(int64_t(K - 1) + at) * a.CW + c);
+                if (at >= 0) {
+                    loadN<IN_BF16, CPT>(p.in, uint64_t(at) * rowE + off, hist[j]);
+                } else {
+                    const float* src = p.window + size_t(int64_t(K - 1) + at) * a.CW + c;
+#pragma unroll
+                    for (int e = 0; e < CPT; ++e) hist[j][e] = src[e];
+                }
             }
         }
         // the dense output this channel range feeds
-        float wcur[4];   // the current token's tap, K - 1
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            wcur[e] = w[e][0];
-#pragma unroll
-            for (int j = 1; j < MAXK; ++j)
-                if (uint32_t(j) == K - 1) wcur[e] = w[e][j];
-        }
         void* dst;
         uint32_t dc, dw;
         if (c < a.KW) dst = p.q, dc = c, dw = a.KW;
@@ -129,32 +163,35 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(ConvArgs a) {
         // UNROLL tokens' loads go out together (rows past the end re-read the
         // last row), then the tokens are computed in order
         for (uint64_t tb = t0; tb < tEnd; tb += UNROLL) {
-            floatx4 xs[UNROLL];
+            float xs[UNROLL][CPT];
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u)
-                xs[u] = load4<IN_BF16>(p.in, in_index<FUSED>(a, tb + u < p.count ? tb + u : p.count - 1, c));
+                loadN<IN_BF16, CPT>(p.in, (tb + u < p.count ? tb + u : p.count - 1) * rowE + off, xs[u]);
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u) {
                 if (tb + u >= tEnd) break;   // uniform over the workgroup
-                const floatx4 x = xs[u];
-                floatx4 o;
+                float o[CPT];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
+                for (int e = 0; e < CPT; ++e) {
                     // taps in the reference's order: j = 0 (oldest) .. K-1 (current)
                     float acc = 0.0f;
 #pragma unroll
-                    for (int j = 0; j < MAXK - 1; ++j)
+                    for (int j = 0; j < KM - 1; ++j)
                         if (uint32_t(j) < K - 1) acc += w[e][j] * hist[j][e];
-                    acc += wcur[e] * x[e];
+                    acc += wcur[e] * xs[u][e];
                     o[e] = silu_of(acc);
                 }
-                store4<OUT_BF16>(dst, (tb + u) * dw + dc, o);
+                storeN<OUT_BF16, CPT>(dst, (tb + u) * dw + dc, o);
 #pragma unroll
-                for (int j = 0; j < MAXK - 2; ++j)
-                    if (uint32_t(j) + 1 < K - 1) hist[j] = hist[j + 1];
+                for (int j = 0; j + 1 < KM - 1; ++j)
+                    if (uint32_t(j) + 1 < K - 1)
 #pragma unroll
-                for (int j = 0; j < MAXK - 1; ++j)
-                    if (uint32_t(j) == K - 2) hist[j] = x;
+                        for (int e = 0; e < CPT; ++e) hist[j][e] = hist[j + 1][e];
+#pragma unroll
+                for (int j = 0; j < KM - 1; ++j)
+                    if (uint32_t(j) == K - 2)
+#pragma unroll
+                        for (int e = 0; e < CPT; ++e) hist[j][e] = xs[u][e];
             }
         }
         return;
@@ -163,23 +200,21 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(ConvArgs a) {
         const uint32_t KD = uint32_t(p.keyDim), VD = uint32_t(p.valueDim);
         const uint32_t G = uint32_t(p.valueHeads / p.keyHeads);
         const size_t stride = 2 * KD + 2 * size_t(G) * VD;
-        if (quad < (a.CW + a.VW) / 4) {   // z: copied, not convolved
-            const uint32_t zc = 4 * quad - a.CW, vh = zc / VD, kh = vh / G;
-            const size_t off = 2 * KD + size_t(G) * VD + (vh % G) * VD + zc % VD;
+        if (grp < (a.CW + a.VW) / CPT) {   // z: copied, not convolved
+            const uint32_t zc = CPT * grp - a.CW, vh = zc / VD, kh = vh / G;
+            const size_t zoff = kh * stride + 2 * KD + size_t(G) * VD + (vh % G) * VD + zc % VD;
             for (uint64_t tb = t0; tb < tEnd; tb += UNROLL) {
-                floatx4 xs[UNROLL];
-#pragma unroll
-                for (int u = 0; u < UNROLL; ++u) {
-                    const uint64_t t = tb + u < p.count ? tb + u : p.count - 1;
-                    xs[u] = load4<IN_BF16>(p.in, (t * p.keyHeads + kh) * stride + off);
-                }
+                float xs[UNROLL][CPT];
 #pragma unroll
                 for (int u = 0; u < UNROLL; ++u)
-                    if (tb + u < tEnd) store4<OUT_BF16>(p.z, (tb + u) * a.VW + zc, xs[u]);
+                    loadN<IN_BF16, CPT>(p.in, (tb + u < p.count ? tb + u : p.count - 1) * rowE + zoff, xs[u]);
+#pragma unroll
+                for (int u = 0; u < UNROLL; ++u)
+                    if (tb + u < tEnd) storeN<OUT_BF16, CPT>(p.z, (tb + u) * a.VW + zc, xs[u]);
             }
             return;
         }
-        const uint32_t vh = quad - (a.CW + a.VW) / 4;   // b, a of one value head
+        const uint32_t vh = grp - (a.CW + a.VW) / CPT;   // b, a of one value head
         if (vh < p.valueHeads) {
             const uint32_t kh = vh / G, j = vh % G;
             for (uint64_t t = t0; t < tEnd; ++t) {
@@ -200,13 +235,14 @@ __global__ __launch_bounds__(256) void gdn_window_kernel(ConvArgs a) {
     const uint32_t c = blockIdx.x * 256 + threadIdx.x;
     if (c >= a.CW) return;
     const uint32_t K = uint32_t(p.kernelSize);
+    const size_t off = channel_offset<FUSED>(a, c), rowE = row_elems<FUSED>(a);
     float next[MAXK - 1];
 #pragma unroll
     for (int i = 0; i < MAXK - 1; ++i) {
         next[i] = 0.0f;
         if (uint32_t(i) < K - 1) {
             const int64_t at = int64_t(p.count) - int64_t(K - 1) + i;
-            next[i] = at >= 0 ? load_elem(p.in, in_index<FUSED>(a, uint64_t(at), c), IN_BF16 ? 1 : 0)
+            next[i] = at >= 0 ? load_elem(p.in, uint64_t(at) * rowE + off, IN_BF16 ? 1 : 0)
                               : p.window[size_t(int64_t(K - 1) + at) * a.CW + c];
         }
     }
@@ -215,30 +251,37 @@ __global__ __launch_bounds__(256) void gdn_window_kernel(ConvArgs a) {
         if (uint32_t(i) < K - 1) p.window[size_t(i) * a.CW + c] = next[i];
 }
 
-/* one wave per (token, value head) row: rmsNormRow with the weight stored
-   directly (offset 0), then x SiLU(z) (LocalModel.hpp:2833-2841) */
-template <bool Z_BF16, bool OUT_BF16>
+/* rmsNormRow with the weight stored directly (offset 0), then x SiLU(z)
+   (LocalModel.hpp:2833-2841). LPR lanes per (token, value head) row, 4
+   elements per lane and step: a wave takes 64 / LPR rows at once, so short
+   rows (valueDim 128: 32 lanes) still use every lane. */
+template <bool Z_BF16, bool OUT_BF16, int LPR>
 __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(GdnGatedNormParams p) {
-    const uint64_t row = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    constexpr int RPW = WAVE / LPR;
     const int lane = threadIdx.x & 63;
-    if (row >= p.count * p.valueHeads) return;
+    const uint64_t row = (uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
+    const int sub = lane % LPR;
+    const bool live = row < p.count * p.valueHeads;
     const uint32_t VD = uint32_t(p.valueDim);
-    const float* x = p.x + row * VD;
+    const uint64_t r = live ? row : 0;
+    const float* x = p.x + r * VD;
     float ss = 0.0f;
-    for (uint32_t d = 4 * lane; d < VD; d += 4 * WAVE) {
+    for (uint32_t d = 4 * sub; d < VD; d += 4 * LPR) {
         const floatx4 v = *reinterpret_cast<const floatx4*>(x + d);
         ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
     }
-    ss = wave_sum(ss);
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o, WAVE);
     const float inv = 1.0f / sqrtf(ss / float(VD) + p.eps);
-    for (uint32_t d = 4 * lane; d < VD; d += 4 * WAVE) {
+    if (!live) return;
+    for (uint32_t d = 4 * sub; d < VD; d += 4 * LPR) {
         const floatx4 v = *reinterpret_cast<const floatx4*>(x + d);
         const floatx4 gm = *reinterpret_cast<const floatx4*>(p.gamma + d);
-        const floatx4 z = load4<Z_BF16>(p.z, row * VD + d);
-        floatx4 o;
+        float z[4], o[4];
+        loadN<Z_BF16, 4>(p.z, r * VD + d, z);
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = v[e] * inv * gm[e] * silu_of(z[e]);
-        store4<OUT_BF16>(p.out, row * VD + d, o);
+        storeN<OUT_BF16, 4>(p.out, r * VD + d, o);
     }
 }
 
@@ -248,18 +291,17 @@ bool launch_gdn_conv(const GdnConvParams& p, hipStream_t stream) {
     Context& ctx = Context::instance();
     if (p.inType > 1 || p.outType > 1) return ctx.fail("gdn conv: unknown tensor type");
     if (p.keyHeads == 0 || p.valueHeads % p.keyHeads) return ctx.fail("gdn conv: valueHeads must be a multiple of keyHeads");
-    if (p.keyDim == 0 || p.valueDim == 0 || p.keyDim % 4 || p.valueDim % 4)
-        return ctx.fail("gdn conv: keyDim and valueDim must be multiples of 4");
+    if (p.keyDim == 0 || p.valueDim == 0 || p.keyDim % 8 || p.valueDim % 8)
+        return ctx.fail("gdn conv: keyDim and valueDim must be multiples of 8");
     if (p.kernelSize < 1 || p.kernelSize > MAXK) return ctx.fail("gdn conv: kernel size must be 1 to 8");
     if (!p.in || !p.kernel || !p.q || !p.k || !p.v || (p.kernelSize > 1 && !p.window))
         return ctx.fail("gdn conv: null tensor");
     if (p.fused && (!p.ba || !p.z || !p.a || !p.b)) return ctx.fail("gdn conv: the fused layout needs ba, z, a and b");
     if (p.count == 0) return true;
-    auto aligned = [](const void* ptr, size_t n) { return (reinterpret_cast<uintptr_t>(ptr) % n) == 0; };
-    const size_t io = p.inType ? 8 : 16, oo = p.outType ? 8 : 16;
-    if (!aligned(p.in, io) || !aligned(p.q, oo) || !aligned(p.k, oo) || !aligned(p.v, oo) ||
-        (p.fused && !aligned(p.z, oo)) || (p.window && !aligned(p.window, 16)))
-        return ctx.fail("gdn conv: tensors must be aligned to 4 elements");
+    auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) % 16) == 0; };
+    if (!aligned(p.in) || !aligned(p.q) || !aligned(p.k) || !aligned(p.v) || (p.fused && !aligned(p.z)) ||
+        (p.window && !aligned(p.window)))
+        return ctx.fail("gdn conv: tensors must be 16-byte aligned");
     ConvArgs a{};
     a.p = p;
     const uint64_t KW = p.keyHeads * p.keyDim, VW = p.valueHeads * p.valueDim, CW = 2 * KW + VW;
@@ -267,13 +309,16 @@ bool launch_gdn_conv(const GdnConvParams& p, hipStream_t stream) {
     a.KW = uint32_t(KW);
     a.VW = uint32_t(VW);
     a.CW = uint32_t(CW);
-    a.quads = uint32_t(CW / 4 + (p.fused ? VW / 4 + (p.valueHeads + 3) / 4 * 4 : 0));
-    const dim3 grid{(a.quads + 255) / 256, unsigned((p.count + TB - 1) / TB)};
+    a.groups = uint32_t(CW / 8 + (p.fused ? VW / 8 + p.valueHeads : 0));
+    const dim3 grid{(a.groups + 255) / 256, unsigned((p.count + TB - 1) / TB)};
     if (grid.y > 65535) return ctx.fail("gdn conv: sequence too long for one call");
 #define AIGPU_CONV(I, O, F)                                                                                    \
     if (p.inType == I && p.outType == O && p.fused == F) {                                                    \
         if (!ctx.launch("gdn_conv_kernel", stream, [&] {                                                      \
-                hipLaunchKernelGGL((gdn_conv_kernel<I == 1, O == 1, F == 1>), grid, dim3(256), 0, stream, a); \
+                if (p.kernelSize == 4)                                                                        \
+                    hipLaunchKernelGGL((gdn_conv_kernel<I == 1, O == 1, F == 1, 4>), grid, dim3(256), 0, stream, a); \
+                else                                                                                          \
+                    hipLaunchKernelGGL((gdn_conv_kernel<I == 1, O == 1, F == 1, 0>), grid, dim3(256), 0, stream, a); \
             }))                                                                                               \
             return false;                                                                                     \
         if (p.kernelSize == 1) return true;                                                                   \
@@ -299,13 +344,23 @@ bool launch_gdn_gated_norm(const GdnGatedNormParams& p, hipStream_t stream) {
         !aligned(p.out, p.outType ? 8 : 16))
         return ctx.fail("gdn gated norm: tensors must be aligned to 4 elements");
     const uint64_t rows = p.count * p.valueHeads;
-    if ((rows + 3) / 4 > 0x7FFFFFFFull) return ctx.fail("gdn gated norm: too many rows");
-    const dim3 grid{unsigned((rows + 3) / 4)};
+    // lanes per row: valueDim / 4 up to a wave, a power of two dividing it
+    int lpr = 64;
+    while (lpr > 1 && (p.valueDim < 4u * lpr || p.valueDim % (4u * lpr))) lpr >>= 1;
+    if (p.valueDim / 4 >= 64) lpr = 64;
+    const uint64_t perBlock = 4ull * (WAVE / lpr);
+    if ((rows + perBlock - 1) / perBlock > 0x7FFFFFFFull) return ctx.fail("gdn gated norm: too many rows");
+    const dim3 grid{unsigned((rows + perBlock - 1) / perBlock)};
     return ctx.launch("gdn_gated_norm_kernel", stream, [&] {
-        if (p.zType == 0 && p.outType == 0) hipLaunchKernelGGL((gdn_gated_norm_kernel<false, false>), grid, dim3(256), 0, stream, p);
-        else if (p.zType == 0) hipLaunchKernelGGL((gdn_gated_norm_kernel<false, true>), grid, dim3(256), 0, stream, p);
-        else if (p.outType == 0) hipLaunchKernelGGL((gdn_gated_norm_kernel<true, false>), grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((gdn_gated_norm_kernel<true, true>), grid, dim3(256), 0, stream, p);
+#define AIGPU_NORM(L)                                                                                           \
+    if (lpr == L) {                                                                                          \
+        if (p.zType == 0 && p.outType == 0) hipLaunchKernelGGL((gdn_gated_norm_kernel<false, false, L>), grid, dim3(256), 0, stream, p); \
+        else if (p.zType == 0) hipLaunchKernelGGL((gdn_gated_norm_kernel<false, true, L>), grid, dim3(256), 0, stream, p); \
+        else if (p.outType == 0) hipLaunchKernelGGL((gdn_gated_norm_kernel<true, false, L>), grid, dim3(256), 0, stream, p); \
+        else hipLaunchKernelGGL((gdn_gated_norm_kernel<true, true, L>), grid, dim3(256), 0, stream, p); \
+    }
+        AIGPU_NORM(64) AIGPU_NORM(32) AIGPU_NORM(16) AIGPU_NORM(8) AIGPU_NORM(4) AIGPU_NORM(2) AIGPU_NORM(1)
+#undef AIGPU_NORM
     });
 }
 

@@ -77,7 +77,7 @@ def test_conv_plain_fp32(gpu, count):
 
 @pytest.mark.parametrize("K", [1, 2, 8])
 def test_conv_kernel_sizes(gpu, K):
-    ref, got, wref, wgot = run_plain(gpu, 45, 1, 2, 8, 12, K, 40 + K)
+    ref, got, wref, wgot = run_plain(gpu, 45, 1, 2, 8, 16, K, 40 + K)
     assert_f32_parity(ref, got, f"conv K={K}")
     if K > 1:
         np.testing.assert_array_equal(wgot, wref)
@@ -182,6 +182,6 @@ def test_rejects_bad_shapes(gpu):
     import aigpu
     x = dev_f32(np.zeros((4, 2 * 6 + 6), np.float32))
     q = torch_empty((4, 1, 6), False)
-    with pytest.raises(aigpu.AiGpuError, match="multiples of 4"):
+    with pytest.raises(aigpu.AiGpuError, match="multiples of 8"):
         gpu.gdn_conv(x, dev_f32(np.zeros((18, 4), np.float32)), dev_f32(np.zeros((3, 18), np.float32)),
                      q, q, torch_empty((4, 1, 6), False), 1, 1, 6, 6)
