@@ -23,7 +23,13 @@ constexpr int MAXK = 8;    // largest convolution kernel
 constexpr int TB = 32;     // tokens per convolution thread
 constexpr int UNROLL = 8;  // tokens whose loads a thread has in flight together
 
-__device__ __forceinline__ float silu_of(float x) { return x / (1.0f + expf(-x)); }   // LocalModel.hpp:1369
+/* siluOf (LocalModel.hpp:1369), x / (1 + e^-x), with the hardware exp2 and
+   reciprocal (about 2 ulp) in place of a correctly rounded exp and divide:
+   these kernels are otherwise VALU-bound on the exact forms. e^-x overflows
+   to infinity for x < -88 and the reciprocal to 0, so SiLU goes to -0 there. */
+__device__ __forceinline__ float silu_of(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * LOG2E));
+}
 
 /* N (4 or 8) consecutive elements at element index i of an fp32 or bf16
    tensor, as fp32 */

@@ -156,9 +156,10 @@ def test_conv_fused_layout(gpu, bf16):
     np.testing.assert_array_equal(host(dw), wref)
 
 
-@pytest.mark.parametrize("z_bf16,out_bf16", [(False, False), (True, True), (True, False)])
-def test_gated_norm(gpu, z_bf16, out_bf16):
-    count, nV, VD = 37, 4, 128
+@pytest.mark.parametrize("z_bf16,out_bf16,VD", [(False, False, 128), (True, True, 128), (True, False, 128),
+                                               (False, False, 48), (True, True, 256), (False, True, 264)])
+def test_gated_norm(gpu, z_bf16, out_bf16, VD):
+    count, nV = 37, 3
     x = O.fill_normal((count, nV, VD), 21, "x")
     z = O.fill_normal((count, nV, VD), 21, "z") * np.float32(2)
     if z_bf16:
