@@ -64,10 +64,13 @@ __device__ __forceinline__ void loadN(const void* base, size_t i, float (&x)[N])
 template <bool BF16, int N>
 __device__ __forceinline__ void storeN(void* base, size_t i, const float (&x)[N]) {
     if constexpr (BF16) {
+        // round to nearest even in hardware (v_cvt_pk_bf16_f32)
         uint32_t w[N / 2];
 #pragma unroll
-        for (int e = 0; e < N / 2; ++e)
-            w[e] = uint32_t(float_to_bf16_bits(x[2 * e])) | (uint32_t(float_to_bf16_bits(x[2 * e + 1])) << 16);
+        for (int e = 0; e < N / 2; ++e) {
+            typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+            w[e] = __builtin_bit_cast(uint32_t, bf16x2{__bf16(x[2 * e]), __bf16(x[2 * e + 1])});
+        }
         if constexpr (N == 8)
             *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i) = u32x4{w[0], w[1], w[2], w[3]};
         else
