@@ -359,9 +359,10 @@ __device__ __forceinline__ void lds_barrier() {
     so the 4 rows x 64 bytes a 32-lane transposed read touches hit distinct
     banks.
 */
-template <int D, int WAVES, int STAGES>
+template <int D, int WAVES, int STAGES, int BN = 64>
 __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_kernel(FlashArgs a) {
-    constexpr int BM = 32 * WAVES, BN = 64;
+    constexpr int BM = 32 * WAVES;
+    constexpr int NKB = BN / 32;          // 32-key blocks per tile
     constexpr int DB = D / 16;            // 16-deep d blocks of the S^T product
     constexpr int DT = D / 32;            // 32-row d tiles of the O^T accumulator
     constexpr int CPR = D / 8;            // 16-byte blocks per row
@@ -617,10 +618,10 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     };
 
     // S^T = K Q^T for the tile in stage J (keys from k0), masked
-    auto scores = [&](uint32_t k0, auto J, floatx16 (&s)[2]) __attribute__((always_inline)) {
+    auto scores = [&](uint32_t k0, auto J, floatx16 (&s)[NKB]) __attribute__((always_inline)) {
         const _Float16* ks = kbuf(J);
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
 #pragma unroll
@@ -633,7 +634,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                               (a.window && uint64_t(k0) + a.window < uint64_t(wPosLast) + 1);
         if (needMask) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const uint32_t key = k0 + 32 * kb + 16 * g + r;
@@ -644,10 +645,10 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
 
     // online softmax of one tile: P^T (fp16) into pk, running max and sum,
     // and O moved to the new running max
-    auto softmax = [&](floatx16 (&s)[2], half8 (&pk)[2][2]) __attribute__((always_inline)) {
+    auto softmax = [&](floatx16 (&s)[NKB], half8 (&pk)[NKB][2]) __attribute__((always_inline)) {
         float mx = -INFINITY;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
         {   // lanes l and l ^ 32 hold the two key halves of one query
@@ -662,22 +663,27 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         const float alpha = grow ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
         const float base = mn == -INFINITY ? 0.0f : mn;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) pk[kb][h][j] = _Float16(__builtin_amdgcn_exp2f(s[kb][8 * h + j] - base));
         // the row sum adds the fp16 P that the P.V product uses, in fp32
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        float ps[2] = {0.0f, 0.0f};
+        float ps[NKB];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb) ps[kb] = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int j = 0; j < 8; j += 2)
                     ps[kb] = __builtin_amdgcn_fdot2(h2{pk[kb][h][j], pk[kb][h][j + 1]}, h2{1, 1}, ps[kb], false);
-        lsum = lsum * alpha + (ps[0] + ps[1]);
+        float psum = ps[0];
+#pragma unroll
+        for (int kb = 1; kb < NKB; ++kb) psum += ps[kb];
+        lsum = lsum * alpha + psum;
         m = mn;
         if (__any(grow)) {
 #pragma unroll
@@ -688,18 +694,67 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     };
 
     // O^T += V^T P^T for the tile in stage J
-    auto pv = [&](auto J, const half8 (&pk)[2][2]) __attribute__((always_inline)) {
+    auto pv = [&](auto J, const half8 (&pk)[NKB][2]) __attribute__((always_inline)) {
         const _Float16* vs = vbuf(J);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const _Float16* a0 = vs + vaddr[dt] + (32 * kb + 8 * h) * D;
                     const half8 va = read_tr16x2(a0, a0 + 4 * D);
                     o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pk[kb][h], o[dt], 0, 0, 0);
                 }
+    };
+    // 128-key tiles: the softmax and P.V go 32 keys at a time, so only one
+    // block's P is live next to the scores (the register budget of two waves
+    // per SIMD does not hold all four at once)
+    auto softmax_pv = [&](auto J, floatx16 (&s)[NKB]) __attribute__((always_inline)) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+            mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const bool grow = mx > m + 8.0f;
+        const float mn = grow ? mx : m;
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
+        const float base = mn == -INFINITY ? 0.0f : mn;
+        m = mn;
+        if (__any(grow)) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+        }
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const _Float16* vs = vbuf(J);
+        float psum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            half8 pk[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) pk[h][j] = _Float16(__builtin_amdgcn_exp2f(s[kb][8 * h + j] - base));
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 8; j += 2)
+                    psum = __builtin_amdgcn_fdot2(h2{pk[h][j], pk[h][j + 1]}, h2{1, 1}, psum, false);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const _Float16* a0 = vs + vaddr[dt] + (32 * kb + 8 * h) * D;
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_tr16x2(a0, a0 + 4 * D), pk[h], o[dt], 0, 0, 0);
+                }
+        }
+        lsum = lsum * alpha + psum;
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
@@ -713,12 +768,16 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     // step `it` in stage it % STAGES: S, softmax, O += P V for one tile
     auto step = [&](uint32_t it, auto J) __attribute__((always_inline)) -> bool {
         if (it >= ntiles) return false;
-        floatx16 s[2];
-        half8 pk[2][2];
+        floatx16 s[NKB];
         sync(it, J);
         scores(kbeg + it * BN, J, s);
-        softmax(s, pk);
-        pv(J, pk);
+        if constexpr (NKB > 2) {
+            softmax_pv(J, s);
+        } else {
+            half8 pk[NKB][2];
+            softmax(s, pk);
+            pv(J, pk);
+        }
         return true;
     };
     for (uint32_t it = 0;; it += STAGES) {
@@ -858,6 +917,13 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
         const char* env = std::getenv("AIGPU_PREFILL_WAVES");
         return env && std::atoi(env) == 4 ? 4 : 8;
     }();
+    // 8-wave workgroups take 128-key tiles in two stages (half the barriers
+    // and DMA rounds of 64-key tiles, 4% faster at configs[2]);
+    // AIGPU_PREFILL_BN=64 selects 64-key tiles in AIGPU_PREFILL_STAGES stages
+    static const int bn = [] {
+        const char* env = std::getenv("AIGPU_PREFILL_BN");
+        return waves == 8 && !(env && std::atoi(env) == 64) ? 128 : 64;
+    }();
     static const int stages = [] {
         const char* env = std::getenv("AIGPU_PREFILL_STAGES");
         const int n = env ? std::atoi(env) : 3;
@@ -869,11 +935,15 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     return ctx.launch("prefill_flash_kernel", stream, [&] {
         const dim3 grid{unsigned(blocks)}, block{unsigned(64 * waves)};
 #define AIGPU_FLASH(DD, WV, ST) \
-    if (p.dim == DD && waves == WV && stages == ST) \
+    if (p.dim == DD && waves == WV && stages == ST && bn == 64) \
         hipLaunchKernelGGL((prefill_flash_kernel<DD, WV, ST>), grid, block, 0, stream, a)
         AIGPU_FLASH(128, 8, 2); AIGPU_FLASH(128, 8, 3); AIGPU_FLASH(128, 8, 4); AIGPU_FLASH(128, 4, 2);
         AIGPU_FLASH(64, 8, 2); AIGPU_FLASH(64, 8, 3); AIGPU_FLASH(64, 8, 4); AIGPU_FLASH(64, 4, 2);
 #undef AIGPU_FLASH
+        if (bn == 128 && p.dim == 128 && waves == 8)
+            hipLaunchKernelGGL((prefill_flash_kernel<128, 8, 2, 128>), grid, block, 0, stream, a);
+        if (bn == 128 && p.dim == 64 && waves == 8)
+            hipLaunchKernelGGL((prefill_flash_kernel<64, 8, 2, 128>), grid, block, 0, stream, a);
     });
 }
 
