@@ -770,7 +770,11 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         if (it >= ntiles) return false;
         floatx16 s[NKB];
         sync(it, J);
-        scores(kbeg + it * BN, J, s);
+        // a tile wholly after this wave's last row (or before the window of its
+        // first) adds nothing to it: the wave only keeps the barrier and DMA
+        const uint32_t k0 = kbeg + it * BN;
+        if (k0 > wPosLast || (a.window && uint64_t(k0) + BN - 1 + a.window <= uint64_t(wPosFirst))) return true;
+        scores(k0, J, s);
         if constexpr (NKB > 2) {
             softmax_pv(J, s);
         } else {
