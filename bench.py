@@ -35,12 +35,12 @@ PEAK_MFMA_F32 = 157.3       # TFLOP/s, fp32
 PEAK_HBM = 8000.0           # GB/s
 CPU_THREADS_CAP = 16        # the GPU box's CPU share for one GPU
 
-# HBM bytes per launch of prefill_flash_kernel<128, 8, 3> on configs[2]:
+# HBM bytes per launch of prefill_flash_kernel<128, 8, 2, 128> on configs[2]:
 # rocprofv3 FETCH_SIZE and WRITE_SIZE passes, each scaled by what the same
 # counter reads for a 1 GiB device copy (fetch x2.000, write x1.000):
-# 183.8 MB read + 134.3 MB written (profiles/prefill_flash_kernel_cfg3_hbm_traffic.md).
+# 185.1 MB read + 158.3 MB written (profiles/prefill_flash_kernel_cfg3_hbm_traffic.md).
 # Re-measure when the kernel changes.
-PREFILL_FLASH_TRAFFIC = 318.0e6
+PREFILL_FLASH_TRAFFIC = 343.4e6
 
 
 def parse():
