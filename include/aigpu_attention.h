@@ -132,6 +132,9 @@ typedef struct AiGpuPrefill {
     float normOffset;         /* spec.normWeightOffset (0 for qwen3) */
     uint32_t rotaryDims;
     uint32_t inType;
+    uint32_t outputGate;      /* 1: out *= sigmoid(q[.. + dim + d]), the gate half of each q row
+                                 (spec.attnOutputGate, LocalModel.hpp:2660-2665); needs qStride >= 2 dim */
+    uint32_t reserved;
     uint64_t count, start, heads, kvHeads, dim, qStride, window, capacity;
     void* stream;
 } AiGpuPrefill;
@@ -166,7 +169,7 @@ typedef struct AiGpuDecode {
     uint32_t rotaryDims;
     uint32_t inType;
     uint32_t maxPosition;     /* >= every positions[b]; sizes the launch */
-    uint32_t reserved;
+    uint32_t outputGate;      /* as AiGpuPrefill::outputGate */
     uint64_t batch, heads, kvHeads, dim, qStride, window, capacity;
     uint64_t batchStride;     /* elements between sequences' caches; 0 = kvHeads*capacity*dim */
     void* stream;

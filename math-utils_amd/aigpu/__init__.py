@@ -45,6 +45,7 @@ class AiGpuPrefill(C.Structure):
                 ("keyCache", _vp), ("valueCache", _vp),
                 ("qNorm", _vp), ("kNorm", _vp), ("rotaryFrequencies", _vp),
                 ("epsilon", _f32), ("normOffset", _f32), ("rotaryDims", _u32), ("inType", _u32),
+                ("outputGate", _u32), ("reserved", _u32),
                 ("count", _u64), ("start", _u64), ("heads", _u64), ("kvHeads", _u64),
                 ("dim", _u64), ("qStride", _u64), ("window", _u64), ("capacity", _u64),
                 ("stream", _vp)]
@@ -55,7 +56,7 @@ class AiGpuDecode(C.Structure):
                 ("keyCache", _vp), ("valueCache", _vp), ("positions", _vp),
                 ("qNorm", _vp), ("kNorm", _vp), ("rotaryFrequencies", _vp),
                 ("epsilon", _f32), ("normOffset", _f32), ("rotaryDims", _u32), ("inType", _u32),
-                ("maxPosition", _u32), ("reserved", _u32),
+                ("maxPosition", _u32), ("outputGate", _u32),
                 ("batch", _u64), ("heads", _u64), ("kvHeads", _u64), ("dim", _u64),
                 ("qStride", _u64), ("window", _u64), ("capacity", _u64), ("batchStride", _u64),
                 ("stream", _vp)]
@@ -257,8 +258,9 @@ def attention_device(q, keys, values, out, count, start, heads, kv_heads, dim, q
 
 def prefill(q, k, v, out, key_cache, value_cache, start, heads, kv_heads, dim, q_stride=None,
             q_norm=None, k_norm=None, eps=1e-6, norm_offset=0.0, freqs=None, rotary_dims=0,
-            window=0, capacity=None, stream=None):
-    """Device form of attentionMixer for `count` tokens at positions start.."""
+            window=0, capacity=None, output_gate=False, stream=None):
+    """Device form of attentionMixer for `count` tokens at positions start..;
+    output_gate applies sigmoid of each q row's second half (q_stride >= 2 dim)."""
     for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out"), (key_cache, "key_cache"),
                  (value_cache, "value_cache"), (q_norm, "q_norm"), (k_norm, "k_norm"),
                  (freqs, "freqs")):
@@ -269,7 +271,7 @@ def prefill(q, k, v, out, key_cache, value_cache, start, heads, kv_heads, dim, q
                      valueCache=_ptr(value_cache), qNorm=_ptr(q_norm), kNorm=_ptr(k_norm),
                      rotaryFrequencies=_ptr(freqs), epsilon=eps, normOffset=norm_offset,
                      rotaryDims=rotary_dims if freqs is not None else 0, inType=_dtype_tag(q),
-                     count=count, start=start, heads=heads, kvHeads=kv_heads, dim=dim,
+                     outputGate=1 if output_gate else 0, count=count, start=start, heads=heads, kvHeads=kv_heads, dim=dim,
                      qStride=q_stride or dim, window=window, capacity=cap,
                      stream=_stream(stream))
     _check(lib().aigpu_prefill_attention(C.byref(a)))
@@ -278,7 +280,7 @@ def prefill(q, k, v, out, key_cache, value_cache, start, heads, kv_heads, dim, q
 
 def decode(q, k, v, out, key_cache, value_cache, positions, max_position, heads, kv_heads, dim,
            q_stride=None, q_norm=None, k_norm=None, eps=1e-6, norm_offset=0.0, freqs=None,
-           rotary_dims=0, window=0, capacity=None, batch_stride=0, stream=None):
+           rotary_dims=0, window=0, capacity=None, batch_stride=0, output_gate=False, stream=None):
     """Device form of the batched decode; positions is a uint32/int32 GPU tensor."""
     for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out"), (key_cache, "key_cache"),
                  (value_cache, "value_cache"), (positions, "positions"), (q_norm, "q_norm"),
@@ -290,7 +292,8 @@ def decode(q, k, v, out, key_cache, value_cache, positions, max_position, heads,
                     valueCache=_ptr(value_cache), positions=_ptr(positions), qNorm=_ptr(q_norm),
                     kNorm=_ptr(k_norm), rotaryFrequencies=_ptr(freqs), epsilon=eps,
                     normOffset=norm_offset, rotaryDims=rotary_dims if freqs is not None else 0,
-                    inType=_dtype_tag(q), maxPosition=max_position, batch=batch, heads=heads,
+                    inType=_dtype_tag(q), maxPosition=max_position, outputGate=1 if output_gate else 0,
+                    batch=batch, heads=heads,
                     kvHeads=kv_heads, dim=dim, qStride=q_stride or dim, window=window,
                     capacity=cap, batchStride=batch_stride, stream=_stream(stream))
     _check(lib().aigpu_decode_attention(C.byref(a)))

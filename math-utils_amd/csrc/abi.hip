@@ -366,6 +366,7 @@ static aigpu::PrefillParams prefill_params(const AiGpuPrefill* a) {
     p.normOffset = a->normOffset;
     p.rotaryDims = int(a->rotaryDims);
     p.inType = int(a->inType);
+    p.outputGate = a->outputGate ? 1 : 0;
     p.count = a->count;
     p.start = a->start;
     p.heads = a->heads;
@@ -434,6 +435,7 @@ static aigpu::DecodeParams decode_params(const AiGpuDecode* a) {
     p.normOffset = a->normOffset;
     p.rotaryDims = int(a->rotaryDims);
     p.inType = int(a->inType);
+    p.outputGate = a->outputGate ? 1 : 0;
     p.maxPosition = a->maxPosition;
     p.batch = a->batch;
     p.heads = a->heads;

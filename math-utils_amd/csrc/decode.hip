@@ -64,6 +64,14 @@ __host__ __device__ constexpr int record_floats(int D) { return 2 * MAXG + MAXG 
    snew[MAXG] and its value row vnew[D] in fp32 */
 __host__ __device__ constexpr int qrec_words(int D) { return (D / 32) * 64 * 4 + MAXG + D; }
 
+/* the attention output of (sequence b, head h, column d), times sigmoid of the
+   gate half of its q row when the output gate is on (LocalModel.hpp:2660-2665) */
+__device__ __forceinline__ float gated(const DecodeParams& p, uint32_t b, uint32_t h, uint32_t d, float x) {
+    if (!p.outputGate) return x;
+    const float gt = load_elem(p.q, (size_t(b) * p.heads + h) * p.qStride + p.dim + d, p.inType);
+    return x * (1.0f / (1.0f + expf(-gt)));
+}
+
 __device__ __forceinline__ uint32_t first_position(const DecodeParams& p, uint32_t L) {
     return (p.window && uint64_t(L) + 1 > p.window) ? uint32_t(uint64_t(L) + 1 - p.window) : 0u;
 }
@@ -415,7 +423,7 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) 
                 at += f * vnewG[d];
             }
             if (nChunks == 1) {
-                outRow[h * D + d] = at / lt;
+                outRow[h * D + d] = gated(p, b, kvh * G + h, d, at / lt);
             } else {
                 rec[2 * MAXG + h * D + d] = at;
                 if (d == 0) {
@@ -495,7 +503,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 #pragma unroll
     for (int k = 0; k < (MAXG * D + 255) / 256; ++k) {
         const uint32_t idx = tid + 256 * k;
-        if (idx < G * D) outRow[idx] = acc[k] / Lh[idx / D];
+        if (idx < G * D) outRow[idx] = gated(p, b, kvh * G + idx / D, idx % D, acc[k] / Lh[idx / D]);
     }
 }
 
@@ -512,6 +520,7 @@ bool launch_decode(const DecodeParams& p, hipStream_t stream) {
     if (p.kvHeads == 0 || p.heads % p.kvHeads) return ctx.fail("decode: heads must be a multiple of kvHeads");
     if (p.heads / p.kvHeads > MAXG) return ctx.fail("decode: at most 8 query heads per kv head");
     if (p.qStride < p.dim) return ctx.fail("decode: qStride < dim");
+    if (p.outputGate && p.qStride < 2 * p.dim) return ctx.fail("decode: the output gate needs qStride >= 2 dim");
     if (p.freqs && (p.rotaryDims == 0 || p.rotaryDims > int(p.dim) || (p.rotaryDims & 1)))
         return ctx.fail("decode: rotaryDims must be even and within dim");
     if (p.inType != 0 && p.inType != 1) return ctx.fail("decode: unknown input type");

@@ -32,7 +32,7 @@ struct PrefillParams {
     const float* kNorm;
     const float* freqs;
     float eps, normOffset;
-    int rotaryDims, inType;
+    int rotaryDims, inType, outputGate;
     uint64_t count, start, heads, kvHeads, dim, qStride, window, capacity;
 };
 bool launch_prefill(const PrefillParams& p, hipStream_t stream);
@@ -50,7 +50,7 @@ struct DecodeParams {
     const float* kNorm;
     const float* freqs;
     float eps, normOffset;
-    int rotaryDims, inType;
+    int rotaryDims, inType, outputGate;
     uint32_t maxPosition;
     uint64_t batch, heads, kvHeads, dim, qStride, window, capacity, batchStride;
 };

@@ -293,6 +293,7 @@ struct FlashArgs {
     const float* rope;   // [count][2][half] cos, sin of each token, or null
     float eps, normOffset, qScale;
     uint32_t qStride, inType, half, fuseQ;
+    uint32_t outputGate;   // out *= sigmoid(qraw[row + D + d]) (LocalModel.hpp:2660-2665)
 };
 
 typedef __fp16 fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
@@ -797,6 +798,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     if (rowValid) {
         const float inv = 1.0f / lsum;
         float* dst = a.out + (size_t(tq) * a.heads + head) * D;
+        const size_t gateRow = (size_t(tq) * a.heads + head) * a.qStride + D;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -804,6 +806,13 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                 floatx4 val;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) val[i] = o[dt][4 * r4 + i] * inv;
+                if (a.outputGate) {   // sigmoidOf (LocalModel.hpp:1371) of the row's gate half
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float gt = load_elem(a.qraw, gateRow + 32 * dt + 8 * r4 + 4 * g + i, int(a.inType));
+                        val[i] *= 1.0f / (1.0f + expf(-gt));
+                    }
+                }
                 *reinterpret_cast<floatx4*>(dst + 32 * dt + 8 * r4 + 4 * g) = val;
             }
     }
@@ -816,6 +825,7 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     if (p.dim != 64 && p.dim != 128) return ctx.fail("prefill: dim must be 64 or 128");
     if (p.kvHeads == 0 || p.heads % p.kvHeads) return ctx.fail("prefill: heads must be a multiple of kvHeads");
     if (p.qStride < p.dim) return ctx.fail("prefill: qStride < dim");
+    if (p.outputGate && p.qStride < 2 * p.dim) return ctx.fail("prefill: the output gate needs qStride >= 2 dim");
     if (p.freqs && (p.rotaryDims == 0 || p.rotaryDims > int(p.dim) || (p.rotaryDims & 1)))
         return ctx.fail("prefill: rotaryDims must be even and within dim");
     if (p.inType != 0 && p.inType != 1) return ctx.fail("prefill: unknown input type");
@@ -915,6 +925,7 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     a.qStride = uint32_t(p.qStride);
     a.inType = uint32_t(p.inType);
     a.half = p.freqs ? uint32_t(p.rotaryDims / 2) : 0u;
+    a.outputGate = p.outputGate ? 1u : 0u;
     // AIGPU_PREFILL_WAVES / AIGPU_PREFILL_STAGES pick the tiling (tuning);
     // 4-wave workgroups run two per CU and take two stages
     static const int waves = [] {

@@ -611,3 +611,14 @@ void or_gdn_gated_norm(const float* x, const float* z, const float* gamma, float
         for (size_t d = 0; d < VD; ++d) out[r * VD + d] *= or_silu(z[r * VD + d]);
     }
 }
+
+/* the attention output gate of attentionMixer, LocalModel.hpp:2660-2665:
+   out[t][h][d] *= sigmoidOf(q[(t heads + h) qStride + dim + d]) */
+void or_output_gate(float* out, const float* q, size_t count, size_t heads, size_t dim, size_t qStride) {
+    for (size_t t = 0; t < count; ++t)
+        for (size_t h = 0; h < heads; ++h) {
+            const float* g = &q[(t * heads + h) * qStride + dim];
+            float* o = &out[(t * heads + h) * dim];
+            for (size_t d = 0; d < dim; ++d) o[d] *= or_sigmoid(g[d]);
+        }
+}

@@ -51,6 +51,9 @@
       or_gdn_gated_norm,
       or_silu                  fp64 closed form; a constant row normalises to
                                sign * gamma; SiLU(0) = 0 and SiLU(x) -> x
+      or_output_gate           fp64 closed form; a zero gate halves the output,
+                               a large one leaves it, and only the second half
+                               of each q row is read
 */
 #ifndef ORACLE_H
 #define ORACLE_H
@@ -173,6 +176,10 @@ void or_gdn_deinterleave(const float* fused, const float* ba, size_t count, size
 /* rmsNormRow then x SiLU(z) per (token, value head) (LocalModel.hpp:2833-2841) */
 void or_gdn_gated_norm(const float* x, const float* z, const float* gamma, float eps, float* out,
                        size_t count, size_t nV, size_t VD);
+
+/* attentionMixer's output gate (LocalModel.hpp:2660-2665): out [count][heads][dim]
+   times sigmoid of the second dim elements of each q row (qStride >= 2 dim) */
+void or_output_gate(float* out, const float* q, size_t count, size_t heads, size_t dim, size_t qStride);
 
 /* number of threads the static pool would use given a request (<=0: all
    online CPUs in this process's affinity mask) */

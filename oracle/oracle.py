@@ -91,6 +91,7 @@ def lib():
         L.or_gdn_conv.argtypes = [_f32p, _sz, _sz, _sz, _f32p, _f32p, _f32p]
         L.or_gdn_deinterleave.argtypes = [_f32p, _f32p] + [_sz] * 5 + [_f32p] * 4
         L.or_gdn_gated_norm.argtypes = [_f32p, _f32p, _f32p, C.c_float, _f32p, _sz, _sz, _sz]
+        L.or_output_gate.argtypes = [_f32p, _f32p, _sz, _sz, _sz, _sz]
         L.or_threads.restype = C.c_int
         L.or_threads.argtypes = [C.c_int]
         _lib = L
@@ -344,3 +345,12 @@ def gdn_gated_norm(x, z, gamma, eps=1e-6):
     out = np.empty_like(x)
     lib().or_gdn_gated_norm(x.reshape(-1), z.reshape(-1), gamma, eps, out.reshape(-1), count, nV, VD)
     return out
+
+
+def output_gate(out, q, heads, dim, q_stride):
+    """attentionMixer's output gate (LocalModel.hpp:2660-2665) restated: returns
+    out [count][heads][dim] times sigmoid of each q row's second half."""
+    o = np.ascontiguousarray(out, np.float32).copy()
+    q = np.ascontiguousarray(q, np.float32)
+    lib().or_output_gate(o.reshape(-1), q.reshape(-1), o.shape[0], heads, dim, q_stride)
+    return o

@@ -12,7 +12,7 @@ pytestmark = pytest.mark.gpu
 
 
 def run_decode(gpu, lengths, H, KV, D, seed, norm=True, rope=True, window=0, dtype="bf16",
-               cap=None, theta=1e6, q_stride=None, check_cache=False):
+               cap=None, theta=1e6, q_stride=None, check_cache=False, gate=False):
     import torch
     B = len(lengths)
     qs = q_stride or D
@@ -42,7 +42,10 @@ def run_decode(gpu, lengths, H, KV, D, seed, norm=True, rope=True, window=0, dty
         qn, kn = O.qk_norm_rope(q[b:b + 1], k[b:b + 1], 1, L, H, KV, D, qs, gq, gk, 1e-6, fr, D)
         keys = np.concatenate([hk.transpose(1, 0, 2), kn], 0)
         vals = np.concatenate([hv.transpose(1, 0, 2), v[b:b + 1]], 0)
-        refs.append(O.attention(qn, keys, vals, 1, L, H, KV, D, qs, window, nthreads=0)[0])
+        att = O.attention(qn, keys, vals, 1, L, H, KV, D, qs, window, nthreads=0)
+        if gate:   # attentionMixer's output gate (LocalModel.hpp:2660-2665)
+            att = O.output_gate(att, q[b:b + 1], H, D, qs)
+        refs.append(att[0])
         refs[-1] = (refs[-1], kn[0])
     key_cache, value_cache = dev_bf16(kc), dev_bf16(vc)
     pos = dev_u32(np.array(lengths, np.uint32))
@@ -51,7 +54,8 @@ def run_decode(gpu, lengths, H, KV, D, seed, norm=True, rope=True, window=0, dty
     gpu.decode(dq, dk, dv, out, key_cache, value_cache, pos, max(lengths), H, KV, D, q_stride=qs,
                q_norm=None if gq is None else dev_f32(gq),
                k_norm=None if gk is None else dev_f32(gk),
-               freqs=None if fr is None else dev_f32(fr), rotary_dims=D, window=window)
+               freqs=None if fr is None else dev_f32(fr), rotary_dims=D, window=window,
+               output_gate=gate)
     got = host(out)
     ref = np.stack([r[0] for r in refs])
     if check_cache:
@@ -146,3 +150,11 @@ def test_prefill_then_decode_shares_the_cache(gpu):
     vals = np.concatenate([hist_v, v[P:]], 0)
     ref = O.attention(qn, keys, vals, 1, P, H, KV, D, D)
     assert_bf16_parity(ref, host(out1), "prefill -> decode")
+
+
+@pytest.mark.parametrize("lengths", [[40], [3000, 17, 700]])
+def test_output_gate(gpu, lengths):
+    """the output gate on both write paths: one-chunk sequences (attention
+    kernel) and multi-chunk ones (merge kernel)"""
+    ref, got = run_decode(gpu, lengths, 8, 2, 128, 91, q_stride=256, gate=True)
+    assert_bf16_parity(ref, got, f"gate {lengths}")

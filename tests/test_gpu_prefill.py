@@ -12,7 +12,7 @@ pytestmark = pytest.mark.gpu
 
 
 def run_case(gpu, count, start, H, KV, D, seed, norm=True, rope=True, window=0, dtype="bf16",
-             rows=None, theta=1e6, q_stride=None, rot=None):
+             rows=None, theta=1e6, q_stride=None, rot=None, gate=False):
     """Builds seeded inputs, runs the GPU prefill and the oracle; returns
     (oracle out, gpu out, oracle-normed keys, gpu caches)."""
     import torch
@@ -47,13 +47,17 @@ def run_case(gpu, count, start, H, KV, D, seed, norm=True, rope=True, window=0, 
     vals = np.concatenate([hv.transpose(1, 0, 2), v], 0)
     ref = O.attention_strided(qn, keys, vals, count, start, H, KV, D, qs, KV * D, D, window,
                               rows=rows, nthreads=0)
+    if gate:   # attentionMixer's output gate: the raw second half of each q row
+        assert rows is None
+        ref = O.output_gate(ref, q, H, D, qs)
 
     out = torch.zeros((count, H, D), dtype=torch.float32, device="cuda")
     say("prefill", dict(count=count, start=start, H=H, KV=KV, D=D, window=window, dtype=dtype))
     gpu.prefill(dq, dk, dv, out, key_cache, value_cache, start, H, KV, D, q_stride=qs,
                 q_norm=None if gq is None else dev_f32(gq),
                 k_norm=None if gk is None else dev_f32(gk),
-                freqs=None if fr is None else dev_f32(fr), rotary_dims=rot, window=window)
+                freqs=None if fr is None else dev_f32(fr), rotary_dims=rot, window=window,
+                output_gate=gate)
     got = host(out)
     if rows is not None:
         got = got[rows]
@@ -139,3 +143,17 @@ def test_rejects_unsupported_dim(gpu):
         gpu.prefill(x, x, x, out, kc, kc, 0, 2, 2, 96)
     assert "dim" in gpu.last_error()
     assert errors(np.ones(2), np.ones(2))["rel_l2"] == 0
+
+
+@pytest.mark.parametrize("dtype,D", [("bf16", 128), ("f32", 64), ("bf16", 64)])
+def test_output_gate(gpu, dtype, D):
+    """Qwen3.5's attnOutputGate (LocalModel.hpp:2660-2665): q rows of 2 D,
+    the second half gating the output through a sigmoid"""
+    ref, got, *_ = run_case(gpu, 150, 20, 8, 2, D, 77, dtype=dtype, q_stride=2 * D, gate=True)
+    assert_bf16_parity(ref, got, f"gate {dtype} D={D}")
+
+
+def test_output_gate_needs_wide_rows(gpu):
+    import aigpu
+    with pytest.raises(aigpu.AiGpuError, match="output gate"):
+        run_case(gpu, 4, 0, 2, 1, 64, 78, q_stride=64, gate=True)

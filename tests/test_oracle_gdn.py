@@ -137,3 +137,22 @@ def test_silu_special_values():
     assert O.silu(0.0) == 0.0
     assert abs(O.silu(40.0) - 40.0) < 1e-5
     assert abs(O.silu(-40.0)) < 1e-15
+
+
+def test_output_gate_closed_form():
+    """attentionMixer's output gate (LocalModel.hpp:2660-2665)"""
+    r = _rng(7)
+    count, H, D, qs = 5, 3, 8, 20
+    out = r.standard_normal((count, H, D)).astype(np.float32)
+    q = r.standard_normal((count, H, qs)).astype(np.float32)
+    got = O.output_gate(out, q, H, D, qs)
+    g = q[:, :, D:2 * D].astype(np.float64)
+    np.testing.assert_allclose(got, out * (1 / (1 + np.exp(-g))), rtol=1e-6)
+    # only the gate half is read: changing the query half or the tail changes nothing
+    q2 = q.copy()
+    q2[:, :, :D] = 123.0
+    q2[:, :, 2 * D:] = -77.0
+    np.testing.assert_array_equal(O.output_gate(out, q2, H, D, qs), got)
+    zero = q.copy()
+    zero[:, :, D:2 * D] = 0.0
+    np.testing.assert_array_equal(O.output_gate(out, zero, H, D, qs), out * np.float32(0.5))
