@@ -210,6 +210,26 @@ AIGPU_ABI int aigpu_gated_delta_rule(const AiGpuDeltaRule* args);
 AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule* args);
 
 /* ------------------------------------------------------------------------ */
+/* 5b. Kimi Delta Attention's recurrence (kimiDeltaMixer,                    */
+/*     LocalModel.hpp:2928-2947): the gated delta rule with one decay per    */
+/*     KEY CHANNEL, deltaStep(perKeyDecay = true) (Kernels.hpp:105-128).     */
+/* ------------------------------------------------------------------------ */
+typedef struct AiGpuKda {
+    const void* q;            /* [count][keyHeads][keyDim], inType */
+    const void* k;            /* [count][keyHeads][keyDim], inType */
+    const void* v;            /* [count][valueHeads][valueDim], inType */
+    const float* g;           /* [count][valueHeads][keyDim] log decay (decay = exp(g) <= 1) */
+    const float* beta;        /* [count][valueHeads] */
+    float* state;             /* [valueHeads][keyDim][valueDim] fp32, in/out */
+    float* out;               /* [count][valueHeads][valueDim] fp32 */
+    uint32_t inType;
+    uint32_t normalize;       /* 1: l2normalise q,k (eps 1e-6) and q *= 1/sqrt(keyDim) */
+    uint64_t count, keyHeads, valueHeads, keyDim, valueDim;
+    void* stream;
+} AiGpuKda;
+AIGPU_ABI int aigpu_kda_rule(const AiGpuKda* args);
+
+/* ------------------------------------------------------------------------ */
 /* 6. The Gated DeltaNet steps either side of the recurrence                 */
 /*    (gatedDeltaNetMixer, LocalModel.hpp:2724-2844). No reference kernel    */
 /*    exists for them: the mixer runs them inline on the host.               */

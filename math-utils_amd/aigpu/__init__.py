@@ -71,6 +71,13 @@ class AiGpuDeltaRule(C.Structure):
                 ("valueDim", _u64), ("stream", _vp)]
 
 
+class AiGpuKda(C.Structure):
+    _fields_ = [("q", _vp), ("k", _vp), ("v", _vp), ("g", _vp), ("beta", _vp), ("state", _vp), ("out", _vp),
+                ("inType", _u32), ("normalize", _u32),
+                ("count", _u64), ("keyHeads", _u64), ("valueHeads", _u64), ("keyDim", _u64),
+                ("valueDim", _u64), ("stream", _vp)]
+
+
 class AiGpuGdnConv(C.Structure):
     _fields_ = [("in_", _vp), ("ba", _vp), ("kernel", _vp), ("window", _vp), ("q", _vp), ("k", _vp),
                 ("v", _vp), ("z", _vp), ("a", _vp), ("b", _vp),
@@ -108,6 +115,7 @@ SIGNATURES = {
     "aigpu_decode_attention": (C.c_int, [C.POINTER(AiGpuDecode)]),
     "aigpu_decode_attention_host": (C.c_int, [C.POINTER(AiGpuDecode)]),
     "aigpu_gdn_conv": (C.c_int, [C.POINTER(AiGpuGdnConv)]),
+    "aigpu_kda_rule": (C.c_int, [C.POINTER(AiGpuKda)]),
     "aigpu_gdn_gated_norm": (C.c_int, [C.POINTER(AiGpuGdnGatedNorm)]),
     "aigpu_gated_delta_rule": (C.c_int, [C.POINTER(AiGpuDeltaRule)]),
     "aigpu_gated_delta_rule_host": (C.c_int, [C.POINTER(AiGpuDeltaRule)]),
@@ -346,4 +354,19 @@ def gdn_gated_norm(x, z, gamma, out, eps=1e-6, stream=None):
                              zType=_dtype_tag(z), outType=_dtype_tag(out), count=count,
                              valueHeads=value_heads, valueDim=value_dim, stream=_stream(stream))
     _check(lib().aigpu_gdn_gated_norm(C.byref(args)))
+    return out
+
+
+def kda_rule(q, k, v, g, beta, state, out, normalize=True, stream=None):
+    """Device form of Kimi Delta Attention's recurrence: g is the log decay per
+    key channel [count][value_heads][key_dim]; state updated in place."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta"), (state, "state"), (out, "out")):
+        _need(t, n)
+    count, key_heads, key_dim = q.shape
+    _, value_heads, value_dim = v.shape
+    args = AiGpuKda(q=_ptr(q), k=_ptr(k), v=_ptr(v), g=_ptr(g), beta=_ptr(beta), state=_ptr(state),
+                    out=_ptr(out), inType=_dtype_tag(q), normalize=1 if normalize else 0, count=count,
+                    keyHeads=key_heads, valueHeads=value_heads, keyDim=key_dim, valueDim=value_dim,
+                    stream=_stream(stream))
+    _check(lib().aigpu_kda_rule(C.byref(args)))
     return out

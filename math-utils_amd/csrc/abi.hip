@@ -617,3 +617,26 @@ AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm* args) {
     p.valueDim = args->valueDim;
     return aigpu::launch_gdn_gated_norm(p, as_stream(args->stream)) ? 1 : 0;
 }
+
+AIGPU_ABI int aigpu_kda_rule(const AiGpuKda* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("kda: null arguments"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    aigpu::KdaParams p{};
+    p.q = args->q;
+    p.k = args->k;
+    p.v = args->v;
+    p.g = args->g;
+    p.beta = args->beta;
+    p.state = args->state;
+    p.out = args->out;
+    p.inType = int(args->inType);
+    p.normalize = args->normalize ? 1 : 0;
+    p.count = args->count;
+    p.keyHeads = args->keyHeads;
+    p.valueHeads = args->valueHeads;
+    p.keyDim = args->keyDim;
+    p.valueDim = args->valueDim;
+    return aigpu::launch_kda(p, as_stream(args->stream)) ? 1 : 0;
+}

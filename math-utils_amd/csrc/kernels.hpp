@@ -74,6 +74,20 @@ struct DeltaRuleParams {
 };
 bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream);
 
+// ---- Kimi Delta Attention: the delta rule with per-key-channel decay ----
+struct KdaParams {
+    const void* q;        // [count][keyHeads][keyDim], inType
+    const void* k;
+    const void* v;        // [count][valueHeads][valueDim], inType
+    const float* g;       // [count][valueHeads][keyDim] log decay per key channel
+    const float* beta;    // [count][valueHeads]
+    float* state;         // [valueHeads][keyDim][valueDim]
+    float* out;           // [count][valueHeads][valueDim]
+    int inType, normalize;
+    uint64_t count, keyHeads, valueHeads, keyDim, valueDim;
+};
+bool launch_kda(const KdaParams& p, hipStream_t stream);
+
 // ---- Gated DeltaNet neighbours: de-interleave + causal conv, gated norm --
 struct GdnConvParams {
     const void* in;       // plain [count][CW] or fused [count][keyHeads][2KD + 2G VD]

@@ -42,6 +42,7 @@ AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode*) { return 0; }
 AIGPU_ABI int aigpu_gated_delta_rule(const AiGpuDeltaRule*) { return 0; }
 AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule*) { return 0; }
 AIGPU_ABI int aigpu_gdn_conv(const AiGpuGdnConv*) { return 0; }
+AIGPU_ABI int aigpu_kda_rule(const AiGpuKda*) { return 0; }
 AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm*) { return 0; }
 
 AIGPU_ABI void aigpu_profile(int) {}

@@ -495,8 +495,10 @@ typedef struct {
     int normalize;
 } or_gdn_ctx;
 
-/* LocalModel.hpp:2802-2830, restricted to value heads [begin, end) */
-static void or_gdn_body(size_t begin, size_t end, void* p) {
+/* LocalModel.hpp:2802-2830, restricted to value heads [begin, end); with
+   perKey set, the decay is one per key channel, g [count][valueHeads][KD] as
+   kimiDeltaMixer's loop (LocalModel.hpp:2928-2947) */
+static void or_gdn_body_impl(size_t begin, size_t end, void* p, int perKey) {
     const or_gdn_ctx* c = (const or_gdn_ctx*)p;
     const size_t KD = c->KD, VD = c->VD, nV = c->valueHeads;
     const size_t group = c->valueHeads / c->keyHeads;
@@ -504,6 +506,7 @@ static void or_gdn_body(size_t begin, size_t end, void* p) {
     float* kh = (float*)malloc(sizeof(float) * KD);
     float* kv = (float*)malloc(sizeof(float) * VD);
     float* delta = (float*)malloc(sizeof(float) * VD);
+    float* decays = (float*)malloc(sizeof(float) * KD);
     const float qScale = 1.0f / sqrtf((float)KD);
     for (size_t t = 0; t < c->count; ++t) {
         for (size_t vHead = begin; vHead < end; ++vHead) {
@@ -515,16 +518,34 @@ static void or_gdn_body(size_t begin, size_t end, void* p) {
                 or_l2normalise(kh, KD, 1e-6f);
                 for (size_t i = 0; i < KD; ++i) qh[i] *= qScale;
             }
-            const float decay = expf(c->g[t * nV + vHead]);
             const float beta = c->beta[t * nV + vHead];
-            or_delta_step(c->state + vHead * KD * VD, kh, qh, c->v + (t * nV + vHead) * VD, &decay,
-                          0, beta, KD, VD, c->out + (t * nV + vHead) * VD, kv, delta);
+            if (perKey) {
+                for (size_t i = 0; i < KD; ++i) decays[i] = expf(c->g[(t * nV + vHead) * KD + i]);
+            } else {
+                decays[0] = expf(c->g[t * nV + vHead]);
+            }
+            or_delta_step(c->state + vHead * KD * VD, kh, qh, c->v + (t * nV + vHead) * VD, decays,
+                          perKey, beta, KD, VD, c->out + (t * nV + vHead) * VD, kv, delta);
         }
     }
+    free(decays);
     free(qh);
     free(kh);
     free(kv);
     free(delta);
+}
+
+static void or_gdn_body(size_t begin, size_t end, void* p) { or_gdn_body_impl(begin, end, p, 0); }
+static void or_kda_body(size_t begin, size_t end, void* p) { or_gdn_body_impl(begin, end, p, 1); }
+
+void or_kda_rule(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                 float* state, float* out, size_t count, size_t keyHeads, size_t valueHeads, size_t KD,
+                 size_t VD, int normalize, int threads) {
+    or_gdn_ctx c = {q, k, v, g, beta, state, out, count, keyHeads, valueHeads, KD, VD, normalize};
+    if (threads > 1)
+        or_pool_run(valueHeads, threads, or_kda_body, &c);
+    else
+        or_kda_body(0, valueHeads, &c);
 }
 
 void or_gated_delta_rule(const float* q, const float* k, const float* v, const float* g,

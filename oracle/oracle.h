@@ -35,6 +35,10 @@
                                by step; beta=0 and decay=1 special cases; one
                                token equals one deltaStep; l2norm closed form
       or_gdn_gates             closed form of softplus / sigmoid
+      or_kda_rule              bit-compared against the reference's deltaStep
+                               with perKeyDecay driven token by token
+                               (ref_kda_rule in oracle/_ref); equal decays in
+                               every channel reduce it to or_gated_delta_rule
       or_gdn_conv              the reference's header (LocalModel.hpp) needs
                                <format>, absent from this image's libstdc++,
                                so it cannot be compiled into oracle/_ref.
@@ -180,6 +184,13 @@ void or_gdn_gated_norm(const float* x, const float* z, const float* gamma, float
 /* attentionMixer's output gate (LocalModel.hpp:2660-2665): out [count][heads][dim]
    times sigmoid of the second dim elements of each q row (qStride >= 2 dim) */
 void or_output_gate(float* out, const float* q, size_t count, size_t heads, size_t dim, size_t qStride);
+
+/* Kimi Delta Attention's recurrence (kimiDeltaMixer, LocalModel.hpp:2928-2947):
+   as or_gated_delta_rule, but the decay is one per key channel: g is the log
+   decay [count][valueHeads][KD], and deltaStep runs with perKeyDecay */
+void or_kda_rule(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                 float* state, float* out, size_t count, size_t keyHeads, size_t valueHeads, size_t KD,
+                 size_t VD, int normalize, int threads);
 
 /* number of threads the static pool would use given a request (<=0: all
    online CPUs in this process's affinity mask) */

@@ -92,6 +92,7 @@ def lib():
         L.or_gdn_deinterleave.argtypes = [_f32p, _f32p] + [_sz] * 5 + [_f32p] * 4
         L.or_gdn_gated_norm.argtypes = [_f32p, _f32p, _f32p, C.c_float, _f32p, _sz, _sz, _sz]
         L.or_output_gate.argtypes = [_f32p, _f32p, _sz, _sz, _sz, _sz]
+        L.or_kda_rule.argtypes = [_f32p] * 7 + [_sz] * 5 + [C.c_int, C.c_int]
         L.or_threads.restype = C.c_int
         L.or_threads.argtypes = [C.c_int]
         _lib = L
@@ -115,6 +116,7 @@ def ref():
         R.ref_dot.argtypes = [_f32p, _f32p, C.c_uint64]
         R.ref_random.argtypes = [C.c_uint64, C.c_int, C.c_uint64, C.c_double, C.c_double, C.c_void_p]
         R.ref_gated_delta_rule.argtypes = [_f32p] * 7 + [C.c_uint64] * 5 + [C.c_int]
+        R.ref_kda_rule.argtypes = [_f32p] * 7 + [C.c_uint64] * 5 + [C.c_int]
         _ref = R
     return _ref
 
@@ -354,3 +356,39 @@ def output_gate(out, q, heads, dim, q_stride):
     q = np.ascontiguousarray(q, np.float32)
     lib().or_output_gate(o.reshape(-1), q.reshape(-1), o.shape[0], heads, dim, q_stride)
     return o
+
+
+def _kda_args(q, k, v, g, beta, state):
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    S, Hk, KD = q.shape
+    _, Hv, VD = v.shape
+    st = (np.zeros((Hv, KD, VD), np.float32) if state is None
+          else np.ascontiguousarray(state, np.float32).copy())
+    g = np.ascontiguousarray(g, np.float32).reshape(S, Hv, KD)
+    beta = np.ascontiguousarray(beta, np.float32).reshape(S, Hv)
+    return q, k, v, g, beta, st, S, Hk, Hv, KD, VD
+
+
+def kda_rule(q, k, v, g, beta, state=None, normalize=True, nthreads=1):
+    """kimiDeltaMixer's recurrence restated: per-key-channel log decay g
+    [S][Hv][KD]; returns (out [S][Hv][VD], final state)."""
+    q, k, v, g, beta, st, S, Hk, Hv, KD, VD = _kda_args(q, k, v, g, beta, state)
+    out = np.zeros((S, Hv, VD), np.float32)
+    lib().or_kda_rule(q.reshape(-1), k.reshape(-1), v.reshape(-1), g.reshape(-1), beta.reshape(-1),
+                      st.reshape(-1), out.reshape(-1), S, Hk, Hv, KD, VD, int(bool(normalize)),
+                      threads(nthreads) if nthreads != 1 else 1)
+    return out, st
+
+
+def ref_kda_rule(q, k, v, g, beta, state=None, normalize=True):
+    """the reference's deltaStep (perKeyDecay) driven token by token (oracle/_ref)"""
+    R = ref()
+    if R is None:
+        raise RuntimeError("oracle/_ref is not built")
+    q, k, v, g, beta, st, S, Hk, Hv, KD, VD = _kda_args(q, k, v, g, beta, state)
+    out = np.zeros((S, Hv, VD), np.float32)
+    R.ref_kda_rule(q.reshape(-1), k.reshape(-1), v.reshape(-1), g.reshape(-1), beta.reshape(-1),
+                   st.reshape(-1), out.reshape(-1), S, Hk, Hv, KD, VD, int(bool(normalize)))
+    return out, st

@@ -106,3 +106,37 @@ void ref_random(uint64_t seed, int kind, uint64_t n, double lo, double hi, void*
 }
 
 } // extern "C"
+
+extern "C" {
+/* kimiDeltaMixer's per-head token loop (LocalModel.hpp:2928-2947) around the
+   reference's own deltaStep with perKeyDecay: g is the log decay per key
+   channel [count][valueHeads][KD]; normalisation as ref_gated_delta_rule */
+void ref_kda_rule(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                  float* state, float* out, uint64_t count, uint64_t keyHeads, uint64_t valueHeads,
+                  uint64_t KD, uint64_t VD, int normalize) {
+    std::vector<float> qh(KD), kh(KD), prediction(VD), delta(VD), decay(KD);
+    const uint64_t group = valueHeads / keyHeads;
+    const float qScale = 1.0f / std::sqrt(float(KD));
+    auto l2 = [](float* x, uint64_t n) {
+        float sum = 0.0f;
+        for (uint64_t i = 0; i < n; ++i) sum += x[i] * x[i];
+        const float inv = 1.0f / std::sqrt(sum + 1e-6f);
+        for (uint64_t i = 0; i < n; ++i) x[i] *= inv;
+    };
+    for (uint64_t t = 0; t < count; ++t)
+        for (uint64_t h = 0; h < valueHeads; ++h) {
+            const uint64_t kHead = h / group;
+            std::memcpy(qh.data(), q + (t * keyHeads + kHead) * KD, sizeof(float) * KD);
+            std::memcpy(kh.data(), k + (t * keyHeads + kHead) * KD, sizeof(float) * KD);
+            if (normalize) {
+                l2(qh.data(), KD);
+                l2(kh.data(), KD);
+                for (uint64_t i = 0; i < KD; ++i) qh[i] *= qScale;
+            }
+            for (uint64_t i = 0; i < KD; ++i) decay[i] = std::exp(g[(t * valueHeads + h) * KD + i]);
+            ai::kernels::deltaStep(state + h * KD * VD, kh.data(), qh.data(), v + (t * valueHeads + h) * VD,
+                                   decay.data(), true, beta[t * valueHeads + h], KD, VD,
+                                   out + (t * valueHeads + h) * VD, prediction.data(), delta.data());
+        }
+}
+}

@@ -336,6 +336,31 @@ def test_gated_delta_rule_matches_reference_delta_step_loop():
     assert np.array_equal(ro, po) and np.array_equal(rs, ps)
 
 
+def _kda_decays(S, hv, kd, seed):
+    return -np.log1p(np.exp(O.fill_normal((S, hv, kd), seed, "gk").astype(np.float64))).astype(np.float32)
+
+
+def test_kda_rule_matches_reference_delta_step_loop():
+    """Kimi Delta Attention's loop (per-key-channel decay) equals the
+    reference's deltaStep with perKeyDecay driven token by token, bit for bit"""
+    if O.ref() is None:
+        pytest.skip("oracle/_ref not built (reference checkout absent)")
+    q, k, v, _, beta = _gdn_inputs(200, 2, 4, 64, 32, 14)
+    g = _kda_decays(200, 4, 64, 14)
+    s0 = O.fill_normal((4, 64, 32), 14, "s0")
+    ro, rs = O.ref_kda_rule(q, k, v, g, beta, state=s0)
+    po, ps = O.kda_rule(q, k, v, g, beta, state=s0)
+    assert np.array_equal(ro, po) and np.array_equal(rs, ps)
+
+
+def test_kda_rule_with_equal_channel_decays_is_the_gated_rule():
+    q, k, v, g, beta = _gdn_inputs(90, 2, 4, 32, 16, 15)
+    gk = np.repeat(g[:, :, None], 32, axis=2)
+    o1, s1 = O.kda_rule(q, k, v, gk, beta)
+    o2, s2 = O.gated_delta_rule(q, k, v, g, beta)
+    assert np.array_equal(o1, o2) and np.array_equal(s1, s2)
+
+
 def test_gated_delta_rule_is_repeated_delta_step():
     S, hk, hv, kd, vd = 7, 2, 4, 16, 8
     q, k, v, g, beta = _gdn_inputs(S, hk, hv, kd, vd, 12)
