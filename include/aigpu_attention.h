@@ -220,6 +220,15 @@ typedef struct AiGpuKda {
     const void* v;            /* [count][valueHeads][valueDim], inType */
     const float* g;           /* [count][valueHeads][keyDim] log decay (decay = exp(g) <= 1) */
     const float* beta;        /* [count][valueHeads] */
+    /* raw gates, used when g and beta are NULL (LocalModel.hpp:2894-2905):  */
+    /*   g = safeGate ? lowerBound sigmoid(exp(aLog) (f + dtBias))            */
+    /*                : -exp(aLog) softplus(f + dtBias),  beta = sigmoid(b)   */
+    const float* f;           /* [count][valueHeads][keyDim] decay projection (f_b output) */
+    const float* b;           /* [count][valueHeads] write-strength projection */
+    const float* aLog;        /* [valueHeads] */
+    const float* dtBias;      /* [valueHeads][keyDim] */
+    float lowerBound;         /* LocalConfig::linLowerBound, <= 0 */
+    uint32_t safeGate;        /* LocalConfig::linSafeGate */
     float* state;             /* [valueHeads][keyDim][valueDim] fp32, in/out */
     float* out;               /* [count][valueHeads][valueDim] fp32 */
     uint32_t inType;
@@ -259,14 +268,15 @@ typedef struct AiGpuGdnConv {
 AIGPU_ABI int aigpu_gdn_conv(const AiGpuGdnConv* args);
 
 /* rmsNormRow of each (token, value head) row of the recurrence output, its  */
-/* weight stored directly, then times SiLU(z) (LocalModel.hpp:2833-2841)     */
+/* weight stored directly, then times SiLU(z) (LocalModel.hpp:2833-2841), or */
+/* with gateKind 1 times sigmoid(z), kimiDeltaMixer's form (:2936-2945)      */
 typedef struct AiGpuGdnGatedNorm {
     const float* x;           /* [count][valueHeads][valueDim] fp32 */
     const void* z;            /* [count][valueHeads][valueDim], zType */
     const float* gamma;       /* [valueDim] (LocalLayer::linNorm) */
     void* out;                /* [count][valueHeads][valueDim], outType */
     float epsilon;            /* LocalConfig::normEps */
-    uint32_t zType, outType, reserved;
+    uint32_t zType, outType, gateKind; /* gateKind 0: SiLU, 1: sigmoid */
     uint64_t count, valueHeads, valueDim;
     void* stream;
 } AiGpuGdnGatedNorm;

@@ -72,8 +72,9 @@ class AiGpuDeltaRule(C.Structure):
 
 
 class AiGpuKda(C.Structure):
-    _fields_ = [("q", _vp), ("k", _vp), ("v", _vp), ("g", _vp), ("beta", _vp), ("state", _vp), ("out", _vp),
-                ("inType", _u32), ("normalize", _u32),
+    _fields_ = [("q", _vp), ("k", _vp), ("v", _vp), ("g", _vp), ("beta", _vp),
+                ("f", _vp), ("b", _vp), ("aLog", _vp), ("dtBias", _vp), ("lowerBound", _f32), ("safeGate", _u32),
+                ("state", _vp), ("out", _vp), ("inType", _u32), ("normalize", _u32),
                 ("count", _u64), ("keyHeads", _u64), ("valueHeads", _u64), ("keyDim", _u64),
                 ("valueDim", _u64), ("stream", _vp)]
 
@@ -88,7 +89,7 @@ class AiGpuGdnConv(C.Structure):
 
 class AiGpuGdnGatedNorm(C.Structure):
     _fields_ = [("x", _vp), ("z", _vp), ("gamma", _vp), ("out", _vp), ("epsilon", C.c_float),
-                ("zType", _u32), ("outType", _u32), ("reserved", _u32),
+                ("zType", _u32), ("outType", _u32), ("gateKind", _u32),
                 ("count", _u64), ("valueHeads", _u64), ("valueDim", _u64), ("stream", _vp)]
 
 
@@ -344,27 +345,36 @@ def gdn_conv(x, kernel, window, q, k, v, key_heads, value_heads, key_dim, value_
     return q, k, v
 
 
-def gdn_gated_norm(x, z, gamma, out, eps=1e-6, stream=None):
+def gdn_gated_norm(x, z, gamma, out, eps=1e-6, gate="silu", stream=None):
     """Device form of the gated norm after the recurrence: x, z, out
-    [count][value_heads][value_dim]."""
+    [count][value_heads][value_dim]; gate "silu" (Gated DeltaNet) or
+    "sigmoid" (Kimi Delta Attention)."""
+    if gate not in ("silu", "sigmoid"):
+        raise ValueError("gate must be 'silu' or 'sigmoid'")
     for t, n in ((x, "x"), (z, "z"), (gamma, "gamma"), (out, "out")):
         _need(t, n)
     count, value_heads, value_dim = x.shape
     args = AiGpuGdnGatedNorm(x=_ptr(x), z=_ptr(z), gamma=_ptr(gamma), out=_ptr(out), epsilon=eps,
-                             zType=_dtype_tag(z), outType=_dtype_tag(out), count=count,
+                             zType=_dtype_tag(z), outType=_dtype_tag(out),
+                             gateKind=1 if gate == "sigmoid" else 0, count=count,
                              valueHeads=value_heads, valueDim=value_dim, stream=_stream(stream))
     _check(lib().aigpu_gdn_gated_norm(C.byref(args)))
     return out
 
 
-def kda_rule(q, k, v, g, beta, state, out, normalize=True, stream=None):
+def kda_rule(q, k, v, g, beta, state, out, normalize=True, f=None, b=None, a_log=None, dt_bias=None,
+             safe_gate=False, lower_bound=-5.0, stream=None):
     """Device form of Kimi Delta Attention's recurrence: g is the log decay per
-    key channel [count][value_heads][key_dim]; state updated in place."""
-    for t, n in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta"), (state, "state"), (out, "out")):
+    key channel [count][value_heads][key_dim] (or g, beta None and the raw
+    gates f, b, a_log, dt_bias given); state updated in place."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta"), (f, "f"), (b, "b"), (a_log, "a_log"),
+                 (dt_bias, "dt_bias"), (state, "state"), (out, "out")):
         _need(t, n)
     count, key_heads, key_dim = q.shape
     _, value_heads, value_dim = v.shape
-    args = AiGpuKda(q=_ptr(q), k=_ptr(k), v=_ptr(v), g=_ptr(g), beta=_ptr(beta), state=_ptr(state),
+    args = AiGpuKda(q=_ptr(q), k=_ptr(k), v=_ptr(v), g=_ptr(g), beta=_ptr(beta), f=_ptr(f), b=_ptr(b),
+                    aLog=_ptr(a_log), dtBias=_ptr(dt_bias), lowerBound=lower_bound,
+                    safeGate=1 if safe_gate else 0, state=_ptr(state),
                     out=_ptr(out), inType=_dtype_tag(q), normalize=1 if normalize else 0, count=count,
                     keyHeads=key_heads, valueHeads=value_heads, keyDim=key_dim, valueDim=value_dim,
                     stream=_stream(stream))

@@ -612,6 +612,8 @@ AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm* args) {
     p.eps = args->epsilon;
     p.zType = args->zType == AIGPU_BF16 ? 1 : (args->zType == AIGPU_F32 ? 0 : 2);
     p.outType = args->outType == AIGPU_BF16 ? 1 : (args->outType == AIGPU_F32 ? 0 : 2);
+    if (args->gateKind > 1) return ctx.fail("gdn gated norm: gateKind must be 0 (SiLU) or 1 (sigmoid)"), 0;
+    p.sigmoidGate = args->gateKind;
     p.count = args->count;
     p.valueHeads = args->valueHeads;
     p.valueDim = args->valueDim;
@@ -629,6 +631,12 @@ AIGPU_ABI int aigpu_kda_rule(const AiGpuKda* args) {
     p.v = args->v;
     p.g = args->g;
     p.beta = args->beta;
+    p.f = args->f;
+    p.b = args->b;
+    p.aLog = args->aLog;
+    p.dtBias = args->dtBias;
+    p.lowerBound = args->lowerBound;
+    p.safeGate = args->safeGate ? 1 : 0;
     p.state = args->state;
     p.out = args->out;
     p.inType = int(args->inType);

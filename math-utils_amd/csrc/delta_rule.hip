@@ -64,8 +64,6 @@ struct DeltaArgs {
     uint32_t vec;      // q, k, v 16-byte aligned: vector loads
 };
 
-__device__ __forceinline__ float softplus_of(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
-__device__ __forceinline__ float sigmoid_of(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 /* raw bits of 16 bytes of input starting at element i: 8 bf16 or 4 f32;
    one vector load when the tensor is 16-byte aligned */

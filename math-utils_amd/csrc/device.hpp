@@ -37,6 +37,10 @@ __device__ __forceinline__ float load_elem(const void* base, size_t i, int type)
 }
 
 /* wave64 butterflies */
+/* softplusOf and sigmoidOf (LocalModel.hpp:1371-1376) with the library exp */
+__device__ __forceinline__ float softplus_of(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float sigmoid_of(float x) { return 1.0f / (1.0f + expf(-x)); }
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, WAVE);

@@ -10,7 +10,8 @@
 //   gdn_window_kernel      the carried window (the last K-1 inputs), after
 //                          the convolution has read the old one
 //   gdn_gated_norm_kernel  rmsNormRow of each (token, value head) row times
-//                          SiLU(z) (:2833-2841)
+//                          SiLU(z) (:2833-2841), or times sigmoid(z) as
+//                          kimiDeltaMixer gates its rows (:2936-2945)
 #include "context.hpp"
 #include "device.hpp"
 #include "kernels.hpp"
@@ -27,9 +28,10 @@ constexpr int UNROLL = 8;  // tokens whose loads a thread has in flight together
    reciprocal (about 2 ulp) in place of a correctly rounded exp and divide:
    these kernels are otherwise VALU-bound on the exact forms. e^-x overflows
    to infinity for x < -88 and the reciprocal to 0, so SiLU goes to -0 there. */
-__device__ __forceinline__ float silu_of(float x) {
-    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * LOG2E));
+__device__ __forceinline__ float fast_sigmoid(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * LOG2E));
 }
+__device__ __forceinline__ float silu_of(float x) { return x * fast_sigmoid(x); }
 
 /* N (4 or 8) consecutive elements at element index i of an fp32 or bf16
    tensor, as fp32 */
@@ -289,7 +291,10 @@ __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(GdnGatedNormParams 
         float z[4], o[4];
         loadN<Z_BF16, 4>(p.z, r * VD + d, z);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = v[e] * inv * gm[e] * silu_of(z[e]);
+        for (int e = 0; e < 4; ++e) {
+            const float s = fast_sigmoid(z[e]);
+            o[e] = v[e] * inv * gm[e] * (p.sigmoidGate ? s : z[e] * s);
+        }
         storeN<OUT_BF16, 4>(p.out, r * VD + d, o);
     }
 }

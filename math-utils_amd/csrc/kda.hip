@@ -110,13 +110,34 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
             kn[r * KS + qq * PE + e] *= kinv;
             qn[r * KS + qq * PE + e] *= qinv;
         }
-        if (tid < CH) bet[tid] = uint32_t(tid) < n ? p.beta[(t0 + tid) * p.valueHeads + h] : 0.0f;
+        if (tid < CH) {
+            float bt = 0.0f;
+            if (uint32_t(tid) < n) {
+                const size_t i = (t0 + tid) * p.valueHeads + h;
+                bt = p.beta ? p.beta[i] : sigmoid_of(p.b[i]);
+            }
+            bet[tid] = bt;
+        }
     }
-    // ---- cumulative log decay of each channel over the chunk ----
+    // ---- cumulative log decay of each channel over the chunk; raw gates
+    //      become log decays as LocalModel.hpp:2894-2905 computes them ----
     if (tid < KD) {
+        const bool raw = p.g == nullptr;
+        const float rate = raw ? expf(p.aLog[h]) : 0.0f;
+        const float bias = raw ? p.dtBias[size_t(h) * KD + tid] : 0.0f;
         float acc = 0.0f;
         for (int r = 0; r < CH; ++r) {
-            if (uint32_t(r) < n) acc += p.g[((t0 + r) * p.valueHeads + h) * KD + tid];
+            if (uint32_t(r) < n) {
+                const size_t i = ((t0 + r) * p.valueHeads + h) * KD + tid;
+                float gt;
+                if (!raw) {
+                    gt = p.g[i];
+                } else {
+                    const float f = p.f[i] + bias;
+                    gt = p.safeGate ? p.lowerBound * sigmoid_of(rate * f) : -rate * softplus_of(f);
+                }
+                acc += gt;
+            }
             gc[r * KS + tid] = acc;
         }
     }
@@ -371,7 +392,11 @@ bool launch_kda(const KdaParams& p, hipStream_t stream) {
     if (p.valueDim == 0 || p.valueDim % NB) return ctx.fail("kda: valueDim must be a multiple of 16");
     if (p.keyHeads == 0 || p.valueHeads % p.keyHeads) return ctx.fail("kda: valueHeads must be a multiple of keyHeads");
     if (p.inType != 0 && p.inType != 1) return ctx.fail("kda: unknown input type");
-    if (!p.q || !p.k || !p.v || !p.g || !p.beta || !p.state || !p.out) return ctx.fail("kda: null tensor");
+    if (!p.q || !p.k || !p.v || !p.state || !p.out) return ctx.fail("kda: null tensor");
+    if (!p.g != !p.beta) return ctx.fail("kda: give g and beta together, or neither (raw gates)");
+    if (!p.g && (!p.f || !p.b || !p.aLog || !p.dtBias))
+        return ctx.fail("kda: raw gates need f, b, aLog and dtBias");
+    if (!p.g && p.safeGate && !(p.lowerBound <= 0.0f)) return ctx.fail("kda: lowerBound must be <= 0");
     if (p.count == 0) return true;
     KdaArgs a{};
     a.p = p;

@@ -81,6 +81,12 @@ struct KdaParams {
     const void* v;        // [count][valueHeads][valueDim], inType
     const float* g;       // [count][valueHeads][keyDim] log decay per key channel
     const float* beta;    // [count][valueHeads]
+    const float* f;       // raw gates instead of g/beta: [count][valueHeads][keyDim]
+    const float* b;       // [count][valueHeads]
+    const float* aLog;    // [valueHeads]
+    const float* dtBias;  // [valueHeads][keyDim]
+    float lowerBound;
+    int safeGate;
     float* state;         // [valueHeads][keyDim][valueDim]
     float* out;           // [count][valueHeads][valueDim]
     int inType, normalize;
@@ -112,6 +118,7 @@ struct GdnGatedNormParams {
     void* out;
     float eps;
     uint32_t zType, outType;
+    uint32_t sigmoidGate;  // 0: x SiLU(z) (Gated DeltaNet), 1: x sigmoid(z) (Kimi)
     uint64_t count, valueHeads, valueDim;
 };
 bool launch_gdn_gated_norm(const GdnGatedNormParams& p, hipStream_t stream);

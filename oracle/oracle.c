@@ -624,13 +624,31 @@ void or_gdn_deinterleave(const float* fused, const float* ba, size_t count, size
 
 /* the gated norm after the recurrence, LocalModel.hpp:2833-2841: per token
    and value head, rmsNormRow(x, gamma, VD, eps) (weight stored directly,
-   offset 0), then times siluOf(z) elementwise. x, z, out [count][nV][VD]. */
+   offset 0), then times siluOf(z) elementwise; kimiDeltaMixer (:2936-2945)
+   multiplies by sigmoidOf(z) instead. x, z, out [count][nV][VD]. */
 void or_gdn_gated_norm(const float* x, const float* z, const float* gamma, float eps, float* out,
-                       size_t count, size_t nV, size_t VD) {
+                       size_t count, size_t nV, size_t VD, int sigmoidGate) {
     for (size_t r = 0; r < count * nV; ++r) {
         or_rms_norm_row(&x[r * VD], gamma, &out[r * VD], VD, eps, 0.0f);
-        for (size_t d = 0; d < VD; ++d) out[r * VD + d] *= or_silu(z[r * VD + d]);
+        for (size_t d = 0; d < VD; ++d)
+            out[r * VD + d] *= sigmoidGate ? or_sigmoid(z[r * VD + d]) : or_silu(z[r * VD + d]);
     }
+}
+
+/* kimiDeltaMixer's gate loop, LocalModel.hpp:2894-2905, kept as the log
+   decay g (the reference goes on to store exp(g)) */
+void or_kda_gates(const float* f, const float* b, const float* aLog, const float* dtBias, int safeGate,
+                  float lowerBound, float* g, float* beta, size_t count, size_t valueHeads, size_t KD) {
+    for (size_t t = 0; t < count; ++t)
+        for (size_t h = 0; h < valueHeads; ++h) {
+            const float rate = expf(aLog[h]);
+            for (size_t i = 0; i < KD; ++i) {
+                const size_t c = (t * valueHeads + h) * KD + i;
+                const float x = f[c] + dtBias[h * KD + i];
+                g[c] = safeGate ? lowerBound * or_sigmoid(rate * x) : -rate * or_softplus(x);
+            }
+            beta[t * valueHeads + h] = or_sigmoid(b[t * valueHeads + h]);
+        }
 }
 
 /* the attention output gate of attentionMixer, LocalModel.hpp:2660-2665:

@@ -53,8 +53,13 @@
                                states (q, k, the group's v, the group's z; b
                                then a), and come back as the plain layout
       or_gdn_gated_norm,
-      or_silu                  fp64 closed form; a constant row normalises to
-                               sign * gamma; SiLU(0) = 0 and SiLU(x) -> x
+      or_silu                  fp64 closed form (both gate kinds); a constant
+                               row normalises to sign * gamma; SiLU(0) = 0 and
+                               SiLU(x) -> x
+      or_kda_gates             fp64 closed forms of both gate forms, including
+                               softplus's x > 20 branch; the safe gate stays in
+                               [lowerBound, 0]; the bias is per channel and the
+                               rate sits inside the sigmoid
       or_output_gate           fp64 closed form; a zero gate halves the output,
                                a large one leaves it, and only the second half
                                of each q row is read
@@ -177,9 +182,10 @@ void or_gdn_conv(const float* in, size_t count, size_t CW, size_t K, const float
 /* the linFusedQKVZ de-interleave (LocalModel.hpp:2739-2776) */
 void or_gdn_deinterleave(const float* fused, const float* ba, size_t count, size_t nK, size_t nV,
                          size_t KD, size_t VD, float* qkv, float* z, float* b, float* a);
-/* rmsNormRow then x SiLU(z) per (token, value head) (LocalModel.hpp:2833-2841) */
+/* rmsNormRow then x SiLU(z) per (token, value head) (LocalModel.hpp:2833-2841);
+   sigmoidGate != 0: x sigmoid(z) instead, kimiDeltaMixer's form (:2936-2945) */
 void or_gdn_gated_norm(const float* x, const float* z, const float* gamma, float eps, float* out,
-                       size_t count, size_t nV, size_t VD);
+                       size_t count, size_t nV, size_t VD, int sigmoidGate);
 
 /* attentionMixer's output gate (LocalModel.hpp:2660-2665): out [count][heads][dim]
    times sigmoid of the second dim elements of each q row (qStride >= 2 dim) */
@@ -191,6 +197,14 @@ void or_output_gate(float* out, const float* q, size_t count, size_t heads, size
 void or_kda_rule(const float* q, const float* k, const float* v, const float* g, const float* beta,
                  float* state, float* out, size_t count, size_t keyHeads, size_t valueHeads, size_t KD,
                  size_t VD, int normalize, int threads);
+
+/* kimiDeltaMixer's gates (LocalModel.hpp:2894-2905) as log decays: with
+   rate = exp(aLog[h]) and x = f[t][h][i] + dtBias[h][i],
+   g = safeGate ? lowerBound sigmoid(rate x) : -rate softplus(x); beta =
+   sigmoid(b). f, g [count][valueHeads][KD]; b, beta [count][valueHeads]. The
+   reference stores exp(g); the recurrence here takes g and exponentiates it. */
+void or_kda_gates(const float* f, const float* b, const float* aLog, const float* dtBias, int safeGate,
+                  float lowerBound, float* g, float* beta, size_t count, size_t valueHeads, size_t KD);
 
 /* number of threads the static pool would use given a request (<=0: all
    online CPUs in this process's affinity mask) */

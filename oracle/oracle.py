@@ -90,7 +90,8 @@ def lib():
         L.or_silu.argtypes = [C.c_float]
         L.or_gdn_conv.argtypes = [_f32p, _sz, _sz, _sz, _f32p, _f32p, _f32p]
         L.or_gdn_deinterleave.argtypes = [_f32p, _f32p] + [_sz] * 5 + [_f32p] * 4
-        L.or_gdn_gated_norm.argtypes = [_f32p, _f32p, _f32p, C.c_float, _f32p, _sz, _sz, _sz]
+        L.or_gdn_gated_norm.argtypes = [_f32p, _f32p, _f32p, C.c_float, _f32p, _sz, _sz, _sz, C.c_int]
+        L.or_kda_gates.argtypes = [_f32p] * 4 + [C.c_int, C.c_float, _f32p, _f32p, _sz, _sz, _sz]
         L.or_output_gate.argtypes = [_f32p, _f32p, _sz, _sz, _sz, _sz]
         L.or_kda_rule.argtypes = [_f32p] * 7 + [_sz] * 5 + [C.c_int, C.c_int]
         L.or_threads.restype = C.c_int
@@ -338,14 +339,16 @@ def gdn_deinterleave(fused, ba, nK, nV, KD, VD):
     return qkv, z, b, a
 
 
-def gdn_gated_norm(x, z, gamma, eps=1e-6):
-    """rmsNormRow then x SiLU(z) per (token, value head) (LocalModel.hpp:2833-2841)."""
+def gdn_gated_norm(x, z, gamma, eps=1e-6, gate="silu"):
+    """rmsNormRow then x SiLU(z) per (token, value head) (LocalModel.hpp:2833-2841);
+    gate="sigmoid": x sigmoid(z), kimiDeltaMixer's form (:2936-2945)."""
     x = np.ascontiguousarray(x, np.float32)
     z = np.ascontiguousarray(z, np.float32)
     gamma = np.ascontiguousarray(gamma, np.float32)
     count, nV, VD = x.shape
     out = np.empty_like(x)
-    lib().or_gdn_gated_norm(x.reshape(-1), z.reshape(-1), gamma, eps, out.reshape(-1), count, nV, VD)
+    lib().or_gdn_gated_norm(x.reshape(-1), z.reshape(-1), gamma, eps, out.reshape(-1), count, nV, VD,
+                            1 if gate == "sigmoid" else 0)
     return out
 
 
@@ -369,6 +372,20 @@ def _kda_args(q, k, v, g, beta, state):
     g = np.ascontiguousarray(g, np.float32).reshape(S, Hv, KD)
     beta = np.ascontiguousarray(beta, np.float32).reshape(S, Hv)
     return q, k, v, g, beta, st, S, Hk, Hv, KD, VD
+
+
+def kda_gates(f, b, a_log, dt_bias, safe_gate, lower_bound=-5.0):
+    """kimiDeltaMixer's gates (LocalModel.hpp:2894-2905) as log decays:
+    f [S][Hv][KD], b [S][Hv], a_log [Hv], dt_bias [Hv][KD] -> (g, beta)."""
+    f = np.ascontiguousarray(f, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    S, Hv, KD = f.shape
+    g = np.zeros_like(f)
+    beta = np.zeros((S, Hv), np.float32)
+    lib().or_kda_gates(f.reshape(-1), b.reshape(-1), np.ascontiguousarray(a_log, np.float32),
+                       np.ascontiguousarray(dt_bias, np.float32).reshape(-1), int(bool(safe_gate)),
+                       float(lower_bound), g.reshape(-1), beta.reshape(-1), S, Hv, KD)
+    return g, beta
 
 
 def kda_rule(q, k, v, g, beta, state=None, normalize=True, nthreads=1):

@@ -179,6 +179,29 @@ def test_gated_norm(gpu, z_bf16, out_bf16, VD):
         assert_f32_parity(ref, host(out), "gated norm")
 
 
+@pytest.mark.parametrize("z_bf16,out_bf16", [(False, False), (True, True)])
+def test_gated_norm_sigmoid_gate(gpu, z_bf16, out_bf16):
+    """kimiDeltaMixer's form of the gated norm: times sigmoid(z) (LocalModel.hpp:2936-2945)"""
+    count, nV, VD = 29, 4, 128
+    x = O.fill_normal((count, nV, VD), 23, "x")
+    z = O.fill_normal((count, nV, VD), 23, "z") * np.float32(2)
+    if z_bf16:
+        zb = O.pack_bf16(z)
+        z = O.unpack_bf16(zb).reshape(z.shape)
+        dz = dev_bf16(zb)
+    else:
+        dz = dev_f32(z)
+    gamma = O.fill_uniform((VD,), 23, "gamma", 0.5, 1.5)
+    out = torch_empty((count, nV, VD), out_bf16)
+    say("gated norm sigmoid", dict(z_bf16=z_bf16, out_bf16=out_bf16))
+    gpu.gdn_gated_norm(dev_f32(x), dz, dev_f32(gamma), out, eps=1e-6, gate="sigmoid")
+    ref = O.gdn_gated_norm(x, z, gamma, 1e-6, gate="sigmoid")
+    if out_bf16:
+        assert bf16_ulps(ref, host(out)).max() <= 1
+    else:
+        assert_f32_parity(ref, host(out), "gated norm sigmoid")
+
+
 def test_rejects_bad_shapes(gpu):
     import aigpu
     x = dev_f32(np.zeros((4, 2 * 6 + 6), np.float32))

@@ -113,3 +113,28 @@ def test_rejects_bad_shapes(gpu):
     st = torch.zeros((1, 96, 16), dtype=torch.float32, device="cuda")
     with pytest.raises(RuntimeError, match="keyDim"):
         gpu.kda_rule(z, z, v, torch.zeros((4, 1, 96), device="cuda"), torch.zeros((4, 1), device="cuda"), st, v)
+
+
+@pytest.mark.parametrize("safe", [False, True])
+def test_raw_gates(gpu, safe):
+    """the gates computed in the solve from f, b, aLog, dtBias as kimiDeltaMixer
+    does (LocalModel.hpp:2894-2905)"""
+    import torch
+    S, H, KD, VD = 140, 4, 128, 64
+    q = O.fill_normal((S, H, KD), 51, "q")
+    k = O.fill_normal((S, H, KD), 51, "k")
+    v = O.fill_normal((S, H, VD), 51, "v")
+    f = O.fill_normal((S, H, KD), 51, "f") * np.float32(2.0)
+    b = O.fill_normal((S, H), 51, "b")
+    a_log = O.fill_normal((H,), 51, "alog") * np.float32(0.5)
+    dt = O.fill_normal((H, KD), 51, "dt")
+    g, beta = O.kda_gates(f, b, a_log, dt, safe, -5.0)
+    s0 = O.fill_normal((H, KD, VD), 51, "s0") * np.float32(0.3)
+    state = dev_f32(s0)
+    out = torch.zeros((S, H, VD), dtype=torch.float32, device="cuda")
+    say("kda raw gates", dict(S=S, safe=safe))
+    gpu.kda_rule(dev_f32(q), dev_f32(k), dev_f32(v), None, None, state, out, f=dev_f32(f), b=dev_f32(b),
+                 a_log=dev_f32(a_log), dt_bias=dev_f32(dt), safe_gate=safe, lower_bound=-5.0)
+    ro, rs = O.kda_rule(q, k, v, g, beta, state=s0, nthreads=0)
+    assert_f32_parity(ro, host(out), f"out raw safe={safe}")
+    assert_f32_parity(rs, host(state), f"state raw safe={safe}")

@@ -156,3 +156,59 @@ def test_output_gate_closed_form():
     zero = q.copy()
     zero[:, :, D:2 * D] = 0.0
     np.testing.assert_array_equal(O.output_gate(out, zero, H, D, qs), out * np.float32(0.5))
+
+
+def test_gated_norm_sigmoid_gate_fp64():
+    """kimiDeltaMixer's gated norm (LocalModel.hpp:2936-2945): sigmoid, not SiLU"""
+    r = _rng(8)
+    count, nV, VD = 3, 2, 16
+    x = r.standard_normal((count, nV, VD)).astype(np.float32)
+    z = r.standard_normal((count, nV, VD)).astype(np.float32) * 3
+    gamma = r.uniform(0.5, 1.5, VD).astype(np.float32)
+    out = O.gdn_gated_norm(x, z, gamma, 1e-6, gate="sigmoid")
+    xd, zd = x.astype(np.float64), z.astype(np.float64)
+    ref = xd / np.sqrt((xd * xd).mean(-1, keepdims=True) + 1e-6) * gamma / (1 + np.exp(-zd))
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+    assert np.max(np.abs(out - O.gdn_gated_norm(x, z, gamma, 1e-6))) > 1e-2
+
+
+def _kda_gate_inputs(seed, S=6, H=3, KD=8):
+    r = _rng(seed)
+    f = (r.standard_normal((S, H, KD)) * 4).astype(np.float32)
+    f[0, 0, :3] = [25.0, 21.0, 19.5]         # either side of softplus's x > 20 branch
+    b = r.standard_normal((S, H)).astype(np.float32)
+    a_log = r.uniform(-1.0, 1.0, H).astype(np.float32)
+    dt = r.standard_normal((H, KD)).astype(np.float32)
+    dt[0, :3] = 0.0
+    return f, b, a_log, dt
+
+
+def test_kda_gates_softplus_form_fp64():
+    """kimiDeltaMixer's default gate (LocalModel.hpp:2900-2901 with
+    linSafeGate false): g = -exp(aLog) softplus(f + dtBias)"""
+    f, b, a_log, dt = _kda_gate_inputs(9)
+    g, beta = O.kda_gates(f, b, a_log, dt, safe_gate=False)
+    rate = np.exp(a_log.astype(np.float64))[None, :, None]
+    x = f.astype(np.float64) + dt[None].astype(np.float64)
+    sp = np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+    np.testing.assert_allclose(g, -rate * sp, rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(beta, 1 / (1 + np.exp(-b.astype(np.float64))), rtol=1e-6)
+    assert np.all(g <= 0)
+    assert g[0, 0, 0] == np.float32(-np.float32(np.exp(np.float32(a_log[0]))) * np.float32(25.0))
+    # a bias taken per head instead of per channel is a plausible mistake; it must not pass
+    bad = -rate * np.log1p(np.exp(np.minimum(f + dt[:, :1][None], 20.0)))
+    assert np.max(np.abs(g - bad)) > 1e-2
+
+
+def test_kda_gates_safe_form_fp64_and_bounds():
+    """the bounded gate (LocalModel.hpp:2900, linSafeGate): lowerBound
+    sigmoid(exp(aLog) (f + dtBias)), always in [lowerBound, 0]"""
+    f, b, a_log, dt = _kda_gate_inputs(10)
+    g, _ = O.kda_gates(f, b, a_log, dt, safe_gate=True, lower_bound=-5.0)
+    rate = np.exp(a_log.astype(np.float64))[None, :, None]
+    x = f.astype(np.float64) + dt[None].astype(np.float64)
+    np.testing.assert_allclose(g, -5.0 / (1 + np.exp(-rate * x)), rtol=2e-6, atol=1e-7)
+    assert np.all(g >= -5.0) and np.all(g <= 0.0)
+    # the rate applied outside the sigmoid is a plausible mistake; it must not pass
+    bad = -5.0 * rate / (1 + np.exp(-x))
+    assert np.max(np.abs(g - bad)) > 1e-2
