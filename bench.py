@@ -2,7 +2,7 @@
 """bench.py - throughput of the MI355X attention hot path against its roofline,
 with the reference's CPU path timed beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|delta|gdn|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|delta|gdn|kda|all]
 
 A step is one call of the hot path over one batch of synthetic, HBM-resident
 input. The headline workload (config.workload) is configs[2] of BASELINE.json,
@@ -50,7 +50,7 @@ def parse():
     # the GPU's clock ramps over the first ~15 ms of sustained work: a short
     # warm-up times the ramp rather than the kernels
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "all"])
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "kda", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of each baseline sample")
@@ -333,6 +333,67 @@ def delta_workload(args, cpu):
     return res
 
 
+def kda_workload(args, cpu):
+    """Kimi Delta Attention's recurrence at the Kimi-Linear shape (32 heads of
+    128, keys and values the same width), the gates fused from the raw
+    projections with the bounded (safe) form"""
+    import torch
+    import aigpu
+    S, H, D = 16384, 32, 128
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    q = randn((S, H, D), gen, torch.bfloat16)
+    k = randn((S, H, D), gen, torch.bfloat16)
+    v = randn((S, H, D), gen, torch.bfloat16)
+    f = torch.randn((S, H, D), generator=gen, device="cuda")
+    b = torch.randn((S, H), generator=gen, device="cuda")
+    a_log = torch.randn((H,), generator=gen, device="cuda") * 0.5
+    dt = torch.randn((H, D), generator=gen, device="cuda")
+    state = torch.zeros((H, D, D), dtype=torch.float32, device="cuda")
+    out = torch.empty((S, H, D), dtype=torch.float32, device="cuda")
+
+    def step():
+        state.zero_()
+        aigpu.kda_rule(q, k, v, None, None, state, out, f=f, b=b, a_log=a_log, dt_bias=dt, safe_gate=True,
+                       lower_bound=-5.0)
+
+    # q, k, v bf16 + f fp32 + b + out fp32 + the state read and written + aLog, dtBias
+    nbytes = float(3 * S * H * D * 2 + S * H * D * 4 + S * H * 4 + S * H * D * 4 + 2 * H * D * D * 4
+                   + H * 4 + H * D * 4)
+    step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "kda_scan_kernel")
+    res = {
+        "workload": "kimi delta attention S=16384 32 heads D=128 chunk 64, raw gates (safe), bf16 in, fp32 state",
+        "dtype": "f32",
+        "value": nbytes / (step_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": step_ms,
+        "roofline": {"kernel": "kda_scan_kernel", "bound": "hbm",
+                     "achieved": nbytes / (launched_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
+                     "frac": nbytes / (launched_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
+                     "kernel_ms": k_ms, "all_kernels_ms": launched_ms, "bytes_per_step": nbytes},
+    }
+    if cpu is not None:
+        # a bounded sample: the first n tokens of every head through the
+        # reference's deltaStep with perKeyDecay, one thread (the reference
+        # spreads heads over its pool; the sample's rate is per thread)
+        O, ref, kind, threads = cpu
+        n = 2048
+        qh = q[:n].float().cpu().numpy()
+        kh = k[:n].float().cpu().numpy()
+        vh = v[:n].float().cpu().numpy()
+        gh, bh = O.kda_gates(f[:n].cpu().numpy(), b[:n].cpu().numpy(), a_log.cpu().numpy(), dt.cpu().numpy(),
+                             True, -5.0)
+        t = time.perf_counter()
+        if ref is not None:
+            O.ref_kda_rule(qh, kh, vh, gh, bh)
+            what = "the reference's kernels::deltaStep (perKeyDecay) driven token by token"
+        else:
+            O.kda_rule(qh, kh, vh, gh, bh, nthreads=1)
+            what = "the C restatement of deltaStep (perKeyDecay)"
+        dt_s = time.perf_counter() - t
+        res["cpu_baseline"] = {"value": nbytes * (n / S) / dt_s / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
+                               "sample": f"the first {n} of 16384 tokens x 32 heads, single-threaded "
+                                         f"({dt_s:.1f} s): {what}"}
+    return res
+
+
 def gdn_workload(args, cpu):
     """the steps either side of the recurrence at configs[4]'s shapes: the fused
     qkvz de-interleave + causal conv (K 4) + SiLU, then the gated norm"""
@@ -478,10 +539,13 @@ def main():
         extra["delta_rule"] = delta_workload(args, cpu)
     if args.workload in ("gdn", "all"):
         extra["gdn_neighbours"] = gdn_workload(args, cpu)
+    if args.workload in ("kda", "all"):
+        extra["kda_rule"] = kda_workload(args, cpu)
     if args.workload == "all":
         extra["others"] = small_workloads(args)
     if head is None:   # a single non-prefill workload becomes the line
-        head = extra.pop("decode", None) or extra.pop("delta_rule", None) or extra.pop("gdn_neighbours")
+        head = (extra.pop("decode", None) or extra.pop("delta_rule", None) or extra.pop("gdn_neighbours", None)
+                or extra.pop("kda_rule"))
     line = {
         "metric": "attn TFLOP/s (prefill) & KV GB/s (decode) as % roofline, 1 MI355X vs host CPU",
         "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,

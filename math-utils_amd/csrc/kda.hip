@@ -3,28 +3,41 @@
 // as a chunked scan for gfx950: the gated delta rule with one decay per KEY
 // CHANNEL instead of one per head.
 //
-// Per value head, token t, with a_t[i] = exp(g_t[i]) the decay of state row i:
+// Per value head, token t, with a_t[i] = exp(g_t[i]) <= 1 the decay of state
+// row i:
 //   S_t = diag(a_t) S_{t-1} + k_t u_t^T,  u_t = beta_t (v_t - (diag(a_t) S_{t-1})^T k_t),
 //   o_t = S_t^T q_t
 // Over a chunk of C = 64 tokens, with gc_t[i] the in-chunk cumulative log
-// decay of channel i and Gamma_t = diag(exp(gc_t)):
+// decay of channel i:
 //   (I + A) U = diag(beta) (V - Kg S0),   Kg_t = k_t * exp(gc_t),
 //       A[t][j] = beta_t sum_i k_t[i] k_j[i] exp(gc_t[i] - gc_j[i])   (j < t)
 //   O  = Qg S0 + QKm U,   Qg_t = q_t * exp(gc_t),
 //       QKm[t][j] = sum_i q_t[i] k_j[i] exp(gc_t[i] - gc_j[i])        (j <= t)
 //   S' = diag(exp(gc_last)) S0 + Kt^T U,   Kt_j = k_j * exp(gc_last - gc_j)
-// Every exponent is <= 0. The decayed products A and QKm cannot be one
-// matrix product (the decay depends on the channel of both rows); between
-// 16-token blocks I > J they become one against the first row r of block I,
-//   exp(gc_t - gc_j) = exp(gc_t - gc_r) exp(gc_r - gc_j),
-// both factors <= 1, and inside a diagonal block they are summed directly.
+// With Tb = (I + A)^-1 diag(beta) and P = QKm Tb, everything that does not
+// depend on S0 is folded in per chunk, independently of the other chunks:
+//   W = Tb Kg,  Qt = Qg - P Kg,  Ut = Tb V,  Ot = P V
+//   U = Ut - W S0,   O = Ot + Qt S0,   S' = diag(exp(gc_last)) S0 + Kt^T U
+// so the sequential part is two products per chunk.
+//
+// The decayed products A and QKm are not one matrix product (the decay
+// depends on the channel of both rows). Between 16-token blocks I > J they
+// become one against the first row r of block I,
+//   exp(gc_t - gc_j) = exp(gc_t - gc_r) exp(gc_r - gc_j),  both factors <= 1;
+// inside a diagonal block against its middle row m, where one factor can
+// exceed 1, as long as the block's decay span keeps both within 2^100
+// (always for Kimi's bounded gate, lowerBound >= -5 per token); a block whose
+// span is larger is summed directly. Logs are kept in base 2 so that every
+// factor is one v_exp_f32.
 //
 // Two launches:
-//   kda_solve_kernel  per (value head, chunk): norms, cumulative decays, A,
-//                     QKm, T = (I + A)^-1, and the scaled rows Kg, Qg, Kt
-//   kda_scan_kernel   per (value head, 16 value columns): the chunks in order
-//                     on v_mfma_f32_16x16x4f32 (fp32 operands, so fp32 inputs
-//                     keep fp32 accuracy)
+//   kda_solve_kernel  per (value head, chunk): norms, gates, cumulative
+//                     decays, A, QKm, Tb, P, then W, Qt, Kt, Ut, Ot
+//   kda_scan_kernel   per (value head, 16 value columns): the chunks in order,
+//                     the next chunk's operands loaded into registers while
+//                     the current one computes
+// Every product is v_mfma_f32_16x16x4f32 (fp32 operands), so fp32 inputs keep
+// fp32 accuracy.
 #include "context.hpp"
 #include "device.hpp"
 #include "kernels.hpp"
@@ -33,13 +46,18 @@ namespace aigpu {
 
 namespace {
 
-constexpr int CH = 64;        // chunk length
-constexpr int CS = CH + 1;    // LDS row stride of CH x CH matrices
-constexpr int NB = 16;        // value columns per scan workgroup
-constexpr int NS = NB + 1;
+constexpr int CH = 64;       // chunk length
+constexpr int CS = CH + 4;   // LDS row stride of CH x CH matrices
+constexpr int NB = 16;       // value columns per scan workgroup
+constexpr float SPAN_MAX = 100.0f;   // log2 span of a diagonal block factorised through its middle row
 
-/* floats per (value head, chunk) record: T, QKm, Kg, Qg, Kt, beta, exp(gc_last) */
-__host__ __device__ constexpr int kda_record(int KD) { return 2 * CH * CH + 3 * CH * KD + CH + KD; }
+/* the per-(value head, chunk) record, in floats:
+     W   [CH][KD]   -W = -Tb Kg (negated: the scan accumulates onto Ut)
+     Qt  [CH][KD]   Qg - P Kg
+     KtT [KD][CH]   Kt transposed
+     eL  [KD]       exp(gc_last)
+     UO  [VD/16][2][CH][16]   per 16 value columns, Ut then Ot */
+__host__ __device__ constexpr size_t kda_record(int KD, size_t VD) { return 3 * size_t(CH) * KD + KD + 2 * CH * VD; }
 
 struct KdaArgs {
     KdaParams p;
@@ -47,31 +65,56 @@ struct KdaArgs {
     uint32_t nChunks;
 };
 
-template <bool F32>
-__device__ __forceinline__ float in_elem(const void* base, size_t i) {
-    if constexpr (F32) return static_cast<const float*>(base)[i];
-    return bf16_bits_to_float(static_cast<const uint16_t*>(base)[i]);
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+/* N consecutive input elements (fp32 or bf16) at element index i, as fp32; i
+   a multiple of 8 (bf16) or 4 (fp32) and the base 16-byte aligned */
+template <bool F32, int N>
+__device__ __forceinline__ void load_row(const void* base, size_t i, float (&x)[N]) {
+    if constexpr (F32) {
+#pragma unroll
+        for (int e = 0; e < N / 4; ++e) {
+            const floatx4 v = *reinterpret_cast<const floatx4*>(static_cast<const float*>(base) + i + 4 * e);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[4 * e + c] = v[c];
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < N / 8; ++e) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i + 8 * e);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                x[8 * e + 2 * c] = __uint_as_float(w[c] << 16);
+                x[8 * e + 2 * c + 1] = __uint_as_float(w[c] & 0xFFFF0000u);
+            }
+        }
+    }
+}
+
+/* block (I, J), J <= I, of the ten lower 16 x 16 blocks of a 64 x 64 matrix */
+__device__ __forceinline__ void lower_block(int b, int& I, int& J) {
+    I = b >= 6 ? 3 : (b >= 3 ? 2 : (b >= 1 ? 1 : 0));
+    J = b - I * (I + 1) / 2;
 }
 
 /*
-    Per (value head, chunk). Thread roles:
-      - norms: 4 threads per row (LocalModel.hpp:1380-1386, q also scaled by
-        1/sqrt(KD) as :2935);
-      - cumulative decays: one thread per channel down the chunk;
-      - decayed products: wave w takes block row I = w of A and QKm; its
-        diagonal block by direct sums, the blocks left of it on MFMA against
-        block I's first row;
-      - T = (I + A)^-1 as in the scalar-decay solve.
+    Per (value head, chunk), 256 threads. LDS (KD 128): kn, qn, gc
+    [64][KD+4] and Am, Qm, Tm [64][68], about 155 KB.
 */
 template <int KD, bool F32>
 __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
-    constexpr int KS = KD + 1;
-    __shared__ float kn[CH * KS];
-    __shared__ float qn[CH * KS];
-    __shared__ float gc[CH * KS];
-    __shared__ float Am[CH * CS];
-    __shared__ float Qm[CH * CS];
-    __shared__ float Tm[CH * CS];
+    constexpr int KS = KD + 4;
+    constexpr int PE = KD / 4;   // row elements per thread in the row passes
+    __shared__ __align__(16) float kn[CH * KS];
+    __shared__ __align__(16) float qn[CH * KS];
+    __shared__ __align__(16) float gc[CH * KS];   // log2 decays; later the value slabs
+    __shared__ __align__(16) float Am[CH * CS];   // A; later P
+    __shared__ __align__(16) float Qm[CH * CS];
+    __shared__ __align__(16) float Tm[CH * CS];
     __shared__ float Xs[4][16 * 17];
     __shared__ float bet[CH];
 
@@ -80,22 +123,24 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
     const uint32_t kh = uint32_t(h / (p.valueHeads / p.keyHeads));
     const uint64_t t0 = uint64_t(chunk) * CH;
     const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c16 = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const size_t VD = p.valueDim, Hv = p.valueHeads;
 
-    // ---- normalised rows; rows past the sequence's end are zero (beta 0) ----
+    // ---- q, k rows normalised (LocalModel.hpp:1380-1386, q also scaled by
+    //      1/sqrt(KD) as :2935); log2 decays; beta. Rows past the end are zero.
     {
         const int r = tid >> 2, qq = tid & 3;
-        constexpr int PE = KD / 4;
         const bool live = uint32_t(r) < n;
-        const size_t src = ((t0 + (live ? r : 0)) * p.keyHeads + kh) * KD + qq * PE;
+        const uint64_t tr = t0 + (live ? r : 0);
+        float kx[PE], qx[PE];
+        load_row<F32, PE>(p.k, (tr * p.keyHeads + kh) * KD + qq * PE, kx);
+        load_row<F32, PE>(p.q, (tr * p.keyHeads + kh) * KD + qq * PE, qx);
         float kss = 0.0f, qss = 0.0f;
+#pragma unroll
         for (int e = 0; e < PE; ++e) {
-            const float kx = live ? in_elem<F32>(p.k, src + e) : 0.0f;
-            const float qx = live ? in_elem<F32>(p.q, src + e) : 0.0f;
-            kn[r * KS + qq * PE + e] = kx;
-            qn[r * KS + qq * PE + e] = qx;
-            kss += kx * kx;
-            qss += qx * qx;
+            kss = fmaf(kx[e], kx[e], kss);
+            qss = fmaf(qx[e], qx[e], qss);
         }
         kss += __shfl_xor(kss, 1, WAVE);
         kss += __shfl_xor(kss, 2, WAVE);
@@ -106,99 +151,121 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
             kinv = 1.0f / sqrtf(kss + 1e-6f);
             qinv = (1.0f / sqrtf(qss + 1e-6f)) * (1.0f / sqrtf(float(KD)));
         }
-        for (int e = 0; e < PE; ++e) {
-            kn[r * KS + qq * PE + e] *= kinv;
-            qn[r * KS + qq * PE + e] *= qinv;
+        if (!live) kinv = qinv = 0.0f;
+#pragma unroll
+        for (int e = 0; e < PE; e += 4) {
+            *reinterpret_cast<floatx4*>(&kn[r * KS + qq * PE + e]) =
+                floatx4{kx[e] * kinv, kx[e + 1] * kinv, kx[e + 2] * kinv, kx[e + 3] * kinv};
+            *reinterpret_cast<floatx4*>(&qn[r * KS + qq * PE + e]) =
+                floatx4{qx[e] * qinv, qx[e + 1] * qinv, qx[e + 2] * qinv, qx[e + 3] * qinv};
+        }
+
+        // gates as LocalModel.hpp:2894-2905 computes them, or given
+        const bool raw = p.g == nullptr;
+        float gx[PE];
+        load_row<true, PE>(raw ? p.f : p.g, (tr * Hv + h) * KD + qq * PE, gx);
+        const float rate = raw ? expf(p.aLog[h]) : 0.0f;
+#pragma unroll
+        for (int e = 0; e < PE; e += 4) {
+            floatx4 o;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                float gt = gx[e + c];
+                if (raw) {
+                    const float x = gt + p.dtBias[size_t(h) * KD + qq * PE + e + c];
+                    gt = p.safeGate ? p.lowerBound * sigmoid_of(rate * x) : -rate * softplus_of(x);
+                }
+                o[c] = live ? gt * LOG2E : 0.0f;
+            }
+            *reinterpret_cast<floatx4*>(&gc[r * KS + qq * PE + e]) = o;
         }
         if (tid < CH) {
             float bt = 0.0f;
             if (uint32_t(tid) < n) {
-                const size_t i = (t0 + tid) * p.valueHeads + h;
+                const size_t i = (t0 + tid) * Hv + h;
                 bt = p.beta ? p.beta[i] : sigmoid_of(p.b[i]);
             }
             bet[tid] = bt;
         }
     }
-    // ---- cumulative log decay of each channel over the chunk; raw gates
-    //      become log decays as LocalModel.hpp:2894-2905 computes them ----
-    if (tid < KD) {
-        const bool raw = p.g == nullptr;
-        const float rate = raw ? expf(p.aLog[h]) : 0.0f;
-        const float bias = raw ? p.dtBias[size_t(h) * KD + tid] : 0.0f;
+    __syncthreads();
+
+    // ---- cumulative log2 decay of each channel down the chunk: the rows in
+    //      256 / KD parts, each summed by its own thread, then offset ----
+    {
+        constexpr int PARTS = 256 / KD, RPP = CH / PARTS;
+        const int ch = tid % KD, part = tid / KD;
         float acc = 0.0f;
-        for (int r = 0; r < CH; ++r) {
-            if (uint32_t(r) < n) {
-                const size_t i = ((t0 + r) * p.valueHeads + h) * KD + tid;
-                float gt;
-                if (!raw) {
-                    gt = p.g[i];
-                } else {
-                    const float f = p.f[i] + bias;
-                    gt = p.safeGate ? p.lowerBound * sigmoid_of(rate * f) : -rate * softplus_of(f);
-                }
-                acc += gt;
-            }
-            gc[r * KS + tid] = acc;
+#pragma unroll 8
+        for (int r = part * RPP; r < (part + 1) * RPP; ++r) {
+            acc += gc[r * KS + ch];
+            gc[r * KS + ch] = acc;
         }
-    }
-    // T is zero above its diagonal blocks
-    for (int idx = tid; idx < CH * CH; idx += 256) {
-        const int i = idx / CH, j = idx % CH;
-        if ((j >> 4) > (i >> 4)) Tm[i * CS + j] = 0.0f;
+        __syncthreads();
+        float off = 0.0f;
+        for (int q2 = 0; q2 < part; ++q2) off += gc[((q2 + 1) * RPP - 1) * KS + ch];
+        __syncthreads();
+        if (part > 0) {
+#pragma unroll 8
+            for (int r = part * RPP; r < (part + 1) * RPP; ++r) gc[r * KS + ch] += off;
+        }
     }
     __syncthreads();
 
-    // ---- block row I = w of A and QKm ----
-    {
-        const int I = w, r0 = 16 * I;
-        // diagonal block: lane (c16, g) holds rows 4g + rr, column c16
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const int t = r0 + 4 * g + rr, j = r0 + c16;
-            float sa = 0.0f, sq = 0.0f;
-            for (int i = 0; i < KD; ++i) {
-                const float e = expf(fminf(gc[t * KS + i] - gc[j * KS + i], 0.0f));
-                const float kj = kn[j * KS + i] * e;
-                sa = fmaf(kn[t * KS + i], kj, sa);
-                sq = fmaf(qn[t * KS + i], kj, sq);
+    // ---- the ten lower blocks of A and QKm: wave w takes blocks w, w+4, w+8 ----
+    for (int b = w; b < 10; b += 4) {
+        int I, J;
+        lower_block(b, I, J);
+        const int r0 = 16 * I, j0 = 16 * J;
+        int ref = r0;
+        bool direct = false;
+        if (I == J) {   // factorise through the middle row if the span allows it
+            ref = r0 + 8;
+            float span = 0.0f;
+            for (int ch = lane; ch < KD; ch += WAVE) {
+                const float gm = gc[ref * KS + ch];
+                span = fmaxf(span, fmaxf(gc[r0 * KS + ch] - gm, gm - gc[(r0 + 15) * KS + ch]));
             }
-            Am[t * CS + j] = j < t ? bet[t] * sa : 0.0f;
-            Qm[t * CS + j] = j <= t ? sq : 0.0f;
+            direct = !(wave_max(span) <= SPAN_MAX);
         }
-        // blocks J < I against row r0: left factors exp(gc_t - gc_r0) per
-        // (row, channel), right factors exp(gc_r0 - gc_j)
-        for (int J = 0; J < I; ++J) {
+        if (!direct) {
             floatx4 xa = {0.0f, 0.0f, 0.0f, 0.0f}, xq = {0.0f, 0.0f, 0.0f, 0.0f};
-            const int t = r0 + c16, j = 16 * J + c16;
+            const int t = r0 + c16, j = j0 + c16;
 #pragma unroll 4
             for (int s = 0; s < KD / 4; ++s) {
                 const int i = 4 * s + g;
-                const float gr = gc[r0 * KS + i];
-                const float lt = expf(gc[t * KS + i] - gr);
-                const float rj = kn[j * KS + i] * expf(gr - gc[j * KS + i]);
-                xa = __builtin_amdgcn_mfma_f32_16x16x4f32(kn[t * KS + i] * lt, rj, xa, 0, 0, 0);
-                xq = __builtin_amdgcn_mfma_f32_16x16x4f32(qn[t * KS + i] * lt, rj, xq, 0, 0, 0);
+                const float gr = gc[ref * KS + i];
+                const float lt = exp2_fast(gc[t * KS + i] - gr);
+                const float rj = kn[j * KS + i] * exp2_fast(gr - gc[j * KS + i]);
+                xa = mfma4(kn[t * KS + i] * lt, rj, xa);
+                xq = mfma4(qn[t * KS + i] * lt, rj, xq);
             }
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 const int tt = r0 + 4 * g + rr;
-                Am[tt * CS + j] = bet[tt] * xa[rr];
-                Qm[tt * CS + j] = xq[rr];
+                Am[tt * CS + j] = (I != J || j < tt) ? bet[tt] * xa[rr] : 0.0f;
+                Qm[tt * CS + j] = (I != J || j <= tt) ? xq[rr] : 0.0f;
             }
-        }
-        // the rest of the row is zero
-        for (int idx = lane; idx < 16 * CH; idx += WAVE) {
-            const int tt = r0 + idx / CH, j = idx % CH;
-            if (j >= r0 + 16) {
-                Am[tt * CS + j] = 0.0f;
-                Qm[tt * CS + j] = 0.0f;
+        } else {   // a diagonal block whose span is too wide to factorise
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int t = r0 + 4 * g + rr, j = r0 + c16;
+                float sa = 0.0f, sq = 0.0f;
+                for (int i = 0; i < KD; ++i) {
+                    const float e = exp2_fast(fminf(gc[t * KS + i] - gc[j * KS + i], 0.0f));
+                    const float kj = kn[j * KS + i] * e;
+                    sa = fmaf(kn[t * KS + i], kj, sa);
+                    sq = fmaf(qn[t * KS + i], kj, sq);
+                }
+                Am[t * CS + j] = j < t ? bet[t] * sa : 0.0f;
+                Qm[t * CS + j] = j <= t ? sq : 0.0f;
             }
         }
     }
     __syncthreads();
 
-    // ---- T = (I + A)^-1: diagonal blocks by forward substitution in
-    //      registers, then the block rows below on MFMA ----
+    // ---- T = (I + A)^-1 (lower blocks only): diagonal blocks by forward
+    //      substitution in registers, then the block rows below on MFMA ----
     {
         const int b0 = 16 * w, j = lane & 15;
         float t[16];
@@ -222,65 +289,160 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
             for (int M = J; M < I; ++M)
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
-                    x = __builtin_amdgcn_mfma_f32_16x16x4f32(Am[(16 * I + c16) * CS + 16 * M + 4 * s + g],
-                                                             Tm[(16 * M + 4 * s + g) * CS + 16 * J + c16], x, 0, 0, 0);
+                    x = mfma4(Am[(16 * I + c16) * CS + 16 * M + 4 * s + g], Tm[(16 * M + 4 * s + g) * CS + 16 * J + c16], x);
 #pragma unroll
             for (int r = 0; r < 4; ++r) Xs[w][(4 * g + r) * 17 + c16] = x[r];
             wave_sync();
             floatx4 y = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < 4; ++s)
-                y = __builtin_amdgcn_mfma_f32_16x16x4f32(Tm[(16 * I + c16) * CS + 16 * I + 4 * s + g],
-                                                         Xs[w][(4 * s + g) * 17 + c16], y, 0, 0, 0);
+                y = mfma4(Tm[(16 * I + c16) * CS + 16 * I + 4 * s + g], Xs[w][(4 * s + g) * 17 + c16], y);
 #pragma unroll
             for (int r = 0; r < 4; ++r) Tm[(16 * I + 4 * g + r) * CS + 16 * J + c16] = -y[r];
         }
     }
     __syncthreads();
 
-    // ---- the record ----
-    float* rec = a.work + (size_t(h) * a.nChunks + chunk) * kda_record(KD);
-    float* rT = rec;
-    float* rQ = rec + CH * CH;
-    float* rKg = rec + 2 * CH * CH;
-    float* rQg = rKg + CH * KD;
-    float* rKt = rQg + CH * KD;
-    float* rB = rKt + CH * KD;
-    float* rE = rB + CH;
+    // ---- Tb = T diag(beta), in place ----
     for (int idx = tid; idx < CH * CH; idx += 256) {
-        rT[idx] = Tm[(idx / CH) * CS + idx % CH];
-        rQ[idx] = Qm[(idx / CH) * CS + idx % CH];
+        const int t = idx / CH, j = idx % CH;
+        if ((j >> 4) <= (t >> 4)) Tm[t * CS + j] *= bet[j];
     }
+    __syncthreads();
+
+    // ---- P = QKm Tb into Am: wave w takes block row I = w ----
+    {
+        const int I = w;
+        for (int J = 0; J <= I; ++J) {
+            floatx4 x = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int M = J; M <= I; ++M)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    x = mfma4(Qm[(16 * I + c16) * CS + 16 * M + 4 * s + g], Tm[(16 * M + 4 * s + g) * CS + 16 * J + c16], x);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) Am[(16 * I + 4 * g + r) * CS + 16 * J + c16] = x[r];
+        }
+    }
+
+    // ---- the record: Kt (transposed) and exp(gc_last) straight from kn, gc ----
+    float* rec = a.work + (size_t(h) * a.nChunks + chunk) * kda_record(KD, VD);
+    float* rW = rec;
+    float* rQ = rec + CH * KD;
+    float* rK = rec + 2 * CH * KD;
+    float* rE = rec + 3 * CH * KD;
+    float* rUO = rE + KD;
     for (int idx = tid; idx < CH * KD; idx += 256) {
-        const int r = idx / KD, i = idx % KD;
-        const float gi = gc[r * KS + i];
-        const float eg = expf(gi);
-        rKg[idx] = kn[r * KS + i] * eg;
-        rQg[idx] = qn[r * KS + i] * eg;
-        rKt[idx] = kn[r * KS + i] * expf(gc[(CH - 1) * KS + i] - gi);
+        const int i = idx / CH, t = idx % CH;
+        rK[idx] = kn[t * KS + i] * exp2_fast(gc[(CH - 1) * KS + i] - gc[t * KS + i]);
     }
-    if (tid < CH) rB[tid] = bet[tid];
-    if (tid < KD) rE[tid] = expf(gc[(CH - 1) * KS + tid]);
+    if (tid < KD) rE[tid] = exp2_fast(gc[(CH - 1) * KS + tid]);
+    __syncthreads();
+    // Kg, Qg in place
+    for (int idx = tid; idx < CH * KD / 4; idx += 256) {
+        const int t = idx / (KD / 4), i = 4 * (idx % (KD / 4));
+        const floatx4 gv = *reinterpret_cast<const floatx4*>(&gc[t * KS + i]);
+        floatx4 kv = *reinterpret_cast<floatx4*>(&kn[t * KS + i]);
+        floatx4 qv = *reinterpret_cast<floatx4*>(&qn[t * KS + i]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float e = exp2_fast(gv[c]);
+            kv[c] *= e;
+            qv[c] *= e;
+        }
+        *reinterpret_cast<floatx4*>(&kn[t * KS + i]) = kv;
+        *reinterpret_cast<floatx4*>(&qn[t * KS + i]) = qv;
+    }
+    __syncthreads();
+
+    // Block row I of Tb and of P has I + 1 nonzero blocks: waves 0, 1 take
+    // rows 0 and 3, waves 2, 3 rows 1 and 2, each half of the column tiles.
+    const int rowA = (w < 2) ? 0 : 1, rowB = 3 - rowA, par = w & 1;
+
+    // ---- -W = -Tb Kg and Qt = Qg - P Kg ----
+    for (int pass = 0; pass < 2; ++pass) {
+        const int I = pass ? rowB : rowA;
+        for (int c = par; c < KD / 16; c += 2) {
+            floatx4 xw = {0.0f, 0.0f, 0.0f, 0.0f}, xq;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) xq[r] = qn[(16 * I + 4 * g + r) * KS + 16 * c + c16];
+            for (int M = 0; M <= I; ++M)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const int k = 16 * M + 4 * s + g;
+                    const float bk = kn[k * KS + 16 * c + c16];
+                    xw = mfma4(-Tm[(16 * I + c16) * CS + k], bk, xw);
+                    xq = mfma4(-Am[(16 * I + c16) * CS + k], bk, xq);
+                }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * I + 4 * g + r;
+                rW[t * KD + 16 * c + c16] = xw[r];
+                rQ[t * KD + 16 * c + c16] = xq[r];
+            }
+        }
+    }
+    __syncthreads();   // gc is free: it holds the value slabs from here
+
+    // ---- Ut = Tb V and Ot = P V, KD value columns at a time ----
+    for (size_t c0 = 0; c0 < VD; c0 += KD) {
+        const int sw = int(VD - c0 < size_t(KD) ? VD - c0 : KD);
+        for (int idx = tid; idx < CH * (sw / 8); idx += 256) {
+            const int t = idx / (sw / 8), c = 8 * (idx % (sw / 8));
+            float x[8];
+            if (uint32_t(t) < n) {
+                load_row<F32, 8>(p.v, ((t0 + t) * Hv + h) * VD + c0 + c, x);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+            }
+            *reinterpret_cast<floatx4*>(&gc[t * KS + c]) = floatx4{x[0], x[1], x[2], x[3]};
+            *reinterpret_cast<floatx4*>(&gc[t * KS + c + 4]) = floatx4{x[4], x[5], x[6], x[7]};
+        }
+        __syncthreads();
+        for (int pass = 0; pass < 2; ++pass) {
+            const int I = pass ? rowB : rowA;
+            for (int c = par; c < sw / 16; c += 2) {
+                floatx4 xu = {0.0f, 0.0f, 0.0f, 0.0f}, xo = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int M = 0; M <= I; ++M)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        const int k = 16 * M + 4 * s + g;
+                        const float bv = gc[k * KS + 16 * c + c16];
+                        xu = mfma4(Tm[(16 * I + c16) * CS + k], bv, xu);
+                        xo = mfma4(Am[(16 * I + c16) * CS + k], bv, xo);
+                    }
+                float* blk = rUO + (c0 / 16 + c) * (2 * CH * 16);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 16 * I + 4 * g + r;
+                    blk[t * 16 + c16] = xu[r];
+                    blk[CH * 16 + t * 16 + c16] = xo[r];
+                }
+            }
+        }
+        __syncthreads();
+    }
 }
 
 /*
-    Per (value head, 16 value columns), chunk by chunk:
-      R  = diag(beta) (V - Kg S)      U = T R
-      O  = Qg S + QKm U               S' = diag(exp(gc_last)) S + Kt^T U
-    S lives in LDS (fp32). Each chunk's record is loaded whole before its
-    products; the products are fp32 MFMAs.
+    Per (value head, 16 value columns), chunk by chunk, S (fp32) in LDS:
+      phase A, wave w on rows 16w..16w+15:  U = Ut - W S,  O = Ot + Qt S
+      phase B, wave w on key tiles w + 4t:  S' = diag(eL) S + Kt^T U
+    The next chunk's W, Qt, Kt, eL, Ut, Ot are loaded into registers at the
+    top of each chunk and written to LDS once the current one is done with
+    them.
 */
-template <int KD, bool F32>
+template <int KD>
 __global__ __launch_bounds__(256) void kda_scan_kernel(KdaArgs a) {
-    constexpr int KS = KD + 1;
-    __shared__ float Kg[CH * KS];
-    __shared__ float Qg[CH * KS];
-    __shared__ float Kt[CH * KS];
-    __shared__ float Tm[CH * CS];
-    __shared__ float Qm[CH * CS];
-    __shared__ float Ss[KD * NS];
-    __shared__ float Rs[CH * NS], Un[CH * NS], vs[CH * NS];
-    __shared__ float bet[CH], eL[KD];
+    constexpr int KS = KD + 4;
+    constexpr int NV = CH * KD / 4 / 256;   // float4 per thread per matrix
+    constexpr int MT = KD / 64;             // key tiles per wave in phase B
+    __shared__ __align__(16) float Wl[CH * KS];
+    __shared__ __align__(16) float Ql[CH * KS];
+    __shared__ __align__(16) float Kl[KD * CS];
+    __shared__ __align__(16) float Ss[KD * NB];
+    __shared__ __align__(16) float Un[CH * NB];
+    __shared__ float eLs[KD];
 
     const KdaParams& p = a.p;
     uint32_t bid = blockIdx.x;
@@ -288,76 +450,76 @@ __global__ __launch_bounds__(256) void kda_scan_kernel(KdaArgs a) {
     if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;   // a head's column blocks on one XCD
     const uint32_t h = bid / nCol, cb = bid % nCol;
     const uint32_t col0 = cb * NB;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c16 = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const size_t VD = p.valueDim, Hv = p.valueHeads;
+    const size_t recSize = kda_record(KD, VD);
 
     float* state = p.state + size_t(h) * KD * VD;
-    for (int idx = tid; idx < KD * NB; idx += 256) Ss[(idx / NB) * NS + idx % NB] = state[size_t(idx / NB) * VD + col0 + idx % NB];
+    for (int idx = tid; idx < KD * NB; idx += 256) Ss[idx] = state[size_t(idx / NB) * VD + col0 + idx % NB];
 
+    floatx4 pw[NV], pq[NV], pk[NV];
+    float pu[4], po[4], pe = 0.0f;
+    auto fetch = [&](uint32_t chunk) {
+        const float* rec = a.work + (size_t(h) * a.nChunks + chunk) * recSize;
+        const floatx4* r4 = reinterpret_cast<const floatx4*>(rec);
+#pragma unroll
+        for (int e = 0; e < NV; ++e) {
+            pw[e] = r4[tid + 256 * e];
+            pq[e] = r4[CH * KD / 4 + tid + 256 * e];
+            pk[e] = r4[2 * CH * KD / 4 + tid + 256 * e];
+        }
+        if (tid < KD) pe = rec[3 * CH * KD + tid];
+        const float* uo = rec + 3 * CH * KD + KD + size_t(cb) * (2 * CH * 16);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            pu[r] = uo[(16 * w + 4 * g + r) * 16 + c16];
+            po[r] = uo[CH * 16 + (16 * w + 4 * g + r) * 16 + c16];
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int e = 0; e < NV; ++e) {
+            const int f = 4 * (tid + 256 * e);
+            *reinterpret_cast<floatx4*>(&Wl[(f / KD) * KS + f % KD]) = pw[e];
+            *reinterpret_cast<floatx4*>(&Ql[(f / KD) * KS + f % KD]) = pq[e];
+            *reinterpret_cast<floatx4*>(&Kl[(f / CH) * CS + f % CH]) = pk[e];
+        }
+        if (tid < KD) eLs[tid] = pe;
+    };
+
+    fetch(0);
+    stash();
+    float u0[4], o0[4];
+    __syncthreads();
     for (uint32_t chunk = 0; chunk < a.nChunks; ++chunk) {
         const uint64_t t0 = uint64_t(chunk) * CH;
         const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
-        const float* rec = a.work + (size_t(h) * a.nChunks + chunk) * kda_record(KD);
-        __syncthreads();   // the previous chunk's reads are done
-        for (int idx = tid; idx < CH * CH; idx += 256) {
-            Tm[(idx / CH) * CS + idx % CH] = rec[idx];
-            Qm[(idx / CH) * CS + idx % CH] = rec[CH * CH + idx];
-        }
-        for (int idx = tid; idx < CH * KD; idx += 256) {
-            const int r = idx / KD, i = idx % KD;
-            Kg[r * KS + i] = rec[2 * CH * CH + idx];
-            Qg[r * KS + i] = rec[2 * CH * CH + CH * KD + idx];
-            Kt[r * KS + i] = rec[2 * CH * CH + 2 * CH * KD + idx];
-        }
-        if (tid < CH) bet[tid] = rec[2 * CH * CH + 3 * CH * KD + tid];
-        if (tid < KD) eL[tid] = rec[2 * CH * CH + 3 * CH * KD + CH + tid];
-        for (int idx = tid; idx < CH * NB; idx += 256) {
-            const int r = idx / NB, c = idx % NB;
-            vs[r * NS + c] = uint32_t(r) < n ? in_elem<F32>(p.v, ((t0 + r) * Hv + h) * VD + col0 + c) : 0.0f;
-        }
-        __syncthreads();
-
-        // R = beta (V - Kg S)
-        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-        for (int s = 0; s < KD / 4; ++s)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Kg[(16 * w + c16) * KS + 4 * s + g], Ss[(4 * s + g) * NS + c16],
-                                                       acc, 0, 0, 0);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int i = 16 * w + 4 * g + r;
-            Rs[i * NS + c16] = bet[i] * (vs[i * NS + c16] - acc[r]);
+            u0[r] = pu[r];
+            o0[r] = po[r];
         }
-        __syncthreads();
+        const bool more = chunk + 1 < a.nChunks;
+        if (more) fetch(chunk + 1);
 
-        // U = T R
-        acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < CH / 4; ++s)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Tm[(16 * w + c16) * CS + 4 * s + g], Rs[(4 * s + g) * NS + c16],
-                                                       acc, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) Un[(16 * w + 4 * g + r) * NS + c16] = acc[r];
-        __syncthreads();
-
-        // O = Qg S + QKm U
-        acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        // phase A
+        floatx4 xu = {u0[0], u0[1], u0[2], u0[3]}, xo = {o0[0], o0[1], o0[2], o0[3]};
 #pragma unroll 8
-        for (int s = 0; s < KD / 4; ++s)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Qg[(16 * w + c16) * KS + 4 * s + g], Ss[(4 * s + g) * NS + c16],
-                                                       acc, 0, 0, 0);
-#pragma unroll
-        for (int s = 0; s < CH / 4; ++s)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Qm[(16 * w + c16) * CS + 4 * s + g], Un[(4 * s + g) * NS + c16],
-                                                       acc, 0, 0, 0);
+        for (int s = 0; s < KD / 4; ++s) {
+            const float b = Ss[(4 * s + g) * NB + c16];
+            xu = mfma4(Wl[(16 * w + c16) * KS + 4 * s + g], b, xu);
+            xo = mfma4(Ql[(16 * w + c16) * KS + 4 * s + g], b, xo);
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t i = 16 * w + 4 * g + r;
-            if (i < n) p.out[((t0 + i) * Hv + h) * VD + col0 + c16] = acc[r];
+            Un[i * NB + c16] = xu[r];
+            if (i < n) p.out[((t0 + i) * Hv + h) * VD + col0 + c16] = xo[r];
         }
+        __syncthreads();
 
-        // S' = diag(exp(gc_last)) S + Kt^T U: wave w's key tiles mt = w + 4t
-        constexpr int MT = KD / 64;
+        // phase B
         floatx4 sn[MT];
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
@@ -365,23 +527,23 @@ __global__ __launch_bounds__(256) void kda_scan_kernel(KdaArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * mt + 4 * g + r;
-                sn[t][r] = eL[i] * Ss[i * NS + c16];
+                sn[t][r] = eLs[i] * Ss[i * NB + c16];
             }
 #pragma unroll
             for (int s = 0; s < CH / 4; ++s)
-                sn[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(Kt[(4 * s + g) * KS + 16 * mt + c16], Un[(4 * s + g) * NS + c16],
-                                                             sn[t], 0, 0, 0);
+                sn[t] = mfma4(Kl[(16 * mt + c16) * CS + 4 * s + g], Un[(4 * s + g) * NB + c16], sn[t]);
         }
-        __syncthreads();   // every read of S is done
+        __syncthreads();   // every read of S, W, Qt, Kt, eL of this chunk is done
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
             const int mt = w + 4 * t;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) Ss[(16 * mt + 4 * g + r) * NS + c16] = sn[t][r];
+            for (int r = 0; r < 4; ++r) Ss[(16 * mt + 4 * g + r) * NB + c16] = sn[t][r];
         }
+        if (more) stash();
+        __syncthreads();
     }
-    __syncthreads();
-    for (int idx = tid; idx < KD * NB; idx += 256) state[size_t(idx / NB) * VD + col0 + idx % NB] = Ss[(idx / NB) * NS + idx % NB];
+    for (int idx = tid; idx < KD * NB; idx += 256) state[size_t(idx / NB) * VD + col0 + idx % NB] = Ss[idx];
 }
 
 } // namespace
@@ -397,12 +559,17 @@ bool launch_kda(const KdaParams& p, hipStream_t stream) {
     if (!p.g && (!p.f || !p.b || !p.aLog || !p.dtBias))
         return ctx.fail("kda: raw gates need f, b, aLog and dtBias");
     if (!p.g && p.safeGate && !(p.lowerBound <= 0.0f)) return ctx.fail("kda: lowerBound must be <= 0");
+    auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) % 16) == 0; };
+    if (!aligned(p.q) || !aligned(p.k) || !aligned(p.v) || !aligned(p.g ? p.g : p.f) ||
+        (!p.g && !aligned(p.dtBias)))
+        return ctx.fail("kda: q, k, v and g (or f and dtBias) must be 16-byte aligned");
     if (p.count == 0) return true;
     KdaArgs a{};
     a.p = p;
     a.nChunks = uint32_t((p.count + CH - 1) / CH);
     if (a.nChunks > 65535u * 1024u) return ctx.fail("kda: sequence too long");
-    const size_t rec = size_t(kda_record(int(p.keyDim)));
+    if (p.valueHeads > 65535u) return ctx.fail("kda: too many value heads");
+    const size_t rec = kda_record(int(p.keyDim), p.valueDim);
     a.work = static_cast<float*>(ctx.grow(SLOT_DELTA_WORK, size_t(p.valueHeads) * a.nChunks * rec * sizeof(float)));
     if (!a.work) return false;
     const dim3 sgrid(a.nChunks, unsigned(p.valueHeads));
@@ -414,7 +581,7 @@ bool launch_kda(const KdaParams& p, hipStream_t stream) {
             }))                                                                                                \
             return false;                                                                                      \
         return ctx.launch("kda_scan_kernel", stream, [&] {                                                     \
-            hipLaunchKernelGGL((kda_scan_kernel<KD, F>), grid, block, 0, stream, a);                           \
+            hipLaunchKernelGGL((kda_scan_kernel<KD>), grid, block, 0, stream, a);                              \
         });                                                                                                    \
     }
     AIGPU_KDA(128, true)
