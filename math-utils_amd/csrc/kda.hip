@@ -51,12 +51,17 @@ constexpr int CS = CH + 4;   // LDS row stride of CH x CH matrices
 constexpr int NB = 16;       // value columns per scan workgroup
 constexpr float SPAN_MAX = 100.0f;   // log2 span of a diagonal block factorised through its middle row
 
-/* the per-(value head, chunk) record, in floats:
-     W   [CH][KD]   -W = -Tb Kg (negated: the scan accumulates onto Ut)
-     Qt  [CH][KD]   Qg - P Kg
-     KtT [KD][CH]   Kt transposed
-     eL  [KD]       exp(gc_last)
-     UO  [VD/16][2][CH][16]   per 16 value columns, Ut then Ot */
+/* the per-(value head, chunk) record, in floats, laid out as the scan's
+   MFMA operands so that each of its lanes loads 16 bytes per 4 products:
+     WF  [CH/16 row block][KD/16 k group][64 lanes][4]   -W = -Tb Kg (negated:
+         the scan accumulates onto Ut); lane (c16, g) of row block rb, group q
+         holds row 16 rb + c16, k = 16 q + 4 g .. +3
+     QF  the same for Qt = Qg - P Kg
+     KF  [KD/16 key tile][CH/16 token group][64][4]   Kt^T: lane (c16, g) of
+         tile mt, group q holds key 16 mt + c16, tokens 16 q + 4 g .. +3
+     eL  [KD]   exp(gc_last)
+     UO  [VD/16 column block][2: Ut, Ot][CH/16 row block][64][4]   the MFMA
+         accumulator layout: lane (c16, g) holds rows 4 g .. +3, column c16 */
 __host__ __device__ constexpr size_t kda_record(int KD, size_t VD) { return 3 * size_t(CH) * KD + KD + 2 * CH * VD; }
 
 struct KdaArgs {
@@ -109,6 +114,7 @@ template <int KD, bool F32>
 __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
     constexpr int KS = KD + 4;
     constexpr int PE = KD / 4;   // row elements per thread in the row passes
+    constexpr int VPRE = CH * KD / 8 / 256;   // 8-element value pieces per thread per slab
     __shared__ __align__(16) float kn[CH * KS];
     __shared__ __align__(16) float qn[CH * KS];
     __shared__ __align__(16) float gc[CH * KS];   // log2 decays; later the value slabs
@@ -188,6 +194,29 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
             bet[tid] = bt;
         }
     }
+    // the first value slab is requested now and written to LDS when gc is free
+    const int sw0 = int(VD < size_t(KD) ? VD : KD);
+    float vpre[VPRE][8];
+    auto vload = [&](size_t c0, int sw, int it, float (&x)[8]) {
+        const int idx = tid + 256 * it;
+        const int t = idx / (sw / 8), c = 8 * (idx % (sw / 8));
+        if (idx < CH * (sw / 8) && uint32_t(t) < n) {
+            load_row<F32, 8>(p.v, ((t0 + t) * Hv + h) * VD + c0 + c, x);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+        }
+    };
+    auto vstore = [&](int sw, int it, const float (&x)[8]) {
+        const int idx = tid + 256 * it;
+        if (idx < CH * (sw / 8)) {
+            const int t = idx / (sw / 8), c = 8 * (idx % (sw / 8));
+            *reinterpret_cast<floatx4*>(&gc[t * KS + c]) = floatx4{x[0], x[1], x[2], x[3]};
+            *reinterpret_cast<floatx4*>(&gc[t * KS + c + 4]) = floatx4{x[4], x[5], x[6], x[7]};
+        }
+    };
+#pragma unroll
+    for (int it = 0; it < VPRE; ++it) vload(0, sw0, it, vpre[it]);
     __syncthreads();
 
     // ---- cumulative log2 decay of each channel down the chunk: the rows in
@@ -195,20 +224,18 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
     {
         constexpr int PARTS = 256 / KD, RPP = CH / PARTS;
         const int ch = tid % KD, part = tid / KD;
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int r = part * RPP; r < (part + 1) * RPP; ++r) {
-            acc += gc[r * KS + ch];
-            gc[r * KS + ch] = acc;
-        }
+        float col[RPP];
+#pragma unroll
+        for (int r = 0; r < RPP; ++r) col[r] = gc[(part * RPP + r) * KS + ch];
+#pragma unroll
+        for (int r = 1; r < RPP; ++r) col[r] += col[r - 1];
+        gc[(part * RPP + RPP - 1) * KS + ch] = col[RPP - 1];
         __syncthreads();
         float off = 0.0f;
         for (int q2 = 0; q2 < part; ++q2) off += gc[((q2 + 1) * RPP - 1) * KS + ch];
         __syncthreads();
-        if (part > 0) {
-#pragma unroll 8
-            for (int r = part * RPP; r < (part + 1) * RPP; ++r) gc[r * KS + ch] += off;
-        }
+#pragma unroll
+        for (int r = 0; r < RPP; ++r) gc[(part * RPP + r) * KS + ch] = col[r] + off;
     }
     __syncthreads();
 
@@ -229,16 +256,24 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
             direct = !(wave_max(span) <= SPAN_MAX);
         }
         if (!direct) {
+            // within each group of 16 channels lane (c16, g) supplies channel
+            // 16q + 4g + s on the s-th of four MFMAs: 16-byte reads
             floatx4 xa = {0.0f, 0.0f, 0.0f, 0.0f}, xq = {0.0f, 0.0f, 0.0f, 0.0f};
             const int t = r0 + c16, j = j0 + c16;
-#pragma unroll 4
-            for (int s = 0; s < KD / 4; ++s) {
-                const int i = 4 * s + g;
-                const float gr = gc[ref * KS + i];
-                const float lt = exp2_fast(gc[t * KS + i] - gr);
-                const float rj = kn[j * KS + i] * exp2_fast(gr - gc[j * KS + i]);
-                xa = mfma4(kn[t * KS + i] * lt, rj, xa);
-                xq = mfma4(qn[t * KS + i] * lt, rj, xq);
+            auto ld4 = [](const float* ptr) { return *reinterpret_cast<const floatx4*>(ptr); };
+#pragma unroll 2
+            for (int q = 0; q < KD / 16; ++q) {
+                const int i = 16 * q + 4 * g;
+                const floatx4 gr = ld4(&gc[ref * KS + i]);
+                const floatx4 gt = ld4(&gc[t * KS + i]), kt = ld4(&kn[t * KS + i]), qt = ld4(&qn[t * KS + i]);
+                const floatx4 gj = ld4(&gc[j * KS + i]), kj = ld4(&kn[j * KS + i]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float lt = exp2_fast(gt[e] - gr[e]);
+                    const float rj = kj[e] * exp2_fast(gr[e] - gj[e]);
+                    xa = mfma4(kt[e] * lt, rj, xa);
+                    xq = mfma4(qt[e] * lt, rj, xq);
+                }
             }
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
@@ -324,16 +359,21 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
         }
     }
 
-    // ---- the record: Kt (transposed) and exp(gc_last) straight from kn, gc ----
+    // ---- the record: Kt and exp(gc_last) straight from kn, gc ----
     float* rec = a.work + (size_t(h) * a.nChunks + chunk) * kda_record(KD, VD);
     float* rW = rec;
     float* rQ = rec + CH * KD;
     float* rK = rec + 2 * CH * KD;
     float* rE = rec + 3 * CH * KD;
     float* rUO = rE + KD;
-    for (int idx = tid; idx < CH * KD; idx += 256) {
-        const int i = idx / CH, t = idx % CH;
-        rK[idx] = kn[t * KS + i] * exp2_fast(gc[(CH - 1) * KS + i] - gc[t * KS + i]);
+    for (int idx = tid; idx < CH * KD / 4; idx += 256) {
+        const int ln = idx % 64, q = (idx / 64) % (CH / 16), mt = idx / 64 / (CH / 16);
+        const int m = 16 * mt + (ln & 15), j0 = 16 * q + 4 * (ln >> 4);
+        const float gl = gc[(CH - 1) * KS + m];
+        floatx4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = kn[(j0 + e) * KS + m] * exp2_fast(gl - gc[(j0 + e) * KS + m]);
+        reinterpret_cast<floatx4*>(rK)[idx] = o;
     }
     if (tid < KD) rE[tid] = exp2_fast(gc[(CH - 1) * KS + tid]);
     __syncthreads();
@@ -358,27 +398,24 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
     // rows 0 and 3, waves 2, 3 rows 1 and 2, each half of the column tiles.
     const int rowA = (w < 2) ? 0 : 1, rowB = 3 - rowA, par = w & 1;
 
-    // ---- -W = -Tb Kg and Qt = Qg - P Kg ----
+    // ---- -W = -Tb Kg and Qt = Qg - P Kg, computed transposed (key rows,
+    //      token columns) so each lane's accumulator is one scan fragment ----
     for (int pass = 0; pass < 2; ++pass) {
         const int I = pass ? rowB : rowA;
         for (int c = par; c < KD / 16; c += 2) {
-            floatx4 xw = {0.0f, 0.0f, 0.0f, 0.0f}, xq;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) xq[r] = qn[(16 * I + 4 * g + r) * KS + 16 * c + c16];
+            floatx4 xw = {0.0f, 0.0f, 0.0f, 0.0f};
+            floatx4 xq = *reinterpret_cast<const floatx4*>(&qn[(16 * I + c16) * KS + 16 * c + 4 * g]);
             for (int M = 0; M <= I; ++M)
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
                     const int k = 16 * M + 4 * s + g;
-                    const float bk = kn[k * KS + 16 * c + c16];
-                    xw = mfma4(-Tm[(16 * I + c16) * CS + k], bk, xw);
-                    xq = mfma4(-Am[(16 * I + c16) * CS + k], bk, xq);
+                    const float ak = kn[k * KS + 16 * c + c16];
+                    xw = mfma4(ak, -Tm[(16 * I + c16) * CS + k], xw);
+                    xq = mfma4(ak, -Am[(16 * I + c16) * CS + k], xq);
                 }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = 16 * I + 4 * g + r;
-                rW[t * KD + 16 * c + c16] = xw[r];
-                rQ[t * KD + 16 * c + c16] = xq[r];
-            }
+            const int frag = (I * (KD / 16) + c) * 64 + lane;
+            reinterpret_cast<floatx4*>(rW)[frag] = xw;
+            reinterpret_cast<floatx4*>(rQ)[frag] = xq;
         }
     }
     __syncthreads();   // gc is free: it holds the value slabs from here
@@ -386,17 +423,15 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
     // ---- Ut = Tb V and Ot = P V, KD value columns at a time ----
     for (size_t c0 = 0; c0 < VD; c0 += KD) {
         const int sw = int(VD - c0 < size_t(KD) ? VD - c0 : KD);
-        for (int idx = tid; idx < CH * (sw / 8); idx += 256) {
-            const int t = idx / (sw / 8), c = 8 * (idx % (sw / 8));
-            float x[8];
-            if (uint32_t(t) < n) {
-                load_row<F32, 8>(p.v, ((t0 + t) * Hv + h) * VD + c0 + c, x);
-            } else {
+        if (c0 == 0) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+            for (int it = 0; it < VPRE; ++it) vstore(sw, it, vpre[it]);
+        } else {
+            for (int it = 0; it < VPRE; ++it) {
+                float x[8];
+                vload(c0, sw, it, x);
+                vstore(sw, it, x);
             }
-            *reinterpret_cast<floatx4*>(&gc[t * KS + c]) = floatx4{x[0], x[1], x[2], x[3]};
-            *reinterpret_cast<floatx4*>(&gc[t * KS + c + 4]) = floatx4{x[4], x[5], x[6], x[7]};
         }
         __syncthreads();
         for (int pass = 0; pass < 2; ++pass) {
@@ -411,13 +446,9 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
                         xu = mfma4(Tm[(16 * I + c16) * CS + k], bv, xu);
                         xo = mfma4(Am[(16 * I + c16) * CS + k], bv, xo);
                     }
-                float* blk = rUO + (c0 / 16 + c) * (2 * CH * 16);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int t = 16 * I + 4 * g + r;
-                    blk[t * 16 + c16] = xu[r];
-                    blk[CH * 16 + t * 16 + c16] = xo[r];
-                }
+                floatx4* blk = reinterpret_cast<floatx4*>(rUO + (c0 / 16 + c) * (2 * CH * 16));
+                blk[I * 64 + lane] = xu;
+                blk[(CH / 16 + I) * 64 + lane] = xo;
             }
         }
         __syncthreads();
@@ -425,24 +456,27 @@ __global__ __launch_bounds__(256) void kda_solve_kernel(KdaArgs a) {
 }
 
 /*
-    Per (value head, 16 value columns), chunk by chunk, S (fp32) in LDS:
-      phase A, wave w on rows 16w..16w+15:  U = Ut - W S,  O = Ot + Qt S
-      phase B, wave w on key tiles w + 4t:  S' = diag(eL) S + Kt^T U
-    The next chunk's W, Qt, Kt, eL, Ut, Ot are loaded into registers at the
-    top of each chunk and written to LDS once the current one is done with
-    them.
+    Per (value head, 16 value columns), chunk by chunk, S (fp32) in LDS,
+    eight waves (two per SIMD, so one can issue while the other waits):
+      phase A, wave w on rows 16 (w % 4)..+15:
+          w < 4:  U = Ut - W S  (into LDS)      w >= 4:  O = Ot + Qt S  (out)
+      phase B, wave w on key tile w (KD / 16 tiles):  S' = diag(eL) S + Kt^T U
+    Each wave's W / Qt / Kt operands and its Ut / Ot accumulator start come
+    straight from the record into registers, one chunk ahead. Only S and U
+    are in LDS, both transposed (St[col][k], Ut[col][token]) so that a lane
+    reads k = 16q + 4g .. +3 of its column at once: within each group of 16 k,
+    lane (c16, g) supplies k = 16q + 4g + s on the s-th of four MFMAs. Row
+    strides of KD + 4 and CH + 4 floats (odd in 16-byte units) keep each
+    16-lane read phase on distinct banks.
 */
+constexpr int SCAN_THREADS = 512;
+
 template <int KD>
-__global__ __launch_bounds__(256) void kda_scan_kernel(KdaArgs a) {
+__global__ __launch_bounds__(SCAN_THREADS) void kda_scan_kernel(KdaArgs a) {
     constexpr int KS = KD + 4;
-    constexpr int NV = CH * KD / 4 / 256;   // float4 per thread per matrix
-    constexpr int MT = KD / 64;             // key tiles per wave in phase B
-    __shared__ __align__(16) float Wl[CH * KS];
-    __shared__ __align__(16) float Ql[CH * KS];
-    __shared__ __align__(16) float Kl[KD * CS];
-    __shared__ __align__(16) float Ss[KD * NB];
-    __shared__ __align__(16) float Un[CH * NB];
-    __shared__ float eLs[KD];
+    constexpr int QA = KD / 16, QB = CH / 16;
+    __shared__ __align__(16) float St[NB * KS];
+    __shared__ __align__(16) float Ut[NB * CS];
 
     const KdaParams& p = a.p;
     uint32_t bid = blockIdx.x;
@@ -452,98 +486,87 @@ __global__ __launch_bounds__(256) void kda_scan_kernel(KdaArgs a) {
     const uint32_t col0 = cb * NB;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rb = w & 3;               // phase A row block
+    const int role = w >> 2;            // phase A: 0 U, 1 O
+    const bool tileWave = w < KD / 16;  // phase B
     const size_t VD = p.valueDim, Hv = p.valueHeads;
     const size_t recSize = kda_record(KD, VD);
 
     float* state = p.state + size_t(h) * KD * VD;
-    for (int idx = tid; idx < KD * NB; idx += 256) Ss[idx] = state[size_t(idx / NB) * VD + col0 + idx % NB];
+    for (int idx = tid; idx < KD * NB; idx += SCAN_THREADS) {
+        const int k = idx / NB, c = idx % NB;
+        St[c * KS + k] = state[size_t(k) * VD + col0 + c];
+    }
 
-    floatx4 pw[NV], pq[NV], pk[NV];
-    float pu[4], po[4], pe = 0.0f;
+    // the next chunk's operands, requested at the top of the current one
+    floatx4 fa[QA], fb[QB], fu, fe = {0.0f, 0.0f, 0.0f, 0.0f};
     auto fetch = [&](uint32_t chunk) {
         const float* rec = a.work + (size_t(h) * a.nChunks + chunk) * recSize;
-        const floatx4* r4 = reinterpret_cast<const floatx4*>(rec);
+        const floatx4* ra = reinterpret_cast<const floatx4*>(rec + role * CH * KD) + rb * QA * 64 + lane;
 #pragma unroll
-        for (int e = 0; e < NV; ++e) {
-            pw[e] = r4[tid + 256 * e];
-            pq[e] = r4[CH * KD / 4 + tid + 256 * e];
-            pk[e] = r4[2 * CH * KD / 4 + tid + 256 * e];
-        }
-        if (tid < KD) pe = rec[3 * CH * KD + tid];
-        const float* uo = rec + 3 * CH * KD + KD + size_t(cb) * (2 * CH * 16);
+        for (int q = 0; q < QA; ++q) fa[q] = ra[q * 64];
+        if (tileWave) {
+            const floatx4* rk = reinterpret_cast<const floatx4*>(rec + 2 * CH * KD) + w * QB * 64 + lane;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            pu[r] = uo[(16 * w + 4 * g + r) * 16 + c16];
-            po[r] = uo[CH * 16 + (16 * w + 4 * g + r) * 16 + c16];
+            for (int q = 0; q < QB; ++q) fb[q] = rk[q * 64];
+            fe = *reinterpret_cast<const floatx4*>(rec + 3 * CH * KD + 16 * w + 4 * g);
         }
+        fu = reinterpret_cast<const floatx4*>(rec + 3 * CH * KD + KD)[((cb * 2 + role) * QB + rb) * 64 + lane];
     };
-    auto stash = [&]() {
-#pragma unroll
-        for (int e = 0; e < NV; ++e) {
-            const int f = 4 * (tid + 256 * e);
-            *reinterpret_cast<floatx4*>(&Wl[(f / KD) * KS + f % KD]) = pw[e];
-            *reinterpret_cast<floatx4*>(&Ql[(f / KD) * KS + f % KD]) = pq[e];
-            *reinterpret_cast<floatx4*>(&Kl[(f / CH) * CS + f % CH]) = pk[e];
-        }
-        if (tid < KD) eLs[tid] = pe;
-    };
+    auto ld4 = [](const float* ptr) { return *reinterpret_cast<const floatx4*>(ptr); };
 
     fetch(0);
-    stash();
-    float u0[4], o0[4];
     __syncthreads();
     for (uint32_t chunk = 0; chunk < a.nChunks; ++chunk) {
         const uint64_t t0 = uint64_t(chunk) * CH;
         const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
+        floatx4 ca[QA], cbk[QB], x = fu, ce = fe;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            u0[r] = pu[r];
-            o0[r] = po[r];
-        }
-        const bool more = chunk + 1 < a.nChunks;
-        if (more) fetch(chunk + 1);
+        for (int q = 0; q < QA; ++q) ca[q] = fa[q];
+#pragma unroll
+        for (int q = 0; q < QB; ++q) cbk[q] = fb[q];
+        if (chunk + 1 < a.nChunks) fetch(chunk + 1);
 
         // phase A
-        floatx4 xu = {u0[0], u0[1], u0[2], u0[3]}, xo = {o0[0], o0[1], o0[2], o0[3]};
-#pragma unroll 8
-        for (int s = 0; s < KD / 4; ++s) {
-            const float b = Ss[(4 * s + g) * NB + c16];
-            xu = mfma4(Wl[(16 * w + c16) * KS + 4 * s + g], b, xu);
-            xo = mfma4(Ql[(16 * w + c16) * KS + 4 * s + g], b, xo);
-        }
+        const float* srow = &St[c16 * KS + 4 * g];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t i = 16 * w + 4 * g + r;
-            Un[i * NB + c16] = xu[r];
-            if (i < n) p.out[((t0 + i) * Hv + h) * VD + col0 + c16] = xo[r];
+        for (int q = 0; q < QA; ++q) {
+            const floatx4 bs = ld4(srow + 16 * q);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) x = mfma4(ca[q][s], bs[s], x);
+        }
+        if (role == 0) {
+            *reinterpret_cast<floatx4*>(&Ut[c16 * CS + 16 * rb + 4 * g]) = x;
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t i = 16 * rb + 4 * g + r;
+                if (i < n) p.out[((t0 + i) * Hv + h) * VD + col0 + c16] = x[r];
+            }
         }
         __syncthreads();
 
-        // phase B
-        floatx4 sn[MT];
+        // phase B: each wave reads and then rewrites only its own tile of S
+        if (tileWave) {
+            const floatx4 s4 = ld4(&St[c16 * KS + 16 * w + 4 * g]);
+            floatx4 sn;
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const int mt = w + 4 * t;
+            for (int r = 0; r < 4; ++r) sn[r] = ce[r] * s4[r];
+            const float* urow = &Ut[c16 * CS + 4 * g];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = 16 * mt + 4 * g + r;
-                sn[t][r] = eLs[i] * Ss[i * NB + c16];
+            for (int q = 0; q < QB; ++q) {
+                const floatx4 bu = ld4(urow + 16 * q);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) sn = mfma4(cbk[q][s], bu[s], sn);
             }
-#pragma unroll
-            for (int s = 0; s < CH / 4; ++s)
-                sn[t] = mfma4(Kl[(16 * mt + c16) * CS + 4 * s + g], Un[(4 * s + g) * NB + c16], sn[t]);
+            *reinterpret_cast<floatx4*>(&St[c16 * KS + 16 * w + 4 * g]) = sn;
         }
-        __syncthreads();   // every read of S, W, Qt, Kt, eL of this chunk is done
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const int mt = w + 4 * t;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) Ss[(16 * mt + 4 * g + r) * NB + c16] = sn[t][r];
-        }
-        if (more) stash();
         __syncthreads();
     }
-    for (int idx = tid; idx < KD * NB; idx += 256) state[size_t(idx / NB) * VD + col0 + idx % NB] = Ss[idx];
+    for (int idx = tid; idx < KD * NB; idx += SCAN_THREADS) {
+        const int k = idx / NB, c = idx % NB;
+        state[size_t(k) * VD + col0 + c] = St[c * KS + k];
+    }
 }
 
 } // namespace
@@ -573,7 +596,7 @@ bool launch_kda(const KdaParams& p, hipStream_t stream) {
     a.work = static_cast<float*>(ctx.grow(SLOT_DELTA_WORK, size_t(p.valueHeads) * a.nChunks * rec * sizeof(float)));
     if (!a.work) return false;
     const dim3 sgrid(a.nChunks, unsigned(p.valueHeads));
-    const dim3 grid{unsigned(p.valueHeads * (p.valueDim / NB))}, block{256};
+    const dim3 grid{unsigned(p.valueHeads * (p.valueDim / NB))}, block{SCAN_THREADS};
 #define AIGPU_KDA(KD, F)                                                                                       \
     if (p.keyDim == KD && (p.inType == 0) == F) {                                                              \
         if (!ctx.launch("kda_solve_kernel", stream, [&] {                                                      \
