@@ -360,21 +360,29 @@ def kda_workload(args, cpu):
     nbytes = float(3 * S * H * D * 2 + S * H * D * 4 + S * H * 4 + S * H * D * 4 + 2 * H * D * D * 4
                    + H * 4 + H * D * 4)
     step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "kda_scan_kernel")
+    # fp32 MFMA work per (head, 64-token chunk) at D = 128: the solve's decayed
+    # products (10 blocks x 2 x 16*16*128*2), P (20 x 16^3*2), W and Qt, Ut and
+    # Ot (2 x 10 x 16*16*128*2 each); the scan's three 64x128x128 products
+    chunks = S // 64
+    scan_flop = 3 * 64 * D * D * 2.0 * chunks * H
+    solve_flop = (10 * 2 * 16 * 16 * D * 2 + 20 * 16 ** 3 * 2 + 2 * 2 * 10 * 16 * 16 * D * 2) * float(chunks * H)
     res = {
         "workload": "kimi delta attention S=16384 32 heads D=128 chunk 64, raw gates (safe), bf16 in, fp32 state",
         "dtype": "f32",
         "value": nbytes / (step_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": step_ms,
-        "roofline": {"kernel": "kda_scan_kernel", "bound": "hbm",
-                     "achieved": nbytes / (launched_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
-                     "frac": nbytes / (launched_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
-                     "kernel_ms": k_ms, "all_kernels_ms": launched_ms, "bytes_per_step": nbytes},
+        "step_tflops": (scan_flop + solve_flop) / (step_ms * 1e-3) / 1e12,
+        "roofline": {"kernel": "kda_scan_kernel", "bound": "mfma",
+                     "achieved": scan_flop / (k_ms * 1e-3) / 1e12, "peak": PEAK_MFMA_F32, "unit": "TFLOP/s",
+                     "frac": scan_flop / (k_ms * 1e-3) / 1e12 / PEAK_MFMA_F32, "traffic": None,
+                     "kernel_ms": k_ms, "all_kernels_ms": launched_ms, "flop_per_launch": scan_flop,
+                     "solve_flop": solve_flop, "bytes_per_step": nbytes},
     }
     if cpu is not None:
         # a bounded sample: the first n tokens of every head through the
         # reference's deltaStep with perKeyDecay, one thread (the reference
         # spreads heads over its pool; the sample's rate is per thread)
         O, ref, kind, threads = cpu
-        n = 2048
+        n = S
         qh = q[:n].float().cpu().numpy()
         kh = k[:n].float().cpu().numpy()
         vh = v[:n].float().cpu().numpy()
@@ -389,7 +397,7 @@ def kda_workload(args, cpu):
             what = "the C restatement of deltaStep (perKeyDecay)"
         dt_s = time.perf_counter() - t
         res["cpu_baseline"] = {"value": nbytes * (n / S) / dt_s / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
-                               "sample": f"the first {n} of 16384 tokens x 32 heads, single-threaded "
+                               "sample": f"all {n} tokens x 32 heads, single-threaded "
                                          f"({dt_s:.1f} s): {what}"}
     return res
 
