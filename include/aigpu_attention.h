@@ -283,6 +283,41 @@ typedef struct AiGpuGdnGatedNorm {
 AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm* args);
 
 /* ------------------------------------------------------------------------ */
+/* 7. Projections (DeviceABI.h:101-112): c[m][n] = a[m][k] . b[n][k]^T, with */
+/*    a and c host fp32 and b a device weight from aigpu_upload, in the     */
+/*    reference's four encodings (Quant.hpp): fp32, bf16, Q8 (int8 codes,   */
+/*    one fp32 scale per 32) and Q4 (two codes a byte, byte j of a block    */
+/*    holding codes j and j+16, offset 8; one fp32 scale per 32). They      */
+/*    return nothing, as the reference's do; failures set aigpu_last_error.  */
+/* ------------------------------------------------------------------------ */
+AIGPU_ABI void aigpu_matmul_nt(const float* a, const void* b, float* c,
+                               uint64_t m, uint64_t k, uint64_t n);            /* DeviceABI.h:101 */
+AIGPU_ABI void aigpu_matmul_nt_bf16(const float* a, const void* b, float* c,
+                                    uint64_t m, uint64_t k, uint64_t n);       /* DeviceABI.h:104 */
+AIGPU_ABI void aigpu_matmul_nt_q8(const float* a, const void* b, const void* scales, float* c,
+                                  uint64_t m, uint64_t k, uint64_t n);         /* DeviceABI.h:107 */
+AIGPU_ABI void aigpu_matmul_nt_q4(const float* a, const void* b, const void* scales, float* c,
+                                  uint64_t m, uint64_t k, uint64_t n);         /* DeviceABI.h:111 */
+
+/* The device form of the same product (no counterpart in the reference,
+   whose matmul stages a and c through the host every call): every pointer
+   is device memory, the bias is optional, and accumulate = 1 adds the
+   product into c (a residual add). */
+enum { AIGPU_W_F32 = 0, AIGPU_W_BF16 = 1, AIGPU_W_Q8 = 2, AIGPU_W_Q4 = 3 };
+typedef struct AiGpuMatmul {
+    const float* a;           /* [m][k] fp32 */
+    const void* b;            /* [n][k] weights in `type` */
+    const float* scales;      /* [n][k/32] for Q8 / Q4 */
+    const float* bias;        /* [n] or NULL */
+    float* c;                 /* [m][ldc] fp32 */
+    uint32_t type;            /* AIGPU_W_* (AiGpuDenseWeight::type) */
+    uint32_t accumulate;
+    uint64_t m, k, n, ldc;    /* ldc 0 means n */
+    void* stream;
+} AiGpuMatmul;
+AIGPU_ABI int aigpu_matmul_device(const AiGpuMatmul* args);
+
+/* ------------------------------------------------------------------------ */
 /* Per-kernel timing. With profiling on, every launch is bracketed by a pair */
 /* of hipEvents on the stream it runs on; aigpu_profile_read synchronises    */
 /* and reports the summed device time and launch count of kernels whose name */

@@ -79,6 +79,11 @@ class AiGpuKda(C.Structure):
                 ("valueDim", _u64), ("stream", _vp)]
 
 
+class AiGpuMatmul(C.Structure):
+    _fields_ = [("a", _vp), ("b", _vp), ("scales", _vp), ("bias", _vp), ("c", _vp), ("type", _u32),
+                ("accumulate", _u32), ("m", _u64), ("k", _u64), ("n", _u64), ("ldc", _u64), ("stream", _vp)]
+
+
 class AiGpuGdnConv(C.Structure):
     _fields_ = [("in_", _vp), ("ba", _vp), ("kernel", _vp), ("window", _vp), ("q", _vp), ("k", _vp),
                 ("v", _vp), ("z", _vp), ("a", _vp), ("b", _vp),
@@ -117,6 +122,11 @@ SIGNATURES = {
     "aigpu_decode_attention_host": (C.c_int, [C.POINTER(AiGpuDecode)]),
     "aigpu_gdn_conv": (C.c_int, [C.POINTER(AiGpuGdnConv)]),
     "aigpu_kda_rule": (C.c_int, [C.POINTER(AiGpuKda)]),
+    "aigpu_matmul_nt": (None, [_vp, _vp, _vp, _u64, _u64, _u64]),
+    "aigpu_matmul_nt_bf16": (None, [_vp, _vp, _vp, _u64, _u64, _u64]),
+    "aigpu_matmul_nt_q8": (None, [_vp, _vp, _vp, _vp, _u64, _u64, _u64]),
+    "aigpu_matmul_nt_q4": (None, [_vp, _vp, _vp, _vp, _u64, _u64, _u64]),
+    "aigpu_matmul_device": (C.c_int, [C.POINTER(AiGpuMatmul)]),
     "aigpu_gdn_gated_norm": (C.c_int, [C.POINTER(AiGpuGdnGatedNorm)]),
     "aigpu_gated_delta_rule": (C.c_int, [C.POINTER(AiGpuDeltaRule)]),
     "aigpu_gated_delta_rule_host": (C.c_int, [C.POINTER(AiGpuDeltaRule)]),
@@ -380,3 +390,59 @@ def kda_rule(q, k, v, g, beta, state, out, normalize=True, f=None, b=None, a_log
                     stream=_stream(stream))
     _check(lib().aigpu_kda_rule(C.byref(args)))
     return out
+
+
+WEIGHT_TYPES = {"f32": 0, "bf16": 1, "q8": 2, "q4": 3}
+
+
+def matmul(a, b, out, kind, scales=None, bias=None, accumulate=False, stream=None):
+    """Device form of the projection: out[m][n] (+)= a[m][k] . w[n][k]^T (+ bias).
+    a, out fp32 torch tensors; b the weight bytes as a torch tensor (fp32,
+    bf16, int8 codes, or uint8 packed 4-bit); kind one of WEIGHT_TYPES."""
+    for t, n in ((a, "a"), (b, "b"), (scales, "scales"), (bias, "bias")):
+        _need(t, n)
+    if not out.is_cuda or out.dim() != 2 or out.stride(1) != 1:
+        raise ValueError("out must be a GPU tensor with unit column stride")
+    m, k = a.shape
+    n = out.shape[1]
+    args = AiGpuMatmul(a=_ptr(a), b=_ptr(b), scales=_ptr(scales), bias=_ptr(bias), c=_ptr(out),
+                       type=WEIGHT_TYPES[kind], accumulate=1 if accumulate else 0, m=m, k=k, n=n,
+                       ldc=out.stride(0), stream=_stream(stream))
+    _check(lib().aigpu_matmul_device(C.byref(args)))
+    return out
+
+
+def matmul_host(a, b_device, kind, n, scales_device=None):
+    """The reference's host-staged aigpu_matmul_nt*: a numpy fp32 [m][k]; the
+    weight (and scales) as device pointers (ints) from upload(); returns c."""
+    import numpy as np
+    a = np.ascontiguousarray(a, np.float32)
+    m, k = a.shape
+    c = np.zeros((m, n), np.float32)
+    L = lib()
+    if kind == "f32":
+        L.aigpu_matmul_nt(a.ctypes.data, b_device, c.ctypes.data, m, k, n)
+    elif kind == "bf16":
+        L.aigpu_matmul_nt_bf16(a.ctypes.data, b_device, c.ctypes.data, m, k, n)
+    elif kind == "q8":
+        L.aigpu_matmul_nt_q8(a.ctypes.data, b_device, scales_device, c.ctypes.data, m, k, n)
+    else:
+        L.aigpu_matmul_nt_q4(a.ctypes.data, b_device, scales_device, c.ctypes.data, m, k, n)
+    err = L.aigpu_last_error()
+    if err:   # the host forms return nothing; a failure leaves its reason here
+        raise RuntimeError(err.decode() if isinstance(err, bytes) else str(err))
+    return c
+
+
+def upload(array):
+    """aigpu_upload of a numpy array's bytes; returns the device pointer (int)"""
+    import numpy as np
+    a = np.ascontiguousarray(array)
+    ptr = lib().aigpu_upload(a.ctypes.data, a.nbytes)
+    if not ptr:
+        _check(0)
+    return ptr
+
+
+def release(ptr, nbytes):
+    lib().aigpu_release(ptr, nbytes)

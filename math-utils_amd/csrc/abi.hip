@@ -648,3 +648,90 @@ AIGPU_ABI int aigpu_kda_rule(const AiGpuKda* args) {
     p.valueDim = args->valueDim;
     return aigpu::launch_kda(p, as_stream(args->stream)) ? 1 : 0;
 }
+
+namespace {
+
+/* the host-staged product of DeviceABI.h's aigpu_matmul_nt* (Kernels.hip
+   dispatch: a in, kernel, c out, each timed into the counters) */
+void matmul_host(const float* a, const void* b, const void* scales, float* c, uint64_t m, uint64_t k, uint64_t n,
+                 int type) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return;
+    if (!a || !b || !c || (type >= 2 && !scales)) {
+        ctx.error = "matmul: null tensor";
+        return;
+    }
+    if (m == 0 || n == 0) return;
+    if (m > 0xFFFFFFFFull || k > 0xFFFFFFFFull || n > 0xFFFFFFFFull || k == 0) {
+        ctx.error = "matmul: dimensions out of range";
+        return;
+    }
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const size_t inBytes = m * k * 4, outBytes = m * n * 4;
+    char* in = static_cast<char*>(ctx.grow(aigpu::SLOT_STAGE_IN, padded(inBytes)));
+    float* dC = static_cast<float*>(ctx.grow(aigpu::SLOT_STAGE_OUT, outBytes));
+    if (!in || !dC) return;
+    size_t at = 0;
+    const float* dA = static_cast<const float*>(stage_in(ctx, in, at, a, inBytes));
+    if (!dA) return;
+    aigpu::GemvParams p{};
+    p.a = dA;
+    p.w = b;
+    p.scales = static_cast<const float*>(scales);
+    p.out = dC;
+    p.type = type;
+    p.m = uint32_t(m);
+    p.k = uint32_t(k);
+    p.n = uint32_t(n);
+    p.ldo = uint32_t(n);
+    const Clock::time_point mark = Clock::now();
+    if (!aigpu::launch_gemv(p, nullptr) || !finish(ctx, mark)) return;
+    if (copy_out(ctx, c, dC, outBytes)) ctx.error.clear();
+}
+
+} // namespace
+
+extern "C" {
+
+AIGPU_ABI void aigpu_matmul_nt(const float* a, const void* b, float* c, uint64_t m, uint64_t k, uint64_t n) {
+    matmul_host(a, b, nullptr, c, m, k, n, 0);
+}
+
+AIGPU_ABI void aigpu_matmul_nt_bf16(const float* a, const void* b, float* c, uint64_t m, uint64_t k, uint64_t n) {
+    matmul_host(a, b, nullptr, c, m, k, n, 1);
+}
+
+AIGPU_ABI void aigpu_matmul_nt_q8(const float* a, const void* b, const void* scales, float* c, uint64_t m,
+                                  uint64_t k, uint64_t n) {
+    matmul_host(a, b, scales, c, m, k, n, 2);
+}
+
+AIGPU_ABI void aigpu_matmul_nt_q4(const float* a, const void* b, const void* scales, float* c, uint64_t m,
+                                  uint64_t k, uint64_t n) {
+    matmul_host(a, b, scales, c, m, k, n, 3);
+}
+
+AIGPU_ABI int aigpu_matmul_device(const AiGpuMatmul* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("matmul: null arguments"), 0;
+    if (args->m > 0xFFFFFFFFull || args->k > 0xFFFFFFFFull || args->n > 0xFFFFFFFFull ||
+        args->ldc > 0xFFFFFFFFull)
+        return ctx.fail("matmul: dimensions out of range"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    aigpu::GemvParams p{};
+    p.a = args->a;
+    p.w = args->b;
+    p.scales = args->scales;
+    p.bias = args->bias;
+    p.out = args->c;
+    p.type = int(args->type);
+    p.accumulate = args->accumulate ? 1 : 0;
+    p.m = uint32_t(args->m);
+    p.k = uint32_t(args->k);
+    p.n = uint32_t(args->n);
+    p.ldo = uint32_t(args->ldc ? args->ldc : args->n);
+    return aigpu::launch_gemv(p, as_stream(args->stream)) ? 1 : 0;
+}
+
+} // extern "C"

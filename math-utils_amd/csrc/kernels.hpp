@@ -74,6 +74,19 @@ struct DeltaRuleParams {
 };
 bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream);
 
+// ---- projections: out[m][n] = a[m][k] . w[n][k] (+ bias) (+ out) ----
+struct GemvParams {
+    const float* a;       // [m][k] fp32
+    const void* w;        // [n][k] in `type`
+    const float* scales;  // [n][k/32] for Q8 and Q4
+    const float* bias;    // [n] or null
+    float* out;           // [m][ldo]
+    int type;             // 0 F32, 1 BF16, 2 Q8, 3 Q4 (AiGpuDenseWeight::type)
+    int accumulate;       // 1: out += a . w^T
+    uint32_t m, k, n, ldo;
+};
+bool launch_gemv(const GemvParams& p, hipStream_t stream);
+
 // ---- Kimi Delta Attention: the delta rule with per-key-channel decay ----
 struct KdaParams {
     const void* q;        // [count][keyHeads][keyDim], inType

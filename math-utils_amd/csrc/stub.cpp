@@ -43,6 +43,11 @@ AIGPU_ABI int aigpu_gated_delta_rule(const AiGpuDeltaRule*) { return 0; }
 AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule*) { return 0; }
 AIGPU_ABI int aigpu_gdn_conv(const AiGpuGdnConv*) { return 0; }
 AIGPU_ABI int aigpu_kda_rule(const AiGpuKda*) { return 0; }
+AIGPU_ABI void aigpu_matmul_nt(const float*, const void*, float*, uint64_t, uint64_t, uint64_t) {}
+AIGPU_ABI void aigpu_matmul_nt_bf16(const float*, const void*, float*, uint64_t, uint64_t, uint64_t) {}
+AIGPU_ABI void aigpu_matmul_nt_q8(const float*, const void*, const void*, float*, uint64_t, uint64_t, uint64_t) {}
+AIGPU_ABI void aigpu_matmul_nt_q4(const float*, const void*, const void*, float*, uint64_t, uint64_t, uint64_t) {}
+AIGPU_ABI int aigpu_matmul_device(const AiGpuMatmul*) { return 0; }
 AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm*) { return 0; }
 
 AIGPU_ABI void aigpu_profile(int) {}

@@ -661,3 +661,49 @@ void or_output_gate(float* out, const float* q, size_t count, size_t heads, size
             for (size_t d = 0; d < dim; ++d) o[d] *= or_sigmoid(g[d]);
         }
 }
+
+/* ---- projections ---- */
+
+void or_dequant(const void* codes, const float* scales, size_t outDim, size_t inDim, int type, float* out) {
+    const size_t blocks = inDim / 32;
+    for (size_t r = 0; r < outDim; ++r) {
+        const float* s = scales + r * blocks;
+        if (type == 2) {
+            const int8_t* q = (const int8_t*)codes + r * inDim;
+            for (size_t i = 0; i < blocks * 32; ++i) out[r * inDim + i] = (float)q[i] * s[i / 32];
+        } else {
+            const uint8_t* q = (const uint8_t*)codes + r * (inDim / 2);
+            for (size_t b = 0; b < blocks; ++b)
+                for (size_t j = 0; j < 16; ++j) {
+                    const uint8_t packed = q[b * 16 + j];
+                    out[r * inDim + b * 32 + j] = (float)((int)(packed & 0x0F) - 8) * s[b];
+                    out[r * inDim + b * 32 + j + 16] = (float)((int)(packed >> 4) - 8) * s[b];
+                }
+        }
+    }
+}
+
+void or_matmul_nt(const float* a, const void* w, const float* scales, const float* bias, float* out,
+                  size_t m, size_t k, size_t n, int type) {
+    float* row = (float*)malloc(sizeof(float) * k);
+    for (size_t j = 0; j < n; ++j) {
+        if (type == 0) {
+            memcpy(row, (const float*)w + j * k, sizeof(float) * k);
+        } else if (type == 1) {
+            const uint16_t* b = (const uint16_t*)w + j * k;
+            for (size_t t = 0; t < k; ++t) {
+                const uint32_t bits = (uint32_t)b[t] << 16;
+                memcpy(&row[t], &bits, 4);
+            }
+        } else {
+            const size_t bytes = type == 2 ? k : k / 2;
+            or_dequant((const uint8_t*)w + j * bytes, scales + j * (k / 32), 1, k, type, row);
+        }
+        for (size_t i = 0; i < m; ++i) {
+            double s = 0.0;
+            for (size_t t = 0; t < k; ++t) s += (double)a[i * k + t] * (double)row[t];
+            out[i * n + j] = (float)s + (bias ? bias[j] : 0.0f);
+        }
+    }
+    free(row);
+}

@@ -206,6 +206,20 @@ void or_kda_rule(const float* q, const float* k, const float* v, const float* g,
 void or_kda_gates(const float* f, const float* b, const float* aLog, const float* dtBias, int safeGate,
                   float lowerBound, float* g, float* beta, size_t count, size_t valueHeads, size_t KD);
 
+/* ---- projections ---- */
+/* dequantRange (Quant.hpp:528-549) of every row: type 2 (Q8) code * scale;
+   type 3 (Q4) byte j of a 32-block gives code j (low nibble) and code j+16
+   (high nibble), each minus 8, times the block's scale. codes [outDim][inDim]
+   (Q8) or [outDim][inDim/2] (Q4), scales [outDim][inDim/32]. */
+void or_dequant(const void* codes, const float* scales, size_t outDim, size_t inDim, int type, float* out);
+/* apply (LocalModel.hpp:1052-1078): out[m][n] = sum_k a[m][k] w[n][k] (+ bias[n]),
+   the weight widened (type 0 fp32, 1 bf16 bits << 16) or dequantised (2 Q8,
+   3 Q4) first; the products of fp32 values are summed in double, so the
+   result is the rounded exact sum (the reference's CPU and GPU paths each
+   sum in their own order). */
+void or_matmul_nt(const float* a, const void* w, const float* scales, const float* bias, float* out,
+                  size_t m, size_t k, size_t n, int type);
+
 /* number of threads the static pool would use given a request (<=0: all
    online CPUs in this process's affinity mask) */
 int or_threads(int requested);

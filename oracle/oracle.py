@@ -94,6 +94,8 @@ def lib():
         L.or_kda_gates.argtypes = [_f32p] * 4 + [C.c_int, C.c_float, _f32p, _f32p, _sz, _sz, _sz]
         L.or_output_gate.argtypes = [_f32p, _f32p, _sz, _sz, _sz, _sz]
         L.or_kda_rule.argtypes = [_f32p] * 7 + [_sz] * 5 + [C.c_int, C.c_int]
+        L.or_dequant.argtypes = [C.c_void_p, _f32p, _sz, _sz, C.c_int, _f32p]
+        L.or_matmul_nt.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_void_p, _f32p, _sz, _sz, _sz, C.c_int]
         L.or_threads.restype = C.c_int
         L.or_threads.argtypes = [C.c_int]
         _lib = L
@@ -118,6 +120,9 @@ def ref():
         R.ref_random.argtypes = [C.c_uint64, C.c_int, C.c_uint64, C.c_double, C.c_double, C.c_void_p]
         R.ref_gated_delta_rule.argtypes = [_f32p] * 7 + [C.c_uint64] * 5 + [C.c_int]
         R.ref_kda_rule.argtypes = [_f32p] * 7 + [C.c_uint64] * 5 + [C.c_int]
+        R.ref_quantize.restype = C.c_int
+        R.ref_quantize.argtypes = [_f32p, C.c_uint64, C.c_uint64, C.c_int, C.c_void_p, _f32p]
+        R.ref_dequant_rows.argtypes = [C.c_void_p, _f32p, C.c_uint64, C.c_uint64, C.c_int, _f32p]
         _ref = R
     return _ref
 
@@ -409,3 +414,62 @@ def ref_kda_rule(q, k, v, g, beta, state=None, normalize=True):
     R.ref_kda_rule(q.reshape(-1), k.reshape(-1), v.reshape(-1), g.reshape(-1), beta.reshape(-1),
                    st.reshape(-1), out.reshape(-1), S, Hk, Hv, KD, VD, int(bool(normalize)))
     return out, st
+
+
+# ---------------------------------------------------------------- projections
+WEIGHT_TYPES = {"f32": 0, "bf16": 1, "q8": 2, "q4": 3}
+
+
+def dequant(codes, scales, kind):
+    """dequantRange (Quant.hpp:528-549) restated: codes [n][k] int8 (q8) or
+    [n][k/2] uint8 (q4), scales [n][k/32] -> [n][k] fp32"""
+    codes = np.ascontiguousarray(codes)
+    scales = np.ascontiguousarray(scales, np.float32)
+    n = codes.shape[0]
+    k = codes.shape[1] * (2 if kind == "q4" else 1)
+    out = np.zeros((n, k), np.float32)
+    lib().or_dequant(codes.ctypes.data, scales.reshape(-1), n, k, WEIGHT_TYPES[kind], out.reshape(-1))
+    return out
+
+
+def matmul_nt(a, w, kind, scales=None, bias=None):
+    """apply (LocalModel.hpp:1052-1078) restated: a [m][k] fp32; w the weight
+    as stored ([n][k] fp32, bf16 bits as uint16, q8 int8 codes, or q4 uint8
+    [n][k/2]); the exact sum rounded to fp32, plus the bias."""
+    a = np.ascontiguousarray(a, np.float32)
+    w = np.ascontiguousarray(w)
+    m, k = a.shape
+    n = w.shape[0]
+    out = np.zeros((m, n), np.float32)
+    sc = None if scales is None else np.ascontiguousarray(scales, np.float32)
+    bi = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().or_matmul_nt(a.reshape(-1), w.ctypes.data, None if sc is None else sc.ctypes.data,
+                       None if bi is None else bi.ctypes.data, out.reshape(-1), m, k, n, WEIGHT_TYPES[kind])
+    return out
+
+
+def ref_quantize(src, kind):
+    """the reference's own ai::quant::quantize (oracle/_ref): (codes, scales)"""
+    R = ref()
+    if R is None:
+        raise RuntimeError("oracle/_ref is not built")
+    src = np.ascontiguousarray(src, np.float32)
+    n, k = src.shape
+    codes = np.zeros((n, k // 2), np.uint8) if kind == "q4" else np.zeros((n, k), np.int8)
+    scales = np.zeros((n, k // 32), np.float32)
+    if not R.ref_quantize(src.reshape(-1), n, k, 1 if kind == "q4" else 0, codes.ctypes.data, scales.reshape(-1)):
+        raise ValueError("the reference declines to quantise this shape")
+    return codes, scales
+
+
+def ref_dequant(codes, scales, kind):
+    R = ref()
+    if R is None:
+        raise RuntimeError("oracle/_ref is not built")
+    codes = np.ascontiguousarray(codes)
+    scales = np.ascontiguousarray(scales, np.float32)
+    n = codes.shape[0]
+    k = codes.shape[1] * (2 if kind == "q4" else 1)
+    out = np.zeros((n, k), np.float32)
+    R.ref_dequant_rows(codes.ctypes.data, scales.reshape(-1), n, k, 1 if kind == "q4" else 0, out.reshape(-1))
+    return out

@@ -13,6 +13,7 @@
                                ref_gated_delta_rule, the mixer's token loop)
       ai::kernels::Pool        include/ai/ThreadPool.hpp:33-124
       math::random::Random     include/math/Random.hpp:15-89
+      ai::quant::quantize, dequantRow   include/ai/Quant.hpp:420-450, 528-558
 */
 #include <sched.h>
 
@@ -139,4 +140,33 @@ void ref_kda_rule(const float* q, const float* k, const float* v, const float* g
                                    out + (t * valueHeads + h) * VD, prediction.data(), delta.data());
         }
 }
+/* ai::quant::quantize (Quant.hpp:420-450) of a float [outDim][inDim]
+   matrix: codes (Q8 one int8 per weight, Q4 two per byte) and scales
+   [outDim][inDim/32]. Returns 0 when the reference declines (inDim not a
+   multiple of 32). */
+int ref_quantize(const float* src, uint64_t outDim, uint64_t inDim, int q4, void* codes, float* scales) {
+    const auto t = ai::quant::quantize(src, size_t(outDim), size_t(inDim),
+                                       q4 ? ai::quant::Type::Q4 : ai::quant::Type::Q8);
+    if (!t.valid()) return 0;
+    const size_t stored = q4 ? size_t(outDim * inDim / 2) : size_t(outDim * inDim);
+    std::memcpy(codes, t.quants.get(), stored);
+    std::memcpy(scales, t.scales.get(), sizeof(float) * size_t(outDim * (inDim / 32)));
+    return 1;
+}
+
+/* ai::quant::dequantRow (Quant.hpp:528-558) of every row of a quantised
+   matrix given as codes and scales */
+void ref_dequant_rows(const void* codes, const float* scales, uint64_t outDim, uint64_t inDim, int q4, float* out) {
+    ai::quant::QuantTensor t;
+    t.type = q4 ? ai::quant::Type::Q4 : ai::quant::Type::Q8;
+    t.outDim = size_t(outDim);
+    t.inDim = size_t(inDim);
+    const size_t stored = q4 ? size_t(outDim * inDim / 2) : size_t(outDim * inDim);
+    t.quants = std::shared_ptr<int8_t[]>(new int8_t[stored]);
+    t.scales = std::shared_ptr<float[]>(new float[size_t(outDim * (inDim / 32))]);
+    std::memcpy(t.quants.get(), codes, stored);
+    std::memcpy(t.scales.get(), scales, sizeof(float) * size_t(outDim * (inDim / 32)));
+    for (size_t r = 0; r < size_t(outDim); ++r) ai::quant::dequantRow(t, r, out + r * size_t(inDim));
+}
+
 }

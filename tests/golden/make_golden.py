@@ -13,6 +13,8 @@ Contents (inputs and the reference's outputs):
   gqa_*           a seeded GQA case with cached history (start > 0)
   delta_*         kernels::deltaStep sequences, scalar and per-key decay
                   (Kernels.hpp:105-128)
+  quant_*         ai::quant::quantize's Q8 and Q4 codes and scales of a
+                  seeded matrix, and dequantRow of them (Quant.hpp:420-558)
 """
 import ctypes as C
 import os
@@ -93,6 +95,15 @@ def main():
             outs[t] = o
         out[tag + "_outs"] = outs
         out[tag + "_state"] = st.reshape(K, V)
+
+    # ai::quant::quantize and dequantRow (Quant.hpp:420-558) on a seeded matrix
+    src = O.fill_normal((6, 96), 41, "quant_src")
+    src[2, 5] = -4.0   # a block whose signed extreme is negative (Q4's scale sign)
+    out["quant_src"] = src
+    for kind in ("q8", "q4"):
+        codes, scales = O.ref_quantize(src, kind)
+        out[f"quant_{kind}_codes"], out[f"quant_{kind}_scales"] = codes, scales
+        out[f"quant_{kind}_dequant"] = O.ref_dequant(codes, scales, kind)
 
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "reference_kernels.npz")
     np.savez_compressed(path, **out)

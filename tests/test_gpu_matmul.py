@@ -1,0 +1,125 @@
+"""GPU parity of the projections (gemv_kernel behind aigpu_matmul_nt* and
+aigpu_matmul_device) against the oracle's restatement of apply
+(LocalModel.hpp:1052-1078) over the reference's weight encodings.
+
+Bar: fp32 outputs within 1e-5 of each dot product's absolute size,
+|got - want| <= 1e-5 * sum_k |a_k w_k| + 1e-6: the fp32 bar scaled to the
+magnitude the sum passes through (the reference's CPU and GPU paths also sum
+in different orders)."""
+import numpy as np
+import pytest
+
+from gpu_util import dev_f32, host, say
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def weights(n, k, kind, seed):
+    src = O.fill_normal((n, k), seed, "w")
+    if kind == "f32":
+        return src, None, src
+    if kind == "bf16":
+        bits = O.pack_bf16(src).reshape(n, k)
+        return bits, None, O.unpack_bf16(bits).reshape(n, k)
+    codes, scales = quantise(src, kind)
+    return codes, scales, O.dequant(codes, scales, kind)
+
+
+def quantise(src, kind):
+    """codes with per-block scales, as the reference's layout holds them"""
+    n, k = src.shape
+    blocks = src.reshape(n, k // 32, 32)
+    amax = np.abs(blocks).max(axis=2)
+    if kind == "q8":
+        scales = (amax / 127.0).astype(np.float32)
+        codes = np.clip(np.round(blocks / scales[..., None]), -127, 127).astype(np.int8).reshape(n, k)
+        return codes, scales
+    scales = (amax / 8.0).astype(np.float32)
+    q = np.clip(np.round(blocks / scales[..., None]) + 8, 0, 15).astype(np.uint8)
+    return (q[:, :, :16] | (q[:, :, 16:] << 4)).reshape(n, k // 2), scales
+
+
+def to_device(w):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(w).view(np.uint8).copy())
+    return t.cuda()
+
+
+def bound(a, dense):
+    return 1e-5 * (np.abs(a).astype(np.float64) @ np.abs(dense).astype(np.float64).T) + 1e-6
+
+
+@pytest.mark.parametrize("kind", ["f32", "bf16", "q8", "q4"])
+@pytest.mark.parametrize("m", [1, 3, 8, 13])
+def test_device_form(gpu, kind, m):
+    import torch
+    k, n = 1024, 1000
+    a = O.fill_normal((m, k), 7 + m, "a")
+    w, scales, dense = weights(n, k, kind, 8 + m)
+    bias = O.fill_normal((n,), 9, "bias")
+    out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    say("matmul", dict(kind=kind, m=m, k=k, n=n))
+    gpu.matmul(dev_f32(a), to_device(w), out, kind, scales=None if scales is None else dev_f32(scales),
+               bias=dev_f32(bias))
+    want = O.matmul_nt(a, w, kind, scales=scales, bias=bias)
+    err = np.abs(host(out) - want)
+    assert np.all(err <= bound(a, dense)), f"{kind} m={m}: max err {err.max()}"
+
+
+@pytest.mark.parametrize("kind", ["f32", "bf16", "q8", "q4"])
+def test_host_form_and_upload(gpu, kind):
+    """the reference's own entry points: host a and c, the weight from aigpu_upload"""
+    m, k, n = 2, 512, 333
+    a = O.fill_normal((m, k), 21, "a")
+    w, scales, dense = weights(n, k, kind, 22)
+    wptr = gpu.upload(w)
+    sptr = gpu.upload(scales) if scales is not None else None
+    try:
+        say("matmul host", dict(kind=kind))
+        got = gpu.matmul_host(a, wptr, kind, n, sptr)
+    finally:
+        gpu.release(wptr, np.ascontiguousarray(w).nbytes)
+        if sptr:
+            gpu.release(sptr, scales.nbytes)
+    want = O.matmul_nt(a, w, kind, scales=scales)
+    assert np.all(np.abs(got - want) <= bound(a, dense))
+
+
+def test_accumulate_and_row_stride(gpu):
+    """a residual add into a strided output: out[:, :n] += a . w^T"""
+    import torch
+    m, k, n = 4, 256, 96
+    a = O.fill_normal((m, k), 31, "a")
+    w, _, dense = weights(n, k, "bf16", 32)
+    base = O.fill_normal((m, 128), 33, "base")
+    out = dev_f32(base)
+    say("matmul accumulate", {})
+    gpu.matmul(dev_f32(a), to_device(w), out[:, :n], "bf16", accumulate=True)
+    got = host(out)
+    want = base.copy()
+    want[:, :n] += O.matmul_nt(a, w, "bf16")
+    assert np.all(np.abs(got[:, :n] - want[:, :n]) <= bound(a, dense) + 1e-6)
+    np.testing.assert_array_equal(got[:, n:], base[:, n:])
+
+
+@pytest.mark.parametrize("kind,k", [("bf16", 100), ("f32", 98)])
+def test_unaligned_rows_take_the_scalar_path(gpu, kind, k):
+    import torch
+    m, n = 2, 50
+    a = O.fill_normal((m, k), 41, "a")
+    w, _, dense = weights(n, k, kind, 42)
+    out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    say("matmul scalar", dict(kind=kind, k=k))
+    gpu.matmul(dev_f32(a), to_device(w), out, kind)
+    assert np.all(np.abs(host(out) - O.matmul_nt(a, w, kind)) <= bound(a, dense))
+
+
+def test_rejects_quantised_k_not_multiple_of_32(gpu):
+    import torch
+    a = dev_f32(np.zeros((1, 48), np.float32))
+    w = torch.zeros((4, 48), dtype=torch.int8, device="cuda")
+    s = dev_f32(np.ones((4, 1), np.float32))
+    out = torch.zeros((1, 4), dtype=torch.float32, device="cuda")
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        gpu.matmul(a, w, out, "q8", scales=s)
