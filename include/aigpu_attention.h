@@ -318,6 +318,46 @@ typedef struct AiGpuMatmul {
 AIGPU_ABI int aigpu_matmul_device(const AiGpuMatmul* args);
 
 /* ------------------------------------------------------------------------ */
+/* 8. The resident single-token decoder (DeviceABI.h:114-157), the same     */
+/*    structs and entry points: a dense RMSNorm / RoPE / SwiGLU model kept   */
+/*    on the device; LocalModel::residentDecode (LocalModel.hpp:3598-3645)   */
+/*    is the caller. Weight codes and scales are device pointers (from      */
+/*    aigpu_upload) and stay the caller's; norms, biases, rotary            */
+/*    frequencies and the cache arrays are host pointers, copied in.        */
+/* ------------------------------------------------------------------------ */
+typedef struct AiGpuDenseWeight {       /* DeviceABI.h:116-121 */
+    const void* codes;
+    const void* scales;
+    uint32_t type, inDim, outDim;       /* F32=0, BF16=1, Q8=2, Q4=3 */
+    const float* bias;                  /* optional, copied at creation */
+} AiGpuDenseWeight;
+typedef struct AiGpuDenseLayer {        /* DeviceABI.h:122-129 */
+    AiGpuDenseWeight q, k, v, o, gate, up, down;
+    const float* inputNorm;
+    const float* postNorm;
+    const float* qNorm;
+    const float* kNorm;
+    uint32_t window;                    /* 0 = full causal attention */
+} AiGpuDenseLayer;
+typedef struct AiGpuDenseConfig {       /* DeviceABI.h:130-138 */
+    uint32_t hidden, layers, heads, kvHeads, headDim, intermediate;
+    uint32_t capacity, rotaryDims, vocab;
+    float epsilon, theta;
+    const float* finalNorm;
+    AiGpuDenseWeight head;
+    const float* rotaryFrequencies;     /* rotaryDims/2 entries; optional */
+} AiGpuDenseConfig;
+AIGPU_ABI int aigpu_dense_supported(void);                                      /* DeviceABI.h:144 */
+AIGPU_ABI void* aigpu_dense_create(const AiGpuDenseConfig* config,
+                                   const AiGpuDenseLayer* layers, const float* const* keys,
+                                   const float* const* values, uint32_t length);  /* DeviceABI.h:145 */
+AIGPU_ABI void aigpu_dense_release(void* context);                             /* DeviceABI.h:148 */
+AIGPU_ABI void aigpu_dense_decode(void* context, const float* embedding,
+                                  float* logits, uint32_t position);           /* DeviceABI.h:149 */
+AIGPU_ABI void aigpu_dense_read_cache(void* context, float* const* keys,
+                                      float* const* values, uint32_t length);  /* DeviceABI.h:151 */
+
+/* ------------------------------------------------------------------------ */
 /* Per-kernel timing. With profiling on, every launch is bracketed by a pair */
 /* of hipEvents on the stream it runs on; aigpu_profile_read synchronises    */
 /* and reports the summed device time and launch count of kernels whose name */

@@ -446,3 +446,108 @@ def upload(array):
 
 def release(ptr, nbytes):
     lib().aigpu_release(ptr, nbytes)
+
+
+# ---------------------------------------------------------------- 8. resident decoder
+class AiGpuDenseWeight(C.Structure):
+    _fields_ = [("codes", _vp), ("scales", _vp), ("type", _u32), ("inDim", _u32), ("outDim", _u32), ("bias", _vp)]
+
+
+class AiGpuDenseLayer(C.Structure):
+    _fields_ = [("q", AiGpuDenseWeight), ("k", AiGpuDenseWeight), ("v", AiGpuDenseWeight),
+                ("o", AiGpuDenseWeight), ("gate", AiGpuDenseWeight), ("up", AiGpuDenseWeight),
+                ("down", AiGpuDenseWeight), ("inputNorm", _vp), ("postNorm", _vp), ("qNorm", _vp),
+                ("kNorm", _vp), ("window", _u32)]
+
+
+class AiGpuDenseConfig(C.Structure):
+    _fields_ = [("hidden", _u32), ("layers", _u32), ("heads", _u32), ("kvHeads", _u32), ("headDim", _u32),
+                ("intermediate", _u32), ("capacity", _u32), ("rotaryDims", _u32), ("vocab", _u32),
+                ("epsilon", _f32), ("theta", _f32), ("finalNorm", _vp), ("head", AiGpuDenseWeight),
+                ("rotaryFrequencies", _vp)]
+
+
+SIGNATURES.update({
+    "aigpu_dense_supported": (C.c_int, []),
+    "aigpu_dense_create": (_vp, [C.POINTER(AiGpuDenseConfig), C.POINTER(AiGpuDenseLayer), _vp, _vp, _u32]),
+    "aigpu_dense_release": (None, [_vp]),
+    "aigpu_dense_decode": (None, [_vp, _vp, _vp, _u32]),
+    "aigpu_dense_read_cache": (None, [_vp, _vp, _vp, _u32]),
+})
+
+
+class DenseDecoder:
+    """The resident decoder through the reference's own entry points.
+
+    weights: dicts with "ptr" (device pointer of the stored weight, e.g. from
+    upload()), "kind", "scales_ptr" (Q8/Q4), "in", "out", "bias" (numpy or
+    None). layers: dicts q, k, v, o, gate, up, down (weights), input_norm,
+    post_norm, q_norm, k_norm (numpy or None), window. keys / values: per
+    layer numpy fp32 [capacity][kv_heads * head_dim], the first `length`
+    positions valid."""
+
+    def __init__(self, cfg, layers, head, final_norm, keys, values, length, freqs=None):
+        import numpy as np
+        keep = []
+        L = lib()
+
+        def arr(x):
+            if x is None:
+                return None
+            a = np.ascontiguousarray(x, np.float32)
+            keep.append(a)
+            return a.ctypes.data
+
+        def w(d):
+            return AiGpuDenseWeight(codes=d["ptr"], scales=d.get("scales_ptr"), type=WEIGHT_TYPES[d["kind"]],
+                                    inDim=d["in"], outDim=d["out"], bias=arr(d.get("bias")))
+
+        self.cfg = cfg
+        self.nlayers = len(layers)
+        larr = (AiGpuDenseLayer * len(layers))()
+        for i, l in enumerate(layers):
+            larr[i] = AiGpuDenseLayer(q=w(l["q"]), k=w(l["k"]), v=w(l["v"]), o=w(l["o"]), gate=w(l["gate"]),
+                                      up=w(l["up"]), down=w(l["down"]), inputNorm=arr(l["input_norm"]),
+                                      postNorm=arr(l["post_norm"]), qNorm=arr(l.get("q_norm")),
+                                      kNorm=arr(l.get("k_norm")), window=l.get("window", 0))
+        c = AiGpuDenseConfig(hidden=cfg["hidden"], layers=len(layers), heads=cfg["heads"], kvHeads=cfg["kv_heads"],
+                             headDim=cfg["head_dim"], intermediate=cfg["intermediate"], capacity=cfg["capacity"],
+                             rotaryDims=cfg["rotary_dims"], vocab=cfg["vocab"], epsilon=cfg["eps"],
+                             theta=cfg["theta"], finalNorm=arr(final_norm), head=w(head),
+                             rotaryFrequencies=arr(freqs))
+        kp = (_vp * len(layers))(*[arr(k) for k in keys])
+        vp = (_vp * len(layers))(*[arr(v) for v in values])
+        self.handle = L.aigpu_dense_create(C.byref(c), larr, C.cast(kp, _vp), C.cast(vp, _vp), length)
+        del keep
+        if not self.handle:
+            _check(0)
+
+    def decode(self, embedding, position):
+        import numpy as np
+        e = np.ascontiguousarray(embedding, np.float32)
+        logits = np.zeros(self.cfg["vocab"], np.float32)
+        L = lib()
+        L.aigpu_dense_decode(self.handle, e.ctypes.data, logits.ctypes.data, position)
+        err = L.aigpu_last_error()
+        if err:
+            raise RuntimeError(err.decode())
+        return logits
+
+    def read_cache(self, length):
+        import numpy as np
+        kvw = self.cfg["kv_heads"] * self.cfg["head_dim"]
+        keys = [np.zeros((length, kvw), np.float32) for _ in range(self.nlayers)]
+        values = [np.zeros((length, kvw), np.float32) for _ in range(self.nlayers)]
+        kp = (_vp * self.nlayers)(*[k.ctypes.data for k in keys])
+        vp = (_vp * self.nlayers)(*[v.ctypes.data for v in values])
+        L = lib()
+        L.aigpu_dense_read_cache(self.handle, C.cast(kp, _vp), C.cast(vp, _vp), length)
+        err = L.aigpu_last_error()
+        if err:
+            raise RuntimeError(err.decode())
+        return keys, values
+
+    def close(self):
+        if self.handle:
+            lib().aigpu_dense_release(self.handle)
+            self.handle = None

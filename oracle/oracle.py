@@ -473,3 +473,56 @@ def ref_dequant(codes, scales, kind):
     out = np.zeros((n, k), np.float32)
     R.ref_dequant_rows(codes.ctypes.data, scales.reshape(-1), n, k, 1 if kind == "q4" else 0, out.reshape(-1))
     return out
+
+
+# ------------------------------------------------------ resident dense decoder
+def rms_norm_row(x, gamma, eps, offset=0.0):
+    """rmsNormRow (LocalModel.hpp:1341-1348) restated by or_rms_norm_row"""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros_like(x)
+    lib().or_rms_norm_row(x, np.ascontiguousarray(gamma, np.float32), out, x.size, eps, offset)
+    return out
+
+
+def dense_decode(cfg, layers, head, final_norm, embedding, keys, values, position):
+    """One token through a dense RMSNorm / RoPE / SwiGLU model, as
+    LocalModel::forward runs it for count = 1 (LocalModel.hpp:3705-3799):
+    per layer the input norm, attentionMixer (q/k/v projections, per-head
+    q/k RMSNorm, RoPE, cache append, kernels::attention, the output
+    projection; :2575-2670), the residual add, the post-attention norm, the
+    SwiGLU MLP (swiglu = silu(gate) * up, :3282-3288, :3760-3770) and the
+    second residual add; then the final norm and the head (:3793-3799).
+
+    cfg: dict hidden, heads, kv_heads, head_dim, rotary_dims, eps, freqs.
+    layers: dicts with weights q, k, v, o, gate, up, down, each a tuple
+    (stored array, kind, scales, bias), norms input_norm, post_norm, q_norm,
+    k_norm (None for none) and window. keys / values: per layer
+    [capacity][kv_heads * head_dim] fp32, written at `position`.
+    Every step is a pinned primitive of this module; returns the logits."""
+    H, nH, nKV, D = cfg["hidden"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    eps = cfg["eps"]
+    x = np.ascontiguousarray(embedding, np.float32).reshape(1, H).copy()
+
+    def proj(inp, w):
+        arr, kind, scales, bias = w
+        return matmul_nt(inp, arr, kind, scales=scales, bias=bias)
+
+    for li, L in enumerate(layers):
+        h = rms_norm_row(x[0], L["input_norm"], eps).reshape(1, H)
+        q = proj(h, L["q"])
+        k = proj(h, L["k"])
+        v = proj(h, L["v"])
+        q, k = qk_norm_rope(q, k, 1, position, nH, nKV, D, D, L["q_norm"], L["k_norm"], eps,
+                            cfg["freqs"], cfg["rotary_dims"])
+        keys[li][position] = k.reshape(-1)
+        values[li][position] = v.reshape(-1)
+        attn = attention(q.reshape(-1), keys[li][:position + 1], values[li][:position + 1], 1, position,
+                         nH, nKV, D, D, L["window"])
+        x = x + proj(attn.reshape(1, nH * D), L["o"])
+        h = rms_norm_row(x[0], L["post_norm"], eps).reshape(1, H)
+        g = proj(h, L["gate"])
+        u = proj(h, L["up"])
+        g = np.array([silu(float(a)) for a in g.reshape(-1)], np.float32).reshape(g.shape) * u
+        x = x + proj(g, L["down"])
+    last = rms_norm_row(x[0], final_norm, eps).reshape(1, H)
+    return proj(last, head).reshape(-1)
