@@ -2,7 +2,7 @@
 """bench.py - throughput of the MI355X attention hot path against its roofline,
 with the reference's CPU path timed beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|delta|gdn|kda|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|delta|gdn|kda|dense|all]
 
 A step is one call of the hot path over one batch of synthetic, HBM-resident
 input. The headline workload (config.workload) is configs[2] of BASELINE.json,
@@ -50,7 +50,7 @@ def parse():
     # the GPU's clock ramps over the first ~15 ms of sustained work: a short
     # warm-up times the ramp rather than the kernels
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "kda", "all"])
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "kda", "dense", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of each baseline sample")
@@ -402,6 +402,72 @@ def kda_workload(args, cpu):
     return res
 
 
+def dense_workload(args, cpu):
+    """the resident decoder (aigpu_dense_*) on a Qwen3-0.6B-shaped model, bf16
+    weights, one token per step at positions from 4096 on"""
+    import numpy as np
+    import torch
+    import aigpu
+    H, NL, NH, KV, D, I, V = 1024, 28, 16, 8, 128, 3072, 151936
+    start = 4096
+    cap = start + args.warmup + 2 * args.steps + 8   # time_steps runs the steps twice
+    gen = torch.Generator(device="cuda").manual_seed(7)
+
+    def w(n, k):
+        t = (torch.randn((n, k), generator=gen, device="cuda") / k ** 0.5).to(torch.bfloat16)
+        keep.append(t)
+        return {"ptr": t.data_ptr(), "kind": "bf16", "in": k, "out": n}
+
+    keep = []
+    rng = np.random.default_rng(7)
+    layers = []
+    for _ in range(NL):
+        layers.append({"q": w(NH * D, H), "k": w(KV * D, H), "v": w(KV * D, H), "o": w(H, NH * D),
+                       "gate": w(I, H), "up": w(I, H), "down": w(H, I),
+                       "input_norm": rng.uniform(0.5, 1.5, H).astype(np.float32),
+                       "post_norm": rng.uniform(0.5, 1.5, H).astype(np.float32),
+                       "q_norm": rng.uniform(0.5, 1.5, D).astype(np.float32),
+                       "k_norm": rng.uniform(0.5, 1.5, D).astype(np.float32), "window": 0})
+    head = w(V, H)
+    cache = rng.standard_normal((cap, KV * D)).astype(np.float32)
+    cfg = dict(hidden=H, heads=NH, kv_heads=KV, head_dim=D, intermediate=I, vocab=V, capacity=cap,
+               rotary_dims=D, eps=1e-6, theta=1e6)
+    dec = aigpu.DenseDecoder(cfg, layers, head, rng.uniform(0.5, 1.5, H).astype(np.float32),
+                             [cache] * NL, [cache] * NL, start)
+    del cache
+    emb = rng.standard_normal(H).astype(np.float32)
+    state = {"pos": start}
+
+    def step():
+        dec.decode(emb, state["pos"])
+        state["pos"] += 1
+
+    step_ms, g_ms, launched_ms = time_steps(step, args.steps, args.warmup, "dense_gemv_kernel")
+    gemv_total, gemv_n = aigpu.profile_read("dense_gemv_kernel")   # pass 2 of time_steps
+    attn_total, attn_n = aigpu.profile_read("dense_attn_kernel")
+    dec.close()
+    del keep
+    weight_bytes = 2.0 * (NL * (H * NH * D + 2 * H * KV * D + NH * D * H + 3 * H * I) + V * H)
+    pos_mid = start + args.warmup + args.steps * 1.5   # mean position of the profiled steps
+    kv_bytes = NL * 2.0 * pos_mid * KV * D * 4
+    gemv_ms = gemv_total / args.steps
+    attn_ms = attn_total / args.steps
+    return {
+        "workload": "resident decoder, Qwen3-0.6B shape (28 layers, 16q/8kv x 128, 3072 MLP, 151936 vocab), "
+                    "bf16 weights, fp32 cache, positions 4096+",
+        "dtype": "f32", "value": 1e3 / step_ms, "unit": "tokens/s", "ms_per_step": step_ms,
+        "kernels_ms_per_step": launched_ms, "bytes_per_step": weight_bytes + kv_bytes,
+        "step_hbm_gbs": (weight_bytes + kv_bytes) / (step_ms * 1e-3) / 1e9,
+        "attention_ms_per_step": attn_ms,
+        "attention_gbs": kv_bytes / (attn_ms * 1e-3) / 1e9,
+        "roofline": {"kernel": "dense_gemv_kernel (the step's projections, weight bytes over their summed time)",
+                     "bound": "hbm", "achieved": weight_bytes / (gemv_ms * 1e-3) / 1e9, "peak": PEAK_HBM,
+                     "unit": "GB/s", "frac": weight_bytes / (gemv_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
+                     "gemv_ms_per_step": gemv_ms, "launches_per_step": gemv_n / args.steps,
+                     "weight_bytes": weight_bytes},
+    }
+
+
 def gdn_workload(args, cpu):
     """the steps either side of the recurrence at configs[4]'s shapes: the fused
     qkvz de-interleave + causal conv (K 4) + SiLU, then the gated norm"""
@@ -549,11 +615,13 @@ def main():
         extra["gdn_neighbours"] = gdn_workload(args, cpu)
     if args.workload in ("kda", "all"):
         extra["kda_rule"] = kda_workload(args, cpu)
+    if args.workload in ("dense", "all"):
+        extra["resident_decoder"] = dense_workload(args, cpu)
     if args.workload == "all":
         extra["others"] = small_workloads(args)
     if head is None:   # a single non-prefill workload becomes the line
         head = (extra.pop("decode", None) or extra.pop("delta_rule", None) or extra.pop("gdn_neighbours", None)
-                or extra.pop("kda_rule"))
+                or extra.pop("kda_rule", None) or extra.pop("resident_decoder"))
     line = {
         "metric": "attn TFLOP/s (prefill) & KV GB/s (decode) as % roofline, 1 MI355X vs host CPU",
         "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,

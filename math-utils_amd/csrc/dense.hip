@@ -6,21 +6,19 @@
 // (LocalModel.hpp:3598-3645) is the caller, and the step is LocalModel::
 // forward's layer loop for count = 1 (:3705-3799).
 //
-// Per layer, on one stream:
-//   dense_norm_kernel      x -> RMSNorm(x) * inputNorm
-//   gemv_kernel x3         q, k, v (+ bias)
-//   dense_qk_kernel        per head: q/k RMSNorm, RoPE at the position, and
-//                          the k, v rows appended to the fp32 cache
-//   dense_attn_kernel      split-K attention: one workgroup per (256
-//                          positions, kv head) for all of that kv head's query
-//                          heads, so each cached row is read once
-//   dense_merge_kernel     the splits' softmax partials combined per head
-//   gemv_kernel            x += o . attn
-//   dense_norm_kernel      RMSNorm(x) * postNorm
-//   gemv_kernel x2, dense_swiglu_kernel, gemv_kernel   x += down . (silu(gate) * up)
-// then the final norm and the head. The position is read from device memory
-// by every kernel that needs it, so the sequence does not depend on host
-// values that change between tokens.
+// Per layer, five launches on one stream:
+//   dense_gemv_kernel   q, k, v (+ bias) of RMSNorm(x) * inputNorm, the norm
+//                       computed by each wave from x
+//   dense_attn_kernel   per (span of positions, kv head): q/k RMSNorm and
+//                       RoPE at the position, the k, v rows appended to the
+//                       cache, split-K attention for all of the kv head's
+//                       query heads, and the merge by the last workgroup
+//   dense_gemv_kernel   x += o . attn
+//   dense_gemv_kernel   gate, up of RMSNorm(x) * postNorm
+//   dense_gemv_kernel   x += down . (silu(gate) * up)
+// then the head of RMSNorm(x) * finalNorm. The position is read from device
+// memory by the kernels that need it, so the sequence does not depend on
+// host values that change between tokens.
 //
 // The cache is the reference's own layout, fp32 [capacity][kvHeads * headDim]
 // per layer (what aigpu_dense_create copies in and aigpu_dense_read_cache
@@ -28,6 +26,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <initializer_list>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -35,15 +34,16 @@
 
 #include "context.hpp"
 #include "device.hpp"
+#include "gemv.hpp"
 #include "kernels.hpp"
 
 namespace aigpu {
 
 namespace {
 
-constexpr int SPLIT = 256;     // positions per attention workgroup
+constexpr int SPLIT = 128;     // positions per attention workgroup
 constexpr int MAX_DIM = 256;   // head dim
-constexpr int MAX_GROUP = 16;  // query heads per kv head
+constexpr int MAX_GROUP = 8;   // query heads per kv head
 
 struct DenseArgs {
     const uint32_t* pos;   // device: the position being decoded
@@ -51,181 +51,352 @@ struct DenseArgs {
     float eps;
 };
 
-/* RMSNorm of one row (rmsNormRow, LocalModel.hpp:1341-1348): out = x *
-   1/sqrt(mean(x^2) + eps) * gamma. One workgroup. */
-__global__ __launch_bounds__(1024) void dense_norm_kernel(const float* x, const float* gamma, float* out, uint32_t n,
-                                                          float eps) {
-    __shared__ float part[16];
-    float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
-    ss = wave_sum(ss);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-    for (uint32_t w = 0; w < blockDim.x / 64; ++w) tot += part[w];
-    const float inv = 1.0f / sqrtf(tot / float(n) + eps);
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * inv * gamma[i];
-}
+/* ---- projections with the step before them fused into the input ----
+   PRE 0: a = x;  PRE 1: a = RMSNorm(x) * gamma (rmsNormRow,
+   LocalModel.hpp:1341-1348), each wave computing the norm itself;
+   PRE 2: a = silu(x) * x2 (swiglu, :3282-3288).
+   Up to three weights of one encoding share the launch (q, k, v; gate, up):
+   rows [start_s, start_s + n_s) belong to segment s. */
+constexpr int DG_ROWS = 2;   // weight rows per wave
 
-/* one wave per head: blocks [0, heads) the query heads (normalised and
-   rotated in place), blocks [heads, heads + kvHeads) the key heads
-   (normalised, rotated and appended with their value rows) */
-__global__ __launch_bounds__(64) void dense_qk_kernel(DenseArgs a, float* q, const float* k, const float* v,
-                                                      const float* qNorm, const float* kNorm, const float* freqs,
-                                                      float* keys, float* values) {
-    __shared__ float row[MAX_DIM];
-    const int lane = threadIdx.x;
-    const uint32_t b = blockIdx.x, D = a.dim, pos = *a.pos;
-    const bool isQ = b < a.heads;
-    const uint32_t hh = isQ ? b : b - a.heads;
-    const float* src = isQ ? q + size_t(hh) * D : k + size_t(hh) * D;
-    for (uint32_t d = lane; d < D; d += WAVE) row[d] = src[d];
-    wave_sync();
-    norm_rope_row(row, int(D), isQ ? qNorm : kNorm, a.eps, 0.0f, freqs, int(a.rot), pos, lane);
-    const size_t kvW = size_t(a.kvHeads) * D;
-    if (isQ) {
-        for (uint32_t d = lane; d < D; d += WAVE) q[size_t(hh) * D + d] = row[d];
-    } else {
-        for (uint32_t d = lane; d < D; d += WAVE) {
-            keys[size_t(pos) * kvW + size_t(hh) * D + d] = row[d];
-            values[size_t(pos) * kvW + size_t(hh) * D + d] = v[size_t(hh) * D + d];
+struct DenseSeg {
+    const char* w;
+    const float* scales;
+    const float* bias;
+    float* out;
+    uint32_t n, start;
+};
+
+struct DenseGemvArgs {
+    DenseSeg seg[3];
+    int nseg, accumulate;
+    uint32_t rows, k;
+    const float* x;
+    const float* x2;
+    const float* gamma;
+    float eps;
+};
+
+template <int TYPE, int PRE>
+__global__ __launch_bounds__(256) void dense_gemv_kernel(DenseGemvArgs p) {
+    constexpr int E = piece_elems<TYPE>();
+    const int lane = threadIdx.x & 63;
+    const uint32_t row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * DG_ROWS;
+    if (row0 >= p.rows) return;   // whole wave leaves; no block barriers
+    int sg = 0;
+    if (p.nseg > 1 && row0 >= p.seg[1].start) sg = 1;
+    if (p.nseg > 2 && row0 >= p.seg[2].start) sg = 2;
+    const DenseSeg S = p.seg[sg];
+    const uint32_t r0 = row0 - S.start;   // DG_ROWS rows never straddle segments (every n is even)
+    const size_t rowBytes = size_t(p.k) * row_bytes_per_k_x2<TYPE>() / 2;
+    const uint32_t pieces = p.k / E, blocks = p.k / 32;
+
+    float inv = 1.0f;
+    if constexpr (PRE == 1) {
+        float ss = 0.0f;
+        for (uint32_t i = lane; i < p.k / 4; i += WAVE) {
+            const floatx4 v = reinterpret_cast<const floatx4*>(p.x)[i];
+            ss = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], fmaf(v[3], v[3], ss))));
+        }
+        inv = 1.0f / sqrtf(wave_sum(ss) / float(p.k) + p.eps);
+    }
+
+    float acc[DG_ROWS] = {};
+#pragma unroll 2
+    for (uint32_t c = lane; c < pieces; c += WAVE) {
+        u32x4 wv[DG_ROWS];
+        float sc[DG_ROWS];
+#pragma unroll
+        for (int r = 0; r < DG_ROWS; ++r) {
+            wv[r] = *reinterpret_cast<const u32x4*>(S.w + (r0 + r) * rowBytes + size_t(c) * 16);
+            sc[r] = TYPE == 2 ? S.scales[size_t(r0 + r) * blocks + (c >> 1)]
+                              : (TYPE == 3 ? S.scales[size_t(r0 + r) * blocks + c] : 1.0f);
+        }
+        float xa[E];
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+            const floatx4 v = *reinterpret_cast<const floatx4*>(p.x + size_t(c) * E + e);
+            if constexpr (PRE == 1) {
+                const floatx4 gm = *reinterpret_cast<const floatx4*>(p.gamma + size_t(c) * E + e);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xa[e + t] = v[t] * inv * gm[t];
+            } else if constexpr (PRE == 2) {
+                const floatx4 u = *reinterpret_cast<const floatx4*>(p.x2 + size_t(c) * E + e);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xa[e + t] = v[t] / (1.0f + expf(-v[t])) * u[t];
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xa[e + t] = v[t];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < DG_ROWS; ++r) {
+            const float d = piece_dot<TYPE>(wv[r], xa);
+            acc[r] = TYPE >= 2 ? fmaf(d, sc[r], acc[r]) : acc[r] + d;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < DG_ROWS; ++r) acc[r] = wave_sum(acc[r]);
+    if (lane < DG_ROWS) {
+        const uint32_t n = r0 + lane;
+        if (n < S.n) {
+            const float v = lane == 0 ? acc[0] : acc[DG_ROWS - 1];
+            float* o = S.out + n;
+            *o = (p.accumulate ? *o : 0.0f) + v + (S.bias ? S.bias[n] : 0.0f);
         }
     }
 }
 
-/* keys [first(pos), pos] in splits of SPLIT: workgroup (split s, kv head)
-   scores its positions for the G query heads of the kv head (lane = position
-   in each wave's 64), then accumulates P.V with the lanes on dimensions.
-   Each wave leaves a partial record per query head: max, sum, acc[D]. */
-__global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const float* q, const float* keys,
-                                                         const float* values, float* partial) {
+/* ---- attention ----
+   Keys [first(pos), pos] in chunks of SPLIT positions, the chunks dealt out
+   to at most MAX_SPLITS workgroups per kv head (chunksPer each, an online
+   softmax across them). Workgroup (split s, kv head):
+   - norms and rotates the G query heads of the kv head itself (attentionMixer,
+     LocalModel.hpp:2606-2648) and, in the split holding `pos`, the new key,
+     appending it and the value row to the cache;
+   - per chunk, scores its positions (lane = position, the key row's 16-byte
+     loads in flight; the new position from LDS) and accumulates P.V (lanes
+     on dimensions, each wave a quarter of the positions, eight rows in
+     flight);
+   - leaves one record per query head: max, sum, acc[D].
+   The last workgroup of each kv head to finish (a ticket per kv head, reset by
+   that workgroup) merges the records into the attention output. */
+constexpr int MAX_SPLITS = 64;
+
+__device__ __forceinline__ void attn_span(uint32_t pos, uint32_t window, uint32_t& first, uint32_t& splits,
+                                          uint32_t& chunksPer) {
+    first = window && pos + 1 > window ? pos + 1 - window : 0;
+    const uint32_t chunks = (pos + 1 - first + SPLIT - 1) / SPLIT;
+    chunksPer = (chunks + MAX_SPLITS - 1) / MAX_SPLITS;
+    splits = (chunks + chunksPer - 1) / chunksPer;
+}
+
+template <int DPL>   // head dimensions per lane: 2 (D <= 128) or 4 (D <= 256)
+__global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const float* qRaw, const float* kRaw,
+                                                         const float* vRaw, const float* qNorm, const float* kNorm,
+                                                         const float* freqs, float* keys, float* values,
+                                                         float* partial, uint32_t* tickets, float* attn) {
     __shared__ float qs[MAX_GROUP * MAX_DIM];
-    __shared__ float pr[4][MAX_GROUP][WAVE];
-    __shared__ float wm[4][MAX_GROUP], wl[4][MAX_GROUP];
+    __shared__ float kn[MAX_DIM], vn[MAX_DIM];
+    __shared__ float pr[MAX_GROUP][SPLIT];
+    __shared__ float wm[4][MAX_GROUP];
+    __shared__ floatx4 red[256];
+    __shared__ uint32_t last;
 
     const uint32_t pos = *a.pos;
-    const uint32_t first = a.window && pos + 1 > a.window ? pos + 1 - a.window : 0;
-    const uint32_t len = pos + 1 - first, splits = (len + SPLIT - 1) / SPLIT;
+    uint32_t first, splits, chunksPer;
+    attn_span(pos, a.window, first, splits, chunksPer);
     const uint32_t s = blockIdx.x, kvh = blockIdx.y;
     if (s >= splits) return;   // whole workgroup leaves before any barrier
     const uint32_t G = a.heads / a.kvHeads, D = a.dim;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const size_t kvW = size_t(a.kvHeads) * D;
     const float scale = 1.0f / sqrtf(float(D));
+    const bool holdsPos = s + 1 == splits;
 
-    for (uint32_t i = tid; i < G * D; i += 256) qs[i] = q[size_t(kvh) * G * D + i];
+    for (uint32_t i = tid; i < G * D; i += 256) qs[i] = qRaw[size_t(kvh) * G * D + i];
+    if (holdsPos)
+        for (uint32_t i = tid; i < D; i += 256) {
+            kn[i] = kRaw[size_t(kvh) * D + i];
+            vn[i] = vRaw[size_t(kvh) * D + i];
+        }
+    __syncthreads();
+    for (uint32_t g = w; g < G; g += 4) norm_rope_row(&qs[g * D], int(D), qNorm, a.eps, 0.0f, freqs, int(a.rot), pos, lane);
+    if (holdsPos && w == int(G % 4)) {
+        norm_rope_row(kn, int(D), kNorm, a.eps, 0.0f, freqs, int(a.rot), pos, lane);
+        for (uint32_t d = lane; d < D; d += WAVE) {
+            keys[size_t(pos) * kvW + size_t(kvh) * D + d] = kn[d];
+            values[size_t(pos) * kvW + size_t(kvh) * D + d] = vn[d];
+        }
+    }
     __syncthreads();
 
-    const uint32_t j = first + s * SPLIT + 64 * w + lane;
-    const bool live = j <= pos && 64 * w + lane < SPLIT;
-    float sc[MAX_GROUP];
+    float mrun[MAX_GROUP], lrun[MAX_GROUP], acc[MAX_GROUP][DPL];
 #pragma unroll
-    for (int g = 0; g < MAX_GROUP; ++g) sc[g] = 0.0f;
-    if (live) {
-        const float* kr = keys + size_t(j) * kvW + size_t(kvh) * D;
-        for (uint32_t d = 0; d < D; d += 4) {
-            const floatx4 kv4 = *reinterpret_cast<const floatx4*>(kr + d);
+    for (int g = 0; g < MAX_GROUP; ++g) {
+        mrun[g] = -INFINITY;
+        lrun[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[g][e] = 0.0f;
+    }
+    constexpr int HALF = DPL * 32;   // key elements per scoring thread: half a row
+    const uint32_t cBegin = s * chunksPer;
+    for (uint32_t c = cBegin; c < cBegin + chunksPer; ++c) {
+        const uint32_t j0 = first + c * SPLIT;
+        if (j0 > pos) break;   // uniform: the last split may hold fewer chunks
+        const uint32_t n = pos + 1 - j0 < uint32_t(SPLIT) ? pos + 1 - j0 : uint32_t(SPLIT);
+        const uint32_t jp = pos - j0 < n ? pos - j0 : 0xFFFFFFFFu;   // the new position, if in this chunk
+
+        // scores: threads 2t and 2t + 1 take the two halves of position t's key
+        // row, every 16-byte load of a half issued at once
+        const uint32_t t = uint32_t(tid) >> 1, hf = uint32_t(tid) & 1;
+        const bool live = t < n;
+        float sc[MAX_GROUP];
+#pragma unroll
+        for (int g = 0; g < MAX_GROUP; ++g) sc[g] = 0.0f;
+        if (live) {
+            floatx4 k4[HALF / 4];
+            if (t == jp) {
+#pragma unroll
+                for (int e = 0; e < HALF / 4; ++e)
+                    k4[e] = hf * HALF + 4 * e < D ? *reinterpret_cast<const floatx4*>(&kn[hf * HALF + 4 * e])
+                                                  : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            } else {
+                const float* kr = keys + size_t(j0 + t) * kvW + size_t(kvh) * D + hf * HALF;
+#pragma unroll
+                for (int e = 0; e < HALF / 4; ++e)
+                    k4[e] = hf * HALF + 4 * e < D ? *reinterpret_cast<const floatx4*>(kr + 4 * e)
+                                                  : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
 #pragma unroll
             for (int g = 0; g < MAX_GROUP; ++g) {
                 if (g < int(G)) {
-                    const floatx4 q4 = *reinterpret_cast<const floatx4*>(&qs[g * D + d]);
-                    sc[g] = fmaf(q4[0], kv4[0], fmaf(q4[1], kv4[1], fmaf(q4[2], kv4[2], fmaf(q4[3], kv4[3], sc[g]))));
+#pragma unroll
+                    for (int e = 0; e < HALF / 4; ++e) {
+                        if (hf * HALF + 4 * e < D) {
+                            const floatx4 q4 = *reinterpret_cast<const floatx4*>(&qs[g * D + hf * HALF + 4 * e]);
+                            sc[g] = fmaf(q4[0], k4[e][0],
+                                         fmaf(q4[1], k4[e][1], fmaf(q4[2], k4[e][2], fmaf(q4[3], k4[e][3], sc[g]))));
+                        }
+                    }
                 }
             }
         }
-    }
-    // per wave softmax partials
-    constexpr int DPL = MAX_DIM / WAVE;   // dims per lane
-    float acc[MAX_GROUP][DPL];
-#pragma unroll
-    for (int g = 0; g < MAX_GROUP; ++g) {
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[g][e] = 0.0f;
-        if (g < int(G)) {
-            const float sv = live ? sc[g] * scale : -INFINITY;
-            const float m = wave_max(sv);
-            const float p = live ? expf(sv - m) : 0.0f;
-            const float l = wave_sum(p);
-            pr[w][g][lane] = p;
-            if (lane == 0) {
-                wm[w][g] = m;
-                wl[w][g] = l;
-            }
-        }
-    }
-    wave_sync();
-    const uint32_t jw = first + s * SPLIT + 64 * w;   // this wave's first position
-    const uint32_t nw = jw <= pos ? (pos + 1 - jw < 64u ? pos + 1 - jw : 64u) : 0u;
-    for (uint32_t jj = 0; jj < nw; ++jj) {
-        const float* vr = values + size_t(jw + jj) * kvW + size_t(kvh) * D;
-        float vv[DPL];
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) vv[e] = (lane + 64 * e) < int(D) ? vr[lane + 64 * e] : 0.0f;
 #pragma unroll
         for (int g = 0; g < MAX_GROUP; ++g) {
             if (g < int(G)) {
-                const float p = pr[w][g][jj];
-#pragma unroll
-                for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(p, vv[e], acc[g][e]);
+                sc[g] += __shfl_xor(sc[g], 1, WAVE);
+                const float m = wave_max(live ? sc[g] * scale : -INFINITY);
+                if (lane == 0) wm[w][g] = m;
             }
         }
+        __syncthreads();
+        // the running max and the chunk's probabilities against it
+        float f[MAX_GROUP];
+#pragma unroll
+        for (int g = 0; g < MAX_GROUP; ++g) {
+            f[g] = 1.0f;
+            if (g < int(G)) {
+                const float cm = fmaxf(fmaxf(wm[0][g], wm[1][g]), fmaxf(wm[2][g], wm[3][g]));
+                const float mn = fmaxf(mrun[g], cm);
+                f[g] = expf(mrun[g] - mn);   // 0 on the first chunk
+                mrun[g] = mn;
+                if (hf == 0 && t < uint32_t(SPLIT)) pr[g][t] = live ? expf(sc[g] * scale - mn) : 0.0f;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < MAX_GROUP; ++g)
+            if (g < int(G)) {
+#pragma unroll
+                for (int e = 0; e < DPL; ++e) acc[g][e] *= f[g];
+                float l = 0.0f;
+                for (uint32_t u = lane; u < n; u += WAVE) l += pr[g][u];
+                lrun[g] = lrun[g] * f[g] + wave_sum(l);
+            }
+        // P.V: wave w takes the 32 positions w + 4u, every row load in flight;
+        // the new position from LDS
+        constexpr int PW = SPLIT / 4;
+        float vv[PW][DPL];
+#pragma unroll
+        for (int u = 0; u < PW; ++u) {
+            const uint32_t jr = uint32_t(w) + 4 * u;
+            // unused slots read row w: the cache is finite everywhere (zeroed at creation)
+            const float* vr = values + size_t(j0 + (jr < n ? jr : uint32_t(w) < n ? w : 0)) * kvW + size_t(kvh) * D;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) vv[u][e] = lane + 64 * e < int(D) ? vr[lane + 64 * e] : 0.0f;
+        }
+#pragma unroll
+        for (int g = 0; g < MAX_GROUP; ++g) {
+            if (g < int(G)) {
+#pragma unroll
+                for (int u = 0; u < PW; ++u) {
+                    const uint32_t jr = uint32_t(w) + 4 * u;
+                    const float p = (jr < n && jr != jp) ? pr[g][jr] : 0.0f;
+#pragma unroll
+                    for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(p, vv[u][e], acc[g][e]);
+                }
+            }
+        }
+        if (jp != 0xFFFFFFFFu && int(jp % 4) == w) {
+#pragma unroll
+            for (int g = 0; g < MAX_GROUP; ++g)
+                if (g < int(G)) {
+                    const float p = pr[g][jp];
+#pragma unroll
+                    for (int e = 0; e < DPL; ++e)
+                        if (lane + 64 * e < int(D)) acc[g][e] = fmaf(p, vn[lane + 64 * e], acc[g][e]);
+                }
+        }
+        __syncthreads();   // pr and wm are rewritten by the next chunk
     }
+
+    // the split's record per query head: the four waves' accumulators summed
     const size_t rec = size_t(D) + 2;
+    float* pbase = reinterpret_cast<float*>(red);
+#pragma unroll
+    for (int g = 0; g < MAX_GROUP; ++g) {
+        if (g >= int(G)) break;   // uniform
+#pragma unroll
+        for (int e = 0; e < DPL; ++e)
+            if (lane + 64 * e < int(D)) pbase[w * MAX_DIM + lane + 64 * e] = acc[g][e];
+        __syncthreads();
+        float* out = partial + ((size_t(kvh) * G + g) * a.maxSplits + s) * rec;
+        for (uint32_t d = tid; d < D; d += 256)
+            out[2 + d] = pbase[d] + pbase[MAX_DIM + d] + pbase[2 * MAX_DIM + d] + pbase[3 * MAX_DIM + d];
+        if (tid == 0) {
+            out[0] = mrun[g];
+            out[1] = lrun[g];
+        }
+        __syncthreads();
+    }
+
+    // the last workgroup of this kv head merges every split's records
+    if (tid == 0) {
+        __threadfence();
+        last = atomicAdd(&tickets[kvh], 1u) + 1 == splits ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    const uint32_t quads = D / 4, RL = 256 / quads;   // D % 4 == 0, D <= 256
+    const uint32_t dq = tid % quads, r = tid / quads;
     for (uint32_t g = 0; g < G; ++g) {
-        float* out = partial + ((size_t(kvh) * G + g) * a.maxSplits * 4 + size_t(s) * 4 + w) * rec;
-        if (lane == 0) {
-            out[0] = wm[w][g];
-            out[1] = wl[w][g];
+        const float* base = partial + (size_t(kvh) * G + g) * a.maxSplits * rec;
+        // every thread reads the (at most MAX_SPLITS) maxima and sums: lane i
+        // of each wave takes split i, a wave reduction combines them
+        float M = -INFINITY, L = 0.0f;
+        {
+            const float mi = lane < int(splits) ? base[lane * rec] : -INFINITY;
+            M = wave_max(mi);
+            L = wave_sum(lane < int(splits) ? base[lane * rec + 1] * expf(mi - M) : 0.0f);
         }
+        floatx4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (r < RL) {
+#pragma unroll 4
+            for (uint32_t i = r; i < splits; i += RL) {
+                const float fi = expf(base[i * rec] - M);
+                const floatx4 v = *reinterpret_cast<const floatx4*>(base + i * rec + 2 + 4 * dq);
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) {
-            const uint32_t d = lane + 64 * e;
-            if (d < D) out[2 + d] = acc[g][e];
+                for (int t = 0; t < 4; ++t) sum[t] = fmaf(v[t], fi, sum[t]);
+            }
         }
-    }
-}
-
-/* combines the partial records of every (split, wave) of one query head */
-__global__ __launch_bounds__(64) void dense_merge_kernel(DenseArgs a, const float* partial, float* attn) {
-    const uint32_t h = blockIdx.x, lane = threadIdx.x, D = a.dim;
-    const uint32_t pos = *a.pos;
-    const uint32_t first = a.window && pos + 1 > a.window ? pos + 1 - a.window : 0;
-    const uint32_t len = pos + 1 - first, splits = (len + SPLIT - 1) / SPLIT;
-    const size_t rec = size_t(D) + 2;
-    const float* base = partial + size_t(h) * a.maxSplits * 4 * rec;
-    const uint32_t parts = splits * 4;
-    float M = -INFINITY;
-    for (uint32_t i = 0; i < parts; ++i) M = fmaxf(M, base[i * rec]);
-    float L = 0.0f;
-    constexpr int DPL = MAX_DIM / WAVE;
-    float acc[DPL] = {};
-    for (uint32_t i = 0; i < parts; ++i) {
-        const float m = base[i * rec];
-        if (m == -INFINITY) continue;
-        const float f = expf(m - M);
-        L = fmaf(base[i * rec + 1], f, L);
+        red[tid] = sum;
+        __syncthreads();
+        if (tid < int(quads)) {
+            floatx4 t = red[tid];
+            for (uint32_t rr = 1; rr < RL; ++rr) {
+                const floatx4 u = red[rr * quads + tid];
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) {
-            const uint32_t d = lane + 64 * e;
-            if (d < D) acc[e] = fmaf(base[i * rec + 2 + d], f, acc[e]);
+                for (int k = 0; k < 4; ++k) t[k] += u[k];
+            }
+            const float inv = 1.0f / L;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) attn[(size_t(kvh) * G + g) * D + 4 * tid + k] = t[k] * inv;
         }
+        __syncthreads();
     }
-    const float inv = 1.0f / L;
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) {
-        const uint32_t d = lane + 64 * e;
-        if (d < D) attn[size_t(h) * D + d] = acc[e] * inv;
-    }
-}
-
-/* gate = silu(gate) * up (swiglu with no limit, LocalModel.hpp:3282-3288;
-   siluOf :1369) */
-__global__ __launch_bounds__(256) void dense_swiglu_kernel(float* gate, const float* up, uint32_t n) {
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) {
-        const float g = gate[i];
-        gate[i] = g / (1.0f + expf(-g)) * up[i];
-    }
+    if (tid == 0) tickets[kvh] = 0;   // ready for the next layer
 }
 
 struct DevWeight {
@@ -252,6 +423,7 @@ struct DenseModel {
     float *x = nullptr, *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
     float *gate = nullptr, *up = nullptr, *logits = nullptr, *partial = nullptr;
     uint32_t* pos = nullptr;
+    uint32_t* tickets = nullptr;   // per kv head, zero between launches
     std::vector<void*> owned;
     uint64_t bytes = 0;
 
@@ -281,8 +453,11 @@ struct DenseModel {
     DevWeight weight(const AiGpuDenseWeight& w, uint64_t in, uint64_t out, const char* what) {
         if (w.inDim != in || w.outDim != out)
             throw std::invalid_argument(std::string("resident ") + what + " dimensions do not match config");
-        if (!w.codes || w.type > 3 || (w.type >= 2 && (!w.scales || w.inDim % 32)) || w.inDim % 4)
-            throw std::invalid_argument(std::string("resident ") + what + " weight is not usable");
+        if (!w.codes || w.type > 3 || (w.type >= 2 && (!w.scales || w.inDim % 32)) || w.inDim % 4 ||
+            (w.type == 1 && w.inDim % 8) || (reinterpret_cast<uintptr_t>(w.codes) % 16))
+            throw std::invalid_argument(std::string("resident ") + what +
+                                        " weight is not usable (bf16 rows need inDim % 8, quantised inDim % 32, "
+                                        "and the codes 16-byte aligned)");
         DevWeight d;
         d.codes = w.codes;
         d.scales = static_cast<const float*>(w.scales);
@@ -294,65 +469,91 @@ struct DenseModel {
     }
 };
 
-bool gemv(const DevWeight& w, const float* a, float* out, bool accumulate, hipStream_t stream) {
-    GemvParams p{};
-    p.a = a;
-    p.w = w.codes;
-    p.scales = w.scales;
-    p.bias = w.bias;
-    p.out = out;
-    p.type = w.type;
-    p.accumulate = accumulate ? 1 : 0;
-    p.m = 1;
-    p.k = w.in;
-    p.n = w.out;
-    p.ldo = w.out;
-    return launch_gemv(p, stream);
+struct Seg {
+    const DevWeight* w;
+    float* out;
+};
+
+template <int TYPE, int PRE>
+void launch_dense_gemv(const DenseGemvArgs& p, hipStream_t stream) {
+    const unsigned grid = unsigned((p.rows + 4 * DG_ROWS - 1) / (4 * DG_ROWS));
+    hipLaunchKernelGGL((dense_gemv_kernel<TYPE, PRE>), dim3(grid), dim3(256), 0, stream, p);
 }
 
-bool norm(const float* x, const float* gamma, float* out, uint32_t n, float eps, hipStream_t stream) {
-    return Context::instance().launch("dense_norm_kernel", stream, [&] {
-        hipLaunchKernelGGL(dense_norm_kernel, dim3(1), dim3(1024), 0, stream, x, gamma, out, n, eps);
+/* one launch for weights of one encoding whose row counts are even (rows
+   of a wave never straddle two of them); otherwise one launch per weight */
+bool dense_gemv(std::initializer_list<Seg> segs, const float* x, const float* x2, const float* gamma, float eps,
+                int pre, bool accumulate, hipStream_t stream) {
+    const Seg* sv = segs.begin();
+    const size_t ns = segs.size();
+    bool together = ns <= 3;
+    for (size_t i = 0; i < ns; ++i)
+        if (sv[i].w->type != sv[0].w->type || sv[i].w->in != sv[0].w->in || (ns > 1 && sv[i].w->out % 2)) together = false;
+    if (!together) {
+        for (size_t i = 0; i < ns; ++i)
+            if (!dense_gemv({sv[i]}, x, x2, gamma, eps, pre, accumulate, stream)) return false;
+        return true;
+    }
+    DenseGemvArgs p{};
+    uint32_t start = 0;
+    for (size_t i = 0; i < ns; ++i) {
+        p.seg[i] = {static_cast<const char*>(sv[i].w->codes), sv[i].w->scales, sv[i].w->bias, sv[i].out, sv[i].w->out, start};
+        start += sv[i].w->out;
+    }
+    p.nseg = int(ns);
+    p.rows = start;
+    p.k = sv[0].w->in;
+    p.accumulate = accumulate ? 1 : 0;
+    p.x = x;
+    p.x2 = x2;
+    p.gamma = gamma;
+    p.eps = eps;
+    const int type = sv[0].w->type;
+    return Context::instance().launch("dense_gemv_kernel", stream, [&] {
+#define AIGPU_DG(T)                                                                                          \
+    if (type == T) {                                                                                         \
+        if (pre == 0) launch_dense_gemv<T, 0>(p, stream);                                                    \
+        else if (pre == 1) launch_dense_gemv<T, 1>(p, stream);                                               \
+        else launch_dense_gemv<T, 2>(p, stream);                                                             \
+    }
+        AIGPU_DG(0) AIGPU_DG(1) AIGPU_DG(2) AIGPU_DG(3)
+#undef AIGPU_DG
     });
 }
 
-/* the launches of one decode step; `splits` attention workgroups per kv head */
+/* the workgroups per kv head of the attention of a step at `pos` */
+uint32_t host_splits(uint32_t pos, uint32_t window) {
+    const uint32_t first = window && pos + 1 > window ? pos + 1 - window : 0;
+    const uint32_t chunks = (pos + 1 - first + SPLIT - 1) / SPLIT;
+    const uint32_t per = (chunks + MAX_SPLITS - 1) / MAX_SPLITS;
+    return (chunks + per - 1) / per;
+}
+
+/* the launches of one decode step; `splits` attention workgroups per kv head
+   (the most any layer needs; the others leave at once) */
 bool run_step(DenseModel& d, uint32_t splits, hipStream_t stream) {
     Context& ctx = Context::instance();
     const AiGpuDenseConfig& c = d.cfg;
     DenseArgs a{d.pos, c.heads, c.kvHeads, c.headDim, c.rotaryDims, d.maxSplits, 0, c.epsilon};
     for (const DevLayer& L : d.layers) {
         a.window = L.window;
-        if (!norm(d.x, L.inputNorm, d.normed, c.hidden, c.epsilon, stream)) return false;
-        if (!gemv(L.q, d.normed, d.q, false, stream) || !gemv(L.k, d.normed, d.k, false, stream) ||
-            !gemv(L.v, d.normed, d.v, false, stream))
-            return false;
-        if (!ctx.launch("dense_qk_kernel", stream, [&] {
-                hipLaunchKernelGGL(dense_qk_kernel, dim3(c.heads + c.kvHeads), dim3(64), 0, stream, a, d.q, d.k, d.v,
-                                   L.qNorm, L.kNorm, d.freqs, L.keys, L.values);
-            }))
+        if (!dense_gemv({{&L.q, d.q}, {&L.k, d.k}, {&L.v, d.v}}, d.x, nullptr, L.inputNorm, c.epsilon, 1, false, stream))
             return false;
         if (!ctx.launch("dense_attn_kernel", stream, [&] {
-                hipLaunchKernelGGL(dense_attn_kernel, dim3(splits, c.kvHeads), dim3(256), 0, stream, a, d.q, L.keys,
-                                   L.values, d.partial);
+                if (c.headDim <= 128)
+                    hipLaunchKernelGGL(dense_attn_kernel<2>, dim3(splits, c.kvHeads), dim3(256), 0, stream, a, d.q, d.k,
+                                       d.v, L.qNorm, L.kNorm, d.freqs, L.keys, L.values, d.partial, d.tickets, d.attn);
+                else
+                    hipLaunchKernelGGL(dense_attn_kernel<4>, dim3(splits, c.kvHeads), dim3(256), 0, stream, a, d.q, d.k,
+                                       d.v, L.qNorm, L.kNorm, d.freqs, L.keys, L.values, d.partial, d.tickets, d.attn);
             }))
             return false;
-        if (!ctx.launch("dense_merge_kernel", stream, [&] {
-                hipLaunchKernelGGL(dense_merge_kernel, dim3(c.heads), dim3(64), 0, stream, a, d.partial, d.attn);
-            }))
+        if (!dense_gemv({{&L.o, d.x}}, d.attn, nullptr, nullptr, 0.0f, 0, true, stream)) return false;
+        if (!dense_gemv({{&L.gate, d.gate}, {&L.up, d.up}}, d.x, nullptr, L.postNorm, c.epsilon, 1, false, stream))
             return false;
-        if (!gemv(L.o, d.attn, d.x, true, stream)) return false;
-        if (!norm(d.x, L.postNorm, d.normed, c.hidden, c.epsilon, stream)) return false;
-        if (!gemv(L.gate, d.normed, d.gate, false, stream) || !gemv(L.up, d.normed, d.up, false, stream)) return false;
-        if (!ctx.launch("dense_swiglu_kernel", stream, [&] {
-                hipLaunchKernelGGL(dense_swiglu_kernel, dim3((c.intermediate + 255) / 256), dim3(256), 0, stream, d.gate,
-                                   d.up, c.intermediate);
-            }))
-            return false;
-        if (!gemv(L.down, d.gate, d.x, true, stream)) return false;
+        if (!dense_gemv({{&L.down, d.x}}, d.gate, d.up, nullptr, 0.0f, 2, true, stream)) return false;
     }
-    if (!norm(d.x, d.finalNorm, d.normed, c.hidden, c.epsilon, stream)) return false;
-    return gemv(d.head, d.normed, d.logits, false, stream);
+    return dense_gemv({{&d.head, d.logits}}, d.x, nullptr, d.finalNorm, c.epsilon, 1, false, stream);
 }
 
 } // namespace
@@ -405,9 +606,10 @@ AIGPU_ABI void* aigpu_dense_create(const AiGpuDenseConfig* c, const AiGpuDenseLa
         d->gate = d->floats(c->intermediate);
         d->up = d->floats(c->intermediate);
         d->logits = d->floats(c->vocab);
-        d->maxSplits = (c->capacity + aigpu::SPLIT - 1) / aigpu::SPLIT;
-        d->partial = d->floats(uint64_t(c->heads) * d->maxSplits * 4 * (c->headDim + 2));
+        d->maxSplits = aigpu::host_splits(c->capacity - 1, 0);
+        d->partial = d->floats(uint64_t(c->heads) * d->maxSplits * (c->headDim + 2));
         d->pos = reinterpret_cast<uint32_t*>(d->floats(1));
+        d->tickets = reinterpret_cast<uint32_t*>(d->floats(c->kvHeads));
         for (uint32_t i = 0; i < c->layers; ++i) {
             const AiGpuDenseLayer& l = layers[i];
             if (!l.inputNorm || !l.postNorm || !keys[i] || !values[i])
@@ -474,8 +676,7 @@ AIGPU_ABI void aigpu_dense_decode(void* handle, const float* embedding, float* l
     // the attention grid covers the positions this step reads
     uint32_t splits = 1;
     for (const aigpu::DevLayer& L : d.layers) {
-        const uint32_t first = L.window && position + 1 > L.window ? position + 1 - L.window : 0;
-        const uint32_t s = (position + 1 - first + aigpu::SPLIT - 1) / aigpu::SPLIT;
+        const uint32_t s = aigpu::host_splits(position, L.window);
         if (s > splits) splits = s;
     }
     if (!aigpu::run_step(d, splits, stream)) return;
