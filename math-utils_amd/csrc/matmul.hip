@@ -12,7 +12,8 @@
 // by the weight bytes, so every lane streams 16-byte pieces of a weight row
 // (4, 8, 16 or 32 weights), one wave owns GEMV_ROWS weight rows and keeps an
 // fp32 accumulator per (weight row, a row), and a shuffle tree reduces the
-// lanes. More rows of a run as blocks of 8 along grid.y.
+// lanes. Up to GEMM_MIN_M - 1 rows of a run as blocks of 8 along grid.y;
+// more rows take gemm_kernel on MFMA.
 #include "context.hpp"
 #include "device.hpp"
 #include "gemv.hpp"
@@ -24,6 +25,7 @@ namespace {
 
 constexpr int GEMV_ROWS = 2;   // weight rows per wave
 constexpr int GEMV_MAX_M = 8;  // rows of a per launch block
+constexpr uint32_t GEMM_MIN_M = 16;   // from here on the MFMA GEMM
 
 template <int TYPE, int M>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
@@ -90,6 +92,192 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     }
 }
 
+/*
+    gemm_kernel: many rows of a (prefill), on v_mfma_f32_16x16x32_bf16.
+    A stays fp32 at the boundary; each value is split into a bf16 high part
+    and the bf16 residual, and hi.B + lo.B keeps about 16 bits of it. BF16
+    weights and the Q8/Q4 codes are exact in bf16; fp32 weights are split
+    the same way (a third product, hi_a.lo_w). For Q8/Q4 one 32-wide K step
+    is one scale block, so each step's products go through a scratch
+    accumulator and are added in times the column's block scale.
+    Tile 128 x 128 x 32 over four waves of 64 x 64 (4 x 4 MFMA tiles); the
+    next K step is loaded into registers while the current one computes.
+    LDS rows are padded to 40 bf16 (80 bytes), so the 16 lanes of each 16-byte
+    operand read land on distinct banks.
+*/
+constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 32, GM_AS = GM_BK + 8;
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void gemm_kernel(GemvParams p) {
+    constexpr bool SPLIT_W = TYPE == 0, QUANT = TYPE >= 2;
+    __shared__ __align__(16) __bf16 Ah[GM_BM * GM_AS];
+    __shared__ __align__(16) __bf16 Al[GM_BM * GM_AS];
+    __shared__ __align__(16) __bf16 Bh[GM_BN * GM_AS];
+    __shared__ __align__(16) __bf16 Bl[SPLIT_W ? GM_BN * GM_AS : 8];
+    __shared__ float Sc[QUANT ? GM_BN : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
+    const uint32_t m0 = blockIdx.y * GM_BM, n0 = blockIdx.x * GM_BN;
+    const uint32_t K = p.k, M = p.m, N = p.n;
+    const int srow = tid >> 1, shalf = tid & 1;   // staging: row and 16-element half of the K step
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    floatx4 ra[4];                   // a: 16 floats
+    u32x4 rw[SPLIT_W ? 4 : 2];       // w: 16 fp32 / 16 bf16 / 16 Q8 codes / a Q4 block
+    float rs = 0.0f;
+    auto load = [&](uint32_t k0) {
+        const uint32_t gm = m0 + srow, kk = k0 + 16 * shalf;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            ra[e] = (gm < M && kk + 4 * e < K) ? *reinterpret_cast<const floatx4*>(p.a + size_t(gm) * K + kk + 4 * e)
+                                               : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        const uint32_t gn = n0 + srow;
+        if constexpr (TYPE == 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                rw[e] = (gn < N && kk + 4 * e < K)
+                            ? *reinterpret_cast<const u32x4*>(static_cast<const float*>(p.w) + size_t(gn) * K + kk + 4 * e)
+                            : u32x4{0u, 0u, 0u, 0u};
+        } else if constexpr (TYPE == 1) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                rw[e] = (gn < N && kk + 8 * e < K)
+                            ? *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.w) + size_t(gn) * K + kk + 8 * e)
+                            : u32x4{0u, 0u, 0u, 0u};
+        } else if constexpr (TYPE == 2) {
+            rw[0] = gn < N ? *reinterpret_cast<const u32x4*>(static_cast<const int8_t*>(p.w) + size_t(gn) * K + kk)
+                           : u32x4{0u, 0u, 0u, 0u};
+        } else {
+            // a Q4 block is 16 bytes: threads 0..127 take one row's block each
+            const uint32_t qn = n0 + uint32_t(tid & 127);
+            rw[0] = (tid < 128 && qn < N)
+                        ? *reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.w) + size_t(qn) * (K / 2) + k0 / 2)
+                        : u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+        }
+        if constexpr (QUANT) rs = (tid < 128 && n0 + tid < N) ? p.scales[size_t(n0 + tid) * (K / 32) + k0 / 32] : 0.0f;
+    };
+    auto split_store = [&](__bf16* hi, __bf16* lo, const float (&x)[16]) {
+        bf16x8 h0, h1, l0, l1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            h0[e] = __bf16(x[e]);
+            h1[e] = __bf16(x[8 + e]);
+            l0[e] = __bf16(x[e] - float(h0[e]));
+            l1[e] = __bf16(x[8 + e] - float(h1[e]));
+        }
+        *reinterpret_cast<bf16x8*>(hi) = h0;
+        *reinterpret_cast<bf16x8*>(hi + 8) = h1;
+        *reinterpret_cast<bf16x8*>(lo) = l0;
+        *reinterpret_cast<bf16x8*>(lo + 8) = l1;
+    };
+    auto store = [&]() {
+        float x[16];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[4 * e + c] = ra[e][c];
+        split_store(&Ah[srow * GM_AS + 16 * shalf], &Al[srow * GM_AS + 16 * shalf], x);
+        if constexpr (TYPE == 0) {
+            float y[16];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) y[4 * e + c] = __uint_as_float(rw[e][c]);
+            split_store(&Bh[srow * GM_AS + 16 * shalf], &Bl[srow * GM_AS + 16 * shalf], y);
+        } else if constexpr (TYPE == 1) {
+            *reinterpret_cast<u32x4*>(&Bh[srow * GM_AS + 16 * shalf]) = rw[0];
+            *reinterpret_cast<u32x4*>(&Bh[srow * GM_AS + 16 * shalf + 8]) = rw[1];
+        } else if constexpr (TYPE == 2) {
+            bf16x8 b0, b1;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float c = float(int32_t(rw[0][e] << (24 - 8 * j)) >> 24);
+                    if (e < 2) b0[4 * e + j] = __bf16(c);
+                    else b1[4 * (e - 2) + j] = __bf16(c);
+                }
+            *reinterpret_cast<bf16x8*>(&Bh[srow * GM_AS + 16 * shalf]) = b0;
+            *reinterpret_cast<bf16x8*>(&Bh[srow * GM_AS + 16 * shalf + 8]) = b1;
+        } else {
+            if (tid < 128) {
+                __bf16* row = &Bh[tid * GM_AS];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    bf16x8 lo4, hi4;   // codes 4e..4e+3 and 16+4e..16+4e+3, two bytes at a time
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t byte = (rw[0][e] >> (8 * j)) & 0xFFu;
+                        lo4[j] = __bf16(float(int(byte & 0xFu) - 8));
+                        hi4[j] = __bf16(float(int(byte >> 4) - 8));
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        row[4 * e + j] = lo4[j];
+                        row[16 + 4 * e + j] = hi4[j];
+                    }
+                }
+            }
+        }
+        if constexpr (QUANT)
+            if (tid < 128) Sc[tid] = rs;
+    };
+
+    load(0);
+    for (uint32_t k0 = 0; k0 < K; k0 += GM_BK) {
+        __syncthreads();   // the previous step's operand reads are done
+        store();
+        __syncthreads();
+        if (k0 + GM_BK < K) load(k0 + GM_BK);
+        bf16x8 ah[4], al[4], bh[4], bl[4];
+        const int fr = lane & 15, fk = 8 * (lane >> 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ah[i] = *reinterpret_cast<const bf16x8*>(&Ah[(64 * wm + 16 * i + fr) * GM_AS + fk]);
+            al[i] = *reinterpret_cast<const bf16x8*>(&Al[(64 * wm + 16 * i + fr) * GM_AS + fk]);
+            bh[i] = *reinterpret_cast<const bf16x8*>(&Bh[(64 * wn + 16 * i + fr) * GM_AS + fk]);
+            if constexpr (SPLIT_W) bl[i] = *reinterpret_cast<const bf16x8*>(&Bl[(64 * wn + 16 * i + fr) * GM_AS + fk]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (QUANT) {
+                    floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], t, 0, 0, 0);
+                    const float sc = Sc[64 * wn + 16 * j + fr];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(sc, t[r], acc[i][j][r]);
+                } else {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+                    if constexpr (SPLIT_W) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+                }
+            }
+    }
+    // the accumulator layout: lane holds rows 4 (lane / 16) + r of column lane % 16
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t n = n0 + 64 * wn + 16 * j + (lane & 15);
+            if (n >= N) continue;
+            const float b = p.bias ? p.bias[n] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t m = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + r;
+                if (m >= M) continue;
+                float* o = p.out + size_t(m) * p.ldo + n;
+                *o = (p.accumulate ? *o : 0.0f) + acc[i][j][r] + b;
+            }
+        }
+}
+
 /* any k for F32 and BF16 (rows not on 16-byte boundaries): one wave per
    weight row and a row of a, element by element */
 template <int TYPE>
@@ -124,6 +312,13 @@ bool launch_type(Context& ctx, const GemvParams& p, hipStream_t stream) {
             });
         }
         return ctx.fail("matmul: quantised weights need k a multiple of 32 and 16-byte aligned rows");
+    }
+    if (p.m >= GEMM_MIN_M) {
+        const dim3 grid(unsigned((p.n + GM_BN - 1) / GM_BN), unsigned((p.m + GM_BM - 1) / GM_BM));
+        if (grid.y > 65535u) return ctx.fail("matmul: too many rows of a");
+        return ctx.launch("gemm_kernel", stream, [&] {
+            hipLaunchKernelGGL((gemm_kernel<TYPE>), grid, dim3(256), 0, stream, p);
+        });
     }
     const unsigned gx = unsigned((p.n + 4 * GEMV_ROWS - 1) / (4 * GEMV_ROWS));
     const int M = p.m <= 1 ? 1 : (p.m <= 2 ? 2 : (p.m <= 4 ? 4 : GEMV_MAX_M));

@@ -1,5 +1,6 @@
-"""GPU parity of the projections (gemv_kernel behind aigpu_matmul_nt* and
-aigpu_matmul_device) against the oracle's restatement of apply
+"""GPU parity of the projections (gemv_kernel for up to 15 rows of a,
+gemm_kernel on MFMA from 16, behind aigpu_matmul_nt* and aigpu_matmul_device)
+against the oracle's restatement of apply
 (LocalModel.hpp:1052-1078) over the reference's weight encodings.
 
 Bar: fp32 outputs within 1e-5 of each dot product's absolute size,
@@ -51,7 +52,7 @@ def bound(a, dense):
 
 
 @pytest.mark.parametrize("kind", ["f32", "bf16", "q8", "q4"])
-@pytest.mark.parametrize("m", [1, 3, 8, 13])
+@pytest.mark.parametrize("m", [1, 3, 8, 13, 16, 200])
 def test_device_form(gpu, kind, m):
     import torch
     k, n = 1024, 1000
@@ -123,3 +124,20 @@ def test_rejects_quantised_k_not_multiple_of_32(gpu):
     out = torch.zeros((1, 4), dtype=torch.float32, device="cuda")
     with pytest.raises(RuntimeError, match="multiple of 32"):
         gpu.matmul(a, w, out, "q8", scales=s)
+
+
+@pytest.mark.parametrize("kind,k", [("f32", 100), ("bf16", 104), ("q8", 96), ("q4", 160)])
+def test_gemm_ragged_tiles(gpu, kind, k):
+    """the MFMA GEMM with m, n and k that do not fill its 128 x 128 x 32 tiles"""
+    import torch
+    m, n = 131, 257
+    a = O.fill_normal((m, k), 51, "a")
+    w, scales, dense = weights(n, k, kind, 52)
+    bias = O.fill_normal((n,), 53, "bias")
+    out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    say("gemm ragged", dict(kind=kind, m=m, k=k, n=n))
+    gpu.matmul(dev_f32(a), to_device(w), out, kind, scales=None if scales is None else dev_f32(scales),
+               bias=dev_f32(bias))
+    want = O.matmul_nt(a, w, kind, scales=scales, bias=bias)
+    err = np.abs(host(out) - want)
+    assert np.all(err <= bound(a, dense)), f"{kind}: max err {err.max()}"
