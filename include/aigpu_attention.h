@@ -283,6 +283,30 @@ typedef struct AiGpuGdnGatedNorm {
 AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm* args);
 
 /* ------------------------------------------------------------------------ */
+/* 5c. Multi-head latent attention (latentAttentionMixer,                    */
+/*     LocalModel.hpp:3118-3158): per token and head, q folded through the  */
+/*     head's key rows of kv_b_proj, softmax against the cached latents     */
+/*     (all positions up to the token, or the indexer's sorted selection,   */
+/*     KeySelection :1203-1206), the weighted latents through the value     */
+/*     rows. Device pointers.                                               */
+/* ------------------------------------------------------------------------ */
+typedef struct AiGpuLatentAttention {
+    const float* q;           /* [count][heads][nopeDim] (q_b_proj output, :3106) */
+    const float* latent;      /* [startPos + count][kvLoraRank] cache, this call's rows included */
+    const void* kvB;          /* [heads * (nopeDim + vDim)][kvLoraRank] kv_b_proj, kvBType */
+    uint32_t kvBType;         /* AIGPU_F32 / AIGPU_BF16 */
+    uint32_t reserved;
+    const uint32_t* selStart; /* [count] or NULL (every token dense) */
+    const uint32_t* selCount; /* [count], 0xFFFFFFFF for a dense token */
+    const uint32_t* selKeys;  /* the concatenated sorted key lists */
+    float* out;               /* [count][heads][vDim] fp32 */
+    float scale;              /* 1/sqrt(qk_nope_head_dim + qk_rope_head_dim), :3116 */
+    uint64_t count, startPos, heads, nopeDim, vDim, kvLoraRank;
+    void* stream;
+} AiGpuLatentAttention;
+AIGPU_ABI int aigpu_latent_attention(const AiGpuLatentAttention* args);
+
+/* ------------------------------------------------------------------------ */
 /* 7. Projections (DeviceABI.h:101-112): c[m][n] = a[m][k] . b[n][k]^T, with */
 /*    a and c host fp32 and b a device weight from aigpu_upload, in the     */
 /*    reference's four encodings (Quant.hpp): fp32, bf16, Q8 (int8 codes,   */

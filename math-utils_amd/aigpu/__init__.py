@@ -551,3 +551,34 @@ class DenseDecoder:
         if self.handle:
             lib().aigpu_dense_release(self.handle)
             self.handle = None
+
+
+
+# ---------------------------------------------------------------- 5c. latent attention
+class AiGpuLatentAttention(C.Structure):
+    _fields_ = [("q", _vp), ("latent", _vp), ("kvB", _vp), ("kvBType", _u32), ("reserved", _u32),
+                ("selStart", _vp), ("selCount", _vp), ("selKeys", _vp), ("out", _vp), ("scale", _f32),
+                ("count", _u64), ("startPos", _u64), ("heads", _u64), ("nopeDim", _u64), ("vDim", _u64),
+                ("kvLoraRank", _u64), ("stream", _vp)]
+
+
+SIGNATURES["aigpu_latent_attention"] = (C.c_int, [C.POINTER(AiGpuLatentAttention)])
+
+
+def latent_attention(q, latent, kv_b, out, start_pos, scale, sel_start=None, sel_count=None, sel_keys=None,
+                     stream=None):
+    """Device form of latentAttentionMixer's attention: q [count][heads][nope],
+    latent [positions][rank], kv_b [heads*(nope+v)][rank] (fp32 or bf16), out
+    [count][heads][v]; the optional selection as int32 tensors (count
+    0xFFFFFFFF marks a dense token)."""
+    for t, n in ((q, "q"), (latent, "latent"), (kv_b, "kv_b"), (out, "out"), (sel_start, "sel_start"),
+                 (sel_count, "sel_count"), (sel_keys, "sel_keys")):
+        _need(t, n)
+    count, heads, nope = q.shape
+    vdim = out.shape[2]
+    args = AiGpuLatentAttention(q=_ptr(q), latent=_ptr(latent), kvB=_ptr(kv_b), kvBType=_dtype_tag(kv_b),
+                                selStart=_ptr(sel_start), selCount=_ptr(sel_count), selKeys=_ptr(sel_keys),
+                                out=_ptr(out), scale=scale, count=count, startPos=start_pos, heads=heads,
+                                nopeDim=nope, vDim=vdim, kvLoraRank=latent.shape[1], stream=_stream(stream))
+    _check(lib().aigpu_latent_attention(C.byref(args)))
+    return out

@@ -735,3 +735,31 @@ AIGPU_ABI int aigpu_matmul_device(const AiGpuMatmul* args) {
 }
 
 } // extern "C"
+
+extern "C" {
+
+AIGPU_ABI int aigpu_latent_attention(const AiGpuLatentAttention* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("latent attention: null arguments"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    aigpu::LatentParams p{};
+    p.q = args->q;
+    p.latent = args->latent;
+    p.wkv = args->kvB;
+    p.wType = args->kvBType == AIGPU_BF16 ? 1 : (args->kvBType == AIGPU_F32 ? 0 : 2);
+    p.selStart = args->selStart;
+    p.selCount = args->selStart ? args->selCount : nullptr;
+    p.selKeys = args->selKeys;
+    p.out = args->out;
+    p.scale = args->scale;
+    p.count = args->count;
+    p.startPos = args->startPos;
+    p.heads = args->heads;
+    p.nope = args->nopeDim;
+    p.vdim = args->vDim;
+    p.rank = args->kvLoraRank;
+    return aigpu::launch_latent_attention(p, as_stream(args->stream)) ? 1 : 0;
+}
+
+} // extern "C"

@@ -27,6 +27,7 @@ enum ScratchSlot {
     SLOT_DECODE_PARTS,   // split-K partial softmax records
     SLOT_DECODE_QUERIES, // prepared decode queries and new-token scores
     SLOT_DELTA_WORK,     // per-chunk solve products of the delta rule
+    SLOT_LATENT,         // folded queries, contexts and split records of latent attention
     SLOT_COUNT
 };
 

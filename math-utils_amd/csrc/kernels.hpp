@@ -87,6 +87,21 @@ struct GemvParams {
 };
 bool launch_gemv(const GemvParams& p, hipStream_t stream);
 
+// ---- multi-head latent attention ----
+struct LatentParams {
+    const float* q;          // [count][heads][nope]
+    const float* latent;     // [positions][rank]
+    const void* wkv;         // [heads * (nope + vdim)][rank], wType
+    int wType;               // 0 fp32, 1 bf16
+    const uint32_t* selStart;   // per token, or null (all dense)
+    const uint32_t* selCount;   // UINT32_MAX: dense
+    const uint32_t* selKeys;
+    float* out;              // [count][heads][vdim]
+    float scale;
+    uint64_t count, startPos, heads, nope, vdim, rank;
+};
+bool launch_latent_attention(const LatentParams& p, hipStream_t stream);
+
 // ---- Kimi Delta Attention: the delta rule with per-key-channel decay ----
 struct KdaParams {
     const void* q;        // [count][keyHeads][keyDim], inType

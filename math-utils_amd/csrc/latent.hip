@@ -1,0 +1,324 @@
+// latent.hip - multi-head latent attention (latentAttentionMixer,
+// LocalModel.hpp:3086-3163; DeepSeek's MLA as GLM-5.3 uses it, without
+// positional encoding). Every token's key and value are one kvLoraRank-wide
+// latent c; head h's key would be Wk_h c and its value Wv_h c, Wk_h and Wv_h
+// its rows of kv_b_proj. Both are linear, so
+//   q . (Wk_h c) = (Wk_h^T q) . c         sum_j p_j Wv_h c_j = Wv_h (sum_j p_j c_j)
+// and nothing is ever expanded:
+//   latent_fold_kernel    folded[t][h] = Wk_h^T q[t][h]
+//   latent_attn_kernel    softmax(folded . c_j * scale) over the token's keys
+//                         (all positions up to it, or the indexer's sorted
+//                         selection), context = sum p_j c_j; every cached
+//                         latent is read once per group of 16 heads
+//   latent_merge_kernel   (decode-sized calls) the key splits combined
+//   latent_unfold_kernel  out[t][h] = Wv_h context[t][h]
+// fp32 throughout, as the reference computes it; kv_b_proj may be fp32 or
+// bf16 (widened).
+#include "context.hpp"
+#include "device.hpp"
+#include "kernels.hpp"
+
+namespace aigpu {
+
+namespace {
+
+constexpr int HG = 16;          // heads per attention workgroup
+constexpr int KPB = 64;         // keys per block (four lanes per key)
+constexpr int MAX_RANK = 512;   // kvLoraRank
+constexpr int MAX_NOPE = 256;
+constexpr int TT = 8;           // tokens per fold / unfold workgroup
+
+struct LatentArgs {
+    LatentParams p;
+    float* folded;    // [count][heads][C]
+    float* context;   // [count][heads][C]
+    float* partial;   // [count][heads][splits][C + 2]
+    uint32_t splits;
+};
+
+template <bool BF16>
+__device__ __forceinline__ float wkv_at(const void* w, size_t i) {
+    if constexpr (BF16) return bf16_bits_to_float(static_cast<const uint16_t*>(w)[i]);
+    return static_cast<const float*>(w)[i];
+}
+
+/* folded[t][h][c] = sum_d q[t][h][d] Wk_h[d][c] (:3124-3129), d in order;
+   workgroup (head, 256 columns, TT tokens) */
+template <bool BF16>
+__global__ __launch_bounds__(256) void latent_fold_kernel(LatentArgs a) {
+    __shared__ float qs[TT][MAX_NOPE];
+    const LatentParams& p = a.p;
+    const uint32_t h = blockIdx.x, c = blockIdx.y * 256 + threadIdx.x;
+    const uint64_t t0 = uint64_t(blockIdx.z) * TT;
+    const uint32_t Dn = uint32_t(p.nope), C = uint32_t(p.rank);
+    for (uint32_t i = threadIdx.x; i < TT * Dn; i += 256) {
+        const uint32_t t = i / Dn, d = i % Dn;
+        qs[t][d] = t0 + t < p.count ? p.q[((t0 + t) * p.heads + h) * Dn + d] : 0.0f;
+    }
+    __syncthreads();
+    if (c >= C) return;
+    const size_t wk = size_t(h) * (p.nope + p.vdim) * C;
+    float acc[TT] = {};
+#pragma unroll 8
+    for (uint32_t d = 0; d < Dn; ++d) {
+        const float w = wkv_at<BF16>(p.wkv, wk + size_t(d) * C + c);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[t] = fmaf(qs[t][d], w, acc[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+        if (t0 + t < p.count) a.folded[((t0 + t) * p.heads + h) * C + c] = acc[t];
+}
+
+/* workgroup (token, 16 heads, key split): online softmax over blocks of KPB
+   keys; four lanes per key share its row in the scores, the lanes own
+   columns in the context */
+__global__ __launch_bounds__(256) void latent_attn_kernel(LatentArgs a) {
+    __shared__ float F[HG * MAX_RANK];
+    __shared__ float pr[HG][KPB];
+    __shared__ uint32_t keyAt[KPB];
+    __shared__ float wred[4][HG];
+
+    const LatentParams& p = a.p;
+    const uint64_t t = blockIdx.x;
+    const uint32_t h0 = blockIdx.y * HG, s = blockIdx.z;
+    const uint32_t C = uint32_t(p.rank);
+    const uint32_t nh = uint32_t(p.heads - h0 < HG ? p.heads - h0 : HG);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint64_t pos = p.startPos + t;
+    const bool dense = !p.selCount || p.selCount[t] == 0xFFFFFFFFu;
+    const uint64_t n = dense ? pos + 1 : p.selCount[t];
+    const uint32_t* sel = dense ? nullptr : p.selKeys + p.selStart[t];
+    const uint64_t blocks = (n + KPB - 1) / KPB;
+    const uint64_t per = (blocks + a.splits - 1) / a.splits;
+    const uint64_t bBegin = uint64_t(s) * per, bEnd = bBegin + per < blocks ? bBegin + per : blocks;
+
+    for (uint32_t i = tid; i < HG * C; i += 256) {
+        const uint32_t hh = i / C, c = i % C;
+        F[hh * MAX_RANK + c] = hh < nh ? a.folded[(t * p.heads + h0 + hh) * C + c] : 0.0f;
+    }
+    __syncthreads();
+
+    constexpr int CPT = MAX_RANK / 256;   // context columns per thread
+    float m[HG], l[HG], acc[HG][CPT];
+#pragma unroll
+    for (int hh = 0; hh < HG; ++hh) {
+        m[hh] = -INFINITY;
+        l[hh] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < CPT; ++e) acc[hh][e] = 0.0f;
+    }
+    const uint32_t kq = uint32_t(tid) >> 2, part = uint32_t(tid) & 3;   // key in block, quarter of its row
+    const uint32_t qlen = C / 4;                                        // C % 16 == 0
+    for (uint64_t b = bBegin; b < bEnd; ++b) {
+        const uint64_t i = b * KPB + kq;
+        const bool live = i < n;
+        const uint32_t key = live ? (dense ? uint32_t(i) : sel[i]) : 0u;
+        if (part == 0) keyAt[kq] = key;
+        float sc[HG];
+#pragma unroll
+        for (int hh = 0; hh < HG; ++hh) sc[hh] = 0.0f;
+        if (live) {
+            const float* lr = p.latent + size_t(key) * C + part * qlen;
+            for (uint32_t c0 = 0; c0 < qlen; c0 += 32) {
+                floatx4 l4[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    l4[e] = c0 + 4 * e < qlen ? *reinterpret_cast<const floatx4*>(lr + c0 + 4 * e)
+                                              : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int hh = 0; hh < HG; ++hh) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        if (c0 + 4 * e < qlen) {
+                            const floatx4 f4 = *reinterpret_cast<const floatx4*>(&F[hh * MAX_RANK + part * qlen + c0 + 4 * e]);
+                            sc[hh] = fmaf(f4[0], l4[e][0], fmaf(f4[1], l4[e][1], fmaf(f4[2], l4[e][2], fmaf(f4[3], l4[e][3], sc[hh]))));
+                        }
+                    }
+                }
+            }
+        }
+        // the key's four quarters, then the block's max per head
+#pragma unroll
+        for (int hh = 0; hh < HG; ++hh) {
+            sc[hh] += __shfl_xor(sc[hh], 1, WAVE);
+            sc[hh] += __shfl_xor(sc[hh], 2, WAVE);
+            sc[hh] = live ? sc[hh] * p.scale : -INFINITY;
+            const float bm = wave_max(sc[hh]);
+            if (lane == 0) wred[w][hh] = bm;
+        }
+        __syncthreads();
+        float f[HG];
+#pragma unroll
+        for (int hh = 0; hh < HG; ++hh) {
+            const float bm = fmaxf(fmaxf(wred[0][hh], wred[1][hh]), fmaxf(wred[2][hh], wred[3][hh]));
+            const float mn = fmaxf(m[hh], bm);
+            f[hh] = expf(m[hh] - mn);   // 0 on the first block
+            m[hh] = mn;
+            if (part == 0) pr[hh][kq] = live ? expf(sc[hh] - mn) : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int hh = 0; hh < HG; ++hh) {
+            l[hh] = l[hh] * f[hh] + wave_sum(pr[hh][lane]);   // KPB == WAVE: lane = key
+#pragma unroll
+            for (int e = 0; e < CPT; ++e) acc[hh][e] *= f[hh];
+        }
+        // context: the block's keys against the thread's columns
+        const uint32_t nb = uint32_t(n - b * KPB < uint64_t(KPB) ? n - b * KPB : uint64_t(KPB));
+        for (uint32_t k0 = 0; k0 < nb; k0 += 8) {
+            float lv[8][CPT];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t kk = k0 + u < nb ? k0 + u : k0;
+                const float* lr = p.latent + size_t(keyAt[kk]) * C;
+#pragma unroll
+                for (int e = 0; e < CPT; ++e) lv[u][e] = tid + 256 * e < int(C) ? lr[tid + 256 * e] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (k0 + u >= nb) break;
+#pragma unroll
+                for (int hh = 0; hh < HG; ++hh) {
+                    const float pv = pr[hh][k0 + u];
+#pragma unroll
+                    for (int e = 0; e < CPT; ++e) acc[hh][e] = fmaf(pv, lv[u][e], acc[hh][e]);
+                }
+            }
+        }
+        __syncthreads();   // pr and keyAt are rewritten by the next block
+    }
+
+    if (a.splits == 1) {
+#pragma unroll
+        for (int hh = 0; hh < HG; ++hh) {
+            if (uint32_t(hh) >= nh) break;
+            const float inv = 1.0f / l[hh];
+#pragma unroll
+            for (int e = 0; e < CPT; ++e)
+                if (tid + 256 * e < int(C)) a.context[(t * p.heads + h0 + hh) * C + tid + 256 * e] = acc[hh][e] * inv;
+        }
+    } else {
+        const size_t rec = size_t(C) + 2;
+#pragma unroll
+        for (int hh = 0; hh < HG; ++hh) {
+            if (uint32_t(hh) >= nh) break;
+            float* out = a.partial + ((t * p.heads + h0 + hh) * a.splits + s) * rec;
+            if (tid == 0) {
+                out[0] = m[hh];
+                out[1] = l[hh];
+            }
+#pragma unroll
+            for (int e = 0; e < CPT; ++e)
+                if (tid + 256 * e < int(C)) out[2 + tid + 256 * e] = acc[hh][e];
+        }
+    }
+}
+
+/* the splits' records of one (token, head) combined into its context */
+__global__ __launch_bounds__(256) void latent_merge_kernel(LatentArgs a) {
+    const LatentParams& p = a.p;
+    const uint64_t t = blockIdx.x;
+    const uint32_t h = blockIdx.y, C = uint32_t(p.rank);
+    const size_t rec = size_t(C) + 2;
+    const float* base = a.partial + (t * p.heads + h) * a.splits * rec;
+    float M = -INFINITY;
+    for (uint32_t i = 0; i < a.splits; ++i) M = fmaxf(M, base[i * rec]);
+    float L = 0.0f;
+    for (uint32_t i = 0; i < a.splits; ++i)
+        if (base[i * rec] != -INFINITY) L = fmaf(base[i * rec + 1], expf(base[i * rec] - M), L);
+    const float inv = 1.0f / L;
+    for (uint32_t c = threadIdx.x; c < C; c += 256) {
+        float acc = 0.0f;
+        for (uint32_t i = 0; i < a.splits; ++i)
+            if (base[i * rec] != -INFINITY) acc = fmaf(base[i * rec + 2 + c], expf(base[i * rec] - M), acc);
+        a.context[(t * p.heads + h) * C + c] = acc * inv;
+    }
+}
+
+/* out[t][h][v] = Wv_h[v] . context[t][h] (:3153-3154); workgroup (head, TT
+   tokens), thread v */
+template <bool BF16>
+__global__ __launch_bounds__(256) void latent_unfold_kernel(LatentArgs a) {
+    __shared__ float cs[TT * MAX_RANK];
+    const LatentParams& p = a.p;
+    const uint32_t h = blockIdx.x;
+    const uint64_t t0 = uint64_t(blockIdx.y) * TT;
+    const uint32_t C = uint32_t(p.rank), Dv = uint32_t(p.vdim);
+    for (uint32_t i = threadIdx.x; i < TT * C; i += 256) {
+        const uint32_t t = i / C, c = i % C;
+        cs[t * MAX_RANK + c] = t0 + t < p.count ? a.context[((t0 + t) * p.heads + h) * C + c] : 0.0f;
+    }
+    __syncthreads();
+    const uint32_t v = threadIdx.x;
+    if (v >= Dv) return;
+    const size_t wv = (size_t(h) * (p.nope + p.vdim) + p.nope + v) * C;
+    float acc[TT] = {};
+#pragma unroll 8
+    for (uint32_t c = 0; c < C; ++c) {
+        const float w = wkv_at<BF16>(p.wkv, wv + c);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[t] = fmaf(w, cs[t * MAX_RANK + c], acc[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+        if (t0 + t < p.count) p.out[((t0 + t) * p.heads + h) * Dv + v] = acc[t];
+}
+
+} // namespace
+
+bool launch_latent_attention(const LatentParams& p, hipStream_t stream) {
+    Context& ctx = Context::instance();
+    if (!p.q || !p.latent || !p.wkv || !p.out) return ctx.fail("latent attention: null tensor");
+    if (p.selCount && (!p.selStart || !p.selKeys)) return ctx.fail("latent attention: a selection needs start and keys");
+    if (p.wType > 1) return ctx.fail("latent attention: kv_b_proj must be fp32 or bf16");
+    if (p.rank == 0 || p.rank > uint64_t(MAX_RANK) || p.rank % 16)
+        return ctx.fail("latent attention: kvLoraRank must be a multiple of 16 up to 512");
+    if (p.nope == 0 || p.nope > uint64_t(MAX_NOPE)) return ctx.fail("latent attention: qk_nope_head_dim must be 1 to 256");
+    if (p.vdim == 0 || p.vdim > 256) return ctx.fail("latent attention: v_head_dim must be 1 to 256");
+    if (p.heads == 0) return ctx.fail("latent attention: no heads");
+    if (reinterpret_cast<uintptr_t>(p.latent) % 16) return ctx.fail("latent attention: latents must be 16-byte aligned");
+    if (p.count == 0) return true;
+    if (p.count > 0x7FFFFFFFull || p.heads > 65535u) return ctx.fail("latent attention: too many tokens or heads");
+    LatentArgs a{};
+    a.p = p;
+    const uint32_t groups = uint32_t((p.heads + HG - 1) / HG);
+    // decode-sized calls split the keys so that about 256 workgroups run
+    const uint64_t maxKeys = p.startPos + p.count;
+    const uint64_t maxBlocks = (maxKeys + KPB - 1) / KPB;
+    uint64_t want = (256 + p.count * groups - 1) / (p.count * groups);
+    if (want > maxBlocks) want = maxBlocks;
+    if (want < 1) want = 1;
+    if (want > 64) want = 64;
+    a.splits = uint32_t(want);
+    const size_t cells = size_t(p.count) * p.heads * p.rank;
+    const size_t bytes = (2 * cells + (a.splits > 1 ? size_t(p.count) * p.heads * a.splits * (p.rank + 2) : 0)) * 4;
+    float* work = static_cast<float*>(ctx.grow(SLOT_LATENT, bytes));
+    if (!work) return false;
+    a.folded = work;
+    a.context = work + cells;
+    a.partial = work + 2 * cells;
+    const bool bf16 = p.wType == 1;
+    const dim3 fgrid(unsigned(p.heads), unsigned((p.rank + 255) / 256), unsigned((p.count + TT - 1) / TT));
+    if (fgrid.z > 65535u) return ctx.fail("latent attention: too many tokens for one call");
+    if (!ctx.launch("latent_fold_kernel", stream, [&] {
+            if (bf16) hipLaunchKernelGGL(latent_fold_kernel<true>, fgrid, dim3(256), 0, stream, a);
+            else hipLaunchKernelGGL(latent_fold_kernel<false>, fgrid, dim3(256), 0, stream, a);
+        }))
+        return false;
+    if (!ctx.launch("latent_attn_kernel", stream, [&] {
+            hipLaunchKernelGGL(latent_attn_kernel, dim3(unsigned(p.count), groups, a.splits), dim3(256), 0, stream, a);
+        }))
+        return false;
+    if (a.splits > 1 && !ctx.launch("latent_merge_kernel", stream, [&] {
+            hipLaunchKernelGGL(latent_merge_kernel, dim3(unsigned(p.count), unsigned(p.heads)), dim3(256), 0, stream, a);
+        }))
+        return false;
+    const dim3 ugrid(unsigned(p.heads), unsigned((p.count + TT - 1) / TT));
+    return ctx.launch("latent_unfold_kernel", stream, [&] {
+        if (bf16) hipLaunchKernelGGL(latent_unfold_kernel<true>, ugrid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL(latent_unfold_kernel<false>, ugrid, dim3(256), 0, stream, a);
+    });
+}
+
+} // namespace aigpu

@@ -707,3 +707,53 @@ void or_matmul_nt(const float* a, const void* w, const float* scales, const floa
     }
     free(row);
 }
+
+/* ---- multi-head latent attention ---- */
+
+void or_latent_attention(const float* q, const float* latent, const float* wkv, const uint32_t* selStart,
+                         const uint32_t* selCount, const uint32_t* selKeys, float* out, size_t count,
+                         size_t startPos, size_t nH, size_t Dn, size_t Dv, size_t C, float scale) {
+    const size_t perHead = Dn + Dv;
+    float* folded = (float*)malloc(sizeof(float) * C);
+    float* context = (float*)malloc(sizeof(float) * C);
+    float* scores = (float*)malloc(sizeof(float) * (startPos + count + 1));
+    for (size_t job = 0; job < count * nH; ++job) {
+        const size_t t = job / nH, head = job % nH;
+        const size_t pos = startPos + t;
+        const float* qh = &q[(t * nH + head) * Dn];
+        const float* Wk = wkv + head * perHead * C;
+        const float* Wv = Wk + Dn * C;
+        for (size_t c = 0; c < C; ++c) folded[c] = 0.0f;
+        for (size_t d = 0; d < Dn; ++d) {
+            const float qd = qh[d];
+            const float* row = Wk + d * C;
+            for (size_t c = 0; c < C; ++c) folded[c] += qd * row[c];
+        }
+        const int dense = !selCount || selCount[t] == 0xFFFFFFFFu;
+        const size_t n = dense ? pos + 1 : selCount[t];
+        float best = -1e30f;
+        for (size_t i = 0; i < n; ++i) {
+            const size_t key = dense ? i : selKeys[selStart[t] + i];
+            scores[i] = or_dot(folded, latent + key * C, C) * scale;
+            if (scores[i] > best) best = scores[i];
+        }
+        float sum = 0.0f;
+        for (size_t i = 0; i < n; ++i) {
+            scores[i] = expf(scores[i] - best);
+            sum += scores[i];
+        }
+        const float inv = 1.0f / sum;
+        for (size_t c = 0; c < C; ++c) context[c] = 0.0f;
+        for (size_t i = 0; i < n; ++i) {
+            const size_t key = dense ? i : selKeys[selStart[t] + i];
+            const float p = scores[i] * inv;
+            const float* cr = latent + key * C;
+            for (size_t j = 0; j < C; ++j) context[j] += p * cr[j];
+        }
+        float* o = &out[(t * nH + head) * Dv];
+        for (size_t v = 0; v < Dv; ++v) o[v] = or_dot(Wv + v * C, context, C);
+    }
+    free(folded);
+    free(context);
+    free(scores);
+}

@@ -220,6 +220,19 @@ void or_dequant(const void* codes, const float* scales, size_t outDim, size_t in
 void or_matmul_nt(const float* a, const void* w, const float* scales, const float* bias, float* out,
                   size_t m, size_t k, size_t n, int type);
 
+/* ---- multi-head latent attention ---- */
+/* latentAttentionMixer's attention (LocalModel.hpp:3118-3158), per token t
+   and head h: folded = sum_d q[t][h][d] Wk_h[d] (Wk_h the first Dn rows of
+   head h's Dn + Dv rows of wkv, each C wide); scores against the cached
+   latents latent[pos][C] by or_dot, times `scale`; the reference's softmax
+   (max, exp, sum, then p = e * (1/sum)); context = sum p * latent; out[v] =
+   or_dot(Wv_h[v], context). Token t sees positions 0..startPos+t (dense),
+   or when selCount[t] != UINT32_MAX the sorted list selKeys[selStart[t] ..
+   + selCount[t]) (KeySelection, :1203-1206). */
+void or_latent_attention(const float* q, const float* latent, const float* wkv, const uint32_t* selStart,
+                         const uint32_t* selCount, const uint32_t* selKeys, float* out, size_t count,
+                         size_t startPos, size_t nH, size_t Dn, size_t Dv, size_t C, float scale);
+
 /* number of threads the static pool would use given a request (<=0: all
    online CPUs in this process's affinity mask) */
 int or_threads(int requested);

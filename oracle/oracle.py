@@ -96,6 +96,8 @@ def lib():
         L.or_kda_rule.argtypes = [_f32p] * 7 + [_sz] * 5 + [C.c_int, C.c_int]
         L.or_dequant.argtypes = [C.c_void_p, _f32p, _sz, _sz, C.c_int, _f32p]
         L.or_matmul_nt.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_void_p, _f32p, _sz, _sz, _sz, C.c_int]
+        L.or_latent_attention.argtypes = [_f32p, _f32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p, _f32p,
+                                          _sz, _sz, _sz, _sz, _sz, _sz, C.c_float]
         L.or_threads.restype = C.c_int
         L.or_threads.argtypes = [C.c_int]
         _lib = L
@@ -526,3 +528,37 @@ def dense_decode(cfg, layers, head, final_norm, embedding, keys, values, positio
         x = x + proj(g, L["down"])
     last = rms_norm_row(x[0], final_norm, eps).reshape(1, H)
     return proj(last, head).reshape(-1)
+
+
+# ------------------------------------------------------ multi-head latent attention
+def selection_csr(selection, count):
+    """per-token key lists (None = dense) as (start, count, keys) arrays with
+    count UINT32_MAX marking a dense token"""
+    starts, counts, keys = [], [], []
+    for t in range(count):
+        sel = None if selection is None or t >= len(selection) else selection[t]
+        starts.append(len(keys))
+        if sel is None:
+            counts.append(0xFFFFFFFF)
+        else:
+            counts.append(len(sel))
+            keys.extend(int(k) for k in sel)
+    return (np.array(starts, np.uint32), np.array(counts, np.uint32),
+            np.array(keys if keys else [0], np.uint32))
+
+
+def latent_attention(q, latent, wkv, start_pos, heads, nope_dim, v_dim, scale, selection=None):
+    """latentAttentionMixer's attention restated (LocalModel.hpp:3118-3158):
+    q [count][heads][nope_dim], latent [positions][C], wkv [heads*(nope+v)][C];
+    selection: None, or per token None (dense) / a sorted key list"""
+    q = np.ascontiguousarray(q, np.float32)
+    latent = np.ascontiguousarray(latent, np.float32)
+    wkv = np.ascontiguousarray(wkv, np.float32)
+    count = q.shape[0]
+    C = latent.shape[1]
+    out = np.zeros((count, heads, v_dim), np.float32)
+    st, ct, ks = selection_csr(selection, count)
+    lib().or_latent_attention(q.reshape(-1), latent.reshape(-1), wkv.reshape(-1), st.ctypes.data, ct.ctypes.data,
+                              ks.ctypes.data, out.reshape(-1), count, start_pos, heads, nope_dim, v_dim, C,
+                              float(scale))
+    return out
