@@ -2,7 +2,7 @@
 """bench.py - throughput of the MI355X attention hot path against its roofline,
 with the reference's CPU path timed beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|delta|gdn|kda|dense|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|delta|gdn|kda|dense|gemm|mla|all]
 
 A step is one call of the hot path over one batch of synthetic, HBM-resident
 input. The headline workload (config.workload) is configs[2] of BASELINE.json,
@@ -50,7 +50,7 @@ def parse():
     # the GPU's clock ramps over the first ~15 ms of sustained work: a short
     # warm-up times the ramp rather than the kernels
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "kda", "dense", "all"])
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "kda", "dense", "gemm", "mla", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of each baseline sample")
@@ -468,6 +468,55 @@ def dense_workload(args, cpu):
     }
 
 
+def gemm_workload(args, cpu):
+    """a prefill projection through aigpu_matmul_device: Qwen3-8B's q_proj
+    shape, 8192 tokens x 4096 -> 4096, fp32 activations, bf16 weights"""
+    import torch
+    import aigpu
+    M, K, N = 8192, 4096, 4096
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    a = torch.randn((M, K), generator=gen, device="cuda")
+    w = (torch.randn((N, K), generator=gen, device="cuda") / K ** 0.5).to(torch.bfloat16)
+    out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    step_ms, k_ms, _ = time_steps(lambda: aigpu.matmul(a, w, out, "bf16"), args.steps, args.warmup, "gemm_kernel")
+    flop = 2.0 * M * N * K
+    return {
+        "workload": "projection 8192 x 4096 -> 4096 (Qwen3-8B q_proj), fp32 a, bf16 w, fp32 out",
+        "dtype": "bf16", "value": flop / (step_ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": step_ms,
+        "roofline": {"kernel": "gemm_kernel", "bound": "mfma", "achieved": flop / (k_ms * 1e-3) / 1e12,
+                     "peak": PEAK_MFMA_F16, "unit": "TFLOP/s", "frac": flop / (k_ms * 1e-3) / 1e12 / PEAK_MFMA_F16,
+                     "traffic": None, "kernel_ms": k_ms,
+                     "note": "two bf16 products per output (a split into high part and residual), so the "
+                             "MFMA work is twice the algorithmic count"},
+    }
+
+
+def mla_workload(args, cpu):
+    """multi-head latent attention decode: one token against 4096 cached
+    latents, 128 heads, qk_nope 128, v 128, kv_lora_rank 512 (DeepSeek-V3 /
+    GLM-5.3 attention shape), fp32 kv_b_proj"""
+    import torch
+    import aigpu
+    H, DN, DV, C, L = 128, 128, 128, 512, 4096
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    q = torch.randn((1, H, DN), generator=gen, device="cuda")
+    lat = torch.randn((L + 1, C), generator=gen, device="cuda")
+    kvb = torch.randn((H * (DN + DV), C), generator=gen, device="cuda") / C ** 0.5
+    out = torch.empty((1, H, DV), dtype=torch.float32, device="cuda")
+    scale = 1.0 / (DN + 64) ** 0.5
+    step_ms, k_ms, launched_ms = time_steps(lambda: aigpu.latent_attention(q, lat, kvb, out, L, scale),
+                                            args.steps, args.warmup, "latent_attn_kernel")
+    nbytes = (L + 1) * C * 4.0 + kvb.numel() * 4.0
+    return {
+        "workload": "latent attention decode, 1 token at 4096, 128 heads, nope/v 128, rank 512, fp32",
+        "dtype": "f32", "value": nbytes / (step_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": step_ms,
+        "roofline": {"kernel": "all four kernels (fold, attention, merge, unfold)", "bound": "hbm",
+                     "achieved": nbytes / (launched_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
+                     "frac": nbytes / (launched_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
+                     "attn_kernel_ms": k_ms, "all_kernels_ms": launched_ms, "bytes_per_step": nbytes},
+    }
+
+
 def gdn_workload(args, cpu):
     """the steps either side of the recurrence at configs[4]'s shapes: the fused
     qkvz de-interleave + causal conv (K 4) + SiLU, then the gated norm"""
@@ -617,11 +666,16 @@ def main():
         extra["kda_rule"] = kda_workload(args, cpu)
     if args.workload in ("dense", "all"):
         extra["resident_decoder"] = dense_workload(args, cpu)
+    if args.workload in ("gemm", "all"):
+        extra["projection_gemm"] = gemm_workload(args, cpu)
+    if args.workload in ("mla", "all"):
+        extra["latent_attention"] = mla_workload(args, cpu)
     if args.workload == "all":
         extra["others"] = small_workloads(args)
     if head is None:   # a single non-prefill workload becomes the line
         head = (extra.pop("decode", None) or extra.pop("delta_rule", None) or extra.pop("gdn_neighbours", None)
-                or extra.pop("kda_rule", None) or extra.pop("resident_decoder"))
+                or extra.pop("kda_rule", None) or extra.pop("resident_decoder", None) or extra.pop("projection_gemm", None)
+                or extra.pop("latent_attention"))
     line = {
         "metric": "attn TFLOP/s (prefill) & KV GB/s (decode) as % roofline, 1 MI355X vs host CPU",
         "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,

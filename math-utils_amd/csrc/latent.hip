@@ -42,13 +42,16 @@ __device__ __forceinline__ float wkv_at(const void* w, size_t i) {
     return static_cast<const float*>(w)[i];
 }
 
-/* folded[t][h][c] = sum_d q[t][h][d] Wk_h[d][c] (:3124-3129), d in order;
-   workgroup (head, 256 columns, TT tokens) */
+/* folded[t][h][c] = sum_d q[t][h][d] Wk_h[d][c] (:3124-3129): workgroup
+   (head, 64 columns, TT tokens); the four waves take a quarter of d each (the
+   lanes on columns, coalesced rows of Wk) and add their sums in LDS */
 template <bool BF16>
 __global__ __launch_bounds__(256) void latent_fold_kernel(LatentArgs a) {
     __shared__ float qs[TT][MAX_NOPE];
+    __shared__ float part[4][TT][WAVE];
     const LatentParams& p = a.p;
-    const uint32_t h = blockIdx.x, c = blockIdx.y * 256 + threadIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t h = blockIdx.x, c = blockIdx.y * WAVE + lane;
     const uint64_t t0 = uint64_t(blockIdx.z) * TT;
     const uint32_t Dn = uint32_t(p.nope), C = uint32_t(p.rank);
     for (uint32_t i = threadIdx.x; i < TT * Dn; i += 256) {
@@ -56,18 +59,25 @@ __global__ __launch_bounds__(256) void latent_fold_kernel(LatentArgs a) {
         qs[t][d] = t0 + t < p.count ? p.q[((t0 + t) * p.heads + h) * Dn + d] : 0.0f;
     }
     __syncthreads();
-    if (c >= C) return;
     const size_t wk = size_t(h) * (p.nope + p.vdim) * C;
     float acc[TT] = {};
+    if (c < C) {
 #pragma unroll 8
-    for (uint32_t d = 0; d < Dn; ++d) {
-        const float w = wkv_at<BF16>(p.wkv, wk + size_t(d) * C + c);
+        for (uint32_t d = w; d < Dn; d += 4) {
+            const float wv = wkv_at<BF16>(p.wkv, wk + size_t(d) * C + c);
 #pragma unroll
-        for (int t = 0; t < TT; ++t) acc[t] = fmaf(qs[t][d], w, acc[t]);
+            for (int t = 0; t < TT; ++t) acc[t] = fmaf(qs[t][d], wv, acc[t]);
+        }
     }
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
-        if (t0 + t < p.count) a.folded[((t0 + t) * p.heads + h) * C + c] = acc[t];
+    for (int t = 0; t < TT; ++t) part[w][t][lane] = acc[t];
+    __syncthreads();
+    if (w == 0 && c < C) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+            if (t0 + t < p.count)
+                a.folded[((t0 + t) * p.heads + h) * C + c] = part[0][t][lane] + part[1][t][lane] + part[2][t][lane] + part[3][t][lane];
+    }
 }
 
 /* workgroup (token, 16 heads, key split): online softmax over blocks of KPB
@@ -93,9 +103,22 @@ __global__ __launch_bounds__(256) void latent_attn_kernel(LatentArgs a) {
     const uint64_t per = (blocks + a.splits - 1) / a.splits;
     const uint64_t bBegin = uint64_t(s) * per, bEnd = bBegin + per < blocks ? bBegin + per : blocks;
 
-    for (uint32_t i = tid; i < HG * C; i += 256) {
-        const uint32_t hh = i / C, c = i % C;
-        F[hh * MAX_RANK + c] = hh < nh ? a.folded[(t * p.heads + h0 + hh) * C + c] : 0.0f;
+    {
+        // 16 rows of C floats as float4, every load in flight (C % 16 == 0)
+        const uint32_t q4 = C / 4;
+        floatx4 fv[HG * MAX_RANK / 4 / 256];
+#pragma unroll
+        for (int e = 0; e < HG * MAX_RANK / 4 / 256; ++e) {
+            const uint32_t i = tid + 256 * e, hh = i / q4, c = 4 * (i % q4);
+            fv[e] = (i < HG * q4 && hh < nh)
+                        ? *reinterpret_cast<const floatx4*>(&a.folded[(t * p.heads + h0 + hh) * C + c])
+                        : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int e = 0; e < HG * MAX_RANK / 4 / 256; ++e) {
+            const uint32_t i = tid + 256 * e, hh = i / q4, c = 4 * (i % q4);
+            if (i < HG * q4) *reinterpret_cast<floatx4*>(&F[hh * MAX_RANK + c]) = fv[e];
+        }
     }
     __syncthreads();
 
@@ -109,7 +132,6 @@ __global__ __launch_bounds__(256) void latent_attn_kernel(LatentArgs a) {
         for (int e = 0; e < CPT; ++e) acc[hh][e] = 0.0f;
     }
     const uint32_t kq = uint32_t(tid) >> 2, part = uint32_t(tid) & 3;   // key in block, quarter of its row
-    const uint32_t qlen = C / 4;                                        // C % 16 == 0
     for (uint64_t b = bBegin; b < bEnd; ++b) {
         const uint64_t i = b * KPB + kq;
         const bool live = i < n;
@@ -119,19 +141,21 @@ __global__ __launch_bounds__(256) void latent_attn_kernel(LatentArgs a) {
 #pragma unroll
         for (int hh = 0; hh < HG; ++hh) sc[hh] = 0.0f;
         if (live) {
-            const float* lr = p.latent + size_t(key) * C + part * qlen;
-            for (uint32_t c0 = 0; c0 < qlen; c0 += 32) {
+            // the key's four lanes take interleaved 16-byte pieces (lane part
+            // reads columns 16 j + 4 part), so the four read neighbouring banks
+            const float* lr = p.latent + size_t(key) * C + 4 * part;
+            for (uint32_t c0 = 0; c0 < C; c0 += 128) {
                 floatx4 l4[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    l4[e] = c0 + 4 * e < qlen ? *reinterpret_cast<const floatx4*>(lr + c0 + 4 * e)
-                                              : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                    l4[e] = c0 + 16 * e < C ? *reinterpret_cast<const floatx4*>(lr + c0 + 16 * e)
+                                            : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int hh = 0; hh < HG; ++hh) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        if (c0 + 4 * e < qlen) {
-                            const floatx4 f4 = *reinterpret_cast<const floatx4*>(&F[hh * MAX_RANK + part * qlen + c0 + 4 * e]);
+                        if (c0 + 16 * e < C) {
+                            const floatx4 f4 = *reinterpret_cast<const floatx4*>(&F[hh * MAX_RANK + c0 + 16 * e + 4 * part]);
                             sc[hh] = fmaf(f4[0], l4[e][0], fmaf(f4[1], l4[e][1], fmaf(f4[2], l4[e][2], fmaf(f4[3], l4[e][3], sc[hh]))));
                         }
                     }
@@ -166,17 +190,17 @@ __global__ __launch_bounds__(256) void latent_attn_kernel(LatentArgs a) {
         }
         // context: the block's keys against the thread's columns
         const uint32_t nb = uint32_t(n - b * KPB < uint64_t(KPB) ? n - b * KPB : uint64_t(KPB));
-        for (uint32_t k0 = 0; k0 < nb; k0 += 8) {
-            float lv[8][CPT];
+        for (uint32_t k0 = 0; k0 < nb; k0 += 16) {
+            float lv[16][CPT];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < 16; ++u) {
                 const uint32_t kk = k0 + u < nb ? k0 + u : k0;
                 const float* lr = p.latent + size_t(keyAt[kk]) * C;
 #pragma unroll
                 for (int e = 0; e < CPT; ++e) lv[u][e] = tid + 256 * e < int(C) ? lr[tid + 256 * e] : 0.0f;
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < 16; ++u) {
                 if (k0 + u >= nb) break;
 #pragma unroll
                 for (int hh = 0; hh < HG; ++hh) {
@@ -215,29 +239,36 @@ __global__ __launch_bounds__(256) void latent_attn_kernel(LatentArgs a) {
     }
 }
 
-/* the splits' records of one (token, head) combined into its context */
+/* the splits' records of one (token, head) combined into its context: each
+   wave reduces the (at most 64) maxima and sums with a lane per split, then
+   the threads sum the accumulators column by column */
 __global__ __launch_bounds__(256) void latent_merge_kernel(LatentArgs a) {
     const LatentParams& p = a.p;
     const uint64_t t = blockIdx.x;
     const uint32_t h = blockIdx.y, C = uint32_t(p.rank);
+    const int lane = threadIdx.x & 63;
     const size_t rec = size_t(C) + 2;
     const float* base = a.partial + (t * p.heads + h) * a.splits * rec;
-    float M = -INFINITY;
-    for (uint32_t i = 0; i < a.splits; ++i) M = fmaxf(M, base[i * rec]);
-    float L = 0.0f;
-    for (uint32_t i = 0; i < a.splits; ++i)
-        if (base[i * rec] != -INFINITY) L = fmaf(base[i * rec + 1], expf(base[i * rec] - M), L);
+    const float mi = lane < int(a.splits) ? base[lane * rec] : -INFINITY;
+    const float M = wave_max(mi);
+    const float fi = (lane < int(a.splits) && mi != -INFINITY) ? expf(mi - M) : 0.0f;
+    const float L = wave_sum(lane < int(a.splits) ? base[lane * rec + 1] * fi : 0.0f);
     const float inv = 1.0f / L;
     for (uint32_t c = threadIdx.x; c < C; c += 256) {
         float acc = 0.0f;
-        for (uint32_t i = 0; i < a.splits; ++i)
-            if (base[i * rec] != -INFINITY) acc = fmaf(base[i * rec + 2 + c], expf(base[i * rec] - M), acc);
+#pragma unroll 8
+        for (uint32_t i = 0; i < a.splits; ++i) {
+            const float m = base[i * rec];
+            acc = fmaf(base[i * rec + 2 + c], m == -INFINITY ? 0.0f : expf(m - M), acc);
+        }
         a.context[(t * p.heads + h) * C + c] = acc * inv;
     }
 }
 
-/* out[t][h][v] = Wv_h[v] . context[t][h] (:3153-3154); workgroup (head, TT
-   tokens), thread v */
+/* out[t][h][v] = Wv_h[v] . context[t][h] (:3153-3154): workgroup (head,
+   TT tokens), each wave a quarter of the v rows, the lanes along the rank
+   (16-byte loads of the row), the TT contexts in LDS, a wave reduction per
+   (row, token) */
 template <bool BF16>
 __global__ __launch_bounds__(256) void latent_unfold_kernel(LatentArgs a) {
     __shared__ float cs[TT * MAX_RANK];
@@ -245,24 +276,45 @@ __global__ __launch_bounds__(256) void latent_unfold_kernel(LatentArgs a) {
     const uint32_t h = blockIdx.x;
     const uint64_t t0 = uint64_t(blockIdx.y) * TT;
     const uint32_t C = uint32_t(p.rank), Dv = uint32_t(p.vdim);
-    for (uint32_t i = threadIdx.x; i < TT * C; i += 256) {
-        const uint32_t t = i / C, c = i % C;
-        cs[t * MAX_RANK + c] = t0 + t < p.count ? a.context[((t0 + t) * p.heads + h) * C + c] : 0.0f;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (uint32_t i = threadIdx.x; i < TT * C / 4; i += 256) {
+        const uint32_t t = i / (C / 4), c = 4 * (i % (C / 4));
+        *reinterpret_cast<floatx4*>(&cs[t * MAX_RANK + c]) =
+            t0 + t < p.count ? *reinterpret_cast<const floatx4*>(&a.context[((t0 + t) * p.heads + h) * C + c])
+                             : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
     __syncthreads();
-    const uint32_t v = threadIdx.x;
-    if (v >= Dv) return;
-    const size_t wv = (size_t(h) * (p.nope + p.vdim) + p.nope + v) * C;
-    float acc[TT] = {};
-#pragma unroll 8
-    for (uint32_t c = 0; c < C; ++c) {
-        const float w = wkv_at<BF16>(p.wkv, wv + c);
+    const size_t wv0 = (size_t(h) * (p.nope + p.vdim) + p.nope) * C;
+    const int tn = int(p.count - t0 < uint64_t(TT) ? p.count - t0 : uint64_t(TT));
+    for (uint32_t v = w; v < Dv; v += 4) {
+        float acc[TT] = {};
+        for (uint32_t c = 4 * lane; c < C; c += 4 * WAVE) {
+            float wr[4];
+            if constexpr (BF16) {
+                const u32x2 b = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(p.wkv) + wv0 + size_t(v) * C + c);
+                wr[0] = __uint_as_float(b[0] << 16);
+                wr[1] = __uint_as_float(b[0] & 0xFFFF0000u);
+                wr[2] = __uint_as_float(b[1] << 16);
+                wr[3] = __uint_as_float(b[1] & 0xFFFF0000u);
+            } else {
+                const floatx4 f = *reinterpret_cast<const floatx4*>(static_cast<const float*>(p.wkv) + wv0 + size_t(v) * C + c);
 #pragma unroll
-        for (int t = 0; t < TT; ++t) acc[t] = fmaf(w, cs[t * MAX_RANK + c], acc[t]);
+                for (int e = 0; e < 4; ++e) wr[e] = f[e];
+            }
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) {
+                if (tt >= tn) break;   // uniform
+                const floatx4 x = *reinterpret_cast<const floatx4*>(&cs[tt * MAX_RANK + c]);
+                acc[tt] = fmaf(wr[0], x[0], fmaf(wr[1], x[1], fmaf(wr[2], x[2], fmaf(wr[3], x[3], acc[tt]))));
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+            if (tt >= tn) break;   // uniform
+            const float sum = wave_sum(acc[tt]);
+            if (lane == 0) p.out[((t0 + tt) * p.heads + h) * Dv + v] = sum;
+        }
     }
-#pragma unroll
-    for (int t = 0; t < TT; ++t)
-        if (t0 + t < p.count) p.out[((t0 + t) * p.heads + h) * Dv + v] = acc[t];
 }
 
 } // namespace
@@ -290,7 +342,8 @@ bool launch_latent_attention(const LatentParams& p, hipStream_t stream) {
     if (want > maxBlocks) want = maxBlocks;
     if (want < 1) want = 1;
     if (want > 64) want = 64;
-    a.splits = uint32_t(want);
+    const uint64_t per = (maxBlocks + want - 1) / want;
+    a.splits = uint32_t((maxBlocks + per - 1) / per);   // every split of the longest token has blocks
     const size_t cells = size_t(p.count) * p.heads * p.rank;
     const size_t bytes = (2 * cells + (a.splits > 1 ? size_t(p.count) * p.heads * a.splits * (p.rank + 2) : 0)) * 4;
     float* work = static_cast<float*>(ctx.grow(SLOT_LATENT, bytes));
@@ -299,7 +352,7 @@ bool launch_latent_attention(const LatentParams& p, hipStream_t stream) {
     a.context = work + cells;
     a.partial = work + 2 * cells;
     const bool bf16 = p.wType == 1;
-    const dim3 fgrid(unsigned(p.heads), unsigned((p.rank + 255) / 256), unsigned((p.count + TT - 1) / TT));
+    const dim3 fgrid(unsigned(p.heads), unsigned((p.rank + WAVE - 1) / WAVE), unsigned((p.count + TT - 1) / TT));
     if (fgrid.z > 65535u) return ctx.fail("latent attention: too many tokens for one call");
     if (!ctx.launch("latent_fold_kernel", stream, [&] {
             if (bf16) hipLaunchKernelGGL(latent_fold_kernel<true>, fgrid, dim3(256), 0, stream, a);
