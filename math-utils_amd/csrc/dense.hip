@@ -6,13 +6,14 @@
 // (LocalModel.hpp:3598-3645) is the caller, and the step is LocalModel::
 // forward's layer loop for count = 1 (:3705-3799).
 //
-// Per layer, five launches on one stream:
+// Per layer, six launches on one stream:
 //   dense_gemv_kernel   q, k, v (+ bias) of RMSNorm(x) * inputNorm, the norm
 //                       computed by each wave from x
 //   dense_attn_kernel   per (span of positions, kv head): q/k RMSNorm and
 //                       RoPE at the position, the k, v rows appended to the
 //                       cache, split-K attention for all of the kv head's
-//                       query heads, and the merge by the last workgroup
+//                       query heads
+//   dense_merge_kernel  the splits combined per kv head
 //   dense_gemv_kernel   x += o . attn
 //   dense_gemv_kernel   gate, up of RMSNorm(x) * postNorm
 //   dense_gemv_kernel   x += down . (silu(gate) * up)
@@ -154,13 +155,11 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseGemvArgs p) {
    - norms and rotates the G query heads of the kv head itself (attentionMixer,
      LocalModel.hpp:2606-2648) and, in the split holding `pos`, the new key,
      appending it and the value row to the cache;
-   - per chunk, scores its positions (lane = position, the key row's 16-byte
-     loads in flight; the new position from LDS) and accumulates P.V (lanes
-     on dimensions, each wave a quarter of the positions, eight rows in
+   - per chunk, scores its positions (two lanes per key row, every 16-byte
+     load in flight; the new position from LDS) and accumulates P.V (lanes on
+     dimensions, each wave a quarter of the positions, all 32 rows in
      flight);
-   - leaves one record per query head: max, sum, acc[D].
-   The last workgroup of each kv head to finish (a ticket per kv head, reset by
-   that workgroup) merges the records into the attention output. */
+   - leaves one record per query head: max, sum, acc[D]. */
 constexpr int MAX_SPLITS = 64;
 
 __device__ __forceinline__ void attn_span(uint32_t pos, uint32_t window, uint32_t& first, uint32_t& splits,
@@ -175,13 +174,12 @@ template <int DPL>   // head dimensions per lane: 2 (D <= 128) or 4 (D <= 256)
 __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const float* qRaw, const float* kRaw,
                                                          const float* vRaw, const float* qNorm, const float* kNorm,
                                                          const float* freqs, float* keys, float* values,
-                                                         float* partial, uint32_t* tickets, float* attn) {
+                                                         float* partial) {
     __shared__ float qs[MAX_GROUP * MAX_DIM];
     __shared__ float kn[MAX_DIM], vn[MAX_DIM];
     __shared__ float pr[MAX_GROUP][SPLIT];
     __shared__ float wm[4][MAX_GROUP];
     __shared__ floatx4 red[256];
-    __shared__ uint32_t last;
 
     const uint32_t pos = *a.pos;
     uint32_t first, splits, chunksPer;
@@ -351,26 +349,29 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
         __syncthreads();
     }
 
-    // the last workgroup of this kv head merges every split's records
-    if (tid == 0) {
-        __threadfence();
-        last = atomicAdd(&tickets[kvh], 1u) + 1 == splits ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
+}
+
+
+/* the splits' records of every query head of one kv head, combined (a launch
+   of its own: a workgroup-to-workgroup handoff inside the attention kernel
+   needs a device-scope fence, which on this part writes back the L2) */
+__global__ __launch_bounds__(256) void dense_merge_kernel(DenseArgs a, const float* partial, float* attn) {
+    __shared__ floatx4 red[256];
+    const uint32_t pos = *a.pos;
+    uint32_t first, splits, chunksPer;
+    attn_span(pos, a.window, first, splits, chunksPer);
+    const uint32_t kvh = blockIdx.x, G = a.heads / a.kvHeads, D = a.dim;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const size_t rec = size_t(D) + 2;
     const uint32_t quads = D / 4, RL = 256 / quads;   // D % 4 == 0, D <= 256
     const uint32_t dq = tid % quads, r = tid / quads;
     for (uint32_t g = 0; g < G; ++g) {
         const float* base = partial + (size_t(kvh) * G + g) * a.maxSplits * rec;
-        // every thread reads the (at most MAX_SPLITS) maxima and sums: lane i
-        // of each wave takes split i, a wave reduction combines them
         float M = -INFINITY, L = 0.0f;
-        {
-            const float mi = lane < int(splits) ? base[lane * rec] : -INFINITY;
-            M = wave_max(mi);
-            L = wave_sum(lane < int(splits) ? base[lane * rec + 1] * expf(mi - M) : 0.0f);
-        }
+        for (uint32_t i = lane; i < splits; i += WAVE) M = fmaxf(M, base[i * rec]);
+        M = wave_max(M);
+        for (uint32_t i = lane; i < splits; i += WAVE) L += base[i * rec + 1] * expf(base[i * rec] - M);
+        L = wave_sum(L);
         floatx4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
         if (r < RL) {
 #pragma unroll 4
@@ -396,7 +397,6 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
         }
         __syncthreads();
     }
-    if (tid == 0) tickets[kvh] = 0;   // ready for the next layer
 }
 
 struct DevWeight {
@@ -423,7 +423,6 @@ struct DenseModel {
     float *x = nullptr, *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
     float *gate = nullptr, *up = nullptr, *logits = nullptr, *partial = nullptr;
     uint32_t* pos = nullptr;
-    uint32_t* tickets = nullptr;   // per kv head, zero between launches
     std::vector<void*> owned;
     uint64_t bytes = 0;
 
@@ -542,10 +541,14 @@ bool run_step(DenseModel& d, uint32_t splits, hipStream_t stream) {
         if (!ctx.launch("dense_attn_kernel", stream, [&] {
                 if (c.headDim <= 128)
                     hipLaunchKernelGGL(dense_attn_kernel<2>, dim3(splits, c.kvHeads), dim3(256), 0, stream, a, d.q, d.k,
-                                       d.v, L.qNorm, L.kNorm, d.freqs, L.keys, L.values, d.partial, d.tickets, d.attn);
+                                       d.v, L.qNorm, L.kNorm, d.freqs, L.keys, L.values, d.partial);
                 else
                     hipLaunchKernelGGL(dense_attn_kernel<4>, dim3(splits, c.kvHeads), dim3(256), 0, stream, a, d.q, d.k,
-                                       d.v, L.qNorm, L.kNorm, d.freqs, L.keys, L.values, d.partial, d.tickets, d.attn);
+                                       d.v, L.qNorm, L.kNorm, d.freqs, L.keys, L.values, d.partial);
+            }))
+            return false;
+        if (!ctx.launch("dense_merge_kernel", stream, [&] {
+                hipLaunchKernelGGL(dense_merge_kernel, dim3(c.kvHeads), dim3(256), 0, stream, a, d.partial, d.attn);
             }))
             return false;
         if (!dense_gemv({{&L.o, d.x}}, d.attn, nullptr, nullptr, 0.0f, 0, true, stream)) return false;
@@ -609,7 +612,6 @@ AIGPU_ABI void* aigpu_dense_create(const AiGpuDenseConfig* c, const AiGpuDenseLa
         d->maxSplits = aigpu::host_splits(c->capacity - 1, 0);
         d->partial = d->floats(uint64_t(c->heads) * d->maxSplits * (c->headDim + 2));
         d->pos = reinterpret_cast<uint32_t*>(d->floats(1));
-        d->tickets = reinterpret_cast<uint32_t*>(d->floats(c->kvHeads));
         for (uint32_t i = 0; i < c->layers; ++i) {
             const AiGpuDenseLayer& l = layers[i];
             if (!l.inputNorm || !l.postNorm || !keys[i] || !values[i])
