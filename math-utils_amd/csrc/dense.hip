@@ -54,7 +54,7 @@ struct DenseArgs {
 
 /* ---- projections with the step before them fused into the input ----
    PRE 0: a = x;  PRE 1: a = RMSNorm(x) * gamma (rmsNormRow,
-   LocalModel.hpp:1341-1348), each wave computing the norm itself;
+   LocalModel.hpp:1341-1348), the workgroup computing the norm once;
    PRE 2: a = silu(x) * x2 (swiglu, :3282-3288).
    Up to three weights of one encoding share the launch (q, k, v; gate, up):
    rows [start_s, start_s + n_s) belong to segment s. */
@@ -78,62 +78,103 @@ struct DenseGemvArgs {
     float eps;
 };
 
+constexpr int DG_LDS_K = 12288;   // activation floats staged in LDS (at most 48 KB, sized to k)
+constexpr int DG_BATCH = 8;       // weight pieces per lane and row loaded together
+
+/* The workgroup first requests each wave's first DG_BATCH weight pieces,
+   then builds the activation (PRE applied) once in LDS, then the waves dot
+   their rows against it; k up to DG_LDS_K. */
 template <int TYPE, int PRE>
 __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseGemvArgs p) {
     constexpr int E = piece_elems<TYPE>();
-    const int lane = threadIdx.x & 63;
-    const uint32_t row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * DG_ROWS;
-    if (row0 >= p.rows) return;   // whole wave leaves; no block barriers
+    extern __shared__ __align__(16) float xa[];   // k floats
+    __shared__ float part[4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t row0 = (blockIdx.x * 4 + w) * DG_ROWS;
+    const bool active = row0 < p.rows;
     int sg = 0;
     if (p.nseg > 1 && row0 >= p.seg[1].start) sg = 1;
     if (p.nseg > 2 && row0 >= p.seg[2].start) sg = 2;
     const DenseSeg S = p.seg[sg];
-    const uint32_t r0 = row0 - S.start;   // DG_ROWS rows never straddle segments (every n is even)
+    const uint32_t r0 = active ? row0 - S.start : 0;   // DG_ROWS rows never straddle segments (every n is even)
     const size_t rowBytes = size_t(p.k) * row_bytes_per_k_x2<TYPE>() / 2;
     const uint32_t pieces = p.k / E, blocks = p.k / 32;
+    const uint32_t rr1 = r0 + 1 < S.n ? r0 + 1 : r0;   // a row count that is odd repeats the last row
 
+    // the first batch of weight pieces, before anything waits
+    u32x4 wv[DG_BATCH][DG_ROWS];
+#pragma unroll
+    for (int b = 0; b < DG_BATCH; ++b) {
+        const uint32_t c = lane + WAVE * b;
+        if (active && c < pieces) {
+            wv[b][0] = *reinterpret_cast<const u32x4*>(S.w + r0 * rowBytes + size_t(c) * 16);
+            wv[b][1] = *reinterpret_cast<const u32x4*>(S.w + rr1 * rowBytes + size_t(c) * 16);
+        }
+    }
+
+    // the activation, once per workgroup
     float inv = 1.0f;
     if constexpr (PRE == 1) {
         float ss = 0.0f;
-        for (uint32_t i = lane; i < p.k / 4; i += WAVE) {
+        for (uint32_t i = tid; i < p.k / 4; i += 256) {
             const floatx4 v = reinterpret_cast<const floatx4*>(p.x)[i];
             ss = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], fmaf(v[3], v[3], ss))));
         }
-        inv = 1.0f / sqrtf(wave_sum(ss) / float(p.k) + p.eps);
+        ss = wave_sum(ss);
+        if (lane == 0) part[w] = ss;
+        __syncthreads();
+        inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / float(p.k) + p.eps);
     }
+    for (uint32_t i = tid; i < p.k / 4; i += 256) {
+        const floatx4 v = reinterpret_cast<const floatx4*>(p.x)[i];
+        floatx4 o;
+        if constexpr (PRE == 1) {
+            const floatx4 gm = reinterpret_cast<const floatx4*>(p.gamma)[i];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) o[t] = v[t] * inv * gm[t];
+        } else if constexpr (PRE == 2) {
+            const floatx4 u = reinterpret_cast<const floatx4*>(p.x2)[i];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) o[t] = v[t] / (1.0f + expf(-v[t])) * u[t];
+        } else {
+            o = v;
+        }
+        reinterpret_cast<floatx4*>(xa)[i] = o;
+    }
+    __syncthreads();
+    if (!active) return;
 
     float acc[DG_ROWS] = {};
-#pragma unroll 2
-    for (uint32_t c = lane; c < pieces; c += WAVE) {
-        u32x4 wv[DG_ROWS];
-        float sc[DG_ROWS];
+    const float* s0 = TYPE >= 2 ? S.scales + size_t(r0) * blocks : nullptr;
+    const float* s1 = TYPE >= 2 ? S.scales + size_t(rr1) * blocks : nullptr;
+    for (uint32_t c0 = 0; c0 < pieces; c0 += WAVE * DG_BATCH) {
+        if (c0 > 0) {
 #pragma unroll
-        for (int r = 0; r < DG_ROWS; ++r) {
-            wv[r] = *reinterpret_cast<const u32x4*>(S.w + (r0 + r) * rowBytes + size_t(c) * 16);
-            sc[r] = TYPE == 2 ? S.scales[size_t(r0 + r) * blocks + (c >> 1)]
-                              : (TYPE == 3 ? S.scales[size_t(r0 + r) * blocks + c] : 1.0f);
-        }
-        float xa[E];
-#pragma unroll
-        for (int e = 0; e < E; e += 4) {
-            const floatx4 v = *reinterpret_cast<const floatx4*>(p.x + size_t(c) * E + e);
-            if constexpr (PRE == 1) {
-                const floatx4 gm = *reinterpret_cast<const floatx4*>(p.gamma + size_t(c) * E + e);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) xa[e + t] = v[t] * inv * gm[t];
-            } else if constexpr (PRE == 2) {
-                const floatx4 u = *reinterpret_cast<const floatx4*>(p.x2 + size_t(c) * E + e);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) xa[e + t] = v[t] / (1.0f + expf(-v[t])) * u[t];
-            } else {
-#pragma unroll
-                for (int t = 0; t < 4; ++t) xa[e + t] = v[t];
+            for (int b = 0; b < DG_BATCH; ++b) {
+                const uint32_t c = c0 + lane + WAVE * b;
+                if (c < pieces) {
+                    wv[b][0] = *reinterpret_cast<const u32x4*>(S.w + r0 * rowBytes + size_t(c) * 16);
+                    wv[b][1] = *reinterpret_cast<const u32x4*>(S.w + rr1 * rowBytes + size_t(c) * 16);
+                }
             }
         }
 #pragma unroll
-        for (int r = 0; r < DG_ROWS; ++r) {
-            const float d = piece_dot<TYPE>(wv[r], xa);
-            acc[r] = TYPE >= 2 ? fmaf(d, sc[r], acc[r]) : acc[r] + d;
+        for (int b = 0; b < DG_BATCH; ++b) {
+            const uint32_t c = c0 + lane + WAVE * b;
+            if (c < pieces) {
+                const float* x = xa + size_t(c) * E;
+                const float d0 = piece_dot<TYPE>(wv[b][0], x), d1 = piece_dot<TYPE>(wv[b][1], x);
+                if constexpr (TYPE == 2) {
+                    acc[0] = fmaf(d0, s0[c >> 1], acc[0]);
+                    acc[1] = fmaf(d1, s1[c >> 1], acc[1]);
+                } else if constexpr (TYPE == 3) {
+                    acc[0] = fmaf(d0, s0[c], acc[0]);
+                    acc[1] = fmaf(d1, s1[c], acc[1]);
+                } else {
+                    acc[0] += d0;
+                    acc[1] += d1;
+                }
+            }
         }
     }
 #pragma unroll
@@ -453,10 +494,11 @@ struct DenseModel {
         if (w.inDim != in || w.outDim != out)
             throw std::invalid_argument(std::string("resident ") + what + " dimensions do not match config");
         if (!w.codes || w.type > 3 || (w.type >= 2 && (!w.scales || w.inDim % 32)) || w.inDim % 4 ||
-            (w.type == 1 && w.inDim % 8) || (reinterpret_cast<uintptr_t>(w.codes) % 16))
+            (w.type == 1 && w.inDim % 8) || (reinterpret_cast<uintptr_t>(w.codes) % 16) ||
+            w.inDim > uint32_t(DG_LDS_K))
             throw std::invalid_argument(std::string("resident ") + what +
                                         " weight is not usable (bf16 rows need inDim % 8, quantised inDim % 32, "
-                                        "and the codes 16-byte aligned)");
+                                        "inDim at most 12288, and the codes 16-byte aligned)");
         DevWeight d;
         d.codes = w.codes;
         d.scales = static_cast<const float*>(w.scales);
@@ -476,7 +518,7 @@ struct Seg {
 template <int TYPE, int PRE>
 void launch_dense_gemv(const DenseGemvArgs& p, hipStream_t stream) {
     const unsigned grid = unsigned((p.rows + 4 * DG_ROWS - 1) / (4 * DG_ROWS));
-    hipLaunchKernelGGL((dense_gemv_kernel<TYPE, PRE>), dim3(grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((dense_gemv_kernel<TYPE, PRE>), dim3(grid), dim3(256), size_t(p.k) * sizeof(float), stream, p);
 }
 
 /* one launch for weights of one encoding whose row counts are even (rows
