@@ -837,15 +837,6 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-/* workgroup barrier that waits for this wave's LDS traffic only: the DMA in
-   flight for a later chunk keeps going */
-__device__ __forceinline__ void lds_barrier() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 /* One 1 KB DMA block: each lane's 16 bytes from `src` into LDS at
    lds + 16 * lane. Written as asm so the compiler's wait analysis does not
    track it (it cannot tell the double-buffered stages apart and would wait for

@@ -7,8 +7,8 @@
 // forward's layer loop for count = 1 (:3705-3799).
 //
 // Per layer, six launches on one stream:
-//   dense_gemv_kernel   q, k, v (+ bias) of RMSNorm(x) * inputNorm, the norm
-//                       computed by each wave from x
+//   dense_gemv_kernel   q, k, v (+ bias) of RMSNorm(x) * inputNorm, the
+//                       normalised row built once per workgroup in LDS
 //   dense_attn_kernel   per (span of positions, kv head): q/k RMSNorm and
 //                       RoPE at the position, the k, v rows appended to the
 //                       cache, split-K attention for all of the kv head's
@@ -48,7 +48,7 @@ constexpr int MAX_GROUP = 8;   // query heads per kv head
 
 struct DenseArgs {
     const uint32_t* pos;   // device: the position being decoded
-    uint32_t heads, kvHeads, dim, rot, maxSplits, window;
+    uint32_t heads, kvHeads, dim, rot, maxSplits, window, capacity;
     float eps;
 };
 
@@ -196,12 +196,16 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseGemvArgs p) {
    - norms and rotates the G query heads of the kv head itself (attentionMixer,
      LocalModel.hpp:2606-2648) and, in the split holding `pos`, the new key,
      appending it and the value row to the cache;
-   - per chunk, scores its positions (two lanes per key row, every 16-byte
-     load in flight; the new position from LDS) and accumulates P.V (lanes on
-     dimensions, each wave a quarter of the positions, all 32 rows in
-     flight);
-   - leaves one record per query head: max, sum, acc[D]. */
+   - per chunk, each wave takes 32 of the positions with a softmax state of
+     its own (no barrier inside the chunk loop): every key and value load of
+     the wave is issued before anything waits, the keys eight lanes to a row
+     so that one load instruction covers 8 rows x 128 contiguous bytes;
+     scores, probabilities and P.V stay in the wave's registers;
+   - combines the four waves into one record per query head: max, sum, pad,
+     acc[D] (D + 4 floats, so acc is 16-byte aligned). */
 constexpr int MAX_SPLITS = 64;
+constexpr int REC_PAD = 4;   // max, sum, two unused floats before acc
+constexpr int BUFFER_FLAGS = 0x00020000;   // buffer descriptor word 3: 32-bit data format, raw (stride 0) access
 
 __device__ __forceinline__ void attn_span(uint32_t pos, uint32_t window, uint32_t& first, uint32_t& splits,
                                           uint32_t& chunksPer) {
@@ -211,16 +215,45 @@ __device__ __forceinline__ void attn_span(uint32_t pos, uint32_t window, uint32_
     splits = (chunks + chunksPer - 1) / chunksPer;
 }
 
-template <int DPL>   // head dimensions per lane: 2 (D <= 128) or 4 (D <= 256)
+/* the sum over each group of 8 lanes (lanes 8i .. 8i + 7), in every lane of
+   the group: quad_perm xor 1, quad_perm xor 2, then row_half_mirror, which
+   pairs each lane of a quad with one of the other quad */
+__device__ __forceinline__ float sum8(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xf, 0xf, false));
+    return x;
+}
+
+/* over lanes l, l ^ 8, l ^ 16, ..., l ^ 56 (the eight groups' lane l % 8):
+   row_ror 8 swaps the halves of each 16-lane row, then two cross-row steps */
+__device__ __forceinline__ float max_across8(float x) {
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false)));
+    x = fmaxf(x, __shfl_xor(x, 16, WAVE));
+    return fmaxf(x, __shfl_xor(x, 32, WAVE));
+}
+__device__ __forceinline__ float sum_across8(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));
+    x += __shfl_xor(x, 16, WAVE);
+    return x + __shfl_xor(x, 32, WAVE);
+}
+
+template <int DPL, int GMAX>   // value dimensions per lane: 2 (D <= 128) or 4 (D <= 256); G <= GMAX
 __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const float* qRaw, const float* kRaw,
                                                          const float* vRaw, const float* qNorm, const float* kNorm,
                                                          const float* freqs, float* keys, float* values,
                                                          float* partial) {
-    __shared__ float qs[MAX_GROUP * MAX_DIM];
-    __shared__ float kn[MAX_DIM], vn[MAX_DIM];
-    __shared__ float pr[MAX_GROUP][SPLIT];
-    __shared__ float wm[4][MAX_GROUP];
-    __shared__ floatx4 red[256];
+    constexpr int KE = 2 * DPL;     // 16-byte key pieces per lane and row (32 floats apart)
+    constexpr int RG = 4;           // groups of 8 rows
+    constexpr int PW = SPLIT / 4;   // rows per wave and chunk
+    static_assert(PW == RG * 8, "a wave's rows are RG groups of 8");
+    constexpr int QPT = GMAX * MAX_DIM / 256;   // query floats per thread, at most
+    __shared__ __align__(16) float qs[GMAX * MAX_DIM];
+    __shared__ __align__(16) float kn[MAX_DIM];
+    __shared__ __align__(16) float vn[MAX_DIM];
+    __shared__ __align__(16) float pb[4][PW];   // a wave's probabilities, broadcast to its lanes
+    __shared__ float wm[4][GMAX], wl[4][GMAX];
+    __shared__ __align__(16) float wacc[4][GMAX * MAX_DIM];
 
     const uint32_t pos = *a.pos;
     uint32_t first, splits, chunksPer;
@@ -228,215 +261,271 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
     const uint32_t s = blockIdx.x, kvh = blockIdx.y;
     if (s >= splits) return;   // whole workgroup leaves before any barrier
     const uint32_t G = a.heads / a.kvHeads, D = a.dim;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform, so row offsets stay scalar
     const size_t kvW = size_t(a.kvHeads) * D;
     const float scale = 1.0f / sqrtf(float(D));
     const bool holdsPos = s + 1 == splits;
-
-    for (uint32_t i = tid; i < G * D; i += 256) qs[i] = qRaw[size_t(kvh) * G * D + i];
-    if (holdsPos)
-        for (uint32_t i = tid; i < D; i += 256) {
-            kn[i] = kRaw[size_t(kvh) * D + i];
-            vn[i] = vRaw[size_t(kvh) * D + i];
-        }
-    __syncthreads();
-    for (uint32_t g = w; g < G; g += 4) norm_rope_row(&qs[g * D], int(D), qNorm, a.eps, 0.0f, freqs, int(a.rot), pos, lane);
-    if (holdsPos && w == int(G % 4)) {
-        norm_rope_row(kn, int(D), kNorm, a.eps, 0.0f, freqs, int(a.rot), pos, lane);
-        for (uint32_t d = lane; d < D; d += WAVE) {
-            keys[size_t(pos) * kvW + size_t(kvh) * D + d] = kn[d];
-            values[size_t(pos) * kvW + size_t(kvh) * D + d] = vn[d];
-        }
-    }
-    __syncthreads();
-
-    float mrun[MAX_GROUP], lrun[MAX_GROUP], acc[MAX_GROUP][DPL];
+    const uint32_t sub = lane & 7, rl = lane >> 3;   // key layout: row rl of a group, floats 4 sub + 32 e
+    const bool vlive = uint32_t(DPL * lane) < D;     // value layout: floats DPL lane .. + DPL - 1
+    // the layer's cache through buffer descriptors: a lane offset in a VGPR,
+    // the row in a scalar offset (byte offsets fit 32 bits: checked at creation)
+    const uint32_t cacheBytes = uint32_t(a.capacity * kvW * sizeof(float));
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(keys, 0, cacheBytes, BUFFER_FLAGS);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(values, 0, cacheBytes, BUFFER_FLAGS);
+    const uint32_t rowBytes = uint32_t(kvW * sizeof(float));
+    // pieces past D load the row's last piece (in bounds) and are zeroed
+    uint32_t kCol[KE];
+    bool kLive[KE];
 #pragma unroll
-    for (int g = 0; g < MAX_GROUP; ++g) {
+    for (int e = 0; e < KE; ++e) {
+        kLive[e] = 4 * sub + 32 * e < D;
+        kCol[e] = kLive[e] ? 4 * sub + 32 * e : D - 4;
+    }
+    const uint32_t kOff = uint32_t(kvh * D * sizeof(float));
+    const uint32_t vOff = uint32_t((kvh * D + (vlive ? DPL * lane : 0)) * sizeof(float));
+
+    // the raw query rows and new key/value rows first, so that their use
+    // below does not wait for the cache loads issued after them
+    float qr[QPT], knr = 0.0f, vnr = 0.0f;
+#pragma unroll
+    for (int t = 0; t < QPT; ++t) {
+        const uint32_t i = uint32_t(tid) + 256 * t;
+        qr[t] = i < G * D ? qRaw[size_t(kvh) * G * D + i] : 0.0f;
+    }
+    if (holdsPos && uint32_t(tid) < D) {
+        knr = kRaw[size_t(kvh) * D + tid];
+        vnr = vRaw[size_t(kvh) * D + tid];
+    }
+
+    float mrun[GMAX], lrun[GMAX], acc[GMAX][DPL];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
         mrun[g] = -INFINITY;
         lrun[g] = 0.0f;
 #pragma unroll
         for (int e = 0; e < DPL; ++e) acc[g][e] = 0.0f;
     }
-    constexpr int HALF = DPL * 32;   // key elements per scoring thread: half a row
     const uint32_t cBegin = s * chunksPer;
+#pragma unroll 1
     for (uint32_t c = cBegin; c < cBegin + chunksPer; ++c) {
         const uint32_t j0 = first + c * SPLIT;
         if (j0 > pos) break;   // uniform: the last split may hold fewer chunks
         const uint32_t n = pos + 1 - j0 < uint32_t(SPLIT) ? pos + 1 - j0 : uint32_t(SPLIT);
         const uint32_t jp = pos - j0 < n ? pos - j0 : 0xFFFFFFFFu;   // the new position, if in this chunk
+        const uint32_t r0 = uint32_t(w) * PW;                        // the wave's rows r0 .. r0 + PW - 1
 
-        // scores: threads 2t and 2t + 1 take the two halves of position t's key
-        // row, every 16-byte load of a half issued at once
-        const uint32_t t = uint32_t(tid) >> 1, hf = uint32_t(tid) & 1;
-        const bool live = t < n;
-        float sc[MAX_GROUP];
+        // every key and value load of the wave's rows; rows past n read row 0
+        // of the chunk (finite: the cache is zeroed at creation) and are masked
+        floatx4 k4[RG][KE];
 #pragma unroll
-        for (int g = 0; g < MAX_GROUP; ++g) sc[g] = 0.0f;
-        if (live) {
-            floatx4 k4[HALF / 4];
-            if (t == jp) {
+        for (int rg = 0; rg < RG; ++rg) {
+            const uint32_t r = r0 + 8 * rg + rl;
+            const uint32_t off = (j0 + (r < n ? r : 0)) * rowBytes + kOff;
 #pragma unroll
-                for (int e = 0; e < HALF / 4; ++e)
-                    k4[e] = hf * HALF + 4 * e < D ? *reinterpret_cast<const floatx4*>(&kn[hf * HALF + 4 * e])
-                                                  : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-            } else {
-                const float* kr = keys + size_t(j0 + t) * kvW + size_t(kvh) * D + hf * HALF;
-#pragma unroll
-                for (int e = 0; e < HALF / 4; ++e)
-                    k4[e] = hf * HALF + 4 * e < D ? *reinterpret_cast<const floatx4*>(kr + 4 * e)
-                                                  : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
-#pragma unroll
-            for (int g = 0; g < MAX_GROUP; ++g) {
-                if (g < int(G)) {
-#pragma unroll
-                    for (int e = 0; e < HALF / 4; ++e) {
-                        if (hf * HALF + 4 * e < D) {
-                            const floatx4 q4 = *reinterpret_cast<const floatx4*>(&qs[g * D + hf * HALF + 4 * e]);
-                            sc[g] = fmaf(q4[0], k4[e][0],
-                                         fmaf(q4[1], k4[e][1], fmaf(q4[2], k4[e][2], fmaf(q4[3], k4[e][3], sc[g]))));
-                        }
-                    }
-                }
-            }
+            for (int e = 0; e < KE; ++e)
+                k4[rg][e] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                            krs, off + kCol[e] * uint32_t(sizeof(float)), 0, 0));
         }
-#pragma unroll
-        for (int g = 0; g < MAX_GROUP; ++g) {
-            if (g < int(G)) {
-                sc[g] += __shfl_xor(sc[g], 1, WAVE);
-                const float m = wave_max(live ? sc[g] * scale : -INFINITY);
-                if (lane == 0) wm[w][g] = m;
-            }
-        }
-        __syncthreads();
-        // the running max and the chunk's probabilities against it
-        float f[MAX_GROUP];
-#pragma unroll
-        for (int g = 0; g < MAX_GROUP; ++g) {
-            f[g] = 1.0f;
-            if (g < int(G)) {
-                const float cm = fmaxf(fmaxf(wm[0][g], wm[1][g]), fmaxf(wm[2][g], wm[3][g]));
-                const float mn = fmaxf(mrun[g], cm);
-                f[g] = expf(mrun[g] - mn);   // 0 on the first chunk
-                mrun[g] = mn;
-                if (hf == 0 && t < uint32_t(SPLIT)) pr[g][t] = live ? expf(sc[g] * scale - mn) : 0.0f;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int g = 0; g < MAX_GROUP; ++g)
-            if (g < int(G)) {
-#pragma unroll
-                for (int e = 0; e < DPL; ++e) acc[g][e] *= f[g];
-                float l = 0.0f;
-                for (uint32_t u = lane; u < n; u += WAVE) l += pr[g][u];
-                lrun[g] = lrun[g] * f[g] + wave_sum(l);
-            }
-        // P.V: wave w takes the 32 positions w + 4u, every row load in flight;
-        // the new position from LDS
-        constexpr int PW = SPLIT / 4;
         float vv[PW][DPL];
 #pragma unroll
         for (int u = 0; u < PW; ++u) {
-            const uint32_t jr = uint32_t(w) + 4 * u;
-            // unused slots read row w: the cache is finite everywhere (zeroed at creation)
-            const float* vr = values + size_t(j0 + (jr < n ? jr : uint32_t(w) < n ? w : 0)) * kvW + size_t(kvh) * D;
+            const uint32_t r = r0 + u;   // uniform: the row goes in the scalar offset
+            const uint32_t rowOff = (j0 + (r < n ? r : 0)) * rowBytes;
+            if constexpr (DPL == 2) {
+                const float2 t = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(vrs, vOff, rowOff, 0));
+                vv[u][0] = t.x;
+                vv[u][1] = t.y;
+            } else {
+                const floatx4 t = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vOff, rowOff, 0));
 #pragma unroll
-            for (int e = 0; e < DPL; ++e) vv[u][e] = lane + 64 * e < int(D) ? vr[lane + 64 * e] : 0.0f;
-        }
-#pragma unroll
-        for (int g = 0; g < MAX_GROUP; ++g) {
-            if (g < int(G)) {
-#pragma unroll
-                for (int u = 0; u < PW; ++u) {
-                    const uint32_t jr = uint32_t(w) + 4 * u;
-                    const float p = (jr < n && jr != jp) ? pr[g][jr] : 0.0f;
-#pragma unroll
-                    for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(p, vv[u][e], acc[g][e]);
-                }
+                for (int e = 0; e < DPL; ++e) vv[u][e] = t[e];
             }
         }
-        if (jp != 0xFFFFFFFFu && int(jp % 4) == w) {
+
+        if (c == cBegin) {   // uniform: the query rows normed and rotated while the loads are in flight
 #pragma unroll
-            for (int g = 0; g < MAX_GROUP; ++g)
-                if (g < int(G)) {
-                    const float p = pr[g][jp];
+            for (int t = 0; t < QPT; ++t) {
+                const uint32_t i = uint32_t(tid) + 256 * t;
+                if (i < G * D) qs[i] = qr[t];
+            }
+            if (holdsPos && uint32_t(tid) < D) {
+                kn[tid] = knr;
+                vn[tid] = vnr;
+            }
+            lds_barrier();
+            for (uint32_t g = w; g < G; g += 4)
+                norm_rope_row(&qs[g * D], int(D), qNorm, a.eps, 0.0f, freqs, int(a.rot), pos, lane);
+            if (holdsPos && w == int(G % 4)) {
+                norm_rope_row(kn, int(D), kNorm, a.eps, 0.0f, freqs, int(a.rot), pos, lane);
+                for (uint32_t d = lane; d < D; d += WAVE) {
+                    keys[size_t(pos) * kvW + size_t(kvh) * D + d] = kn[d];
+                    values[size_t(pos) * kvW + size_t(kvh) * D + d] = vn[d];
+                }
+            }
+            lds_barrier();
+        }
+        if (jp - r0 < uint32_t(PW)) {   // uniform: the new position is one of this wave's rows; from LDS
+            const uint32_t ju = jp - r0;
 #pragma unroll
-                    for (int e = 0; e < DPL; ++e)
-                        if (lane + 64 * e < int(D)) acc[g][e] = fmaf(p, vn[lane + 64 * e], acc[g][e]);
+            for (int rg = 0; rg < RG; ++rg)
+                if (8 * rg + rl == ju) {
+#pragma unroll
+                    for (int e = 0; e < KE; ++e) k4[rg][e] = *reinterpret_cast<const floatx4*>(&kn[kCol[e]]);
+                }
+#pragma unroll
+            for (int u = 0; u < PW; ++u)
+                if (u == int(ju)) {
+#pragma unroll
+                    for (int e = 0; e < DPL; ++e) vv[u][e] = vn[vlive ? DPL * lane + e : e];
                 }
         }
-        __syncthreads();   // pr and wm are rewritten by the next chunk
-    }
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+            for (int e = 0; e < KE; ++e)
+                if (!kLive[e]) k4[rg][e] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // the split's record per query head: the four waves' accumulators summed
-    const size_t rec = size_t(D) + 2;
-    float* pbase = reinterpret_cast<float*>(red);
 #pragma unroll
-    for (int g = 0; g < MAX_GROUP; ++g) {
-        if (g >= int(G)) break;   // uniform
+        for (int g = 0; g < GMAX; ++g) {
+            if (g >= int(G)) break;   // uniform
+            // scores: the 8 lanes of a row sum their pieces
+            float sc[RG];
 #pragma unroll
-        for (int e = 0; e < DPL; ++e)
-            if (lane + 64 * e < int(D)) pbase[w * MAX_DIM + lane + 64 * e] = acc[g][e];
-        __syncthreads();
-        float* out = partial + ((size_t(kvh) * G + g) * a.maxSplits + s) * rec;
-        for (uint32_t d = tid; d < D; d += 256)
-            out[2 + d] = pbase[d] + pbase[MAX_DIM + d] + pbase[2 * MAX_DIM + d] + pbase[3 * MAX_DIM + d];
-        if (tid == 0) {
-            out[0] = mrun[g];
-            out[1] = lrun[g];
+            for (int rg = 0; rg < RG; ++rg) sc[rg] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < KE; ++e) {
+                const floatx4 q4 = *reinterpret_cast<const floatx4*>(&qs[g * D + kCol[e]]);
+#pragma unroll
+                for (int rg = 0; rg < RG; ++rg)
+                    sc[rg] = fmaf(q4[0], k4[rg][e][0],
+                                  fmaf(q4[1], k4[rg][e][1], fmaf(q4[2], k4[rg][e][2], fmaf(q4[3], k4[rg][e][3], sc[rg]))));
+            }
+            float m = -INFINITY;
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+                sc[rg] = r0 + 8 * rg + rl < n ? sum8(sc[rg]) * scale : -INFINITY;
+                m = fmaxf(m, sc[rg]);
+            }
+            m = max_across8(m);
+            // the wave's running max; -inf until the wave has seen a position
+            const float mn = fmaxf(mrun[g], m);
+            const float f = mrun[g] == -INFINITY ? 0.0f : expf(mrun[g] - mn);
+            float l = 0.0f;
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+                sc[rg] = sc[rg] == -INFINITY ? 0.0f : expf(sc[rg] - mn);
+                l += sc[rg];
+            }
+            l = sum_across8(l);
+            mrun[g] = mn;
+            lrun[g] = lrun[g] * f + l;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) acc[g][e] *= f;
+            // P.V: the probabilities through LDS, read back as broadcasts
+            if (sub == 0) {
+#pragma unroll
+                for (int rg = 0; rg < RG; ++rg) pb[w][8 * rg + rl] = sc[rg];
+            }
+            wave_sync();
+#pragma unroll
+            for (int u4 = 0; u4 < PW / 4; ++u4) {
+                const floatx4 p4 = *reinterpret_cast<const floatx4*>(&pb[w][4 * u4]);
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(p4[t], vv[4 * u4 + t][e], acc[g][e]);
+            }
+            wave_sync();   // pb is rewritten by the next query head
         }
-        __syncthreads();
     }
 
+    // the split's record per query head: the four waves combined
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        if (g >= int(G)) break;   // uniform
+        if (lane == 0) {
+            wm[w][g] = mrun[g];
+            wl[w][g] = lrun[g];
+        }
+        if (vlive) {
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) wacc[w][g * D + DPL * lane + e] = acc[g][e];
+        }
+    }
+    __syncthreads();
+    const size_t rec = size_t(D) + REC_PAD;
+    for (uint32_t i = tid; i < G * D; i += 256) {
+        const uint32_t g = i / D, d = i - g * D;
+        // wave 0 always holds position first + s * chunksPer * SPLIT, so M is finite
+        const float M = fmaxf(fmaxf(wm[0][g], wm[1][g]), fmaxf(wm[2][g], wm[3][g]));
+        float v = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) v = fmaf(wacc[ww][i], expf(wm[ww][g] - M), v);
+        float* out = partial + ((size_t(kvh) * G + g) * a.maxSplits + s) * rec;
+        out[REC_PAD + d] = v;
+        if (d == 0) {
+            float L = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < 4; ++ww) L = fmaf(wl[ww][g], expf(wm[ww][g] - M), L);
+            out[0] = M;
+            out[1] = L;
+        }
+    }
 }
 
 
-/* the splits' records of every query head of one kv head, combined (a launch
-   of its own: a workgroup-to-workgroup handoff inside the attention kernel
-   needs a device-scope fence, which on this part writes back the L2) */
+/* the splits' records of one query head combined (a launch of its own: a
+   workgroup-to-workgroup handoff inside the attention kernel needs a
+   device-scope fence, which on this part writes back the L2). Workgroup
+   (query head in the group, kv head); every load issued at once. */
 __global__ __launch_bounds__(256) void dense_merge_kernel(DenseArgs a, const float* partial, float* attn) {
+    constexpr int MAXT = MAX_SPLITS / 4;   // splits per thread when D = 256
     __shared__ floatx4 red[256];
     const uint32_t pos = *a.pos;
     uint32_t first, splits, chunksPer;
     attn_span(pos, a.window, first, splits, chunksPer);
-    const uint32_t kvh = blockIdx.x, G = a.heads / a.kvHeads, D = a.dim;
+    const uint32_t g = blockIdx.x, kvh = blockIdx.y, G = a.heads / a.kvHeads, D = a.dim;
     const int tid = threadIdx.x, lane = tid & 63;
-    const size_t rec = size_t(D) + 2;
-    const uint32_t quads = D / 4, RL = 256 / quads;   // D % 4 == 0, D <= 256
+    const size_t rec = size_t(D) + REC_PAD;
+    const uint32_t quads = D / 4, RL = 256 / quads;   // D % 4 == 0, D <= 256: RL >= 4
     const uint32_t dq = tid % quads, r = tid / quads;
-    for (uint32_t g = 0; g < G; ++g) {
-        const float* base = partial + (size_t(kvh) * G + g) * a.maxSplits * rec;
-        float M = -INFINITY, L = 0.0f;
-        for (uint32_t i = lane; i < splits; i += WAVE) M = fmaxf(M, base[i * rec]);
-        M = wave_max(M);
-        for (uint32_t i = lane; i < splits; i += WAVE) L += base[i * rec + 1] * expf(base[i * rec] - M);
-        L = wave_sum(L);
-        floatx4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (r < RL) {
-#pragma unroll 4
-            for (uint32_t i = r; i < splits; i += RL) {
-                const float fi = expf(base[i * rec] - M);
-                const floatx4 v = *reinterpret_cast<const floatx4*>(base + i * rec + 2 + 4 * dq);
+    const float* base = partial + (size_t(kvh) * G + g) * a.maxSplits * rec;
+    const bool mine = uint32_t(lane) < splits;
+    const float mi = mine ? base[size_t(lane) * rec] : -INFINITY;
+    const float li = mine ? base[size_t(lane) * rec + 1] : 0.0f;
+    floatx4 v[MAXT];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) sum[t] = fmaf(v[t], fi, sum[t]);
-            }
+    for (int t = 0; t < MAXT; ++t) {
+        const uint32_t i = r + RL * t;
+        v[t] = r < RL && i < splits ? *reinterpret_cast<const floatx4*>(base + i * rec + REC_PAD + 4 * dq)
+                                    : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    const float M = wave_max(mi);
+    const float L = wave_sum(li * expf(mi - M));
+    floatx4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < MAXT; ++t) {
+        const uint32_t i = r + RL * t;
+        const float fi = __shfl(mi, int(i < splits ? i : 0), WAVE);
+        if (r < RL && i < splits) {
+            const float e = expf(fi - M);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) sum[k] = fmaf(v[t][k], e, sum[k]);
         }
-        red[tid] = sum;
-        __syncthreads();
-        if (tid < int(quads)) {
-            floatx4 t = red[tid];
-            for (uint32_t rr = 1; rr < RL; ++rr) {
-                const floatx4 u = red[rr * quads + tid];
+    }
+    red[tid] = sum;
+    __syncthreads();
+    if (tid < int(quads)) {
+        floatx4 t = red[tid];
+        for (uint32_t rr = 1; rr < RL; ++rr) {
+            const floatx4 u = red[rr * quads + tid];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) t[k] += u[k];
-            }
-            const float inv = 1.0f / L;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) attn[(size_t(kvh) * G + g) * D + 4 * tid + k] = t[k] * inv;
+            for (int k = 0; k < 4; ++k) t[k] += u[k];
         }
-        __syncthreads();
+        const float inv = 1.0f / L;
+        *reinterpret_cast<floatx4*>(attn + (size_t(kvh) * G + g) * D + 4 * tid) =
+            floatx4{t[0] * inv, t[1] * inv, t[2] * inv, t[3] * inv};
     }
 }
 
@@ -575,22 +664,32 @@ uint32_t host_splits(uint32_t pos, uint32_t window) {
 bool run_step(DenseModel& d, uint32_t splits, hipStream_t stream) {
     Context& ctx = Context::instance();
     const AiGpuDenseConfig& c = d.cfg;
-    DenseArgs a{d.pos, c.heads, c.kvHeads, c.headDim, c.rotaryDims, d.maxSplits, 0, c.epsilon};
+    DenseArgs a{d.pos, c.heads, c.kvHeads, c.headDim, c.rotaryDims, d.maxSplits, 0, c.capacity, c.epsilon};
     for (const DevLayer& L : d.layers) {
         a.window = L.window;
         if (!dense_gemv({{&L.q, d.q}, {&L.k, d.k}, {&L.v, d.v}}, d.x, nullptr, L.inputNorm, c.epsilon, 1, false, stream))
             return false;
         if (!ctx.launch("dense_attn_kernel", stream, [&] {
-                if (c.headDim <= 128)
-                    hipLaunchKernelGGL(dense_attn_kernel<2>, dim3(splits, c.kvHeads), dim3(256), 0, stream, a, d.q, d.k,
-                                       d.v, L.qNorm, L.kNorm, d.freqs, L.keys, L.values, d.partial);
-                else
-                    hipLaunchKernelGGL(dense_attn_kernel<4>, dim3(splits, c.kvHeads), dim3(256), 0, stream, a, d.q, d.k,
-                                       d.v, L.qNorm, L.kNorm, d.freqs, L.keys, L.values, d.partial);
+                const dim3 grid(splits, c.kvHeads);
+                const uint32_t G = c.heads / c.kvHeads;
+#define AIGPU_DA(DPL, GM)                                                                                   \
+    hipLaunchKernelGGL((dense_attn_kernel<DPL, GM>), grid, dim3(256), 0, stream, a, d.q, d.k, d.v, L.qNorm, \
+                       L.kNorm, d.freqs, L.keys, L.values, d.partial)
+                if (c.headDim <= 128) {
+                    if (G <= 2) AIGPU_DA(2, 2);
+                    else if (G <= 4) AIGPU_DA(2, 4);
+                    else AIGPU_DA(2, 8);
+                } else {
+                    if (G <= 2) AIGPU_DA(4, 2);
+                    else if (G <= 4) AIGPU_DA(4, 4);
+                    else AIGPU_DA(4, 8);
+                }
+#undef AIGPU_DA
             }))
             return false;
         if (!ctx.launch("dense_merge_kernel", stream, [&] {
-                hipLaunchKernelGGL(dense_merge_kernel, dim3(c.kvHeads), dim3(256), 0, stream, a, d.partial, d.attn);
+                hipLaunchKernelGGL(dense_merge_kernel, dim3(c.heads / c.kvHeads, c.kvHeads), dim3(256), 0, stream, a,
+                                   d.partial, d.attn);
             }))
             return false;
         if (!dense_gemv({{&L.o, d.x}}, d.attn, nullptr, nullptr, 0.0f, 0, true, stream)) return false;
@@ -627,6 +726,8 @@ AIGPU_ABI void* aigpu_dense_create(const AiGpuDenseConfig* c, const AiGpuDenseLa
             c->rotaryDims > c->headDim || !c->intermediate || !c->capacity || !c->vocab || length > c->capacity ||
             !c->finalNorm)
             throw std::invalid_argument("invalid resident decoder configuration");
+        if (uint64_t(c->capacity) * c->kvHeads * c->headDim * sizeof(float) >= (uint64_t(1) << 32))
+            throw std::invalid_argument("resident decoder cache over 4 GiB per layer (capacity * kvHeads * headDim * 4)");
         auto d = std::make_unique<DenseModel>();
         d->cfg = *c;
         d->length = length;
@@ -652,7 +753,7 @@ AIGPU_ABI void* aigpu_dense_create(const AiGpuDenseConfig* c, const AiGpuDenseLa
         d->up = d->floats(c->intermediate);
         d->logits = d->floats(c->vocab);
         d->maxSplits = aigpu::host_splits(c->capacity - 1, 0);
-        d->partial = d->floats(uint64_t(c->heads) * d->maxSplits * (c->headDim + 2));
+        d->partial = d->floats(uint64_t(c->heads) * d->maxSplits * (c->headDim + aigpu::REC_PAD));
         d->pos = reinterpret_cast<uint32_t*>(d->floats(1));
         for (uint32_t i = 0; i < c->layers; ++i) {
             const AiGpuDenseLayer& l = layers[i];

@@ -60,6 +60,19 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+/* s_waitcnt lgkmcnt(0) (vmcnt and expcnt left alone), then s_barrier. Unlike
+   __syncthreads() it carries no workgroup release fence, which on gfx950 waits
+   for every outstanding vector-memory operation (vmcnt(0)) and so would also
+   wait for loads or DMA issued for later work; those are ordered by the
+   waits the compiler places before their uses. The signal fences keep the
+   compiler from moving LDS accesses across the barrier. */
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 /*
     QK-RMSNorm then rotate-half RoPE of one row held in LDS (`x`, dim floats),
     done by one wave. Restates attentionMixer (LocalModel.hpp:2608-2648):

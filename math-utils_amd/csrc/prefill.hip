@@ -326,19 +326,6 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-/* s_waitcnt lgkmcnt(0) (vmcnt and expcnt left alone), then s_barrier. Unlike
-   __syncthreads() it carries no workgroup release fence, which on gfx950 waits
-   for every outstanding vector-memory operation (vmcnt(0)) and so would also
-   wait for the DMA of tiles prefetched for later iterations; DMA completion is
-   ordered by the explicit vmcnt waits instead. The signal fences keep the
-   compiler from moving LDS accesses across the barrier. */
-__device__ __forceinline__ void lds_barrier() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 /*
     Flash attention, one workgroup = WAVES waves of 32 query rows of one
     head; key tiles of 64 keys staged in LDS by DMA (global_load_lds, 1 KB

@@ -78,9 +78,11 @@ class Model:
             self.gpu.release(ptr, n)
 
 
-def run(gpu, kind, length=5, steps=5, qk_norm=True, biases=False, windows=(0, 0), rot=64, capacity=40, seed=1):
+def run(gpu, kind, length=5, steps=5, qk_norm=True, biases=False, windows=(0, 0), rot=64, capacity=40, seed=1,
+        shape=None):
     cfg = dict(hidden=256, heads=4, kv_heads=2, head_dim=64, intermediate=512, vocab=777, capacity=capacity,
                rotary_dims=rot, eps=1e-6, theta=1e6)
+    cfg.update(shape or {})
     m = Model(gpu, cfg, kind, seed, qk_norm=qk_norm, biases=biases, windows=windows)
     rng = np.random.default_rng(seed + 100)
     kvw = cfg["kv_heads"] * cfg["head_dim"]
@@ -91,7 +93,7 @@ def run(gpu, kind, length=5, steps=5, qk_norm=True, biases=False, windows=(0, 0)
         v[:length] = rng.standard_normal((length, kvw)).astype(np.float32)
     freqs = O.rotary_frequencies(rot, cfg["theta"])
     say("dense decoder", dict(kind=kind, length=length, steps=steps, qk_norm=qk_norm, biases=biases,
-                              windows=windows, rot=rot))
+                              windows=windows, rot=rot, shape=shape))
     dec = gpu.DenseDecoder(cfg, m.dev_layers, m.dev_head, m.final_norm, keys, values, length)
     rcfg = dict(cfg, freqs=freqs)
     try:
@@ -122,8 +124,26 @@ def test_llama_layers_with_biases_window_and_partial_rotary(gpu):
 
 
 def test_long_history_crosses_attention_splits(gpu):
-    """a cache longer than one 256-position split"""
+    """a cache of several 128-position attention workgroups"""
     run(gpu, "bf16", length=600, steps=2, capacity=620)
+
+
+def test_very_long_history_puts_several_chunks_in_a_split(gpu):
+    """past 64 x 128 positions each attention workgroup takes two chunks or more"""
+    run(gpu, "bf16", length=8300, steps=2, capacity=8310, windows=(0, 3000))
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [
+    (4, 4, 64),     # one query head per kv head
+    (6, 2, 96),     # three, and a head dim that leaves key pieces and value lanes idle
+    (8, 2, 128),    # four
+    (8, 1, 128),    # eight
+    (4, 2, 256),    # four dims per value lane
+    (8, 1, 256),    # both at their largest
+])
+def test_group_sizes_and_head_dims(gpu, heads, kv_heads, head_dim):
+    run(gpu, "bf16", length=300, steps=3, capacity=310, rot=head_dim // 2,
+        shape=dict(heads=heads, kv_heads=kv_heads, head_dim=head_dim))
 
 
 def test_empty_cache_and_position_checks(gpu):
