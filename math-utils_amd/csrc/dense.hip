@@ -270,19 +270,16 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
     const bool vlive = uint32_t(DPL * lane) < D;     // value layout: floats DPL lane .. + DPL - 1
     // the layer's cache through buffer descriptors: a lane offset in a VGPR,
     // the row in a scalar offset (byte offsets fit 32 bits: checked at creation)
-    const uint32_t cacheBytes = uint32_t(a.capacity * kvW * sizeof(float));
+    const uint32_t cacheBytes = uint32_t((a.capacity * kvW + MAX_DIM) * sizeof(float));
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(keys, 0, cacheBytes, BUFFER_FLAGS);
     const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(values, 0, cacheBytes, BUFFER_FLAGS);
     const uint32_t rowBytes = uint32_t(kvW * sizeof(float));
-    // pieces past D load the row's last piece (in bounds) and are zeroed
-    uint32_t kCol[KE];
+    // pieces past D read on into the next head or row (the cache carries
+    // MAX_DIM floats of padding, so the last row's stay inside it) and are zeroed
     bool kLive[KE];
 #pragma unroll
-    for (int e = 0; e < KE; ++e) {
-        kLive[e] = 4 * sub + 32 * e < D;
-        kCol[e] = kLive[e] ? 4 * sub + 32 * e : D - 4;
-    }
-    const uint32_t kOff = uint32_t(kvh * D * sizeof(float));
+    for (int e = 0; e < KE; ++e) kLive[e] = 4 * sub + 32 * e < D;
+    const uint32_t kOff = uint32_t((kvh * D + 4 * sub) * sizeof(float));
     const uint32_t vOff = uint32_t((kvh * D + (vlive ? DPL * lane : 0)) * sizeof(float));
 
     // the raw query rows and new key/value rows first, so that their use
@@ -324,8 +321,7 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
             const uint32_t off = (j0 + (r < n ? r : 0)) * rowBytes + kOff;
 #pragma unroll
             for (int e = 0; e < KE; ++e)
-                k4[rg][e] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                            krs, off + kCol[e] * uint32_t(sizeof(float)), 0, 0));
+                k4[rg][e] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(krs, off + 128 * e, 0, 0));
         }
         float vv[PW][DPL];
 #pragma unroll
@@ -371,7 +367,8 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
             for (int rg = 0; rg < RG; ++rg)
                 if (8 * rg + rl == ju) {
 #pragma unroll
-                    for (int e = 0; e < KE; ++e) k4[rg][e] = *reinterpret_cast<const floatx4*>(&kn[kCol[e]]);
+                    for (int e = 0; e < KE; ++e)
+                        if (kLive[e]) k4[rg][e] = *reinterpret_cast<const floatx4*>(&kn[4 * sub + 32 * e]);
                 }
 #pragma unroll
             for (int u = 0; u < PW; ++u)
@@ -395,7 +392,9 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
             for (int rg = 0; rg < RG; ++rg) sc[rg] = 0.0f;
 #pragma unroll
             for (int e = 0; e < KE; ++e) {
-                const floatx4 q4 = *reinterpret_cast<const floatx4*>(&qs[g * D + kCol[e]]);
+                // past D: the next query head's or unwritten LDS (in qs's bounds), zeroed
+                floatx4 q4 = *reinterpret_cast<const floatx4*>(&qs[g * D + 4 * sub + 32 * e]);
+                if (!kLive[e]) q4 = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int rg = 0; rg < RG; ++rg)
                     sc[rg] = fmaf(q4[0], k4[rg][e][0],
@@ -771,8 +770,10 @@ AIGPU_ABI void* aigpu_dense_create(const AiGpuDenseConfig* c, const AiGpuDenseLa
             L.postNorm = d->floats(H, l.postNorm, H);
             if (l.qNorm) L.qNorm = d->floats(c->headDim, l.qNorm, c->headDim);
             if (l.kNorm) L.kNorm = d->floats(c->headDim, l.kNorm, c->headDim);
-            L.keys = d->floats(uint64_t(c->capacity) * kw, keys[i], uint64_t(length) * kw);
-            L.values = d->floats(uint64_t(c->capacity) * kw, values[i], uint64_t(length) * kw);
+            // one head row of padding: the attention's key pieces past headDim
+            // read into it (and are zeroed) when headDim is not 128 or 256
+            L.keys = d->floats(uint64_t(c->capacity) * kw + aigpu::MAX_DIM, keys[i], uint64_t(length) * kw);
+            L.values = d->floats(uint64_t(c->capacity) * kw + aigpu::MAX_DIM, values[i], uint64_t(length) * kw);
             L.window = l.window;
             d->layers.push_back(L);
         }
