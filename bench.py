@@ -50,7 +50,7 @@ def parse():
     # the GPU's clock ramps over the first ~15 ms of sustained work: a short
     # warm-up times the ramp rather than the kernels
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "kda", "dense", "gemm", "mla", "all"])
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "kda", "dense", "gemm", "mla", "mixer", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of each baseline sample")
@@ -491,6 +491,61 @@ def gemm_workload(args, cpu):
     }
 
 
+def mixer_workload(args, cpu):
+    """attentionMixer for a Qwen3-8B prefill of 8192 tokens through
+    aigpu_prefill_mixer (projections with the k / v epilogue, flash attention,
+    o projection), and the same layer through the separate entry points
+    (four matmuls, prefill attention with its own prep) for comparison"""
+    import torch
+    import aigpu
+    S, HID, H, KV, D = 8192, 4096, 32, 8, 128
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    x = torch.randn((S, HID), generator=gen, device="cuda")
+    ws = {}
+    for name, (n, k) in {"q": (H * D, HID), "k": (KV * D, HID), "v": (KV * D, HID), "o": (HID, H * D)}.items():
+        w = (torch.randn((n, k), generator=gen, device="cuda") / k ** 0.5).to(torch.bfloat16)
+        ws[name] = {"w": w, "kind": "bf16", "out": n, "in": k}
+    gq, gk = gammas(D, gen), gammas(D, gen)
+    fr = torch.from_numpy(rotary_table(D, 1e6)).cuda()
+    kc = torch.zeros((KV, S, D), dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    out = torch.empty((S, HID), dtype=torch.float32, device="cuda")
+
+    def fused():
+        aigpu.prefill_mixer(x, ws, out, kc, vc, 0, H, KV, D, q_norm=gq, k_norm=gk, freqs=fr, rotary_dims=D)
+
+    qb = torch.empty((S, H, D), dtype=torch.float32, device="cuda")
+    kb = torch.empty((S, KV, D), dtype=torch.float32, device="cuda")
+    vb = torch.empty_like(kb)
+    att = torch.empty((S, H, D), dtype=torch.float32, device="cuda")
+
+    def separate():
+        aigpu.matmul(x, ws["q"]["w"], qb.view(S, H * D), "bf16")
+        aigpu.matmul(x, ws["k"]["w"], kb.view(S, KV * D), "bf16")
+        aigpu.matmul(x, ws["v"]["w"], vb.view(S, KV * D), "bf16")
+        aigpu.prefill(qb, kb, vb, att, kc, vc, 0, H, KV, D, q_norm=gq, k_norm=gk, freqs=fr, rotary_dims=D)
+        aigpu.matmul(att.view(S, H * D), ws["o"]["w"], out, "bf16")
+
+    sep_ms, _, _ = time_steps(separate, args.steps, args.warmup, "gemm_kernel")
+    step_ms, kv_ms, _ = time_steps(fused, args.steps, args.warmup, "gemm_kv_kernel")
+    proj = 2.0 * S * HID * (2 * H * D + 2 * KV * D)
+    attn = 2.0 * D * H * S * (S + 1)
+    flop = proj + attn
+    kv_flop = 2.0 * S * HID * KV * D
+    return {
+        "workload": "attentionMixer prefill, Qwen3-8B layer (4096 hidden, 32q/8kv x 128), 8192 tokens, "
+                    "fp32 x, bf16 weights, QK-norm + RoPE, bf16 cache",
+        "dtype": "bf16", "value": S / (step_ms * 1e-3), "unit": "tokens/s", "ms_per_step": step_ms,
+        "tflops": flop / (step_ms * 1e-3) / 1e12,
+        "separate_entry_points_ms": sep_ms,
+        "roofline": {"kernel": "gemm_kernel<bf16, kv epilogue> (k and v projections with norm/RoPE/append)",
+                     "bound": "mfma", "achieved": kv_flop / (kv_ms * 1e-3) / 1e12, "peak": PEAK_MFMA_F16,
+                     "unit": "TFLOP/s", "frac": kv_flop / (kv_ms * 1e-3) / 1e12 / PEAK_MFMA_F16, "traffic": None,
+                     "kernel_ms": kv_ms,
+                     "note": "algorithmic flops of one projection; fp32 x is split into two bf16 products"},
+    }
+
+
 def mla_workload(args, cpu):
     """multi-head latent attention decode: one token against 4096 cached
     latents, 128 heads, qk_nope 128, v 128, kv_lora_rank 512 (DeepSeek-V3 /
@@ -670,12 +725,14 @@ def main():
         extra["projection_gemm"] = gemm_workload(args, cpu)
     if args.workload in ("mla", "all"):
         extra["latent_attention"] = mla_workload(args, cpu)
+    if args.workload in ("mixer", "all"):
+        extra["prefill_mixer"] = mixer_workload(args, cpu)
     if args.workload == "all":
         extra["others"] = small_workloads(args)
     if head is None:   # a single non-prefill workload becomes the line
         head = (extra.pop("decode", None) or extra.pop("delta_rule", None) or extra.pop("gdn_neighbours", None)
                 or extra.pop("kda_rule", None) or extra.pop("resident_decoder", None) or extra.pop("projection_gemm", None)
-                or extra.pop("latent_attention"))
+                or extra.pop("latent_attention", None) or extra.pop("prefill_mixer"))
     line = {
         "metric": "attn TFLOP/s (prefill) & KV GB/s (decode) as % roofline, 1 MI355X vs host CPU",
         "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
@@ -686,6 +743,9 @@ def main():
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
     }
+    details = {k: v for k, v in head.items() if k not in line and k != "workload"}
+    if details:
+        line["details"] = details
     line.update(extra)
     print(json.dumps(line))
 

@@ -382,6 +382,35 @@ AIGPU_ABI void aigpu_dense_read_cache(void* context, float* const* keys,
                                       float* const* values, uint32_t length);  /* DeviceABI.h:151 */
 
 /* ------------------------------------------------------------------------ */
+/* 9. attentionMixer for a prefill in one call (LocalModel.hpp:2577-2667):  */
+/*    the q, k, v projections of x (apply, :2604-2606), QK-RMSNorm -> RoPE  */
+/*    -> KV append (:2608-2655) as the k and v projections' epilogue, the   */
+/*    causal attention over the cache (:2657-2659), the output gate         */
+/*    (:2660-2665) and the o projection (:2667) into out. The weights are   */
+/*    AiGpuDenseWeight with every pointer on the device (bias included);    */
+/*    qStride is dim, or 2 dim with outputGate (q_proj's per-head gate      */
+/*    half). dim 64 or 128; codes 16-byte aligned.                          */
+/* ------------------------------------------------------------------------ */
+typedef struct AiGpuPrefillMixer {
+    const float* x;                 /* [count][hidden] fp32, the normed hidden states */
+    AiGpuDenseWeight q, k, v, o;    /* q [heads*qStride][hidden], k and v [kvHeads*dim][hidden],
+                                       o [hidden][heads*dim] */
+    float* out;                     /* [count][hidden] fp32 */
+    void* keyCache;                 /* bf16 [kvHeads][capacity][dim], positions [0, start) valid */
+    void* valueCache;
+    const float* qNorm;             /* [dim] gamma or NULL (LocalModel.hpp:2609-2617) */
+    const float* kNorm;
+    const float* rotaryFrequencies; /* [rotaryDims/2] or NULL = no RoPE */
+    float epsilon, normOffset;
+    uint32_t rotaryDims, outputGate;
+    uint32_t accumulate;            /* 1: out += the mixer's output (the residual add) */
+    uint32_t reserved;
+    uint64_t count, start, hidden, heads, kvHeads, dim, window, capacity;
+    void* stream;
+} AiGpuPrefillMixer;
+AIGPU_ABI int aigpu_prefill_mixer(const AiGpuPrefillMixer* args);
+
+/* ------------------------------------------------------------------------ */
 /* Per-kernel timing. With profiling on, every launch is bracketed by a pair */
 /* of hipEvents on the stream it runs on; aigpu_profile_read synchronises    */
 /* and reports the summed device time and launch count of kernels whose name */

@@ -582,3 +582,48 @@ def latent_attention(q, latent, kv_b, out, start_pos, scale, sel_start=None, sel
                                 nopeDim=nope, vDim=vdim, kvLoraRank=latent.shape[1], stream=_stream(stream))
     _check(lib().aigpu_latent_attention(C.byref(args)))
     return out
+
+
+class AiGpuPrefillMixer(C.Structure):
+    _fields_ = [("x", _vp), ("q", AiGpuDenseWeight), ("k", AiGpuDenseWeight), ("v", AiGpuDenseWeight),
+                ("o", AiGpuDenseWeight), ("out", _vp), ("keyCache", _vp), ("valueCache", _vp), ("qNorm", _vp),
+                ("kNorm", _vp), ("rotaryFrequencies", _vp), ("epsilon", _f32), ("normOffset", _f32),
+                ("rotaryDims", _u32), ("outputGate", _u32), ("accumulate", _u32), ("reserved", _u32),
+                ("count", _u64), ("start", _u64), ("hidden", _u64), ("heads", _u64), ("kvHeads", _u64),
+                ("dim", _u64), ("window", _u64), ("capacity", _u64), ("stream", _vp)]
+
+
+SIGNATURES["aigpu_prefill_mixer"] = (C.c_int, [C.POINTER(AiGpuPrefillMixer)])
+
+
+def prefill_mixer(x, weights, out, key_cache, value_cache, start, heads, kv_heads, dim, q_norm=None,
+                  k_norm=None, eps=1e-6, norm_offset=0.0, freqs=None, rotary_dims=0, window=0, capacity=None,
+                  output_gate=False, accumulate=False, stream=None):
+    """attentionMixer for the x.shape[0] tokens at positions start..: x [count][hidden]
+    fp32; weights maps "q", "k", "v", "o" to dicts with "w" (the stored weight
+    as a GPU tensor: fp32, bf16, int8 codes or packed 4-bit), "kind" (a
+    WEIGHT_TYPES key), "out" (rows) and optional "scales" / "bias" GPU tensors;
+    out [count][hidden] fp32 (+= with accumulate); the head-major bf16 caches
+    gain positions start .. start + count - 1."""
+    for t, n in ((x, "x"), (out, "out"), (key_cache, "key_cache"), (value_cache, "value_cache"),
+                 (q_norm, "q_norm"), (k_norm, "k_norm"), (freqs, "freqs")):
+        _need(t, n)
+    count, hidden = x.shape
+
+    def w(d):
+        for t, n in ((d["w"], "w"), (d.get("scales"), "scales"), (d.get("bias"), "bias")):
+            _need(t, n)
+        return AiGpuDenseWeight(codes=_ptr(d["w"]), scales=_ptr(d.get("scales")), type=WEIGHT_TYPES[d["kind"]],
+                                inDim=d.get("in", hidden), outDim=d["out"], bias=_ptr(d.get("bias")))
+
+    cap = capacity if capacity is not None else key_cache.shape[-2]
+    args = AiGpuPrefillMixer(x=_ptr(x), q=w(weights["q"]), k=w(weights["k"]), v=w(weights["v"]),
+                             o=w(weights["o"]), out=_ptr(out), keyCache=_ptr(key_cache),
+                             valueCache=_ptr(value_cache), qNorm=_ptr(q_norm), kNorm=_ptr(k_norm),
+                             rotaryFrequencies=_ptr(freqs), epsilon=eps, normOffset=norm_offset,
+                             rotaryDims=rotary_dims if freqs is not None else 0,
+                             outputGate=1 if output_gate else 0, accumulate=1 if accumulate else 0,
+                             count=count, start=start, hidden=hidden, heads=heads, kvHeads=kv_heads, dim=dim,
+                             window=window, capacity=cap, stream=_stream(stream))
+    _check(lib().aigpu_prefill_mixer(C.byref(args)))
+    return out

@@ -738,6 +738,55 @@ AIGPU_ABI int aigpu_matmul_device(const AiGpuMatmul* args) {
 
 extern "C" {
 
+AIGPU_ABI int aigpu_prefill_mixer(const AiGpuPrefillMixer* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("prefill mixer: null arguments"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    auto weight = [](const AiGpuDenseWeight& w) {
+        aigpu::MixerWeight m{};
+        m.codes = w.codes;
+        m.scales = static_cast<const float*>(w.scales);
+        m.bias = w.bias;
+        m.type = int(w.type);
+        m.in = w.inDim;
+        m.out = w.outDim;
+        return m;
+    };
+    for (const AiGpuDenseWeight* w : {&args->q, &args->k, &args->v, &args->o})
+        if (w->type > AIGPU_W_Q4 || (w->type >= AIGPU_W_Q8 && !w->scales))
+            return ctx.fail("prefill mixer: unknown weight type or missing scales"), 0;
+    if (args->hidden > 0xFFFFFFFFull || args->heads * args->dim * 2 > 0xFFFFFFFFull)
+        return ctx.fail("prefill mixer: dimensions out of range"), 0;
+    aigpu::MixerParams p{};
+    p.x = args->x;
+    p.q = weight(args->q);
+    p.k = weight(args->k);
+    p.v = weight(args->v);
+    p.o = weight(args->o);
+    p.out = args->out;
+    p.keyCache = static_cast<uint16_t*>(args->keyCache);
+    p.valueCache = static_cast<uint16_t*>(args->valueCache);
+    p.qNorm = args->qNorm;
+    p.kNorm = args->kNorm;
+    p.freqs = args->rotaryFrequencies;
+    p.eps = args->epsilon;
+    p.normOffset = args->normOffset;
+    p.rotaryDims = args->rotaryFrequencies ? int(args->rotaryDims) : 0;
+    p.outputGate = args->outputGate ? 1 : 0;
+    p.accumulate = args->accumulate ? 1 : 0;
+    p.count = args->count;
+    p.start = args->start;
+    p.hidden = args->hidden;
+    p.heads = args->heads;
+    p.kvHeads = args->kvHeads;
+    p.dim = args->dim;
+    p.qStride = args->outputGate ? 2 * args->dim : args->dim;
+    p.window = args->window;
+    p.capacity = args->capacity;
+    return aigpu::launch_prefill_mixer(p, as_stream(args->stream)) ? 1 : 0;
+}
+
 AIGPU_ABI int aigpu_latent_attention(const AiGpuLatentAttention* args) {
     Context& ctx = Context::instance();
     if (!ctx.ok) return 0;

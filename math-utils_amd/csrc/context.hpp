@@ -28,6 +28,8 @@ enum ScratchSlot {
     SLOT_DECODE_QUERIES, // prepared decode queries and new-token scores
     SLOT_DELTA_WORK,     // per-chunk solve products of the delta rule
     SLOT_LATENT,         // folded queries, contexts and split records of latent attention
+    SLOT_MIXER_Q,        // fp32 q projection of a prefill mixer
+    SLOT_MIXER_ATTN,     // fp32 attention output of a prefill mixer
     SLOT_COUNT
 };
 

@@ -33,9 +33,15 @@ struct PrefillParams {
     const float* freqs;
     float eps, normOffset;
     int rotaryDims, inType, outputGate;
+    // 1: k and v are not read; the new rows [start, start + count) are already
+    // in the caches and in the working buffers of prefill_work_buffers (the k
+    // and v projections' epilogue wrote them)
+    int kvReady;
     uint64_t count, start, heads, kvHeads, dim, qStride, window, capacity;
 };
 bool launch_prefill(const PrefillParams& p, hipStream_t stream);
+// the flash kernel's fp16 copies of the cache, [kvHeads][start + count][dim]
+bool prefill_work_buffers(const PrefillParams& p, void** kh, void** vh);
 
 // ---- decode: norm + RoPE on load, append, split-K attention, merge --------
 struct DecodeParams {
@@ -86,6 +92,44 @@ struct GemvParams {
     uint32_t m, k, n, ldo;
 };
 bool launch_gemv(const GemvParams& p, hipStream_t stream);
+
+// the k or v projection of a prefill with attentionMixer's per-token work
+// as its epilogue: QK-RMSNorm (gamma), rotate-half RoPE (freqs), then the
+// row appended to the bf16 cache and to the flash kernel's fp16 copy
+struct KvEpilogue {
+    uint16_t* cache;      // bf16 [kvHeads][capacity][dim]
+    void* work;           // fp16 [kvHeads][T][dim]
+    const float* gamma;   // [dim] or null
+    const float* freqs;   // [rot / 2] or null
+    float eps, offset;
+    uint32_t dim, rot, start, T;
+    uint64_t capacity;
+};
+bool launch_gemm_kv(const GemvParams& p, const KvEpilogue& e, hipStream_t stream);
+
+// ---- attentionMixer for a prefill: projections, norm/RoPE/append, flash
+// attention, output gate, o projection ----
+struct MixerWeight {
+    const void* codes;
+    const float* scales;
+    const float* bias;
+    int type;
+    uint32_t in, out;
+};
+struct MixerParams {
+    const float* x;
+    MixerWeight q, k, v, o;
+    float* out;
+    uint16_t* keyCache;
+    uint16_t* valueCache;
+    const float* qNorm;
+    const float* kNorm;
+    const float* freqs;
+    float eps, normOffset;
+    int rotaryDims, outputGate, accumulate;
+    uint64_t count, start, hidden, heads, kvHeads, dim, qStride, window, capacity;
+};
+bool launch_prefill_mixer(const MixerParams& p, hipStream_t stream);
 
 // ---- multi-head latent attention ----
 struct LatentParams {

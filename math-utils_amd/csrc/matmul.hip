@@ -106,14 +106,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     operand read land on distinct banks.
 */
 constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 32, GM_AS = GM_BK + 8;
+constexpr int GM_OP = GM_BM * GM_AS;   // bf16 elements of one operand buffer
+constexpr int GM_ES = GM_BN + 4;       // row stride (floats) of the epilogue's half tile
 
-template <int TYPE>
-__global__ __launch_bounds__(256) void gemm_kernel(GemvParams p) {
+/* KV: the k / v epilogue of a prefill (launch_gemm_kv) instead of the plain
+   store. It takes the tile through LDS in two halves of 64 rows; four threads
+   per row, each 32 consecutive columns, which lie in one head (dim 64 or 128,
+   tiles start on multiples of 128). */
+template <int TYPE, bool KV>
+__global__ __launch_bounds__(256) void gemm_kernel(GemvParams p, KvEpilogue ep) {
     constexpr bool SPLIT_W = TYPE == 0, QUANT = TYPE >= 2;
-    __shared__ __align__(16) __bf16 Ah[GM_BM * GM_AS];
-    __shared__ __align__(16) __bf16 Al[GM_BM * GM_AS];
-    __shared__ __align__(16) __bf16 Bh[GM_BN * GM_AS];
-    __shared__ __align__(16) __bf16 Bl[SPLIT_W ? GM_BN * GM_AS : 8];
+    constexpr int OPS = (SPLIT_W ? 4 : 3) * GM_OP;   // Ah, Al, Bh (, Bl)
+    constexpr int EPI = KV ? 64 * GM_ES * 2 : 0;      // the half tile in fp32, counted in bf16
+    __shared__ __align__(16) __bf16 smem[OPS > EPI ? OPS : EPI];
+    __bf16* const Ah = smem;
+    __bf16* const Al = smem + GM_OP;
+    __bf16* const Bh = smem + 2 * GM_OP;
+    __bf16* const Bl = smem + 3 * GM_OP;   // SPLIT_W only
     __shared__ float Sc[QUANT ? GM_BN : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
@@ -261,21 +270,103 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvParams p) {
             }
     }
     // the accumulator layout: lane holds rows 4 (lane / 16) + r of column lane % 16
+    if constexpr (!KV) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t n = n0 + 64 * wn + 16 * j + (lane & 15);
-            if (n >= N) continue;
-            const float b = p.bias ? p.bias[n] : 0.0f;
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t n = n0 + 64 * wn + 16 * j + (lane & 15);
+                if (n >= N) continue;
+                const float b = p.bias ? p.bias[n] : 0.0f;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t m = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + r;
-                if (m >= M) continue;
-                float* o = p.out + size_t(m) * p.ldo + n;
-                *o = (p.accumulate ? *o : 0.0f) + acc[i][j][r] + b;
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t m = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + r;
+                    if (m >= M) continue;
+                    float* o = p.out + size_t(m) * p.ldo + n;
+                    *o = (p.accumulate ? *o : 0.0f) + acc[i][j][r] + b;
+                }
+            }
+    } else {
+        float* tile = reinterpret_cast<float*>(smem);
+        const uint32_t D = ep.dim;
+        const int row = tid >> 2, c0 = 32 * (tid & 3);   // half-tile row, first column
+        const uint32_t n = n0 + uint32_t(c0);                // k or v column: head n / D, dim n % D
+        const uint32_t d0 = n % D, head = n / D, hc = uint32_t(c0) - d0;
+        const uint32_t half = ep.freqs ? ep.rot / 2 : 0;
+        for (int hf = 0; hf < 2; ++hf) {
+            __syncthreads();   // the operand reads, or the previous half's tile reads, are done
+            if (wm == hf) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t c = 64 * wn + 16 * j + (lane & 15);
+                        const float b = p.bias && n0 + c < N ? p.bias[n0 + c] : 0.0f;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) tile[(16 * i + 4 * (lane >> 4) + r) * GM_ES + c] = acc[i][j][r] + b;
+                    }
+            }
+            __syncthreads();
+            const float* tr = tile + row * GM_ES;
+            float x[32];
+#pragma unroll
+            for (int e = 0; e < 32; e += 4) {
+                const floatx4 t = *reinterpret_cast<const floatx4*>(tr + c0 + e);
+                x[e] = t[0];
+                x[e + 1] = t[1];
+                x[e + 2] = t[2];
+                x[e + 3] = t[3];
+            }
+            // the head's D / 32 threads are lanes 4 t + (0..3) or (0, 1) / (2, 3): the
+            // butterflies run in every lane, rows past M or columns past N included
+            float inv = 1.0f;
+            if (ep.gamma) {   // rmsNormRow (LocalModel.hpp:1341-1348)
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 32; ++e) ss = fmaf(x[e], x[e], ss);
+                ss += __shfl_xor(ss, 1, WAVE);
+                if (D == 128) ss += __shfl_xor(ss, 2, WAVE);
+                inv = 1.0f / sqrtf(ss / float(D) + ep.eps);
+            }
+            const uint32_t m = m0 + 64 * hf + row;
+            if (m < M && n < N) {
+                const uint32_t pos = ep.start + m;
+                float y[32];
+#pragma unroll
+                for (int e = 0; e < 32; ++e) y[e] = ep.gamma ? x[e] * inv * (ep.gamma[d0 + e] + ep.offset) : x[e];
+                if (half) {   // rotate-half pairs (LocalModel.hpp:2624-2641), the angle float(pos) * freq
+                    const float fpos = float(pos);
+#pragma unroll
+                    for (int e = 0; e < 32; ++e) {
+                        const uint32_t d = d0 + e;
+                        if (d < 2 * half) {
+                            const bool low = d < half;
+                            const uint32_t dp = low ? d + half : d - half;
+                            const float xp = ep.gamma ? tr[hc + dp] * inv * (ep.gamma[dp] + ep.offset) : tr[hc + dp];
+                            float sn, cs;
+                            sincosf(fpos * ep.freqs[low ? d : dp], &sn, &cs);
+                            y[e] = low ? y[e] * cs - xp * sn : y[e] * cs + xp * sn;
+                        }
+                    }
+                }
+                uint16_t* cdst = ep.cache + (size_t(head) * ep.capacity + pos) * D + d0;
+                _Float16* wdst = static_cast<_Float16*>(ep.work) + (size_t(head) * ep.T + pos) * D + d0;
+#pragma unroll
+                for (int e = 0; e < 32; e += 8) {
+                    u32x4 wb;
+                    half8 wh;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        wb[t] = uint32_t(float_to_bf16_bits(y[e + 2 * t])) |
+                                (uint32_t(float_to_bf16_bits(y[e + 2 * t + 1])) << 16);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) wh[t] = _Float16(y[e + t]);
+                    *reinterpret_cast<u32x4*>(cdst + e) = wb;
+                    *reinterpret_cast<half8*>(wdst + e) = wh;
+                }
             }
         }
+    }
 }
 
 /* any k for F32 and BF16 (rows not on 16-byte boundaries): one wave per
@@ -317,7 +408,7 @@ bool launch_type(Context& ctx, const GemvParams& p, hipStream_t stream) {
         const dim3 grid(unsigned((p.n + GM_BN - 1) / GM_BN), unsigned((p.m + GM_BM - 1) / GM_BM));
         if (grid.y > 65535u) return ctx.fail("matmul: too many rows of a");
         return ctx.launch("gemm_kernel", stream, [&] {
-            hipLaunchKernelGGL((gemm_kernel<TYPE>), grid, dim3(256), 0, stream, p);
+            hipLaunchKernelGGL((gemm_kernel<TYPE, false>), grid, dim3(256), 0, stream, p, KvEpilogue{});
         });
     }
     const unsigned gx = unsigned((p.n + 4 * GEMV_ROWS - 1) / (4 * GEMV_ROWS));
@@ -350,6 +441,32 @@ bool launch_gemv(const GemvParams& p, hipStream_t stream) {
         case 3: return launch_type<3>(ctx, p, stream);
         default: return ctx.fail("matmul: unknown weight type");
     }
+}
+
+bool launch_gemm_kv(const GemvParams& p, const KvEpilogue& e, hipStream_t stream) {
+    Context& ctx = Context::instance();
+    if (p.m == 0) return true;
+    if (!p.a || !p.w || !e.cache || !e.work) return ctx.fail("projection epilogue: null tensor");
+    if (e.dim != 64 && e.dim != 128) return ctx.fail("projection epilogue: dim must be 64 or 128");
+    if (p.n == 0 || p.n % e.dim) return ctx.fail("projection epilogue: n must be a multiple of dim");
+    if (e.freqs && (e.rot == 0 || e.rot > e.dim || e.rot % 2)) return ctx.fail("projection epilogue: bad rotaryDims");
+    if (uint64_t(e.start) + p.m > e.T || e.T > e.capacity) return ctx.fail("projection epilogue: rows past the cache");
+    if (p.k == 0) return ctx.fail("matmul: k must be positive");
+    if (p.type >= 2 && (!p.scales || p.k % 32)) return ctx.fail("matmul: quantised weights need scales and k % 32");
+    const int E = p.type == 0 ? 4 : (p.type == 1 ? 8 : (p.type == 2 ? 16 : 32));
+    if (p.k % E || (reinterpret_cast<uintptr_t>(p.w) % 16) || (reinterpret_cast<uintptr_t>(p.a) % 16) ||
+        (reinterpret_cast<uintptr_t>(e.cache) % 16) || (reinterpret_cast<uintptr_t>(e.work) % 16))
+        return ctx.fail("projection epilogue: rows of a, w and the caches must be 16-byte aligned");
+    const dim3 grid(unsigned((p.n + GM_BN - 1) / GM_BN), unsigned((p.m + GM_BM - 1) / GM_BM));
+    if (grid.y > 65535u) return ctx.fail("matmul: too many rows of a");
+    return ctx.launch("gemm_kv_kernel", stream, [&] {
+        switch (p.type) {
+            case 0: hipLaunchKernelGGL((gemm_kernel<0, true>), grid, dim3(256), 0, stream, p, e); break;
+            case 1: hipLaunchKernelGGL((gemm_kernel<1, true>), grid, dim3(256), 0, stream, p, e); break;
+            case 2: hipLaunchKernelGGL((gemm_kernel<2, true>), grid, dim3(256), 0, stream, p, e); break;
+            default: hipLaunchKernelGGL((gemm_kernel<3, true>), grid, dim3(256), 0, stream, p, e); break;
+        }
+    });
 }
 
 } // namespace aigpu

@@ -73,7 +73,8 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(PrefillParams p, _Flo
     const uint32_t shift = __builtin_ctz(uint32_t(p.dim));   // dim is 64 or 128
     const uint32_t nq = uint32_t(H) << shift, nk = uint32_t(KVH) << shift;
     const size_t qrow = t * H * p.qStride, krow = t * nk;
-    for (uint32_t i = tid; i < nq + 2 * nk; i += 256) {
+    const uint32_t nrows = p.kvReady ? nq : nq + 2 * nk;   // kvReady: the k, v rows are already written
+    for (uint32_t i = tid; i < nrows; i += 256) {
         float x;
         if (i < nq) x = load_elem(p.q, qrow + size_t(i >> shift) * p.qStride + (i & (uint32_t(p.dim) - 1)), p.inType);
         else if (i < nq + nk) x = load_elem(p.k, krow + (i - nq), p.inType);
@@ -86,7 +87,7 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(PrefillParams p, _Flo
     }
     __syncthreads();
 
-    for (uint64_t h = w; h < H + 2 * KVH; h += 4) {
+    for (uint64_t h = w; h < (p.kvReady ? H : H + 2 * KVH); h += 4) {
         float* x = tok + h * p.dim;
         const bool isQuery = h < H, isKey = !isQuery && h < H + KVH;
         if (isQuery || isKey) {
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(256) void prefill_prep_vec_kernel(PrefillParams p, 
     __shared__ float cs[D / 2], sn[D / 2];
     const int tid = threadIdx.x, sub = tid % LPR, lane = tid % WAVE;
     const uint32_t t = blockIdx.x, pos = uint32_t(p.start) + t;
-    const uint32_t H = uint32_t(p.heads), KVH = uint32_t(p.kvHeads), rows = H + 2 * KVH;
+    const uint32_t H = uint32_t(p.heads), KVH = uint32_t(p.kvHeads), rows = p.kvReady ? H : H + 2 * KVH;
     const int half = p.freqs ? p.rotaryDims / 2 : 0;
     if (tid < half) {
         const float fpos = float(pos);   // the reference's fp32 angle (LocalModel.hpp:2632)
@@ -807,6 +808,14 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
 
 } // namespace
 
+bool prefill_work_buffers(const PrefillParams& p, void** kh, void** vh) {
+    Context& ctx = Context::instance();
+    const uint64_t T = p.start + p.count;
+    *kh = ctx.grow(SLOT_PREFILL_K, p.kvHeads * T * p.dim * 2);
+    *vh = ctx.grow(SLOT_PREFILL_V, p.kvHeads * T * p.dim * 2);
+    return *kh && *vh;
+}
+
 bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     Context& ctx = Context::instance();
     if (p.dim != 64 && p.dim != 128) return ctx.fail("prefill: dim must be 64 or 128");
@@ -816,7 +825,8 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     if (p.freqs && (p.rotaryDims == 0 || p.rotaryDims > int(p.dim) || (p.rotaryDims & 1)))
         return ctx.fail("prefill: rotaryDims must be even and within dim");
     if (p.inType != 0 && p.inType != 1) return ctx.fail("prefill: unknown input type");
-    if (!p.q || !p.k || !p.v || !p.out || !p.keyCache || !p.valueCache) return ctx.fail("prefill: null tensor");
+    if (!p.q || (!p.kvReady && (!p.k || !p.v)) || !p.out || !p.keyCache || !p.valueCache)
+        return ctx.fail("prefill: null tensor");
     if (p.count == 0) return true;
     const uint64_t T = p.start + p.count;
     if (p.capacity < T) return ctx.fail("prefill: cache capacity below start + count");
@@ -825,9 +835,11 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     if (T * p.dim >= (1ull << 31) || p.heads * p.count >= (1ull << 31) || p.kvHeads > 65535)
         return ctx.fail("prefill: sequence too long");
 
-    _Float16* kh = static_cast<_Float16*>(ctx.grow(SLOT_PREFILL_K, p.kvHeads * T * p.dim * 2));
-    _Float16* vh = static_cast<_Float16*>(ctx.grow(SLOT_PREFILL_V, p.kvHeads * T * p.dim * 2));
-    if (!kh || !vh) return false;
+    void* khv = nullptr;
+    void* vhv = nullptr;
+    if (!prefill_work_buffers(p, &khv, &vhv)) return false;
+    _Float16* kh = static_cast<_Float16*>(khv);
+    _Float16* vh = static_cast<_Float16*>(vhv);
 
     // the register-row kernels need 16-byte aligned rows and rot % 16 == 0
     const size_t inAlign = p.inType == 0 ? 4 : 8;   // elements per 16 bytes
@@ -869,7 +881,10 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     }
 
     const float qScale = LOG2E / sqrtf(float(p.dim));
-    if (!ctx.launch("prefill_prep_kernel", stream, [&] {
+    // with the k, v rows already written and q read raw by the flash kernel,
+    // prep has work only for the cos/sin table
+    const bool prepIdle = p.kvReady && fuseQ && !rope;
+    if (!prepIdle && !ctx.launch("prefill_prep_kernel", stream, [&] {
             const dim3 grid{unsigned(p.count)}, block{256};
             const uint32_t t32 = uint32_t(T);
             if (!vec)
