@@ -50,7 +50,7 @@ def parse():
     # the GPU's clock ramps over the first ~15 ms of sustained work: a short
     # warm-up times the ramp rather than the kernels
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "kda", "dense", "gemm", "mla", "mixer", "all"])
+    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "kda", "dense", "gemm", "mla", "mixer", "indexer", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of each baseline sample")
@@ -546,6 +546,54 @@ def mixer_workload(args, cpu):
     }
 
 
+def indexer_workload(args, cpu):
+    """selectKeys through aigpu_select_keys at DeepSeek-V3.2's indexer shapes
+    in the pooled form (64 heads x 128, topK 2048, pools of 4; hidden 7168,
+    q rank 1536, bf16 weights): a decode step against 32K positions, and a
+    4096-token prefill from empty"""
+    import torch
+    import aigpu
+    HID, QR, NI, DI, P, TOPK = 7168, 1536, 64, 128, 4, 2048
+    CAP = 32768 + 8
+    gen = torch.Generator(device="cuda").manual_seed(10)
+
+    def wt(n, k):
+        return {"w": (torch.randn((n, k), generator=gen, device="cuda") / k ** 0.5).to(torch.bfloat16),
+                "kind": "bf16", "out": n, "in": k}
+
+    ws = {"k": wt(DI, HID), "gate": wt(DI, HID), "q": wt(NI * DI, QR), "w": wt(NI, HID)}
+    kn = torch.ones(DI, device="cuda")
+    ape = torch.randn((P, DI), generator=gen, device="cuda")
+    keys = torch.randn((CAP, DI), generator=gen, device="cuda")
+    gates = torch.randn((CAP, DI), generator=gen, device="cuda")
+    pools = torch.randn((CAP // P + 1, DI), generator=gen, device="cuda")
+    i32 = dict(dtype=torch.int32, device="cuda")
+    stride = TOPK // P * P + P
+
+    def case(count, start):
+        h = torch.randn((count, HID), generator=gen, device="cuda")
+        qr = torch.randn((count, QR), generator=gen, device="cuda")
+        ss, sn, sk = torch.empty(count, **i32), torch.empty(count, **i32), torch.empty(count * stride, **i32)
+        return lambda: aigpu.select_keys(h, qr, ws, kn, None, ape, keys, gates, pools, ss, sn, sk, start, NI, DI,
+                                         TOPK, P)
+
+    dec_ms, score_ms, _ = time_steps(case(1, 32768), args.steps, args.warmup, "index_score_kernel")
+    pre_ms, pre_score_ms, _ = time_steps(case(4096, 0), max(2, args.steps // 10), 2, "index_score_kernel")
+    macs = (32769 // P) * NI * DI
+    pre_macs = sum((t + 1) // P for t in range(4096) if (t + 1) // P > TOPK // P) * NI * DI
+    return {
+        "workload": "selectKeys, DeepSeek-V3.2 indexer shapes pooled by 4 (64 x 128 heads, topK 2048), bf16 weights: "
+                    "decode step at 32K positions",
+        "dtype": "f32", "value": 1e3 / dec_ms, "unit": "steps/s", "ms_per_step": dec_ms,
+        "prefill_4096_ms": pre_ms,
+        "roofline": {"kernel": "index_score_kernel", "bound": "valu",
+                     "achieved": 2 * macs / (score_ms * 1e-3) / 1e12, "peak": 157.3, "unit": "TFLOP/s",
+                     "frac": 2 * macs / (score_ms * 1e-3) / 1e12 / 157.3, "traffic": None, "kernel_ms": score_ms,
+                     "prefill_kernel_ms": pre_score_ms,
+                     "prefill_tflops": 2 * pre_macs / (pre_score_ms * 1e-3) / 1e12},
+    }
+
+
 def mla_workload(args, cpu):
     """multi-head latent attention decode: one token against 4096 cached
     latents, 128 heads, qk_nope 128, v 128, kv_lora_rank 512 (DeepSeek-V3 /
@@ -727,12 +775,15 @@ def main():
         extra["latent_attention"] = mla_workload(args, cpu)
     if args.workload in ("mixer", "all"):
         extra["prefill_mixer"] = mixer_workload(args, cpu)
+    if args.workload in ("indexer", "all"):
+        extra["indexer"] = indexer_workload(args, cpu)
     if args.workload == "all":
         extra["others"] = small_workloads(args)
     if head is None:   # a single non-prefill workload becomes the line
         head = (extra.pop("decode", None) or extra.pop("delta_rule", None) or extra.pop("gdn_neighbours", None)
                 or extra.pop("kda_rule", None) or extra.pop("resident_decoder", None) or extra.pop("projection_gemm", None)
-                or extra.pop("latent_attention", None) or extra.pop("prefill_mixer"))
+                or extra.pop("latent_attention", None) or extra.pop("prefill_mixer", None)
+                or extra.pop("indexer"))
     line = {
         "metric": "attn TFLOP/s (prefill) & KV GB/s (decode) as % roofline, 1 MI355X vs host CPU",
         "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,

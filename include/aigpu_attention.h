@@ -411,6 +411,39 @@ typedef struct AiGpuPrefillMixer {
 AIGPU_ABI int aigpu_prefill_mixer(const AiGpuPrefillMixer* args);
 
 /* ------------------------------------------------------------------------ */
+/* 10. The sparse-attention indexer (selectKeys, LocalModel.hpp:2971-3068),  */
+/*    GLM-5.3's pooled form: the call's index keys layer-normed into the     */
+/*    key cache and folded, pool by pool, into pooled keys; each query token */
+/*    scoring the pools wholly at or before it and keeping the topK / pool   */
+/*    best, plus the unfinished pool with indexTail. The result is the       */
+/*    selection aigpu_latent_attention takes. Among equal scores at the      */
+/*    boundary the lower pool is kept (the reference's nth_element leaves    */
+/*    that order unspecified). Device pointers throughout.                   */
+/* ------------------------------------------------------------------------ */
+typedef struct AiGpuSelectKeys {
+    const float* h;                 /* [count][hidden], latentAttentionMixer's input (the call, :3110) */
+    const float* qResid;            /* [count][qRank], q_a_proj's normed output (:3097-3099) */
+    AiGpuDenseWeight idxK;          /* [dim][hidden] */
+    AiGpuDenseWeight idxGate;       /* [dim][hidden] */
+    AiGpuDenseWeight idxQB;         /* [heads*dim][qRank] */
+    AiGpuDenseWeight idxWeights;    /* [heads][hidden] */
+    const float* kNorm;             /* [dim] layerNorm weight */
+    const float* kNormBias;         /* [dim] or NULL */
+    const float* ape;               /* [pool][dim] */
+    float* indexKeys;               /* [capacity][dim]; positions < startPos valid */
+    float* indexGates;              /* [capacity][dim] */
+    float* poolKeys;                /* [capacity/pool + 1][dim] */
+    uint32_t* selStart;             /* [count] */
+    uint32_t* selCount;             /* [count]; UINT32_MAX: the token sees every key */
+    uint32_t* selKeys;              /* [count][topK/pool*pool + pool], each token's keys sorted */
+    float* scores;                  /* optional [count][(startPos+count)/pool]: sparse tokens' pool scores */
+    uint32_t indexTail, reserved;
+    uint64_t count, startPos, hidden, qRank, heads, dim, topK, pool, capacity;
+    void* stream;
+} AiGpuSelectKeys;
+AIGPU_ABI int aigpu_select_keys(const AiGpuSelectKeys* args);
+
+/* ------------------------------------------------------------------------ */
 /* Per-kernel timing. With profiling on, every launch is bracketed by a pair */
 /* of hipEvents on the stream it runs on; aigpu_profile_read synchronises    */
 /* and reports the summed device time and launch count of kernels whose name */

@@ -627,3 +627,45 @@ def prefill_mixer(x, weights, out, key_cache, value_cache, start, heads, kv_head
                              window=window, capacity=cap, stream=_stream(stream))
     _check(lib().aigpu_prefill_mixer(C.byref(args)))
     return out
+
+
+class AiGpuSelectKeys(C.Structure):
+    _fields_ = [("h", _vp), ("qResid", _vp), ("idxK", AiGpuDenseWeight), ("idxGate", AiGpuDenseWeight),
+                ("idxQB", AiGpuDenseWeight), ("idxWeights", AiGpuDenseWeight), ("kNorm", _vp), ("kNormBias", _vp),
+                ("ape", _vp), ("indexKeys", _vp), ("indexGates", _vp), ("poolKeys", _vp), ("selStart", _vp),
+                ("selCount", _vp), ("selKeys", _vp), ("scores", _vp), ("indexTail", _u32), ("reserved", _u32),
+                ("count", _u64), ("startPos", _u64), ("hidden", _u64), ("qRank", _u64), ("heads", _u64),
+                ("dim", _u64), ("topK", _u64), ("pool", _u64), ("capacity", _u64), ("stream", _vp)]
+
+
+SIGNATURES["aigpu_select_keys"] = (C.c_int, [C.POINTER(AiGpuSelectKeys)])
+
+
+def select_keys(h, q_resid, weights, k_norm, k_norm_bias, ape, index_keys, index_gates, pool_keys, sel_start,
+                sel_count, sel_keys, start_pos, heads, dim, top_k, pool, tail=True, scores=None, stream=None):
+    """selectKeys on the device for the h.shape[0] tokens at start_pos: weights
+    maps "k", "gate", "q", "w" (idxK, idxGate, idxQB, idxWeights) to dicts as
+    prefill_mixer takes; the index key / gate / pool caches are updated in
+    place; sel_start / sel_count / sel_keys (int32 GPU tensors) receive the
+    selection aigpu_latent_attention takes."""
+    for t, n in ((h, "h"), (q_resid, "q_resid"), (k_norm, "k_norm"), (k_norm_bias, "k_norm_bias"), (ape, "ape"),
+                 (index_keys, "index_keys"), (index_gates, "index_gates"), (pool_keys, "pool_keys"),
+                 (sel_start, "sel_start"), (sel_count, "sel_count"), (sel_keys, "sel_keys"), (scores, "scores")):
+        _need(t, n)
+    count, hidden = h.shape
+
+    def w(d, k_in):
+        for t, n in ((d["w"], "w"), (d.get("scales"), "scales"), (d.get("bias"), "bias")):
+            _need(t, n)
+        return AiGpuDenseWeight(codes=_ptr(d["w"]), scales=_ptr(d.get("scales")), type=WEIGHT_TYPES[d["kind"]],
+                                inDim=d.get("in", k_in), outDim=d["out"], bias=_ptr(d.get("bias")))
+
+    args = AiGpuSelectKeys(h=_ptr(h), qResid=_ptr(q_resid), idxK=w(weights["k"], hidden),
+                           idxGate=w(weights["gate"], hidden), idxQB=w(weights["q"], q_resid.shape[1]),
+                           idxWeights=w(weights["w"], hidden), kNorm=_ptr(k_norm), kNormBias=_ptr(k_norm_bias),
+                           ape=_ptr(ape), indexKeys=_ptr(index_keys), indexGates=_ptr(index_gates),
+                           poolKeys=_ptr(pool_keys), selStart=_ptr(sel_start), selCount=_ptr(sel_count),
+                           selKeys=_ptr(sel_keys), scores=_ptr(scores), indexTail=1 if tail else 0, count=count,
+                           startPos=start_pos, hidden=hidden, qRank=q_resid.shape[1], heads=heads, dim=dim,
+                           topK=top_k, pool=pool, capacity=index_keys.shape[0], stream=_stream(stream))
+    _check(lib().aigpu_select_keys(C.byref(args)))

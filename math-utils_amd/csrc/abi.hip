@@ -787,6 +787,54 @@ AIGPU_ABI int aigpu_prefill_mixer(const AiGpuPrefillMixer* args) {
     return aigpu::launch_prefill_mixer(p, as_stream(args->stream)) ? 1 : 0;
 }
 
+AIGPU_ABI int aigpu_select_keys(const AiGpuSelectKeys* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("select keys: null arguments"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    auto weight = [](const AiGpuDenseWeight& w) {
+        aigpu::MixerWeight m{};
+        m.codes = w.codes;
+        m.scales = static_cast<const float*>(w.scales);
+        m.bias = w.bias;
+        m.type = int(w.type);
+        m.in = w.inDim;
+        m.out = w.outDim;
+        return m;
+    };
+    for (const AiGpuDenseWeight* w : {&args->idxK, &args->idxGate, &args->idxQB, &args->idxWeights})
+        if (w->type > AIGPU_W_Q4 || (w->type >= AIGPU_W_Q8 && !w->scales))
+            return ctx.fail("select keys: unknown weight type or missing scales"), 0;
+    aigpu::IndexerParams p{};
+    p.h = args->h;
+    p.qResid = args->qResid;
+    p.wk = weight(args->idxK);
+    p.wgate = weight(args->idxGate);
+    p.wq = weight(args->idxQB);
+    p.ww = weight(args->idxWeights);
+    p.kNorm = args->kNorm;
+    p.kNormBias = args->kNormBias;
+    p.ape = args->ape;
+    p.keys = args->indexKeys;
+    p.gates = args->indexGates;
+    p.pools = args->poolKeys;
+    p.selStart = args->selStart;
+    p.selCount = args->selCount;
+    p.selKeys = args->selKeys;
+    p.scores = args->scores;
+    p.tail = args->indexTail ? 1 : 0;
+    p.count = args->count;
+    p.startPos = args->startPos;
+    p.hidden = args->hidden;
+    p.qRank = args->qRank;
+    p.heads = args->heads;
+    p.dim = args->dim;
+    p.topK = args->topK;
+    p.pool = args->pool;
+    p.capacity = args->capacity;
+    return aigpu::launch_select_keys(p, as_stream(args->stream)) ? 1 : 0;
+}
+
 AIGPU_ABI int aigpu_latent_attention(const AiGpuLatentAttention* args) {
     Context& ctx = Context::instance();
     if (!ctx.ok) return 0;

@@ -30,6 +30,7 @@ enum ScratchSlot {
     SLOT_LATENT,         // folded queries, contexts and split records of latent attention
     SLOT_MIXER_Q,        // fp32 q projection of a prefill mixer
     SLOT_MIXER_ATTN,     // fp32 attention output of a prefill mixer
+    SLOT_INDEXER,        // index keys, queries, head weights and scores of selectKeys
     SLOT_COUNT
 };
 

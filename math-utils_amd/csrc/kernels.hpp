@@ -131,6 +131,26 @@ struct MixerParams {
 };
 bool launch_prefill_mixer(const MixerParams& p, hipStream_t stream);
 
+// ---- the sparse-attention indexer (selectKeys) ----
+struct IndexerParams {
+    const float* h;          // [count][hidden]
+    const float* qResid;     // [count][qRank]
+    MixerWeight wk, wgate, wq, ww;   // idxK, idxGate, idxQB, idxWeights
+    const float* kNorm;      // [dim] layerNorm weight
+    const float* kNormBias;  // [dim] or null
+    const float* ape;        // [pool][dim]
+    float* keys;             // [capacity][dim]
+    float* gates;            // [capacity][dim]
+    float* pools;            // [capacity / pool + 1][dim]
+    uint32_t* selStart;
+    uint32_t* selCount;
+    uint32_t* selKeys;       // [count][topK / pool * pool + pool]
+    float* scores;           // optional [count][(startPos + count) / pool]
+    int tail;
+    uint64_t count, startPos, hidden, qRank, heads, dim, topK, pool, capacity;
+};
+bool launch_select_keys(const IndexerParams& p, hipStream_t stream);
+
 // ---- multi-head latent attention ----
 struct LatentParams {
     const float* q;          // [count][heads][nope]

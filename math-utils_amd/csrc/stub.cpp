@@ -50,6 +50,7 @@ AIGPU_ABI void aigpu_matmul_nt_q4(const float*, const void*, const void*, float*
 AIGPU_ABI int aigpu_matmul_device(const AiGpuMatmul*) { return 0; }
 AIGPU_ABI int aigpu_latent_attention(const AiGpuLatentAttention*) { return 0; }
 AIGPU_ABI int aigpu_prefill_mixer(const AiGpuPrefillMixer*) { return 0; }
+AIGPU_ABI int aigpu_select_keys(const AiGpuSelectKeys*) { return 0; }
 AIGPU_ABI int aigpu_dense_supported(void) { return 0; }
 AIGPU_ABI void* aigpu_dense_create(const AiGpuDenseConfig*, const AiGpuDenseLayer*, const float* const*,
                                    const float* const*, uint32_t) { return nullptr; }

@@ -757,3 +757,95 @@ void or_latent_attention(const float* q, const float* latent, const float* wkv, 
     free(context);
     free(scores);
 }
+
+/* ---- the sparse-attention indexer (selectKeys, LocalModel.hpp:2971-3068) ---- */
+
+/* layerNormRow (LocalModel.hpp:1355-1367): mean, then the mean square of the
+   deviations, both summed in order in fp32 */
+static void or_layer_norm_row(const float* x, const float* w, const float* b, float* out, size_t n, float eps) {
+    float mean = 0.0f;
+    for (size_t i = 0; i < n; ++i) mean += x[i];
+    mean /= (float)n;
+    float var = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        const float d = x[i] - mean;
+        var += d * d;
+    }
+    var /= (float)n;
+    const float inv = 1.0f / sqrtf(var + eps);
+    for (size_t i = 0; i < n; ++i) out[i] = (x[i] - mean) * inv * w[i] + (b ? b[i] : 0.0f);
+}
+
+void or_index_update(const float* k, const float* kNorm, const float* kNormBias, const float* ape, float* keys,
+                     const float* gates, float* pools, size_t count, size_t startPos, size_t Di, size_t P) {
+    float* weight = (float*)malloc(sizeof(float) * (P ? P : 1));
+    for (size_t t = 0; t < count; ++t) {
+        const size_t pos = startPos + t;
+        or_layer_norm_row(k + t * Di, kNorm, kNormBias, keys + pos * Di, Di, 1e-6f);   /* :2988-2990 */
+        if ((pos + 1) % P != 0) continue;                                               /* :2994 */
+        const size_t first = pos + 1 - P;
+        float* pooled = pools + (pos / P) * Di;
+        for (size_t d = 0; d < Di; ++d) {                                               /* :2998-3009 */
+            float best = -1e30f;
+            for (size_t i = 0; i < P; ++i) {
+                weight[i] = gates[(first + i) * Di + d] + ape[i * Di + d];
+                if (weight[i] > best) best = weight[i];
+            }
+            float sum = 0.0f;
+            for (size_t i = 0; i < P; ++i) {
+                weight[i] = expf(weight[i] - best);
+                sum += weight[i];
+            }
+            float acc = 0.0f;
+            for (size_t i = 0; i < P; ++i) acc += weight[i] / sum * keys[(first + i) * Di + d];
+            pooled[d] = acc;
+        }
+    }
+    free(weight);
+}
+
+void or_select_keys(const float* q, const float* w, const float* pools, uint32_t* selStart, uint32_t* selCount,
+                    uint32_t* selKeys, float* scores, size_t count, size_t startPos, size_t nI, size_t Di,
+                    size_t P, size_t topK, int tail) {
+    const size_t budget = topK / P, stride = budget * P + P;
+    const size_t maxPools = (startPos + count) / P;
+    const float headScale = 1.0f / sqrtf((float)nI), dimScale = 1.0f / sqrtf((float)Di);   /* :3024-3025 */
+    float* score = (float*)malloc(sizeof(float) * (maxPools ? maxPools : 1));
+    uint8_t* chosen = (uint8_t*)malloc(maxPools ? maxPools : 1);
+    for (size_t t = 0; t < count; ++t) {
+        const size_t pos = startPos + t, complete = (pos + 1) / P;
+        selStart[t] = (uint32_t)(t * stride);
+        if (complete <= budget && tail) {   /* :3036: sees everything */
+            selCount[t] = 0xFFFFFFFFu;
+            continue;
+        }
+        for (size_t p = 0; p < complete; ++p) {   /* :3038-3047 */
+            float total = 0.0f;
+            for (size_t h = 0; h < nI; ++h) {
+                const float logit = or_dot(&q[(t * nI + h) * Di], pools + p * Di, Di) * dimScale;
+                total += w[t * nI + h] * headScale * (logit > 0.0f ? logit : 0.0f);
+            }
+            score[p] = total;
+            if (scores) scores[t * maxPools + p] = total;
+        }
+        /* the keep best (:3049-3053); among equal scores the lower pool index
+           (nth_element leaves that order unspecified) */
+        const size_t keep = budget < complete ? budget : complete;
+        for (size_t p = 0; p < complete; ++p) {
+            size_t above = 0;
+            for (size_t o = 0; o < complete && above < keep; ++o)
+                if (score[o] > score[p] || (score[o] == score[p] && o < p)) ++above;
+            chosen[p] = above < keep;
+        }
+        size_t n = 0;
+        for (size_t p = 0; p < complete; ++p)   /* :3055-3059, in key order (the sort, :3066) */
+            if (chosen[p])
+                for (size_t j = 0; j < P; ++j) selKeys[t * stride + n++] = (uint32_t)(p * P + j);
+        if (tail)                               /* :3062-3064 */
+            for (size_t j = complete * P; j <= pos; ++j) selKeys[t * stride + n++] = (uint32_t)j;
+        selCount[t] = (uint32_t)n;
+    }
+    free(score);
+    free(chosen);
+}
+

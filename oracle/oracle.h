@@ -233,6 +233,24 @@ void or_latent_attention(const float* q, const float* latent, const float* wkv, 
                          const uint32_t* selCount, const uint32_t* selKeys, float* out, size_t count,
                          size_t startPos, size_t nH, size_t Dn, size_t Dv, size_t C, float scale);
 
+/* selectKeys's cache update (LocalModel.hpp:2982-3011): layerNormRow (eps
+   1e-6, :1355-1367) of each new token's index key k[t] into keys[pos], and
+   every pool a token of the call completes folded from its P members, channel
+   by channel, by the softmax of gates + ape. gates[pos] hold the caller's
+   idxGate projection already. */
+void or_index_update(const float* k, const float* kNorm, const float* kNormBias, const float* ape, float* keys,
+                     const float* gates, float* pools, size_t count, size_t startPos, size_t Di, size_t P);
+
+/* selectKeys's choice (:3013-3067): per token, relu-scored pools summed over
+   the nI heads under w, the topK / P best (equal scores: the lower pool
+   index), expanded to their keys in order, then the unfinished pool when
+   tail. selStart[t] = t * (topK / P * P + P); selCount[t] = UINT32_MAX for a
+   token that sees every key. scores, if not NULL, receives [count][(startPos
+   + count) / P] (entries past a token's complete pools untouched). */
+void or_select_keys(const float* q, const float* w, const float* pools, uint32_t* selStart, uint32_t* selCount,
+                    uint32_t* selKeys, float* scores, size_t count, size_t startPos, size_t nI, size_t Di,
+                    size_t P, size_t topK, int tail);
+
 /* number of threads the static pool would use given a request (<=0: all
    online CPUs in this process's affinity mask) */
 int or_threads(int requested);

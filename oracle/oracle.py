@@ -98,6 +98,9 @@ def lib():
         L.or_matmul_nt.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_void_p, _f32p, _sz, _sz, _sz, C.c_int]
         L.or_latent_attention.argtypes = [_f32p, _f32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p, _f32p,
                                           _sz, _sz, _sz, _sz, _sz, _sz, C.c_float]
+        L.or_index_update.argtypes = [_f32p, _f32p, C.c_void_p, _f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz]
+        L.or_select_keys.argtypes = [_f32p, _f32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                     _sz, _sz, _sz, _sz, _sz, _sz, C.c_int]
         L.or_threads.restype = C.c_int
         L.or_threads.argtypes = [C.c_int]
         _lib = L
@@ -562,3 +565,40 @@ def latent_attention(q, latent, wkv, start_pos, heads, nope_dim, v_dim, scale, s
                               ks.ctypes.data, out.reshape(-1), count, start_pos, heads, nope_dim, v_dim, C,
                               float(scale))
     return out
+
+
+# ------------------------------------------------------------- sparse-attention indexer
+def index_update(k, k_norm, k_norm_bias, ape, keys, gates, pools, start_pos, pool):
+    """selectKeys's cache update restated (LocalModel.hpp:2982-3011): the count
+    = k.shape[0] new index keys layer-normed into keys[start_pos:], and the
+    pools they complete folded into pools; keys and pools are updated in place."""
+    k = np.ascontiguousarray(k, np.float32)
+    count, di = k.shape
+    bias = None if k_norm_bias is None else np.ascontiguousarray(k_norm_bias, np.float32)
+    assert keys.dtype == np.float32 and pools.dtype == np.float32 and keys.flags.c_contiguous
+    lib().or_index_update(k.reshape(-1), np.ascontiguousarray(k_norm, np.float32),
+                          None if bias is None else bias.ctypes.data, np.ascontiguousarray(ape, np.float32),
+                          keys.reshape(-1), np.ascontiguousarray(gates, np.float32).reshape(-1), pools.reshape(-1),
+                          count, start_pos, di, pool)
+
+
+def select_keys(q, w, pools, start_pos, heads, dim, pool, top_k, tail=True):
+    """selectKeys's choice restated (LocalModel.hpp:3013-3067): q [count][heads*dim],
+    w [count][heads]; returns (per-token key lists, None for a token that sees
+    every key; the [count][(start_pos + count) // pool] score table)"""
+    q = np.ascontiguousarray(q, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    count = q.shape[0]
+    budget = top_k // pool
+    stride = budget * pool + pool
+    st = np.zeros(count, np.uint32)
+    ct = np.zeros(count, np.uint32)
+    ks = np.zeros(max(1, count * stride), np.uint32)
+    max_pools = (start_pos + count) // pool
+    sc = np.zeros(max(1, count * max_pools), np.float32)
+    lib().or_select_keys(q.reshape(-1), w.reshape(-1), np.ascontiguousarray(pools, np.float32).reshape(-1),
+                         st.ctypes.data, ct.ctypes.data, ks.ctypes.data, sc.ctypes.data, count, start_pos, heads,
+                         dim, pool, top_k, 1 if tail else 0)
+    sel = [None if ct[t] == 0xFFFFFFFF else ks[st[t]:st[t] + ct[t]].copy() for t in range(count)]
+    return sel, sc[:count * max_pools].reshape(count, max_pools)
+
