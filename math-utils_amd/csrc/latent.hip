@@ -23,7 +23,7 @@ namespace aigpu {
 namespace {
 
 constexpr int HG = 16;          // heads per attention workgroup
-constexpr int KPB = 64;         // keys per block (four lanes per key)
+constexpr int KPB = 64;         // keys per block (eight lanes per pair of keys)
 constexpr int MAX_RANK = 512;   // kvLoraRank
 constexpr int MAX_NOPE = 256;
 constexpr int TT = 8;           // tokens per fold / unfold workgroup
@@ -81,11 +81,11 @@ __global__ __launch_bounds__(256) void latent_fold_kernel(LatentArgs a) {
 }
 
 /* workgroup (token, 16 heads, key split): online softmax over blocks of KPB
-   keys; four lanes per key share its row in the scores, the lanes own
+   keys; eight lanes share a pair of keys' rows in the scores, the lanes own
    columns in the context */
 __global__ __launch_bounds__(256) void latent_attn_kernel(LatentArgs a) {
     __shared__ float F[HG * MAX_RANK];
-    __shared__ float pr[HG][KPB];
+    __shared__ __align__(16) float pr[HG][KPB];
     __shared__ uint32_t keyAt[KPB];
     __shared__ float wred[4][HG];
 
@@ -131,44 +131,59 @@ __global__ __launch_bounds__(256) void latent_attn_kernel(LatentArgs a) {
 #pragma unroll
         for (int e = 0; e < CPT; ++e) acc[hh][e] = 0.0f;
     }
-    const uint32_t kq = uint32_t(tid) >> 2, part = uint32_t(tid) & 3;   // key in block, quarter of its row
+    // scores: thread (kq, part) takes keys kq and kq + 32 of the block, and
+    // in each 256-column chunk the interleaved 16-byte pieces 32 j + 4 part:
+    // the eight parts of a key read 128 contiguous bytes, and each piece of
+    // F read from LDS serves both keys
+    const uint32_t kq = uint32_t(tid) >> 3, part = uint32_t(tid) & 7;
     for (uint64_t b = bBegin; b < bEnd; ++b) {
-        const uint64_t i = b * KPB + kq;
-        const bool live = i < n;
-        const uint32_t key = live ? (dense ? uint32_t(i) : sel[i]) : 0u;
-        if (part == 0) keyAt[kq] = key;
-        float sc[HG];
+        const uint64_t i0 = b * KPB + kq, i1 = i0 + KPB / 2;
+        const bool live0 = i0 < n, live1 = i1 < n;
+        const uint32_t key0 = live0 ? (dense ? uint32_t(i0) : sel[i0]) : 0u;
+        const uint32_t key1 = live1 ? (dense ? uint32_t(i1) : sel[i1]) : 0u;
+        if (part == 0) {
+            keyAt[kq] = key0;
+            keyAt[kq + KPB / 2] = key1;
+        }
+        float s0[HG], s1[HG];
 #pragma unroll
-        for (int hh = 0; hh < HG; ++hh) sc[hh] = 0.0f;
-        if (live) {
-            // the key's four lanes take interleaved 16-byte pieces (lane part
-            // reads columns 16 j + 4 part), so the four read neighbouring banks
-            const float* lr = p.latent + size_t(key) * C + 4 * part;
-            for (uint32_t c0 = 0; c0 < C; c0 += 128) {
-                floatx4 l4[8];
+        for (int hh = 0; hh < HG; ++hh) s0[hh] = s1[hh] = 0.0f;
+        {
+            // rows past n read row `key` 0 (finite) and are masked below
+            const float* r0 = p.latent + size_t(key0) * C + 4 * part;
+            const float* r1 = p.latent + size_t(key1) * C + 4 * part;
+            for (uint32_t c0 = 0; c0 < C; c0 += 256) {
+                floatx4 k0v[8], k1v[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    l4[e] = c0 + 16 * e < C ? *reinterpret_cast<const floatx4*>(lr + c0 + 16 * e)
-                                            : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                for (int e = 0; e < 8; ++e) {
+                    const bool in = c0 + 32 * e < C;
+                    k0v[e] = in ? *reinterpret_cast<const floatx4*>(r0 + c0 + 32 * e) : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                    k1v[e] = in ? *reinterpret_cast<const floatx4*>(r1 + c0 + 32 * e) : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
 #pragma unroll
                 for (int hh = 0; hh < HG; ++hh) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        if (c0 + 16 * e < C) {
-                            const floatx4 f4 = *reinterpret_cast<const floatx4*>(&F[hh * MAX_RANK + c0 + 16 * e + 4 * part]);
-                            sc[hh] = fmaf(f4[0], l4[e][0], fmaf(f4[1], l4[e][1], fmaf(f4[2], l4[e][2], fmaf(f4[3], l4[e][3], sc[hh]))));
+                        if (c0 + 32 * e < C) {
+                            const floatx4 f4 = *reinterpret_cast<const floatx4*>(&F[hh * MAX_RANK + c0 + 32 * e + 4 * part]);
+                            s0[hh] = fmaf(f4[0], k0v[e][0], fmaf(f4[1], k0v[e][1], fmaf(f4[2], k0v[e][2], fmaf(f4[3], k0v[e][3], s0[hh]))));
+                            s1[hh] = fmaf(f4[0], k1v[e][0], fmaf(f4[1], k1v[e][1], fmaf(f4[2], k1v[e][2], fmaf(f4[3], k1v[e][3], s1[hh]))));
                         }
                     }
                 }
             }
         }
-        // the key's four quarters, then the block's max per head
+        // the keys' eight parts, then the block's max per head
 #pragma unroll
         for (int hh = 0; hh < HG; ++hh) {
-            sc[hh] += __shfl_xor(sc[hh], 1, WAVE);
-            sc[hh] += __shfl_xor(sc[hh], 2, WAVE);
-            sc[hh] = live ? sc[hh] * p.scale : -INFINITY;
-            const float bm = wave_max(sc[hh]);
+#pragma unroll
+            for (int o = 1; o < 8; o <<= 1) {
+                s0[hh] += __shfl_xor(s0[hh], o, WAVE);
+                s1[hh] += __shfl_xor(s1[hh], o, WAVE);
+            }
+            s0[hh] = live0 ? s0[hh] * p.scale : -INFINITY;
+            s1[hh] = live1 ? s1[hh] * p.scale : -INFINITY;
+            const float bm = wave_max(fmaxf(s0[hh], s1[hh]));
             if (lane == 0) wred[w][hh] = bm;
         }
         __syncthreads();
@@ -179,7 +194,10 @@ __global__ __launch_bounds__(256) void latent_attn_kernel(LatentArgs a) {
             const float mn = fmaxf(m[hh], bm);
             f[hh] = expf(m[hh] - mn);   // 0 on the first block
             m[hh] = mn;
-            if (part == 0) pr[hh][kq] = live ? expf(sc[hh] - mn) : 0.0f;
+            if (part == 0) {
+                pr[hh][kq] = live0 ? expf(s0[hh] - mn) : 0.0f;
+                pr[hh][kq + KPB / 2] = live1 ? expf(s1[hh] - mn) : 0.0f;
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -199,14 +217,16 @@ __global__ __launch_bounds__(256) void latent_attn_kernel(LatentArgs a) {
 #pragma unroll
                 for (int e = 0; e < CPT; ++e) lv[u][e] = tid + 256 * e < int(C) ? lr[tid + 256 * e] : 0.0f;
             }
+            // keys past nb have probability 0 against a finite row
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                if (k0 + u >= nb) break;
+            for (int v = 0; v < 4; ++v) {
 #pragma unroll
                 for (int hh = 0; hh < HG; ++hh) {
-                    const float pv = pr[hh][k0 + u];
+                    const floatx4 p4 = *reinterpret_cast<const floatx4*>(&pr[hh][k0 + 4 * v]);
 #pragma unroll
-                    for (int e = 0; e < CPT; ++e) acc[hh][e] = fmaf(pv, lv[u][e], acc[hh][e]);
+                    for (int u = 0; u < 4; ++u)
+#pragma unroll
+                        for (int e = 0; e < CPT; ++e) acc[hh][e] = fmaf(p4[u], lv[4 * v + u][e], acc[hh][e]);
                 }
             }
         }
