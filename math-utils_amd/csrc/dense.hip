@@ -725,7 +725,8 @@ AIGPU_ABI void* aigpu_dense_create(const AiGpuDenseConfig* c, const AiGpuDenseLa
             c->rotaryDims > c->headDim || !c->intermediate || !c->capacity || !c->vocab || length > c->capacity ||
             !c->finalNorm)
             throw std::invalid_argument("invalid resident decoder configuration");
-        if (uint64_t(c->capacity) * c->kvHeads * c->headDim * sizeof(float) >= (uint64_t(1) << 32))
+        // 32-bit buffer offsets over the cache and its one head row of padding
+        if ((uint64_t(c->capacity) * c->kvHeads * c->headDim + aigpu::MAX_DIM) * sizeof(float) >= (uint64_t(1) << 32))
             throw std::invalid_argument("resident decoder cache over 4 GiB per layer (capacity * kvHeads * headDim * 4)");
         auto d = std::make_unique<DenseModel>();
         d->cfg = *c;
