@@ -87,7 +87,8 @@ __global__ __launch_bounds__(256) void index_pool_kernel(IndexArgs a, const floa
     pools[size_t(p) * Di + d] = acc;
 }
 
-/* token blockIdx.x, pools blockIdx.y * 32 + lane % 32. The 256 threads are
+/* token blockIdx.x; blocks of 32 pools blockIdx.y, blockIdx.y + gridDim.y,
+   ..., pool 32 block + lane % 32. The 256 threads are
    32 pools x 8 head groups: wave w holds groups 2w (lanes 0-31) and 2w + 1
    (lanes 32-63), each of ceil(nI / 8) heads, so a decode step still fills
    the chip. The token's q rows and head weights sit in LDS (read as
@@ -102,46 +103,50 @@ __global__ __launch_bounds__(256) void index_score_kernel(IndexArgs a, const flo
     __shared__ float ws[IX_MAX_HEADS];
     __shared__ float part[IX_GROUPS][IX_POOLS];
     const uint32_t t = blockIdx.x, pos = a.startPos + t, complete = (pos + 1) / a.P;
-    const uint32_t p0 = blockIdx.y * IX_POOLS;
-    if (sees_everything(a, complete) || p0 >= complete) return;   // uniform, before any barrier
+    if (sees_everything(a, complete) || blockIdx.y * IX_POOLS >= complete) return;   // uniform, before any barrier
     const uint32_t nI = a.nI, Di = a.Di, tid = threadIdx.x;
     for (uint32_t i = tid; i < nI * Di / 4; i += 256)
         reinterpret_cast<floatx4*>(qs)[i] = reinterpret_cast<const floatx4*>(q + size_t(t) * nI * Di)[i];
     if (tid < nI) ws[tid] = w[size_t(t) * nI + tid];
     __syncthreads();
-    const uint32_t pl = tid % IX_POOLS, g = tid / IX_POOLS, p = p0 + pl;
+    const uint32_t pl = tid % IX_POOLS, g = tid / IX_POOLS;
     const uint32_t hpg = (nI + IX_GROUPS - 1) / IX_GROUPS, h0 = g * hpg;
-    float total = 0.0f;
-    if (p < complete) {
-        float acc[IX_HPT];
+    // pool blocks blockIdx.y, + gridDim.y, ...: one load of q serves them all
+    for (uint32_t p0 = blockIdx.y * IX_POOLS; p0 < complete; p0 += gridDim.y * IX_POOLS) {   // uniform
+        const uint32_t p = p0 + pl;
+        float total = 0.0f;
+        if (p < complete) {
+            float acc[IX_HPT];
 #pragma unroll
-        for (int h = 0; h < IX_HPT; ++h) acc[h] = 0.0f;
-        const floatx4* pr = reinterpret_cast<const floatx4*>(pools + size_t(p) * Di);
-        for (uint32_t d4 = 0; d4 < Di / 4; ++d4) {
-            const floatx4 pv = pr[d4];
+            for (int h = 0; h < IX_HPT; ++h) acc[h] = 0.0f;
+            const floatx4* pr = reinterpret_cast<const floatx4*>(pools + size_t(p) * Di);
+            for (uint32_t d4 = 0; d4 < Di / 4; ++d4) {
+                const floatx4 pv = pr[d4];
+#pragma unroll
+                for (int h = 0; h < IX_HPT; ++h) {
+                    if (h < int(hpg) && h0 + h < nI) {
+                        const floatx4 qv = reinterpret_cast<const floatx4*>(qs + (h0 + h) * Di)[d4];
+                        acc[h] = fmaf(qv[0], pv[0], fmaf(qv[1], pv[1], fmaf(qv[2], pv[2], fmaf(qv[3], pv[3], acc[h]))));
+                    }
+                }
+            }
 #pragma unroll
             for (int h = 0; h < IX_HPT; ++h) {
                 if (h < int(hpg) && h0 + h < nI) {
-                    const floatx4 qv = reinterpret_cast<const floatx4*>(qs + (h0 + h) * Di)[d4];
-                    acc[h] = fmaf(qv[0], pv[0], fmaf(qv[1], pv[1], fmaf(qv[2], pv[2], fmaf(qv[3], pv[3], acc[h]))));
+                    const float logit = acc[h] * a.dimScale;
+                    total += ws[h0 + h] * a.headScale * (logit > 0.0f ? logit : 0.0f);
                 }
             }
         }
+        part[g][pl] = total;
+        __syncthreads();
+        if (tid < IX_POOLS && p < complete) {
+            float s = 0.0f;
 #pragma unroll
-        for (int h = 0; h < IX_HPT; ++h) {
-            if (h < int(hpg) && h0 + h < nI) {
-                const float logit = acc[h] * a.dimScale;
-                total += ws[h0 + h] * a.headScale * (logit > 0.0f ? logit : 0.0f);
-            }
+            for (int i = 0; i < IX_GROUPS; ++i) s += part[i][tid];
+            scores[size_t(t) * a.maxPools + p] = s;
         }
-    }
-    part[g][pl] = total;
-    __syncthreads();
-    if (tid < IX_POOLS && p < complete) {
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < IX_GROUPS; ++i) s += part[i][tid];
-        scores[size_t(t) * a.maxPools + p] = s;
+        __syncthreads();   // part is rewritten by the next block
     }
 }
 
@@ -370,8 +375,12 @@ bool launch_select_keys(const IndexerParams& p, hipStream_t stream) {
         if (!launch_gemv(projection(p.ww, p.h, w, m, uint32_t(nI)), stream)) return false;
         if (maxPools > 0 &&
             !ctx.launch("index_score_kernel", stream, [&] {
-                hipLaunchKernelGGL(index_score_kernel, dim3(m, unsigned((maxPools + IX_POOLS - 1) / IX_POOLS)), dim3(256),
-                                   0, stream, a, q, w, p.pools, scores);
+                // about 2048 workgroups: a decode step splits its pools 256 ways,
+                // a long prefill gives each token one workgroup and one load of q
+                const uint64_t blocks = (maxPools + IX_POOLS - 1) / IX_POOLS;
+                const uint64_t want = m >= 2048 ? 1 : (2048 + m - 1) / m;
+                const unsigned gy = unsigned(blocks < want ? blocks : want);
+                hipLaunchKernelGGL(index_score_kernel, dim3(m, gy), dim3(256), 0, stream, a, q, w, p.pools, scores);
             }))
             return false;
     }
