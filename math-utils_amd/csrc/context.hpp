@@ -31,6 +31,7 @@ enum ScratchSlot {
     SLOT_MIXER_Q,        // fp32 q projection of a prefill mixer
     SLOT_MIXER_ATTN,     // fp32 attention output of a prefill mixer
     SLOT_INDEXER,        // index keys, queries, head weights and scores of selectKeys
+    SLOT_GEMM_SPLIT,     // the K slices' partial tiles of a split GEMM
     SLOT_COUNT
 };
 

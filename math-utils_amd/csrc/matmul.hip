@@ -114,7 +114,7 @@ constexpr int GM_ES = GM_BN + 4;       // row stride (floats) of the epilogue's 
    per row, each 32 consecutive columns, which lie in one head (dim 64 or 128,
    tiles start on multiples of 128). */
 template <int TYPE, bool KV>
-__global__ __launch_bounds__(256) void gemm_kernel(GemvParams p, KvEpilogue ep) {
+__global__ __launch_bounds__(256) void gemm_kernel(GemvParams p, KvEpilogue ep, uint32_t kSlice) {
     constexpr bool SPLIT_W = TYPE == 0, QUANT = TYPE >= 2;
     constexpr int OPS = (SPLIT_W ? 4 : 3) * GM_OP;   // Ah, Al, Bh (, Bl)
     constexpr int EPI = KV ? 64 * GM_ES * 2 : 0;      // the half tile in fp32, counted in bf16
@@ -237,12 +237,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvParams p, KvEpilogue ep) 
             if (tid < 128) Sc[tid] = rs;
     };
 
-    load(0);
-    for (uint32_t k0 = 0; k0 < K; k0 += GM_BK) {
+    // split K: slice blockIdx.z of kSlice (a multiple of GM_BK) columns
+    const uint32_t kBegin = blockIdx.z * kSlice, kEnd = kBegin + kSlice < K ? kBegin + kSlice : K;
+    load(kBegin);
+    for (uint32_t k0 = kBegin; k0 < kEnd; k0 += GM_BK) {
         __syncthreads();   // the previous step's operand reads are done
         store();
         __syncthreads();
-        if (k0 + GM_BK < K) load(k0 + GM_BK);
+        if (k0 + GM_BK < kEnd) load(k0 + GM_BK);
         bf16x8 ah[4], al[4], bh[4], bl[4];
         const int fr = lane & 15, fk = 8 * (lane >> 4);
 #pragma unroll
@@ -282,7 +284,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvParams p, KvEpilogue ep) 
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t m = m0 + 64 * wm + 16 * i + 4 * (lane >> 4) + r;
                     if (m >= M) continue;
-                    float* o = p.out + size_t(m) * p.ldo + n;
+                    // a K slice writes its own partial tile (no bias, no accumulate)
+                    float* o = p.out + size_t(blockIdx.z) * M * p.ldo + size_t(m) * p.ldo + n;
                     *o = (p.accumulate ? *o : 0.0f) + acc[i][j][r] + b;
                 }
             }
@@ -369,6 +372,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvParams p, KvEpilogue ep) 
     }
 }
 
+/* the K slices' partial tiles added in slice order, then the bias and the
+   accumulate: out[m][n] (+)= sum_s part[s][m][n] + bias[n] */
+__global__ __launch_bounds__(256) void split_reduce_kernel(GemvParams p, const float* part, uint32_t slices) {
+    const uint64_t outs = uint64_t(p.m) * p.n;
+    for (uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x; i < outs; i += uint64_t(gridDim.x) * 256) {
+        float v = 0.0f;
+        for (uint32_t sl = 0; sl < slices; ++sl) v += part[uint64_t(sl) * outs + i];
+        const uint32_t m = uint32_t(i / p.n), n = uint32_t(i % p.n);
+        float* o = p.out + size_t(m) * p.ldo + n;
+        *o = (p.accumulate ? *o : 0.0f) + v + (p.bias ? p.bias[n] : 0.0f);
+    }
+}
+
 /* any k for F32 and BF16 (rows not on 16-byte boundaries): one wave per
    weight row and a row of a, element by element */
 template <int TYPE>
@@ -405,10 +421,39 @@ bool launch_type(Context& ctx, const GemvParams& p, hipStream_t stream) {
         return ctx.fail("matmul: quantised weights need k a multiple of 32 and 16-byte aligned rows");
     }
     if (p.m >= GEMM_MIN_M) {
-        const dim3 grid(unsigned((p.n + GM_BN - 1) / GM_BN), unsigned((p.m + GM_BM - 1) / GM_BM));
+        const uint32_t tiles = ((p.n + GM_BN - 1) / GM_BN) * ((p.m + GM_BM - 1) / GM_BM);
+        // fewer tiles than CUs and a long K: split K into slices of at least
+        // 256 (multiples of a 32-wide step, so Q8/Q4 scale blocks stay whole),
+        // each writing a partial tile; split_reduce_kernel adds them in order
+        uint32_t slices = 1;
+        if (tiles < 256 && p.k >= 512) {
+            slices = (512 + tiles - 1) / tiles;
+            if (slices > p.k / 256) slices = p.k / 256;
+            if (slices > 64) slices = 64;
+        }
+        const uint32_t kSlice = ((p.k + slices - 1) / slices + GM_BK - 1) / GM_BK * GM_BK;
+        slices = (p.k + kSlice - 1) / kSlice;
+        const dim3 grid(unsigned((p.n + GM_BN - 1) / GM_BN), unsigned((p.m + GM_BM - 1) / GM_BM), slices);
         if (grid.y > 65535u) return ctx.fail("matmul: too many rows of a");
-        return ctx.launch("gemm_kernel", stream, [&] {
-            hipLaunchKernelGGL((gemm_kernel<TYPE, false>), grid, dim3(256), 0, stream, p, KvEpilogue{});
+        if (slices == 1)
+            return ctx.launch("gemm_kernel", stream, [&] {
+                hipLaunchKernelGGL((gemm_kernel<TYPE, false>), grid, dim3(256), 0, stream, p, KvEpilogue{}, kSlice);
+            });
+        float* part = static_cast<float*>(ctx.grow(SLOT_GEMM_SPLIT, size_t(slices) * p.m * p.n * sizeof(float)));
+        if (!part) return false;
+        GemvParams q = p;
+        q.out = part;
+        q.ldo = p.n;
+        q.bias = nullptr;
+        q.accumulate = 0;
+        if (!ctx.launch("gemm_kernel", stream, [&] {
+                hipLaunchKernelGGL((gemm_kernel<TYPE, false>), grid, dim3(256), 0, stream, q, KvEpilogue{}, kSlice);
+            }))
+            return false;
+        const uint64_t outs = uint64_t(p.m) * p.n;
+        const unsigned rg = unsigned((outs + 255) / 256 < 65536 ? (outs + 255) / 256 : 65536);
+        return ctx.launch("split_reduce_kernel", stream, [&] {
+            hipLaunchKernelGGL(split_reduce_kernel, dim3(rg), dim3(256), 0, stream, p, part, slices);
         });
     }
     const unsigned gx = unsigned((p.n + 4 * GEMV_ROWS - 1) / (4 * GEMV_ROWS));
@@ -461,10 +506,10 @@ bool launch_gemm_kv(const GemvParams& p, const KvEpilogue& e, hipStream_t stream
     if (grid.y > 65535u) return ctx.fail("matmul: too many rows of a");
     return ctx.launch("gemm_kv_kernel", stream, [&] {
         switch (p.type) {
-            case 0: hipLaunchKernelGGL((gemm_kernel<0, true>), grid, dim3(256), 0, stream, p, e); break;
-            case 1: hipLaunchKernelGGL((gemm_kernel<1, true>), grid, dim3(256), 0, stream, p, e); break;
-            case 2: hipLaunchKernelGGL((gemm_kernel<2, true>), grid, dim3(256), 0, stream, p, e); break;
-            default: hipLaunchKernelGGL((gemm_kernel<3, true>), grid, dim3(256), 0, stream, p, e); break;
+            case 0: hipLaunchKernelGGL((gemm_kernel<0, true>), grid, dim3(256), 0, stream, p, e, p.k + GM_BK); break;
+            case 1: hipLaunchKernelGGL((gemm_kernel<1, true>), grid, dim3(256), 0, stream, p, e, p.k + GM_BK); break;
+            case 2: hipLaunchKernelGGL((gemm_kernel<2, true>), grid, dim3(256), 0, stream, p, e, p.k + GM_BK); break;
+            default: hipLaunchKernelGGL((gemm_kernel<3, true>), grid, dim3(256), 0, stream, p, e, p.k + GM_BK); break;
         }
     });
 }

@@ -68,6 +68,25 @@ def test_device_form(gpu, kind, m):
     assert np.all(err <= bound(a, dense)), f"{kind} m={m}: max err {err.max()}"
 
 
+@pytest.mark.parametrize("kind", ["bf16", "q8", "q4"])
+def test_split_k_for_few_tiles_and_long_k(gpu, kind):
+    """3 x 1 tiles against k = 7168: K is split into slices whose partial
+    tiles are added in order, then the bias and the residual"""
+    import torch
+    m, k, n = 300, 7168, 128
+    a = O.fill_normal((m, k), 31, "a")
+    w, scales, dense = weights(n, k, kind, 32)
+    bias = O.fill_normal((n,), 33, "bias")
+    base = O.fill_normal((m, n), 34, "residual")
+    out = dev_f32(base)
+    say("matmul split-k", dict(kind=kind, m=m, k=k, n=n))
+    gpu.matmul(dev_f32(a), to_device(w), out, kind, scales=None if scales is None else dev_f32(scales),
+               bias=dev_f32(bias), accumulate=True)
+    want = O.matmul_nt(a, w, kind, scales=scales, bias=bias) + base
+    err = np.abs(host(out) - want)
+    assert np.all(err <= bound(a, dense) + 1e-6 * np.abs(base)), f"{kind}: max err {err.max()}"
+
+
 @pytest.mark.parametrize("kind", ["f32", "bf16", "q8", "q4"])
 def test_host_form_and_upload(gpu, kind):
     """the reference's own entry points: host a and c, the weight from aigpu_upload"""
