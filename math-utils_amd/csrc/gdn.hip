@@ -276,8 +276,15 @@ __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(GdnGatedNormParams 
     const uint32_t VD = uint32_t(p.valueDim);
     const uint64_t r = live ? row : 0;
     const float* x = p.x + r * VD;
-    float ss = 0.0f;
-    for (uint32_t d = 4 * sub; d < VD; d += 4 * LPR) {
+    // the first piece's x, gamma and z are requested together, before the
+    // reduction waits (at VD = 4 LPR that is the whole row)
+    const uint32_t d0 = 4 * sub;
+    const floatx4 v0 = *reinterpret_cast<const floatx4*>(x + d0);
+    const floatx4 g0 = *reinterpret_cast<const floatx4*>(p.gamma + d0);
+    float z0[4];
+    loadN<Z_BF16, 4>(p.z, r * VD + d0, z0);
+    float ss = v0[0] * v0[0] + v0[1] * v0[1] + v0[2] * v0[2] + v0[3] * v0[3];
+    for (uint32_t d = d0 + 4 * LPR; d < VD; d += 4 * LPR) {
         const floatx4 v = *reinterpret_cast<const floatx4*>(x + d);
         ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
     }
@@ -285,7 +292,16 @@ __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(GdnGatedNormParams 
     for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o, WAVE);
     const float inv = 1.0f / sqrtf(ss / float(VD) + p.eps);
     if (!live) return;
-    for (uint32_t d = 4 * sub; d < VD; d += 4 * LPR) {
+    {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float s = fast_sigmoid(z0[e]);
+            o[e] = v0[e] * inv * g0[e] * (p.sigmoidGate ? s : z0[e] * s);
+        }
+        storeN<OUT_BF16, 4>(p.out, r * VD + d0, o);
+    }
+    for (uint32_t d = d0 + 4 * LPR; d < VD; d += 4 * LPR) {
         const floatx4 v = *reinterpret_cast<const floatx4*>(x + d);
         const floatx4 gm = *reinterpret_cast<const floatx4*>(p.gamma + d);
         float z[4], o[4];
