@@ -261,9 +261,10 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) 
                 const int cb = (lane % LPR) ^ v_swizzle(r, D);          // 16-byte column block
                 uint32_t row = p0 + r;
                 if (row > lastRow) row = lastRow;
+                // cache policy 2: nontemporal (each V byte is read once)
                 __builtin_amdgcn_global_load_lds(vc + size_t(row) * D + 8 * cb,
                                                  (__attribute__((address_space(3))) void*)(vs + jj * RPL * D),
-                                                 16, 0, 0);
+                                                 16, 0, 2);
             }
         };
 
