@@ -101,14 +101,15 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseGemvArgs p) {
     const uint32_t pieces = p.k / E, blocks = p.k / 32;
     const uint32_t rr1 = r0 + 1 < S.n ? r0 + 1 : r0;   // a row count that is odd repeats the last row
 
-    // the first batch of weight pieces, before anything waits
+    // the first batch of weight pieces, before anything waits (nontemporal:
+    // each weight byte is read once per token)
     u32x4 wv[DG_BATCH][DG_ROWS];
 #pragma unroll
     for (int b = 0; b < DG_BATCH; ++b) {
         const uint32_t c = lane + WAVE * b;
         if (active && c < pieces) {
-            wv[b][0] = *reinterpret_cast<const u32x4*>(S.w + r0 * rowBytes + size_t(c) * 16);
-            wv[b][1] = *reinterpret_cast<const u32x4*>(S.w + rr1 * rowBytes + size_t(c) * 16);
+            wv[b][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(S.w + r0 * rowBytes + size_t(c) * 16));
+            wv[b][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(S.w + rr1 * rowBytes + size_t(c) * 16));
         }
     }
 
@@ -153,8 +154,8 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseGemvArgs p) {
             for (int b = 0; b < DG_BATCH; ++b) {
                 const uint32_t c = c0 + lane + WAVE * b;
                 if (c < pieces) {
-                    wv[b][0] = *reinterpret_cast<const u32x4*>(S.w + r0 * rowBytes + size_t(c) * 16);
-                    wv[b][1] = *reinterpret_cast<const u32x4*>(S.w + rr1 * rowBytes + size_t(c) * 16);
+                    wv[b][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(S.w + r0 * rowBytes + size_t(c) * 16));
+                    wv[b][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(S.w + rr1 * rowBytes + size_t(c) * 16));
                 }
             }
         }
@@ -269,7 +270,8 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
     const uint32_t sub = lane & 7, rl = lane >> 3;   // key layout: row rl of a group, floats 4 sub + 32 e
     const bool vlive = uint32_t(DPL * lane) < D;     // value layout: floats DPL lane .. + DPL - 1
     // the layer's cache through buffer descriptors: a lane offset in a VGPR,
-    // the row in a scalar offset (byte offsets fit 32 bits: checked at creation)
+    // the row in a scalar offset (byte offsets fit 32 bits: checked at
+    // creation); cache policy 2, nontemporal: each row is read once per step
     const uint32_t cacheBytes = uint32_t((a.capacity * kvW + MAX_DIM) * sizeof(float));
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(keys, 0, cacheBytes, BUFFER_FLAGS);
     const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(values, 0, cacheBytes, BUFFER_FLAGS);
@@ -321,7 +323,7 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
             const uint32_t off = (j0 + (r < n ? r : 0)) * rowBytes + kOff;
 #pragma unroll
             for (int e = 0; e < KE; ++e)
-                k4[rg][e] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(krs, off + 128 * e, 0, 0));
+                k4[rg][e] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(krs, off + 128 * e, 0, 2));
         }
         float vv[PW][DPL];
 #pragma unroll
@@ -329,11 +331,11 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
             const uint32_t r = r0 + u;   // uniform: the row goes in the scalar offset
             const uint32_t rowOff = (j0 + (r < n ? r : 0)) * rowBytes;
             if constexpr (DPL == 2) {
-                const float2 t = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(vrs, vOff, rowOff, 0));
+                const float2 t = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(vrs, vOff, rowOff, 2));
                 vv[u][0] = t.x;
                 vv[u][1] = t.y;
             } else {
-                const floatx4 t = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vOff, rowOff, 0));
+                const floatx4 t = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vOff, rowOff, 2));
 #pragma unroll
                 for (int e = 0; e < DPL; ++e) vv[u][e] = t[e];
             }
