@@ -40,6 +40,25 @@
 #include <stddef.h>
 #include <stdint.h>
 
+/*
+    Shared with the reference's boundary. include/ai/gpu/DeviceABI.h
+    (guard AI_GPU_DEVICE_ABI_H) defines AiGpuCounters, the AiGpuDense*
+    structs and the device-management, projection and resident-decoder entry
+    points that this backend implements too. Where that header is reachable
+    (on the include path as ai/gpu/DeviceABI.h, or beside this file) it is
+    included here and those definitions are taken from it, so both headers
+    can share a translation unit in either order. Elsewhere this file
+    declares the same types, with the same layouts, and the same entry
+    points itself.
+*/
+#if !defined(AI_GPU_DEVICE_ABI_H) && defined(__has_include)
+#if __has_include("ai/gpu/DeviceABI.h")
+#include "ai/gpu/DeviceABI.h"
+#elif __has_include("DeviceABI.h")
+#include "DeviceABI.h"
+#endif
+#endif
+
 #if defined(_WIN32)
 #define AIGPU_ABI __declspec(dllexport)
 #else
@@ -53,6 +72,7 @@ extern "C" {
 /* element types of tensors crossing the boundary */
 enum { AIGPU_F32 = 0, AIGPU_BF16 = 1 };
 
+#ifndef AI_GPU_DEVICE_ABI_H
 /* DeviceABI.h:66-72 */
 typedef struct AiGpuCounters {
     uint64_t launches;
@@ -75,6 +95,7 @@ AIGPU_ABI int aigpu_download(void* host, const void* device, uint64_t bytes); /*
 AIGPU_ABI void aigpu_synchronize(void);                            /* DeviceABI.h:115 */
 AIGPU_ABI void aigpu_counters(AiGpuCounters* out);                 /* DeviceABI.h:117 */
 AIGPU_ABI void aigpu_reset_counters(void);                         /* DeviceABI.h:118 */
+#endif /* !AI_GPU_DEVICE_ABI_H */
 
 /* New beside aigpu_upload: a zero-filled device allocation (KV caches,
    recurrent states) released by aigpu_release, and a host->device copy into
@@ -314,6 +335,7 @@ AIGPU_ABI int aigpu_latent_attention(const AiGpuLatentAttention* args);
 /*    holding codes j and j+16, offset 8; one fp32 scale per 32). They      */
 /*    return nothing, as the reference's do; failures set aigpu_last_error.  */
 /* ------------------------------------------------------------------------ */
+#ifndef AI_GPU_DEVICE_ABI_H
 AIGPU_ABI void aigpu_matmul_nt(const float* a, const void* b, float* c,
                                uint64_t m, uint64_t k, uint64_t n);            /* DeviceABI.h:101 */
 AIGPU_ABI void aigpu_matmul_nt_bf16(const float* a, const void* b, float* c,
@@ -322,6 +344,7 @@ AIGPU_ABI void aigpu_matmul_nt_q8(const float* a, const void* b, const void* sca
                                   uint64_t m, uint64_t k, uint64_t n);         /* DeviceABI.h:107 */
 AIGPU_ABI void aigpu_matmul_nt_q4(const float* a, const void* b, const void* scales, float* c,
                                   uint64_t m, uint64_t k, uint64_t n);         /* DeviceABI.h:111 */
+#endif /* !AI_GPU_DEVICE_ABI_H */
 
 /* The device form of the same product (no counterpart in the reference,
    whose matmul stages a and c through the host every call): every pointer
@@ -342,20 +365,21 @@ typedef struct AiGpuMatmul {
 AIGPU_ABI int aigpu_matmul_device(const AiGpuMatmul* args);
 
 /* ------------------------------------------------------------------------ */
-/* 8. The resident single-token decoder (DeviceABI.h:114-157), the same     */
+/* 8. The resident single-token decoder (DeviceABI.h:119-152), the same     */
 /*    structs and entry points: a dense RMSNorm / RoPE / SwiGLU model kept   */
 /*    on the device; LocalModel::residentDecode (LocalModel.hpp:3598-3645)   */
 /*    is the caller. Weight codes and scales are device pointers (from      */
 /*    aigpu_upload) and stay the caller's; norms, biases, rotary            */
 /*    frequencies and the cache arrays are host pointers, copied in.        */
 /* ------------------------------------------------------------------------ */
-typedef struct AiGpuDenseWeight {       /* DeviceABI.h:116-121 */
+#ifndef AI_GPU_DEVICE_ABI_H
+typedef struct AiGpuDenseWeight {       /* DeviceABI.h:122-127 */
     const void* codes;
     const void* scales;
     uint32_t type, inDim, outDim;       /* F32=0, BF16=1, Q8=2, Q4=3 */
     const float* bias;                  /* optional, copied at creation */
 } AiGpuDenseWeight;
-typedef struct AiGpuDenseLayer {        /* DeviceABI.h:122-129 */
+typedef struct AiGpuDenseLayer {        /* DeviceABI.h:128-135 */
     AiGpuDenseWeight q, k, v, o, gate, up, down;
     const float* inputNorm;
     const float* postNorm;
@@ -363,7 +387,7 @@ typedef struct AiGpuDenseLayer {        /* DeviceABI.h:122-129 */
     const float* kNorm;
     uint32_t window;                    /* 0 = full causal attention */
 } AiGpuDenseLayer;
-typedef struct AiGpuDenseConfig {       /* DeviceABI.h:130-138 */
+typedef struct AiGpuDenseConfig {       /* DeviceABI.h:136-143 */
     uint32_t hidden, layers, heads, kvHeads, headDim, intermediate;
     uint32_t capacity, rotaryDims, vocab;
     float epsilon, theta;
@@ -380,6 +404,7 @@ AIGPU_ABI void aigpu_dense_decode(void* context, const float* embedding,
                                   float* logits, uint32_t position);           /* DeviceABI.h:149 */
 AIGPU_ABI void aigpu_dense_read_cache(void* context, float* const* keys,
                                       float* const* values, uint32_t length);  /* DeviceABI.h:151 */
+#endif /* !AI_GPU_DEVICE_ABI_H */
 
 /* ------------------------------------------------------------------------ */
 /* 9. attentionMixer for a prefill in one call (LocalModel.hpp:2577-2667):  */

@@ -1,5 +1,5 @@
 // dense.hip - the resident single-token decoder behind aigpu_dense_*
-// (DeviceABI.h:114-157): a dense RMSNorm / RoPE / SwiGLU model (Qwen3,
+// (DeviceABI.h:119-152): a dense RMSNorm / RoPE / SwiGLU model (Qwen3,
 // Llama) kept on the device between tokens, so one decode step moves only the
 // embedding in and the logits out. The reference's HIP backend stubs these
 // entry points (Kernels.hip:636-641); LocalModel::residentDecode
