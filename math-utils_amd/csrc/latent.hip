@@ -237,7 +237,9 @@ __global__ __launch_bounds__(256) void latent_attn_kernel(LatentArgs a) {
 #pragma unroll
         for (int hh = 0; hh < HG; ++hh) {
             if (uint32_t(hh) >= nh) break;
-            const float inv = 1.0f / l[hh];
+            // an empty selection (no key at or before the token) leaves the
+            // context at zero, as the mixer's job does (l = 0, acc = 0)
+            const float inv = l[hh] > 0.0f ? 1.0f / l[hh] : 0.0f;
 #pragma unroll
             for (int e = 0; e < CPT; ++e)
                 if (tid + 256 * e < int(C)) a.context[(t * p.heads + h0 + hh) * C + tid + 256 * e] = acc[hh][e] * inv;
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(256) void latent_merge_kernel(LatentArgs a) {
     const float M = wave_max(mi);
     const float fi = (lane < int(a.splits) && mi != -INFINITY) ? expf(mi - M) : 0.0f;
     const float L = wave_sum(lane < int(a.splits) ? base[lane * rec + 1] * fi : 0.0f);
-    const float inv = 1.0f / L;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;   // every split empty: a zero context
     for (uint32_t c = threadIdx.x; c < C; c += 256) {
         float acc = 0.0f;
 #pragma unroll 8

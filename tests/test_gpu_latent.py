@@ -66,6 +66,16 @@ def test_sparse_selection(gpu):
     run(gpu, count, start, 20, 64, 32, 128, 5, selection=selection)
 
 
+def test_empty_selection_gives_zero_context(gpu):
+    """tokens whose selection is empty (indexTail off, before the first full
+    pool) attend to nothing: their output is 0, on one split and when the
+    keys of a decode token are split over workgroups"""
+    count, start = 5, 40
+    selection = [[], [1, 3], [], None, list(range(0, 40, 3))]
+    run(gpu, count, start, 20, 64, 32, 128, 6, selection=selection)
+    run(gpu, 1, 300, 20, 64, 48, 512, 7, selection=[[]])
+
+
 def test_rejects_bad_rank(gpu):
     import torch
     q = torch.zeros((1, 2, 8), device="cuda")

@@ -69,3 +69,15 @@ def test_one_key_returns_its_value():
     W = wkv.astype(np.float64).reshape(heads, dn + dv, -1)
     want = np.stack([W[h, dn:] @ latent[0].astype(np.float64) for h in range(heads)])
     np.testing.assert_allclose(got[0], want, rtol=1e-5, atol=1e-6)
+
+
+def test_empty_selection_leaves_the_context_zero():
+    """LocalModel.hpp:3145-3156 sums nothing for a token with no selected key:
+    its context, and so its output, stays zero (indexTail off, before the
+    first full pool)"""
+    q, latent, wkv = setup(4)
+    start, heads, dn, dv = 6, 3, 8, 6
+    sel = [[], None, [2], [], [0, 1]]
+    got = O.latent_attention(q, latent, wkv, start, heads, dn, dv, 0.3, selection=sel)
+    assert np.all(got[0] == 0.0) and np.all(got[3] == 0.0)
+    assert np.isfinite(got).all() and np.abs(got[1]).max() > 0.0
