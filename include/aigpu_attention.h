@@ -199,6 +199,16 @@ AIGPU_ABI int aigpu_decode_attention(const AiGpuDecode* args);
 /* q, k, v, out, positions, qNorm, kNorm, rotaryFrequencies are host
    pointers; the caches are device allocations. */
 AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode* args);
+/* aigpu_decode_attention without any allocation. No counterpart in the
+   reference: it is for callers that cannot allocate device memory (code
+   under HIP graph capture, serving loops that forbid hipMalloc). Its
+   split-K records and prepared queries live in a fixed 32 MiB device array
+   per GPU, held until the process ends; larger batches run in slices that
+   fit it, and a call whose single sequence does not fit returns 0 with the
+   reason. Calls that overlap on one GPU share that array and race: order
+   them on one stream. Same arguments, kernels and results as
+   aigpu_decode_attention. */
+AIGPU_ABI int aigpu_decode_attention_static(const AiGpuDecode* args);
 
 /* ------------------------------------------------------------------------ */
 /* 5. Gated delta rule over a token range (the recurrence of                  */

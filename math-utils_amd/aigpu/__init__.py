@@ -120,6 +120,7 @@ SIGNATURES = {
     "aigpu_prefill_attention_host": (C.c_int, [C.POINTER(AiGpuPrefill)]),
     "aigpu_decode_attention": (C.c_int, [C.POINTER(AiGpuDecode)]),
     "aigpu_decode_attention_host": (C.c_int, [C.POINTER(AiGpuDecode)]),
+    "aigpu_decode_attention_static": (C.c_int, [C.POINTER(AiGpuDecode)]),
     "aigpu_gdn_conv": (C.c_int, [C.POINTER(AiGpuGdnConv)]),
     "aigpu_kda_rule": (C.c_int, [C.POINTER(AiGpuKda)]),
     "aigpu_matmul_nt": (None, [_vp, _vp, _vp, _u64, _u64, _u64]),

@@ -456,6 +456,21 @@ AIGPU_ABI int aigpu_decode_attention(const AiGpuDecode* args) {
     return aigpu::launch_decode(decode_params(args), as_stream(args->stream)) ? 1 : 0;
 }
 
+AIGPU_ABI int aigpu_decode_attention_static(const AiGpuDecode* args) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    if (!args) return ctx.fail("decode (no allocation): null arguments"), 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    aigpu::FixedScratch fixed{};
+    if (!aigpu::decode_static_scratch(&fixed.base, &fixed.bytes)) return 0;
+    struct NoAlloc {
+        Context& c;
+        explicit NoAlloc(Context& x) : c(x) { c.noAlloc = true; }
+        ~NoAlloc() { c.noAlloc = false; }
+    } guard(ctx);
+    return aigpu::launch_decode(decode_params(args), as_stream(args->stream), &fixed) ? 1 : 0;
+}
+
 AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode* args) {
     Context& ctx = Context::instance();
     if (!ctx.ok) return 0;

@@ -49,6 +49,8 @@ struct Context {
 
     // profiling: events bracketing each launch, resolved on read
     bool profiling = false;
+    // set during a call that must allocate nothing: no profiling events
+    bool noAlloc = false;
     struct Pending { std::string kernel; hipEvent_t begin, end; };
     std::vector<Pending> pending;
     std::vector<hipEvent_t> spareEvents;
@@ -71,14 +73,15 @@ struct Context {
     template <typename Launch>
     bool launch(const char* kernel, hipStream_t stream, Launch body) {
         hipEvent_t a = nullptr, b = nullptr;
-        if (profiling) {
+        const bool timed = profiling && !noAlloc;
+        if (timed) {
             a = takeEvent();
             b = takeEvent();
             if (a) (void)hipEventRecord(a, stream);
         }
         body();
         const hipError_t e = hipGetLastError();
-        if (profiling && a && b) {
+        if (timed && a && b) {
             (void)hipEventRecord(b, stream);
             pending.push_back({kernel, a, b});
         }

@@ -513,9 +513,45 @@ uint32_t env_u32(const char* name, uint32_t fallback) {
     return env ? uint32_t(std::atol(env)) : fallback;
 }
 
+/*
+    The fixed scratch of aigpu_decode_attention_static: the split-K records
+    and the prepared queries, in device memory that exists from module load
+    until the process ends, so that the entry point allocates nothing. Each
+    GPU holds its own copy at its own address; host code never passes the
+    array's name (a host-side stand-in) to a kernel, only the address
+    hipGetSymbolAddress returns for the current device.
+*/
+constexpr size_t DECODE_STATIC_SCRATCH = size_t(32) << 20;
+__device__ __align__(256) unsigned char scratch[DECODE_STATIC_SCRATCH];
+
+constexpr int MAX_DEVICES = 64;
+void* staticScratch[MAX_DEVICES] = {};
+
 } // namespace
 
-bool launch_decode(const DecodeParams& p, hipStream_t stream) {
+bool decode_static_scratch(void** base, size_t* bytes) {
+    Context& ctx = Context::instance();
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+        (void)hipGetLastError();
+        return ctx.fail("decode (no allocation): no current device");
+    }
+    if (!staticScratch[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            (void)hipGetLastError();
+            return ctx.fail(std::string("decode (no allocation): hipGetSymbolAddress of the fixed scratch failed: ") +
+                            hipGetErrorString(e));
+        }
+        staticScratch[dev] = ptr;
+    }
+    *base = staticScratch[dev];
+    *bytes = DECODE_STATIC_SCRATCH;
+    return true;
+}
+
+bool launch_decode(const DecodeParams& p, hipStream_t stream, const FixedScratch* fixed) {
     Context& ctx = Context::instance();
     if (p.dim != 64 && p.dim != 128) return ctx.fail("decode: dim must be 64 or 128");
     if (p.kvHeads == 0 || p.heads % p.kvHeads) return ctx.fail("decode: heads must be a multiple of kvHeads");
@@ -536,22 +572,41 @@ bool launch_decode(const DecodeParams& p, hipStream_t stream) {
     // every resident workgroup (2 per CU) two items; AIGPU_DECODE_CHUNK overrides
     static const uint32_t chunkEnv = env_u32("AIGPU_DECODE_CHUNK", 0);
     static const uint32_t gridEnv = env_u32("AIGPU_DECODE_GRID", 512);
-    uint32_t chunkLen = 2048;
-    if (chunkEnv) {
-        chunkLen = chunkEnv < 4 * SLAB ? 4 * SLAB : chunkEnv / (4 * SLAB) * (4 * SLAB);
-    } else {
-        const uint64_t bs = p.batch < MAXB ? p.batch : MAXB;
-        while (chunkLen > 256 && bs * p.kvHeads * ((uint64_t(p.maxPosition) + chunkLen) / chunkLen) < 2ull * gridEnv)
-            chunkLen /= 2;
-    }
-    const uint32_t maxChunks = (p.maxPosition + 1 + chunkLen - 1) / chunkLen;
-    const uint64_t slice = p.batch < MAXB ? p.batch : MAXB;
+    auto chunk_for = [&](uint64_t bs) {
+        uint32_t len = 2048;
+        if (chunkEnv) return chunkEnv < 4 * SLAB ? uint32_t(4 * SLAB) : chunkEnv / (4 * SLAB) * (4 * SLAB);
+        while (len > 256 && bs * p.kvHeads * ((uint64_t(p.maxPosition) + len) / len) < 2ull * gridEnv) len /= 2;
+        return len;
+    };
     const size_t rs = size_t(record_floats(int(p.dim)));
-    float* parts = static_cast<float*>(ctx.grow(SLOT_DECODE_PARTS, slice * p.kvHeads * maxChunks * rs * sizeof(float)));
-    if (!parts) return false;
-    uint32_t* qrec = static_cast<uint32_t*>(
-        ctx.grow(SLOT_DECODE_QUERIES, slice * p.kvHeads * size_t(qrec_words(int(p.dim))) * 4));
-    if (!qrec) return false;
+    const size_t qwords = size_t(qrec_words(int(p.dim)));
+    uint64_t slice = p.batch < MAXB ? p.batch : MAXB;
+    uint32_t chunkLen = chunk_for(slice);
+    uint32_t maxChunks = (p.maxPosition + 1 + chunkLen - 1) / chunkLen;
+    auto parts_bytes = [&] { return (slice * p.kvHeads * maxChunks * rs * sizeof(float) + 255) & ~size_t(255); };
+    auto qrec_bytes = [&] { return slice * p.kvHeads * qwords * 4; };
+    float* parts = nullptr;
+    uint32_t* qrec = nullptr;
+    if (fixed) {
+        // the records of a slice of sequences must fit the fixed scratch:
+        // halve the slice until they do
+        while (slice > 1 && parts_bytes() + qrec_bytes() > fixed->bytes) {
+            slice = (slice + 1) / 2;
+            chunkLen = chunk_for(slice);
+            maxChunks = (p.maxPosition + 1 + chunkLen - 1) / chunkLen;
+        }
+        if (parts_bytes() + qrec_bytes() > fixed->bytes)
+            return ctx.fail("decode (no allocation): one sequence's split-K records need " +
+                            std::to_string(parts_bytes() + qrec_bytes()) + " bytes, above the fixed scratch of " +
+                            std::to_string(fixed->bytes));
+        parts = static_cast<float*>(fixed->base);
+        qrec = reinterpret_cast<uint32_t*>(static_cast<char*>(fixed->base) + parts_bytes());
+    } else {
+        parts = static_cast<float*>(ctx.grow(SLOT_DECODE_PARTS, parts_bytes()));
+        if (!parts) return false;
+        qrec = static_cast<uint32_t*>(ctx.grow(SLOT_DECODE_QUERIES, qrec_bytes()));
+        if (!qrec) return false;
+    }
 
     const uint64_t batchStride = p.batchStride ? p.batchStride : p.kvHeads * p.capacity * p.dim;
     for (uint64_t b0 = 0; b0 < p.batch; b0 += slice) {

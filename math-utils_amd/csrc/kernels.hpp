@@ -60,7 +60,15 @@ struct DecodeParams {
     uint32_t maxPosition;
     uint64_t batch, heads, kvHeads, dim, qStride, window, capacity, batchStride;
 };
-bool launch_decode(const DecodeParams& p, hipStream_t stream);
+// caller-provided scratch in place of the context's growable slots
+struct FixedScratch {
+    void* base;
+    size_t bytes;
+};
+bool launch_decode(const DecodeParams& p, hipStream_t stream, const FixedScratch* fixed = nullptr);
+// the address and size of the decode path's fixed device scratch on the
+// current device (hipGetSymbolAddress, taken once per device)
+bool decode_static_scratch(void** base, size_t* bytes);
 
 // ---- gated delta rule: chunked scan --------------------------------------
 struct DeltaRuleParams {

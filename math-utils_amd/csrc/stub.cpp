@@ -39,6 +39,7 @@ AIGPU_ABI int aigpu_prefill_attention(const AiGpuPrefill*) { return 0; }
 AIGPU_ABI int aigpu_prefill_attention_host(const AiGpuPrefill*) { return 0; }
 AIGPU_ABI int aigpu_decode_attention(const AiGpuDecode*) { return 0; }
 AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode*) { return 0; }
+AIGPU_ABI int aigpu_decode_attention_static(const AiGpuDecode*) { return 0; }
 AIGPU_ABI int aigpu_gated_delta_rule(const AiGpuDeltaRule*) { return 0; }
 AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule*) { return 0; }
 AIGPU_ABI int aigpu_gdn_conv(const AiGpuGdnConv*) { return 0; }
