@@ -489,6 +489,45 @@ def rms_norm_row(x, gamma, eps, offset=0.0):
     return out
 
 
+def attention_mixer(h, layer, keys, values, start, cfg, q_stride=None, gate=False):
+    """attentionMixer restated for `count` = h.shape[0] new rows at positions
+    start.. (LocalModel.hpp:2577-2667): the q/k/v projections (apply,
+    :2604-2606), per-head q/k RMSNorm and RoPE (:2608-2648), the append of k
+    and v into the position-major fp32 cache (:2650-2655), kernels::attention
+    over positions [0, start + count) with the layer's window (:2657-2659),
+    the optional output gate (:2660-2665) and the o projection (:2667).
+
+    h [count][hidden] (the normed hidden states); layer: weights q, k, v, o as
+    (stored, kind, scales, bias), q_norm, k_norm (None for none), window;
+    keys / values [capacity][kv_heads * head_dim] fp32, written in place at
+    [start, start + count). cfg: heads, kv_heads, head_dim, rotary_dims, eps,
+    freqs. q_stride is head_dim, or 2 head_dim with the gate. Returns
+    (o-projection output [count][hidden], the normed and rotated q
+    [count][heads][q_stride], the appended k rows [count][kv_heads][head_dim])."""
+    nH, nKV, D = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    qs = q_stride or D
+    h = np.ascontiguousarray(h, np.float32)
+    count = h.shape[0]
+
+    def proj(inp, w):
+        arr, kind, scales, bias = w
+        return matmul_nt(inp, arr, kind, scales=scales, bias=bias)
+
+    q = proj(h, layer["q"])
+    k = proj(h, layer["k"])
+    v = proj(h, layer["v"])
+    qn, kn = qk_norm_rope(q, k, count, start, nH, nKV, D, qs, layer["q_norm"], layer["k_norm"], cfg["eps"],
+                          cfg["freqs"], cfg["rotary_dims"])
+    keys[start:start + count] = kn.reshape(count, -1)
+    values[start:start + count] = v.reshape(count, -1)
+    attn = attention(qn.reshape(-1), keys[:start + count], values[:start + count], count, start, nH, nKV, D, qs,
+                     layer.get("window", 0))
+    if gate:
+        attn = output_gate(attn, q, nH, D, qs)
+    out = proj(attn.reshape(count, nH * D), layer["o"])
+    return out, qn.reshape(count, nH, qs), kn.reshape(count, nKV, D)
+
+
 def dense_decode(cfg, layers, head, final_norm, embedding, keys, values, position):
     """One token through a dense RMSNorm / RoPE / SwiGLU model, as
     LocalModel::forward runs it for count = 1 (LocalModel.hpp:3705-3799):
@@ -502,9 +541,10 @@ def dense_decode(cfg, layers, head, final_norm, embedding, keys, values, positio
     layers: dicts with weights q, k, v, o, gate, up, down, each a tuple
     (stored array, kind, scales, bias), norms input_norm, post_norm, q_norm,
     k_norm (None for none) and window. keys / values: per layer
-    [capacity][kv_heads * head_dim] fp32, written at `position`.
-    Every step is a pinned primitive of this module; returns the logits."""
-    H, nH, nKV, D = cfg["hidden"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    [capacity][kv_heads * head_dim] fp32, written at `position`. Returns the
+    logits. The composition is pinned by the reference's independent FP64
+    model (tools/make_gpu_fixture.py; tests/test_oracle_fixture_model.py)."""
+    H = cfg["hidden"]
     eps = cfg["eps"]
     x = np.ascontiguousarray(embedding, np.float32).reshape(1, H).copy()
 
@@ -514,16 +554,7 @@ def dense_decode(cfg, layers, head, final_norm, embedding, keys, values, positio
 
     for li, L in enumerate(layers):
         h = rms_norm_row(x[0], L["input_norm"], eps).reshape(1, H)
-        q = proj(h, L["q"])
-        k = proj(h, L["k"])
-        v = proj(h, L["v"])
-        q, k = qk_norm_rope(q, k, 1, position, nH, nKV, D, D, L["q_norm"], L["k_norm"], eps,
-                            cfg["freqs"], cfg["rotary_dims"])
-        keys[li][position] = k.reshape(-1)
-        values[li][position] = v.reshape(-1)
-        attn = attention(q.reshape(-1), keys[li][:position + 1], values[li][:position + 1], 1, position,
-                         nH, nKV, D, D, L["window"])
-        x = x + proj(attn.reshape(1, nH * D), L["o"])
+        x = x + attention_mixer(h, L, keys[li], values[li], position, cfg)[0]
         h = rms_norm_row(x[0], L["post_norm"], eps).reshape(1, H)
         g = proj(h, L["gate"])
         u = proj(h, L["up"])
@@ -601,4 +632,3 @@ def select_keys(q, w, pools, start_pos, heads, dim, pool, top_k, tail=True):
                          dim, pool, top_k, 1 if tail else 0)
     sel = [None if ct[t] == 0xFFFFFFFF else ks[st[t]:st[t] + ct[t]].copy() for t in range(count)]
     return sel, sc[:count * max_pools].reshape(count, max_pools)
-

@@ -59,20 +59,18 @@ def run(gpu, kind="bf16", count=70, start=25, hidden=256, H=8, KV=2, D=128, gate
     kc[:, :start] = hkb
     vc[:, :start] = hvb
 
-    def proj(a, name):
-        stored, scales, bias = ref[name]
-        return O.matmul_nt(a, stored, kind, scales, bias)
-
-    q = proj(x, "q").reshape(count, H, qs)
-    k = proj(x, "k").reshape(count, KV, D)
-    v = proj(x, "v").reshape(count, KV, D)
-    qn, kn = O.qk_norm_rope(q, k, count, start, H, KV, D, qs, gq, gk, 1e-6, fr, rot)
-    keys = np.concatenate([hk.transpose(1, 0, 2), kn], 0)
-    vals = np.concatenate([hv.transpose(1, 0, 2), v], 0)
-    att = O.attention_strided(qn, keys, vals, count, start, H, KV, D, qs, KV * D, D, window, nthreads=0)
-    if gate:
-        att = O.output_gate(att, q, H, D, qs)
-    want = proj(att.reshape(count, H * D), "o")
+    # attentionMixer through the oracle function whose composition the
+    # reference's FP64 model pins (tests/test_oracle_fixture_model.py), over
+    # the widened bf16 history in the reference's position-major fp32 cache
+    layer = {name: (stored, kind, scales, bias) for name, (stored, scales, bias) in ref.items()}
+    layer.update(q_norm=gq, k_norm=gk, window=window)
+    keys = np.zeros((start + count, KV * D), np.float32)
+    vals = np.zeros((start + count, KV * D), np.float32)
+    keys[:start] = hk.transpose(1, 0, 2).reshape(start, KV * D)
+    vals[:start] = hv.transpose(1, 0, 2).reshape(start, KV * D)
+    mcfg = dict(heads=H, kv_heads=KV, head_dim=D, rotary_dims=rot, eps=1e-6, freqs=fr)
+    want, _, kn = O.attention_mixer(x, layer, keys, vals, start, mcfg, q_stride=qs, gate=gate)
+    v = vals[start:start + count].reshape(count, KV, D)
     base = O.fill_normal((count, hidden), seed, "residual") if accumulate else None
     if accumulate:
         want = want + base
