@@ -837,29 +837,7 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-/* One 1 KB DMA block: each lane's 16 bytes from `src` into LDS at
-   lds + 16 * lane. Written as asm so the compiler's wait analysis does not
-   track it (it cannot tell the double-buffered stages apart and would wait for
-   all DMA before reading any of them); the scan orders its DMA with explicit
-   vmcnt waits and barriers. One wait state separates the M0 write from the
-   DMA that reads it; nothing else in the scan uses M0. */
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"   // M0 is reserved, and clobbered on purpose
-__device__ __forceinline__ void dma_block(const void* src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds)
-                 : "memory", "m0");
-}
-/* the same from a uniform base plus a 32-bit per-lane byte offset */
-__device__ __forceinline__ void dma_block(const void* base, uint32_t off, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "s"(lds)
-                 : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
-/* LDS byte address of a __shared__ object */
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-    return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
-}
 
 /*
     The scan for 16-byte aligned bf16 inputs with every chunk input DMA'd into

@@ -107,4 +107,29 @@ __device__ __forceinline__ void norm_rope_row(float* x, int dim, const float* ga
     }
 }
 
+/* One 1 KB DMA block: each lane's 16 bytes from `src` into LDS at
+   lds + 16 * lane. Written as asm so the compiler's wait analysis does not
+   track it: it cannot tell double-buffered stages apart, and a pending
+   global_load_lds (a FLAT-family load that also counts in lgkmcnt) makes
+   it wait for every LDS read with lgkmcnt(0). Callers order their DMA with
+   explicit vmcnt waits and barriers. One wait state separates the M0 write
+   from the DMA that reads it; no other code of these kernels uses M0. */
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   // M0 is reserved, and clobbered on purpose
+__device__ __forceinline__ void dma_block(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds)
+                 : "memory", "m0");
+}
+/* the same from a uniform base plus a 32-bit per-lane byte offset */
+__device__ __forceinline__ void dma_block(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+/* LDS byte address of a __shared__ object */
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
 } // namespace aigpu

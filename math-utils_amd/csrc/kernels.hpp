@@ -40,6 +40,8 @@ struct PrefillParams {
     uint64_t count, start, heads, kvHeads, dim, qStride, window, capacity;
 };
 bool launch_prefill(const PrefillParams& p, hipStream_t stream);
+// rows of zeros after the last kv head in the flash kernel's working copies
+constexpr uint32_t PREFILL_PAD_ROWS = 128;
 // the flash kernel's fp16 copies of the cache, [kvHeads][start + count][dim]
 bool prefill_work_buffers(const PrefillParams& p, void** kh, void** vh);
 

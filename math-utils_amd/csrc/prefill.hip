@@ -40,6 +40,17 @@ namespace {
 
 constexpr int PREP_MAX_DIM = 256;
 
+/* zero the pad rows that follow the last kv head's working rows: reads of
+   the flash kernel's last tile run past a head's rows into the next head's
+   (finite) rows, or, for the last head, into these */
+__device__ __forceinline__ void zero_pad_rows(_Float16* kh, _Float16* vh, uint64_t padAt, uint32_t dim) {
+    const uint32_t n8 = PREFILL_PAD_ROWS * dim / 8;
+    for (uint32_t i = threadIdx.x; i < n8; i += blockDim.x) {
+        reinterpret_cast<half8*>(kh + padAt)[i] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        reinterpret_cast<half8*>(vh + padAt)[i] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+}
+
 /* grid.y = kv head; each kv head's history [0, start) is one contiguous run */
 __global__ __launch_bounds__(256) void prefill_history_kernel(
     const uint16_t* __restrict__ keyCache, const uint16_t* __restrict__ valueCache,
@@ -70,6 +81,7 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(PrefillParams p, _Flo
     const int dim = int(p.dim), half = p.rotaryDims / 2;
     const uint64_t H = p.heads, KVH = p.kvHeads;
 
+    if (blockIdx.x == 0) zero_pad_rows(kh, vh, KVH * T * p.dim, uint32_t(p.dim));
     const uint32_t shift = __builtin_ctz(uint32_t(p.dim));   // dim is 64 or 128
     const uint32_t nq = uint32_t(H) << shift, nk = uint32_t(KVH) << shift;
     const size_t qrow = t * H * p.qStride, krow = t * nk;
@@ -179,6 +191,7 @@ __global__ __launch_bounds__(256) void prefill_prep_vec_kernel(PrefillParams p, 
     const uint32_t t = blockIdx.x, pos = uint32_t(p.start) + t;
     const uint32_t H = uint32_t(p.heads), KVH = uint32_t(p.kvHeads), rows = p.kvReady ? H : H + 2 * KVH;
     const int half = p.freqs ? p.rotaryDims / 2 : 0;
+    if (blockIdx.x == 0) zero_pad_rows(kh, vh, uint64_t(KVH) * T * D, uint32_t(D));
     if (tid < half) {
         const float fpos = float(pos);   // the reference's fp32 angle (LocalModel.hpp:2632)
         sincosf(fpos * p.freqs[tid], &sn[tid], &cs[tid]);
@@ -348,8 +361,9 @@ __device__ __forceinline__ void wait_vmcnt() {
     so the 4 rows x 64 bytes a 32-lane transposed read touches hit distinct
     banks.
 */
-template <int D, int WAVES, int STAGES, int BN = 64>
+template <int D, int WAVES, int STAGES, int BN = 64, bool PP = false>
 __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_kernel(FlashArgs a) {
+    static_assert(!PP || (WAVES == 8 && STAGES == 2 && BN == 128), "ping-pong: 8 waves, 2 stages, 128-key tiles");
     constexpr int BM = 32 * WAVES;
     constexpr int NKB = BN / 32;          // 32-key blocks per tile
     constexpr int DB = D / 16;            // 16-deep d blocks of the S^T product
@@ -405,6 +419,8 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     const uint32_t P = a.start + tq;
     const uint32_t wLast = (wq0 + 31 < a.count ? wq0 + 31 : a.count - 1);
     const uint32_t wPosFirst = a.start + wq0, wPosLast = a.start + wLast;
+    // the first key this lane's query sees (Kernels.hpp:142)
+    const uint32_t firstKey = (a.window && P + 1 > a.window) ? P + 1 - a.window : 0u;
 
     half8 qreg[DB];
     if (a.fuseQ) {
@@ -622,12 +638,20 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         const bool needMask = (k0 + BN - 1 > wPosFirst) ||
                               (a.window && uint64_t(k0) + a.window < uint64_t(wPosLast) + 1);
         if (needMask) {
+            // register r of block kb holds key k0 + 16 g + c, c = 32 kb + r,
+            // and the lane's query sees keys [firstKey, P]. The mask is built
+            // without compares (whose 64 lane masks would all sit in scalar
+            // registers): the sign of hi - c (and of c - lo) selects the bit
+            // pattern of -inf or of +0, which is added to the score
+            const int base = int(k0 + 16 * g);
+            const int hi = int(P) - base;
+            const int lo = a.window ? int(firstKey) - base : -(1 << 30);
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const uint32_t key = k0 + 32 * kb + 16 * g + r;
-                    if (key > P || (a.window && uint64_t(key) + a.window <= P)) s[kb][r] = -INFINITY;
+                    const int out = (hi - (32 * kb + r)) | ((32 * kb + r) - lo);
+                    s[kb][r] += __int_as_float((out >> 31) & int(0xFF800000u));
                 }
         }
     };
@@ -748,6 +772,287 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
     using S2 = std::integral_constant<int, 2>;
+    if constexpr (PP) {
+        /*
+            Ping-pong. Group 0 (waves 0-3) leads and group 1 (waves 4-7) runs
+            one interval behind; every interval ends in a workgroup barrier.
+            A wave's own steps alternate: step 2j is its MFMA phase (O += P V
+            of tile j - 1, then S of tile j), step 2j + 1 the softmax of tile
+            j. Waves w and w + 4 share a SIMD, so in every interval one of
+            them feeds the matrix core while the other runs the softmax on
+            the VALU.
+
+            K and V are double-buffered by tile parity. In the intervals where
+            it runs the softmax, group 1 DMAs the K tile one ahead of the one
+            group 0 reads next and the V tile group 0 will need two intervals
+            later; it waits for that DMA before the barrier ending the
+            following interval, the last point before group 0 reads it. Each
+            stage a DMA refills was last read in the interval before.
+        */
+        const int grp = w >> 2, wq = w & 3;
+        constexpr int PB = NBLK / 4;   // DMA blocks per issuing wave per tile (K or V)
+        static_assert(D == 128 && RPB == 4 && PB == 8, "the ping-pong DMA offsets assume D = 128");
+        // Block n of issuing wave wq holds tile rows i = 4 (8 wq + n) + r,
+        // r = lane / 16, 16-byte column pos = lane % 16. K row i is key
+        // 32 wq + 16 (n & 1) + 4 (n >> 1) + r (key_of_row), its column block
+        // at pos ^ (4 (n & 3) + r) (kswz); V row i is key i, its block at
+        // pos ^ 4 r (vswz). So every offset is a per-lane base plus a
+        // compile-time constant: the K bases for the four values of n & 3
+        // and one V base.
+        const int rr = lane >> 4, cp = lane & 15;
+        int kb0[4], vb0;   // byte offsets
+#pragma unroll
+        for (int m = 0; m < 4; ++m) kb0[m] = 2 * ((32 * wq + rr) * D + 8 * ((cp ^ rr) ^ (4 * m)));
+        vb0 = 2 * ((32 * wq + rr) * D + 8 * (cp ^ (4 * rr)));
+        // the wave's first LDS block of a stage, in a scalar register
+        const uint32_t ldsWave = __builtin_amdgcn_readfirstlane(uint32_t(wq) * PB * 1024);
+        // DMA blocks [n0, n1) of this wave's share of one K or V tile. The
+        // per-block constant goes into the (scalar) source base, so a block
+        // costs no vector instruction. A tile running past a head's last
+        // row reads the next head's rows, or the zeroed pad rows after the
+        // last head; the causal mask drops those keys (their finite values
+        // meet P = 0).
+        auto dma_rows = [&](uint32_t k0, auto J, bool isK, auto N0, auto N1) __attribute__((always_inline)) {
+            constexpr int n0 = decltype(N0)::value, n1 = decltype(N1)::value;
+            const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_address(isK ? kbuf(J) : vbuf(J)) + ldsWave);
+            const char* src = reinterpret_cast<const char*>((isK ? kbase : vbase) + size_t(k0) * D);
+            // fresh each call: the offsets are not worth registers across the loop
+#pragma unroll
+            for (int m = 0; m < 4; ++m) asm volatile("" : "+v"(kb0[m]));
+            asm volatile("" : "+v"(vb0));
+#pragma unroll
+            for (int n = n0; n < n1; ++n) {
+                if (isK) dma_block(src + 2 * (16 * (n & 1) + 4 * (n >> 1)) * D, uint32_t(kb0[n & 3]), lds + n * 1024);
+                else dma_block(src + 2 * 4 * n * D, uint32_t(vb0), lds + n * 1024);
+            }
+        };
+        auto active = [&](uint32_t j) __attribute__((always_inline)) {
+            const uint32_t k0 = kbeg + j * BN;
+            return j < ntiles && !(k0 > wPosLast || (a.window && uint64_t(k0) + BN - 1 + a.window <= uint64_t(wPosFirst)));
+        };
+        // The MFMA phase's two products, each software-pipelined: operand
+        // fragments are read from LDS AHEAD products in advance into a ring,
+        // and the four accumulator chains are interleaved, so neither the
+        // LDS latency nor an accumulator dependence stalls the matrix core.
+        // The scheduling groups pin that order (the default schedule waits
+        // for every read just before its product).
+        constexpr int AHEAD_PP = 3;
+        auto pv_pp = [&](auto J, const half8 (&pk)[NKB][2]) __attribute__((always_inline)) {
+            const _Float16* vs = vbuf(J);
+            constexpr int N = NKB * 2 * DT;   // products: (kb, h) outer, dt inner
+            auto frag = [&](int i) __attribute__((always_inline)) {
+                const int dt = i % DT, hh = (i / DT) % 2, kb = i / (2 * DT);
+                const _Float16* a0 = vs + vaddr[dt] + (32 * kb + 8 * hh) * D;
+                return read_tr16x2(a0, a0 + 4 * D);
+            };
+            half8 f[AHEAD_PP + 1];
+#pragma unroll
+            for (int i = 0; i < AHEAD_PP; ++i) f[i] = frag(i);
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                if (i + AHEAD_PP < N) f[(i + AHEAD_PP) % (AHEAD_PP + 1)] = frag(i + AHEAD_PP);
+                const int dt = i % DT, hh = (i / DT) % 2, kb = i / (2 * DT);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i % (AHEAD_PP + 1)], pk[kb][hh], o[dt], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * AHEAD_PP, 0);
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                if (i + AHEAD_PP < N) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+        };
+        auto scores_pp = [&](uint32_t k0, auto J, floatx16 (&s)[NKB]) __attribute__((always_inline)) {
+            const _Float16* ks = kbuf(J);
+            constexpr int N = NKB * DB;   // products: db outer, kb inner
+            auto frag = [&](int i) __attribute__((always_inline)) {
+                const int kb = i % NKB, db = i / NKB;
+                return *reinterpret_cast<const half8*>(ks + kaddr[db] + 32 * kb * D);
+            };
+            half8 f[AHEAD_PP + 1];
+#pragma unroll
+            for (int i = 0; i < AHEAD_PP; ++i) f[i] = frag(i);
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                if (i + AHEAD_PP < N) f[(i + AHEAD_PP) % (AHEAD_PP + 1)] = frag(i + AHEAD_PP);
+                const int kb = i % NKB, db = i / NKB;
+                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i % (AHEAD_PP + 1)], qreg[db], s[kb], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, AHEAD_PP, 0);
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                if (i + AHEAD_PP < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+            const bool needMask = (k0 + BN - 1 > wPosFirst) ||
+                                  (a.window && uint64_t(k0) + a.window < uint64_t(wPosLast) + 1);
+            if (needMask) {
+                const int base = int(k0 + 16 * g);
+                const int hi = int(P) - base;
+                const int lo = a.window ? int(firstKey) - base : -(1 << 30);
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int out = (hi - (32 * kb + r)) | ((32 * kb + r) - lo);
+                        s[kb][r] += __int_as_float((out >> 31) & int(0xFF800000u));
+                    }
+            }
+        };
+        floatx16 s[NKB];
+        half8 pk[NKB][2];
+        bool haveP = false, haveS = false;
+        // MFMA phase of tile j: P.V of tile j - 1 (V stage VS), S of tile j (K stage KS)
+        auto mphase = [&](uint32_t j, auto KS, auto VS) __attribute__((always_inline)) {
+            haveS = active(j);
+            if (haveS) {   // S starts at -base (the registers are free: P holds the last tile)
+                const float nb = m == -INFINITY ? 0.0f : -m;
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) s[kb][r] = nb;
+            }
+            if (haveP) {
+                pv_pp(VS, pk);
+                haveP = false;
+            }
+            if (haveS) scores_pp(kbeg + j * BN, KS, s);
+        };
+        // The softmax of the ping-pong loop: as softmax(), with `hook(kb)`
+        // called after each 32-key block's exponentials. Group 1 issues its
+        // DMA there, two blocks of K and two of V at a time: issued back to
+        // back, a wave's sixteen DMA instructions stall it on the CU's memory
+        // queue (about 30 bytes a cycle) for longer than the softmax takes.
+        // The softmax of the ping-pong loop. The S accumulators start at
+        // -base (the running max, or 0 before the row's first key), so the
+        // products arrive as s - base and P = exp2 of them needs no
+        // subtraction. Only when a row's maximum passes base + 8 (P would
+        // exceed 2^8) does base move, to that maximum, with one subtraction
+        // pass and O rescaled. `hook(kb)` runs after each 32-key block's
+        // exponentials: group 1 issues its DMA there, two blocks of K and two
+        // of V at a time (issued back to back, a wave's sixteen DMA
+        // instructions stall it on the CU's memory queue, about 30 bytes a
+        // cycle, for longer than the softmax takes).
+        auto softmax_pp = [&](floatx16 (&s)[NKB], half8 (&pk)[NKB][2], auto hook) __attribute__((always_inline)) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+            {
+                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+                mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+            }
+            const bool fresh = m == -INFINITY;   // no visible key in earlier tiles
+            const bool grow = fresh ? mx != -INFINITY : mx > 8.0f;
+            const float shift = grow ? mx : 0.0f;
+            const float alpha = fresh ? 0.0f : (grow ? __builtin_amdgcn_exp2f(-shift) : 1.0f);
+            if (__any(grow)) {
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) s[kb][r] -= shift;
+            }
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            float psum = 0.0f;
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) pk[kb][h][j] = _Float16(__builtin_amdgcn_exp2f(s[kb][8 * h + j]));
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int j = 0; j < 8; j += 2)
+                        psum = __builtin_amdgcn_fdot2(h2{pk[kb][h][j], pk[kb][h][j + 1]}, h2{1, 1}, psum, false);
+                hook(kb, s, pk[kb][1]);
+            }
+            lsum = lsum * alpha + psum;
+            if (grow) m = (fresh ? 0.0f : m) + shift;
+            if (__any(grow)) {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+            }
+        };
+        auto vphase = [&](auto hook) __attribute__((always_inline)) {
+            if (haveS) {
+                softmax_pp(s, pk, hook);
+                haveP = true;
+                haveS = false;
+            } else {
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) hook(kb, s, pk[kb][1]);
+            }
+        };
+        auto no_dma = [](int, floatx16 (&)[NKB], const half8&) __attribute__((always_inline)) {};
+        using std::integral_constant;
+        // group 1's DMA during its softmax: K tile kt into stage KS and V tile
+        // vt into stage VS, blocks 2 kb and 2 kb + 1 of each after block kb
+        auto dma_hook = [&](uint32_t kt, uint32_t vt, auto KS, auto VS) __attribute__((always_inline)) {
+            return [&, kt, vt, KS, VS](int kb, floatx16 (&sc)[NKB], const half8& last) __attribute__((always_inline)) {
+                // ordering only (the asm statements emit nothing): the DMA
+                // follows block kb's exponentials, whose last result it takes,
+                // and precedes block kb + 1's, whose scores pass through the
+                // asm after it
+                asm volatile("" : : "v"(last));
+                const bool doK = kt < ntiles, doV = vt < ntiles;
+                auto two = [&](auto N0) __attribute__((always_inline)) {
+                    constexpr int n = decltype(N0)::value;
+                    if (doK) dma_rows(kbeg + kt * BN, KS, true, integral_constant<int, n>{}, integral_constant<int, n + 2>{});
+                    if (doV) dma_rows(kbeg + vt * BN, VS, false, integral_constant<int, n>{}, integral_constant<int, n + 2>{});
+                };
+                if (kb == 0) two(integral_constant<int, 0>{});
+                else if (kb == 1) two(integral_constant<int, 2>{});
+                else if (kb == 2) two(integral_constant<int, 4>{});
+                else two(integral_constant<int, 6>{});
+                if (kb + 1 < NKB) asm volatile("" : "+v"(sc[kb + 1 < NKB ? kb + 1 : kb]));
+            };
+        };
+        if (grp == 1) {
+            dma_rows(kbeg, S0{}, true, integral_constant<int, 0>{}, integral_constant<int, PB>{});
+            wait_vmcnt<0>();
+        }
+        lds_barrier();
+        const uint32_t nI = 2 * ntiles + 2;
+        for (uint32_t i0 = 0; i0 < nI; i0 += 4) {
+            const uint32_t j0 = i0 / 2;   // the even tile of this round
+            // interval i0: group 0 MFMA on tile j0; group 1 softmax of j0 - 1
+            // and DMA of K j0 + 1 and V j0
+            opaque_addresses();
+            if (grp == 0) mphase(j0, S0{}, S1{});
+            else vphase(dma_hook(j0 + 1, j0, S1{}, S0{}));
+            lds_barrier();
+            if (i0 + 1 >= nI) break;
+            // interval i0 + 1: group 0 softmax of j0; group 1 MFMA on j0
+            opaque_addresses();
+            if (grp == 0) {
+                vphase(no_dma);
+            } else {
+                mphase(j0, S0{}, S1{});
+                wait_vmcnt<0>();
+            }
+            lds_barrier();
+            if (i0 + 2 >= nI) break;
+            // interval i0 + 2: group 0 MFMA on tile j0 + 1; group 1 softmax of
+            // j0 and DMA of K j0 + 2 and V j0 + 1
+            opaque_addresses();
+            if (grp == 0) mphase(j0 + 1, S1{}, S0{});
+            else vphase(dma_hook(j0 + 2, j0 + 1, S0{}, S1{}));
+            lds_barrier();
+            if (i0 + 3 >= nI) break;
+            // interval i0 + 3: group 0 softmax of j0 + 1; group 1 MFMA on j0 + 1
+            opaque_addresses();
+            if (grp == 0) {
+                vphase(no_dma);
+            } else {
+                mphase(j0 + 1, S1{}, S0{});
+                wait_vmcnt<0>();
+            }
+            lds_barrier();
+        }
+    } else {
     issue(kbeg, S0{});
     if constexpr (AHEAD > 1)
         if (ntiles > 1) issue(kbeg + BN, S1{});
@@ -781,6 +1086,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         if constexpr (STAGES > 3)
             if (!step(it + 3, std::integral_constant<int, 3>{})) break;
     }
+    }
 
     lsum += __shfl_xor(lsum, 32, WAVE);
     if (rowValid) {
@@ -811,8 +1117,10 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
 bool prefill_work_buffers(const PrefillParams& p, void** kh, void** vh) {
     Context& ctx = Context::instance();
     const uint64_t T = p.start + p.count;
-    *kh = ctx.grow(SLOT_PREFILL_K, p.kvHeads * T * p.dim * 2);
-    *vh = ctx.grow(SLOT_PREFILL_V, p.kvHeads * T * p.dim * 2);
+    // PREFILL_PAD_ROWS rows past the last kv head, zeroed by prep: the flash
+    // kernel's last tile reads up to a tile past each head's rows unclamped
+    *kh = ctx.grow(SLOT_PREFILL_K, (p.kvHeads * T + PREFILL_PAD_ROWS) * p.dim * 2);
+    *vh = ctx.grow(SLOT_PREFILL_V, (p.kvHeads * T + PREFILL_PAD_ROWS) * p.dim * 2);
     return *kh && *vh;
 }
 
@@ -881,10 +1189,9 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     }
 
     const float qScale = LOG2E / sqrtf(float(p.dim));
-    // with the k, v rows already written and q read raw by the flash kernel,
-    // prep has work only for the cos/sin table
-    const bool prepIdle = p.kvReady && fuseQ && !rope;
-    if (!prepIdle && !ctx.launch("prefill_prep_kernel", stream, [&] {
+    // prep always runs: besides q/k/v rows and the cos/sin table it zeroes
+    // the working copies' pad rows
+    if (!ctx.launch("prefill_prep_kernel", stream, [&] {
             const dim3 grid{unsigned(p.count)}, block{256};
             const uint32_t t32 = uint32_t(T);
             if (!vec)
@@ -946,6 +1253,11 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
         const int n = env ? std::atoi(env) : 3;
         return waves == 4 ? 2 : (n >= 2 && n <= 4 ? n : 3);
     }();
+    // AIGPU_PREFILL_PP=0 selects the single-phase loop for 128-key tiles
+    static const bool pingPong = [] {
+        const char* env = std::getenv("AIGPU_PREFILL_PP");
+        return !(env && std::atoi(env) == 0);
+    }();
     a.nQT = uint32_t((p.count + 32 * waves - 1) / (32 * waves));
     const uint64_t blocks = uint64_t(a.nQT) * p.heads;
     a.xcdRemap = (blocks % 8 == 0) ? 1u : 0u;
@@ -957,7 +1269,9 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
         AIGPU_FLASH(128, 8, 2); AIGPU_FLASH(128, 8, 3); AIGPU_FLASH(128, 8, 4); AIGPU_FLASH(128, 4, 2);
         AIGPU_FLASH(64, 8, 2); AIGPU_FLASH(64, 8, 3); AIGPU_FLASH(64, 8, 4); AIGPU_FLASH(64, 4, 2);
 #undef AIGPU_FLASH
-        if (bn == 128 && p.dim == 128 && waves == 8)
+        if (bn == 128 && p.dim == 128 && waves == 8 && pingPong)
+            hipLaunchKernelGGL((prefill_flash_kernel<128, 8, 2, 128, true>), grid, block, 0, stream, a);
+        if (bn == 128 && p.dim == 128 && waves == 8 && !pingPong)
             hipLaunchKernelGGL((prefill_flash_kernel<128, 8, 2, 128>), grid, block, 0, stream, a);
         if (bn == 128 && p.dim == 64 && waves == 8)
             hipLaunchKernelGGL((prefill_flash_kernel<64, 8, 2, 128>), grid, block, 0, stream, a);
