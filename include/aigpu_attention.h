@@ -137,7 +137,11 @@ AIGPU_ABI int aigpu_attention_device(const AiGpuAttention* args);
 /*    attention (LocalModel.hpp:2608-2659) for `count` new tokens at          */
 /*    positions start..start+count-1, against a head-major bf16 cache that    */
 /*    already holds positions [0, start). Flash-style kernel on fp16 MFMA     */
-/*    with fp32 accumulation. dim must be 64 or 128.                          */
+/*    with fp32 accumulation. dim must be 64 or 128. q, k, v (after norm,     */
+/*    RoPE and q's scale) and the cached history go through fp16: a value     */
+/*    fp16 cannot hold (|x| >= 65520) makes the call return 0 with a reason;  */
+/*    to check, the call waits for its stream unless that stream is being    */
+/*    captured into a graph.                                                  */
 /* ------------------------------------------------------------------------ */
 typedef struct AiGpuPrefill {
     const void* q;            /* [count][heads][qStride], inType */
@@ -443,6 +447,7 @@ typedef struct AiGpuPrefillMixer {
     uint64_t count, start, hidden, heads, kvHeads, dim, window, capacity;
     void* stream;
 } AiGpuPrefillMixer;
+/* returns 0 with a reason for values outside fp16's range, as section 3 */
 AIGPU_ABI int aigpu_prefill_mixer(const AiGpuPrefillMixer* args);
 
 /* ------------------------------------------------------------------------ */

@@ -48,7 +48,30 @@ Context::Context() {
         return;
     }
     name = props.name;
+    if (hipHostMalloc(reinterpret_cast<void**>(&rangeHost), sizeof(uint32_t), hipHostMallocMapped) != hipSuccess ||
+        hipHostGetDevicePointer(reinterpret_cast<void**>(&rangeDev), rangeHost, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        error = "hipHostMalloc of the fp16 range flag failed";
+        return;
+    }
+    *rangeHost = 0;
     ok = true;
+}
+
+bool Context::checkRange(const char* what, hipStream_t stream) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
+        (void)hipGetLastError();
+        capture = hipStreamCaptureStatusNone;
+    }
+    if (capture != hipStreamCaptureStatusNone) return true;
+    if (hipStreamSynchronize(stream) != hipSuccess)
+        return fail(std::string(what) + ": " + hipGetErrorString(hipGetLastError()));
+    if (__atomic_load_n(rangeHost, __ATOMIC_ACQUIRE) == 0) return true;
+    __atomic_store_n(rangeHost, 0u, __ATOMIC_RELEASE);
+    return fail(std::string(what) +
+                ": a q, k or v element (after its norm, rotation and scale) or a cached key or value "
+                "lies outside fp16's range (|x| > 65504): the fp16 working copies cannot hold it");
 }
 
 Context::~Context() {
@@ -383,7 +406,10 @@ AIGPU_ABI int aigpu_prefill_attention(const AiGpuPrefill* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("prefill: null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
-    return aigpu::launch_prefill(prefill_params(args), as_stream(args->stream)) ? 1 : 0;
+    aigpu::PrefillParams p = prefill_params(args);
+    p.rangeFlag = ctx.rangeDev;
+    return aigpu::launch_prefill(p, as_stream(args->stream)) && ctx.checkRange("prefill", as_stream(args->stream))
+               ? 1 : 0;
 }
 
 AIGPU_ABI int aigpu_prefill_attention_host(const AiGpuPrefill* args) {
@@ -413,7 +439,9 @@ AIGPU_ABI int aigpu_prefill_attention_host(const AiGpuPrefill* args) {
     dev.out = dOut;
     if (!dev.q || !dev.k || !dev.v) return 0;
     const Clock::time_point mark = Clock::now();
-    if (!aigpu::launch_prefill(prefill_params(&dev), nullptr) || !finish(ctx, mark)) return 0;
+    aigpu::PrefillParams p = prefill_params(&dev);
+    p.rangeFlag = ctx.rangeDev;
+    if (!aigpu::launch_prefill(p, nullptr) || !finish(ctx, mark) || !ctx.checkRange("prefill", nullptr)) return 0;
     return copy_out(ctx, args->out, dOut, outBytes) ? 1 : 0;
 }
 
@@ -799,7 +827,9 @@ AIGPU_ABI int aigpu_prefill_mixer(const AiGpuPrefillMixer* args) {
     p.qStride = args->outputGate ? 2 * args->dim : args->dim;
     p.window = args->window;
     p.capacity = args->capacity;
-    return aigpu::launch_prefill_mixer(p, as_stream(args->stream)) ? 1 : 0;
+    return aigpu::launch_prefill_mixer(p, as_stream(args->stream)) &&
+                   ctx.checkRange("prefill mixer", as_stream(args->stream))
+               ? 1 : 0;
 }
 
 AIGPU_ABI int aigpu_select_keys(const AiGpuSelectKeys* args) {

@@ -51,6 +51,16 @@ struct Context {
     bool profiling = false;
     // set during a call that must allocate nothing: no profiling events
     bool noAlloc = false;
+
+    // one word of mapped pinned host memory that kernels converting into the
+    // prefill's fp16 working copies set to 1 when a finite value overflows
+    // fp16; rangeDev is its device address
+    uint32_t* rangeHost = nullptr;
+    uint32_t* rangeDev = nullptr;
+    // waits for `stream` and reports (and clears) a raised range flag as a
+    // failure of `what`; a stream being captured into a graph is not waited
+    // for and the flag stays for the next checked call
+    bool checkRange(const char* what, hipStream_t stream);
     struct Pending { std::string kernel; hipEvent_t begin, end; };
     std::vector<Pending> pending;
     std::vector<hipEvent_t> spareEvents;

@@ -107,6 +107,21 @@ __device__ __forceinline__ void norm_rope_row(float* x, int dim, const float* ga
     }
 }
 
+/* fp16 of a finite fp32 value, noting in `bad` when it does not fit fp16's
+   range (|x| >= 65520 rounds to infinity); infinite or NaN inputs stay what
+   they are and are not noted */
+__device__ __forceinline__ _Float16 to_f16_checked(float x, bool& bad) {
+    const _Float16 h = _Float16(x);
+    bad |= __builtin_isinf(float(h)) && !__builtin_isinf(x) && !__builtin_isnan(x);
+    return h;
+}
+
+/* a vector store of 1 into the range flag (a benign race: every writer
+   stores the same value) */
+__device__ __forceinline__ void raise_range_flag(uint32_t* flag, bool bad) {
+    if (bad && flag) *reinterpret_cast<volatile uint32_t*>(flag) = 1u;
+}
+
 /* One 1 KB DMA block: each lane's 16 bytes from `src` into LDS at
    lds + 16 * lane. Written as asm so the compiler's wait analysis does not
    track it: it cannot tell double-buffered stages apart, and a pending

@@ -38,6 +38,9 @@ struct PrefillParams {
     // and v projections' epilogue wrote them)
     int kvReady;
     uint64_t count, start, heads, kvHeads, dim, qStride, window, capacity;
+    // set to 1 by any conversion into the fp16 working copies that overflows
+    // fp16's range (device address; null: not tracked)
+    uint32_t* rangeFlag;
 };
 bool launch_prefill(const PrefillParams& p, hipStream_t stream);
 // rows of zeros after the last kv head in the flash kernel's working copies
@@ -114,6 +117,7 @@ struct KvEpilogue {
     float eps, offset;
     uint32_t dim, rot, start, T;
     uint64_t capacity;
+    uint32_t* rangeFlag;  // as PrefillParams::rangeFlag
 };
 bool launch_gemm_kv(const GemvParams& p, const KvEpilogue& e, hipStream_t stream);
 

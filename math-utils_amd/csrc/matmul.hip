@@ -296,6 +296,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvParams p, KvEpilogue ep, 
         const uint32_t n = n0 + uint32_t(c0);                // k or v column: head n / D, dim n % D
         const uint32_t d0 = n % D, head = n / D, hc = uint32_t(c0) - d0;
         const uint32_t half = ep.freqs ? ep.rot / 2 : 0;
+        bool bad = false;   // an fp16 conversion out of range
         for (int hf = 0; hf < 2; ++hf) {
             __syncthreads();   // the operand reads, or the previous half's tile reads, are done
             if (wm == hf) {
@@ -363,12 +364,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvParams p, KvEpilogue ep, 
                         wb[t] = uint32_t(float_to_bf16_bits(y[e + 2 * t])) |
                                 (uint32_t(float_to_bf16_bits(y[e + 2 * t + 1])) << 16);
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) wh[t] = _Float16(y[e + t]);
+                    for (int t = 0; t < 8; ++t) wh[t] = to_f16_checked(y[e + t], bad);
                     *reinterpret_cast<u32x4*>(cdst + e) = wb;
                     *reinterpret_cast<half8*>(wdst + e) = wh;
                 }
             }
         }
+        raise_range_flag(ep.rangeFlag, bad);
     }
 }
 

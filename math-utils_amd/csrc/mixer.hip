@@ -77,6 +77,7 @@ bool launch_prefill_mixer(const MixerParams& p, hipStream_t stream) {
     pp.qStride = p.qStride;
     pp.window = p.window;
     pp.capacity = p.capacity;
+    pp.rangeFlag = ctx.rangeDev;
     void* kh = nullptr;
     void* vh = nullptr;
     if (!prefill_work_buffers(pp, &kh, &vh)) return false;
@@ -94,6 +95,7 @@ bool launch_prefill_mixer(const MixerParams& p, hipStream_t stream) {
     ek.start = uint32_t(p.start);
     ek.T = uint32_t(T);
     ek.capacity = p.capacity;
+    ek.rangeFlag = ctx.rangeDev;
     if (!launch_gemm_kv(projection(p.k, p.x, nullptr, p.count, 0), ek, stream)) return false;
     KvEpilogue ev = ek;
     ev.cache = p.valueCache;

@@ -2,8 +2,9 @@
 //
 // Three launches per call:
 //   prefill_history_kernel  converts cached positions [0, start) of the bf16
-//                           cache to the fp16 working copies (exact: every
-//                           bf16 value in fp16's range is an fp16 value)
+//                           cache to the fp16 working copies (exact for every
+//                           bf16 value in fp16's range; the rest raise the
+//                           range flag)
 //   prefill_prep_kernel     attentionMixer's QK-RMSNorm -> RoPE -> KV append
 //                           (LocalModel.hpp:2608-2655) for the new tokens, in
 //                           fp32; writes the bf16 cache and the fp16 copies
@@ -12,11 +13,14 @@
 //
 // Why fp16 operands: Q, K and P rounded to bf16 (8 significant bits) give
 // max-abs errors near 6e-3 on the 8k configuration; fp16 (11 bits) keeps
-// them near 5e-4, inside the 2e-3 bound, at the same MFMA rate. The KV cache
-// itself stays bf16.
+// them near 1.4e-3, inside the 2e-3 bound, at the same MFMA rate. The KV
+// cache itself stays bf16. Every conversion into fp16 is checked
+// (to_f16_checked): a finite value that overflows sets the caller's range
+// flag and the entry point fails instead of returning inf / NaN.
 //
 // Flash kernel layout (one workgroup = 8 waves = 256 query rows of one head,
-// one wave = 32 rows; key tiles of 64, DMA'd into LDS one tile ahead):
+// one wave = 32 rows; key tiles of 128, DMA'd into LDS, K and V each double
+// buffered):
 //   S^T = K Q^T     A = K rows (LDS), B = Q^T (registers, loaded once, already
 //                   scaled by log2(e)/sqrt(D) so the softmax is exp2 of it)
 //                   -> each lane owns one query (lane % 32) and 16 keys, so
@@ -27,6 +31,15 @@
 // The K tile rows are stored permuted so that accumulator register r of the
 // S^T tile holds key 16*(lane/32) + r, which makes each lane's 8-key slice of
 // P^T 8 consecutive keys.
+//
+// Ping-pong schedule (the default for D = 128): waves 0-3 and 4-7 share the
+// four SIMDs pairwise and run a tile interval apart, so while one wave of a
+// pair issues MFMAs (PV of the previous tile, then QK of this one) its
+// partner runs the softmax on the VALU; waves 4-7 also issue the next
+// tiles' DMA between their softmax steps. The running max is folded into the
+// score accumulators' initial value and rescaling is lazy (only when the max
+// grows by more than 8 in log2 units). AIGPU_PREFILL_PP=0 selects the
+// single-phase loop.
 #include "context.hpp"
 #include "device.hpp"
 #include "kernels.hpp"
@@ -55,16 +68,18 @@ __device__ __forceinline__ void zero_pad_rows(_Float16* kh, _Float16* vh, uint64
 __global__ __launch_bounds__(256) void prefill_history_kernel(
     const uint16_t* __restrict__ keyCache, const uint16_t* __restrict__ valueCache,
     _Float16* __restrict__ kh, _Float16* __restrict__ vh, uint32_t per, uint64_t capacity,
-    uint64_t dim, uint64_t T) {
+    uint64_t dim, uint64_t T, uint32_t* rangeFlag) {
     const uint64_t kv = blockIdx.y;
     const uint16_t* ks = keyCache + kv * capacity * dim;
     const uint16_t* vs = valueCache + kv * capacity * dim;
     _Float16* kd = kh + kv * T * dim;
     _Float16* vd = vh + kv * T * dim;
+    bool bad = false;
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < per; i += gridDim.x * blockDim.x) {
-        kd[i] = _Float16(bf16_bits_to_float(ks[i]));
-        vd[i] = _Float16(bf16_bits_to_float(vs[i]));
+        kd[i] = to_f16_checked(bf16_bits_to_float(ks[i]), bad);
+        vd[i] = to_f16_checked(bf16_bits_to_float(vs[i]), bad);
     }
+    raise_range_flag(rangeFlag, bad);
 }
 
 /* one workgroup per token: the token's q, k, v rows are staged in LDS with all
@@ -99,6 +114,7 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(PrefillParams p, _Flo
     }
     __syncthreads();
 
+    bool bad = false;   // an fp16 conversion out of range
     for (uint64_t h = w; h < (p.kvReady ? H : H + 2 * KVH); h += 4) {
         float* x = tok + h * p.dim;
         const bool isQuery = h < H, isKey = !isQuery && h < H + KVH;
@@ -123,7 +139,7 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(PrefillParams p, _Flo
         }
         if (isQuery) {
             _Float16* dst = qh + (h * p.count + t) * p.dim;
-            for (int d = lane; d < dim; d += WAVE) dst[d] = _Float16(x[d] * qScale);
+            for (int d = lane; d < dim; d += WAVE) dst[d] = to_f16_checked(x[d] * qScale, bad);
         } else {
             const uint64_t kv = isKey ? h - H : h - H - KVH;
             const uint64_t work = (kv * T + pos) * p.dim;
@@ -131,11 +147,12 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(PrefillParams p, _Flo
             _Float16* wdst = isKey ? kh : vh;
             uint16_t* cdst = isKey ? p.keyCache : p.valueCache;
             for (int d = lane; d < dim; d += WAVE) {
-                wdst[work + d] = _Float16(x[d]);
+                wdst[work + d] = to_f16_checked(x[d], bad);
                 cdst[cache + d] = float_to_bf16_bits(x[d]);
             }
         }
     }
+    raise_range_flag(p.rangeFlag, bad);
 }
 
 /* 8 consecutive input elements, widened to fp32 (16 B of bf16 or 32 B of f32) */
@@ -156,10 +173,10 @@ __device__ __forceinline__ void load8(const void* base, size_t i, float (&x)[8])
     }
 }
 
-__device__ __forceinline__ void store8_f16(_Float16* dst, const float (&x)[8], float scale) {
+__device__ __forceinline__ void store8_f16(_Float16* dst, const float (&x)[8], float scale, bool& bad) {
     half8 h;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = _Float16(x[e] * scale);
+    for (int e = 0; e < 8; ++e) h[e] = to_f16_checked(x[e] * scale, bad);
     *reinterpret_cast<half8*>(dst) = h;
 }
 
@@ -215,6 +232,7 @@ __global__ __launch_bounds__(256) void prefill_prep_vec_kernel(PrefillParams p, 
         }
     }
 
+    bool bad = false;   // an fp16 conversion out of range
     for (uint32_t r0 = firstRow + tid / LPR; r0 < rows; r0 += UNROLL * RPP) {
         float x[UNROLL][8];
 #pragma unroll
@@ -258,23 +276,25 @@ __global__ __launch_bounds__(256) void prefill_prep_vec_kernel(PrefillParams p, 
                 }
             }
             if (r < H) {
-                store8_f16(qh + (size_t(r) * p.count + t) * D + e0, v, qScale);
+                store8_f16(qh + (size_t(r) * p.count + t) * D + e0, v, qScale, bad);
             } else {
                 const bool isKey = r < H + KVH;
                 const uint32_t kv = isKey ? r - H : r - H - KVH;
-                store8_f16((isKey ? kh : vh) + (size_t(kv) * T + pos) * D + e0, v, 1.0f);
+                store8_f16((isKey ? kh : vh) + (size_t(kv) * T + pos) * D + e0, v, 1.0f, bad);
                 store8_bf16((isKey ? p.keyCache : p.valueCache) + (size_t(kv) * p.capacity + pos) * D + e0, v);
             }
         }
     }
+    raise_range_flag(p.rangeFlag, bad);
 }
 
 /* prefill_history_kernel with 8 elements (16 B) per lane and step */
 __global__ __launch_bounds__(256) void prefill_history_vec_kernel(
     const uint16_t* __restrict__ keyCache, const uint16_t* __restrict__ valueCache,
     _Float16* __restrict__ kh, _Float16* __restrict__ vh, uint32_t per8, uint64_t capacity,
-    uint32_t dim, uint32_t T) {
+    uint32_t dim, uint32_t T, uint32_t* rangeFlag) {
     const uint32_t kv = blockIdx.y;
+    bool bad = false;
     const u32x4* ks = reinterpret_cast<const u32x4*>(keyCache + kv * capacity * dim);
     const u32x4* vs = reinterpret_cast<const u32x4*>(valueCache + kv * capacity * dim);
     half8* kd = reinterpret_cast<half8*>(kh + size_t(kv) * T * dim);
@@ -284,14 +304,15 @@ __global__ __launch_bounds__(256) void prefill_history_vec_kernel(
         half8 x, y;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            x[2 * e] = _Float16(__uint_as_float(a[e] << 16));
-            x[2 * e + 1] = _Float16(__uint_as_float(a[e] & 0xFFFF0000u));
-            y[2 * e] = _Float16(__uint_as_float(b[e] << 16));
-            y[2 * e + 1] = _Float16(__uint_as_float(b[e] & 0xFFFF0000u));
+            x[2 * e] = to_f16_checked(__uint_as_float(a[e] << 16), bad);
+            x[2 * e + 1] = to_f16_checked(__uint_as_float(a[e] & 0xFFFF0000u), bad);
+            y[2 * e] = to_f16_checked(__uint_as_float(b[e] << 16), bad);
+            y[2 * e + 1] = to_f16_checked(__uint_as_float(b[e] & 0xFFFF0000u), bad);
         }
         kd[i] = x;
         vd[i] = y;
     }
+    raise_range_flag(rangeFlag, bad);
 }
 
 struct FlashArgs {
@@ -308,6 +329,7 @@ struct FlashArgs {
     float eps, normOffset, qScale;
     uint32_t qStride, inType, half, fuseQ;
     uint32_t outputGate;   // out *= sigmoid(qraw[row + D + d]) (LocalModel.hpp:2660-2665)
+    uint32_t* rangeFlag;   // set when a q element overflows fp16 (PrefillParams::rangeFlag)
 };
 
 typedef __fp16 fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
@@ -338,6 +360,105 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+/* One query row into the score MFMA's B operand: this lane's half of row tq
+   of head `head` (elements 16 db + 8 g + j) as fp16, scaled by
+   log2(e)/sqrt(D). With fuseQ the raw row is normed (QK-RMSNorm, the other
+   half's sum over one v_permlane32_swap) and rotated (RoPE pairs (e, e +
+   half) within the lane, half % 16 == 0) here, as attentionMixer does
+   (LocalModel.hpp:2608-2648); otherwise prep's scaled fp16 copy is read.
+   Rows past the call's count give zeros. The caller waits for the loads. */
+template <int D>
+__device__ __forceinline__ void load_query(const FlashArgs& a, uint32_t tq, bool rowValid, uint32_t head, int g,
+                                           half8 (&qreg)[D / 16]) {
+    constexpr int DB = D / 16;
+    if (a.fuseQ) {
+        // this lane's half of its query row: elements 16 db + 8g + j. QK-RMSNorm
+        // over the row (the other half is in lane ^ 32), RoPE pairs (e, e + half)
+        // within the lane (half % 16 == 0), then the log2(e)/sqrt(D) scale
+        // (attentionMixer, LocalModel.hpp:2608-2648)
+        float x[DB][8];
+        bool bad = false;   // an fp16 conversion out of range
+        const size_t row = (size_t(rowValid ? tq : 0) * a.heads + head) * a.qStride;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            if (a.inType == 0) {
+                const floatx4* src = reinterpret_cast<const floatx4*>(static_cast<const float*>(a.qraw) + row + 16 * db + 8 * g);
+                const floatx4 lo = src[0], hi = src[1];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[db][j] = lo[j];
+                    x[db][4 + j] = hi[j];
+                }
+            } else {
+                const u32x4 wv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qraw) + row + 16 * db + 8 * g);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[db][2 * j] = __uint_as_float(wv[j] << 16);
+                    x[db][2 * j + 1] = __uint_as_float(wv[j] & 0xFFFF0000u);
+                }
+            }
+        }
+        if (a.qNorm) {   // rmsNormRow (LocalModel.hpp:1341-1348)
+            float ss = 0.0f;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) ss += x[db][j] * x[db][j];
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+            ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+            const float inv = 1.0f / sqrtf(ss / float(D) + a.eps);
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const floatx4* gm = reinterpret_cast<const floatx4*>(a.qNorm + 16 * db + 8 * g);
+                const floatx4 g0 = gm[0], g1 = gm[1];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[db][j] = x[db][j] * inv * (g0[j] + a.normOffset);
+                    x[db][4 + j] = x[db][4 + j] * inv * (g1[j] + a.normOffset);
+                }
+            }
+        }
+        if (a.rope) {   // rotate-half pairs (LocalModel.hpp:2636-2641)
+            const float* cs = a.rope + size_t(rowValid ? tq : 0) * 2 * a.half;
+            const int hb = int(a.half) / 16;   // partner block offset
+#pragma unroll
+            for (int db = 0; db < DB / 2; ++db) {
+                if (db < hb) {
+                    const floatx4* cp = reinterpret_cast<const floatx4*>(cs + 16 * db + 8 * g);
+                    const floatx4* sp = reinterpret_cast<const floatx4*>(cs + a.half + 16 * db + 8 * g);
+                    const floatx4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float cj = j < 4 ? c0[j] : c1[j - 4], sj = j < 4 ? s0[j] : s1[j - 4];
+                        const float lo = x[db][j];
+                        float hi = 0.0f;
+#pragma unroll
+                        for (int pb = 0; pb < DB; ++pb)
+                            if (pb == db + hb) hi = x[pb][j];
+                        const float nlo = lo * cj - hi * sj, nhi = hi * cj + lo * sj;
+                        x[db][j] = nlo;
+#pragma unroll
+                        for (int pb = 0; pb < DB; ++pb)
+                            if (pb == db + hb) x[pb][j] = nhi;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qreg[db][j] = rowValid ? to_f16_checked(x[db][j] * a.qScale, bad) : _Float16(0.0f);
+        raise_range_flag(a.rangeFlag, bad);
+    } else {
+        const _Float16* qrow = a.qh + (size_t(head) * a.count + (rowValid ? tq : 0)) * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            if (rowValid) qreg[db] = *reinterpret_cast<const half8*>(qrow + 16 * db + 8 * g);
+            else qreg[db] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+    }
 }
 
 /*
@@ -423,98 +544,12 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     const uint32_t firstKey = (a.window && P + 1 > a.window) ? P + 1 - a.window : 0u;
 
     half8 qreg[DB];
-    if (a.fuseQ) {
-        // this lane's half of its query row: elements 16 db + 8g + j. QK-RMSNorm
-        // over the row (the other half is in lane ^ 32), RoPE pairs (e, e + half)
-        // within the lane (half % 16 == 0), then the log2(e)/sqrt(D) scale
-        // (attentionMixer, LocalModel.hpp:2608-2648)
-        float x[DB][8];
-        const size_t row = (size_t(rowValid ? tq : 0) * a.heads + head) * a.qStride;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            if (a.inType == 0) {
-                const floatx4* src = reinterpret_cast<const floatx4*>(static_cast<const float*>(a.qraw) + row + 16 * db + 8 * g);
-                const floatx4 lo = src[0], hi = src[1];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    x[db][j] = lo[j];
-                    x[db][4 + j] = hi[j];
-                }
-            } else {
-                const u32x4 wv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qraw) + row + 16 * db + 8 * g);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    x[db][2 * j] = __uint_as_float(wv[j] << 16);
-                    x[db][2 * j + 1] = __uint_as_float(wv[j] & 0xFFFF0000u);
-                }
-            }
-        }
-        if (a.qNorm) {   // rmsNormRow (LocalModel.hpp:1341-1348)
-            float ss = 0.0f;
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) ss += x[db][j] * x[db][j];
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
-            ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-            const float inv = 1.0f / sqrtf(ss / float(D) + a.eps);
-#pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                const floatx4* gm = reinterpret_cast<const floatx4*>(a.qNorm + 16 * db + 8 * g);
-                const floatx4 g0 = gm[0], g1 = gm[1];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    x[db][j] = x[db][j] * inv * (g0[j] + a.normOffset);
-                    x[db][4 + j] = x[db][4 + j] * inv * (g1[j] + a.normOffset);
-                }
-            }
-        }
-        if (a.rope) {   // rotate-half pairs (LocalModel.hpp:2636-2641)
-            const float* cs = a.rope + size_t(rowValid ? tq : 0) * 2 * a.half;
-            const int hb = int(a.half) / 16;   // partner block offset
-#pragma unroll
-            for (int db = 0; db < DB / 2; ++db) {
-                if (db < hb) {
-                    const floatx4* cp = reinterpret_cast<const floatx4*>(cs + 16 * db + 8 * g);
-                    const floatx4* sp = reinterpret_cast<const floatx4*>(cs + a.half + 16 * db + 8 * g);
-                    const floatx4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const float cj = j < 4 ? c0[j] : c1[j - 4], sj = j < 4 ? s0[j] : s1[j - 4];
-                        const float lo = x[db][j];
-                        float hi = 0.0f;
-#pragma unroll
-                        for (int pb = 0; pb < DB; ++pb)
-                            if (pb == db + hb) hi = x[pb][j];
-                        const float nlo = lo * cj - hi * sj, nhi = hi * cj + lo * sj;
-                        x[db][j] = nlo;
-#pragma unroll
-                        for (int pb = 0; pb < DB; ++pb)
-                            if (pb == db + hb) x[pb][j] = nhi;
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) qreg[db][j] = rowValid ? _Float16(x[db][j] * a.qScale) : _Float16(0.0f);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        wait_vmcnt<0>();
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    } else {
-        const _Float16* qrow = a.qh + (size_t(head) * a.count + (rowValid ? tq : 0)) * D;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            if (rowValid) qreg[db] = *reinterpret_cast<const half8*>(qrow + 16 * db + 8 * g);
-            else qreg[db] = half8{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-        // Q lands before any DMA is issued, so the vmcnt waits in the loop
-        // only ever count DMA
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        wait_vmcnt<0>();
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    }
+    load_query<D>(a, tq, rowValid, head, g, qreg);
+    // Q lands before any DMA is issued, so the vmcnt waits in the loop only
+    // ever count DMA
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    wait_vmcnt<0>();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
     floatx16 o[DT];
 #pragma unroll
@@ -1180,10 +1215,11 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
                 const dim3 grid{blocks, unsigned(p.kvHeads)};
                 if (vec)
                     hipLaunchKernelGGL(prefill_history_vec_kernel, grid, dim3(256), 0, stream, p.keyCache,
-                                       p.valueCache, kh, vh, per8, p.capacity, uint32_t(p.dim), uint32_t(T));
+                                       p.valueCache, kh, vh, per8, p.capacity, uint32_t(p.dim), uint32_t(T),
+                                       p.rangeFlag);
                 else
                     hipLaunchKernelGGL(prefill_history_kernel, grid, dim3(256), 0, stream, p.keyCache,
-                                       p.valueCache, kh, vh, per, p.capacity, p.dim, T);
+                                       p.valueCache, kh, vh, per, p.capacity, p.dim, T, p.rangeFlag);
             }))
             return false;
     }
@@ -1235,6 +1271,7 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     a.inType = uint32_t(p.inType);
     a.half = p.freqs ? uint32_t(p.rotaryDims / 2) : 0u;
     a.outputGate = p.outputGate ? 1u : 0u;
+    a.rangeFlag = p.rangeFlag;
     // AIGPU_PREFILL_WAVES / AIGPU_PREFILL_STAGES pick the tiling (tuning);
     // 4-wave workgroups run two per CU and take two stages
     static const int waves = [] {

@@ -34,12 +34,12 @@ def weight(n, k, kind, seed, tag):
 
 
 def run(gpu, kind="bf16", count=70, start=25, hidden=256, H=8, KV=2, D=128, gate=False, norm=True,
-        rope=True, rot=None, biases=False, window=0, seed=3, accumulate=False):
+        rope=True, rot=None, biases=False, window=0, seed=3, accumulate=False, x_scale=1.0):
     import torch
     qs = 2 * D if gate else D
     cap = start + count + 5
     rot = rot or D
-    x = O.fill_normal((count, hidden), seed, "x")
+    x = O.fill_normal((count, hidden), seed, "x") * np.float32(x_scale)
     shapes = {"q": (H * qs, hidden), "k": (KV * D, hidden), "v": (KV * D, hidden), "o": (hidden, H * D)}
     dev, ref = {}, {}
     for i, (name, (n, k)) in enumerate(shapes.items()):
