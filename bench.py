@@ -35,12 +35,16 @@ PEAK_MFMA_F32 = 157.3       # TFLOP/s, fp32
 PEAK_HBM = 8000.0           # GB/s
 CPU_THREADS_CAP = 16        # the GPU box's CPU share for one GPU
 
-# HBM bytes per launch of prefill_flash_kernel<128, 8, 2, 128> on configs[2]:
-# rocprofv3 FETCH_SIZE and WRITE_SIZE passes, each scaled by what the same
-# counter reads for a 1 GiB device copy (fetch x2.000, write x1.000):
-# 185.1 MB read + 158.3 MB written (profiles/prefill_flash_kernel_cfg3_hbm_traffic.md).
+# HBM bytes per launch of prefill_flash_kernel<128, 8, 2, 128, true> on
+# rocprofv3 FETCH_SIZE and WRITE_SIZE passes, each scaled by what
+# the same counter reads for a 1 GiB device copy (fetch x2.000, write x1.000):
+# 184.1 MB read + 135.6 MB written (profiles/prefill_flash_kernel_cfg3_hbm_traffic.md).
 # Re-measure when the kernel changes.
-PREFILL_FLASH_TRAFFIC = 343.4e6
+PREFILL_FLASH_TRAFFIC = 319.7e6
+# HBM bytes per launch of decode_attention_kernel<128> on configs[3], measured
+# the same way: 1,240.4 MB read + 5.2 MB written
+# (profiles/decode_attention_kernel_cfg4_hbm_traffic.md)
+DECODE_ATTENTION_TRAFFIC = 1245.6e6
 
 
 def parse():
@@ -154,6 +158,27 @@ def cpu_lib():
     return O, None, "port", threads
 
 
+def cpu_model():
+    """the host CPU's model string (/proc/cpuinfo), for the baseline record"""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
+
+
+def cpu_threads(cpu, n):
+    """sizes the reference library's pool (or the port's thread count) to n"""
+    O, ref, kind, threads = cpu
+    if ref is not None:
+        ref.ref_configure_pool(n)
+    return n
+
+
 # --------------------------------------------------------------- workloads
 def prefill_workload(args, cpu):
     import numpy as np
@@ -192,7 +217,8 @@ def prefill_workload(args, cpu):
         kh = k.float().cpu().numpy()
         vh = v.float().cpu().numpy()
 
-        def run(n):
+        def run(n, nthreads):
+            cpu_threads(cpu, nthreads)
             start = S - n
             qq = np.ascontiguousarray(np.resize(qh, (n, H, D)), np.float32)
             o = np.zeros(n * H * D, np.float32)
@@ -201,14 +227,23 @@ def prefill_workload(args, cpu):
                 ref.ref_attention(qq.reshape(-1), kh.reshape(-1), vh.reshape(-1), o, n, start, H, KV, D,
                                   D, 0, 1)
             else:
-                O.attention(qq, kh, vh, n, start, H, KV, D, D, nthreads=threads)
+                O.attention(qq, kh, vh, n, start, H, KV, D, D, nthreads=nthreads)
             dt = time.perf_counter() - t
             return 4.0 * D * H * sum(start + i + 1 for i in range(n)), dt
 
-        f0, t0 = run(32)
+        f0, t0 = run(32, threads)
         n = int(min(S, max(32, 32 * args.cpu_seconds / max(t0, 1e-3))))
-        f1, t1 = run(n)
+        f1, t1 = run(n, threads)
+        # one core, on a third of the time
+        g0, u0 = run(4, 1)
+        n1 = int(min(S, max(4, 4 * args.cpu_seconds / 3 / max(u0, 1e-3))))
+        g1, u1 = run(n1, 1)
+        cpu_threads(cpu, threads)
         res["cpu_baseline"] = {"value": f1 / t1 / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": kind,
+                               "cpu_model": cpu_model(),
+                               "single_core": {"value": g1 / u1 / 1e12, "unit": "TFLOP/s",
+                                               "sample": f"the last {n1} query rows on one thread "
+                                                         f"({g1 / 1e9:.1f} GFLOP in {u1:.1f} s)"},
                                "sample": f"kernels::attention over the last {n} of the 8192 query rows "
                                          f"(full causal history, {f1 / 1e9:.1f} GFLOP in {t1:.1f} s, "
                                          f"fp32, static-split pool)"}
@@ -244,37 +279,67 @@ def decode_workload(args, cpu):
         "workload": "configs[3] qwen3-30b-a3b batched ragged GQA decode B=32 L~U[1k,32k] 32q/4kv D=128 bf16 KV",
         "dtype": "bf16",
         "value": nbytes / (step_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": step_ms,
+        "step_frac": nbytes / (step_ms * 1e-3) / 1e9 / PEAK_HBM,
         "kv_bytes": nbytes,
         "roofline": {"kernel": "decode_attention_kernel", "bound": "hbm",
                      "achieved": nbytes / (k_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
-                     "frac": nbytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
+                     "frac": nbytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": DECODE_ATTENTION_TRAFFIC,
                      "kernel_ms": k_ms, "bytes_per_launch": nbytes},
     }
     if cpu is not None:
         O, ref, kind, threads = cpu
         qh = q.float().cpu().numpy()
-        done_bytes, spent, seqs = 0.0, 0.0, 0
-        for b in range(B):
-            L = lengths[b]
-            keys = np.ascontiguousarray(kc[b, :, :L + 1].float().cpu().numpy().transpose(1, 0, 2))
-            vals = np.ascontiguousarray(vc[b, :, :L + 1].float().cpu().numpy().transpose(1, 0, 2))
-            o = np.zeros(H * D, np.float32)
-            t = time.perf_counter()
-            if ref is not None:
-                ref.ref_attention(np.ascontiguousarray(qh[b]).reshape(-1), keys.reshape(-1), vals.reshape(-1),
-                                  o, 1, L, H, KV, D, D, 0, 1)
-            else:
-                O.attention(qh[b:b + 1], keys, vals, 1, L, H, KV, D, D, nthreads=threads)
-            spent += time.perf_counter() - t
-            done_bytes += 2048.0 * (L + 1)
-            seqs += 1
-            if spent > args.cpu_seconds:
-                break
-        res["cpu_baseline"] = {"value": done_bytes / spent / 1e9, "unit": "GB/s", "cores": threads,
-                               "kind": kind,
+
+        def run(nthreads, budget):
+            cpu_threads(cpu, nthreads)
+            done_bytes, spent, seqs = 0.0, 0.0, 0
+            for b in range(B):
+                L = lengths[b]
+                keys = np.ascontiguousarray(kc[b, :, :L + 1].float().cpu().numpy().transpose(1, 0, 2))
+                vals = np.ascontiguousarray(vc[b, :, :L + 1].float().cpu().numpy().transpose(1, 0, 2))
+                o = np.zeros(H * D, np.float32)
+                t = time.perf_counter()
+                if ref is not None:
+                    ref.ref_attention(np.ascontiguousarray(qh[b]).reshape(-1), keys.reshape(-1),
+                                      vals.reshape(-1), o, 1, L, H, KV, D, D, 0, 1)
+                else:
+                    O.attention(qh[b:b + 1], keys, vals, 1, L, H, KV, D, D, nthreads=nthreads)
+                spent += time.perf_counter() - t
+                done_bytes += 2048.0 * (L + 1)
+                seqs += 1
+                if spent > budget:
+                    break
+            return done_bytes / spent / 1e9, seqs
+
+        value, seqs = run(threads, args.cpu_seconds)
+        single, seqs1 = run(1, args.cpu_seconds / 3)
+        cpu_threads(cpu, threads)
+        res["cpu_baseline"] = {"value": value, "unit": "GB/s", "cores": threads, "kind": kind,
+                               "cpu_model": cpu_model(),
+                               "single_core": {"value": single, "unit": "GB/s",
+                                               "sample": f"the first {seqs1} sequences on one thread"},
                                "sample": f"kernels::attention for {seqs} of the 32 sequences, one call each "
                                          f"(count=1, start=L_b) as the reference decodes, fp32 "
                                          f"position-major KV; GB/s on the same bf16 KV byte count"}
+    del kc, vc
+
+    # the same shape with every sequence at 32768 cached positions
+    Lu = 32768
+    kcu = randn((B, KV, Lu + 1, D), gen, torch.bfloat16)
+    vcu = randn((B, KV, Lu + 1, D), gen, torch.bfloat16)
+    posu = torch.full((B,), Lu, dtype=torch.int32, device="cuda")
+
+    def step_uniform():
+        aigpu.decode(q, k, v, out, kcu, vcu, posu, Lu, H, KV, D, q_norm=gq, k_norm=gk, freqs=fr, rotary_dims=D)
+
+    ubytes = 2048.0 * B * (Lu + 1)
+    u_step, u_k, _ = time_steps(step_uniform, args.steps, args.warmup, "decode_attention_kernel")
+    res["uniform_32k"] = {"workload": "B=32, every sequence at L=32768, 32q/4kv D=128 bf16 KV",
+                          "value": ubytes / (u_step * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": u_step,
+                          "step_frac": ubytes / (u_step * 1e-3) / 1e9 / PEAK_HBM,
+                          "kernel_ms": u_k, "kernel_frac": ubytes / (u_k * 1e-3) / 1e9 / PEAK_HBM,
+                          "kv_bytes": ubytes}
+    del kcu, vcu
     return res
 
 
@@ -296,18 +361,27 @@ def delta_workload(args, cpu):
         state.zero_()
         aigpu.gated_delta_rule(q, k, v, state, out, g=g, beta=beta)
 
-    nbytes = 543162368.0
+    # the step's algorithmic bytes: q, k, v (bf16), g and beta (fp32) in,
+    # out (fp32) and the final state out
+    nbytes = float(2 * S * HK * KD * 2 + S * HV * VD * 2 + 2 * S * HV * 4 + S * HV * VD * 4 + HV * KD * VD * 4)
+    # the scan's own: q, k, v in, out and the state out, the state in (the
+    # per-chunk records it reads are the solve's output, not the step's input)
+    scan_bytes = float(2 * S * HK * KD * 2 + S * HV * VD * 2 + S * HV * VD * 4 + 2 * HV * KD * VD * 4)
     step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "delta_scan_kernel")
     flops = S * HV * (7.0 * KD * VD + 4.0 * VD)
     res = {
         "workload": "configs[4] qwen3-next gated delta rule S=16384 16qk/32v heads D=128 chunk 64 bf16 in, fp32 state",
-        "dtype": "f32",
+        # products on bf16 MFMA, each fp32 operand split into a bf16 high and
+        # low part (three products), accumulated and kept in fp32
+        "dtype": "bf16x3",
         "value": nbytes / (step_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": step_ms,
         "recurrence_tflops": flops / (step_ms * 1e-3) / 1e12,
         "roofline": {"kernel": "delta_scan_kernel", "bound": "hbm",
-                     "achieved": nbytes / (launched_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
-                     "frac": nbytes / (launched_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
-                     "kernel_ms": k_ms, "all_kernels_ms": launched_ms, "bytes_per_step": nbytes},
+                     "achieved": scan_bytes / (k_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
+                     "frac": scan_bytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
+                     "kernel_ms": k_ms, "bytes_per_launch": scan_bytes,
+                     "all_kernels_ms": launched_ms, "all_kernels_frac": nbytes / (launched_ms * 1e-3) / 1e9 / PEAK_HBM,
+                     "bytes_per_step": nbytes},
     }
     if cpu is not None:
         # the whole workload: the mixer's token loop around the reference's own

@@ -25,7 +25,6 @@ enum ScratchSlot {
     SLOT_PREFILL_K,      // fp16 head-major k history of a prefill
     SLOT_PREFILL_V,      // fp16 head-major v history of a prefill
     SLOT_DECODE_PARTS,   // split-K partial softmax records
-    SLOT_DECODE_QUERIES, // prepared decode queries and new-token scores
     SLOT_DELTA_WORK,     // per-chunk solve products of the delta rule
     SLOT_LATENT,         // folded queries, contexts and split records of latent attention
     SLOT_MIXER_Q,        // fp32 q projection of a prefill mixer

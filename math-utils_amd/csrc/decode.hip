@@ -1,16 +1,18 @@
 // decode.hip - batched single-token GQA decode for gfx950, HBM-bound.
 //
-// Three launches:
-//   decode_prep_kernel       per (sequence b, kv head): QK-RMSNorm and RoPE at
-//                            position positions[b] for the G query heads and the
-//                            new k (attentionMixer, LocalModel.hpp:2608-2648),
-//                            the new k and v appended to the bf16 cache at
-//                            positions[b] (LocalModel.hpp:2650-2655), and q
-//                            written as the score MFMA's B operand;
+// Two launches:
 //   decode_attention_kernel  one persistent launch over a flattened work list of
 //                            (sequence, kv head, chunk of CH positions) items;
 //                            workgroup i takes items i, i + gridDim.x, ... so
-//                            ragged lengths leave no empty workgroups;
+//                            ragged lengths leave no empty workgroups. Each item
+//                            first prepares its query rows: QK-RMSNorm and RoPE
+//                            at position positions[b] for the G query heads
+//                            (attentionMixer, LocalModel.hpp:2608-2648), packed
+//                            as the score MFMA's B operand; the item holding
+//                            the sequence's last chunk also norms and rotates
+//                            the new k, appends the new k and v to the bf16
+//                            cache at positions[b] (LocalModel.hpp:2650-2655)
+//                            and scores the new token;
 //   decode_merge_kernel      combines the (m, l, acc) records of sequences that
 //                            span several chunks.
 // Per item, 4 waves split the chunk into slabs of 32 positions, software-
@@ -51,18 +53,12 @@ constexpr int MAXB = 1024;       // sequences per launch (larger batches are spl
 struct DecodeArgs {
     DecodeParams p;
     float* parts;                // [batch][kvHeads][maxChunks][RS]
-    uint32_t* qrec;              // [batch][kvHeads][QREC] prepared queries and new token
     uint32_t chunkLen;           // CH, a multiple of 4 * SLAB
     uint32_t maxChunks;
     float scaleLog2;
 };
 
 __host__ __device__ constexpr int record_floats(int D) { return 2 * MAXG + MAXG * D; }
-
-/* per (sequence, kv head), written by decode_prep_kernel: q as the score
-   MFMA's B operand (D/32 blocks x 64 lanes x 16 bytes), the new token's scores
-   snew[MAXG] and its value row vnew[D] in fp32 */
-__host__ __device__ constexpr int qrec_words(int D) { return (D / 32) * 64 * 4 + MAXG + D; }
 
 /* the attention output of (sequence b, head h, column d), times sigmoid of the
    gate half of its q row when the output gate is on (LocalModel.hpp:2660-2665) */
@@ -107,72 +103,6 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-/* Once per (sequence b, kv head): QK-RMSNorm and RoPE of the G query rows and
-   of the new key at position positions[b] (attentionMixer, LocalModel.hpp:
-   2608-2648), the new key and value appended to the bf16 cache
-   (LocalModel.hpp:2650-2655), the new token's scores, and q packed as the
-   score MFMA's B operand (bf16 high part in columns 0-7, residual in 8-15). */
-template <int D>
-__global__ __launch_bounds__(256) void decode_prep_kernel(DecodeArgs a) {
-    constexpr int DB = D / 32;
-    typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
-    const DecodeParams& p = a.p;
-    const uint32_t KVH = uint32_t(p.kvHeads), G = uint32_t(p.heads / p.kvHeads);
-    const uint32_t b = blockIdx.x / KVH, kvh = blockIdx.x % KVH;
-    const uint32_t L = p.positions[b];
-    if (L > p.maxPosition) return;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    __shared__ float rows[MAXG + 1][D];   // normed, rotated q rows (scaled) and the new key
-    const size_t cacheBase = size_t(b) * p.batchStride + size_t(kvh) * p.capacity * D;
-    uint32_t* rec = a.qrec + (size_t(b) * KVH + kvh) * qrec_words(D);
-    float* snew = reinterpret_cast<float*>(rec + DB * 64 * 4);
-    float* vnew = snew + MAXG;
-
-    for (uint32_t r = w; r <= G; r += 4) {
-        float* x = rows[r];
-        const bool isKey = r == G;
-        const size_t src = isKey ? (size_t(b) * p.kvHeads + kvh) * D
-                                 : (size_t(b) * p.heads + size_t(kvh) * G + r) * p.qStride;
-        for (int d = lane; d < D; d += WAVE) x[d] = load_elem(isKey ? p.k : p.q, src + d, p.inType);
-        wave_sync();
-        norm_rope_row(x, D, isKey ? p.kNorm : p.qNorm, p.eps, p.normOffset, p.freqs, p.rotaryDims, L, lane);
-        if (isKey) {
-            uint16_t* kdst = p.keyCache + cacheBase + size_t(L) * D;
-            uint16_t* vdst = p.valueCache + cacheBase + size_t(L) * D;
-            for (int d = lane; d < D; d += WAVE) {
-                kdst[d] = float_to_bf16_bits(x[d]);
-                const float vv = load_elem(p.v, (size_t(b) * p.kvHeads + kvh) * D + d, p.inType);
-                vdst[d] = float_to_bf16_bits(vv);
-                vnew[d] = vv;
-            }
-        } else {
-            for (int d = lane; d < D; d += WAVE) x[d] *= a.scaleLog2;
-        }
-        wave_sync();
-    }
-    __syncthreads();
-    for (uint32_t h = w; h < G; h += 4) {
-        float part = 0.0f;
-        for (int d = lane; d < D; d += WAVE) part += rows[h][d] * rows[G][d];
-        part = wave_sum(part);
-        if (lane == 0) snew[h] = part;
-    }
-    if (w == 0) {
-        const int g = lane >> 4, c16 = lane & 15;
-        const uint32_t h = c16 & 7;
-        const bool residual = c16 >= 8;
-        for (int db = 0; db < DB; ++db) {
-            u16x8 bits;
-            for (int s = 0; s < 8; ++s) {
-                const float x = h < G ? rows[h][32 * db + 8 * g + s] : 0.0f;
-                const uint16_t top = float_to_bf16_bits(x);
-                bits[s] = residual ? float_to_bf16_bits(x - bf16_bits_to_float(top)) : top;
-            }
-            reinterpret_cast<u32x4*>(rec)[db * 64 + lane] = __builtin_bit_cast(u32x4, bits);
-        }
-    }
-}
-
 template <int D>
 __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) {
     constexpr int DB = D / 32;   // 32-deep d blocks of the score MFMA
@@ -193,6 +123,8 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) 
 
     __shared__ uint32_t pre[MAXB + 1];
     __shared__ float wm[4][MAXG], wl[4][MAXG];
+    __shared__ float rows[MAXG + 1][D];           // normed, rotated q rows (scaled) and the new key
+    __shared__ float snew[MAXG], vnew[D];         // the new token's scores and value
     __shared__ __attribute__((aligned(16))) uint16_t vbuf[4 * 2 * VSLAB];   // per-wave V slabs (x2)
 
     // ---- chunk counts -> prefix over the batch (the work list) ----
@@ -218,18 +150,30 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) 
         }
     }
     __syncthreads();
+    // items in (sequence, kv head, chunk) order, chunk fastest; workgroup i
+    // takes a contiguous run of them, so consecutive items mostly share a
+    // (sequence, kv head) and its prepared queries
     const uint32_t items = pre[B] * KVH;
+    const uint32_t perWg = items / gridDim.x, extra = items % gridDim.x;
+    const uint32_t itBegin = blockIdx.x * perWg + (blockIdx.x < extra ? blockIdx.x : extra);
+    const uint32_t itEnd = itBegin + perWg + (blockIdx.x < extra ? 1u : 0u);
     uint16_t* vw = vbuf + w * (2 * VSLAB);
+    uint32_t preparedPair = 0xFFFFFFFFu;
+    bf16x8 qb[DB];   // the prepared (sequence, kv head)'s queries as the score B operand
 
-    for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
-        const uint32_t kvh = item % KVH, j = item / KVH;
-        uint32_t lo_b = 0, hi_b = B;   // pre[lo_b] <= j < pre[hi_b]
+    for (uint32_t item = itBegin; item < itEnd; ++item) {
+        const uint32_t j = item / KVH;   // pre[b] <= j < pre[b + 1] for item's sequence b
+        uint32_t lo_b = 0, hi_b = B;
         while (hi_b - lo_b > 1) {
             const uint32_t mid = (lo_b + hi_b) / 2;
             if (pre[mid] <= j) lo_b = mid;
             else hi_b = mid;
         }
-        const uint32_t b = lo_b, chunk = j - pre[b], nChunks = pre[b + 1] - pre[b];
+        const uint32_t b = lo_b, nChunks = pre[b + 1] - pre[b];
+        const uint32_t local = item - KVH * pre[b];
+        const uint32_t kvh = local / nChunks, chunk = local % nChunks;
+        const bool samePair = b * KVH + kvh == preparedPair;
+        preparedPair = b * KVH + kvh;
         const uint32_t L = p.positions[b];
         const uint32_t first = first_position(p, L);
         const uint32_t lo = first + chunk * a.chunkLen;
@@ -243,8 +187,8 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) 
 
         // a slab's loads: K rows into registers as MFMA A operands (row =
         // lane % 16); V rows straight into LDS slab `half` by DMA, 1 KB per
-        // instruction, each lane's 16-byte column block XOR-swizzled by its row
-        // so the transposed reads below are bank-conflict free
+        // instruction, each lane's 16-byte column block XOR-swizzled by its
+        // row so the transposed reads below are bank-conflict free
         auto issue = [&](uint32_t p0, u32x4 (&kr)[2][DB], int half) {
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
@@ -270,20 +214,120 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) 
 
         __syncthreads();   // LDS of the previous item is free
 
-        // this wave's first slab is requested before the queries are prepared
+        // ---- this item's query rows, QK-RMSNorm and RoPE at position L
+        //      (attentionMixer, LocalModel.hpp:2608-2648), scaled by
+        //      log2(e)/sqrt(D); the item with the new token also prepares the
+        //      new key (row G) and appends it and the new value to the cache
+        //      (LocalModel.hpp:2650-2655). The rows are requested before the
+        //      first slab, so they arrive first and their preparation runs
+        //      while the slab is in flight ----
+        constexpr int EPL = D / WAVE;   // elements per lane of one row
+        const uint32_t firstRow = samePair ? G : 0u;   // rows < G are still prepared
+        const uint32_t nRows = G + (hasNew ? 1u : 0u);
+        float xin[3][EPL], vin[EPL];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const uint32_t r = w + 4 * i;
+            if (r >= firstRow && r < nRows) {
+                const bool isKey = r == G;
+                const size_t src = isKey ? (size_t(b) * p.kvHeads + kvh) * D
+                                         : (size_t(b) * p.heads + size_t(kvh) * G + r) * p.qStride;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) xin[i][e] = load_elem(isKey ? p.k : p.q, src + lane + WAVE * e, p.inType);
+                if (isKey) {
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) vin[e] = load_elem(p.v, src + lane + WAVE * e, p.inType);
+                }
+            }
+        }
+
+        // the first two slabs go out before the preparation too, so the
+        // pipeline is full while it runs
         u32x4 krA[2][DB], krB[2][DB];
         uint32_t pA = lo + SLAB * w;
         if (pA < cachedHi) issue(pA, krA, 0);
+        if (pA + 4 * SLAB < cachedHi) issue(pA + 4 * SLAB, krB, 1);
         __builtin_amdgcn_sched_barrier(0);
 
-        // ---- the prepared q operand (written by decode_prep_kernel) ----
-        const uint32_t* qr = a.qrec + (size_t(b) * KVH + kvh) * qrec_words(D);
-        bf16x8 qb[DB];
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
-            qb[db] = __builtin_bit_cast(bf16x8, reinterpret_cast<const u32x4*>(qr)[db * 64 + lane]);
-        const float* snewG = reinterpret_cast<const float*>(qr + DB * 64 * 4);
-        const float* vnewG = snewG + MAXG;
+        for (int i = 0; i < 3; ++i) {
+            const uint32_t r = w + 4 * i;
+            if (r >= firstRow && r < nRows) {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) rows[r][lane + WAVE * e] = xin[i][e];
+            }
+        }
+        wave_sync();
+        // the rotation at position L, lane j < rotaryDims / 2 holding pair
+        // (j, j + rotaryDims / 2): shared by every row of the item
+        const int half = p.freqs ? p.rotaryDims / 2 : 0;
+        float rc = 1.0f, rs = 0.0f;
+        if (lane < half && firstRow < nRows) sincosf(float(L) * p.freqs[lane], &rs, &rc);
+        const uint32_t rowStart = w >= firstRow ? w : w + 4 * ((firstRow - w + 3) / 4);
+#pragma unroll 1
+        for (uint32_t r = rowStart; r < nRows; r += 4) {
+            const bool isKey = r == G;
+            float* x = rows[r];
+            const float* gamma = isKey ? p.kNorm : p.qNorm;
+            if (gamma) {   // rmsNormRow (LocalModel.hpp:1341-1348)
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) ss += x[lane + WAVE * e] * x[lane + WAVE * e];
+                const float inv = 1.0f / sqrtf(wave_sum(ss) / float(D) + p.eps);
+#pragma unroll
+                for (int e = 0; e < EPL; ++e)
+                    x[lane + WAVE * e] = x[lane + WAVE * e] * inv * (gamma[lane + WAVE * e] + p.normOffset);
+                wave_sync();
+            }
+            if (lane < half) {   // rotate-half pairs (LocalModel.hpp:2624-2641)
+                const float u = x[lane], v = x[lane + half];
+                x[lane] = u * rc - v * rs;
+                x[lane + half] = v * rc + u * rs;
+            }
+            wave_sync();
+            if (isKey) {
+                uint16_t* kdst = p.keyCache + cacheBase + size_t(L) * D;
+                uint16_t* vdst = p.valueCache + cacheBase + size_t(L) * D;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const int d = lane + WAVE * e;
+                    kdst[d] = float_to_bf16_bits(x[d]);
+                    vdst[d] = float_to_bf16_bits(vin[e]);
+                    vnew[d] = vin[e];
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) x[lane + WAVE * e] *= a.scaleLog2;
+            }
+            wave_sync();
+        }
+        __syncthreads();
+        if (hasNew) {   // the new token's scores, one head per wave
+            for (uint32_t h = w; h < G; h += 4) {
+                float part = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) part += rows[h][lane + WAVE * e] * rows[G][lane + WAVE * e];
+                part = wave_sum(part);
+                if (lane == 0) snew[h] = part;
+            }
+        }
+        // q as the B operand: column j < 8 is head j's bf16 high part, column
+        // 8 + j its residual; lane group g holds d = 32 db + 8 g + 0..7
+        if (!samePair) {
+            const uint32_t h = c16 & 7;
+            const bool residual = c16 >= 8;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                u16x8 bits;
+#pragma unroll
+                for (int s8 = 0; s8 < 8; ++s8) {
+                    const float x = h < G ? rows[h][32 * db + 8 * g + s8] : 0.0f;
+                    const uint16_t top = float_to_bf16_bits(x);
+                    bits[s8] = residual ? float_to_bf16_bits(x - bf16_bits_to_float(top)) : top;
+                }
+                qb[db] = __builtin_bit_cast(bf16x8, bits);
+            }
+        }
 
         float m = -INFINITY, lsum = 0.0f;   // per lane: head c16 & 7
         floatx4 acc[CT];                    // rows 0-7: P_hi.V, rows 8-15: P_lo.V
@@ -371,9 +415,11 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) 
 
         // ---- slabs, software-pipelined: the next slab's loads are in flight
         //      while the current one computes (two register/LDS buffers) ----
+        bool bIssued = true;   // the first slab B went out with slab A
         while (pA < cachedHi) {
             const uint32_t pB = pA + 4 * SLAB;
-            if (pB < cachedHi) issue(pB, krB, 1);
+            if (pB < cachedHi && !bIssued) issue(pB, krB, 1);
+            bIssued = false;
             __builtin_amdgcn_sched_barrier(0);
             compute(pA, krA, 0, pB < cachedHi);
             if (pB >= cachedHi) break;
@@ -407,7 +453,7 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) 
         float* outRow = p.out + (size_t(b) * p.heads + size_t(kvh) * G) * D;
         for (uint32_t idx = tid; idx < G * D; idx += 256) {
             const uint32_t h = idx / D, d = idx % D;
-            const float sn = hasNew ? snewG[h] : -INFINITY;
+            const float sn = hasNew ? snew[h] : -INFINITY;
             float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
             M = fmaxf(M, sn);
             float lt = 0.0f, at = 0.0f;
@@ -421,7 +467,7 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) 
             if (hasNew) {
                 const float f = exp2f(sn - M);
                 lt += f;
-                at += f * vnewG[d];
+                at += f * vnew[d];
             }
             if (nChunks == 1) {
                 outRow[h * D + d] = gated(p, b, kvh * G + h, d, at / lt);
@@ -443,69 +489,54 @@ __global__ __launch_bounds__(256, 2) void decode_attention_kernel(DecodeArgs a) 
     }
 }
 
-/* combines the chunk records of every (sequence, kv head) with more than one
-   chunk; one workgroup per (sequence, kv head). The per-chunk weights
-   exp2(m_c - M) are staged in LDS so the accumulator loads are independent. */
+/* combines the chunk records of every (sequence, query head) whose sequence
+   spans more than one chunk (the split-K algebra of Kernels.metal:318-345);
+   one workgroup of D threads per (sequence, kv head, head of the group),
+   thread d owning output column d. A tile of chunks is read at once (the
+   chunk's m and l are the same address across the workgroup, the
+   accumulators contiguous across it), all its loads independent, so a tile
+   costs one memory round trip; the running sums are rescaled to each tile's
+   new maximum. */
 template <int D>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(D) void decode_merge_kernel(DecodeArgs a) {
     constexpr int RS = record_floats(D);
-    constexpr int TILE = 256;   // chunks whose weights sit in LDS at once
-    __shared__ float wts[TILE][MAXG];
-    __shared__ float Mh[MAXG], Lh[MAXG];
+    constexpr int TILE = 16;
     const DecodeParams& p = a.p;
     const uint32_t KVH = uint32_t(p.kvHeads), G = uint32_t(p.heads / p.kvHeads);
-    const uint32_t b = blockIdx.x / KVH, kvh = blockIdx.x % KVH;
+    const uint32_t pair = blockIdx.x / G, h = blockIdx.x % G;
+    const uint32_t b = pair / KVH, kvh = pair % KVH;
     const uint32_t L = p.positions[b];
     if (L > p.maxPosition) return;
     const uint32_t nChunks = (L + 1 - first_position(p, L) + a.chunkLen - 1) / a.chunkLen;
     if (nChunks < 2) return;   // written by the attention kernel itself
-    const float* recs = a.parts + (size_t(b) * KVH + kvh) * a.maxChunks * RS;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-
-    for (uint32_t h = w; h < G; h += 4) {   // per head: max, then weighted sum of l
-        float mx = -INFINITY;
-        for (uint32_t c = lane; c < nChunks; c += WAVE) mx = fmaxf(mx, recs[size_t(c) * RS + h]);
-        mx = wave_max(mx);
-        float lt = 0.0f;
-        for (uint32_t c = lane; c < nChunks; c += WAVE) {
-            const float* r = recs + size_t(c) * RS;
-            lt += r[MAXG + h] * exp2f(r[h] - mx);
-        }
-        lt = wave_sum(lt);
-        if (lane == 0) {
-            Mh[h] = mx;
-            Lh[h] = lt;
-        }
-    }
-    __syncthreads();
-
-    float acc[(MAXG * D + 255) / 256] = {};
+    const float* recs = a.parts + size_t(pair) * a.maxChunks * RS;
+    const uint32_t d = threadIdx.x;
+    float M = -INFINITY, lt = 0.0f, at = 0.0f;
     for (uint32_t c0 = 0; c0 < nChunks; c0 += TILE) {
-        const uint32_t nc = nChunks - c0 < TILE ? nChunks - c0 : TILE;
-        __syncthreads();
-        for (uint32_t idx = tid; idx < nc * G; idx += 256) {
-            const uint32_t c = idx / G, h = idx % G;
-            wts[c][h] = exp2f(recs[size_t(c0 + c) * RS + h] - Mh[h]);
-        }
-        __syncthreads();
+        float mc[TILE], lc[TILE], ac[TILE];
 #pragma unroll
-        for (int k = 0; k < (MAXG * D + 255) / 256; ++k) {
-            const uint32_t idx = tid + 256 * k;
-            if (idx >= G * D) break;
-            const uint32_t h = idx / D;
-            const float* col = recs + size_t(c0) * RS + 2 * MAXG + idx;
-            float s = 0.0f;
-#pragma unroll 8
-            for (uint32_t c = 0; c < nc; ++c) s += col[size_t(c) * RS] * wts[c][h];
-            acc[k] += s;
+        for (int c = 0; c < TILE; ++c) {
+            const bool in = c0 + c < nChunks;
+            const float* r = recs + size_t(in ? c0 + c : c0) * RS;
+            mc[c] = in ? r[h] : -INFINITY;
+            lc[c] = r[MAXG + h];
+            ac[c] = r[2 * MAXG + h * D + d];
         }
-    }
-    float* outRow = p.out + (size_t(b) * p.heads + size_t(kvh) * G) * D;
+        float mt = M;
 #pragma unroll
-    for (int k = 0; k < (MAXG * D + 255) / 256; ++k) {
-        const uint32_t idx = tid + 256 * k;
-        if (idx < G * D) outRow[idx] = gated(p, b, kvh * G + idx / D, idx % D, acc[k] / Lh[idx / D]);
+        for (int c = 0; c < TILE; ++c) mt = fmaxf(mt, mc[c]);
+        const float scale = M == -INFINITY ? 0.0f : exp2f(M - mt);
+        lt *= scale;
+        at *= scale;
+#pragma unroll
+        for (int c = 0; c < TILE; ++c) {
+            const float f = mc[c] == -INFINITY ? 0.0f : exp2f(mc[c] - mt);
+            lt += lc[c] * f;
+            at += ac[c] * f;
+        }
+        M = mt;
     }
+    p.out[(size_t(b) * p.heads + size_t(kvh) * G + h) * D + d] = gated(p, b, kvh * G + h, d, at / lt);
 }
 
 uint32_t env_u32(const char* name, uint32_t fallback) {
@@ -579,33 +610,27 @@ bool launch_decode(const DecodeParams& p, hipStream_t stream, const FixedScratch
         return len;
     };
     const size_t rs = size_t(record_floats(int(p.dim)));
-    const size_t qwords = size_t(qrec_words(int(p.dim)));
     uint64_t slice = p.batch < MAXB ? p.batch : MAXB;
     uint32_t chunkLen = chunk_for(slice);
     uint32_t maxChunks = (p.maxPosition + 1 + chunkLen - 1) / chunkLen;
     auto parts_bytes = [&] { return (slice * p.kvHeads * maxChunks * rs * sizeof(float) + 255) & ~size_t(255); };
-    auto qrec_bytes = [&] { return slice * p.kvHeads * qwords * 4; };
     float* parts = nullptr;
-    uint32_t* qrec = nullptr;
     if (fixed) {
         // the records of a slice of sequences must fit the fixed scratch:
         // halve the slice until they do
-        while (slice > 1 && parts_bytes() + qrec_bytes() > fixed->bytes) {
+        while (slice > 1 && parts_bytes() > fixed->bytes) {
             slice = (slice + 1) / 2;
             chunkLen = chunk_for(slice);
             maxChunks = (p.maxPosition + 1 + chunkLen - 1) / chunkLen;
         }
-        if (parts_bytes() + qrec_bytes() > fixed->bytes)
+        if (parts_bytes() > fixed->bytes)
             return ctx.fail("decode (no allocation): one sequence's split-K records need " +
-                            std::to_string(parts_bytes() + qrec_bytes()) + " bytes, above the fixed scratch of " +
+                            std::to_string(parts_bytes()) + " bytes, above the fixed scratch of " +
                             std::to_string(fixed->bytes));
         parts = static_cast<float*>(fixed->base);
-        qrec = reinterpret_cast<uint32_t*>(static_cast<char*>(fixed->base) + parts_bytes());
     } else {
         parts = static_cast<float*>(ctx.grow(SLOT_DECODE_PARTS, parts_bytes()));
         if (!parts) return false;
-        qrec = static_cast<uint32_t*>(ctx.grow(SLOT_DECODE_QUERIES, qrec_bytes()));
-        if (!qrec) return false;
     }
 
     const uint64_t batchStride = p.batchStride ? p.batchStride : p.kvHeads * p.capacity * p.dim;
@@ -623,27 +648,22 @@ bool launch_decode(const DecodeParams& p, hipStream_t stream, const FixedScratch
         a.p.valueCache = p.valueCache + b0 * batchStride;
         a.p.positions = p.positions + b0;
         a.parts = parts;
-        a.qrec = qrec;
         a.chunkLen = chunkLen;
         a.maxChunks = maxChunks;
         a.scaleLog2 = LOG2E / sqrtf(float(p.dim));
         const uint64_t upper = a.p.batch * p.kvHeads * maxChunks;
         const unsigned grid = unsigned(upper < gridEnv ? upper : gridEnv);
-        const unsigned mgrid = unsigned(a.p.batch * p.kvHeads);
+        const unsigned mgrid = unsigned(a.p.batch * p.heads);   // one merge workgroup per query head
         const bool ok = p.dim == 128
-            ? ctx.launch("decode_prep_kernel", stream, [&] {
-                  hipLaunchKernelGGL(decode_prep_kernel<128>, dim3(mgrid), dim3(256), 0, stream, a);
-              }) && ctx.launch("decode_attention_kernel", stream, [&] {
+            ? ctx.launch("decode_attention_kernel", stream, [&] {
                   hipLaunchKernelGGL(decode_attention_kernel<128>, dim3(grid), dim3(256), 0, stream, a);
               }) && (maxChunks < 2 || ctx.launch("decode_merge_kernel", stream, [&] {
-                  hipLaunchKernelGGL(decode_merge_kernel<128>, dim3(mgrid), dim3(256), 0, stream, a);
+                  hipLaunchKernelGGL(decode_merge_kernel<128>, dim3(mgrid), dim3(128), 0, stream, a);
               }))
-            : ctx.launch("decode_prep_kernel", stream, [&] {
-                  hipLaunchKernelGGL(decode_prep_kernel<64>, dim3(mgrid), dim3(256), 0, stream, a);
-              }) && ctx.launch("decode_attention_kernel", stream, [&] {
+            : ctx.launch("decode_attention_kernel", stream, [&] {
                   hipLaunchKernelGGL(decode_attention_kernel<64>, dim3(grid), dim3(256), 0, stream, a);
               }) && (maxChunks < 2 || ctx.launch("decode_merge_kernel", stream, [&] {
-                  hipLaunchKernelGGL(decode_merge_kernel<64>, dim3(mgrid), dim3(256), 0, stream, a);
+                  hipLaunchKernelGGL(decode_merge_kernel<64>, dim3(mgrid), dim3(64), 0, stream, a);
               }));
         if (!ok) return false;
     }
