@@ -25,6 +25,7 @@
 // per layer (what aigpu_dense_create copies in and aigpu_dense_read_cache
 // copies out).
 #include <chrono>
+#include <cstdlib>
 #include <cmath>
 #include <cstring>
 #include <initializer_list>
@@ -545,6 +546,15 @@ struct DevLayer {
     uint32_t window = 0;
 };
 
+/* one captured decode step: the step's kernels for a given attention grid,
+   replayed as a HIP graph (the kernels read the position from device memory,
+   so one capture serves every position with the same grid) */
+struct StepGraph {
+    uint32_t splits = 0;
+    hipGraphExec_t exec = nullptr;
+    uint64_t launches = 0;   // kernels per replay
+};
+
 struct DenseModel {
     AiGpuDenseConfig cfg{};
     uint32_t length = 0, maxSplits = 0;
@@ -556,8 +566,15 @@ struct DenseModel {
     uint32_t* pos = nullptr;
     std::vector<void*> owned;
     uint64_t bytes = 0;
+    // the decoder's own stream (blocking: ordered after the legacy default
+    // stream, where callers upload weights) and its captured steps
+    hipStream_t stream = nullptr;
+    std::vector<StepGraph> graphs;
 
     ~DenseModel() {
+        for (StepGraph& g : graphs)
+            if (g.exec) (void)hipGraphExecDestroy(g.exec);
+        if (stream) (void)hipStreamDestroy(stream);
         for (void* ptr : owned) (void)hipFree(ptr);
         Context::instance().allocated -= bytes;
     }
@@ -701,6 +718,53 @@ bool run_step(DenseModel& d, uint32_t splits, hipStream_t stream) {
     return dense_gemv({{&d.head, d.logits}}, d.x, nullptr, d.finalNorm, c.epsilon, 1, false, stream);
 }
 
+/* the step for `splits`, as a replayed graph: captured on first use of each
+   attention grid (the grid grows by one workgroup per kv head every 128
+   positions up to 64, so a sequence captures at most 64 graphs). Without
+   graphs (AIGPU_DENSE_GRAPH=0, or profiling, whose per-launch events a graph
+   cannot carry) the kernels are launched one by one. */
+bool launch_step(DenseModel& d, uint32_t splits) {
+    Context& ctx = Context::instance();
+    const char* env = std::getenv("AIGPU_DENSE_GRAPH");
+    if (ctx.profiling || (env && std::atoi(env) == 0)) return run_step(d, splits, d.stream);
+    StepGraph* g = nullptr;
+    for (StepGraph& x : d.graphs)
+        if (x.splits == splits) g = &x;
+    if (!g) {
+        const uint64_t before = ctx.stats.launches;
+        if (hipStreamBeginCapture(d.stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+            (void)hipGetLastError();
+            return ctx.fail("resident decode: graph capture could not begin");
+        }
+        const bool ok = run_step(d, splits, d.stream);
+        hipGraph_t graph = nullptr;
+        const hipError_t e = hipStreamEndCapture(d.stream, &graph);
+        if (!ok || e != hipSuccess || !graph) {
+            (void)hipGetLastError();
+            if (graph) (void)hipGraphDestroy(graph);
+            return ok ? ctx.fail("resident decode: graph capture failed") : false;
+        }
+        StepGraph fresh;
+        fresh.splits = splits;
+        fresh.launches = ctx.stats.launches - before;
+        const hipError_t ie = hipGraphInstantiate(&fresh.exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (ie != hipSuccess) {
+            (void)hipGetLastError();
+            return ctx.fail(std::string("resident decode: graph instantiation failed: ") + hipGetErrorString(ie));
+        }
+        ctx.stats.launches = before;   // counted per replay below
+        d.graphs.push_back(fresh);
+        g = &d.graphs.back();
+    }
+    if (hipGraphLaunch(g->exec, d.stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return ctx.fail("resident decode: graph launch failed");
+    }
+    ctx.stats.launches += g->launches;
+    return true;
+}
+
 } // namespace
 } // namespace aigpu
 
@@ -757,6 +821,10 @@ AIGPU_ABI void* aigpu_dense_create(const AiGpuDenseConfig* c, const AiGpuDenseLa
         d->maxSplits = aigpu::host_splits(c->capacity - 1, 0);
         d->partial = d->floats(uint64_t(c->heads) * d->maxSplits * (c->headDim + aigpu::REC_PAD));
         d->pos = reinterpret_cast<uint32_t*>(d->floats(1));
+        if (hipStreamCreate(&d->stream) != hipSuccess) {
+            (void)hipGetLastError();
+            throw std::runtime_error("resident decoder stream creation failed");
+        }
         for (uint32_t i = 0; i < c->layers; ++i) {
             const AiGpuDenseLayer& l = layers[i];
             if (!l.inputNorm || !l.postNorm || !keys[i] || !values[i])
@@ -814,7 +882,7 @@ AIGPU_ABI void aigpu_dense_decode(void* handle, const float* embedding, float* l
         ctx.error = "resident decode position does not match KV cache";
         return;
     }
-    const hipStream_t stream = nullptr;
+    const hipStream_t stream = d.stream;
     const auto mark = std::chrono::steady_clock::now();
     if (hipMemcpyAsync(d.x, embedding, size_t(c.hidden) * 4, hipMemcpyHostToDevice, stream) != hipSuccess ||
         hipMemcpyAsync(d.pos, &position, 4, hipMemcpyHostToDevice, stream) != hipSuccess) {
@@ -828,7 +896,7 @@ AIGPU_ABI void aigpu_dense_decode(void* handle, const float* embedding, float* l
         const uint32_t s = aigpu::host_splits(position, L.window);
         if (s > splits) splits = s;
     }
-    if (!aigpu::run_step(d, splits, stream)) return;
+    if (!aigpu::launch_step(d, splits)) return;
     if (hipMemcpyAsync(logits, d.logits, size_t(c.vocab) * 4, hipMemcpyDeviceToHost, stream) != hipSuccess ||
         hipStreamSynchronize(stream) != hipSuccess) {
         ctx.error = std::string("resident decode failed: ") + hipGetErrorString(hipGetLastError());

@@ -173,3 +173,41 @@ def test_rejects_bad_config(gpu):
     L = aigpu.lib()
     assert not L.aigpu_dense_create(c, None, None, None, 0)
     assert "configuration" in aigpu.last_error()
+
+
+def test_graph_replay_matches_launches_one_by_one(gpu, monkeypatch):
+    """the step replayed as a captured HIP graph (the default) gives the same
+    logits, bit for bit, as the same kernels launched one by one
+    (AIGPU_DENSE_GRAPH=0), step after step across a change of the attention
+    grid at position 256 (a second capture), with other GPU work and
+    synchronisations between the replays; the caches agree too"""
+    import torch
+    cfg = dict(hidden=256, heads=4, kv_heads=2, head_dim=64, intermediate=512, vocab=777, capacity=270,
+               rotary_dims=64, eps=1e-6, theta=1e6)
+    m = Model(gpu, cfg, "bf16", 9)
+    rng = np.random.default_rng(77)
+    length, steps = 250, 10
+    keys = [rng.standard_normal((270, 128)).astype(np.float32) for _ in range(2)]
+    values = [rng.standard_normal((270, 128)).astype(np.float32) for _ in range(2)]
+    embs = [rng.standard_normal(256).astype(np.float32) for _ in range(steps)]
+    say("dense graph replay", dict(length=length, steps=steps))
+    graph = gpu.DenseDecoder(cfg, m.dev_layers, m.dev_head, m.final_norm, keys, values, length)
+    eager = gpu.DenseDecoder(cfg, m.dev_layers, m.dev_head, m.final_norm, keys, values, length)
+    try:
+        noise = torch.ones(1 << 20, device="cuda")
+        for t in range(steps):
+            monkeypatch.delenv("AIGPU_DENSE_GRAPH", raising=False)
+            got = graph.decode(embs[t], length + t)
+            noise.mul_(1.0001).sum().item()   # eager work and a synchronisation between replays
+            monkeypatch.setenv("AIGPU_DENSE_GRAPH", "0")
+            want = eager.decode(embs[t], length + t)
+            assert np.array_equal(got, want), f"step {t}: graph and launches differ"
+        gk, gv = graph.read_cache(length + steps)
+        ek, ev = eager.read_cache(length + steps)
+        for a, b in zip(gk + gv, ek + ev):
+            assert np.array_equal(a, b)
+    finally:
+        monkeypatch.delenv("AIGPU_DENSE_GRAPH", raising=False)
+        graph.close()
+        eager.close()
+        m.release()
