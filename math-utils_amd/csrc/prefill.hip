@@ -19,8 +19,7 @@
 // flag and the entry point fails instead of returning inf / NaN.
 //
 // Flash kernel layout (one workgroup = 8 waves = 256 query rows of one head,
-// one wave = 32 rows; key tiles of 128, DMA'd into LDS, K and V each double
-// buffered):
+// one wave = 32 rows; key tiles of 128, DMA'd into LDS):
 //   S^T = K Q^T     A = K rows (LDS), B = Q^T (registers, loaded once, already
 //                   scaled by log2(e)/sqrt(D) so the softmax is exp2 of it)
 //                   -> each lane owns one query (lane % 32) and 16 keys, so
@@ -34,12 +33,13 @@
 //
 // Ping-pong schedule (the default for D = 128): waves 0-3 and 4-7 share the
 // four SIMDs pairwise and run a tile interval apart, so while one wave of a
-// pair issues MFMAs (PV of the previous tile, then QK of this one) its
-// partner runs the softmax on the VALU; waves 4-7 also issue the next
-// tiles' DMA between their softmax steps. The running max is folded into the
-// score accumulators' initial value and rescaling is lazy (only when the max
-// grows by more than 8 in log2 units). AIGPU_PREFILL_PP=0 selects the
-// single-phase loop.
+// pair issues MFMAs (PV of the previous tile, then QK of this one, at a
+// raised wave priority) its partner runs the softmax on the VALU; each group
+// issues DMA between its softmax steps (waves 4-7 the next K tile, waves 0-3
+// the next V tile; K is double- and V triple-buffered, 160 KB of LDS). The
+// running max is folded into the score accumulators' initial value and
+// rescaling is lazy (only when the max grows by more than 8 in log2 units).
+// AIGPU_PREFILL_PP=0 selects the single-phase loop.
 #include "context.hpp"
 #include "device.hpp"
 #include "kernels.hpp"
@@ -506,6 +506,9 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     // immediate; K needs one lane address per stage
     __shared__ __attribute__((aligned(16))) _Float16 V0[TILE], V1[TILE], V2[TILE], V3[TILE];
     __shared__ __attribute__((aligned(16))) _Float16 K0[TILE], K1[TILE], K2[TILE], K3[TILE];
+    // the ping-pong loop's three V stages, indexed at run time (its DMA is
+    // issued and waited for explicitly, so no stage needs its own object)
+    __shared__ __attribute__((aligned(16))) _Float16 VP[3 * TILE];
     auto kbuf = [&](auto j) __attribute__((always_inline)) -> _Float16* {
         if constexpr (decltype(j)::value == 0) return K0;
         else if constexpr (decltype(j)::value == 1) return K1;
@@ -817,12 +820,17 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
             them feeds the matrix core while the other runs the softmax on
             the VALU.
 
-            K and V are double-buffered by tile parity. In the intervals where
-            it runs the softmax, group 1 DMAs the K tile one ahead of the one
-            group 0 reads next and the V tile group 0 will need two intervals
-            later; it waits for that DMA before the barrier ending the
-            following interval, the last point before group 0 reads it. Each
-            stage a DMA refills was last read in the interval before.
+            K is double-buffered by tile parity and V triple-buffered (tile j
+            in stage j mod 3), 160 KB in all, so that the DMA splits evenly
+            between the groups' softmax phases, the only phases that can
+            absorb the ~2,100 cycles a 64 KB tile takes on the CU's memory
+            path: in interval A_j (group 0 MFMA on tile j, group 1 softmax of
+            j - 1) group 1 DMAs K tile j + 1, which it waits for at the end of
+            B_j, the last point before group 0 reads it; in interval B_j
+            (group 0 softmax of j, group 1 MFMA on j) group 0 DMAs V tile
+            j + 1, needed from A_{j+2} on, and waits for it at the end of
+            B_{j+1}. Each stage a DMA refills was last read in the interval
+            before (K) or two intervals before (V).
         */
         const int grp = w >> 2, wq = w & 3;
         constexpr int PB = NBLK / 4;   // DMA blocks per issuing wave per tile (K or V)
@@ -847,9 +855,9 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         // row reads the next head's rows, or the zeroed pad rows after the
         // last head; the causal mask drops those keys (their finite values
         // meet P = 0).
-        auto dma_rows = [&](uint32_t k0, auto J, bool isK, auto N0, auto N1) __attribute__((always_inline)) {
+        auto dma_rows = [&](uint32_t k0, uint32_t stage, bool isK, auto N0, auto N1) __attribute__((always_inline)) {
             constexpr int n0 = decltype(N0)::value, n1 = decltype(N1)::value;
-            const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_address(isK ? kbuf(J) : vbuf(J)) + ldsWave);
+            const uint32_t lds = __builtin_amdgcn_readfirstlane(stage + ldsWave);
             const char* src = reinterpret_cast<const char*>((isK ? kbase : vbase) + size_t(k0) * D);
             // fresh each call: the offsets are not worth registers across the loop
 #pragma unroll
@@ -872,8 +880,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         // The scheduling groups pin that order (the default schedule waits
         // for every read just before its product).
         constexpr int AHEAD_PP = 3;
-        auto pv_pp = [&](auto J, const half8 (&pk)[NKB][2]) __attribute__((always_inline)) {
-            const _Float16* vs = vbuf(J);
+        auto pv_pp = [&](const _Float16* vs, const half8 (&pk)[NKB][2]) __attribute__((always_inline)) {
             constexpr int N = NKB * 2 * DT;   // products: (kb, h) outer, dt inner
             auto frag = [&](int i) __attribute__((always_inline)) {
                 const int dt = i % DT, hh = (i / DT) % 2, kb = i / (2 * DT);
@@ -936,8 +943,13 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         floatx16 s[NKB];
         half8 pk[NKB][2];
         bool haveP = false, haveS = false;
-        // MFMA phase of tile j: P.V of tile j - 1 (V stage VS), S of tile j (K stage KS)
-        auto mphase = [&](uint32_t j, auto KS, auto VS) __attribute__((always_inline)) {
+        // MFMA phase of tile j: P.V of tile j - 1 (V stage vs), S of tile j (K
+        // stage KS). The wave runs it at a raised priority: the SIMD then
+        // issues its LDS reads and MFMAs ahead of the partner wave's softmax
+        // (without it the younger group's MFMA phase ran a third longer than
+        // the older group's, 3,380 against 2,770 cycles per interval)
+        auto mphase = [&](uint32_t j, auto KS, const _Float16* vs) __attribute__((always_inline)) {
+            __builtin_amdgcn_s_setprio(3);
             haveS = active(j);
             if (haveS) {   // S starts at -base (the registers are free: P holds the last tile)
                 const float nb = m == -INFINITY ? 0.0f : -m;
@@ -947,26 +959,20 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                     for (int r = 0; r < 16; ++r) s[kb][r] = nb;
             }
             if (haveP) {
-                pv_pp(VS, pk);
+                pv_pp(vs, pk);
                 haveP = false;
             }
             if (haveS) scores_pp(kbeg + j * BN, KS, s);
         };
-        // The softmax of the ping-pong loop: as softmax(), with `hook(kb)`
-        // called after each 32-key block's exponentials. Group 1 issues its
-        // DMA there, two blocks of K and two of V at a time: issued back to
-        // back, a wave's sixteen DMA instructions stall it on the CU's memory
-        // queue (about 30 bytes a cycle) for longer than the softmax takes.
         // The softmax of the ping-pong loop. The S accumulators start at
         // -base (the running max, or 0 before the row's first key), so the
         // products arrive as s - base and P = exp2 of them needs no
         // subtraction. Only when a row's maximum passes base + 8 (P would
         // exceed 2^8) does base move, to that maximum, with one subtraction
         // pass and O rescaled. `hook(kb)` runs after each 32-key block's
-        // exponentials: group 1 issues its DMA there, two blocks of K and two
-        // of V at a time (issued back to back, a wave's sixteen DMA
-        // instructions stall it on the CU's memory queue, about 30 bytes a
-        // cycle, for longer than the softmax takes).
+        // exponentials: the softmax phase's DMA goes there, two blocks at a
+        // time (issued back to back, a wave's DMA instructions stall it on
+        // the CU's memory queue, about 30 bytes a cycle).
         auto softmax_pp = [&](floatx16 (&s)[NKB], half8 (&pk)[NKB][2], auto hook) __attribute__((always_inline)) {
             float mx = -INFINITY;
 #pragma unroll
@@ -1012,6 +1018,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
             }
         };
         auto vphase = [&](auto hook) __attribute__((always_inline)) {
+            __builtin_amdgcn_s_setprio(0);
             if (haveS) {
                 softmax_pp(s, pk, hook);
                 haveP = true;
@@ -1023,70 +1030,83 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         };
         auto no_dma = [](int, floatx16 (&)[NKB], const half8&) __attribute__((always_inline)) {};
         using std::integral_constant;
-        // group 1's DMA during its softmax: K tile kt into stage KS and V tile
-        // vt into stage VS, blocks 2 kb and 2 kb + 1 of each after block kb
-        auto dma_hook = [&](uint32_t kt, uint32_t vt, auto KS, auto VS) __attribute__((always_inline)) {
-            return [&, kt, vt, KS, VS](int kb, floatx16 (&sc)[NKB], const half8& last) __attribute__((always_inline)) {
+        // the softmax phase's DMA: tile t (K or V) into the LDS stage at
+        // `stage`, blocks 2 kb and 2 kb + 1 after 32-key block kb
+        auto dma_hook = [&](uint32_t t, uint32_t stage, bool isK) __attribute__((always_inline)) {
+            return [&, t, stage, isK](int kb, floatx16 (&sc)[NKB], const half8& last) __attribute__((always_inline)) {
                 // ordering only (the asm statements emit nothing): the DMA
                 // follows block kb's exponentials, whose last result it takes,
                 // and precedes block kb + 1's, whose scores pass through the
                 // asm after it
                 asm volatile("" : : "v"(last));
-                const bool doK = kt < ntiles, doV = vt < ntiles;
-                auto two = [&](auto N0) __attribute__((always_inline)) {
-                    constexpr int n = decltype(N0)::value;
-                    if (doK) dma_rows(kbeg + kt * BN, KS, true, integral_constant<int, n>{}, integral_constant<int, n + 2>{});
-                    if (doV) dma_rows(kbeg + vt * BN, VS, false, integral_constant<int, n>{}, integral_constant<int, n + 2>{});
-                };
-                if (kb == 0) two(integral_constant<int, 0>{});
-                else if (kb == 1) two(integral_constant<int, 2>{});
-                else if (kb == 2) two(integral_constant<int, 4>{});
-                else two(integral_constant<int, 6>{});
+                if (t < ntiles) {
+                    const uint32_t k0 = kbeg + t * BN;
+                    if (kb == 0) dma_rows(k0, stage, isK, integral_constant<int, 0>{}, integral_constant<int, 2>{});
+                    else if (kb == 1) dma_rows(k0, stage, isK, integral_constant<int, 2>{}, integral_constant<int, 4>{});
+                    else if (kb == 2) dma_rows(k0, stage, isK, integral_constant<int, 4>{}, integral_constant<int, 6>{});
+                    else dma_rows(k0, stage, isK, integral_constant<int, 6>{}, integral_constant<int, 8>{});
+                }
                 if (kb + 1 < NKB) asm volatile("" : "+v"(sc[kb + 1 < NKB ? kb + 1 : kb]));
             };
         };
-        if (grp == 1) {
-            dma_rows(kbeg, S0{}, true, integral_constant<int, 0>{}, integral_constant<int, PB>{});
-            wait_vmcnt<0>();
-        }
+        static_assert(NKB == 4 && PB == 8, "two DMA blocks after each of four 32-key blocks");
+        constexpr uint32_t VSTAGE = TILE * 2;   // bytes of one V stage
+        const uint32_t ldsK0 = lds_address(K0), ldsK1 = lds_address(K1), ldsV = lds_address(VP);
+        auto vstage = [&](uint32_t j) __attribute__((always_inline)) -> const _Float16* {
+            return VP + (j % 3) * TILE;
+        };
+        // prologue: K tile 0 by group 1, V tile 0 by group 0
+        if (grp == 1) dma_rows(kbeg, ldsK0, true, integral_constant<int, 0>{}, integral_constant<int, PB>{});
+        else dma_rows(kbeg, ldsV, false, integral_constant<int, 0>{}, integral_constant<int, PB>{});
+        wait_vmcnt<0>();
         lds_barrier();
+        // group 0 waits at the end of each softmax phase for the V tile it
+        // issued in the previous one: the newer PB blocks may stay in flight
+        auto wait_v = [&](uint32_t issuedNow) __attribute__((always_inline)) {
+            if (issuedNow < ntiles) wait_vmcnt<PB>();
+            else wait_vmcnt<0>();
+        };
         const uint32_t nI = 2 * ntiles + 2;
         for (uint32_t i0 = 0; i0 < nI; i0 += 4) {
             const uint32_t j0 = i0 / 2;   // the even tile of this round
-            // interval i0: group 0 MFMA on tile j0; group 1 softmax of j0 - 1
-            // and DMA of K j0 + 1 and V j0
+            // A_j0: group 0 MFMA on tile j0; group 1 softmax of j0 - 1 and
+            // DMA of K j0 + 1
             opaque_addresses();
-            if (grp == 0) mphase(j0, S0{}, S1{});
-            else vphase(dma_hook(j0 + 1, j0, S1{}, S0{}));
+            if (grp == 0) mphase(j0, S0{}, vstage(j0 + 2));   // V of tile j0 - 1
+            else vphase(dma_hook(j0 + 1, ldsK1, true));
             lds_barrier();
             if (i0 + 1 >= nI) break;
-            // interval i0 + 1: group 0 softmax of j0; group 1 MFMA on j0
+            // B_j0: group 0 softmax of j0 and DMA of V j0 + 1; group 1 MFMA on j0
             opaque_addresses();
             if (grp == 0) {
-                vphase(no_dma);
+                vphase(dma_hook(j0 + 1, ldsV + ((j0 + 1) % 3) * VSTAGE, false));
+                wait_v(j0 + 1);
             } else {
-                mphase(j0, S0{}, S1{});
+                mphase(j0, S0{}, vstage(j0 + 2));
                 wait_vmcnt<0>();
             }
             lds_barrier();
             if (i0 + 2 >= nI) break;
-            // interval i0 + 2: group 0 MFMA on tile j0 + 1; group 1 softmax of
-            // j0 and DMA of K j0 + 2 and V j0 + 1
+            // A_j0+1: group 0 MFMA on tile j0 + 1; group 1 softmax of j0 and
+            // DMA of K j0 + 2
             opaque_addresses();
-            if (grp == 0) mphase(j0 + 1, S1{}, S0{});
-            else vphase(dma_hook(j0 + 2, j0 + 1, S0{}, S1{}));
+            if (grp == 0) mphase(j0 + 1, S1{}, vstage(j0));
+            else vphase(dma_hook(j0 + 2, ldsK0, true));
             lds_barrier();
             if (i0 + 3 >= nI) break;
-            // interval i0 + 3: group 0 softmax of j0 + 1; group 1 MFMA on j0 + 1
+            // B_j0+1: group 0 softmax of j0 + 1 and DMA of V j0 + 2; group 1
+            // MFMA on j0 + 1
             opaque_addresses();
             if (grp == 0) {
-                vphase(no_dma);
+                vphase(dma_hook(j0 + 2, ldsV + ((j0 + 2) % 3) * VSTAGE, false));
+                wait_v(j0 + 2);
             } else {
-                mphase(j0 + 1, S1{}, S0{});
+                mphase(j0 + 1, S1{}, vstage(j0));
                 wait_vmcnt<0>();
             }
             lds_barrier();
         }
+        __builtin_amdgcn_s_setprio(0);
     } else {
     issue(kbeg, S0{});
     if constexpr (AHEAD > 1)
