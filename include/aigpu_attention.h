@@ -206,11 +206,12 @@ AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode* args);
 /* aigpu_decode_attention without any allocation. No counterpart in the
    reference: it is for callers that cannot allocate device memory (code
    under HIP graph capture, serving loops that forbid hipMalloc). Its
-   split-K records and prepared queries live in a fixed 32 MiB device array
-   per GPU, held until the process ends; larger batches run in slices that
-   fit it, and a call whose single sequence does not fit returns 0 with the
-   reason. Calls that overlap on one GPU share that array and race: order
-   them on one stream. Same arguments, kernels and results as
+   split-K records live in a fixed 32 MiB device array per GPU, held until
+   the process ends; larger batches run in slices that fit it, and a call
+   whose single sequence does not fit returns 0 with the reason. Every call
+   on a GPU shares that array: calls on different streams are ordered by the
+   backend, but replays of graphs captured from it that overlap on one GPU
+   race on it. Same arguments, kernels and results as
    aigpu_decode_attention. */
 AIGPU_ABI int aigpu_decode_attention_static(const AiGpuDecode* args);
 

@@ -55,6 +55,11 @@ Context::Context() {
         return;
     }
     *rangeHost = 0;
+    if (hipEventCreateWithFlags(&handoff, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        error = "hipEventCreate of the stream handoff event failed";
+        return;
+    }
     ok = true;
 }
 
@@ -145,6 +150,42 @@ using aigpu::since;
 namespace {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+/* Orders a call after the previous call when the two use different streams:
+   every call shares the backend's scratch, so the new stream first waits for
+   the event recorded after the previous call's launches, and this call's own
+   launches are followed by the event in turn. A stream being captured into a
+   graph is left alone (the caller orders captured work); so is the case of
+   one stream, where stream order already holds. */
+struct StreamOrder {
+    Context& ctx;
+    hipStream_t stream;
+    bool active = true;
+    StreamOrder(Context& c, hipStream_t s) : ctx(c), stream(s) {
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &capture) != hipSuccess) {
+            (void)hipGetLastError();
+            capture = hipStreamCaptureStatusNone;
+        }
+        if (capture != hipStreamCaptureStatusNone) {
+            active = false;
+            return;
+        }
+        if (ctx.handoffValid && ctx.handoffStream != s && hipStreamWaitEvent(s, ctx.handoff, 0) != hipSuccess)
+            (void)hipGetLastError();
+    }
+    ~StreamOrder() {
+        if (!active) return;
+        if (hipEventRecord(ctx.handoff, stream) == hipSuccess) {
+            ctx.handoffStream = stream;
+            ctx.handoffValid = true;
+        } else {
+            (void)hipGetLastError();
+        }
+    }
+    StreamOrder(const StreamOrder&) = delete;
+    StreamOrder& operator=(const StreamOrder&) = delete;
+};
 
 size_t elem_bytes(uint32_t type) { return type == AIGPU_BF16 ? 2 : 4; }
 
@@ -325,6 +366,7 @@ AIGPU_ABI int aigpu_attention_device(const AiGpuAttention* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("attention: null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, as_stream(args->stream));
     aigpu::AttentionF32Params p{};
     p.q = args->q;
     p.keys = args->keys;
@@ -342,7 +384,7 @@ AIGPU_ABI int aigpu_attention_device(const AiGpuAttention* args) {
     p.posStride = args->posStride;
     p.headStride = args->headStride;
     if (!p.q || !p.keys || !p.values || !p.out) return ctx.fail("attention: null tensor"), 0;
-    return aigpu::launch_attention_f32(p, as_stream(args->stream)) ? 1 : 0;
+    return aigpu::launch_attention_f32(p, order.stream) ? 1 : 0;
 }
 
 AIGPU_ABI int aigpu_attention(const float* q, const float* keys, const float* values, float* out,
@@ -354,6 +396,7 @@ AIGPU_ABI int aigpu_attention(const float* q, const float* keys, const float* va
     if (count == 0) return 1;
     if (kvHeads == 0 || heads % kvHeads) return ctx.fail("attention: heads must be a multiple of kvHeads"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, nullptr);
     const size_t qBytes = ((count - 1) * heads * qStride + (heads - 1) * qStride + dim) * 4;
     const size_t kvBytes = (start + count) * kvHeads * dim * 4;
     const size_t outBytes = count * heads * dim * 4;
@@ -406,9 +449,10 @@ AIGPU_ABI int aigpu_prefill_attention(const AiGpuPrefill* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("prefill: null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, as_stream(args->stream));
     aigpu::PrefillParams p = prefill_params(args);
     p.rangeFlag = ctx.rangeDev;
-    return aigpu::launch_prefill(p, as_stream(args->stream)) && ctx.checkRange("prefill", as_stream(args->stream))
+    return aigpu::launch_prefill(p, order.stream) && ctx.checkRange("prefill", order.stream)
                ? 1 : 0;
 }
 
@@ -418,6 +462,7 @@ AIGPU_ABI int aigpu_prefill_attention_host(const AiGpuPrefill* args) {
     if (!args || !args->q || !args->k || !args->v || !args->out) return ctx.fail("prefill: null tensor"), 0;
     if (args->count == 0) return 1;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, nullptr);
     const size_t es = elem_bytes(args->inType);
     const size_t qBytes = args->count * args->heads * args->qStride * es;
     const size_t kvBytes = args->count * args->kvHeads * args->dim * es;
@@ -481,7 +526,8 @@ AIGPU_ABI int aigpu_decode_attention(const AiGpuDecode* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("decode: null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
-    return aigpu::launch_decode(decode_params(args), as_stream(args->stream)) ? 1 : 0;
+    const StreamOrder order(ctx, as_stream(args->stream));
+    return aigpu::launch_decode(decode_params(args), order.stream) ? 1 : 0;
 }
 
 AIGPU_ABI int aigpu_decode_attention_static(const AiGpuDecode* args) {
@@ -489,6 +535,7 @@ AIGPU_ABI int aigpu_decode_attention_static(const AiGpuDecode* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("decode (no allocation): null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, as_stream(args->stream));
     aigpu::FixedScratch fixed{};
     if (!aigpu::decode_static_scratch(&fixed.base, &fixed.bytes)) return 0;
     struct NoAlloc {
@@ -496,7 +543,7 @@ AIGPU_ABI int aigpu_decode_attention_static(const AiGpuDecode* args) {
         explicit NoAlloc(Context& x) : c(x) { c.noAlloc = true; }
         ~NoAlloc() { c.noAlloc = false; }
     } guard(ctx);
-    return aigpu::launch_decode(decode_params(args), as_stream(args->stream), &fixed) ? 1 : 0;
+    return aigpu::launch_decode(decode_params(args), order.stream, &fixed) ? 1 : 0;
 }
 
 AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode* args) {
@@ -506,6 +553,7 @@ AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode* args) {
         return ctx.fail("decode: null tensor"), 0;
     if (args->batch == 0) return 1;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, nullptr);
     const size_t es = elem_bytes(args->inType);
     const size_t qBytes = args->batch * args->heads * args->qStride * es;
     const size_t kvBytes = args->batch * args->kvHeads * args->dim * es;
@@ -567,7 +615,8 @@ AIGPU_ABI int aigpu_gated_delta_rule(const AiGpuDeltaRule* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("delta rule: null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
-    return aigpu::launch_delta_rule(delta_params(args), as_stream(args->stream)) ? 1 : 0;
+    const StreamOrder order(ctx, as_stream(args->stream));
+    return aigpu::launch_delta_rule(delta_params(args), order.stream) ? 1 : 0;
 }
 
 AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule* args) {
@@ -577,6 +626,7 @@ AIGPU_ABI int aigpu_gated_delta_rule_host(const AiGpuDeltaRule* args) {
         return ctx.fail("delta rule: null tensor"), 0;
     if (args->count == 0) return 1;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, nullptr);
     const size_t es = elem_bytes(args->inType);
     const size_t qkBytes = args->count * args->keyHeads * args->keyDim * es;
     const size_t vBytes = args->count * args->valueHeads * args->valueDim * es;
@@ -619,6 +669,7 @@ AIGPU_ABI int aigpu_gdn_conv(const AiGpuGdnConv* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("gdn conv: null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, as_stream(args->stream));
     aigpu::GdnConvParams p{};
     p.in = args->in;
     p.ba = args->ba;
@@ -639,7 +690,7 @@ AIGPU_ABI int aigpu_gdn_conv(const AiGpuGdnConv* args) {
     p.keyDim = args->keyDim;
     p.valueDim = args->valueDim;
     p.kernelSize = args->kernelSize;
-    return aigpu::launch_gdn_conv(p, as_stream(args->stream)) ? 1 : 0;
+    return aigpu::launch_gdn_conv(p, order.stream) ? 1 : 0;
 }
 
 AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm* args) {
@@ -647,6 +698,7 @@ AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("gdn gated norm: null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, as_stream(args->stream));
     aigpu::GdnGatedNormParams p{};
     p.x = args->x;
     p.z = args->z;
@@ -660,7 +712,7 @@ AIGPU_ABI int aigpu_gdn_gated_norm(const AiGpuGdnGatedNorm* args) {
     p.count = args->count;
     p.valueHeads = args->valueHeads;
     p.valueDim = args->valueDim;
-    return aigpu::launch_gdn_gated_norm(p, as_stream(args->stream)) ? 1 : 0;
+    return aigpu::launch_gdn_gated_norm(p, order.stream) ? 1 : 0;
 }
 
 AIGPU_ABI int aigpu_kda_rule(const AiGpuKda* args) {
@@ -668,6 +720,7 @@ AIGPU_ABI int aigpu_kda_rule(const AiGpuKda* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("kda: null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, as_stream(args->stream));
     aigpu::KdaParams p{};
     p.q = args->q;
     p.k = args->k;
@@ -689,7 +742,7 @@ AIGPU_ABI int aigpu_kda_rule(const AiGpuKda* args) {
     p.valueHeads = args->valueHeads;
     p.keyDim = args->keyDim;
     p.valueDim = args->valueDim;
-    return aigpu::launch_kda(p, as_stream(args->stream)) ? 1 : 0;
+    return aigpu::launch_kda(p, order.stream) ? 1 : 0;
 }
 
 namespace {
@@ -710,6 +763,7 @@ void matmul_host(const float* a, const void* b, const void* scales, float* c, ui
         return;
     }
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, nullptr);
     const size_t inBytes = m * k * 4, outBytes = m * n * 4;
     char* in = static_cast<char*>(ctx.grow(aigpu::SLOT_STAGE_IN, padded(inBytes)));
     float* dC = static_cast<float*>(ctx.grow(aigpu::SLOT_STAGE_OUT, outBytes));
@@ -762,6 +816,7 @@ AIGPU_ABI int aigpu_matmul_device(const AiGpuMatmul* args) {
         args->ldc > 0xFFFFFFFFull)
         return ctx.fail("matmul: dimensions out of range"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, as_stream(args->stream));
     aigpu::GemvParams p{};
     p.a = args->a;
     p.w = args->b;
@@ -774,7 +829,7 @@ AIGPU_ABI int aigpu_matmul_device(const AiGpuMatmul* args) {
     p.k = uint32_t(args->k);
     p.n = uint32_t(args->n);
     p.ldo = uint32_t(args->ldc ? args->ldc : args->n);
-    return aigpu::launch_gemv(p, as_stream(args->stream)) ? 1 : 0;
+    return aigpu::launch_gemv(p, order.stream) ? 1 : 0;
 }
 
 } // extern "C"
@@ -786,6 +841,7 @@ AIGPU_ABI int aigpu_prefill_mixer(const AiGpuPrefillMixer* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("prefill mixer: null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, as_stream(args->stream));
     auto weight = [](const AiGpuDenseWeight& w) {
         aigpu::MixerWeight m{};
         m.codes = w.codes;
@@ -827,8 +883,8 @@ AIGPU_ABI int aigpu_prefill_mixer(const AiGpuPrefillMixer* args) {
     p.qStride = args->outputGate ? 2 * args->dim : args->dim;
     p.window = args->window;
     p.capacity = args->capacity;
-    return aigpu::launch_prefill_mixer(p, as_stream(args->stream)) &&
-                   ctx.checkRange("prefill mixer", as_stream(args->stream))
+    return aigpu::launch_prefill_mixer(p, order.stream) &&
+                   ctx.checkRange("prefill mixer", order.stream)
                ? 1 : 0;
 }
 
@@ -837,6 +893,7 @@ AIGPU_ABI int aigpu_select_keys(const AiGpuSelectKeys* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("select keys: null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, as_stream(args->stream));
     auto weight = [](const AiGpuDenseWeight& w) {
         aigpu::MixerWeight m{};
         m.codes = w.codes;
@@ -877,7 +934,7 @@ AIGPU_ABI int aigpu_select_keys(const AiGpuSelectKeys* args) {
     p.topK = args->topK;
     p.pool = args->pool;
     p.capacity = args->capacity;
-    return aigpu::launch_select_keys(p, as_stream(args->stream)) ? 1 : 0;
+    return aigpu::launch_select_keys(p, order.stream) ? 1 : 0;
 }
 
 AIGPU_ABI int aigpu_latent_attention(const AiGpuLatentAttention* args) {
@@ -885,6 +942,7 @@ AIGPU_ABI int aigpu_latent_attention(const AiGpuLatentAttention* args) {
     if (!ctx.ok) return 0;
     if (!args) return ctx.fail("latent attention: null arguments"), 0;
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, as_stream(args->stream));
     aigpu::LatentParams p{};
     p.q = args->q;
     p.latent = args->latent;
@@ -901,7 +959,7 @@ AIGPU_ABI int aigpu_latent_attention(const AiGpuLatentAttention* args) {
     p.nope = args->nopeDim;
     p.vdim = args->vDim;
     p.rank = args->kvLoraRank;
-    return aigpu::launch_latent_attention(p, as_stream(args->stream)) ? 1 : 0;
+    return aigpu::launch_latent_attention(p, order.stream) ? 1 : 0;
 }
 
 } // extern "C"

@@ -56,6 +56,13 @@ struct Context {
     // fp16; rangeDev is its device address
     uint32_t* rangeHost = nullptr;
     uint32_t* rangeDev = nullptr;
+
+    // calls on different streams share the scratch slots (and the fixed
+    // decode scratch): an event recorded on the stream of each call, which
+    // a call on another stream waits for before its first launch
+    hipEvent_t handoff = nullptr;
+    hipStream_t handoffStream = nullptr;
+    bool handoffValid = false;
     // waits for `stream` and reports (and clears) a raised range flag as a
     // failure of `what`; a stream being captured into a graph is not waited
     // for and the flag stays for the next checked call

@@ -34,8 +34,9 @@
 // records: on gfx950 such a fence writes back and invalidates the XCD's whole
 // L2, which costs far more than a launch.
 //
-// Calls that share the backend's scratch (the records) must not run
-// concurrently on different streams.
+// Calls on different streams share the backend's scratch (the records); the
+// entry points order a call after the previous one when its stream differs
+// (an event handoff), so their kernels never overlap on it.
 #include "context.hpp"
 #include "device.hpp"
 #include "kernels.hpp"

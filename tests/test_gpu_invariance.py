@@ -186,3 +186,48 @@ def test_concurrent_host_calls(gpu):
         assert gpu.counters()["launches"] == repeats * per_round
     finally:
         gpu.release(wptr, w.nbytes)
+
+
+def test_calls_on_two_streams_keep_their_scratch_apart(gpu):
+    """device-form decodes issued back to back on two streams, with no
+    synchronisation between them, share the backend's split-K record scratch;
+    each call waits for the other stream's previous call, so both give what
+    the same calls give one after another on one stream (bit for bit)"""
+    import torch
+    B, H, KV, D, L = 16, 32, 4, 128, 9000
+    gen = torch.Generator(device="cuda").manual_seed(41)
+
+    def case():
+        q = torch.randn((B, H, D), generator=gen, device="cuda").to(torch.bfloat16)
+        k = torch.randn((B, KV, D), generator=gen, device="cuda").to(torch.bfloat16)
+        v = torch.randn((B, KV, D), generator=gen, device="cuda").to(torch.bfloat16)
+        kc = torch.randn((B, KV, L + 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+        vc = torch.randn((B, KV, L + 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+        pos = torch.full((B,), L, dtype=torch.int32, device="cuda")
+        return q, k, v, kc, vc, pos
+
+    cases = [case(), case()]
+
+    def run(c, caches, out, stream=None):
+        q, k, v, _, _, pos = c
+        gpu.decode(q, k, v, out, caches[0], caches[1], pos, L, H, KV, D,
+                   stream=None if stream is None else stream.cuda_stream)
+
+    def fresh_caches():
+        return [(c[3].clone(), c[4].clone()) for c in cases]
+
+    ref = [torch.zeros((B, H, D), device="cuda") for _ in cases]
+    for c, cc, o in zip(cases, fresh_caches(), ref):
+        run(c, cc, o)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    say("decode on two streams", dict(B=B, L=L))
+    for rep in range(3):
+        got = [torch.zeros((B, H, D), device="cuda") for _ in cases]
+        caches = fresh_caches()
+        torch.cuda.synchronize()   # inputs ready before either stream starts
+        run(cases[0], caches[0], got[0], s1)
+        run(cases[1], caches[1], got[1], s2)
+        torch.cuda.synchronize()
+        for g, r in zip(got, ref):
+            assert torch.equal(g, r), f"repeat {rep}: a call's records were overwritten"
