@@ -211,6 +211,20 @@ def prefill_workload(args, cpu):
                      "unit": "TFLOP/s", "frac": flops / (k_ms * 1e-3) / 1e12 / PEAK_MFMA_F16,
                      "traffic": PREFILL_FLASH_TRAFFIC, "kernel_ms": k_ms, "flops_per_launch": flops},
     }
+
+    # the same prefill with a sliding window of 4096 keys (per-layer windows,
+    # LocalModel.hpp:821-830; the first key a query sees, Kernels.hpp:142)
+    W = 4096
+
+    def step_window():
+        aigpu.prefill(q, k, v, out, kc, vc, 0, H, KV, D, q_norm=gq, k_norm=gk, freqs=fr, rotary_dims=D, window=W)
+
+    wflops = 4.0 * D * H * sum(min(i + 1, W) for i in range(S))
+    w_step, w_k, _ = time_steps(step_window, args.steps, args.warmup, "prefill_flash_kernel")
+    res["window_4096"] = {"workload": "configs[2] shape with a sliding window of 4096 keys",
+                          "value": wflops / (w_step * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": w_step,
+                          "kernel_ms": w_k, "kernel_frac": wflops / (w_k * 1e-3) / 1e12 / PEAK_MFMA_F16,
+                          "flops_per_launch": wflops}
     if cpu is not None:
         O, ref, kind, threads = cpu
         qh = q[-64:].float().cpu().numpy()
