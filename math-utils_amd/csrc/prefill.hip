@@ -974,11 +974,20 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         // time (issued back to back, a wave's DMA instructions stall it on
         // the CU's memory queue, about 30 bytes a cycle).
         auto softmax_pp = [&](floatx16 (&s)[NKB], half8 (&pk)[NKB][2], auto hook) __attribute__((always_inline)) {
-            float mx = -INFINITY;
+            // eight partial maxima (one per 16-key half block): short
+            // independent chains instead of one of 32 dependent max3s
+            float mp[NKB][2];
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+                for (int h = 0; h < 2; ++h) {
+                    mp[kb][h] = s[kb][8 * h];
+#pragma unroll
+                    for (int j = 1; j < 8; ++j) mp[kb][h] = fmaxf(mp[kb][h], s[kb][8 * h + j]);
+                }
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) mp[kb][0] = fmaxf(mp[kb][0], mp[kb][1]);
+            float mx = fmaxf(fmaxf(mp[0][0], mp[1][0]), fmaxf(mp[2][0], mp[3][0]));
             {
                 const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
                 mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
@@ -994,7 +1003,8 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                     for (int r = 0; r < 16; ++r) s[kb][r] -= shift;
             }
             typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-            float psum = 0.0f;
+            // eight partial row sums, one per 16-key half block
+            float ps[NKB][2];
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
@@ -1002,12 +1012,15 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
 #pragma unroll
                     for (int j = 0; j < 8; ++j) pk[kb][h][j] = _Float16(__builtin_amdgcn_exp2f(s[kb][8 * h + j]));
 #pragma unroll
-                for (int h = 0; h < 2; ++h)
+                for (int h = 0; h < 2; ++h) {
+                    ps[kb][h] = 0.0f;
 #pragma unroll
                     for (int j = 0; j < 8; j += 2)
-                        psum = __builtin_amdgcn_fdot2(h2{pk[kb][h][j], pk[kb][h][j + 1]}, h2{1, 1}, psum, false);
+                        ps[kb][h] = __builtin_amdgcn_fdot2(h2{pk[kb][h][j], pk[kb][h][j + 1]}, h2{1, 1}, ps[kb][h], false);
+                }
                 hook(kb, s, pk[kb][1]);
             }
+            const float psum = ((ps[0][0] + ps[0][1]) + (ps[1][0] + ps[1][1])) + ((ps[2][0] + ps[2][1]) + (ps[3][0] + ps[3][1]));
             lsum = lsum * alpha + psum;
             if (grow) m = (fresh ? 0.0f : m) + shift;
             if (__any(grow)) {
