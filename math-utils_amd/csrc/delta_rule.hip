@@ -50,12 +50,23 @@ constexpr int NS = NB + 1;
 constexpr int SC = 4 * CH;               // gc, beta, kinv, qinv per chunk
 constexpr int WORK = 2 * CH * CH + SC;   // floats per (head, chunk) record, fp32 form
 // the split form, laid out as the DMA scan's LDS image: T hi, T lo, QKm hi,
-// QKm lo ([64][64] bf16 each, 16-byte block b of row r at b ^ (r % 8)), then
-// 512 floats: beta, gamma kinv, gamma qinv, kinv exp(gc_last - gc),
-// exp(gc_last) (64 copies), zeros
-constexpr int SPLIT_MAT = CH * CH / 2;          // floats per bf16 [64][64] matrix
+// QKm lo, then 512 floats: beta, gamma kinv, gamma qinv, kinv exp(gc_last -
+// gc), exp(gc_last) (64 copies), zeros. T and QKm are lower triangular, so
+// rows 0-31 keep only their first 32 columns (the scan's waves 0 and 1 read
+// no other k block): a packed bf16 matrix is rows 0-31 x 32 columns (16-byte
+// block b of row r at b ^ ((r >> 1 ^ r >> 3) & 3)) followed by rows 32-63 x
+// 64 columns (block b at b ^ (r & 7)), 3,072 elements, a quarter less than
+// the square. Both swizzles keep any 8 or 16 consecutive rows' reads of one
+// block column on distinct banks.
+constexpr int PMAT = 32 * 32 + 32 * 64;         // bf16 elements per packed matrix
+constexpr int PMAT_BYTES = PMAT * 2;
 constexpr int SPLIT_SC = 512;
-constexpr int WORK_SPLIT = 4 * SPLIT_MAT + SPLIT_SC;
+constexpr int WORK_SPLIT = 4 * PMAT / 2 + SPLIT_SC;   // floats
+
+/* element offset of row r's 16-byte block b in a packed T / QKm matrix */
+__host__ __device__ constexpr int pmat_offset(int r, int b) {
+    return r < 32 ? r * 32 + 8 * (b ^ (((r >> 1) ^ (r >> 3)) & 3)) : 1024 + (r - 32) * 64 + 8 * (b ^ (r & 7));
+}
 
 struct DeltaArgs {
     DeltaRuleParams p;
@@ -322,7 +333,8 @@ __global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs
 #pragma unroll
             for (int it = 0; it < 2; ++it) {
                 const int idx = tid + 256 * it, r = idx >> 3, b = idx & 7;
-                const int dst = r * CH + 8 * (b ^ (r & 7));
+                if (r < 32 && b >= 4) continue;   // above the diagonal blocks: zero, not stored
+                const int dst = pmat_offset(r, b);
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
                     const float* src = (m == 0 ? Tm : Am) + r * CS + 8 * b;
@@ -336,13 +348,13 @@ __global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs
                         hi[e] = uint32_t(h0) | (uint32_t(h1) << 16);
                         lo[e] = uint32_t(l0) | (uint32_t(l1) << 16);
                     }
-                    *reinterpret_cast<u32x4*>(out16 + (2 * m) * CH * CH + dst) = hi;
-                    *reinterpret_cast<u32x4*>(out16 + (2 * m + 1) * CH * CH + dst) = lo;
+                    *reinterpret_cast<u32x4*>(out16 + (2 * m) * PMAT + dst) = hi;
+                    *reinterpret_cast<u32x4*>(out16 + (2 * m + 1) * PMAT + dst) = lo;
                 }
             }
             // per-row scalars of the scan: rows past the sequence's end have
             // beta 0, so they add nothing to U, O or the state
-            float* sc = rec + 4 * SPLIT_MAT;
+            float* sc = rec + 2 * PMAT;
             const float gLast = gsc[CH - 1];
             for (int idx = tid; idx < SPLIT_SC; idx += 256) {
                 const int i = idx & (CH - 1), part = idx >> 6;
@@ -866,17 +878,17 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
     constexpr int KBLK = KD / 8;                     // 16-byte blocks per k/q row
     constexpr int RPI = 1024 / (2 * KD);             // k/q rows per 1 KB DMA block
     constexpr int KI = CH / RPI / 4;                 // k (or q) DMA blocks per wave
-    constexpr int TI = 4;                            // T (or QKm) hi+lo blocks per wave: 16 KB / 4
+    constexpr int TI = 2 * PMAT_BYTES / 1024 / 4;   // T (or QKm) hi+lo DMA blocks per wave: 12 KB / 4
 
     constexpr int KST = KD + 8;                      // S^T row stride (elements)
     constexpr int CHH = CH + 8;                      // R^T, U^T, W^T row stride
     constexpr int MT = KD / 64;                      // 16-row state tiles per wave
     static_assert(KI * 4 * RPI == CH, "k rows split evenly over the waves");
     __shared__ __attribute__((aligned(16))) __bf16 Kb[2][CH * KD];        // raw k rows, swizzled
-    __shared__ __attribute__((aligned(16))) __bf16 Tb[2][2 * CH * CH];    // T hi, lo (solve's image)
+    __shared__ __attribute__((aligned(16))) __bf16 Tb[2][2 * PMAT];       // T hi, lo (solve's packed image)
     __shared__ __attribute__((aligned(16))) float Ax[2][1024];           // v [64][16] bf16, then scalars
     __shared__ __attribute__((aligned(16))) __bf16 Qb[2][CH * KD];        // raw q rows, swizzled
-    __shared__ __attribute__((aligned(16))) __bf16 Mb[2][2 * CH * CH];    // QKm hi, lo
+    __shared__ __attribute__((aligned(16))) __bf16 Mb[2][2 * PMAT];       // QKm hi, lo
     __shared__ __attribute__((aligned(16))) __bf16 St[2][NB * KST];       // [hi/lo] S^T [col][key]
     __shared__ __attribute__((aligned(16))) __bf16 Rt[2][NB * CHH];       // R^T hi, lo
     __shared__ __attribute__((aligned(16))) __bf16 Ut[2][NB * CHH];       // U^T
@@ -905,7 +917,7 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
     // DMA targets: LDS byte addresses of each buffer (uniform)
     const uint32_t ldsK = lds_address(Kb), ldsQ = lds_address(Qb), ldsT = lds_address(Tb);
     const uint32_t ldsM = lds_address(Mb), ldsA = lds_address(Ax);
-    constexpr uint32_t KBUF = CH * KD * 2, TBUF = 2 * CH * CH * 2, ABUF = 4096;   // bytes per buffer
+    constexpr uint32_t KBUF = CH * KD * 2, TBUF = 2 * PMAT_BYTES, ABUF = 4096;   // bytes per buffer
     // per-lane byte offsets of this wave's DMA blocks within a chunk: k/q
     // rows (block j: rows RPI (w KI + j) + lane / KBLK, swizzled; rows past a
     // partial chunk's end repeat its last row, whose beta is 0), the split
@@ -946,14 +958,14 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
         dma_block(nx.rec + j * 1024, matOff, ldsT + nx.buf * TBUF + (w * TI + j) * 1024);
     };
     auto dma_m_j = [&](const Next& nx, int j) __attribute__((always_inline)) {
-        dma_block(nx.rec + 2 * SPLIT_MAT * 4 + j * 1024, matOff, ldsM + nx.buf * TBUF + (w * TI + j) * 1024);
+        dma_block(nx.rec + 2 * PMAT_BYTES + j * 1024, matOff, ldsM + nx.buf * TBUF + (w * TI + j) * 1024);
     };
     auto dma_aux = [&](const Next& nx) __attribute__((always_inline)) {
         if (w < 2) {   // value block: 32 rows of 32 bytes per DMA block
             const uint32_t rr = uint32_t(vRow) < nx.n ? uint32_t(vRow) : nx.n - 1;
             dma_block(nx.v, rr * vRowBytes + 16 * (lane & 1), ldsA + nx.buf * ABUF + 1024 * w);
         } else {       // scalars
-            dma_block(nx.rec + 4 * SPLIT_MAT * 4, uint32_t(1024 * (w - 2) + 16 * lane),
+            dma_block(nx.rec + 4 * PMAT_BYTES, uint32_t(1024 * (w - 2) + 16 * lane),
                       ldsA + nx.buf * ABUF + 2048 + 1024 * (w - 2));
         }
     };
@@ -976,10 +988,11 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
         const int r = 16 * w + c16, lb = 4 * kb + g;
         return *reinterpret_cast<const bf16x8*>(X + r * KD + 8 * (lb ^ (r % KBLK)));
     };
-    // A operand from a [64][64] split matrix in the solve's image
+    // A operand from a packed split matrix in the solve's image (k block kb
+    // of rows 16w ..; waves 0 and 1 only ever read kb = 0)
     auto mat_a = [&](const __bf16* X, int kb) __attribute__((always_inline)) -> bf16x8 {
         const int r = 16 * w + c16, lb = 4 * kb + g;
-        return *reinterpret_cast<const bf16x8*>(X + r * CH + 8 * (lb ^ (r & 7)));
+        return *reinterpret_cast<const bf16x8*>(X + pmat_offset(r, lb));
     };
 
     // S: wave w's tiles mt = w + 4t hold key rows 16 mt + 4g + r, column c16
@@ -1072,18 +1085,26 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
 
         // U = T R, W = diag(kdk) U
         floatx4 u = {0.0f, 0.0f, 0.0f, 0.0f};
+        static_assert(TI == 3, "the T and QKm DMA is issued as 2 + 1 blocks each");
 #pragma unroll
         for (int kb = 0; kb < CH / 32; ++kb) {
-            dma_t_j(nx, 2 * kb);
-            dma_t_j(nx, 2 * kb + 1);
-            dma_m_j(nx, 2 * kb);
-            dma_m_j(nx, 2 * kb + 1);
-            const bf16x8 th = mat_a(T, kb), tl = mat_a(T + CH * CH, kb);
-            const int yo = c16 * CHH + 32 * kb + 8 * g;
-            const bf16x8 rh = *reinterpret_cast<const bf16x8*>(&Rt[0][yo]);
-            u = mfma_bf(th, rh, u);
-            u = mfma_bf(th, *reinterpret_cast<const bf16x8*>(&Rt[1][yo]), u);
-            u = mfma_bf(tl, rh, u);
+            if (kb == 0) {
+                dma_t_j(nx, 0);
+                dma_t_j(nx, 1);
+                dma_m_j(nx, 0);
+                dma_m_j(nx, 1);
+            } else {
+                dma_t_j(nx, 2);
+                dma_m_j(nx, 2);
+            }
+            if (kb == 0 || w >= 2) {   // rows < 32 have no nonzero T past column 31
+                const bf16x8 th = mat_a(T, kb), tl = mat_a(T + PMAT, kb);
+                const int yo = c16 * CHH + 32 * kb + 8 * g;
+                const bf16x8 rh = *reinterpret_cast<const bf16x8*>(&Rt[0][yo]);
+                u = mfma_bf(th, rh, u);
+                u = mfma_bf(th, *reinterpret_cast<const bf16x8*>(&Rt[1][yo]), u);
+                u = mfma_bf(tl, rh, u);
+            }
         }
         dma_aux(nx);
         put_t(Ut[0], Ut[1], CHH, 16 * w, u);
@@ -1121,7 +1142,8 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
         for (int r = 0; r < 4; ++r) acc[r] = qs[r] * gqinv[16 * w + 4 * g + r];
 #pragma unroll
         for (int kb = 0; kb < CH / 32; ++kb) {
-            const bf16x8 mh = mat_a(M, kb), ml = mat_a(M + CH * CH, kb);
+            if (kb == 1 && w < 2) continue;   // QKm is zero past column 31 on rows < 32
+            const bf16x8 mh = mat_a(M, kb), ml = mat_a(M + PMAT, kb);
             const int yo = c16 * CHH + 32 * kb + 8 * g;
             const bf16x8 uh = *reinterpret_cast<const bf16x8*>(&Ut[0][yo]);
             acc = mfma_bf(mh, uh, acc);
