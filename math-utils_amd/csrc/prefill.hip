@@ -190,19 +190,24 @@ __device__ __forceinline__ void store8_bf16(uint16_t* dst, const float (&x)[8]) 
 
 /*
     The same work as prefill_prep_kernel with every row held in registers:
-    one workgroup per token, D/8 lanes per row, 8 consecutive elements per
-    lane (one 16-byte load of bf16). The RMS sum is a butterfly over the
-    row's lanes; the rotate-half partner of element e (e +- rot/2) sits in
-    lane +- rot/16 at the same slot, which needs rot % 16 == 0. Rows are taken
-    four at a time with all four loads issued before any arithmetic.
+    one workgroup of one wave per token, D/8 lanes per row, 8 consecutive
+    elements per lane (one 16-byte load of bf16). The RMS sum is a butterfly
+    over the row's lanes; the rotate-half partner of element e (e +- rot/2)
+    sits in lane +- rot/16 at the same slot, which needs rot % 16 == 0. Each
+    lane takes four rows at a time with all four loads issued before any
+    arithmetic (a wave per token measured ~1% faster over the cfg3 step than
+    four waves per token, which left three of them idle in the sin/cos).
 */
+constexpr int PREP_THREADS = 64;   // one wave per token: its rows four at a time per lane
+
 template <int D, bool F32>
-__global__ __launch_bounds__(256) void prefill_prep_vec_kernel(PrefillParams p, _Float16* __restrict__ qh,
-                                                               _Float16* __restrict__ kh,
-                                                               _Float16* __restrict__ vh, uint32_t T,
-                                                               float qScale, uint32_t firstRow,
-                                                               float* __restrict__ rope) {
-    constexpr int LPR = D / 8, RPP = 256 / LPR, UNROLL = 4;
+__global__ __launch_bounds__(PREP_THREADS) void prefill_prep_vec_kernel(PrefillParams p, _Float16* __restrict__ qh,
+                                                                        _Float16* __restrict__ kh,
+                                                                        _Float16* __restrict__ vh, uint32_t T,
+                                                                        float qScale, uint32_t firstRow,
+                                                                        float* __restrict__ rope) {
+    static_assert(PREP_THREADS >= D / 2, "one thread per rotary pair");
+    constexpr int LPR = D / 8, RPP = PREP_THREADS / LPR, UNROLL = 4;
     __shared__ float cs[D / 2], sn[D / 2];
     const int tid = threadIdx.x, sub = tid % LPR, lane = tid % WAVE;
     const uint32_t t = blockIdx.x, pos = uint32_t(p.start) + t;
@@ -1268,16 +1273,16 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
                                    (p.heads + 2 * p.kvHeads) * p.dim * sizeof(float), stream, p, qh, kh, vh, T,
                                    qScale);
             else if (p.dim == 128 && p.inType == 1)
-                hipLaunchKernelGGL((prefill_prep_vec_kernel<128, false>), grid, block, 0, stream, p, qh, kh, vh,
+                hipLaunchKernelGGL((prefill_prep_vec_kernel<128, false>), grid, dim3(PREP_THREADS), 0, stream, p, qh, kh, vh,
                                    t32, qScale, firstRow, rope);
             else if (p.dim == 128)
-                hipLaunchKernelGGL((prefill_prep_vec_kernel<128, true>), grid, block, 0, stream, p, qh, kh, vh,
+                hipLaunchKernelGGL((prefill_prep_vec_kernel<128, true>), grid, dim3(PREP_THREADS), 0, stream, p, qh, kh, vh,
                                    t32, qScale, firstRow, rope);
             else if (p.inType == 1)
-                hipLaunchKernelGGL((prefill_prep_vec_kernel<64, false>), grid, block, 0, stream, p, qh, kh, vh,
+                hipLaunchKernelGGL((prefill_prep_vec_kernel<64, false>), grid, dim3(PREP_THREADS), 0, stream, p, qh, kh, vh,
                                    t32, qScale, firstRow, rope);
             else
-                hipLaunchKernelGGL((prefill_prep_vec_kernel<64, true>), grid, block, 0, stream, p, qh, kh, vh,
+                hipLaunchKernelGGL((prefill_prep_vec_kernel<64, true>), grid, dim3(PREP_THREADS), 0, stream, p, qh, kh, vh,
                                    t32, qScale, firstRow, rope);
         }))
         return false;
