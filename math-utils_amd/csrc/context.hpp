@@ -31,6 +31,7 @@ enum ScratchSlot {
     SLOT_MIXER_ATTN,     // fp32 attention output of a prefill mixer
     SLOT_INDEXER,        // index keys, queries, head weights and scores of selectKeys
     SLOT_GEMM_SPLIT,     // the K slices' partial tiles of a split GEMM
+    SLOT_GEMM_A,         // a split into bf16 high parts and residuals for gemm_dma_kernel
     SLOT_COUNT
 };
 

@@ -566,7 +566,6 @@ __global__ __launch_bounds__(256) void delta_scan_f32_kernel(DeltaArgs a) {
     }
 }
 
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __fp16 fp16x4v __attribute__((__vector_size__(4 * sizeof(__fp16))));
 
 /* fp32 -> bf16 high part and bf16 residual (round to nearest even): hi + lo

@@ -13,7 +13,9 @@
 // (4, 8, 16 or 32 weights), one wave owns GEMV_ROWS weight rows and keeps an
 // fp32 accumulator per (weight row, a row), and a shuffle tree reduces the
 // lanes. Up to GEMM_MIN_M - 1 rows of a run as blocks of 8 along grid.y;
-// more rows take gemm_kernel on MFMA.
+// more rows take gemm_kernel on MFMA, and bf16 weights with enough rows for
+// 256 x 256 tiles split_a_kernel and gemm_dma_kernel.
+#include <type_traits>
 #include "context.hpp"
 #include "device.hpp"
 #include "gemv.hpp"
@@ -374,6 +376,150 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvParams p, KvEpilogue ep, 
     }
 }
 
+/*
+    gemm_dma_kernel: bf16 weights and enough rows for 256 x 256 tiles, after
+    split_a_kernel has split a into bf16 high parts and residuals ([M][K]
+    each). Four waves of 128 x 128 (8 x 8 v_mfma_f32_16x16x32_bf16 tiles, the
+    256 fp32 accumulators per lane in AGPRs, one workgroup per CU); per
+    32-wide K step a wave reads 24 KB of operands from LDS for 128 MFMAs.
+    Every operand comes in by DMA (global_load_lds, 1 KB blocks) into a
+    three-stage LDS ring of 48 KB stages, step t + 2 issued between step t's
+    MFMAs, so nothing passes through registers or the VALU and each step's
+    loads have two steps of compute to land; one barrier per step. Within a
+    1 KB block (16 rows of 64 bytes) row r keeps its 16-byte chunk c at
+    position c ^ s(r % 16), s(x) = ((x / 2) % 4) ^ (x / 8): the 16 rows of an
+    operand read fall on distinct banks both as one 256-byte access and as
+    two 128-byte halves.
+*/
+constexpr int GD_BM = 256, GD_BN = 256, GD_BK = 32, GD_STAGES = 3;
+constexpr int GD_OPB = GD_BM * GD_BK * 2;   // bytes of one operand's tile per step (16 KB)
+constexpr int GD_STAGE = 3 * GD_OPB;         // a hi, a lo, w
+
+__global__ __launch_bounds__(256) void split_a_kernel(const float* a, bf16x8* hi, bf16x8* lo, uint64_t pieces) {
+    for (uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x; i < pieces; i += uint64_t(gridDim.x) * 256) {
+        const floatx4 x0 = reinterpret_cast<const floatx4*>(a)[2 * i];
+        const floatx4 x1 = reinterpret_cast<const floatx4*>(a)[2 * i + 1];
+        bf16x8 h, l;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            h[t] = __bf16(x0[t]);
+            l[t] = __bf16(x0[t] - float(h[t]));
+            h[4 + t] = __bf16(x1[t]);
+            l[4 + t] = __bf16(x1[t] - float(h[4 + t]));
+        }
+        hi[i] = h;
+        lo[i] = l;
+    }
+}
+
+/* s_waitcnt vmcnt(N) alone (N < 64) */
+template <int N>
+__device__ __forceinline__ void gd_wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__global__ __launch_bounds__(256) void gemm_dma_kernel(GemvParams p, const __bf16* ahi, const __bf16* alo) {
+    __shared__ __align__(16) uint8_t smem[GD_STAGES * GD_STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wm = (tid >> 6) >> 1, wn = (tid >> 6) & 1;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: DMA targets are scalar
+    const uint32_t K = p.k, M = p.m, N = p.n;
+    const uint32_t ntN = (N + GD_BN - 1) / GD_BN;
+    const uint32_t m0 = (blockIdx.x / ntN) * GD_BM, n0 = (blockIdx.x % ntN) * GD_BN;
+    const uint32_t ldsBase = lds_address(smem);
+
+    // this wave's twelve DMA blocks of a step: block j is operand j / 4 (a hi,
+    // a lo, w), rows 16 (4 w + j % 4) .. + 15 of its tile; lane l takes row
+    // + l / 4, LDS chunk l % 4, which holds the row's chunk (l % 4) ^ s(l / 4).
+    // Rows past M or N read the last row: they only reach outputs past M or
+    // N, which are not stored.
+    uint32_t doff[12];
+#pragma unroll
+    for (int j = 0; j < 12; ++j) {
+        const uint32_t row = 16u * (4u * uint32_t(w) + (j & 3)) + uint32_t(lane >> 2);
+        const uint32_t chunk = uint32_t(lane & 3) ^ uint32_t(((lane >> 3) & 3) ^ (lane >> 5));
+        const uint32_t g = (j < 8 ? m0 : n0) + row, lim = j < 8 ? M : N;
+        doff[j] = ((g < lim ? g : lim - 1) * K + 8 * chunk) * 2;
+    }
+    const uint8_t* const bases[3] = {reinterpret_cast<const uint8_t*>(ahi), reinterpret_cast<const uint8_t*>(alo),
+                                     static_cast<const uint8_t*>(p.w)};
+    auto dma = [&](uint32_t kt, int j) __attribute__((always_inline)) {
+        const uint32_t stage = kt % GD_STAGES;
+        dma_block(bases[j >> 2] + size_t(kt) * GD_BK * 2, doff[j],
+                  ldsBase + stage * GD_STAGE + (j >> 2) * GD_OPB + (4 * w + (j & 3)) * 1024);
+    };
+
+    floatx4 acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int fr = lane & 15, sw = 16 * ((lane >> 4) ^ ((fr >> 1) & 3) ^ (fr >> 3));   // swizzled chunk of k 8 (lane / 16) ..
+    const uint32_t nk = K / GD_BK;
+#pragma unroll
+    for (int j = 0; j < 12; ++j) dma(0, j);
+    if (nk > 1) {
+#pragma unroll
+        for (int j = 0; j < 12; ++j) dma(1, j);
+    }
+    // step kt; MORE: step kt + 2's DMA goes out between its row tiles
+    auto step = [&](uint32_t kt, auto MORE) __attribute__((always_inline)) {
+        // step kt's blocks have landed (in order: step kt + 1's may still be
+        // in flight); after the barrier every wave's have, and every read of
+        // the stage step kt + 2 goes into (that of step kt - 1) is done. Not
+        // __syncthreads(): its fence would wait for step kt + 1's blocks too.
+        if (kt + 1 < nk) gd_wait_vmcnt<12>();
+        else gd_wait_vmcnt<0>();
+        lds_barrier();
+        const uint8_t* st = smem + (kt % GD_STAGES) * GD_STAGE;
+        bf16x8 bh[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            bh[j] = *reinterpret_cast<const bf16x8*>(st + 2 * GD_OPB + (128 * wn + 16 * j + fr) * 64 + sw);
+        const int ro = (128 * wm + fr) * 64 + sw;
+        bf16x8 ah = *reinterpret_cast<const bf16x8*>(st + ro);
+        bf16x8 al = *reinterpret_cast<const bf16x8*>(st + GD_OPB + ro);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {   // row tile i + 1's a operands are read while tile i computes
+            bf16x8 nh = ah, nl = al;
+            if (i < 7) {
+                nh = *reinterpret_cast<const bf16x8*>(st + ro + (i + 1) * 1024);
+                nl = *reinterpret_cast<const bf16x8*>(st + GD_OPB + ro + (i + 1) * 1024);
+            }
+            if constexpr (decltype(MORE)::value) {   // the 12 blocks over the 8 row tiles: two, one, two, ...
+                dma(kt + 2, 3 * (i / 2) + 2 * (i & 1));
+                if (!(i & 1)) dma(kt + 2, 3 * (i / 2) + 1);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh[j], acc[i][j], 0, 0, 0);
+            }
+            ah = nh;
+            al = nl;
+        }
+    };
+    uint32_t kt = 0;
+    for (; kt + 2 < nk; ++kt) step(kt, std::integral_constant<bool, true>{});
+    for (; kt < nk; ++kt) step(kt, std::integral_constant<bool, false>{});
+    // the accumulator layout: lane holds rows 4 (lane / 16) + r of column lane % 16
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t n = n0 + 128 * wn + 16 * j + fr;
+        if (n >= N) continue;
+        const float b = p.bias ? p.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t m = m0 + 128 * wm + 16 * i + 4 * (lane >> 4) + r;
+                if (m >= M) continue;
+                float* o = p.out + size_t(m) * p.ldo + n;
+                *o = (p.accumulate ? *o : 0.0f) + acc[i][j][r] + b;
+            }
+    }
+}
+
 /* the K slices' partial tiles added in slice order, then the bias and the
    accumulate: out[m][n] (+)= sum_s part[s][m][n] + bias[n] */
 __global__ __launch_bounds__(256) void split_reduce_kernel(GemvParams p, const float* part, uint32_t slices) {
@@ -421,6 +567,29 @@ bool launch_type(Context& ctx, const GemvParams& p, hipStream_t stream) {
             });
         }
         return ctx.fail("matmul: quantised weights need k a multiple of 32 and 16-byte aligned rows");
+    }
+    if constexpr (TYPE == 1) {
+        // 256 x 256 tiles once there are enough of them to fill the CUs: a
+        // split into bf16 high parts and residuals first
+        const uint64_t wide = uint64_t((p.m + GD_BM - 1) / GD_BM) * ((p.n + GD_BN - 1) / GD_BN);
+        const uint64_t aBytes = uint64_t(p.m) * p.k * 2;   // one bf16 image of a
+        if (p.k % GD_BK == 0 && wide >= 256 && wide <= 0x7FFFFFFFull && aBytes < (1ull << 32) &&
+            uint64_t(p.n) * p.k * 2 < (1ull << 32)) {
+            uint8_t* split = static_cast<uint8_t*>(ctx.grow(SLOT_GEMM_A, 2 * aBytes));
+            if (!split) return false;
+            bf16x8* hi = reinterpret_cast<bf16x8*>(split);
+            bf16x8* lo = reinterpret_cast<bf16x8*>(split + aBytes);
+            const uint64_t pieces = aBytes / 16;
+            const unsigned sg = unsigned((pieces + 255) / 256 < 8192 ? (pieces + 255) / 256 : 8192);
+            if (!ctx.launch("split_a_kernel", stream, [&] {
+                    hipLaunchKernelGGL(split_a_kernel, dim3(sg), dim3(256), 0, stream, p.a, hi, lo, pieces);
+                }))
+                return false;
+            return ctx.launch("gemm_dma_kernel", stream, [&] {
+                hipLaunchKernelGGL(gemm_dma_kernel, dim3(unsigned(wide)), dim3(256), 0, stream, p,
+                                   reinterpret_cast<const __bf16*>(hi), reinterpret_cast<const __bf16*>(lo));
+            });
+        }
     }
     if (p.m >= GEMM_MIN_M) {
         const uint32_t tiles = ((p.n + GM_BN - 1) / GM_BN) * ((p.m + GM_BM - 1) / GM_BM);

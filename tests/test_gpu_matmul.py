@@ -1,5 +1,7 @@
 """GPU parity of the projections (gemv_kernel for up to 15 rows of a,
-gemm_kernel on MFMA from 16, behind aigpu_matmul_nt* and aigpu_matmul_device)
+gemm_kernel on MFMA from 16, split_a_kernel and gemm_dma_kernel for bf16
+weights with enough 256 x 256 tiles, behind aigpu_matmul_nt* and
+aigpu_matmul_device)
 against the oracle's restatement of apply
 (LocalModel.hpp:1052-1078) over the reference's weight encodings.
 
@@ -160,3 +162,25 @@ def test_gemm_ragged_tiles(gpu, kind, k):
     want = O.matmul_nt(a, w, kind, scales=scales, bias=bias)
     err = np.abs(host(out) - want)
     assert np.all(err <= bound(a, dense)), f"{kind}: max err {err.max()}"
+
+
+@pytest.mark.parametrize("k,accumulate", [(32, False), (96, True), (128, False)])
+def test_gemm_wide_tiles(gpu, k, accumulate):
+    """bf16 weights with enough 256 x 256 tiles for split_a_kernel and
+    gemm_dma_kernel (17 x 16 of them here, the last row and column of tiles
+    ragged; one, three and four K steps through its three-stage ring), bias,
+    and a residual add into a strided output"""
+    import torch
+    m, n, ld = 4100, 4000, 4008
+    a = O.fill_normal((m, k), 61, "a")
+    w, _, dense = weights(n, k, "bf16", 62)
+    bias = O.fill_normal((n,), 63, "bias")
+    base = O.fill_normal((m, ld), 64, "base") if accumulate else np.zeros((m, ld), np.float32)
+    out = dev_f32(base)
+    say("gemm wide", dict(m=m, k=k, n=n, accumulate=accumulate))
+    gpu.matmul(dev_f32(a), to_device(w), out[:, :n], "bf16", bias=dev_f32(bias), accumulate=accumulate)
+    got = host(out)
+    want = base[:, :n] + O.matmul_nt(a, w, "bf16", bias=bias)
+    err = np.abs(got[:, :n] - want)
+    assert np.all(err <= bound(a, dense) + 1e-6), f"max err {err.max()}"
+    np.testing.assert_array_equal(got[:, n:], base[:, n:])
