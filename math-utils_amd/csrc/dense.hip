@@ -43,7 +43,7 @@ namespace aigpu {
 
 namespace {
 
-constexpr int SPLIT = 128;     // positions per attention workgroup
+constexpr int PW_MAX = 40;     // positions per wave and pass of the attention
 constexpr int MAX_DIM = 256;   // head dim
 constexpr int MAX_GROUP = 8;   // query heads per kv head
 
@@ -192,14 +192,17 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseGemvArgs p) {
 }
 
 /* ---- attention ----
-   Keys [first(pos), pos] in chunks of SPLIT positions, the chunks dealt out
-   to at most MAX_SPLITS workgroups per kv head (chunksPer each, an online
-   softmax across them). Workgroup (split s, kv head):
+   Keys [first(pos), pos] in `splits` contiguous ranges of P positions per kv
+   head (the last one shorter), one workgroup each: at most 256 workgroups
+   (one per CU: 264 for 33 ranges of 128 put two on eight CUs, whose waves
+   then set the kernel's length) and at least 32 positions per range. A
+   workgroup takes its range in passes of at most 4 x PW_MAX positions,
+   with an online softmax across them. Workgroup (split s, kv head):
    - norms and rotates the G query heads of the kv head itself (attentionMixer,
      LocalModel.hpp:2606-2648) and, in the split holding `pos`, the new key,
      appending it and the value row to the cache;
-   - per chunk, each wave takes 32 of the positions with a softmax state of
-     its own (no barrier inside the chunk loop): every key and value load of
+   - per pass, each wave takes a quarter of the positions (up to PW_MAX)
+     with a softmax state of its own (no barrier inside the pass loop): every key and value load of
      the wave is issued before anything waits, the keys eight lanes to a row
      so that one load instruction covers 8 rows x 128 contiguous bytes;
      scores, probabilities and P.V stay in the wave's registers;
@@ -209,12 +212,20 @@ constexpr int MAX_SPLITS = 64;
 constexpr int REC_PAD = 4;   // max, sum, two unused floats before acc
 constexpr int BUFFER_FLAGS = 0x00020000;   // buffer descriptor word 3: 32-bit data format, raw (stride 0) access
 
-__device__ __forceinline__ void attn_span(uint32_t pos, uint32_t window, uint32_t& first, uint32_t& splits,
-                                          uint32_t& chunksPer) {
+constexpr uint32_t MIN_RANGE = 32;   // positions per split, at least
+
+/* the attention's ranges at `pos`: positions [first, pos], `splits` of them
+   per kv head, P positions each (the last one what is left, at least one:
+   splits (splits - 1) < pos + 1 - first for every splits this picks) */
+__host__ __device__ __forceinline__ void attn_span(uint32_t pos, uint32_t window, uint32_t kvHeads, uint32_t& first,
+                                                   uint32_t& splits, uint32_t& P) {
     first = window && pos + 1 > window ? pos + 1 - window : 0;
-    const uint32_t chunks = (pos + 1 - first + SPLIT - 1) / SPLIT;
-    chunksPer = (chunks + MAX_SPLITS - 1) / MAX_SPLITS;
-    splits = (chunks + chunksPer - 1) / chunksPer;
+    const uint32_t range = pos + 1 - first;
+    uint32_t target = 256 / kvHeads;
+    target = target < 1 ? 1 : (target > uint32_t(MAX_SPLITS) ? uint32_t(MAX_SPLITS) : target);
+    const uint32_t most = (range + MIN_RANGE - 1) / MIN_RANGE;
+    splits = most < target ? most : target;
+    P = (range + splits - 1) / splits;
 }
 
 /* the sum over each group of 8 lanes (lanes 8i .. 8i + 7), in every lane of
@@ -245,10 +256,13 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
                                                          const float* vRaw, const float* qNorm, const float* kNorm,
                                                          const float* freqs, float* keys, float* values,
                                                          float* partial) {
-    constexpr int KE = 2 * DPL;     // 16-byte key pieces per lane and row (32 floats apart)
-    constexpr int RG = 4;           // groups of 8 rows
-    constexpr int PW = SPLIT / 4;   // rows per wave and chunk
-    static_assert(PW == RG * 8, "a wave's rows are RG groups of 8");
+    constexpr int KE = 2 * DPL;   // 16-byte key pieces per lane and row (32 floats apart)
+    // rows per wave and pass, at most: 40, or 32 where the query heads' state
+    // would not fit the registers (a range past 128 positions then takes two
+    // passes)
+    constexpr int PW = DPL * GMAX <= 8 ? PW_MAX : 32;
+    constexpr int RG = PW / 8;    // groups of 8 rows
+    static_assert(PW == RG * 8 && PW <= PW_MAX, "a wave's rows are RG groups of 8");
     constexpr int QPT = GMAX * MAX_DIM / 256;   // query floats per thread, at most
     __shared__ __align__(16) float qs[GMAX * MAX_DIM];
     __shared__ __align__(16) float kn[MAX_DIM];
@@ -258,8 +272,8 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
     __shared__ __align__(16) float wacc[4][GMAX * MAX_DIM];
 
     const uint32_t pos = *a.pos;
-    uint32_t first, splits, chunksPer;
-    attn_span(pos, a.window, first, splits, chunksPer);
+    uint32_t first, splits, P;
+    attn_span(pos, a.window, a.kvHeads, first, splits, P);
     const uint32_t s = blockIdx.x, kvh = blockIdx.y;
     if (s >= splits) return;   // whole workgroup leaves before any barrier
     const uint32_t G = a.heads / a.kvHeads, D = a.dim;
@@ -306,43 +320,55 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
 #pragma unroll
         for (int e = 0; e < DPL; ++e) acc[g][e] = 0.0f;
     }
-    const uint32_t cBegin = s * chunksPer;
+    // this split's positions [j0s, j0s + rows), in passes of R (a quarter to each wave)
+    const uint32_t j0s = first + s * P;
+    const uint32_t rows = pos + 1 - j0s < P ? pos + 1 - j0s : P;
+    const uint32_t passes = (rows + 4 * PW - 1) / (4 * PW);
+    const uint32_t R = (rows + passes - 1) / passes;
+    const uint32_t pw = (R + 3) / 4;   // rows per wave, <= PW
 #pragma unroll 1
-    for (uint32_t c = cBegin; c < cBegin + chunksPer; ++c) {
-        const uint32_t j0 = first + c * SPLIT;
-        if (j0 > pos) break;   // uniform: the last split may hold fewer chunks
-        const uint32_t n = pos + 1 - j0 < uint32_t(SPLIT) ? pos + 1 - j0 : uint32_t(SPLIT);
-        const uint32_t jp = pos - j0 < n ? pos - j0 : 0xFFFFFFFFu;   // the new position, if in this chunk
-        const uint32_t r0 = uint32_t(w) * PW;                        // the wave's rows r0 .. r0 + PW - 1
+    for (uint32_t c = 0; c < passes; ++c) {
+        const uint32_t j0 = j0s + c * R;
+        const uint32_t n = rows - c * R < R ? rows - c * R : R;      // positions in this pass
+        const uint32_t jp = pos - j0 < n ? pos - j0 : 0xFFFFFFFFu;   // the new position, if in this pass
+        const uint32_t r0 = uint32_t(w) * pw;                        // the wave's rows r0 .. r0 + pw - 1
+        auto live = [&](uint32_t u) { return u < pw && r0 + u < n; };
 
-        // every key and value load of the wave's rows; rows past n read row 0
-        // of the chunk (finite: the cache is zeroed at creation) and are masked
+        // every key and value load of the wave's rows; rows not live read row 0
+        // of the pass (finite: the cache is zeroed at creation) and are masked
         floatx4 k4[RG][KE];
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) {
-            const uint32_t r = r0 + 8 * rg + rl;
-            const uint32_t off = (j0 + (r < n ? r : 0)) * rowBytes + kOff;
+            const uint32_t u = 8 * rg + rl;
+            const uint32_t off = (j0 + (live(u) ? r0 + u : 0)) * rowBytes + kOff;
 #pragma unroll
             for (int e = 0; e < KE; ++e)
                 k4[rg][e] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(krs, off + 128 * e, 0, 2));
         }
         float vv[PW][DPL];
+        // value rows from the wave's first row on, in a lane offset; row u in the
+        // scalar offset. Rows past the wave's pw are not read (zeros); the
+        // last wave's rows past n are read as they are (later positions' rows,
+        // zero rows never written, or past the descriptor's end, where the
+        // load returns 0: finite, and their probabilities are 0)
+        const uint32_t vRow0 = vOff + (j0 + r0) * rowBytes;
 #pragma unroll
         for (int u = 0; u < PW; ++u) {
-            const uint32_t r = r0 + u;   // uniform: the row goes in the scalar offset
-            const uint32_t rowOff = (j0 + (r < n ? r : 0)) * rowBytes;
-            if constexpr (DPL == 2) {
-                const float2 t = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(vrs, vOff, rowOff, 2));
+            if (uint32_t(u) >= pw) {   // uniform
+#pragma unroll
+                for (int e = 0; e < DPL; ++e) vv[u][e] = 0.0f;
+            } else if constexpr (DPL == 2) {
+                const float2 t = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(vrs, vRow0, u * rowBytes, 2));
                 vv[u][0] = t.x;
                 vv[u][1] = t.y;
             } else {
-                const floatx4 t = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vOff, rowOff, 2));
+                const floatx4 t = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vRow0, u * rowBytes, 2));
 #pragma unroll
                 for (int e = 0; e < DPL; ++e) vv[u][e] = t[e];
             }
         }
 
-        if (c == cBegin) {   // uniform: the query rows normed and rotated while the loads are in flight
+        if (c == 0) {   // uniform: the query rows normed and rotated while the loads are in flight
 #pragma unroll
             for (int t = 0; t < QPT; ++t) {
                 const uint32_t i = uint32_t(tid) + 256 * t;
@@ -364,7 +390,7 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
             }
             lds_barrier();
         }
-        if (jp - r0 < uint32_t(PW)) {   // uniform: the new position is one of this wave's rows; from LDS
+        if (jp - r0 < pw) {   // uniform: the new position is one of this wave's rows; from LDS
             const uint32_t ju = jp - r0;
 #pragma unroll
             for (int rg = 0; rg < RG; ++rg)
@@ -406,7 +432,7 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
             float m = -INFINITY;
 #pragma unroll
             for (int rg = 0; rg < RG; ++rg) {
-                sc[rg] = r0 + 8 * rg + rl < n ? sum8(sc[rg]) * scale : -INFINITY;
+                sc[rg] = live(uint32_t(8 * rg + rl)) ? sum8(sc[rg]) * scale : -INFINITY;
                 m = fmaxf(m, sc[rg]);
             }
             m = max_across8(m);
@@ -459,7 +485,7 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a, const floa
     const size_t rec = size_t(D) + REC_PAD;
     for (uint32_t i = tid; i < G * D; i += 256) {
         const uint32_t g = i / D, d = i - g * D;
-        // wave 0 always holds position first + s * chunksPer * SPLIT, so M is finite
+        // wave 0 always holds position j0s (pw >= 1), so M is finite
         const float M = fmaxf(fmaxf(wm[0][g], wm[1][g]), fmaxf(wm[2][g], wm[3][g]));
         float v = 0.0f;
 #pragma unroll
@@ -485,8 +511,8 @@ __global__ __launch_bounds__(256) void dense_merge_kernel(DenseArgs a, const flo
     constexpr int MAXT = MAX_SPLITS / 4;   // splits per thread when D = 256
     __shared__ floatx4 red[256];
     const uint32_t pos = *a.pos;
-    uint32_t first, splits, chunksPer;
-    attn_span(pos, a.window, first, splits, chunksPer);
+    uint32_t first, splits, P;
+    attn_span(pos, a.window, a.kvHeads, first, splits, P);
     const uint32_t g = blockIdx.x, kvh = blockIdx.y, G = a.heads / a.kvHeads, D = a.dim;
     const int tid = threadIdx.x, lane = tid & 63;
     const size_t rec = size_t(D) + REC_PAD;
@@ -670,11 +696,10 @@ bool dense_gemv(std::initializer_list<Seg> segs, const float* x, const float* x2
 }
 
 /* the workgroups per kv head of the attention of a step at `pos` */
-uint32_t host_splits(uint32_t pos, uint32_t window) {
-    const uint32_t first = window && pos + 1 > window ? pos + 1 - window : 0;
-    const uint32_t chunks = (pos + 1 - first + SPLIT - 1) / SPLIT;
-    const uint32_t per = (chunks + MAX_SPLITS - 1) / MAX_SPLITS;
-    return (chunks + per - 1) / per;
+uint32_t host_splits(uint32_t pos, uint32_t window, uint32_t kvHeads) {
+    uint32_t first, splits, P;
+    attn_span(pos, window, kvHeads, first, splits, P);
+    return splits;
 }
 
 /* the launches of one decode step; `splits` attention workgroups per kv head
@@ -719,8 +744,9 @@ bool run_step(DenseModel& d, uint32_t splits, hipStream_t stream) {
 }
 
 /* the step for `splits`, as a replayed graph: captured on first use of each
-   attention grid (the grid grows by one workgroup per kv head every 128
-   positions up to 64, so a sequence captures at most 64 graphs). Without
+   attention grid (the grid grows by one workgroup per kv head every 32
+   positions up to 256 / kvHeads, at most 64, so a sequence captures at most
+   64 graphs). Without
    graphs (AIGPU_DENSE_GRAPH=0, or profiling, whose per-launch events a graph
    cannot carry) the kernels are launched one by one. */
 bool launch_step(DenseModel& d, uint32_t splits) {
@@ -818,7 +844,7 @@ AIGPU_ABI void* aigpu_dense_create(const AiGpuDenseConfig* c, const AiGpuDenseLa
         d->gate = d->floats(c->intermediate);
         d->up = d->floats(c->intermediate);
         d->logits = d->floats(c->vocab);
-        d->maxSplits = aigpu::host_splits(c->capacity - 1, 0);
+        d->maxSplits = aigpu::host_splits(c->capacity - 1, 0, c->kvHeads);
         d->partial = d->floats(uint64_t(c->heads) * d->maxSplits * (c->headDim + aigpu::REC_PAD));
         d->pos = reinterpret_cast<uint32_t*>(d->floats(1));
         if (hipStreamCreate(&d->stream) != hipSuccess) {
@@ -893,7 +919,7 @@ AIGPU_ABI void aigpu_dense_decode(void* handle, const float* embedding, float* l
     // the attention grid covers the positions this step reads
     uint32_t splits = 1;
     for (const aigpu::DevLayer& L : d.layers) {
-        const uint32_t s = aigpu::host_splits(position, L.window);
+        const uint32_t s = aigpu::host_splits(position, L.window, c.kvHeads);
         if (s > splits) splits = s;
     }
     if (!aigpu::launch_step(d, splits)) return;
