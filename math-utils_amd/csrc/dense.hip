@@ -59,7 +59,7 @@ struct DenseArgs {
    PRE 2: a = silu(x) * x2 (swiglu, :3282-3288).
    Up to three weights of one encoding share the launch (q, k, v; gate, up):
    rows [start_s, start_s + n_s) belong to segment s. */
-constexpr int DG_ROWS = 2;   // weight rows per wave
+constexpr int DG_ROWS = 2;   // weight rows per wave, at most
 
 struct DenseSeg {
     const char* w;
@@ -85,32 +85,34 @@ constexpr int DG_BATCH = 8;       // weight pieces per lane and row loaded toget
 /* The workgroup first requests each wave's first DG_BATCH weight pieces,
    then builds the activation (PRE applied) once in LDS, then the waves dot
    their rows against it; k up to DG_LDS_K. */
-template <int TYPE, int PRE>
+template <int TYPE, int PRE, int ROWS>   // ROWS weight rows per wave: 2, or 1 for short weights
 __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseGemvArgs p) {
+    static_assert(ROWS == 1 || ROWS == DG_ROWS, "one or two rows per wave");
     constexpr int E = piece_elems<TYPE>();
     extern __shared__ __align__(16) float xa[];   // k floats
     __shared__ float part[4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const uint32_t row0 = (blockIdx.x * 4 + w) * DG_ROWS;
+    const uint32_t row0 = (blockIdx.x * 4 + w) * ROWS;
     const bool active = row0 < p.rows;
     int sg = 0;
     if (p.nseg > 1 && row0 >= p.seg[1].start) sg = 1;
     if (p.nseg > 2 && row0 >= p.seg[2].start) sg = 2;
     const DenseSeg S = p.seg[sg];
-    const uint32_t r0 = active ? row0 - S.start : 0;   // DG_ROWS rows never straddle segments (every n is even)
+    const uint32_t r0 = active ? row0 - S.start : 0;   // ROWS rows never straddle segments (every n is even)
     const size_t rowBytes = size_t(p.k) * row_bytes_per_k_x2<TYPE>() / 2;
     const uint32_t pieces = p.k / E, blocks = p.k / 32;
     const uint32_t rr1 = r0 + 1 < S.n ? r0 + 1 : r0;   // a row count that is odd repeats the last row
 
     // the first batch of weight pieces, before anything waits (nontemporal:
     // each weight byte is read once per token)
-    u32x4 wv[DG_BATCH][DG_ROWS];
+    u32x4 wv[DG_BATCH][ROWS];
 #pragma unroll
     for (int b = 0; b < DG_BATCH; ++b) {
         const uint32_t c = lane + WAVE * b;
         if (active && c < pieces) {
             wv[b][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(S.w + r0 * rowBytes + size_t(c) * 16));
-            wv[b][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(S.w + rr1 * rowBytes + size_t(c) * 16));
+            if constexpr (ROWS == 2)
+                wv[b][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(S.w + rr1 * rowBytes + size_t(c) * 16));
         }
     }
 
@@ -146,7 +148,7 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseGemvArgs p) {
     __syncthreads();
     if (!active) return;
 
-    float acc[DG_ROWS] = {};
+    float acc[ROWS] = {};
     const float* s0 = TYPE >= 2 ? S.scales + size_t(r0) * blocks : nullptr;
     const float* s1 = TYPE >= 2 ? S.scales + size_t(rr1) * blocks : nullptr;
     for (uint32_t c0 = 0; c0 < pieces; c0 += WAVE * DG_BATCH) {
@@ -156,7 +158,8 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseGemvArgs p) {
                 const uint32_t c = c0 + lane + WAVE * b;
                 if (c < pieces) {
                     wv[b][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(S.w + r0 * rowBytes + size_t(c) * 16));
-                    wv[b][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(S.w + rr1 * rowBytes + size_t(c) * 16));
+                    if constexpr (ROWS == 2)
+                        wv[b][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(S.w + rr1 * rowBytes + size_t(c) * 16));
                 }
             }
         }
@@ -165,26 +168,22 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(DenseGemvArgs p) {
             const uint32_t c = c0 + lane + WAVE * b;
             if (c < pieces) {
                 const float* x = xa + size_t(c) * E;
-                const float d0 = piece_dot<TYPE>(wv[b][0], x), d1 = piece_dot<TYPE>(wv[b][1], x);
-                if constexpr (TYPE == 2) {
-                    acc[0] = fmaf(d0, s0[c >> 1], acc[0]);
-                    acc[1] = fmaf(d1, s1[c >> 1], acc[1]);
-                } else if constexpr (TYPE == 3) {
-                    acc[0] = fmaf(d0, s0[c], acc[0]);
-                    acc[1] = fmaf(d1, s1[c], acc[1]);
-                } else {
-                    acc[0] += d0;
-                    acc[1] += d1;
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) {
+                    const float d = piece_dot<TYPE>(wv[b][r], x);
+                    if constexpr (TYPE == 2) acc[r] = fmaf(d, (r ? s1 : s0)[c >> 1], acc[r]);
+                    else if constexpr (TYPE == 3) acc[r] = fmaf(d, (r ? s1 : s0)[c], acc[r]);
+                    else acc[r] += d;
                 }
             }
         }
     }
 #pragma unroll
-    for (int r = 0; r < DG_ROWS; ++r) acc[r] = wave_sum(acc[r]);
-    if (lane < DG_ROWS) {
+    for (int r = 0; r < ROWS; ++r) acc[r] = wave_sum(acc[r]);
+    if (lane < ROWS) {
         const uint32_t n = r0 + lane;
         if (n < S.n) {
-            const float v = lane == 0 ? acc[0] : acc[DG_ROWS - 1];
+            const float v = lane == 0 ? acc[0] : acc[ROWS - 1];
             float* o = S.out + n;
             *o = (p.accumulate ? *o : 0.0f) + v + (S.bias ? S.bias[n] : 0.0f);
         }
@@ -650,8 +649,15 @@ struct Seg {
 
 template <int TYPE, int PRE>
 void launch_dense_gemv(const DenseGemvArgs& p, hipStream_t stream) {
-    const unsigned grid = unsigned((p.rows + 4 * DG_ROWS - 1) / (4 * DG_ROWS));
-    hipLaunchKernelGGL((dense_gemv_kernel<TYPE, PRE>), dim3(grid), dim3(256), size_t(p.k) * sizeof(float), stream, p);
+    // one row per wave where two would leave CUs without a workgroup
+    const uint32_t grid2 = (p.rows + 4 * DG_ROWS - 1) / (4 * DG_ROWS);
+    if (grid2 < 256) {
+        hipLaunchKernelGGL((dense_gemv_kernel<TYPE, PRE, 1>), dim3((p.rows + 3) / 4), dim3(256), size_t(p.k) * sizeof(float),
+                           stream, p);
+    } else {
+        hipLaunchKernelGGL((dense_gemv_kernel<TYPE, PRE, DG_ROWS>), dim3(grid2), dim3(256), size_t(p.k) * sizeof(float),
+                           stream, p);
+    }
 }
 
 /* one launch for weights of one encoding whose row counts are even (rows
