@@ -425,7 +425,12 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemvParams p, const __bf1
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: DMA targets are scalar
     const uint32_t K = p.k, M = p.m, N = p.n;
     const uint32_t ntN = (N + GD_BN - 1) / GD_BN;
-    const uint32_t m0 = (blockIdx.x / ntN) * GD_BM, n0 = (blockIdx.x % ntN) * GD_BN;
+    // consecutive workgroups go to different XCDs: remap them so that each XCD
+    // takes a band of whole rows of tiles (its L2 then holds a band of a and
+    // every XCD reads w), when the tile count splits evenly over the eight
+    uint32_t lg = blockIdx.x;
+    if (gridDim.x % 8 == 0) lg = (lg % 8) * (gridDim.x / 8) + lg / 8;
+    const uint32_t m0 = (lg / ntN) * GD_BM, n0 = (lg % ntN) * GD_BN;
     const uint32_t ldsBase = lds_address(smem);
 
     // this wave's twelve DMA blocks of a step: block j is operand j / 4 (a hi,
