@@ -124,13 +124,22 @@ def test_llama_layers_with_biases_window_and_partial_rotary(gpu):
 
 
 def test_long_history_crosses_attention_splits(gpu):
-    """a cache of several 128-position attention workgroups"""
+    """a cache dealt over several attention workgroups (19 ranges of 32)"""
     run(gpu, "bf16", length=600, steps=2, capacity=620)
 
 
-def test_very_long_history_puts_several_chunks_in_a_split(gpu):
-    """past 64 x 128 positions each attention workgroup takes two chunks or more"""
+def test_very_long_history_fills_every_split(gpu):
+    """64 ranges of 130 positions (one pass of up to 160 each), and a window
+    of 3000 in 64 ranges of 47"""
     run(gpu, "bf16", length=8300, steps=2, capacity=8310, windows=(0, 3000))
+
+
+@pytest.mark.parametrize("length,heads", [
+    (10300, 4),   # 64 ranges of 161: two passes of up to 160 positions
+    (8300, 16),   # eight query heads per kv head, 32 rows per wave: two passes for 130
+])
+def test_ranges_take_several_passes(gpu, length, heads):
+    run(gpu, "bf16", length=length, steps=2, capacity=length + 10, shape=dict(heads=heads, kv_heads=2))
 
 
 @pytest.mark.parametrize("heads,kv_heads,head_dim", [
