@@ -6,7 +6,12 @@
 // This is the exact-arithmetic path behind the drop-in aigpu_attention: fp32
 // loads, fp32 FMAs, expf. One wave owns one (token, head) and walks the keys
 // in blocks of 64 with an online softmax: lane j scores key j of the block,
-// then the lanes switch to owning dimensions for the P.V accumulation.
+// then the lanes switch to owning dimensions for the P.V accumulation. Both
+// loops issue their loads in batches before using them (a key row as up to
+// 16 16-byte pieces per lane with four partial sums when rows are 16-byte
+// aligned; value rows as 16-byte pieces, several rows per load instruction,
+// or else eight rows at a time), so that a block costs a few memory round
+// trips rather than one per dimension or per key.
 #include "context.hpp"
 #include "device.hpp"
 #include "kernels.hpp"
@@ -18,7 +23,7 @@ namespace {
 constexpr int MAX_DIM = 256;
 
 __global__ __launch_bounds__(256) void attention_f32_kernel(AttentionF32Params p) {
-    __shared__ float qs[4][MAX_DIM];
+    __shared__ __align__(16) float qs[4][MAX_DIM];
     __shared__ float ps[4][WAVE];
 
     const int lane = threadIdx.x & (WAVE - 1);
@@ -40,6 +45,22 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(AttentionF32Params p
     const size_t kvBase = kv * p.headStride;
     float m = -INFINITY, l = 0.0f;
     float acc[MAX_DIM / WAVE] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // key rows in 16-byte pieces: every row start (and q's copy in LDS) on a
+    // 16-byte boundary, which fp32 rows with dim % 4 == 0 and bf16 rows with
+    // dim % 8 == 0 and strides to match give
+    const size_t esz = p.kvType == 0 ? 4 : 2, per = 16 / esz;
+    const bool vec = dim % int(per) == 0 && (reinterpret_cast<uintptr_t>(p.keys) % 16) == 0 &&
+                     (kvBase * esz) % 16 == 0 && (p.posStride * esz) % 16 == 0;
+    // fp32 value rows of dim / 4 16-byte pieces, a power of two: LPR lanes per
+    // row, RPI = 64 / LPR rows per load instruction, each lane a four-float
+    // accumulator for its piece and its group of rows (summed across the
+    // groups at the end); up to 16 pieces per lane in flight
+    const int LPR = dim / 4;
+    const bool vecv = p.kvType == 0 && dim % 4 == 0 && (LPR & (LPR - 1)) == 0 &&
+                      (reinterpret_cast<uintptr_t>(p.values) % 16) == 0 && (kvBase * 4) % 16 == 0 &&
+                      (p.posStride * 4) % 16 == 0;
+    const int RPI = vecv ? WAVE / LPR : 1, vg = vecv ? lane / LPR : 0, vc = vecv ? lane % LPR : 0;
+    floatx4 acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
 
     for (uint64_t j0 = first; j0 <= position; j0 += WAVE) {
         const uint64_t j = j0 + lane;
@@ -48,7 +69,51 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(AttentionF32Params p
         if (ok) {
             const size_t row = kvBase + j * p.posStride;
             float dot = 0.0f;
-            if (p.kvType == 0) {
+            if (vec && p.kvType == 0) {
+                // up to 64 dimensions per batch: 16 pieces in flight, four partial sums
+                const floatx4* kr = reinterpret_cast<const floatx4*>(static_cast<const float*>(p.keys) + row);
+                const floatx4* q4 = reinterpret_cast<const floatx4*>(qs[w]);
+                floatx4 part = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int c0 = 0; c0 < dim / 4; c0 += 16) {
+                    floatx4 kp[16];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (c0 + i < dim / 4) kp[i] = kr[c0 + i];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (c0 + i < dim / 4) {
+                            const floatx4 qv = q4[c0 + i];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) part[e] = fmaf(qv[e], kp[i][e], part[e]);
+                        }
+                }
+                dot = (part[0] + part[1]) + (part[2] + part[3]);
+            } else if (vec) {
+                // bf16: eight elements per piece, up to 128 dimensions per batch
+                const u32x4* kr = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.keys) + row);
+                const floatx4* q4 = reinterpret_cast<const floatx4*>(qs[w]);
+                floatx4 part = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int c0 = 0; c0 < dim / 8; c0 += 16) {
+                    u32x4 kp[16];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (c0 + i < dim / 8) kp[i] = kr[c0 + i];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (c0 + i < dim / 8) {
+                            const floatx4 qa = q4[2 * (c0 + i)], qb = q4[2 * (c0 + i) + 1];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const uint32_t wv = kp[i][e];
+                                const float lo = __uint_as_float(wv << 16), hi = __uint_as_float(wv & 0xFFFF0000u);
+                                const float q0 = e < 2 ? qa[2 * e] : qb[2 * e - 4];
+                                const float q1 = e < 2 ? qa[2 * e + 1] : qb[2 * e - 3];
+                                part[e] = fmaf(q1, hi, fmaf(q0, lo, part[e]));
+                            }
+                        }
+                }
+                dot = (part[0] + part[1]) + (part[2] + part[3]);
+            } else if (p.kvType == 0) {
                 const float* kr = static_cast<const float*>(p.keys) + row;
                 for (int d = 0; d < dim; ++d) dot = fmaf(qs[w][d], kr[d], dot);
             } else {
@@ -64,17 +129,50 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(AttentionF32Params p
         m = mn;
 #pragma unroll
         for (int i = 0; i < MAX_DIM / WAVE; ++i) acc[i] *= alpha;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc2[e] *= alpha;
 
         ps[w][lane] = pj;
         wave_sync();
         const int nb = int(position + 1 - j0 < WAVE ? position + 1 - j0 : WAVE);
-        for (int jj = 0; jj < nb; ++jj) {
-            const float pv = ps[w][jj];
-            const size_t row = kvBase + (j0 + jj) * p.posStride;
+        if (vecv) {
+            const floatx4* vb = reinterpret_cast<const floatx4*>(static_cast<const float*>(p.values) + kvBase) + vc;
+            const size_t rs = p.posStride / 4;
+            for (int t0 = 0; t0 < LPR; t0 += 16) {
+                floatx4 vp[16];
 #pragma unroll
-            for (int i = 0; i < MAX_DIM / WAVE; ++i) {
-                const int d = lane + i * WAVE;
-                if (d < dim) acc[i] = fmaf(pv, load_elem(p.values, row + d, p.kvType), acc[i]);
+                for (int u = 0; u < 16; ++u) {
+                    const int r = (t0 + u) * RPI + vg;
+                    vp[u] = t0 + u < LPR && r < nb ? vb[(j0 + uint64_t(r)) * rs] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const int r = (t0 + u) * RPI + vg;
+                    if (t0 + u < LPR && r < nb) {
+                        const float pv = ps[w][r];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc2[e] = fmaf(pv, vp[u][e], acc2[e]);
+                    }
+                }
+            }
+        }
+        for (int jb = 0; !vecv && jb < nb; jb += 8) {   // eight value rows' loads in flight
+            float vr[8][MAX_DIM / WAVE];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const size_t row = kvBase + (j0 + jb + u) * p.posStride;
+#pragma unroll
+                for (int i = 0; i < MAX_DIM / WAVE; ++i) {
+                    const int d = lane + i * WAVE;
+                    vr[u][i] = jb + u < nb && d < dim ? load_elem(p.values, row + d, p.kvType) : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (jb + u >= nb) break;   // uniform
+                const float pv = ps[w][jb + u];
+#pragma unroll
+                for (int i = 0; i < MAX_DIM / WAVE; ++i) acc[i] = fmaf(pv, vr[u][i], acc[i]);
             }
         }
         wave_sync();
@@ -82,6 +180,16 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(AttentionF32Params p
 
     const float inv = 1.0f / l;
     float* dst = p.out + task * p.dim;
+    if (vecv) {
+        for (int off = LPR; off < WAVE; off <<= 1)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc2[e] += __shfl_xor(acc2[e], off, WAVE);
+        if (vg == 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dst[4 * vc + e] = acc2[e] * inv;
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MAX_DIM / WAVE; ++i) {
         const int d = lane + i * WAVE;

@@ -58,6 +58,21 @@ def test_long_context_single_token(gpu):
     assert_f32_parity(ref, got, "long")
 
 
+@pytest.mark.parametrize("dim", [4, 32, 256, 36])
+def test_value_row_groups(gpu, dim):
+    """fp32 value rows read as 16-byte pieces, dim / 4 lanes per row (1, 8 and
+    64 lanes; 9 lanes is not a power of two and takes the row-by-row path),
+    with history so blocks of 64 keys are partly filled"""
+    T, S, H, KV = 9, 70, 4, 2
+    q = O.fill_normal((T, H, dim), 41, "q")
+    k = O.fill_normal((S + T, KV, dim), 42, "k")
+    v = O.fill_normal((S + T, KV, dim), 43, "v")
+    ref = O.attention(q, k, v, T, S, H, KV, dim, dim)
+    say("value row groups", dim)
+    got = gpu.attention(q, k, v, T, S, H, KV, dim, dim)
+    assert_f32_parity(ref, got, f"dim {dim}")
+
+
 def test_device_form_head_major_bf16_cache(gpu):
     """one entry serves the head-major bf16 cache through explicit strides"""
     import torch
