@@ -142,6 +142,13 @@ def test_ranges_take_several_passes(gpu, length, heads):
     run(gpu, "bf16", length=length, steps=2, capacity=length + 10, shape=dict(heads=heads, kv_heads=2))
 
 
+@pytest.mark.parametrize("kind", ["bf16", "q4"])
+def test_long_odd_head(gpu, kind):
+    """a vocabulary of 70001 rows (8751 workgroups, the last wave's second row
+    repeating the last one)"""
+    run(gpu, kind, steps=2, shape=dict(vocab=70001))
+
+
 @pytest.mark.parametrize("heads,kv_heads,head_dim", [
     (4, 4, 64),     # one query head per kv head
     (6, 2, 96),     # three, and a head dim that leaves key pieces and value lanes idle
