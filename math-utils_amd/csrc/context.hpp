@@ -32,6 +32,7 @@ enum ScratchSlot {
     SLOT_INDEXER,        // index keys, queries, head weights and scores of selectKeys
     SLOT_GEMM_SPLIT,     // the K slices' partial tiles of a split GEMM
     SLOT_GEMM_A,         // a split into bf16 high parts and residuals for gemm_dma_kernel
+    SLOT_MIXER_KV,       // fp32 k and v projections of a prefill mixer before their epilogue
     SLOT_COUNT
 };
 

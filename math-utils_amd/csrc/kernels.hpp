@@ -120,6 +120,14 @@ struct KvEpilogue {
     uint32_t* rangeFlag;  // as PrefillParams::rangeFlag
 };
 bool launch_gemm_kv(const GemvParams& p, const KvEpilogue& e, hipStream_t stream);
+// whether launch_gemv splits p.a into the bf16 images a following
+// launch_gemm_kv_pair can reuse (aSplit)
+bool gemm_splits_a(const GemvParams& p);
+// the k and v projections of the same rows: one GEMM over both weights, then
+// the epilogue as its own kernel, where the shapes allow; otherwise two
+// launch_gemm_kv calls
+bool launch_gemm_kv_pair(const GemvParams& pk, const GemvParams& pv, const KvEpilogue& ek, const KvEpilogue& ev,
+                         bool aSplit, hipStream_t stream);
 
 // ---- attentionMixer for a prefill: projections, norm/RoPE/append, flash
 // attention, output gate, o projection ----

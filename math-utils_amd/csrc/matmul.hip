@@ -419,7 +419,10 @@ __device__ __forceinline__ void gd_wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-__global__ __launch_bounds__(256) void gemm_dma_kernel(GemvParams p, const __bf16* ahi, const __bf16* alo) {
+/* w2: columns from nSplit on come from w2's rows (n - nSplit), a multiple of
+   256 so that no tile straddles the two; null for one weight */
+__global__ __launch_bounds__(256) void gemm_dma_kernel(GemvParams p, const __bf16* ahi, const __bf16* alo,
+                                                       const void* w2, uint32_t nSplit) {
     __shared__ __align__(16) uint8_t smem[GD_STAGES * GD_STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wm = (tid >> 6) >> 1, wn = (tid >> 6) & 1;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: DMA targets are scalar
@@ -438,16 +441,18 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemvParams p, const __bf1
     // + l / 4, LDS chunk l % 4, which holds the row's chunk (l % 4) ^ s(l / 4).
     // Rows past M or N read the last row: they only reach outputs past M or
     // N, which are not stored.
+    const bool second = w2 && n0 >= nSplit;
+    const uint32_t wn0 = second ? n0 - nSplit : n0, wlim = w2 ? (second ? N - nSplit : nSplit) : N;
     uint32_t doff[12];
 #pragma unroll
     for (int j = 0; j < 12; ++j) {
         const uint32_t row = 16u * (4u * uint32_t(w) + (j & 3)) + uint32_t(lane >> 2);
         const uint32_t chunk = uint32_t(lane & 3) ^ uint32_t(((lane >> 3) & 3) ^ (lane >> 5));
-        const uint32_t g = (j < 8 ? m0 : n0) + row, lim = j < 8 ? M : N;
+        const uint32_t g = (j < 8 ? m0 : wn0) + row, lim = j < 8 ? M : wlim;
         doff[j] = ((g < lim ? g : lim - 1) * K + 8 * chunk) * 2;
     }
     const uint8_t* const bases[3] = {reinterpret_cast<const uint8_t*>(ahi), reinterpret_cast<const uint8_t*>(alo),
-                                     static_cast<const uint8_t*>(p.w)};
+                                     static_cast<const uint8_t*>(second ? w2 : p.w)};
     auto dma = [&](uint32_t kt, int j) __attribute__((always_inline)) {
         const uint32_t stage = kt % GD_STAGES;
         dma_block(bases[j >> 2] + size_t(kt) * GD_BK * 2, doff[j],
@@ -525,6 +530,62 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemvParams p, const __bf1
     }
 }
 
+/* The k and v projections' per-token work after one GEMM over both
+   (kv[m][0 .. N1) k, [N1 .. 2 N1) v, fp32): the bias, then for k RMSNorm
+   (gamma) and rotate-half RoPE (freqs), and each row appended to its bf16
+   cache and to the flash kernel's fp16 copy, as gemm_kernel's k / v
+   epilogue does (the same operations in the same order per element; the
+   norm's sum of squares is reduced in another order). One wave per (token,
+   kv head, k or v); the row staged in LDS for the RoPE partner. */
+__global__ __launch_bounds__(256) void kv_epilogue_kernel(const float* kv, const float* kBias, const float* vBias,
+                                                          KvEpilogue ek, KvEpilogue ev, uint32_t m, uint32_t heads) {
+    __shared__ float row[4][128];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint64_t task = uint64_t(blockIdx.x) * 4 + w;
+    if (task >= uint64_t(m) * heads * 2) return;   // whole wave leaves; no block barriers below
+    const uint32_t which = uint32_t(task % 2), h = uint32_t((task / 2) % heads), t = uint32_t(task / (2 * heads));
+    const KvEpilogue& e = which ? ev : ek;
+    const float* bias = which ? vBias : kBias;
+    const uint32_t D = e.dim, N1 = heads * D, EPL = D / 64;   // D 64 or 128
+    const float* src = kv + (size_t(t) * 2 + which) * N1 + size_t(h) * D;
+    float x[2], y[2];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t d = lane * EPL + i;
+        x[i] = uint32_t(i) < EPL ? src[d] + (bias ? bias[size_t(h) * D + d] : 0.0f) : 0.0f;
+        ss = fmaf(x[i], x[i], ss);
+    }
+    float inv = 1.0f;
+    if (e.gamma) inv = 1.0f / sqrtf(wave_sum(ss) / float(D) + e.eps);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t d = lane * EPL + i;
+        y[i] = e.gamma && uint32_t(i) < EPL ? x[i] * inv * (e.gamma[d] + e.offset) : x[i];
+        if (uint32_t(i) < EPL) row[w][d] = y[i];
+    }
+    wave_sync();
+    const uint32_t half = e.freqs ? e.rot / 2 : 0;
+    const uint32_t pos = e.start + t;
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t d = lane * EPL + i;
+        if (uint32_t(i) >= EPL) continue;
+        float v = y[i];
+        if (d < 2 * half) {   // rotate-half pairs (LocalModel.hpp:2624-2641), the angle float(pos) * freq
+            const bool low = d < half;
+            const uint32_t dp = low ? d + half : d - half;
+            float sn, cs;
+            sincosf(float(pos) * e.freqs[low ? d : dp], &sn, &cs);
+            v = low ? y[i] * cs - row[w][dp] * sn : y[i] * cs + row[w][dp] * sn;
+        }
+        e.cache[(size_t(h) * e.capacity + pos) * D + d] = float_to_bf16_bits(v);
+        static_cast<_Float16*>(e.work)[(size_t(h) * e.T + pos) * D + d] = to_f16_checked(v, bad);
+    }
+    raise_range_flag(e.rangeFlag, bad);
+}
+
 /* the K slices' partial tiles added in slice order, then the bias and the
    accumulate: out[m][n] (+)= sum_s part[s][m][n] + bias[n] */
 __global__ __launch_bounds__(256) void split_reduce_kernel(GemvParams p, const float* part, uint32_t slices) {
@@ -560,6 +621,40 @@ __global__ __launch_bounds__(256) void gemv_scalar_kernel(GemvParams p) {
     }
 }
 
+/* bf16 weights with at least 256 tiles of 256 x 256 (a and w under 4 GB,
+   k a multiple of 32) take split_a_kernel and gemm_dma_kernel */
+bool dma_eligible(const GemvParams& p) {
+    if (p.type != 1 || p.k % GD_BK || (reinterpret_cast<uintptr_t>(p.w) % 16) || (reinterpret_cast<uintptr_t>(p.a) % 16))
+        return false;
+    const uint64_t wide = uint64_t((p.m + GD_BM - 1) / GD_BM) * ((p.n + GD_BN - 1) / GD_BN);
+    return wide >= 256 && wide <= 0x7FFFFFFFull && uint64_t(p.m) * p.k * 2 < (1ull << 32) &&
+           uint64_t(p.n) * p.k * 2 < (1ull << 32);
+}
+
+/* a split into its bf16 high parts and residuals (scratch slot SLOT_GEMM_A),
+   unless `split` says the slot already holds them, then the DMA GEMM; w2 /
+   nSplit as gemm_dma_kernel */
+bool launch_dma(Context& ctx, const GemvParams& p, const void* w2, uint32_t nSplit, bool split, hipStream_t stream) {
+    const uint64_t wide = uint64_t((p.m + GD_BM - 1) / GD_BM) * ((p.n + GD_BN - 1) / GD_BN);
+    const uint64_t aBytes = uint64_t(p.m) * p.k * 2;   // one bf16 image of a
+    uint8_t* img = static_cast<uint8_t*>(ctx.grow(SLOT_GEMM_A, 2 * aBytes));
+    if (!img) return false;
+    bf16x8* hi = reinterpret_cast<bf16x8*>(img);
+    bf16x8* lo = reinterpret_cast<bf16x8*>(img + aBytes);
+    if (!split) {
+        const uint64_t pieces = aBytes / 16;
+        const unsigned sg = unsigned((pieces + 255) / 256 < 8192 ? (pieces + 255) / 256 : 8192);
+        if (!ctx.launch("split_a_kernel", stream, [&] {
+                hipLaunchKernelGGL(split_a_kernel, dim3(sg), dim3(256), 0, stream, p.a, hi, lo, pieces);
+            }))
+            return false;
+    }
+    return ctx.launch("gemm_dma_kernel", stream, [&] {
+        hipLaunchKernelGGL(gemm_dma_kernel, dim3(unsigned(wide)), dim3(256), 0, stream, p,
+                           reinterpret_cast<const __bf16*>(hi), reinterpret_cast<const __bf16*>(lo), w2, nSplit);
+    });
+}
+
 template <int TYPE>
 bool launch_type(Context& ctx, const GemvParams& p, hipStream_t stream) {
     constexpr int E = piece_elems<TYPE>();
@@ -574,27 +669,7 @@ bool launch_type(Context& ctx, const GemvParams& p, hipStream_t stream) {
         return ctx.fail("matmul: quantised weights need k a multiple of 32 and 16-byte aligned rows");
     }
     if constexpr (TYPE == 1) {
-        // 256 x 256 tiles once there are enough of them to fill the CUs: a
-        // split into bf16 high parts and residuals first
-        const uint64_t wide = uint64_t((p.m + GD_BM - 1) / GD_BM) * ((p.n + GD_BN - 1) / GD_BN);
-        const uint64_t aBytes = uint64_t(p.m) * p.k * 2;   // one bf16 image of a
-        if (p.k % GD_BK == 0 && wide >= 256 && wide <= 0x7FFFFFFFull && aBytes < (1ull << 32) &&
-            uint64_t(p.n) * p.k * 2 < (1ull << 32)) {
-            uint8_t* split = static_cast<uint8_t*>(ctx.grow(SLOT_GEMM_A, 2 * aBytes));
-            if (!split) return false;
-            bf16x8* hi = reinterpret_cast<bf16x8*>(split);
-            bf16x8* lo = reinterpret_cast<bf16x8*>(split + aBytes);
-            const uint64_t pieces = aBytes / 16;
-            const unsigned sg = unsigned((pieces + 255) / 256 < 8192 ? (pieces + 255) / 256 : 8192);
-            if (!ctx.launch("split_a_kernel", stream, [&] {
-                    hipLaunchKernelGGL(split_a_kernel, dim3(sg), dim3(256), 0, stream, p.a, hi, lo, pieces);
-                }))
-                return false;
-            return ctx.launch("gemm_dma_kernel", stream, [&] {
-                hipLaunchKernelGGL(gemm_dma_kernel, dim3(unsigned(wide)), dim3(256), 0, stream, p,
-                                   reinterpret_cast<const __bf16*>(hi), reinterpret_cast<const __bf16*>(lo));
-            });
-        }
+        if (dma_eligible(p)) return launch_dma(ctx, p, nullptr, 0, false, stream);
     }
     if (p.m >= GEMM_MIN_M) {
         const uint32_t tiles = ((p.n + GM_BN - 1) / GM_BN) * ((p.m + GM_BM - 1) / GM_BM);
@@ -664,9 +739,41 @@ bool launch_gemv(const GemvParams& p, hipStream_t stream) {
     }
 }
 
-bool launch_gemm_kv(const GemvParams& p, const KvEpilogue& e, hipStream_t stream) {
+static bool kv_checks(Context& ctx, const GemvParams& p, const KvEpilogue& e);
+
+bool gemm_splits_a(const GemvParams& p) { return dma_eligible(p); }
+
+bool launch_gemm_kv_pair(const GemvParams& pk, const GemvParams& pv, const KvEpilogue& ek, const KvEpilogue& ev,
+                         bool aSplit, hipStream_t stream) {
     Context& ctx = Context::instance();
-    if (p.m == 0) return true;
+    // one DMA GEMM over both weights when each is a multiple of 256 columns
+    // (no tile straddles them) and the pair has the tiles for it
+    GemvParams both = pk;
+    both.n = pk.n + pv.n;
+    both.ldo = both.n;
+    both.bias = nullptr;
+    both.accumulate = 0;
+    const bool pair = pk.type == 1 && pv.type == 1 && pk.k == pv.k && pk.m == pv.m && pk.a == pv.a && pk.n == pv.n &&
+                      pk.n % GD_BN == 0 && (ek.dim == 64 || ek.dim == 128) && ek.dim == ev.dim &&
+                      (reinterpret_cast<uintptr_t>(pv.w) % 16) == 0 && dma_eligible(both);
+    if (!pair) return launch_gemm_kv(pk, ek, stream) && launch_gemm_kv(pv, ev, stream);
+    if (pk.m == 0) return true;
+    if (!kv_checks(ctx, pk, ek) || !kv_checks(ctx, pv, ev)) return false;
+    float* kv = static_cast<float*>(ctx.grow(SLOT_MIXER_KV, size_t(pk.m) * both.n * sizeof(float)));
+    if (!kv) return false;
+    both.out = kv;
+    if (!launch_dma(ctx, both, pv.w, pk.n, aSplit, stream)) return false;
+    const uint32_t heads = pk.n / ek.dim;
+    const uint64_t waves = uint64_t(pk.m) * heads * 2;
+    if ((waves + 3) / 4 > 0x7FFFFFFFull) return ctx.fail("projection epilogue: too many rows");
+    return ctx.launch("kv_epilogue_kernel", stream, [&] {
+        hipLaunchKernelGGL(kv_epilogue_kernel, dim3(unsigned((waves + 3) / 4)), dim3(256), 0, stream, kv, pk.bias,
+                           pv.bias, ek, ev, pk.m, heads);
+    });
+}
+
+/* the shapes and alignments a k or v projection with its epilogue needs */
+static bool kv_checks(Context& ctx, const GemvParams& p, const KvEpilogue& e) {
     if (!p.a || !p.w || !e.cache || !e.work) return ctx.fail("projection epilogue: null tensor");
     if (e.dim != 64 && e.dim != 128) return ctx.fail("projection epilogue: dim must be 64 or 128");
     if (p.n == 0 || p.n % e.dim) return ctx.fail("projection epilogue: n must be a multiple of dim");
@@ -678,6 +785,13 @@ bool launch_gemm_kv(const GemvParams& p, const KvEpilogue& e, hipStream_t stream
     if (p.k % E || (reinterpret_cast<uintptr_t>(p.w) % 16) || (reinterpret_cast<uintptr_t>(p.a) % 16) ||
         (reinterpret_cast<uintptr_t>(e.cache) % 16) || (reinterpret_cast<uintptr_t>(e.work) % 16))
         return ctx.fail("projection epilogue: rows of a, w and the caches must be 16-byte aligned");
+    return true;
+}
+
+bool launch_gemm_kv(const GemvParams& p, const KvEpilogue& e, hipStream_t stream) {
+    Context& ctx = Context::instance();
+    if (p.m == 0) return true;
+    if (!kv_checks(ctx, p, e)) return false;
     const dim3 grid(unsigned((p.n + GM_BN - 1) / GM_BN), unsigned((p.m + GM_BM - 1) / GM_BM));
     if (grid.y > 65535u) return ctx.fail("matmul: too many rows of a");
     return ctx.launch("gemm_kv_kernel", stream, [&] {

@@ -82,7 +82,8 @@ bool launch_prefill_mixer(const MixerParams& p, hipStream_t stream) {
     void* vh = nullptr;
     if (!prefill_work_buffers(pp, &kh, &vh)) return false;
 
-    if (!launch_gemv(projection(p.q, p.x, q, p.count, 0), stream)) return false;
+    const GemvParams pq = projection(p.q, p.x, q, p.count, 0);
+    if (!launch_gemv(pq, stream)) return false;
     KvEpilogue ek{};
     ek.cache = p.keyCache;
     ek.work = kh;
@@ -96,13 +97,15 @@ bool launch_prefill_mixer(const MixerParams& p, hipStream_t stream) {
     ek.T = uint32_t(T);
     ek.capacity = p.capacity;
     ek.rangeFlag = ctx.rangeDev;
-    if (!launch_gemm_kv(projection(p.k, p.x, nullptr, p.count, 0), ek, stream)) return false;
     KvEpilogue ev = ek;
     ev.cache = p.valueCache;
     ev.work = vh;
     ev.gamma = nullptr;
     ev.freqs = nullptr;
-    if (!launch_gemm_kv(projection(p.v, p.x, nullptr, p.count, 0), ev, stream)) return false;
+    // the q projection left x's bf16 split in scratch when it took the DMA GEMM
+    if (!launch_gemm_kv_pair(projection(p.k, p.x, nullptr, p.count, 0), projection(p.v, p.x, nullptr, p.count, 0), ek,
+                             ev, gemm_splits_a(pq), stream))
+        return false;
     if (!launch_prefill(pp, stream)) return false;
     return launch_gemv(projection(p.o, attn, p.out, p.count, p.accumulate ? 1 : 0), stream);
 }
