@@ -104,6 +104,17 @@ def test_counts_and_history(gpu, count, start):
     run(gpu, "bf16", count=count, start=start)
 
 
+@pytest.mark.parametrize("H,KV,D,rot,biases", [(16, 8, 128, None, False), (8, 8, 128, None, True),
+                                                (32, 16, 64, 32, True)])
+def test_fused_kv_projection(gpu, H, KV, D, rot, biases):
+    """8192 rows and 2 KV D = 2048 k and v columns make 256 tiles of 256 x 256:
+    k and v run as one DMA GEMM over both weights, then kv_epilogue_kernel. At
+    H D = 2048 the q projection takes the DMA GEMM too and its bf16 split of x
+    is reused; at H D = 1024 the pair splits x itself. A window of 64 keeps the
+    oracle's attention short."""
+    run(gpu, "bf16", count=8192, start=40, hidden=64, H=H, KV=KV, D=D, rot=rot, biases=biases, window=64)
+
+
 def test_head_dim_64_partial_rotary_and_biases(gpu):
     run(gpu, "bf16", D=64, H=4, KV=2, rot=32, biases=True)
 
