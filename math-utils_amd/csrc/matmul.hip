@@ -535,55 +535,84 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemvParams p, const __bf1
    (gamma) and rotate-half RoPE (freqs), and each row appended to its bf16
    cache and to the flash kernel's fp16 copy, as gemm_kernel's k / v
    epilogue does (the same operations in the same order per element; the
-   norm's sum of squares is reduced in another order). One wave per (token,
-   kv head, k or v); the row staged in LDS for the RoPE partner. */
+   norm's sum of squares is reduced in another order). One workgroup per
+   token: the token's rotation angles float(pos) * freq go through sincosf
+   once into LDS, then the four waves take its 2 * heads rows (k and v of
+   each kv head) in turn, a row staged in LDS for the RoPE partner. A lane
+   holds D / 64 consecutive elements. */
 __global__ __launch_bounds__(256) void kv_epilogue_kernel(const float* kv, const float* kBias, const float* vBias,
-                                                          KvEpilogue ek, KvEpilogue ev, uint32_t m, uint32_t heads) {
+                                                          KvEpilogue ek, KvEpilogue ev, uint32_t heads) {
     __shared__ float row[4][128];
+    __shared__ float sinT[64], cosT[64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const uint64_t task = uint64_t(blockIdx.x) * 4 + w;
-    if (task >= uint64_t(m) * heads * 2) return;   // whole wave leaves; no block barriers below
-    const uint32_t which = uint32_t(task % 2), h = uint32_t((task / 2) % heads), t = uint32_t(task / (2 * heads));
-    const KvEpilogue& e = which ? ev : ek;
-    const float* bias = which ? vBias : kBias;
-    const uint32_t D = e.dim, N1 = heads * D, EPL = D / 64;   // D 64 or 128
-    const float* src = kv + (size_t(t) * 2 + which) * N1 + size_t(h) * D;
-    float x[2], y[2];
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t d = lane * EPL + i;
-        x[i] = uint32_t(i) < EPL ? src[d] + (bias ? bias[size_t(h) * D + d] : 0.0f) : 0.0f;
-        ss = fmaf(x[i], x[i], ss);
+    const uint32_t t = blockIdx.x, pos = ek.start + t;
+    const uint32_t half = ek.freqs ? ek.rot / 2 : 0;   // rot <= D <= 128
+    if (w == 0 && uint32_t(lane) < half) {
+        float sn, cs;
+        sincosf(float(pos) * ek.freqs[lane], &sn, &cs);
+        sinT[lane] = sn;
+        cosT[lane] = cs;
     }
-    float inv = 1.0f;
-    if (e.gamma) inv = 1.0f / sqrtf(wave_sum(ss) / float(D) + e.eps);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t d = lane * EPL + i;
-        y[i] = e.gamma && uint32_t(i) < EPL ? x[i] * inv * (e.gamma[d] + e.offset) : x[i];
-        if (uint32_t(i) < EPL) row[w][d] = y[i];
-    }
-    wave_sync();
-    const uint32_t half = e.freqs ? e.rot / 2 : 0;
-    const uint32_t pos = e.start + t;
-    bool bad = false;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t d = lane * EPL + i;
-        if (uint32_t(i) >= EPL) continue;
-        float v = y[i];
-        if (d < 2 * half) {   // rotate-half pairs (LocalModel.hpp:2624-2641), the angle float(pos) * freq
-            const bool low = d < half;
-            const uint32_t dp = low ? d + half : d - half;
-            float sn, cs;
-            sincosf(float(pos) * e.freqs[low ? d : dp], &sn, &cs);
-            v = low ? y[i] * cs - row[w][dp] * sn : y[i] * cs + row[w][dp] * sn;
+    __syncthreads();
+    const uint32_t D = ek.dim, N1 = heads * D, EPL = D / 64;   // D 64 or 128
+    const uint32_t d0 = uint32_t(lane) * EPL;
+    for (uint32_t r = uint32_t(w); r < 2 * heads; r += 4) {
+        const uint32_t which = r & 1, h = r >> 1;
+        const KvEpilogue& e = which ? ev : ek;
+        const float* bias = which ? vBias : kBias;
+        const float* src = kv + (size_t(t) * 2 + which) * N1 + size_t(h) * D + d0;
+        float x[2] = {0.0f, 0.0f};
+        if (EPL == 2) {
+            const float2 v2 = *reinterpret_cast<const float2*>(src);   // kv rows are 8-byte aligned
+            x[0] = v2.x;
+            x[1] = v2.y;
+        } else {
+            x[0] = src[0];
         }
-        e.cache[(size_t(h) * e.capacity + pos) * D + d] = float_to_bf16_bits(v);
-        static_cast<_Float16*>(e.work)[(size_t(h) * e.T + pos) * D + d] = to_f16_checked(v, bad);
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (bias && uint32_t(i) < EPL) x[i] += bias[size_t(h) * D + d0 + i];
+            ss = fmaf(x[i], x[i], ss);
+        }
+        float inv = 1.0f;
+        if (e.gamma) inv = 1.0f / sqrtf(wave_sum(ss) / float(D) + e.eps);
+        float y[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            y[i] = e.gamma && uint32_t(i) < EPL ? x[i] * inv * (e.gamma[d0 + i] + e.offset) : x[i];
+            if (uint32_t(i) < EPL) row[w][d0 + i] = y[i];
+        }
+        wave_sync();
+        const uint32_t hf = e.freqs ? half : 0;
+        bool bad = false;
+        uint16_t cb[2];
+        _Float16 wb[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t d = d0 + i;
+            float v = y[i];
+            if (d < 2 * hf) {   // rotate-half pairs (LocalModel.hpp:2624-2641)
+                const bool low = d < hf;
+                const uint32_t j = low ? d : d - hf, dp = low ? d + hf : d - hf;
+                v = low ? y[i] * cosT[j] - row[w][dp] * sinT[j] : y[i] * cosT[j] + row[w][dp] * sinT[j];
+            }
+            cb[i] = float_to_bf16_bits(v);
+            wb[i] = to_f16_checked(v, bad);
+        }
+        uint16_t* cdst = e.cache + (size_t(h) * e.capacity + pos) * D + d0;
+        _Float16* wdst = static_cast<_Float16*>(e.work) + (size_t(h) * e.T + pos) * D + d0;
+        if (EPL == 2) {   // 4-byte stores: rows are 16-byte aligned, d0 even
+            *reinterpret_cast<uint32_t*>(cdst) = uint32_t(cb[0]) | (uint32_t(cb[1]) << 16);
+            _Float16 __attribute__((ext_vector_type(2))) w2 = {wb[0], wb[1]};
+            *reinterpret_cast<decltype(w2)*>(wdst) = w2;
+        } else {
+            cdst[0] = cb[0];
+            wdst[0] = wb[0];
+        }
+        raise_range_flag(e.rangeFlag, bad);
+        wave_sync();   // the row's partner reads are done before the next row is staged
     }
-    raise_range_flag(e.rangeFlag, bad);
 }
 
 /* the K slices' partial tiles added in slice order, then the bias and the
@@ -764,11 +793,9 @@ bool launch_gemm_kv_pair(const GemvParams& pk, const GemvParams& pv, const KvEpi
     both.out = kv;
     if (!launch_dma(ctx, both, pv.w, pk.n, aSplit, stream)) return false;
     const uint32_t heads = pk.n / ek.dim;
-    const uint64_t waves = uint64_t(pk.m) * heads * 2;
-    if ((waves + 3) / 4 > 0x7FFFFFFFull) return ctx.fail("projection epilogue: too many rows");
+    if (pk.m > 0x7FFFFFFFu) return ctx.fail("projection epilogue: too many rows");
     return ctx.launch("kv_epilogue_kernel", stream, [&] {
-        hipLaunchKernelGGL(kv_epilogue_kernel, dim3(unsigned((waves + 3) / 4)), dim3(256), 0, stream, kv, pk.bias,
-                           pv.bias, ek, ev, pk.m, heads);
+        hipLaunchKernelGGL(kv_epilogue_kernel, dim3(pk.m), dim3(256), 0, stream, kv, pk.bias, pv.bias, ek, ev, heads);
     });
 }
 
