@@ -41,6 +41,10 @@ struct PrefillParams {
     // set to 1 by any conversion into the fp16 working copies that overflows
     // fp16's range (device address; null: not tracked)
     uint32_t* rangeFlag;
+    // when set, out is not written: each output row goes as bf16 high parts
+    // here ([count][heads·dim]) and as bf16 residuals x - hi right after them
+    // (the operand images of gemm_split_image)
+    uint16_t* outSplit;
 };
 bool launch_prefill(const PrefillParams& p, hipStream_t stream);
 // rows of zeros after the last kv head in the flash kernel's working copies
@@ -123,6 +127,12 @@ bool launch_gemm_kv(const GemvParams& p, const KvEpilogue& e, hipStream_t stream
 // whether launch_gemv splits p.a into the bf16 images a following
 // launch_gemm_kv_pair can reuse (aSplit)
 bool gemm_splits_a(const GemvParams& p);
+// the DMA GEMM's operand images of p.a (bf16 high parts [m][k], then the
+// residuals), grown for p, when p takes that GEMM; null otherwise
+uint16_t* gemm_split_image(const GemvParams& p);
+// launch_gemv for a p that takes the DMA GEMM, with gemm_split_image(p)
+// already written (p.a is not read)
+bool launch_gemv_presplit(const GemvParams& p, hipStream_t stream);
 // the k and v projections of the same rows: one GEMM over both weights, then
 // the epilogue as its own kernel, where the shapes allow; otherwise two
 // launch_gemm_kv calls

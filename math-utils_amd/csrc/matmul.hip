@@ -772,6 +772,18 @@ static bool kv_checks(Context& ctx, const GemvParams& p, const KvEpilogue& e);
 
 bool gemm_splits_a(const GemvParams& p) { return dma_eligible(p); }
 
+uint16_t* gemm_split_image(const GemvParams& p) {
+    if (!dma_eligible(p)) return nullptr;
+    return static_cast<uint16_t*>(Context::instance().grow(SLOT_GEMM_A, 2 * uint64_t(p.m) * p.k * 2));
+}
+
+bool launch_gemv_presplit(const GemvParams& p, hipStream_t stream) {
+    Context& ctx = Context::instance();
+    if (p.m == 0 || p.n == 0) return true;
+    if (!p.w || !p.out || p.ldo < p.n || !dma_eligible(p)) return ctx.fail("matmul: no presplit GEMM for this shape");
+    return launch_dma(ctx, p, nullptr, 0, true, stream);
+}
+
 bool launch_gemm_kv_pair(const GemvParams& pk, const GemvParams& pv, const KvEpilogue& ek, const KvEpilogue& ev,
                          bool aSplit, hipStream_t stream) {
     Context& ctx = Context::instance();

@@ -106,8 +106,12 @@ bool launch_prefill_mixer(const MixerParams& p, hipStream_t stream) {
     if (!launch_gemm_kv_pair(projection(p.k, p.x, nullptr, p.count, 0), projection(p.v, p.x, nullptr, p.count, 0), ek,
                              ev, gemm_splits_a(pq), stream))
         return false;
+    // when the o projection takes the DMA GEMM, the flash kernel writes its
+    // bf16 operand images directly (no fp32 round trip and split pass)
+    const GemvParams po = projection(p.o, attn, p.out, p.count, p.accumulate ? 1 : 0);
+    pp.outSplit = gemm_split_image(po);
     if (!launch_prefill(pp, stream)) return false;
-    return launch_gemv(projection(p.o, attn, p.out, p.count, p.accumulate ? 1 : 0), stream);
+    return pp.outSplit ? launch_gemv_presplit(po, stream) : launch_gemv(po, stream);
 }
 
 } // namespace aigpu

@@ -325,6 +325,8 @@ struct FlashArgs {
     const _Float16* kh;  // [kvHeads][T][D]
     const _Float16* vh;  // [kvHeads][T][D]
     float* out;          // [count][heads][D]
+    __bf16* outHi;       // set: out goes here as bf16 high parts ...
+    __bf16* outLo;       // ... and residuals instead
     uint32_t count, start, heads, kvHeads, window, T, nQT, xcdRemap;
     // fused Q: the raw q rows are normed, rotated and scaled on load instead
     // of read from qh
@@ -1180,7 +1182,19 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                         val[i] *= 1.0f / (1.0f + expf(-gt));
                     }
                 }
-                *reinterpret_cast<floatx4*>(dst + 32 * dt + 8 * r4 + 4 * g) = val;
+                if (a.outHi) {   // the o projection's operand images, as split_a_kernel writes them
+                    bf16x4 h, l;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        h[i] = __bf16(val[i]);
+                        l[i] = __bf16(val[i] - float(h[i]));
+                    }
+                    const size_t at = size_t(dst - a.out) + 32 * dt + 8 * r4 + 4 * g;
+                    *reinterpret_cast<bf16x4*>(a.outHi + at) = h;
+                    *reinterpret_cast<bf16x4*>(a.outLo + at) = l;
+                } else {
+                    *reinterpret_cast<floatx4*>(dst + 32 * dt + 8 * r4 + 4 * g) = val;
+                }
             }
     }
 }
@@ -1292,6 +1306,8 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     a.kh = kh;
     a.vh = vh;
     a.out = p.out;
+    a.outHi = reinterpret_cast<__bf16*>(p.outSplit);
+    a.outLo = p.outSplit ? a.outHi + p.count * p.heads * p.dim : nullptr;
     a.count = uint32_t(p.count);
     a.start = uint32_t(p.start);
     a.heads = uint32_t(p.heads);

@@ -104,15 +104,22 @@ def test_counts_and_history(gpu, count, start):
     run(gpu, "bf16", count=count, start=start)
 
 
-@pytest.mark.parametrize("H,KV,D,rot,biases", [(16, 8, 128, None, False), (8, 8, 128, None, True),
-                                                (32, 16, 64, 32, True)])
-def test_fused_kv_projection(gpu, H, KV, D, rot, biases):
+@pytest.mark.parametrize("H,KV,D,rot,biases,hidden,gate,acc", [
+    (16, 8, 128, None, False, 64, False, False), (8, 8, 128, None, True, 64, False, False),
+    (32, 16, 64, 32, True, 64, False, False), (2, 1, 64, None, False, 2048, False, True),
+    (2, 1, 64, 32, True, 2048, True, False)])
+def test_fused_kv_projection(gpu, H, KV, D, rot, biases, hidden, gate, acc):
     """8192 rows and 2 KV D = 2048 k and v columns make 256 tiles of 256 x 256:
     k and v run as one DMA GEMM over both weights, then kv_epilogue_kernel. At
     H D = 2048 the q projection takes the DMA GEMM too and its bf16 split of x
-    is reused; at H D = 1024 the pair splits x itself. A window of 64 keeps the
-    oracle's attention short."""
-    run(gpu, "bf16", count=8192, start=40, hidden=64, H=H, KV=KV, D=D, rot=rot, biases=biases, window=64)
+    is reused; at H D = 1024 the pair splits x itself. At hidden = 2048 the o
+    projection has 256 such tiles too (here with 2 heads of 64, to keep the
+    oracle's projections short; k and v then take two launch_gemm_kv calls): the flash kernel then writes its bf16
+    operand images in place of fp32 rows (with the output gate applied first
+    when there is one), and the residual add rides on the GEMM. A window of 64
+    keeps the oracle's attention short."""
+    run(gpu, "bf16", count=8192, start=40, hidden=hidden, H=H, KV=KV, D=D, rot=rot, biases=biases, window=64,
+        gate=gate, accumulate=acc)
 
 
 def test_head_dim_64_partial_rotary_and_biases(gpu):
