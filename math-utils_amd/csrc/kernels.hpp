@@ -45,12 +45,21 @@ struct PrefillParams {
     // here ([count][heads·dim]) and as bf16 residuals x - hi right after them
     // (the operand images of gemm_split_image)
     uint16_t* outSplit;
+    // 1 (with kvReady): the caller has written the q rotation's cos/sin table
+    // (prefill_prep_foldable) and zeroed the working copies' pad rows, all
+    // that prep would do: it is not launched
+    int prepDone;
 };
 bool launch_prefill(const PrefillParams& p, hipStream_t stream);
 // rows of zeros after the last kv head in the flash kernel's working copies
 constexpr uint32_t PREFILL_PAD_ROWS = 128;
 // the flash kernel's fp16 copies of the cache, [kvHeads][start + count][dim]
 bool prefill_work_buffers(const PrefillParams& p, void** kh, void** vh);
+// whether launch_prefill's prep, for these kvReady parameters, would only
+// write the cos/sin table of the flash kernel's q rotation and zero the pad
+// rows; *rope is then that table ([count][rotaryDims]: cos, then sin, per
+// token), grown, or null without RoPE
+bool prefill_prep_foldable(const PrefillParams& p, float** rope);
 
 // ---- decode: norm + RoPE on load, append, split-K attention, merge --------
 struct DecodeParams {
@@ -136,8 +145,10 @@ bool launch_gemv_presplit(const GemvParams& p, hipStream_t stream);
 // the k and v projections of the same rows: one GEMM over both weights, then
 // the epilogue as its own kernel, where the shapes allow; otherwise two
 // launch_gemm_kv calls
+// fold: also write prep's cos/sin table (rope, may be null) and zero the
+// working copies' pad rows; *folded says whether that was done
 bool launch_gemm_kv_pair(const GemvParams& pk, const GemvParams& pv, const KvEpilogue& ek, const KvEpilogue& ev,
-                         bool aSplit, hipStream_t stream);
+                         bool aSplit, bool fold, float* rope, bool* folded, hipStream_t stream);
 
 // ---- attentionMixer for a prefill: projections, norm/RoPE/append, flash
 // attention, output gate, o projection ----

@@ -539,9 +539,13 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemvParams p, const __bf1
    token: the token's rotation angles float(pos) * freq go through sincosf
    once into LDS, then the four waves take its 2 * heads rows (k and v of
    each kv head) in turn, a row staged in LDS for the RoPE partner. A lane
-   holds D / 64 consecutive elements. */
+   holds D / 64 consecutive elements. With rope set, the angles' cos and sin
+   also go to the flash kernel's table (rope[t][0 .. rot/2) cos, then sin);
+   with padK / padV set, workgroup 0 zeroes pad16 16-byte pieces of each
+   (the working copies' pad rows). */
 __global__ __launch_bounds__(256) void kv_epilogue_kernel(const float* kv, const float* kBias, const float* vBias,
-                                                          KvEpilogue ek, KvEpilogue ev, uint32_t heads) {
+                                                          KvEpilogue ek, KvEpilogue ev, uint32_t heads, float* rope,
+                                                          uint4* padK, uint4* padV, uint32_t pad16) {
     __shared__ float row[4][128];
     __shared__ float sinT[64], cosT[64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -552,7 +556,16 @@ __global__ __launch_bounds__(256) void kv_epilogue_kernel(const float* kv, const
         sincosf(float(pos) * ek.freqs[lane], &sn, &cs);
         sinT[lane] = sn;
         cosT[lane] = cs;
+        if (rope) {
+            rope[size_t(t) * 2 * half + lane] = cs;
+            rope[size_t(t) * 2 * half + half + lane] = sn;
+        }
     }
+    if (padK && t == 0)
+        for (uint32_t i = threadIdx.x; i < pad16; i += 256) {
+            padK[i] = uint4{0u, 0u, 0u, 0u};
+            padV[i] = uint4{0u, 0u, 0u, 0u};
+        }
     __syncthreads();
     const uint32_t D = ek.dim, N1 = heads * D, EPL = D / 64;   // D 64 or 128
     const uint32_t d0 = uint32_t(lane) * EPL;
@@ -785,8 +798,9 @@ bool launch_gemv_presplit(const GemvParams& p, hipStream_t stream) {
 }
 
 bool launch_gemm_kv_pair(const GemvParams& pk, const GemvParams& pv, const KvEpilogue& ek, const KvEpilogue& ev,
-                         bool aSplit, hipStream_t stream) {
+                         bool aSplit, bool fold, float* rope, bool* folded, hipStream_t stream) {
     Context& ctx = Context::instance();
+    *folded = false;
     // one DMA GEMM over both weights when each is a multiple of 256 columns
     // (no tile straddles them) and the pair has the tiles for it
     GemvParams both = pk;
@@ -806,9 +820,19 @@ bool launch_gemm_kv_pair(const GemvParams& pk, const GemvParams& pv, const KvEpi
     if (!launch_dma(ctx, both, pv.w, pk.n, aSplit, stream)) return false;
     const uint32_t heads = pk.n / ek.dim;
     if (pk.m > 0x7FFFFFFFu) return ctx.fail("projection epilogue: too many rows");
-    return ctx.launch("kv_epilogue_kernel", stream, [&] {
-        hipLaunchKernelGGL(kv_epilogue_kernel, dim3(pk.m), dim3(256), 0, stream, kv, pk.bias, pv.bias, ek, ev, heads);
-    });
+    if (fold && rope && !ek.freqs) return ctx.fail("projection epilogue: a cos/sin table needs RoPE");
+    // the pad rows start past the last head's T rows (16-byte aligned: dim is 64 or 128)
+    const size_t padAt = size_t(heads) * ek.T * ek.dim * 2;
+    uint4* padK = fold ? reinterpret_cast<uint4*>(static_cast<uint8_t*>(ek.work) + padAt) : nullptr;
+    uint4* padV = fold ? reinterpret_cast<uint4*>(static_cast<uint8_t*>(ev.work) + padAt) : nullptr;
+    const uint32_t pad16 = PREFILL_PAD_ROWS * ek.dim * 2 / 16;
+    if (!ctx.launch("kv_epilogue_kernel", stream, [&] {
+            hipLaunchKernelGGL(kv_epilogue_kernel, dim3(pk.m), dim3(256), 0, stream, kv, pk.bias, pv.bias, ek, ev,
+                               heads, fold ? rope : nullptr, padK, padV, pad16);
+        }))
+        return false;
+    *folded = fold;
+    return true;
 }
 
 /* the shapes and alignments a k or v projection with its epilogue needs */

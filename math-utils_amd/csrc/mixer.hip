@@ -102,10 +102,15 @@ bool launch_prefill_mixer(const MixerParams& p, hipStream_t stream) {
     ev.work = vh;
     ev.gamma = nullptr;
     ev.freqs = nullptr;
-    // the q projection left x's bf16 split in scratch when it took the DMA GEMM
+    // the q projection left x's bf16 split in scratch when it took the DMA GEMM;
+    // the k / v pass after the pair's GEMM can also do all that prep would
+    float* rope = nullptr;
+    const bool foldable = prefill_prep_foldable(pp, &rope);
+    bool folded = false;
     if (!launch_gemm_kv_pair(projection(p.k, p.x, nullptr, p.count, 0), projection(p.v, p.x, nullptr, p.count, 0), ek,
-                             ev, gemm_splits_a(pq), stream))
+                             ev, gemm_splits_a(pq), foldable, rope, &folded, stream))
         return false;
+    pp.prepDone = folded ? 1 : 0;
     // when the o projection takes the DMA GEMM, the flash kernel writes its
     // bf16 operand images directly (no fp32 round trip and split pass)
     const GemvParams po = projection(p.o, attn, p.out, p.count, p.accumulate ? 1 : 0);

@@ -1201,6 +1201,30 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
 
 } // namespace
 
+/* the register-row kernels need 16-byte aligned rows and rot % 16 == 0
+   (vec); the flash kernel normalises and rotates its own q rows when each
+   lane's RoPE partners are in the lane itself (rot / 2 a multiple of 16):
+   prep then handles only k and v, plus a cos/sin table for the q rotation */
+static void prep_shape(const PrefillParams& p, bool* vec, bool* fuseQ) {
+    const size_t inAlign = p.inType == 0 ? 4 : 8;   // elements per 16 bytes
+    auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    *vec = aligned(p.q) && aligned(p.k) && aligned(p.v) && aligned(p.keyCache) && aligned(p.valueCache) &&
+           (p.qStride % inAlign) == 0 && (!p.qNorm || aligned(p.qNorm)) && (!p.kNorm || aligned(p.kNorm)) &&
+           (!p.freqs || (p.rotaryDims % 16) == 0);
+    *fuseQ = *vec && p.qStride < (1ull << 32) && (!p.freqs || (p.rotaryDims % 32) == 0);
+}
+
+bool prefill_prep_foldable(const PrefillParams& p, float** rope) {
+    *rope = nullptr;
+    bool vec = false, fuseQ = false;
+    prep_shape(p, &vec, &fuseQ);
+    if (!p.kvReady || !fuseQ || p.count == 0) return false;
+    if (!p.freqs) return true;
+    // the same slot and size launch_prefill takes for the table
+    *rope = static_cast<float*>(Context::instance().grow(SLOT_PREFILL_Q, p.count * size_t(p.rotaryDims) * sizeof(float)));
+    return *rope != nullptr;
+}
+
 bool prefill_work_buffers(const PrefillParams& p, void** kh, void** vh) {
     Context& ctx = Context::instance();
     const uint64_t T = p.start + p.count;
@@ -1236,17 +1260,9 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     _Float16* kh = static_cast<_Float16*>(khv);
     _Float16* vh = static_cast<_Float16*>(vhv);
 
-    // the register-row kernels need 16-byte aligned rows and rot % 16 == 0
-    const size_t inAlign = p.inType == 0 ? 4 : 8;   // elements per 16 bytes
-    auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
-    const bool vec = aligned(p.q) && aligned(p.k) && aligned(p.v) && aligned(p.keyCache) &&
-                     aligned(p.valueCache) && (p.qStride % inAlign) == 0 &&
-                     (!p.qNorm || aligned(p.qNorm)) && (!p.kNorm || aligned(p.kNorm)) &&
-                     (!p.freqs || (p.rotaryDims % 16) == 0);
-    // the flash kernel normalises and rotates its own q rows when each lane's
-    // RoPE partners are in the lane itself (rot / 2 a multiple of 16); prep
-    // then handles only k and v, plus a cos/sin table for the q rotation
-    const bool fuseQ = vec && p.qStride < (1ull << 32) && (!p.freqs || (p.rotaryDims % 32) == 0);
+    bool vec = false, fuseQ = false;
+    prep_shape(p, &vec, &fuseQ);
+    if (p.prepDone && !(p.kvReady && fuseQ)) return ctx.fail("prefill: prep cannot be skipped for these parameters");
     _Float16* qh = nullptr;
     float* rope = nullptr;
     if (!fuseQ) {
@@ -1277,9 +1293,9 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     }
 
     const float qScale = LOG2E / sqrtf(float(p.dim));
-    // prep always runs: besides q/k/v rows and the cos/sin table it zeroes
-    // the working copies' pad rows
-    if (!ctx.launch("prefill_prep_kernel", stream, [&] {
+    // prep runs unless the caller did its work: besides q/k/v rows and the
+    // cos/sin table it zeroes the working copies' pad rows
+    if (!p.prepDone && !ctx.launch("prefill_prep_kernel", stream, [&] {
             const dim3 grid{unsigned(p.count)}, block{256};
             const uint32_t t32 = uint32_t(T);
             if (!vec)
