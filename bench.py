@@ -2,16 +2,20 @@
 """bench.py - throughput of the MI355X attention hot path against its roofline,
 with the reference's CPU path timed beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|delta|gdn|kda|dense|gemm|mla|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|delta|small|published|bandwidth|gdn|kda|dense|gemm|mla|mixer|indexer|all]
 
 A step is one call of the hot path over one batch of synthetic, HBM-resident
 input. The headline workload (config.workload) is configs[2] of BASELINE.json,
 the Qwen3-8B-shaped causal GQA prefill at 8k (32 q / 8 kv heads, head_dim
 128, QK-RMSNorm + RoPE theta 1e6, bf16 in, fp32 accumulate): `value` is its
 whole-step TFLOP/s (norm/RoPE/append + flash attention) with the algorithmic
-count 2*D*Hq*S*(S+1). `decode` carries configs[3] (Qwen3-30B-A3B batched
-ragged decode, KV GB/s with 2048*sum(L_b+1) bytes) in the same form, and
-`others` the remaining configurations.
+count 2*D*Hq*S*(S+1). `configs` carries all five configurations in the same
+form (value, roofline of the dominant kernel, cpu_baseline, parity);
+`published_shape` the reference's one published attention measurement (128
+queries after 384 cached, docs/apple-gpu-plan.md:114-118); `bandwidth` a
+device copy and the reference's own bandwidth test (a bf16 GEMV over 512 MiB
+of weights, src/gpu-testing.cpp:298-351); `next_rows` the paths either side
+of the hot path.
 
 `roofline` is for the dominant kernel of the step: algorithmic flops (or
 bytes) per launch over its average duration, from hipEvents the backend
@@ -19,6 +23,15 @@ records around every launch on the stream it runs on. `cpu_baseline` is the
 reference's own kernels::attention / deltaStep (compiled from its headers into
 oracle/_ref, "reference"), or the C restatement ("port") where that library
 is absent, timed on the host's cores on a bounded sample of the same workload.
+The CPU leg also checks the GPU's output of the timed step against the
+reference (or the restatement) on the same inputs, outside the timed region:
+`parity` gives max-abs, rel-L2 and the reference's own maxAbs/rms
+(src/gpu-testing.cpp:85-95).
+
+Every workload first runs its step untimed for CLOCK_RAMP_S seconds: the
+GPU's clock rises over its first ~15 ms of sustained work and falls back
+while the host runs a CPU baseline, so a few warm-up steps alone would time
+the ramp. Then the W warm-up steps, then exactly K timed steps.
 """
 import argparse
 import json
@@ -54,9 +67,11 @@ def parse():
     # the GPU's clock ramps over the first ~15 ms of sustained work: a short
     # warm-up times the ramp rather than the kernels
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="all", choices=["prefill", "decode", "delta", "gdn", "kda", "dense", "gemm", "mla", "mixer", "indexer", "all"])
+    ap.add_argument("--workload", default="all",
+                    choices=["prefill", "decode", "delta", "small", "published", "bandwidth", "gdn", "kda", "dense",
+                             "gemm", "mla", "mixer", "indexer", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="target CPU time of each baseline sample")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run a 1 GiB device copy first (scales HBM counters in profiles)")
@@ -117,11 +132,22 @@ def gammas(dim, gen):
 
 
 # ------------------------------------------------------------------ timing
-def time_steps(step, steps, warmup, kernel):
-    """warmup, then K timed steps between synchronisations; returns step ms and
-    the named kernel's average launch ms from the backend's hipEvents"""
+CLOCK_RAMP_S = 0.25
+
+
+def time_steps(step, steps, warmup, kernel, ramp_max=None):
+    """clock ramp, W warm-up steps, then K timed steps between synchronisations;
+    returns the step's ms, the named kernel's average launch ms from the
+    backend's hipEvents, and all launched kernels' ms per step"""
     import torch
     import aigpu
+    t = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t < CLOCK_RAMP_S and (ramp_max is None or n < ramp_max):
+        step()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -144,6 +170,40 @@ def time_steps(step, steps, warmup, kernel):
     k_ms, n = aigpu.profile_read(kernel)
     all_ms, _ = aigpu.profile_read(None)
     return step_ms, (k_ms / n if n else float("nan")), all_ms / steps
+
+
+def parity(ref, got, max_abs_bar, rel_l2_bar=None, what=""):
+    """max-abs and rel-L2 (the north star's bars) and the reference's own
+    maxAbs/rms (src/gpu-testing.cpp:85-95) of got against ref"""
+    import numpy as np
+    ref = np.asarray(ref, np.float64).reshape(-1)
+    got = np.asarray(got, np.float64).reshape(-1)
+    diff = np.abs(ref - got)
+    max_abs = float(diff.max()) if diff.size else 0.0
+    norm = float(np.linalg.norm(ref))
+    rel = float(np.linalg.norm(ref - got) / norm) if norm > 0 else max_abs
+    rms = float(np.sqrt(np.mean(ref * ref))) if ref.size else 0.0
+    ok = bool(np.isfinite(got).all()) and max_abs <= max_abs_bar and (rel_l2_bar is None or rel <= rel_l2_bar)
+    out = {"max_abs": max_abs, "rel_l2": rel, "ref_error": max_abs / rms if rms > 0 else max_abs,
+           "bar": {"max_abs": max_abs_bar, "rel_l2": rel_l2_bar}, "pass": ok}
+    if what:
+        out["checked"] = what
+    return out
+
+
+def median_time(fn, runs=5, budget=None):
+    """one warm-up, then the median of `runs` timings (fewer past `budget` s)"""
+    fn()
+    times = []
+    t_all = time.perf_counter()
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+        if budget is not None and time.perf_counter() - t_all > budget:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times)
 
 
 def cpu_lib():
@@ -201,16 +261,19 @@ def prefill_workload(args, cpu):
 
     flops = 2.0 * D * H * S * (S + 1)
     step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "prefill_flash_kernel")
+    aigpu.check_range()   # no fp16 range error in any timed call
     res = {
         "workload": "configs[2] qwen3-8b causal GQA prefill S=8192 32q/8kv D=128 bf16, QK-norm+RoPE",
         # bf16 in; the flash MFMAs take fp16 operands (3 more mantissa bits) and accumulate in fp32
         "dtype": "fp16",
         "value": flops / (step_ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": step_ms,
+        "kernels_ms_per_step": launched_ms,
         "roofline": {"kernel": "prefill_flash_kernel", "bound": "mfma",
                      "achieved": flops / (k_ms * 1e-3) / 1e12, "peak": PEAK_MFMA_F16,
                      "unit": "TFLOP/s", "frac": flops / (k_ms * 1e-3) / 1e12 / PEAK_MFMA_F16,
                      "traffic": PREFILL_FLASH_TRAFFIC, "kernel_ms": k_ms, "flops_per_launch": flops},
     }
+    got = out.cpu().numpy()
 
     # the same prefill with a sliding window of 4096 keys (per-layer windows,
     # LocalModel.hpp:821-830; the first key a query sees, Kernels.hpp:142)
@@ -221,20 +284,31 @@ def prefill_workload(args, cpu):
 
     wflops = 4.0 * D * H * sum(min(i + 1, W) for i in range(S))
     w_step, w_k, _ = time_steps(step_window, args.steps, args.warmup, "prefill_flash_kernel")
+    aigpu.check_range()
     res["window_4096"] = {"workload": "configs[2] shape with a sliding window of 4096 keys",
                           "value": wflops / (w_step * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": w_step,
                           "kernel_ms": w_k, "kernel_frac": wflops / (w_k * 1e-3) / 1e12 / PEAK_MFMA_F16,
                           "flops_per_launch": wflops}
     if cpu is not None:
         O, ref, kind, threads = cpu
-        qh = q[-64:].float().cpu().numpy()
+        qh = q.float().cpu().numpy()
         kh = k.float().cpu().numpy()
         vh = v.float().cpu().numpy()
+        # parity of the timed (full causal) step on 64 sampled query rows,
+        # the last 16 (the longest histories) among them
+        rows = sorted(set(range(0, S, S // 48)) | set(range(S - 16, S)))
+        qn, kn = O.qk_norm_rope(qh, kh, S, 0, H, KV, D, D, gq.cpu().numpy(), gk.cpu().numpy(), 1e-6,
+                                fr.cpu().numpy(), D)
+        want = O.attention_strided(qn, kn, vh, S, 0, H, KV, D, D, KV * D, D, 0, rows=rows, nthreads=threads)
+        res["parity"] = parity(want, got[rows], 2e-3, 1e-3,
+                               f"{len(rows)} query rows x 32 heads (rows 0, 170, ..., and the last 16) "
+                               f"against the C restatement of QK-norm, RoPE and kernels::attention")
+        del qn, kn, want
 
         def run(n, nthreads):
             cpu_threads(cpu, nthreads)
             start = S - n
-            qq = np.ascontiguousarray(np.resize(qh, (n, H, D)), np.float32)
+            qq = np.ascontiguousarray(np.resize(qh[-64:], (n, H, D)), np.float32)
             o = np.zeros(n * H * D, np.float32)
             t = time.perf_counter()
             if ref is not None:
@@ -264,6 +338,23 @@ def prefill_workload(args, cpu):
     return res
 
 
+def decode_parity(O, q, k, v, kc, vc, lengths, gq, gk, fr, H, KV, D, threads):
+    """the timed decode step's output against the C restatement: QK-norm and
+    RoPE of each sequence's new q and k at its position, then
+    kernels::attention over its cached positions [0, L) and the new token"""
+    import numpy as np
+    want = []
+    for b, L in enumerate(lengths):
+        qn, kn = O.qk_norm_rope(q[b].float().cpu().numpy().reshape(1, H, D),
+                                k[b].float().cpu().numpy().reshape(1, KV, D), 1, L, H, KV, D, D,
+                                gq, gk, 1e-6, fr, D)
+        keys = np.concatenate([kc[b, :, :L].float().cpu().numpy().transpose(1, 0, 2), kn], 0)
+        vals = np.concatenate([vc[b, :, :L].float().cpu().numpy().transpose(1, 0, 2),
+                               v[b].float().cpu().numpy().reshape(1, KV, D)], 0)
+        want.append(O.attention(qn, keys, vals, 1, L, H, KV, D, D, nthreads=threads)[0])
+    return np.stack(want)
+
+
 def decode_workload(args, cpu):
     import numpy as np
     import torch
@@ -289,11 +380,14 @@ def decode_workload(args, cpu):
 
     nbytes = 2048.0 * sum(L + 1 for L in lengths)
     step_ms, k_ms, launched_ms = time_steps(step, args.steps, args.warmup, "decode_attention_kernel")
+    merge_ms, merge_n = aigpu.profile_read("decode_merge_kernel")   # pass 2 of time_steps
     res = {
         "workload": "configs[3] qwen3-30b-a3b batched ragged GQA decode B=32 L~U[1k,32k] 32q/4kv D=128 bf16 KV",
         "dtype": "bf16",
         "value": nbytes / (step_ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": step_ms,
         "step_frac": nbytes / (step_ms * 1e-3) / 1e9 / PEAK_HBM,
+        "kernels_ms_per_step": launched_ms,
+        "merge_kernel_ms": merge_ms / merge_n if merge_n else None,
         "kv_bytes": nbytes,
         "roofline": {"kernel": "decode_attention_kernel", "bound": "hbm",
                      "achieved": nbytes / (k_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
@@ -302,6 +396,11 @@ def decode_workload(args, cpu):
     }
     if cpu is not None:
         O, ref, kind, threads = cpu
+        got = out.cpu().numpy()
+        want = decode_parity(O, q, k, v, kc, vc, lengths, gq.cpu().numpy(), gk.cpu().numpy(),
+                             fr.cpu().numpy(), H, KV, D, threads)
+        res["parity"] = parity(want, got, 2e-3, 1e-3, "all 32 sequences x 32 heads against the C restatement "
+                                                      "of QK-norm, RoPE and kernels::attention")
         qh = q.float().cpu().numpy()
 
         def run(nthreads, budget):
@@ -347,10 +446,11 @@ def decode_workload(args, cpu):
         aigpu.decode(q, k, v, out, kcu, vcu, posu, Lu, H, KV, D, q_norm=gq, k_norm=gk, freqs=fr, rotary_dims=D)
 
     ubytes = 2048.0 * B * (Lu + 1)
-    u_step, u_k, _ = time_steps(step_uniform, args.steps, args.warmup, "decode_attention_kernel")
+    u_step, u_k, u_all = time_steps(step_uniform, args.steps, args.warmup, "decode_attention_kernel")
     res["uniform_32k"] = {"workload": "B=32, every sequence at L=32768, 32q/4kv D=128 bf16 KV",
                           "value": ubytes / (u_step * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": u_step,
                           "step_frac": ubytes / (u_step * 1e-3) / 1e9 / PEAK_HBM,
+                          "kernels_ms_per_step": u_all,
                           "kernel_ms": u_k, "kernel_frac": ubytes / (u_k * 1e-3) / 1e9 / PEAK_HBM,
                           "kv_bytes": ubytes}
     del kcu, vcu
@@ -409,15 +509,19 @@ def delta_workload(args, cpu):
         bh = beta.cpu().numpy()
         t = time.perf_counter()
         if ref is not None:
-            O.ref_gated_delta_rule(qh, kh, vh, gh, bh)
+            want, want_state = O.ref_gated_delta_rule(qh, kh, vh, gh, bh)
             what = "the reference's kernels::deltaStep driven token by token (restated l2norm/q-scale glue)"
         else:
-            O.gated_delta_rule(qh, kh, vh, gh, bh, nthreads=1)
+            want, want_state = O.gated_delta_rule(qh, kh, vh, gh, bh, nthreads=1)
             what = "the C restatement of deltaStep"
         dt = time.perf_counter() - t
         res["cpu_baseline"] = {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
                                "sample": f"all 16384 tokens x 32 value heads, single-threaded as "
                                          f"gatedDeltaNetMixer runs it ({dt:.1f} s): {what}"}
+        # the timed step (state zeroed, then the whole sequence) against the
+        # same run: every output row and the final state
+        res["parity"] = parity(want, out.cpu().numpy(), 2e-3, 1e-3, f"all 16384 x 32 x 128 outputs against {what}")
+        res["parity"]["state"] = parity(want_state, state.cpu().numpy(), 2e-3, 1e-3, "the final 32 x 128 x 128 state")
     return res
 
 
@@ -498,7 +602,8 @@ def dense_workload(args, cpu):
     import aigpu
     H, NL, NH, KV, D, I, V = 1024, 28, 16, 8, 128, 3072, 151936
     start = 4096
-    cap = start + args.warmup + 2 * args.steps + 8   # time_steps runs the steps twice
+    ramp = 200   # clock-ramp steps at most; each step decodes the next position
+    cap = start + ramp + args.warmup + 2 * args.steps + 8   # time_steps runs the steps twice
     gen = torch.Generator(device="cuda").manual_seed(7)
 
     def w(n, k):
@@ -530,13 +635,13 @@ def dense_workload(args, cpu):
         dec.decode(emb, state["pos"])
         state["pos"] += 1
 
-    step_ms, g_ms, launched_ms = time_steps(step, args.steps, args.warmup, "dense_gemv_kernel")
+    step_ms, g_ms, launched_ms = time_steps(step, args.steps, args.warmup, "dense_gemv_kernel", ramp_max=ramp)
     gemv_total, gemv_n = aigpu.profile_read("dense_gemv_kernel")   # pass 2 of time_steps
     attn_total, attn_n = aigpu.profile_read("dense_attn_kernel")
     dec.close()
     del keep
     weight_bytes = 2.0 * (NL * (H * NH * D + 2 * H * KV * D + NH * D * H + 3 * H * I) + V * H)
-    pos_mid = start + args.warmup + args.steps * 1.5   # mean position of the profiled steps
+    pos_mid = state["pos"] - args.steps * 0.5   # mean position of the profiled steps
     kv_bytes = NL * 2.0 * pos_mid * KV * D * 4
     gemv_ms = gemv_total / args.steps
     attn_ms = attn_total / args.steps
@@ -618,6 +723,7 @@ def mixer_workload(args, cpu):
 
     sep_ms, _, _ = time_steps(separate, args.steps, args.warmup, "gemm_kernel")
     step_ms, gd_ms, _ = time_steps(fused, args.steps, args.warmup, "gemm_dma_kernel")
+    aigpu.check_range()   # no fp16 range error in any timed call
     proj = 2.0 * S * HID * (2 * H * D + 2 * KV * D)
     attn = 2.0 * D * H * S * (S + 1)
     flop = proj + attn
@@ -785,12 +891,12 @@ def gdn_workload(args, cpu):
     return res
 
 
-def small_workloads(args):
-    """configs[0] and configs[1]: launch-latency-bound, reported as measured"""
+def cfg2_workload(args, cpu):
+    """Qwen3-0.6B decode, one token against 4096 cached positions
+    (latency-bound: 16.8 MB of K and V)"""
+    import numpy as np
     import torch
     import aigpu
-    out = []
-    # configs[1]: Qwen3-0.6B decode at 4096
     H, KV, D, L = 16, 8, 128, 4096
     gen = torch.Generator(device="cuda").manual_seed(1)
     q = randn((1, H, D), gen, torch.bfloat16)
@@ -802,26 +908,244 @@ def small_workloads(args):
     fr = torch.from_numpy(rotary_table(D, 1e6)).cuda()
     pos = torch.tensor([L], dtype=torch.int32, device="cuda")
     o = torch.empty((1, H, D), dtype=torch.float32, device="cuda")
-    step_ms, k_ms, _ = time_steps(lambda: aigpu.decode(q, k, v, o, kc, vc, pos, L, H, KV, D, q_norm=gq,
-                                                       k_norm=gk, freqs=fr, rotary_dims=D),
-                                  max(args.steps, 50), args.warmup, "decode_attention_kernel")
+
+    def step():
+        aigpu.decode(q, k, v, o, kc, vc, pos, L, H, KV, D, q_norm=gq, k_norm=gk, freqs=fr, rotary_dims=D)
+
+    step_ms, k_ms, launched_ms = time_steps(step, max(args.steps, 50), args.warmup, "decode_attention_kernel")
+    merge_ms, merge_n = aigpu.profile_read("decode_merge_kernel")
     nbytes = 2.0 * (L + 1) * KV * D * 2
-    out.append({"workload": "configs[1] qwen3-0.6b decode L=4096 16q/8kv D=128", "unit": "GB/s",
-                "value": nbytes / (step_ms * 1e-3) / 1e9, "ms_per_step": step_ms,
-                "kernel_ms": k_ms, "kernel_frac_of_hbm": nbytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM})
-    # GPT-2 MHA prefill fp32 through the exact fp32 path (device form)
+    res = {"workload": "configs[1] qwen3-0.6b decode L=4096 16q/8kv D=128 bf16 KV, QK-norm+RoPE", "dtype": "bf16",
+           "unit": "GB/s", "value": nbytes / (step_ms * 1e-3) / 1e9, "ms_per_step": step_ms,
+           "kernels_ms_per_step": launched_ms, "merge_kernel_ms": merge_ms / merge_n if merge_n else None,
+           "roofline": {"kernel": "decode_attention_kernel", "bound": "hbm",
+                        "achieved": nbytes / (k_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
+                        "frac": nbytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None, "kernel_ms": k_ms,
+                        "bytes_per_launch": nbytes,
+                        "note": "latency-bound: 16.8 MB take 2.1 us at 8 TB/s"}}
+    if cpu is not None:
+        O, ref, kind, threads = cpu
+        want = decode_parity(O, q, k, v, kc, vc, [L], gq.cpu().numpy(), gk.cpu().numpy(), fr.cpu().numpy(),
+                             H, KV, D, threads)
+        res["parity"] = parity(want, o.cpu().numpy(), 2e-3, 1e-3, "16 heads against the C restatement of QK-norm, "
+                                                                  "RoPE and kernels::attention")
+        qh = np.ascontiguousarray(q.float().cpu().numpy().reshape(-1))
+        keys = np.ascontiguousarray(kc[0].float().cpu().numpy().transpose(1, 0, 2)).reshape(-1)
+        vals = np.ascontiguousarray(vc[0].float().cpu().numpy().transpose(1, 0, 2)).reshape(-1)
+        out = np.zeros(H * D, np.float32)
+
+        def call(nthreads):
+            cpu_threads(cpu, nthreads)
+            if ref is not None:
+                return lambda: ref.ref_attention(qh, keys, vals, out, 1, L, H, KV, D, D, 0, 1)
+            return lambda: O.attention(qh.reshape(1, H, D), keys.reshape(-1, KV, D), vals.reshape(-1, KV, D), 1, L,
+                                       H, KV, D, D, nthreads=nthreads)
+
+        t1, n1 = median_time(call(1), 7)
+        tp, npool = median_time(call(threads), 7)
+        cpu_threads(cpu, threads)
+        res["cpu_baseline"] = {"value": nbytes / tp / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
+                               "cpu_model": cpu_model(), "ms": tp * 1e3,
+                               "single_core": {"value": nbytes / t1 / 1e9, "unit": "GB/s", "ms": t1 * 1e3},
+                               "sample": f"the whole call: kernels::attention (count=1, start=4096), fp32 "
+                                         f"position-major KV, median of {npool} (pool) and {n1} (one thread) runs "
+                                         f"after a warm-up; GB/s on the same bf16 KV byte count. The reference "
+                                         f"threads attention only above 262144 work units (Kernels.hpp:165), so "
+                                         f"this call runs on one thread either way"}
+    return res
+
+
+def cfg1_workload(args, cpu):
+    """GPT-2-small MHA prefill, fp32, 128 tokens, through the
+    fp32 drop-in aigpu_attention_device (position-major KV, as kernels::attention)"""
+    import numpy as np
+    import torch
+    import aigpu
     S, H, D = 128, 12, 64
+    gen = torch.Generator(device="cuda").manual_seed(0)
     qf = torch.randn((S, H, D), generator=gen, device="cuda")
     kf = torch.randn((S, H, D), generator=gen, device="cuda")
     vf = torch.randn((S, H, D), generator=gen, device="cuda")
     of = torch.empty((S, H, D), dtype=torch.float32, device="cuda")
-    step_ms, k_ms, _ = time_steps(lambda: aigpu.attention_device(qf, kf, vf, of, S, 0, H, H, D, D, H * D, D),
-                                  max(args.steps, 50), args.warmup, "attention_f32_kernel")
+
+    def step():
+        aigpu.attention_device(qf, kf, vf, of, S, 0, H, H, D, D, H * D, D)
+
+    step_ms, k_ms, launched_ms = time_steps(step, max(args.steps, 50), args.warmup, "attention_f32_kernel")
     flops = 4.0 * D * H * S * (S + 1) / 2
-    out.append({"workload": "configs[0] gpt2-small MHA prefill fp32 S=128 12 heads D=64", "unit": "TFLOP/s",
-                "value": flops / (step_ms * 1e-3) / 1e12, "ms_per_step": step_ms, "kernel_ms": k_ms,
-                "kernel_frac_of_fp32": flops / (k_ms * 1e-3) / 1e12 / PEAK_MFMA_F32})
-    return out
+    res = {"workload": "configs[0] gpt2-small MHA prefill fp32 S=128 12 heads D=64", "dtype": "f32",
+           "unit": "TFLOP/s", "value": flops / (step_ms * 1e-3) / 1e12, "ms_per_step": step_ms,
+           "roofline": {"kernel": "attention_f32_kernel", "bound": "fp32",
+                        "achieved": flops / (k_ms * 1e-3) / 1e12, "peak": PEAK_MFMA_F32, "unit": "TFLOP/s",
+                        "frac": flops / (k_ms * 1e-3) / 1e12 / PEAK_MFMA_F32, "traffic": None, "kernel_ms": k_ms,
+                        "flops_per_launch": flops,
+                        "note": "latency-bound: 25.4 MFLOP take 0.16 us at the fp32 peak"}}
+    if cpu is not None:
+        O, ref, kind, threads = cpu
+        qh, kh, vh = (np.ascontiguousarray(t.cpu().numpy()) for t in (qf, kf, vf))
+        out = np.zeros(S * H * D, np.float32)
+
+        def call(threaded):
+            if ref is not None:
+                return lambda: ref.ref_attention(qh.reshape(-1), kh.reshape(-1), vh.reshape(-1), out, S, 0, H, H, D,
+                                                 D, 0, threaded)
+            return lambda: O.attention(qh, kh, vh, S, 0, H, H, D, D, nthreads=threads if threaded else 1)
+
+        cpu_threads(cpu, threads)
+        call(0)()
+        want = out.reshape(S, H, D).copy() if ref is not None else O.attention(qh, kh, vh, S, 0, H, H, D, D)
+        res["parity"] = parity(want, of.cpu().numpy(), 1e-5, None,
+                               "every output against the reference's own kernels::attention"
+                               if ref is not None else "every output against the C restatement")
+        t1, n1 = median_time(call(0), 7)
+        tp, npool = median_time(call(1), 7)
+        res["cpu_baseline"] = {"value": flops / tp / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": kind,
+                               "cpu_model": cpu_model(), "ms": tp * 1e3,
+                               "single_core": {"value": flops / t1 / 1e12, "unit": "TFLOP/s", "ms": t1 * 1e3},
+                               "sample": f"the whole call: kernels::attention (count=128, start=0), threaded "
+                                         f"(1536 query-head tasks of 64-key history: below the reference's "
+                                         f"262144-unit threshold, Kernels.hpp:165, so one thread) and "
+                                         f"serial; median of {npool} and {n1} runs after a warm-up"}
+    return res
+
+
+def published_workload(args, cpu):
+    """the reference's one published attention measurement: 128 queries after
+    384 cached tokens, 32 query / 8 kv heads, D = 128, 35.8 ms serial and
+    3.2 ms parallel on an M5 Pro CPU (docs/apple-gpu-plan.md:114-118); here
+    the same call on the GPU through the fp32 drop-in and through the bf16
+    flash prefill, and the reference's own kernels::attention on the host"""
+    import numpy as np
+    import torch
+    import aigpu
+    n, start, H, KV, D = 128, 384, 32, 8, 128
+    T = start + n
+    gen = torch.Generator(device="cuda").manual_seed(12)
+    q = torch.randn((n, H, D), generator=gen, device="cuda")
+    keys = torch.randn((T, KV, D), generator=gen, device="cuda")   # position-major, as the reference
+    vals = torch.randn((T, KV, D), generator=gen, device="cuda")
+    out = torch.empty((n, H, D), dtype=torch.float32, device="cuda")
+    flops = 4.0 * D * H * sum(start + i + 1 for i in range(n))
+
+    def step_f32():
+        aigpu.attention_device(q, keys, vals, out, n, start, H, KV, D, D, KV * D, D)
+
+    f_ms, fk_ms, _ = time_steps(step_f32, max(args.steps, 50), args.warmup, "attention_f32_kernel")
+    got_f32 = out.cpu().numpy()
+    # the bf16 flash path: history in the head-major bf16 cache, the 128 new
+    # rows through prep (no norm, no RoPE: kernels::attention alone)
+    qb, kb, vb = q.to(torch.bfloat16), keys[start:].to(torch.bfloat16), vals[start:].to(torch.bfloat16)
+    kc = torch.zeros((KV, T, D), dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    kc[:, :start] = keys[:start].transpose(0, 1).to(torch.bfloat16)
+    vc[:, :start] = vals[:start].transpose(0, 1).to(torch.bfloat16)
+    out_b = torch.empty((n, H, D), dtype=torch.float32, device="cuda")
+
+    def step_flash():
+        aigpu.prefill(qb, kb, vb, out_b, kc, vc, start, H, KV, D)
+
+    b_ms, bk_ms, b_all = time_steps(step_flash, max(args.steps, 50), args.warmup, "prefill_flash_kernel")
+    aigpu.check_range()
+    res = {"workload": "reference microbenchmark shape: 128 queries after 384 cached, 32q/8kv D=128 "
+                       "(docs/apple-gpu-plan.md:114-118: 35.8 ms serial, 3.2 ms parallel on an M5 Pro CPU)",
+           "flops": flops,
+           "gpu_f32": {"entry": "aigpu_attention_device (fp32, position-major KV, kernels::attention semantics)",
+                       "ms_per_step": f_ms, "kernel_ms": fk_ms, "tflops": flops / (f_ms * 1e-3) / 1e12},
+           "gpu_flash_bf16": {"entry": "aigpu_prefill_attention (bf16 in, fp16 MFMA; history conversion, prep, "
+                                       "flash)", "ms_per_step": b_ms, "flash_kernel_ms": bk_ms,
+                              "kernels_ms_per_step": b_all, "tflops": flops / (b_ms * 1e-3) / 1e12}}
+    if cpu is not None:
+        O, ref, kind, threads = cpu
+        qh = np.ascontiguousarray(q.cpu().numpy())
+        kh = np.ascontiguousarray(keys.cpu().numpy())
+        vh = np.ascontiguousarray(vals.cpu().numpy())
+        o = np.zeros(n * H * D, np.float32)
+
+        def call(threaded):
+            if ref is not None:
+                return lambda: ref.ref_attention(qh.reshape(-1), kh.reshape(-1), vh.reshape(-1), o, n, start, H, KV,
+                                                 D, D, 0, threaded)
+            return lambda: O.attention(qh, kh, vh, n, start, H, KV, D, D, nthreads=threads if threaded else 1)
+
+        cpu_threads(cpu, threads)
+        call(0)()
+        want = o.reshape(n, H, D).copy() if ref is not None else O.attention(qh, kh, vh, n, start, H, KV, D, D)
+        res["gpu_f32"]["parity"] = parity(want, got_f32, 1e-5, None, "every output against kernels::attention")
+        # the flash path's inputs are bf16: the reference sees the same
+        # rounded values, widened
+        qr, kr, vr = (np.ascontiguousarray(t.to(torch.bfloat16).float().cpu().numpy()) for t in (q, keys, vals))
+        if ref is not None:
+            ob = np.zeros(n * H * D, np.float32)
+            ref.ref_attention(qr.reshape(-1), kr.reshape(-1), vr.reshape(-1), ob, n, start, H, KV, D, D, 0, 0)
+            want_b = ob.reshape(n, H, D)
+        else:
+            want_b = O.attention(qr, kr, vr, n, start, H, KV, D, D)
+        res["gpu_flash_bf16"]["parity"] = parity(want_b, out_b.cpu().numpy(), 2e-3, 1e-3,
+                                                 "every output against kernels::attention on the same "
+                                                 "bf16-rounded inputs, widened")
+        t1, n1 = median_time(call(0), 5)
+        tp, npool = median_time(call(1), 5)
+        res["cpu_baseline"] = {"kind": kind, "cpu_model": cpu_model(), "cores": threads,
+                               "serial_ms": t1 * 1e3, "parallel_ms": tp * 1e3,
+                               "serial_tflops": flops / t1 / 1e12, "parallel_tflops": flops / tp / 1e12,
+                               "sample": f"kernels::attention, serial and on the static-split pool of {threads} "
+                                         f"threads, median of {n1} / {npool} runs after a warm-up"}
+    return res
+
+
+def bandwidth_workload(args, cpu):
+    """what HBM delivers on this box, beside the 8 TB/s spec peak the HBM
+    fractions use: a 1 GiB device-to-device copy, and the reference's own
+    bandwidth test (src/gpu-testing.cpp:298-351): y = x W^T with W 65536 x
+    4096 bf16 (512 MiB) and one row x, through aigpu_matmul_device's GEMV, and
+    through the reference's matmulNTBF16 on the host"""
+    import numpy as np
+    import torch
+    import aigpu
+    a = torch.empty((1 << 28,), dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    c_ms, ck_ms, _ = time_steps(lambda: aigpu.copy_device(b, a), 20, 5, "copy_kernel")
+    t_ms, _, _ = time_steps(lambda: b.copy_(a), 20, 5, "none")
+    copy_bytes = 2.0 * a.numel() * 4
+    del a, b
+    K, N = 4096, 65536
+    gen = torch.Generator(device="cuda").manual_seed(13)
+    x = torch.randn((1, K), generator=gen, device="cuda")
+    w = torch.randn((N, K), generator=gen, device="cuda").to(torch.bfloat16)
+    y = torch.empty((1, N), dtype=torch.float32, device="cuda")
+    g_ms, gk_ms, _ = time_steps(lambda: aigpu.matmul(x, w, y, "bf16"), max(args.steps, 20), args.warmup,
+                                "gemv_kernel")
+    wbytes = float(N * K * 2)
+    res = {"workload": "HBM bandwidth: device copy and the reference's bf16 GEMV bandwidth test",
+           "peak": PEAK_HBM, "unit": "GB/s",
+           "device_copy": {"bytes": copy_bytes, "ms_per_step": c_ms, "kernel_ms": ck_ms,
+                           "value": copy_bytes / (ck_ms * 1e-3) / 1e9,
+                           "frac": copy_bytes / (ck_ms * 1e-3) / 1e9 / PEAK_HBM,
+                           "what": "aigpu_copy_device (copy_kernel: 16-byte nontemporal loads and stores) of "
+                                   "1 GiB, read + write bytes over the kernel's time"},
+           "torch_copy": {"bytes": copy_bytes, "ms_per_step": t_ms, "value": copy_bytes / (t_ms * 1e-3) / 1e9,
+                          "frac": copy_bytes / (t_ms * 1e-3) / 1e9 / PEAK_HBM,
+                          "what": "torch copy_ of the same 1 GiB"},
+           "gemv_bf16": {"bytes": wbytes, "ms_per_step": g_ms, "kernel_ms": gk_ms,
+                         "value": wbytes / (gk_ms * 1e-3) / 1e9, "frac": wbytes / (gk_ms * 1e-3) / 1e9 / PEAK_HBM,
+                         "what": "gemv_kernel, 512 MiB of bf16 weights against one fp32 row (weight bytes over "
+                                 "kernel time, as the reference's test counts)"}}
+    if cpu is not None:
+        O, ref, kind, threads = cpu
+        wh = w.view(torch.int16).cpu().numpy().view(np.uint16)
+        xh = x.cpu().numpy()
+        res["gemv_bf16"]["parity"] = parity(xh.astype(np.float64) @ O.unpack_bf16(wh).astype(np.float64).T,
+                                            y.cpu().numpy(), 1e-3, 1e-5, "all 65536 outputs against an fp64 product")
+        if ref is not None:
+            out = np.zeros(N, np.float32)
+            cpu_threads(cpu, threads)
+            fn = lambda: ref.ref_matmul_nt_bf16(xh.reshape(-1), wh.ctypes.data, out, 1, K, N, 1)  # noqa: E731
+            tp, runs = median_time(fn, 8)
+            res["cpu_baseline"] = {"value": wbytes / tp / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
+                                   "cpu_model": cpu_model(),
+                                   "sample": f"the reference's matmulNTBF16 on the static-split pool, median of "
+                                             f"{runs} runs after a warm-up"}
+    return res
 
 
 def calibrate_copy():
@@ -840,55 +1164,61 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(each GPU box has one MI355X); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
-    import torch
+    import torch  # noqa: F401
     import aigpu
     aigpu.require()
     if args.calibrate_copy:
         calibrate_copy()
     cpu = None if args.no_cpu else cpu_lib()
-    head = None
+    want = args.workload
+    run = lambda name: want in (name, "all")  # noqa: E731
+    configs = {}
+    if run("prefill"):
+        configs["cfg3"] = prefill_workload(args, cpu)
+    if run("decode"):
+        configs["cfg4"] = decode_workload(args, cpu)
+    if run("delta"):
+        configs["cfg5"] = delta_workload(args, cpu)
+    if run("small"):
+        configs["cfg1"] = cfg1_workload(args, cpu)
+        configs["cfg2"] = cfg2_workload(args, cpu)
     extra = {}
-    if args.workload in ("prefill", "all"):
-        head = prefill_workload(args, cpu)
-    if args.workload in ("decode", "all"):
-        extra["decode"] = decode_workload(args, cpu)
-    if args.workload in ("delta", "all"):
-        extra["delta_rule"] = delta_workload(args, cpu)
-    if args.workload in ("gdn", "all"):
-        extra["gdn_neighbours"] = gdn_workload(args, cpu)
-    if args.workload in ("kda", "all"):
-        extra["kda_rule"] = kda_workload(args, cpu)
-    if args.workload in ("dense", "all"):
-        extra["resident_decoder"] = dense_workload(args, cpu)
-    if args.workload in ("gemm", "all"):
-        extra["projection_gemm"] = gemm_workload(args, cpu)
-    if args.workload in ("mla", "all"):
-        extra["latent_attention"] = mla_workload(args, cpu)
-    if args.workload in ("mixer", "all"):
-        extra["prefill_mixer"] = mixer_workload(args, cpu)
-    if args.workload in ("indexer", "all"):
-        extra["indexer"] = indexer_workload(args, cpu)
-    if args.workload == "all":
-        extra["others"] = small_workloads(args)
-    if head is None:   # a single non-prefill workload becomes the line
-        head = (extra.pop("decode", None) or extra.pop("delta_rule", None) or extra.pop("gdn_neighbours", None)
-                or extra.pop("kda_rule", None) or extra.pop("resident_decoder", None) or extra.pop("projection_gemm", None)
-                or extra.pop("latent_attention", None) or extra.pop("prefill_mixer", None)
-                or extra.pop("indexer"))
+    if run("published"):
+        extra["published_shape"] = published_workload(args, cpu)
+    if run("bandwidth"):
+        extra["bandwidth"] = bandwidth_workload(args, cpu)
+    rows = {}
+    for name, fn in (("gdn_neighbours", gdn_workload), ("kda_rule", kda_workload), ("resident_decoder", dense_workload),
+                     ("projection_gemm", gemm_workload), ("latent_attention", mla_workload),
+                     ("prefill_mixer", mixer_workload), ("indexer", indexer_workload)):
+        key = {"gdn_neighbours": "gdn", "kda_rule": "kda", "resident_decoder": "dense", "projection_gemm": "gemm",
+               "latent_attention": "mla", "prefill_mixer": "mixer", "indexer": "indexer"}[name]
+        if run(key):
+            rows[name] = fn(args, cpu)
+    # the line's headline: configs[2] (prefill) when it ran, else the first that did
+    order = ["cfg3", "cfg4", "cfg5", "cfg2", "cfg1"]
+    head = next((configs[c] for c in order if c in configs), None)
+    if head is None:
+        head = next(iter(rows.values()), None) or next(iter(extra.values()))
     line = {
         "metric": "attn TFLOP/s (prefill) & KV GB/s (decode) as % roofline, 1 MI355X vs host CPU",
-        "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": head["dtype"],
+        "value": head.get("value"), "unit": head.get("unit"), "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head.get("ms_per_step"), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": head.get("dtype"),
         "data": "synthetic (torch seeded N(0,1) at each configuration's shape)",
-        "config": {"workload": head["workload"], "device": aigpu.device_name()},
-        "roofline": head["roofline"],
+        "config": {"workload": head.get("workload"), "device": aigpu.device_name()},
+        "roofline": head.get("roofline"),
         "cpu_baseline": head.get("cpu_baseline"),
+        "parity": head.get("parity"),
+        "clock_ramp_s": CLOCK_RAMP_S,
     }
     details = {k: v for k, v in head.items() if k not in line and k != "workload"}
     if details:
         line["details"] = details
+    line["configs"] = {c: configs[c] for c in ["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"] if c in configs}
     line.update(extra)
+    if rows:
+        line["next_rows"] = rows
     print(json.dumps(line))
 
 

@@ -138,10 +138,12 @@ AIGPU_ABI int aigpu_attention_device(const AiGpuAttention* args);
 /*    positions start..start+count-1, against a head-major bf16 cache that    */
 /*    already holds positions [0, start). Flash-style kernel on fp16 MFMA     */
 /*    with fp32 accumulation. dim must be 64 or 128. q, k, v (after norm,     */
-/*    RoPE and q's scale) and the cached history go through fp16: a value     */
-/*    fp16 cannot hold (|x| >= 65520) makes the call return 0 with a reason;  */
-/*    to check, the call waits for its stream unless that stream is being    */
-/*    captured into a graph.                                                  */
+/*    RoPE and q's scale) and the cached history go through fp16. A value     */
+/*    fp16 cannot hold (|x| >= 65520) raises the call's range flag (below);   */
+/*    the call has still written out and the new k, v rows of the cache.     */
+/*    The device form is asynchronous: it launches on its stream and         */
+/*    returns without waiting, and aigpu_range_status reports its flag. The   */
+/*    host form waits for its kernels anyway and returns 0 with a reason.     */
 /* ------------------------------------------------------------------------ */
 typedef struct AiGpuPrefill {
     const void* q;            /* [count][heads][qStride], inType */
@@ -168,6 +170,28 @@ AIGPU_ABI int aigpu_prefill_attention(const AiGpuPrefill* args);
 /* q, k, v, out, qNorm, kNorm, rotaryFrequencies are host pointers (fp32 or
    bf16 per inType); the caches are device allocations. Staged in and out. */
 AIGPU_ABI int aigpu_prefill_attention_host(const AiGpuPrefill* args);
+
+/* A plain streaming copy of `bytes` between two device buffers (16-byte
+   aligned, not overlapping) on `stream`. No counterpart in the reference's
+   ABI: it measures what HBM delivers on this part, the ceiling beside the
+   spec peak for the HBM-bound kernels (the reference's GPU testing measures
+   bandwidth with a bf16 GEMV, src/gpu-testing.cpp:298-351). Asynchronous. */
+AIGPU_ABI int aigpu_copy_device(void* dst, const void* src, uint64_t bytes, void* stream);
+
+/* fp16 range flags of the asynchronous prefill calls (aigpu_prefill_attention,
+   aigpu_prefill_mixer). No counterpart in the reference, whose calls are all
+   synchronous on the host. Every prefill call takes the next ticket (1, 2,
+   ...; aigpu_range_ticket returns the latest) and a flag word of its own,
+   which its kernels raise when a value overflows fp16. aigpu_range_status
+   waits for the device and returns 1 when no call since the previous query
+   raised its flag; otherwise 0, with *ticket (when not NULL) the earliest
+   raising call's ticket and aigpu_last_error naming it. Either way the flags
+   are clear afterwards. A call captured into a graph has no ticket of its
+   own: its replays raise a shared flag, reported as ticket UINT64_MAX. 255
+   tickets share the flag words in turn, so a flag is lost only if 255 later
+   calls are queued before its call runs. */
+AIGPU_ABI uint64_t aigpu_range_ticket(void);
+AIGPU_ABI int aigpu_range_status(uint64_t* ticket);
 
 /* ------------------------------------------------------------------------ */
 /* 4. Decode: one new token for each of `batch` sequences with ragged         */
@@ -211,8 +235,10 @@ AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode* args);
    whose single sequence does not fit returns 0 with the reason. Every call
    on a GPU shares that array: calls on different streams are ordered by the
    backend, but replays of graphs captured from it that overlap on one GPU
-   race on it. Same arguments, kernels and results as
-   aigpu_decode_attention. */
+   race on it. Make one call (or aigpu_available) before a capture: the
+   first call of a process sets up the backend and looks up the array's
+   address, which capture does not allow. Same arguments, kernels and
+   results as aigpu_decode_attention. */
 AIGPU_ABI int aigpu_decode_attention_static(const AiGpuDecode* args);
 
 /* ------------------------------------------------------------------------ */
@@ -448,7 +474,8 @@ typedef struct AiGpuPrefillMixer {
     uint64_t count, start, hidden, heads, kvHeads, dim, window, capacity;
     void* stream;
 } AiGpuPrefillMixer;
-/* returns 0 with a reason for values outside fp16's range, as section 3 */
+/* asynchronous like aigpu_prefill_attention: values outside fp16's range
+   raise the call's range flag (aigpu_range_status) */
 AIGPU_ABI int aigpu_prefill_mixer(const AiGpuPrefillMixer* args);
 
 /* ------------------------------------------------------------------------ */

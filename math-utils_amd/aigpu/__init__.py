@@ -118,6 +118,9 @@ SIGNATURES = {
     "aigpu_attention_device": (C.c_int, [C.POINTER(AiGpuAttention)]),
     "aigpu_prefill_attention": (C.c_int, [C.POINTER(AiGpuPrefill)]),
     "aigpu_prefill_attention_host": (C.c_int, [C.POINTER(AiGpuPrefill)]),
+    "aigpu_copy_device": (C.c_int, [_vp, _vp, _u64, _vp]),
+    "aigpu_range_ticket": (_u64, []),
+    "aigpu_range_status": (C.c_int, [C.POINTER(_u64)]),
     "aigpu_decode_attention": (C.c_int, [C.POINTER(AiGpuDecode)]),
     "aigpu_decode_attention_host": (C.c_int, [C.POINTER(AiGpuDecode)]),
     "aigpu_decode_attention_static": (C.c_int, [C.POINTER(AiGpuDecode)]),
@@ -276,11 +279,41 @@ def attention_device(q, keys, values, out, count, start, heads, kv_heads, dim, q
     return out
 
 
+def copy_device(dst, src, nbytes=None, stream=None):
+    """aigpu_copy_device: nbytes (default: all of src) from GPU tensor src to
+    GPU tensor dst with the streaming copy kernel; asynchronous"""
+    for t, n in ((dst, "dst"), (src, "src")):
+        _need(t, n)
+    nbytes = src.numel() * src.element_size() if nbytes is None else nbytes
+    if nbytes > dst.numel() * dst.element_size():
+        raise ValueError("dst is smaller than the copy")
+    _check(lib().aigpu_copy_device(_ptr(dst), _ptr(src), nbytes, _stream(stream)))
+    return dst
+
+
+def range_ticket():
+    """the ticket of the latest prefill call (aigpu_range_ticket)"""
+    return int(lib().aigpu_range_ticket())
+
+
+def check_range():
+    """waits for the device (aigpu_range_status); raises AiGpuError, with the
+    earliest offending call's ticket as .ticket, when a prefill call since the
+    last check met a value outside fp16's range"""
+    t = _u64(0)
+    if not lib().aigpu_range_status(C.byref(t)):
+        err = AiGpuError(last_error())
+        err.ticket = t.value
+        raise err
+
+
 def prefill(q, k, v, out, key_cache, value_cache, start, heads, kv_heads, dim, q_stride=None,
             q_norm=None, k_norm=None, eps=1e-6, norm_offset=0.0, freqs=None, rotary_dims=0,
-            window=0, capacity=None, output_gate=False, stream=None):
+            window=0, capacity=None, output_gate=False, stream=None, check=False):
     """Device form of attentionMixer for `count` tokens at positions start..;
-    output_gate applies sigmoid of each q row's second half (q_stride >= 2 dim)."""
+    output_gate applies sigmoid of each q row's second half (q_stride >= 2 dim).
+    Asynchronous: check=True waits and raises for an fp16 range error
+    (check_range)."""
     for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out"), (key_cache, "key_cache"),
                  (value_cache, "value_cache"), (q_norm, "q_norm"), (k_norm, "k_norm"),
                  (freqs, "freqs")):
@@ -295,6 +328,37 @@ def prefill(q, k, v, out, key_cache, value_cache, start, heads, kv_heads, dim, q
                      qStride=q_stride or dim, window=window, capacity=cap,
                      stream=_stream(stream))
     _check(lib().aigpu_prefill_attention(C.byref(a)))
+    if check:
+        check_range()
+    return out
+
+
+def prefill_host(q, k, v, key_cache, value_cache, start, heads, kv_heads, dim, q_stride=None,
+                 q_norm=None, k_norm=None, eps=1e-6, norm_offset=0.0, freqs=None, rotary_dims=0,
+                 window=0, capacity=None, output_gate=False):
+    """Host form (aigpu_prefill_attention_host): q, k, v numpy fp32 arrays
+    ([count][heads][q_stride], [count][kv_heads][dim]), the norms and
+    frequencies numpy fp32 or None, the caches GPU tensors; returns out
+    [count][heads][dim] as numpy. Synchronous: an fp16 range error raises."""
+    for t, n in ((key_cache, "key_cache"), (value_cache, "value_cache")):
+        _need(t, n)
+    arrs = [np.ascontiguousarray(x, np.float32) if x is not None else None
+            for x in (q, k, v, q_norm, k_norm, freqs)]
+    q, k, v, q_norm, k_norm, freqs = arrs
+    count = q.shape[0]
+    out = np.zeros((count, heads, dim), np.float32)
+    cap = capacity if capacity is not None else key_cache.shape[-2]
+
+    def hp(x):
+        return None if x is None else x.ctypes.data
+
+    a = AiGpuPrefill(q=hp(q), k=hp(k), v=hp(v), out=out.ctypes.data, keyCache=_ptr(key_cache),
+                     valueCache=_ptr(value_cache), qNorm=hp(q_norm), kNorm=hp(k_norm),
+                     rotaryFrequencies=hp(freqs), epsilon=eps, normOffset=norm_offset,
+                     rotaryDims=rotary_dims if freqs is not None else 0, inType=F32,
+                     outputGate=1 if output_gate else 0, count=count, start=start, heads=heads,
+                     kvHeads=kv_heads, dim=dim, qStride=q_stride or dim, window=window, capacity=cap)
+    _check(lib().aigpu_prefill_attention_host(C.byref(a)))
     return out
 
 
@@ -599,13 +663,14 @@ SIGNATURES["aigpu_prefill_mixer"] = (C.c_int, [C.POINTER(AiGpuPrefillMixer)])
 
 def prefill_mixer(x, weights, out, key_cache, value_cache, start, heads, kv_heads, dim, q_norm=None,
                   k_norm=None, eps=1e-6, norm_offset=0.0, freqs=None, rotary_dims=0, window=0, capacity=None,
-                  output_gate=False, accumulate=False, stream=None):
+                  output_gate=False, accumulate=False, stream=None, check=False):
     """attentionMixer for the x.shape[0] tokens at positions start..: x [count][hidden]
     fp32; weights maps "q", "k", "v", "o" to dicts with "w" (the stored weight
     as a GPU tensor: fp32, bf16, int8 codes or packed 4-bit), "kind" (a
     WEIGHT_TYPES key), "out" (rows) and optional "scales" / "bias" GPU tensors;
     out [count][hidden] fp32 (+= with accumulate); the head-major bf16 caches
-    gain positions start .. start + count - 1."""
+    gain positions start .. start + count - 1. Asynchronous: check=True waits
+    and raises for an fp16 range error (check_range)."""
     for t, n in ((x, "x"), (out, "out"), (key_cache, "key_cache"), (value_cache, "value_cache"),
                  (q_norm, "q_norm"), (k_norm, "k_norm"), (freqs, "freqs")):
         _need(t, n)
@@ -627,6 +692,8 @@ def prefill_mixer(x, weights, out, key_cache, value_cache, start, heads, kv_head
                              count=count, start=start, hidden=hidden, heads=heads, kvHeads=kv_heads, dim=dim,
                              window=window, capacity=cap, stream=_stream(stream))
     _check(lib().aigpu_prefill_mixer(C.byref(args)))
+    if check:
+        check_range()
     return out
 
 

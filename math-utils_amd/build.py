@@ -18,7 +18,7 @@ OUT = os.path.join(HERE, "aigpu")
 OBJ = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["abi.hip", "attention_f32.hip", "prefill.hip", "decode.hip", "delta_rule.hip", "gdn.hip", "kda.hip", "matmul.hip", "dense.hip", "latent.hip", "mixer.hip", "indexer.hip"]
+SOURCES = ["abi.hip", "attention_f32.hip", "prefill.hip", "decode.hip", "delta_rule.hip", "gdn.hip", "kda.hip", "matmul.hip", "dense.hip", "latent.hip", "mixer.hip", "indexer.hip", "copy.hip"]
 
 # packed-fp32 instructions off; gfx950 only; only AIGPU_ABI symbols exported
 HIP_FLAGS = [

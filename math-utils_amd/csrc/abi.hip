@@ -48,13 +48,14 @@ Context::Context() {
         return;
     }
     name = props.name;
-    if (hipHostMalloc(reinterpret_cast<void**>(&rangeHost), sizeof(uint32_t), hipHostMallocMapped) != hipSuccess ||
+    if (hipHostMalloc(reinterpret_cast<void**>(&rangeHost), RANGE_SLOTS * sizeof(uint32_t), hipHostMallocMapped) !=
+            hipSuccess ||
         hipHostGetDevicePointer(reinterpret_cast<void**>(&rangeDev), rangeHost, 0) != hipSuccess) {
         (void)hipGetLastError();
-        error = "hipHostMalloc of the fp16 range flag failed";
+        error = "hipHostMalloc of the fp16 range flags failed";
         return;
     }
-    *rangeHost = 0;
+    for (int i = 0; i < RANGE_SLOTS; ++i) rangeHost[i] = 0;
     if (hipEventCreateWithFlags(&handoff, hipEventDisableTiming) != hipSuccess) {
         (void)hipGetLastError();
         error = "hipEventCreate of the stream handoff event failed";
@@ -63,20 +64,60 @@ Context::Context() {
     ok = true;
 }
 
-bool Context::checkRange(const char* what, hipStream_t stream) {
+static bool capturing(hipStream_t stream) {
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
         (void)hipGetLastError();
-        capture = hipStreamCaptureStatusNone;
+        return false;
     }
-    if (capture != hipStreamCaptureStatusNone) return true;
-    if (hipStreamSynchronize(stream) != hipSuccess)
-        return fail(std::string(what) + ": " + hipGetErrorString(hipGetLastError()));
-    if (__atomic_load_n(rangeHost, __ATOMIC_ACQUIRE) == 0) return true;
-    __atomic_store_n(rangeHost, 0u, __ATOMIC_RELEASE);
-    return fail(std::string(what) +
-                ": a q, k or v element (after its norm, rotation and scale) or a cached key or value "
-                "lies outside fp16's range (|x| > 65504): the fp16 working copies cannot hold it");
+    return capture != hipStreamCaptureStatusNone;
+}
+
+uint32_t* Context::rangeSlot(hipStream_t stream, uint64_t* ticket) {
+    if (capturing(stream)) {
+        *ticket = UINT64_MAX;
+        return rangeDev;   // slot 0: not cleared, a replay of an earlier capture may have raised it
+    }
+    const uint64_t t = ++rangeTickets;
+    const int slot = 1 + int((t - 1) % (RANGE_SLOTS - 1));
+    // the slot's previous ticket (RANGE_SLOTS - 1 calls ago) has long
+    // completed unless that many calls are queued; a flag it raised is kept
+    if (__atomic_load_n(rangeHost + slot, __ATOMIC_ACQUIRE) != 0) rangeRaised.push_back(slotTicket[slot]);
+    __atomic_store_n(rangeHost + slot, 0u, __ATOMIC_RELEASE);
+    slotTicket[slot] = t;
+    *ticket = t;
+    return rangeDev + slot;
+}
+
+bool Context::rangeRaisedFor(uint64_t ticket) {
+    const int slot = ticket == UINT64_MAX ? 0 : 1 + int((ticket - 1) % (RANGE_SLOTS - 1));
+    if (slot != 0 && slotTicket[slot] != ticket) return false;
+    if (__atomic_load_n(rangeHost + slot, __ATOMIC_ACQUIRE) == 0) return false;
+    __atomic_store_n(rangeHost + slot, 0u, __ATOMIC_RELEASE);
+    return true;
+}
+
+int Context::rangeStatus(uint64_t* ticket) {
+    if (ticket) *ticket = 0;
+    const hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return fail(std::string("range status: ") + hipGetErrorString(e)), 0;
+    std::vector<uint64_t> raised;
+    raised.swap(rangeRaised);
+    for (int slot = 0; slot < RANGE_SLOTS; ++slot) {
+        if (__atomic_load_n(rangeHost + slot, __ATOMIC_ACQUIRE) == 0) continue;
+        __atomic_store_n(rangeHost + slot, 0u, __ATOMIC_RELEASE);
+        raised.push_back(slot == 0 ? UINT64_MAX : slotTicket[slot]);
+    }
+    if (raised.empty()) return 1;
+    uint64_t first = raised[0];
+    for (uint64_t t : raised) first = t < first ? t : first;
+    if (ticket) *ticket = first;
+    const std::string who = first == UINT64_MAX ? std::string("a prefill call captured into a graph (a replay)")
+                                                : "prefill call ticket " + std::to_string(first);
+    fail(who + (raised.size() > 1 ? " (and " + std::to_string(raised.size() - 1) + " more)" : std::string()) +
+         ": a q, k or v element (after its norm, rotation and scale) or a cached key or value lies outside "
+         "fp16's range (|x| > 65504): the fp16 working copies cannot hold it");
+    return 0;
 }
 
 Context::~Context() {
@@ -329,6 +370,28 @@ AIGPU_ABI void aigpu_counters(AiGpuCounters* out) {
 
 AIGPU_ABI void aigpu_reset_counters(void) { Context::instance().stats = AiGpuCounters{}; }
 
+AIGPU_ABI int aigpu_copy_device(void* dst, const void* src, uint64_t bytes, void* stream) {
+    Context& ctx = Context::instance();
+    if (!ctx.ok) return 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    const StreamOrder order(ctx, as_stream(stream));
+    return aigpu::launch_copy(dst, src, bytes, order.stream) ? 1 : 0;
+}
+
+AIGPU_ABI uint64_t aigpu_range_ticket(void) {
+    Context& ctx = Context::instance();
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    return ctx.rangeTickets;
+}
+
+AIGPU_ABI int aigpu_range_status(uint64_t* ticket) {
+    Context& ctx = Context::instance();
+    if (ticket) *ticket = 0;
+    if (!ctx.ok) return 0;
+    std::lock_guard<std::recursive_mutex> lock(ctx.gate);
+    return ctx.rangeStatus(ticket);
+}
+
 AIGPU_ABI void aigpu_profile(int enable) {
     Context& ctx = Context::instance();
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
@@ -451,9 +514,9 @@ AIGPU_ABI int aigpu_prefill_attention(const AiGpuPrefill* args) {
     std::lock_guard<std::recursive_mutex> lock(ctx.gate);
     const StreamOrder order(ctx, as_stream(args->stream));
     aigpu::PrefillParams p = prefill_params(args);
-    p.rangeFlag = ctx.rangeDev;
-    return aigpu::launch_prefill(p, order.stream) && ctx.checkRange("prefill", order.stream)
-               ? 1 : 0;
+    uint64_t ticket = 0;
+    p.rangeFlag = ctx.rangeSlot(order.stream, &ticket);
+    return aigpu::launch_prefill(p, order.stream) ? 1 : 0;
 }
 
 AIGPU_ABI int aigpu_prefill_attention_host(const AiGpuPrefill* args) {
@@ -485,8 +548,13 @@ AIGPU_ABI int aigpu_prefill_attention_host(const AiGpuPrefill* args) {
     if (!dev.q || !dev.k || !dev.v) return 0;
     const Clock::time_point mark = Clock::now();
     aigpu::PrefillParams p = prefill_params(&dev);
-    p.rangeFlag = ctx.rangeDev;
-    if (!aigpu::launch_prefill(p, nullptr) || !finish(ctx, mark) || !ctx.checkRange("prefill", nullptr)) return 0;
+    uint64_t ticket = 0;
+    p.rangeFlag = ctx.rangeSlot(nullptr, &ticket);
+    if (!aigpu::launch_prefill(p, nullptr) || !finish(ctx, mark)) return 0;
+    if (ctx.rangeRaisedFor(ticket))
+        return ctx.fail("prefill: a q, k or v element (after its norm, rotation and scale) or a cached key or value "
+                        "lies outside fp16's range (|x| > 65504): the fp16 working copies cannot hold it"),
+               0;
     return copy_out(ctx, args->out, dOut, outBytes) ? 1 : 0;
 }
 
@@ -883,9 +951,9 @@ AIGPU_ABI int aigpu_prefill_mixer(const AiGpuPrefillMixer* args) {
     p.qStride = args->outputGate ? 2 * args->dim : args->dim;
     p.window = args->window;
     p.capacity = args->capacity;
-    return aigpu::launch_prefill_mixer(p, order.stream) &&
-                   ctx.checkRange("prefill mixer", order.stream)
-               ? 1 : 0;
+    uint64_t ticket = 0;
+    p.rangeFlag = ctx.rangeSlot(order.stream, &ticket);
+    return aigpu::launch_prefill_mixer(p, order.stream) ? 1 : 0;
 }
 
 AIGPU_ABI int aigpu_select_keys(const AiGpuSelectKeys* args) {

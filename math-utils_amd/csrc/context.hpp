@@ -53,11 +53,26 @@ struct Context {
     // set during a call that must allocate nothing: no profiling events
     bool noAlloc = false;
 
-    // one word of mapped pinned host memory that kernels converting into the
-    // prefill's fp16 working copies set to 1 when a finite value overflows
-    // fp16; rangeDev is its device address
+    // fp16 range flags: RANGE_SLOTS words of mapped pinned host memory
+    // (rangeDev is their device address). Every prefill call takes a ticket
+    // and the word of its slot; kernels converting into the fp16 working
+    // copies store 1 there when a finite value overflows fp16. Slot 0 belongs
+    // to calls captured into a graph (their replays have no ticket of their
+    // own); tickets 1, 2, ... cycle through slots 1 .. RANGE_SLOTS - 1.
+    static constexpr int RANGE_SLOTS = 256;
     uint32_t* rangeHost = nullptr;
     uint32_t* rangeDev = nullptr;
+    uint64_t rangeTickets = 0;                 // tickets issued so far
+    uint64_t slotTicket[RANGE_SLOTS] = {};     // the ticket that last took each slot
+    std::vector<uint64_t> rangeRaised;         // raised tickets found when their slot was taken again
+    // a ticket for a call on `stream` and the device address of its flag word
+    // (cleared); a stream being captured gets slot 0 and ticket UINT64_MAX
+    uint32_t* rangeSlot(hipStream_t stream, uint64_t* ticket);
+    // whether `ticket`'s word is raised, clearing it (its call has completed)
+    bool rangeRaisedFor(uint64_t ticket);
+    // waits for the device; 1 when no call since the last query raised its
+    // word, else 0 with the error naming the earliest ticket that did
+    int rangeStatus(uint64_t* ticket);
 
     // calls on different streams share the scratch slots (and the fixed
     // decode scratch): an event recorded on the stream of each call, which
@@ -65,10 +80,6 @@ struct Context {
     hipEvent_t handoff = nullptr;
     hipStream_t handoffStream = nullptr;
     bool handoffValid = false;
-    // waits for `stream` and reports (and clears) a raised range flag as a
-    // failure of `what`; a stream being captured into a graph is not waited
-    // for and the flag stays for the next checked call
-    bool checkRange(const char* what, hipStream_t stream);
     struct Pending { std::string kernel; hipEvent_t begin, end; };
     std::vector<Pending> pending;
     std::vector<hipEvent_t> spareEvents;

@@ -41,7 +41,6 @@
 #include "device.hpp"
 #include "kernels.hpp"
 
-#include <cstdlib>
 
 namespace aigpu {
 
@@ -50,6 +49,7 @@ namespace {
 constexpr int MAXG = 8;          // query heads per kv head handled by one workgroup
 constexpr int SLAB = 32;         // positions per wave step
 constexpr int MAXB = 1024;       // sequences per launch (larger batches are split)
+constexpr uint32_t GRID = 512;   // persistent workgroups (two per CU)
 
 struct DecodeArgs {
     DecodeParams p;
@@ -540,14 +540,10 @@ __global__ __launch_bounds__(D) void decode_merge_kernel(DecodeArgs a) {
     p.out[(size_t(b) * p.heads + size_t(kvh) * G + h) * D + d] = gated(p, b, kvh * G + h, d, at / lt);
 }
 
-uint32_t env_u32(const char* name, uint32_t fallback) {
-    const char* env = std::getenv(name);
-    return env ? uint32_t(std::atol(env)) : fallback;
-}
-
 /*
     The fixed scratch of aigpu_decode_attention_static: the split-K records
-    and the prepared queries, in device memory that exists from module load
+    (the queries are prepared inside the attention kernel and need no
+    scratch), in device memory that exists from module load
     until the process ends, so that the entry point allocates nothing. Each
     GPU holds its own copy at its own address; host code never passes the
     array's name (a host-side stand-in) to a kernel, only the address
@@ -600,14 +596,14 @@ bool launch_decode(const DecodeParams& p, hipStream_t stream, const FixedScratch
         return ctx.fail("decode: maxPosition + 1 exceeds the cache capacity");
     if (p.kvHeads > 65535) return ctx.fail("decode: kvHeads too large");
 
-    // chunk length: the longest of 2048/1024/512/256 positions that still gives
-    // every resident workgroup (2 per CU) two items; AIGPU_DECODE_CHUNK overrides
-    static const uint32_t chunkEnv = env_u32("AIGPU_DECODE_CHUNK", 0);
-    static const uint32_t gridEnv = env_u32("AIGPU_DECODE_GRID", 512);
+    // chunk length: the longest of 2048/1024/512/256 positions that still
+    // gives every resident workgroup (2 per CU, GRID in all) two items; below
+    // that, 128 positions (one slab per wave) when 256 would leave CUs idle
     auto chunk_for = [&](uint64_t bs) {
+        auto items = [&](uint32_t len) { return bs * p.kvHeads * ((uint64_t(p.maxPosition) + len) / len); };
         uint32_t len = 2048;
-        if (chunkEnv) return chunkEnv < 4 * SLAB ? uint32_t(4 * SLAB) : chunkEnv / (4 * SLAB) * (4 * SLAB);
-        while (len > 256 && bs * p.kvHeads * ((uint64_t(p.maxPosition) + len) / len) < 2ull * gridEnv) len /= 2;
+        while (len > 256 && items(len) < 2ull * GRID) len /= 2;
+        if (items(len) < GRID / 2 && items(4 * SLAB) > items(len)) len = 4 * SLAB;
         return len;
     };
     const size_t rs = size_t(record_floats(int(p.dim)));
@@ -653,7 +649,7 @@ bool launch_decode(const DecodeParams& p, hipStream_t stream, const FixedScratch
         a.maxChunks = maxChunks;
         a.scaleLog2 = LOG2E / sqrtf(float(p.dim));
         const uint64_t upper = a.p.batch * p.kvHeads * maxChunks;
-        const unsigned grid = unsigned(upper < gridEnv ? upper : gridEnv);
+        const unsigned grid = unsigned(upper < GRID ? upper : GRID);
         const unsigned mgrid = unsigned(a.p.batch * p.heads);   // one merge workgroup per query head
         const bool ok = p.dim == 128
             ? ctx.launch("decode_attention_kernel", stream, [&] {

@@ -110,10 +110,10 @@ __device__ __forceinline__ void norm_rope_row(float* x, int dim, const float* ga
 
 /* fp16 of a finite fp32 value, noting in `bad` when it does not fit fp16's
    range (|x| >= 65520 rounds to infinity); infinite or NaN inputs stay what
-   they are and are not noted */
+   they are and are not noted (a NaN converts to a NaN, never to an infinity) */
 __device__ __forceinline__ _Float16 to_f16_checked(float x, bool& bad) {
     const _Float16 h = _Float16(x);
-    bad |= __builtin_isinf(float(h)) && !__builtin_isinf(x) && !__builtin_isnan(x);
+    bad |= __builtin_isinf(float(h)) && !__builtin_isinf(x);
     return h;
 }
 

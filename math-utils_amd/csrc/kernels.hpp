@@ -39,7 +39,7 @@ struct PrefillParams {
     int kvReady;
     uint64_t count, start, heads, kvHeads, dim, qStride, window, capacity;
     // set to 1 by any conversion into the fp16 working copies that overflows
-    // fp16's range (device address; null: not tracked)
+    // fp16's range (device address of the call's flag word; null: not tracked)
     uint32_t* rangeFlag;
     // when set, out is not written: each output row goes as bf16 high parts
     // here ([count][heads·dim]) and as bf16 residuals x - hi right after them
@@ -171,6 +171,7 @@ struct MixerParams {
     float eps, normOffset;
     int rotaryDims, outputGate, accumulate;
     uint64_t count, start, hidden, heads, kvHeads, dim, qStride, window, capacity;
+    uint32_t* rangeFlag;  // as PrefillParams::rangeFlag
 };
 bool launch_prefill_mixer(const MixerParams& p, hipStream_t stream);
 
@@ -257,5 +258,8 @@ struct GdnGatedNormParams {
     uint64_t count, valueHeads, valueDim;
 };
 bool launch_gdn_gated_norm(const GdnGatedNormParams& p, hipStream_t stream);
+
+// ---- a plain streaming device copy (the bench's achievable-bandwidth line) ----
+bool launch_copy(void* dst, const void* src, uint64_t bytes, hipStream_t stream);
 
 } // namespace aigpu

@@ -666,7 +666,10 @@ __global__ __launch_bounds__(256) void gemv_scalar_kernel(GemvParams p) {
 /* bf16 weights with at least 256 tiles of 256 x 256 (a and w under 4 GB,
    k a multiple of 32) take split_a_kernel and gemm_dma_kernel */
 bool dma_eligible(const GemvParams& p) {
-    if (p.type != 1 || p.k % GD_BK || (reinterpret_cast<uintptr_t>(p.w) % 16) || (reinterpret_cast<uintptr_t>(p.a) % 16))
+    // at least half a 256-row tile of a: fewer rows (a decode step's GEMV
+    // against a wide weight such as an LM head) would waste most of every tile
+    if (p.type != 1 || p.m < GD_BM / 2 || p.k % GD_BK || (reinterpret_cast<uintptr_t>(p.w) % 16) ||
+        (reinterpret_cast<uintptr_t>(p.a) % 16))
         return false;
     const uint64_t wide = uint64_t((p.m + GD_BM - 1) / GD_BM) * ((p.n + GD_BN - 1) / GD_BN);
     return wide >= 256 && wide <= 0x7FFFFFFFull && uint64_t(p.m) * p.k * 2 < (1ull << 32) &&

@@ -77,7 +77,7 @@ bool launch_prefill_mixer(const MixerParams& p, hipStream_t stream) {
     pp.qStride = p.qStride;
     pp.window = p.window;
     pp.capacity = p.capacity;
-    pp.rangeFlag = ctx.rangeDev;
+    pp.rangeFlag = p.rangeFlag;
     void* kh = nullptr;
     void* vh = nullptr;
     if (!prefill_work_buffers(pp, &kh, &vh)) return false;
@@ -96,7 +96,7 @@ bool launch_prefill_mixer(const MixerParams& p, hipStream_t stream) {
     ek.start = uint32_t(p.start);
     ek.T = uint32_t(T);
     ek.capacity = p.capacity;
-    ek.rangeFlag = ctx.rangeDev;
+    ek.rangeFlag = p.rangeFlag;
     KvEpilogue ev = ek;
     ev.cache = p.valueCache;
     ev.work = vh;

@@ -39,12 +39,12 @@
 // the next V tile; K is double- and V triple-buffered, 160 KB of LDS). The
 // running max is folded into the score accumulators' initial value and
 // rescaling is lazy (only when the max grows by more than 8 in log2 units).
-// AIGPU_PREFILL_PP=0 selects the single-phase loop.
+// D = 64 takes the single-phase loop: every wave computes S, the softmax and
+// P.V of each tile in turn, one barrier per tile.
 #include "context.hpp"
 #include "device.hpp"
 #include "kernels.hpp"
 
-#include <cstdlib>
 #include <type_traits>
 
 namespace aigpu {
@@ -470,12 +470,14 @@ __device__ __forceinline__ void load_query(const FlashArgs& a, uint32_t tq, bool
 
 /*
     Flash attention, one workgroup = WAVES waves of 32 query rows of one
-    head; key tiles of 64 keys staged in LDS by DMA (global_load_lds, 1 KB
-    per wave instruction) in STAGES stages, STAGES - 1 tiles ahead of the one
-    being computed. One barrier per tile: past it, tile `it` has landed for
-    every wave and every wave has finished tile it - 1, whose stage is then
-    refilled. Per tile a wave runs S^T = K Q^T (16 MFMAs for D = 128), the
-    online softmax, and O^T += V^T P^T (16 MFMAs).
+    head; key tiles of BN = 128 keys staged in LDS by DMA (global_load_lds,
+    1 KB per wave instruction). Built in two forms: the ping-pong schedule
+    (PP, D = 128; described at its loop) and the single-phase loop (D = 64):
+    STAGES = 2 stages, one tile ahead of the one being computed, and one
+    barrier per tile: past it, tile `it` has landed for every wave and every
+    wave has finished tile it - 1, whose stage is then refilled. Per tile a
+    wave runs S^T = K Q^T, the online softmax, and O^T += V^T P^T, 32 keys
+    at a time.
 
     Every wave computes every tile of the workgroup's key range; keys past a
     row's position (or outside its window) are masked, so such tiles add
@@ -489,7 +491,7 @@ __device__ __forceinline__ void load_query(const FlashArgs& a, uint32_t tq, bool
     so the 4 rows x 64 bytes a 32-lane transposed read touches hit distinct
     banks.
 */
-template <int D, int WAVES, int STAGES, int BN = 64, bool PP = false>
+template <int D, int WAVES, int STAGES, int BN, bool PP>
 __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_kernel(FlashArgs a) {
     static_assert(!PP || (WAVES == 8 && STAGES == 2 && BN == 128), "ping-pong: 8 waves, 2 stages, 128-key tiles");
     constexpr int BM = 32 * WAVES;
@@ -701,70 +703,6 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         }
     };
 
-    // online softmax of one tile: P^T (fp16) into pk, running max and sum,
-    // and O moved to the new running max
-    auto softmax = [&](floatx16 (&s)[NKB], half8 (&pk)[NKB][2]) __attribute__((always_inline)) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-        {   // lanes l and l ^ 32 hold the two key halves of one query
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-            mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        }
-        // lazy rescale: the running max only moves when a tile exceeds it by
-        // more than 2^8, so P = exp2(s - m) <= 256 stays exact enough in fp16
-        // and most tiles skip rescaling O
-        const bool grow = mx > m + 8.0f;
-        const float mn = grow ? mx : m;
-        const float alpha = grow ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
-        const float base = mn == -INFINITY ? 0.0f : mn;
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) pk[kb][h][j] = _Float16(__builtin_amdgcn_exp2f(s[kb][8 * h + j] - base));
-        // the row sum adds the fp16 P that the P.V product uses, in fp32
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        float ps[NKB];
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) ps[kb] = 0.0f;
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int j = 0; j < 8; j += 2)
-                    ps[kb] = __builtin_amdgcn_fdot2(h2{pk[kb][h][j], pk[kb][h][j + 1]}, h2{1, 1}, ps[kb], false);
-        float psum = ps[0];
-#pragma unroll
-        for (int kb = 1; kb < NKB; ++kb) psum += ps[kb];
-        lsum = lsum * alpha + psum;
-        m = mn;
-        if (__any(grow)) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-        }
-    };
-
-    // O^T += V^T P^T for the tile in stage J
-    auto pv = [&](auto J, const half8 (&pk)[NKB][2]) __attribute__((always_inline)) {
-        const _Float16* vs = vbuf(J);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const _Float16* a0 = vs + vaddr[dt] + (32 * kb + 8 * h) * D;
-                    const half8 va = read_tr16x2(a0, a0 + 4 * D);
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pk[kb][h], o[dt], 0, 0, 0);
-                }
-    };
     // 128-key tiles: the softmax and P.V go 32 keys at a time, so only one
     // block's P is live next to the scores (the register budget of two waves
     // per SIMD does not hold all four at once)
@@ -789,21 +727,21 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
         }
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
         const _Float16* vs = vbuf(J);
         float psum = 0.0f;
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
             half8 pk[2];
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < 2; ++h) {
+                float e[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) pk[h][j] = _Float16(__builtin_amdgcn_exp2f(s[kb][8 * h + j] - base));
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int j = 0; j < 8; j += 2)
-                    psum = __builtin_amdgcn_fdot2(h2{pk[h][j], pk[h][j + 1]}, h2{1, 1}, psum, false);
+                for (int j = 0; j < 8; ++j) {
+                    e[j] = __builtin_amdgcn_exp2f(s[kb][8 * h + j] - base);
+                    pk[h][j] = _Float16(e[j]);
+                }
+                psum += ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+            }
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -1009,21 +947,22 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
 #pragma unroll
                     for (int r = 0; r < 16; ++r) s[kb][r] -= shift;
             }
-            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-            // eight partial row sums, one per 16-key half block
+            // eight partial row sums, one per 16-key half block, added in fp32
+            // from the exponentials before their fp16 rounding: plain adds
+            // issue beside the partner wave's MFMAs, where v_dot2c over the
+            // fp16 P stalls the matrix core
             float ps[NKB][2];
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) pk[kb][h][j] = _Float16(__builtin_amdgcn_exp2f(s[kb][8 * h + j]));
-#pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    ps[kb][h] = 0.0f;
+                    float e[8];
 #pragma unroll
-                    for (int j = 0; j < 8; j += 2)
-                        ps[kb][h] = __builtin_amdgcn_fdot2(h2{pk[kb][h][j], pk[kb][h][j + 1]}, h2{1, 1}, ps[kb][h], false);
+                    for (int j = 0; j < 8; ++j) {
+                        e[j] = __builtin_amdgcn_exp2f(s[kb][8 * h + j]);
+                        pk[kb][h][j] = _Float16(e[j]);
+                    }
+                    ps[kb][h] = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
                 }
                 hook(kb, s, pk[kb][1]);
             }
@@ -1144,13 +1083,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         const uint32_t k0 = kbeg + it * BN;
         if (k0 > wPosLast || (a.window && uint64_t(k0) + BN - 1 + a.window <= uint64_t(wPosFirst))) return true;
         scores(k0, J, s);
-        if constexpr (NKB > 2) {
-            softmax_pv(J, s);
-        } else {
-            half8 pk[NKB][2];
-            softmax(s, pk);
-            pv(J, pk);
-        }
+        softmax_pv(J, s);
         return true;
     };
     for (uint32_t it = 0;; it += STAGES) {
@@ -1342,46 +1275,18 @@ bool launch_prefill(const PrefillParams& p, hipStream_t stream) {
     a.half = p.freqs ? uint32_t(p.rotaryDims / 2) : 0u;
     a.outputGate = p.outputGate ? 1u : 0u;
     a.rangeFlag = p.rangeFlag;
-    // AIGPU_PREFILL_WAVES / AIGPU_PREFILL_STAGES pick the tiling (tuning);
-    // 4-wave workgroups run two per CU and take two stages
-    static const int waves = [] {
-        const char* env = std::getenv("AIGPU_PREFILL_WAVES");
-        return env && std::atoi(env) == 4 ? 4 : 8;
-    }();
-    // 8-wave workgroups take 128-key tiles in two stages (half the barriers
-    // and DMA rounds of 64-key tiles, 4% faster at configs[2]);
-    // AIGPU_PREFILL_BN=64 selects 64-key tiles in AIGPU_PREFILL_STAGES stages
-    static const int bn = [] {
-        const char* env = std::getenv("AIGPU_PREFILL_BN");
-        return waves == 8 && !(env && std::atoi(env) == 64) ? 128 : 64;
-    }();
-    static const int stages = [] {
-        const char* env = std::getenv("AIGPU_PREFILL_STAGES");
-        const int n = env ? std::atoi(env) : 3;
-        return waves == 4 ? 2 : (n >= 2 && n <= 4 ? n : 3);
-    }();
-    // AIGPU_PREFILL_PP=0 selects the single-phase loop for 128-key tiles
-    static const bool pingPong = [] {
-        const char* env = std::getenv("AIGPU_PREFILL_PP");
-        return !(env && std::atoi(env) == 0);
-    }();
+    // 8 waves of 32 query rows per workgroup, 128-key tiles: the ping-pong
+    // schedule for D = 128, the single-phase loop (two stages) for D = 64
+    constexpr int waves = 8;
     a.nQT = uint32_t((p.count + 32 * waves - 1) / (32 * waves));
     const uint64_t blocks = uint64_t(a.nQT) * p.heads;
     a.xcdRemap = (blocks % 8 == 0) ? 1u : 0u;
     return ctx.launch("prefill_flash_kernel", stream, [&] {
         const dim3 grid{unsigned(blocks)}, block{unsigned(64 * waves)};
-#define AIGPU_FLASH(DD, WV, ST) \
-    if (p.dim == DD && waves == WV && stages == ST && bn == 64) \
-        hipLaunchKernelGGL((prefill_flash_kernel<DD, WV, ST>), grid, block, 0, stream, a)
-        AIGPU_FLASH(128, 8, 2); AIGPU_FLASH(128, 8, 3); AIGPU_FLASH(128, 8, 4); AIGPU_FLASH(128, 4, 2);
-        AIGPU_FLASH(64, 8, 2); AIGPU_FLASH(64, 8, 3); AIGPU_FLASH(64, 8, 4); AIGPU_FLASH(64, 4, 2);
-#undef AIGPU_FLASH
-        if (bn == 128 && p.dim == 128 && waves == 8 && pingPong)
-            hipLaunchKernelGGL((prefill_flash_kernel<128, 8, 2, 128, true>), grid, block, 0, stream, a);
-        if (bn == 128 && p.dim == 128 && waves == 8 && !pingPong)
-            hipLaunchKernelGGL((prefill_flash_kernel<128, 8, 2, 128>), grid, block, 0, stream, a);
-        if (bn == 128 && p.dim == 64 && waves == 8)
-            hipLaunchKernelGGL((prefill_flash_kernel<64, 8, 2, 128>), grid, block, 0, stream, a);
+        if (p.dim == 128)
+            hipLaunchKernelGGL((prefill_flash_kernel<128, waves, 2, 128, true>), grid, block, 0, stream, a);
+        else
+            hipLaunchKernelGGL((prefill_flash_kernel<64, waves, 2, 128, false>), grid, block, 0, stream, a);
     });
 }
 

@@ -37,6 +37,12 @@ AIGPU_ABI int aigpu_attention(const float*, const float*, const float*, float*, 
 AIGPU_ABI int aigpu_attention_device(const AiGpuAttention*) { return 0; }
 AIGPU_ABI int aigpu_prefill_attention(const AiGpuPrefill*) { return 0; }
 AIGPU_ABI int aigpu_prefill_attention_host(const AiGpuPrefill*) { return 0; }
+AIGPU_ABI int aigpu_copy_device(void*, const void*, uint64_t, void*) { return 0; }
+AIGPU_ABI uint64_t aigpu_range_ticket(void) { return 0; }
+AIGPU_ABI int aigpu_range_status(uint64_t* ticket) {
+    if (ticket) *ticket = 0;
+    return 0;
+}
 AIGPU_ABI int aigpu_decode_attention(const AiGpuDecode*) { return 0; }
 AIGPU_ABI int aigpu_decode_attention_host(const AiGpuDecode*) { return 0; }
 AIGPU_ABI int aigpu_decode_attention_static(const AiGpuDecode*) { return 0; }

@@ -121,6 +121,7 @@ def ref():
         R.ref_delta_step.argtypes = ([_f32p] * 5 + [C.c_int, C.c_float, C.c_uint64, C.c_uint64] +
                                      [_f32p] * 3)
         R.ref_dot.restype = C.c_float
+        R.ref_matmul_nt_bf16.argtypes = [_f32p, C.c_void_p, _f32p] + [C.c_uint64] * 3 + [C.c_int]
         R.ref_dot.argtypes = [_f32p, _f32p, C.c_uint64]
         R.ref_random.argtypes = [C.c_uint64, C.c_int, C.c_uint64, C.c_double, C.c_double, C.c_void_p]
         R.ref_gated_delta_rule.argtypes = [_f32p] * 7 + [C.c_uint64] * 5 + [C.c_int]

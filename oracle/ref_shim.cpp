@@ -56,6 +56,13 @@ void ref_delta_step(float* state, const float* key, const float* query, const fl
 
 float ref_dot(const float* a, const float* b, uint64_t n) { return ai::kernels::dot(a, b, n); }
 
+/* the reference's matmulNTBF16 (Kernels.hpp:243-257), the kernel its
+   bandwidth test times (gpu-testing.cpp:298-351) */
+void ref_matmul_nt_bf16(const float* a, const uint16_t* b, float* c, uint64_t m, uint64_t k, uint64_t n,
+                        int threaded) {
+    ai::kernels::matmulNTBF16(a, b, c, m, k, n, threaded != 0);
+}
+
 /* gatedDeltaNetMixer's per-token loop (LocalModel.hpp:2802-2830) around the
    reference's own deltaStep, single-threaded as the mixer runs it. The l2
    normalisation with eps inside the square root (LocalModel.hpp:1380-1386)

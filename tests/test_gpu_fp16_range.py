@@ -6,8 +6,10 @@ scale) and every cached key and value of the history is converted to fp16
 on its way in. The reference computes in fp32 and has no such limit
 (attentionMixer, LocalModel.hpp:2608-2659), so a finite value that fp16
 cannot hold (|x| >= 65520 rounds to infinity) must not turn into a silent
-inf / NaN output: the call returns 0 and names the cause, and the next call
-with ordinary inputs runs as before.
+inf / NaN output. The device-form calls are asynchronous: each takes a
+ticket, its kernels raise the ticket's flag, and aigpu_range_status
+(check_range here) names the earliest offending call. The host form waits
+for its kernels and fails itself.
 
 bf16 brackets the limit exactly: 65280 (0x477F) is the largest bf16 value
 below 65504 and converts exactly; 65536 (0x4780) is the next one up and
@@ -25,9 +27,9 @@ BELOW = 65280.0   # largest bf16 value fp16 holds
 ABOVE = 65536.0   # smallest bf16 value that overflows fp16
 
 
-def call(gpu, *, count=40, start=0, H=4, KV=2, D=128, dtype="bf16", q_big=None,
-         v_big=None, cache_big=None, norm=True):
-    """one prefill of ordinary N(0, 1) inputs with one planted element"""
+def inputs(*, count=40, start=0, H=4, KV=2, D=128, dtype="bf16", q_big=None, v_big=None, cache_big=None,
+           norm=True):
+    """ordinary N(0, 1) inputs with one planted element"""
     import torch
     torch_type = torch.bfloat16 if dtype == "bf16" else torch.float32
     g = torch.Generator(device="cpu").manual_seed(5)
@@ -51,9 +53,20 @@ def call(gpu, *, count=40, start=0, H=4, KV=2, D=128, dtype="bf16", q_big=None,
     out = torch.zeros((count, H, D), dtype=torch.float32, device="cuda")
     say("prefill fp16 range", dict(count=count, start=start, D=D, dtype=dtype, q_big=q_big, v_big=v_big,
                                    cache_big=cache_big, norm=norm))
-    gpu.prefill(q, k, v, out, kc, vc, start, H, KV, D, q_norm=gn, k_norm=gn)
-    torch.cuda.synchronize()
-    return out
+    return dict(q=q, k=k, v=v, kc=kc, vc=vc, gn=gn, out=out, start=start, H=H, KV=KV, D=D)
+
+
+def launch(gpu, x, check=True):
+    """one device-form prefill; returns its ticket"""
+    gpu.prefill(x["q"], x["k"], x["v"], x["out"], x["kc"], x["vc"], x["start"], x["H"], x["KV"], x["D"],
+                q_norm=x["gn"], k_norm=x["gn"], check=check)
+    return gpu.range_ticket()
+
+
+def call(gpu, **kw):
+    x = inputs(**kw)
+    launch(gpu, x)
+    return x["out"]
 
 
 def expect_range_error(gpu, **kw):
@@ -93,9 +106,54 @@ def test_an_ordinary_call_after_the_error_matches_the_oracle(gpu):
     assert_bf16_parity(ref, got, "after a range error")
 
 
+def test_asynchronous_calls_report_the_offending_ticket(gpu):
+    """the device form returns without waiting; a later status query names the
+    ticket of the call that overflowed, not of the ordinary calls around it,
+    and leaves every flag clear"""
+    gpu.check_range()   # start clear
+    good = inputs(count=33)
+    bad = inputs(count=40, v_big=ABOVE)
+    before = launch(gpu, good, check=False)
+    offending = launch(gpu, bad, check=False)
+    after = launch(gpu, good, check=False)
+    assert before + 1 == offending and offending + 1 == after
+    with pytest.raises(gpu.AiGpuError, match="fp16") as err:
+        gpu.check_range()
+    assert err.value.ticket == offending
+    assert f"ticket {offending}" in str(err.value)
+    gpu.check_range()   # the flags are clear again
+
+
+def test_host_form_fails_its_own_call(gpu):
+    """aigpu_prefill_attention_host waits for its kernels and fails itself;
+    the next host call with ordinary inputs runs and matches the device form"""
+    x = inputs(count=40, v_big=ABOVE, dtype="f32")
+    args = (x["kc"], x["vc"], 0, x["H"], x["KV"], x["D"])
+    gn = x["gn"].cpu().numpy()
+    with pytest.raises(gpu.AiGpuError, match="fp16"):
+        gpu.prefill_host(x["q"].cpu().numpy(), x["k"].cpu().numpy(), x["v"].cpu().numpy(), *args,
+                         q_norm=gn, k_norm=gn)
+    gpu.check_range()   # the host form cleared its own flag
+    y = inputs(count=40, dtype="f32")
+    got = gpu.prefill_host(y["q"].cpu().numpy(), y["k"].cpu().numpy(), y["v"].cpu().numpy(), y["kc"], y["vc"], 0,
+                           y["H"], y["KV"], y["D"], q_norm=gn, k_norm=gn)
+    launch(gpu, y)
+    np.testing.assert_array_equal(got, y["out"].cpu().numpy())
+
+
 def test_mixer_value_projection_beyond_fp16_fails(gpu):
     """hidden states scaled by 1e5 project to values of ~N(0, 1e10) (weights
     ~ N(0, 1/hidden)): the v GEMM's epilogue converts them into the fp16 copy"""
     with pytest.raises(RuntimeError, match="fp16"):
         run_mixer(gpu, x_scale=1e5)
     run_mixer(gpu)   # and the next call is unaffected
+
+
+def test_fused_kv_projection_beyond_fp16_fails(gpu):
+    """at a shape where k and v run as one DMA GEMM followed by
+    kv_epilogue_kernel (8192 rows, 2 KV D = 2048 columns), the epilogue's
+    conversion raises the flag; an ordinary call afterwards matches the oracle"""
+    kw = dict(count=8192, start=40, hidden=64, H=16, KV=8, D=128, window=64)
+    with pytest.raises(RuntimeError, match="fp16"):
+        run_mixer(gpu, "bf16", x_scale=1e5, **kw)
+    run_mixer(gpu, "bf16", **kw)

@@ -184,3 +184,24 @@ def test_gemm_wide_tiles(gpu, k, accumulate):
     err = np.abs(got[:, :n] - want)
     assert np.all(err <= bound(a, dense) + 1e-6), f"max err {err.max()}"
     np.testing.assert_array_equal(got[:, n:], base[:, n:])
+
+
+def test_one_row_against_a_wide_weight_takes_the_gemv(gpu):
+    """a decode step's product against a wide weight (an LM head: one row of a,
+    65536 weight rows, 256 tiles of 256 x 256) runs on gemv_kernel: the DMA
+    GEMM's 256-row tiles would waste 255 of every 256 rows"""
+    import torch
+    m, k, n = 1, 256, 65536
+    a = O.fill_normal((m, k), 65, "a")
+    w, _, dense = weights(n, k, "bf16", 66)
+    out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    say("gemv wide", dict(m=m, k=k, n=n))
+    gpu.profile_reset()
+    gpu.profile(True)
+    gpu.matmul(dev_f32(a), to_device(w), out, "bf16")
+    torch.cuda.synchronize()
+    gpu.profile(False)
+    assert gpu.profile_read("gemv_kernel")[1] == 1
+    assert gpu.profile_read("gemm_dma_kernel")[1] == 0
+    err = np.abs(host(out) - O.matmul_nt(a, w, "bf16"))
+    assert np.all(err <= bound(a, dense)), f"max err {err.max()}"

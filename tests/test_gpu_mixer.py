@@ -82,7 +82,7 @@ def run(gpu, kind="bf16", count=70, start=25, hidden=256, H=8, KV=2, D=128, gate
     gpu.prefill_mixer(dev_f32(x), dev, out, key_cache, value_cache, start, H, KV, D,
                       q_norm=None if gq is None else dev_f32(gq), k_norm=None if gk is None else dev_f32(gk),
                       freqs=None if fr is None else dev_f32(fr), rotary_dims=rot, window=window,
-                      output_gate=gate, accumulate=accumulate)
+                      output_gate=gate, accumulate=accumulate, check=True)
     got = host(out)
     assert_bf16_parity(want, got, f"mixer {kind}")
     gk_all, gv_all = host(key_cache), host(value_cache)

@@ -57,7 +57,7 @@ def run_case(gpu, count, start, H, KV, D, seed, norm=True, rope=True, window=0, 
                 q_norm=None if gq is None else dev_f32(gq),
                 k_norm=None if gk is None else dev_f32(gk),
                 freqs=None if fr is None else dev_f32(fr), rotary_dims=rot, window=window,
-                output_gate=gate)
+                output_gate=gate, check=True)
     got = host(out)
     if rows is not None:
         got = got[rows]
