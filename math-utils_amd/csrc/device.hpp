@@ -143,6 +143,15 @@ __device__ __forceinline__ void dma_block(const void* base, uint32_t off, uint32
 }
 #pragma clang diagnostic pop
 
+/* The flash kernel's table of each new token's RoPE cos and sin (rot / 2
+   each, rot % 32 == 0): element i of token t's cos (which = 0) or sin
+   (which = 1) at ((which * rot / 8 + i / 4) * count + t) * 4 + i % 4. The
+   16-byte groups of consecutive tokens are adjacent, so a load in which
+   each lane reads one token's group touches the fewest cache lines. */
+__device__ __forceinline__ size_t rope_at(uint32_t t, uint32_t which, uint32_t i, uint32_t half, uint32_t count) {
+    return ((size_t(which) * (half / 4) + i / 4) * count + t) * 4 + i % 4;
+}
+
 /* LDS byte address of a __shared__ object */
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
     return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));

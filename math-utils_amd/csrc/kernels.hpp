@@ -57,8 +57,8 @@ constexpr uint32_t PREFILL_PAD_ROWS = 128;
 bool prefill_work_buffers(const PrefillParams& p, void** kh, void** vh);
 // whether launch_prefill's prep, for these kvReady parameters, would only
 // write the cos/sin table of the flash kernel's q rotation and zero the pad
-// rows; *rope is then that table ([count][rotaryDims]: cos, then sin, per
-// token), grown, or null without RoPE
+// rows; *rope is then that table (count * rotaryDims floats in the layout of
+// rope_at in device.hpp), grown, or null without RoPE
 bool prefill_prep_foldable(const PrefillParams& p, float** rope);
 
 // ---- decode: norm + RoPE on load, append, split-K attention, merge --------

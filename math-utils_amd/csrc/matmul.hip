@@ -540,7 +540,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemvParams p, const __bf1
    once into LDS, then the four waves take its 2 * heads rows (k and v of
    each kv head) in turn, a row staged in LDS for the RoPE partner. A lane
    holds D / 64 consecutive elements. With rope set, the angles' cos and sin
-   also go to the flash kernel's table (rope[t][0 .. rot/2) cos, then sin);
+   also go to the flash kernel's table (rope_at);
    with padK / padV set, workgroup 0 zeroes pad16 16-byte pieces of each
    (the working copies' pad rows). */
 __global__ __launch_bounds__(256) void kv_epilogue_kernel(const float* kv, const float* kBias, const float* vBias,
@@ -557,8 +557,8 @@ __global__ __launch_bounds__(256) void kv_epilogue_kernel(const float* kv, const
         sinT[lane] = sn;
         cosT[lane] = cs;
         if (rope) {
-            rope[size_t(t) * 2 * half + lane] = cs;
-            rope[size_t(t) * 2 * half + half + lane] = sn;
+            rope[rope_at(t, 0, uint32_t(lane), half, gridDim.x)] = cs;
+            rope[rope_at(t, 1, uint32_t(lane), half, gridDim.x)] = sn;
         }
     }
     if (padK && t == 0)

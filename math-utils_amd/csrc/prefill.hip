@@ -217,9 +217,9 @@ __global__ __launch_bounds__(PREP_THREADS) void prefill_prep_vec_kernel(PrefillP
     if (tid < half) {
         const float fpos = float(pos);   // the reference's fp32 angle (LocalModel.hpp:2632)
         sincosf(fpos * p.freqs[tid], &sn[tid], &cs[tid]);
-        if (rope) {   // the token's cos/sin row for the flash kernel's own q rotation
-            rope[size_t(t) * 2 * half + tid] = cs[tid];
-            rope[size_t(t) * 2 * half + half + tid] = sn[tid];
+        if (rope) {   // the token's cos/sin for the flash kernel's own q rotation
+            rope[rope_at(t, 0, tid, half, gridDim.x)] = cs[tid];
+            rope[rope_at(t, 1, tid, half, gridDim.x)] = sn[tid];
         }
     }
     __syncthreads();
@@ -332,7 +332,7 @@ struct FlashArgs {
     // of read from qh
     const void* qraw;    // [count][heads][qStride], inType
     const float* qNorm;  // [D] gamma or null
-    const float* rope;   // [count][2][half] cos, sin of each token, or null
+    const float* rope;   // cos, sin of each token (rope_at), or null
     float eps, normOffset, qScale;
     uint32_t qStride, inType, half, fuseQ;
     uint32_t outputGate;   // out *= sigmoid(qraw[row + D + d]) (LocalModel.hpp:2660-2665)
@@ -375,37 +375,89 @@ __device__ __forceinline__ void wait_vmcnt() {
    half's sum over one v_permlane32_swap) and rotated (RoPE pairs (e, e +
    half) within the lane, half % 16 == 0) here, as attentionMixer does
    (LocalModel.hpp:2608-2648); otherwise prep's scaled fp16 copy is read.
-   Rows past the call's count give zeros. The caller waits for the loads. */
-template <int D>
+   Rows past the call's count give zeros. `dma()` runs after the loads of
+   gamma and the cos/sin table are issued and before the q row is read: with
+   qlds set (bf16 rows, fused), it has brought the wave's 32 raw rows into
+   LDS at qlds (row r's 16-byte block c at c ^ (r % 16)) and waited for all
+   of the wave's loads, and the row is read from there. The caller waits for
+   the rest. */
+template <int D, typename Dma>
 __device__ __forceinline__ void load_query(const FlashArgs& a, uint32_t tq, bool rowValid, uint32_t head, int g,
-                                           half8 (&qreg)[D / 16]) {
+                                           half8 (&qreg)[D / 16], const _Float16* qlds, Dma&& dma) {
     constexpr int DB = D / 16;
     if (a.fuseQ) {
         // this lane's half of its query row: elements 16 db + 8g + j. QK-RMSNorm
         // over the row (the other half is in lane ^ 32), RoPE pairs (e, e + half)
         // within the lane (half % 16 == 0), then the log2(e)/sqrt(D) scale
         // (attentionMixer, LocalModel.hpp:2608-2648)
+        // Every load (gamma, the cos/sin of the rotated blocks, the q half
+        // row) is issued before any is used: one memory round trip. Written
+        // as loads inside the loops that use them, the compiler issued and
+        // waited for them one 16-byte block at a time.
         float x[DB][8];
         bool bad = false;   // an fp16 conversion out of range
         const size_t row = (size_t(rowValid ? tq : 0) * a.heads + head) * a.qStride;
+        floatx4 gam[DB][2];
+        if (a.qNorm) {
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            if (a.inType == 0) {
-                const floatx4* src = reinterpret_cast<const floatx4*>(static_cast<const float*>(a.qraw) + row + 16 * db + 8 * g);
-                const floatx4 lo = src[0], hi = src[1];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    x[db][j] = lo[j];
-                    x[db][4 + j] = hi[j];
-                }
-            } else {
-                const u32x4 wv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qraw) + row + 16 * db + 8 * g);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    x[db][2 * j] = __uint_as_float(wv[j] << 16);
-                    x[db][2 * j + 1] = __uint_as_float(wv[j] & 0xFFFF0000u);
-                }
+            for (int db = 0; db < DB; ++db) {
+                const floatx4* gm = reinterpret_cast<const floatx4*>(a.qNorm + 16 * db + 8 * g);
+                gam[db][0] = gm[0];
+                gam[db][1] = gm[1];
             }
+        }
+        // rotate-half pairs (e, e + half) sit in one lane when half % 16 == 0:
+        // blocks db < hb rotate with block db + hb
+        const int hb = int(a.half) / 16;
+        floatx4 cs[DB / 2][4];   // cos lo, cos hi, sin lo, sin hi
+        if (a.rope) {
+            const uint32_t t = rowValid ? tq : 0;
+#pragma unroll
+            for (int db = 0; db < DB / 2; ++db) {
+                // blocks past hb are not rotated: their loads read block 0 again
+                const uint32_t at = db < hb ? uint32_t(16 * db + 8 * g) : 0u;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)   // cos lo, cos hi, sin lo, sin hi
+                    cs[db][k] = *reinterpret_cast<const floatx4*>(
+                        a.rope + rope_at(t, uint32_t(k >> 1), at + 4 * uint32_t(k & 1), a.half, a.count));
+            }
+        }
+        dma();
+        if (a.inType == 0) {
+            floatx4 raw[DB][2];
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const floatx4* src = reinterpret_cast<const floatx4*>(static_cast<const float*>(a.qraw) + row + 16 * db + 8 * g);
+                raw[db][0] = src[0];
+                raw[db][1] = src[1];
+            }
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[db][j] = raw[db][0][j];
+                    x[db][4 + j] = raw[db][1][j];
+                }
+        } else {
+            u32x4 raw[DB];
+            if (qlds) {   // LDS-typed reads: a generic pointer would make these flat loads
+                typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
+                const int c = int(threadIdx.x & 31);
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+                    raw[db] = *(lds_u32x4*)(qlds + c * D + 8 * ((2 * db + g) ^ (c & 15)));
+            } else {
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+                    raw[db] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qraw) + row + 16 * db + 8 * g);
+            }
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[db][2 * j] = __uint_as_float(raw[db][j] << 16);
+                    x[db][2 * j + 1] = __uint_as_float(raw[db][j] & 0xFFFF0000u);
+                }
         }
         if (a.qNorm) {   // rmsNormRow (LocalModel.hpp:1341-1348)
             float ss = 0.0f;
@@ -417,28 +469,21 @@ __device__ __forceinline__ void load_query(const FlashArgs& a, uint32_t tq, bool
             ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
             const float inv = 1.0f / sqrtf(ss / float(D) + a.eps);
 #pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                const floatx4* gm = reinterpret_cast<const floatx4*>(a.qNorm + 16 * db + 8 * g);
-                const floatx4 g0 = gm[0], g1 = gm[1];
+            for (int db = 0; db < DB; ++db)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    x[db][j] = x[db][j] * inv * (g0[j] + a.normOffset);
-                    x[db][4 + j] = x[db][4 + j] * inv * (g1[j] + a.normOffset);
+                    x[db][j] = x[db][j] * inv * (gam[db][0][j] + a.normOffset);
+                    x[db][4 + j] = x[db][4 + j] * inv * (gam[db][1][j] + a.normOffset);
                 }
-            }
         }
         if (a.rope) {   // rotate-half pairs (LocalModel.hpp:2636-2641)
-            const float* cs = a.rope + size_t(rowValid ? tq : 0) * 2 * a.half;
-            const int hb = int(a.half) / 16;   // partner block offset
 #pragma unroll
             for (int db = 0; db < DB / 2; ++db) {
                 if (db < hb) {
-                    const floatx4* cp = reinterpret_cast<const floatx4*>(cs + 16 * db + 8 * g);
-                    const floatx4* sp = reinterpret_cast<const floatx4*>(cs + a.half + 16 * db + 8 * g);
-                    const floatx4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        const float cj = j < 4 ? c0[j] : c1[j - 4], sj = j < 4 ? s0[j] : s1[j - 4];
+                        const float cj = j < 4 ? cs[db][0][j] : cs[db][1][j - 4];
+                        const float sj = j < 4 ? cs[db][2][j] : cs[db][3][j - 4];
                         const float lo = x[db][j];
                         float hi = 0.0f;
 #pragma unroll
@@ -459,6 +504,7 @@ __device__ __forceinline__ void load_query(const FlashArgs& a, uint32_t tq, bool
             for (int j = 0; j < 8; ++j) qreg[db][j] = rowValid ? to_f16_checked(x[db][j] * a.qScale, bad) : _Float16(0.0f);
         raise_range_flag(a.rangeFlag, bad);
     } else {
+        dma();
         const _Float16* qrow = a.qh + (size_t(head) * a.count + (rowValid ? tq : 0)) * D;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
@@ -556,12 +602,14 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     const uint32_t firstKey = (a.window && P + 1 > a.window) ? P + 1 - a.window : 0u;
 
     half8 qreg[DB];
-    load_query<D>(a, tq, rowValid, head, g, qreg);
-    // Q lands before any DMA is issued, so the vmcnt waits in the loop only
-    // ever count DMA
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    wait_vmcnt<0>();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if constexpr (!PP) {   // the ping-pong form loads Q with its first DMA
+        load_query<D>(a, tq, rowValid, head, g, qreg, nullptr, [] {});
+        // Q lands before any DMA is issued, so the vmcnt waits in the loop only
+        // ever count DMA
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        wait_vmcnt<0>();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
 
     floatx16 o[DT];
 #pragma unroll
@@ -848,6 +896,24 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
         };
+        // the causal (and window) mask of a tile's scores, arithmetic: the sign
+        // of (hi - c) | (c - lo) shifted into a -inf bit pattern and added
+        auto mask_scores = [&](uint32_t k0, floatx16 (&s)[NKB]) __attribute__((always_inline)) {
+            const bool needMask = (k0 + BN - 1 > wPosFirst) ||
+                                  (a.window && uint64_t(k0) + a.window < uint64_t(wPosLast) + 1);
+            if (needMask) {
+                const int base = int(k0 + 16 * g);
+                const int hi = int(P) - base;
+                const int lo = a.window ? int(firstKey) - base : -(1 << 30);
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int out = (hi - (32 * kb + r)) | ((32 * kb + r) - lo);
+                        s[kb][r] += __int_as_float((out >> 31) & int(0xFF800000u));
+                    }
+            }
+        };
         auto scores_pp = [&](uint32_t k0, auto J, floatx16 (&s)[NKB]) __attribute__((always_inline)) {
             const _Float16* ks = kbuf(J);
             constexpr int N = NKB * DB;   // products: db outer, kb inner
@@ -870,20 +936,52 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                 if (i + AHEAD_PP < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
-            const bool needMask = (k0 + BN - 1 > wPosFirst) ||
-                                  (a.window && uint64_t(k0) + a.window < uint64_t(wPosLast) + 1);
-            if (needMask) {
-                const int base = int(k0 + 16 * g);
-                const int hi = int(P) - base;
-                const int lo = a.window ? int(firstKey) - base : -(1 << 30);
+            mask_scores(k0, s);
+        };
+        // P.V of the previous tile and S of this one as one pipeline: the
+        // first K fragments are read during the last P.V products, so the
+        // matrix core does not wait for LDS between the two products
+        auto pv_scores_pp = [&](const _Float16* vs, const half8 (&pk)[NKB][2], uint32_t k0, auto J,
+                                floatx16 (&s)[NKB], float nb) __attribute__((always_inline)) {
+            const _Float16* ks = kbuf(J);
+            constexpr int NP = NKB * 2 * DT, N = NP + NKB * DB;
+            auto frag = [&](int i) __attribute__((always_inline)) {
+                if (i < NP) {
+                    const int dt = i % DT, hh = (i / DT) % 2, kb = i / (2 * DT);
+                    const _Float16* a0 = vs + vaddr[dt] + (32 * kb + 8 * hh) * D;
+                    return read_tr16x2(a0, a0 + 4 * D);
+                }
+                const int kb = (i - NP) % NKB, db = (i - NP) / NKB;
+                return *reinterpret_cast<const half8*>(ks + kaddr[db] + 32 * kb * D);
+            };
+            half8 f[AHEAD_PP + 1];
 #pragma unroll
-                for (int kb = 0; kb < NKB; ++kb)
+            for (int i = 0; i < AHEAD_PP; ++i) f[i] = frag(i);
+            // S starts at -base; the moves issue beside the first P.V products
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int out = (hi - (32 * kb + r)) | ((32 * kb + r) - lo);
-                        s[kb][r] += __int_as_float((out >> 31) & int(0xFF800000u));
-                    }
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s[kb][r] = nb;
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                if (i + AHEAD_PP < N) f[(i + AHEAD_PP) % (AHEAD_PP + 1)] = frag(i + AHEAD_PP);
+                if (i < NP) {
+                    const int dt = i % DT, hh = (i / DT) % 2, kb = i / (2 * DT);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i % (AHEAD_PP + 1)], pk[kb][hh], o[dt], 0, 0, 0);
+                } else {
+                    const int kb = (i - NP) % NKB, db = (i - NP) / NKB;
+                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i % (AHEAD_PP + 1)], qreg[db], s[kb], 0, 0, 0);
+                }
             }
+            // DS reads per fragment: two transposed halves for P.V, one for S
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * AHEAD_PP, 0);
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                if (i + AHEAD_PP < NP) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                else if (i + AHEAD_PP < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+            mask_scores(k0, s);
         };
         floatx16 s[NKB];
         half8 pk[NKB][2];
@@ -896,8 +994,14 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         auto mphase = [&](uint32_t j, auto KS, const _Float16* vs) __attribute__((always_inline)) {
             __builtin_amdgcn_s_setprio(3);
             haveS = active(j);
-            if (haveS) {   // S starts at -base (the registers are free: P holds the last tile)
-                const float nb = m == -INFINITY ? 0.0f : -m;
+            // S starts at -base (the registers are free: P holds the last tile)
+            const float nb = m == -INFINITY ? 0.0f : -m;
+            if (haveP && haveS) {
+                pv_scores_pp(vs, pk, kbeg + j * BN, KS, s, nb);
+                haveP = false;
+                return;
+            }
+            if (haveS) {
 #pragma unroll
                 for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
@@ -906,8 +1010,9 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
             if (haveP) {
                 pv_pp(vs, pk);
                 haveP = false;
+            } else if (haveS) {
+                scores_pp(kbeg + j * BN, KS, s);
             }
-            if (haveS) scores_pp(kbeg + j * BN, KS, s);
         };
         // The softmax of the ping-pong loop. The S accumulators start at
         // -base (the running max, or 0 before the row's first key), so the
@@ -1014,9 +1119,38 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         auto vstage = [&](uint32_t j) __attribute__((always_inline)) -> const _Float16* {
             return VP + (j % 3) * TILE;
         };
-        // prologue: K tile 0 by group 1, V tile 0 by group 0
+        // prologue: K tile 0 (group 1) or V tile 0 (group 0), the loads of
+        // gamma and the cos/sin table, then the wave's 32 raw bf16 q rows by
+        // DMA (1 KB, 4 rows, per instruction; a per-lane load of its own row
+        // touches 32 cache lines per instruction) into V stages 1 and 2, which
+        // the loop first fills in interval B_0: all in flight at once. The
+        // wave then waits for all of it and reads its q rows back from LDS.
+        // Without the q DMA, the compiler's waits for the q loads count only
+        // its own loads, which is safe: the older DMA completes first. All of
+        // it lands before the loop, whose waits then count only its DMA.
+        const bool qDma = a.fuseQ && a.inType == 1 && uint64_t(a.heads) * a.qStride < (1ull << 26);   // 32-bit offsets
+        const uint32_t wu = __builtin_amdgcn_readfirstlane(uint32_t(w));
+        const _Float16* qlds = VP + TILE + wu * 32 * D;
         if (grp == 1) dma_rows(kbeg, ldsK0, true, integral_constant<int, 0>{}, integral_constant<int, PB>{});
         else dma_rows(kbeg, ldsV, false, integral_constant<int, 0>{}, integral_constant<int, PB>{});
+        auto q_dma = [&]() __attribute__((always_inline)) {
+            if (qDma) {
+                // rows past the call's count repeat its last row (their q is zeroed)
+                const uint32_t first = q0 + 32 * wu < a.count ? q0 + 32 * wu : a.count - 1;
+                const char* src = static_cast<const char*>(a.qraw) + (size_t(first) * a.heads + head) * a.qStride * 2;
+                const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_address(qlds));
+#pragma unroll
+                for (int n = 0; n < 8; ++n) {
+                    const uint32_t r = uint32_t(4 * n + (lane >> 4));
+                    const uint32_t tr = (q0 + 32 * wu + r < a.count ? q0 + 32 * wu + r : a.count - 1) - first;
+                    const uint32_t off = uint32_t((size_t(tr) * a.heads * a.qStride + 8 * ((lane & 15) ^ (r & 15))) * 2);
+                    dma_block(src, off, lds + n * 1024);
+                }
+                wait_vmcnt<0>();
+            }
+        };
+        load_query<D>(a, tq, rowValid, head, g, qreg, qDma ? qlds : nullptr, q_dma);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         wait_vmcnt<0>();
         lds_barrier();
         // group 0 waits at the end of each softmax phase for the V tile it
@@ -1097,7 +1231,42 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     }
 
     lsum += __shfl_xor(lsum, 32, WAVE);
-    if (rowValid) {
+    bool direct = true;
+    if constexpr (PP) {
+        if (!a.outHi && !a.outputGate) {
+            // The output rows leave through LDS. A lane's 16-byte pieces all
+            // belong to its own row, so a store of them touches 32 cache lines
+            // per instruction. Written to the wave's 16 KB of LDS (piece p of
+            // row r at p ^ (r % 16): conflict-free both ways) and read back
+            // two rows per instruction, each store covers 2 rows of 512 B.
+            // The loop's last barrier has passed, so no wave reads K or V any
+            // more.
+            direct = false;
+            static_assert(D == 128, "32 pieces of 16 bytes per row");
+            typedef __attribute__((address_space(3))) floatx4 lds_floatx4;
+            const int wv = int(__builtin_amdgcn_readfirstlane(uint32_t(w)));
+            float* ob = reinterpret_cast<float*>(wv < 6 ? VP + wv * 8192 : K0 + (wv - 6) * 8192);
+            const float inv = rowValid ? 1.0f / lsum : 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    floatx4 val;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) val[i] = o[dt][4 * r4 + i] * inv;
+                    const int p = 8 * dt + 2 * r4 + g;
+                    *(lds_floatx4*)(ob + c * D + 4 * (p ^ (c & 15))) = val;
+                }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int r = 2 * i + (lane >> 5), p = lane & 31;
+                const floatx4 val = *(lds_floatx4*)(ob + r * D + 4 * (p ^ (r & 15)));
+                const uint32_t row = wq0 + uint32_t(r);
+                if (row < a.count) *reinterpret_cast<floatx4*>(a.out + (size_t(row) * a.heads + head) * D + 4 * p) = val;
+            }
+        }
+    }
+    if (direct && rowValid) {
         const float inv = 1.0f / lsum;
         float* dst = a.out + (size_t(tq) * a.heads + head) * D;
         const size_t gateRow = (size_t(tq) * a.heads + head) * a.qStride + D;
