@@ -498,10 +498,30 @@ __device__ __forceinline__ void load_query(const FlashArgs& a, uint32_t tq, bool
                 }
             }
         }
+        // Scale and round to fp16. |y| >= 65520 rounds to infinity, and the
+        // rounding is monotone, so the lane's largest magnitude decides: one
+        // test in the common case (fmaxf passes over NaN; an infinite input
+        // takes the element-wise check, which does not count it)
+        float big = 0.0f;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) qreg[db][j] = rowValid ? to_f16_checked(x[db][j] * a.qScale, bad) : _Float16(0.0f);
+            for (int j = 0; j < 8; ++j) big = fmaxf(big, fabsf(x[db][j]));
+        if (big * a.qScale < 65520.0f) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) qreg[db][j] = _Float16(x[db][j] * a.qScale);
+        } else {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) qreg[db][j] = to_f16_checked(x[db][j] * a.qScale, bad);
+        }
+        if (!rowValid) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db) qreg[db] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
         raise_range_flag(a.rangeFlag, bad);
     } else {
         dma();
@@ -590,6 +610,10 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
     const uint32_t head = kvh * G + rest % G;
     const uint32_t qt = a.nQT - 1 - rest / G;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, c = lane & 31;
+    // the wave index in a scalar register, for code after the main loop: it
+    // rebuilds its lane quantities from the lane counter, so that nothing
+    // computed before the loop has to stay live (or spilled) across it
+    const uint32_t wsc = __builtin_amdgcn_readfirstlane(uint32_t(tid >> 6));
 
     const uint32_t q0 = qt * BM;
     const uint32_t wq0 = q0 + 32 * w;
@@ -1129,7 +1153,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         // its own loads, which is safe: the older DMA completes first. All of
         // it lands before the loop, whose waits then count only its DMA.
         const bool qDma = a.fuseQ && a.inType == 1 && uint64_t(a.heads) * a.qStride < (1ull << 26);   // 32-bit offsets
-        const uint32_t wu = __builtin_amdgcn_readfirstlane(uint32_t(w));
+        const uint32_t wu = wsc;
         const _Float16* qlds = VP + TILE + wu * 32 * D;
         if (grp == 1) dma_rows(kbeg, ldsK0, true, integral_constant<int, 0>{}, integral_constant<int, PB>{});
         else dma_rows(kbeg, ldsV, false, integral_constant<int, 0>{}, integral_constant<int, PB>{});
@@ -1244,9 +1268,11 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
             direct = false;
             static_assert(D == 128, "32 pieces of 16 bytes per row");
             typedef __attribute__((address_space(3))) floatx4 lds_floatx4;
-            const int wv = int(__builtin_amdgcn_readfirstlane(uint32_t(w)));
+            const int le = int(__lane_id()), ce = le & 31, ge = le >> 5;
+            const uint32_t wqe = q0 + 32 * wsc;
+            const int wv = int(wsc);
             float* ob = reinterpret_cast<float*>(wv < 6 ? VP + wv * 8192 : K0 + (wv - 6) * 8192);
-            const float inv = rowValid ? 1.0f / lsum : 0.0f;
+            const float inv = wqe + uint32_t(ce) < a.count ? 1.0f / lsum : 0.0f;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -1254,14 +1280,14 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                     floatx4 val;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) val[i] = o[dt][4 * r4 + i] * inv;
-                    const int p = 8 * dt + 2 * r4 + g;
-                    *(lds_floatx4*)(ob + c * D + 4 * (p ^ (c & 15))) = val;
+                    const int p = 8 * dt + 2 * r4 + ge;
+                    *(lds_floatx4*)(ob + ce * D + 4 * (p ^ (ce & 15))) = val;
                 }
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const int r = 2 * i + (lane >> 5), p = lane & 31;
+                const int r = 2 * i + ge, p = le & 31;
                 const floatx4 val = *(lds_floatx4*)(ob + r * D + 4 * (p ^ (r & 15)));
-                const uint32_t row = wq0 + uint32_t(r);
+                const uint32_t row = wqe + uint32_t(r);
                 if (row < a.count) *reinterpret_cast<floatx4*>(a.out + (size_t(row) * a.heads + head) * D + 4 * p) = val;
             }
         }
