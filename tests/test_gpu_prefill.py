@@ -134,6 +134,19 @@ def test_cfg3_qwen3_8b_prefill_8k_sampled_rows(gpu):
     say("cfg3 errors", e)
 
 
+@pytest.mark.parametrize("count,start,H,KV,window", [(4000, 300, 64, 8, 0), (4000, 300, 64, 8, 700),
+                                                      (3600, 0, 40, 8, 0)])
+def test_large_grids_sampled_rows(gpu, count, start, H, KV, window):
+    """Grids of 600 to 1,024 workgroups (several per compute unit): a ragged
+    last tile, history, a window that moves the first key tile of every
+    query tile, and 5 query heads per kv head. Sampled rows cover every
+    query tile's first and last rows and the call's last rows."""
+    rows = sorted(set(list(range(0, count, 256)) + list(range(255, count, 256)) +
+                      list(range(37, count, 211)) + list(range(count - 40, count))))
+    ref, got, *_ = run_case(gpu, count, start, H, KV, 128, 60 + H + window, window=window, rows=rows)
+    assert_bf16_parity(ref, got, f"count {count} H {H} window {window}")
+
+
 def test_rejects_unsupported_dim(gpu):
     import torch
     x = torch.zeros((2, 2, 96), dtype=torch.bfloat16, device="cuda")
