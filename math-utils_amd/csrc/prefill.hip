@@ -1288,7 +1288,8 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                 const int r = 2 * i + ge, p = le & 31;
                 const floatx4 val = *(lds_floatx4*)(ob + r * D + 4 * (p ^ (r & 15)));
                 const uint32_t row = wqe + uint32_t(r);
-                if (row < a.count) *reinterpret_cast<floatx4*>(a.out + (size_t(row) * a.heads + head) * D + 4 * p) = val;
+                if (row < a.count)   // written once: nontemporal, so as not to displace K and V in L2
+                    __builtin_nontemporal_store(val, reinterpret_cast<floatx4*>(a.out + (size_t(row) * a.heads + head) * D + 4 * p));
             }
         }
     }
