@@ -383,7 +383,8 @@ __device__ __forceinline__ void wait_vmcnt() {
    the rest. */
 template <int D, typename Dma>
 __device__ __forceinline__ void load_query(const FlashArgs& a, uint32_t tq, bool rowValid, uint32_t head, int g,
-                                           half8 (&qreg)[D / 16], const _Float16* qlds, Dma&& dma) {
+                                           half8 (&qreg)[D / 16], const _Float16* qlds, Dma&& dma,
+                                           float* glds = nullptr) {
     constexpr int DB = D / 16;
     if (a.fuseQ) {
         // this lane's half of its query row: elements 16 db + 8g + j. QK-RMSNorm
@@ -397,13 +398,22 @@ __device__ __forceinline__ void load_query(const FlashArgs& a, uint32_t tq, bool
         float x[DB][8];
         bool bad = false;   // an fp16 conversion out of range
         const size_t row = (size_t(rowValid ? tq : 0) * a.heads + head) * a.qStride;
+        // gamma: with glds (D = 128), one 8-byte load per lane, staged
+        // through the wave's 512 B of LDS and read back by broadcast where it
+        // is used, instead of 16 loads of 1 KB per wave held in 64 registers
+        typedef float floatx2 __attribute__((ext_vector_type(2)));
         floatx4 gam[DB][2];
+        floatx2 gpair{0.0f, 0.0f};
         if (a.qNorm) {
+            if (glds) {
+                gpair = reinterpret_cast<const floatx2*>(a.qNorm)[threadIdx.x & 63];
+            } else {
 #pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                const floatx4* gm = reinterpret_cast<const floatx4*>(a.qNorm + 16 * db + 8 * g);
-                gam[db][0] = gm[0];
-                gam[db][1] = gm[1];
+                for (int db = 0; db < DB; ++db) {
+                    const floatx4* gm = reinterpret_cast<const floatx4*>(a.qNorm + 16 * db + 8 * g);
+                    gam[db][0] = gm[0];
+                    gam[db][1] = gm[1];
+                }
             }
         }
         // rotate-half pairs (e, e + half) sit in one lane when half % 16 == 0:
@@ -468,6 +478,17 @@ __device__ __forceinline__ void load_query(const FlashArgs& a, uint32_t tq, bool
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
             ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
             const float inv = 1.0f / sqrtf(ss / float(D) + a.eps);
+            if (glds) {
+                static_assert(D == 128 || D == 64, "gamma staging: 64 lanes x 2 floats");
+                typedef __attribute__((address_space(3))) floatx2 lds_float2;
+                typedef __attribute__((address_space(3))) const floatx4 lds_floatx4c;
+                *(lds_float2*)(glds + 2 * (threadIdx.x & 63)) = gpair;
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    gam[db][0] = *(lds_floatx4c*)(glds + 16 * db + 8 * g);
+                    gam[db][1] = *(lds_floatx4c*)(glds + 16 * db + 8 * g + 4);
+                }
+            }
 #pragma unroll
             for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -1173,7 +1194,9 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                 wait_vmcnt<0>();
             }
         };
-        load_query<D>(a, tq, rowValid, head, g, qreg, qDma ? qlds : nullptr, q_dma);
+        // gamma staging: the wave's 512 B of K stage 1, first filled in A_0
+        float* glds = D == 128 ? reinterpret_cast<float*>(K1 + wu * 256) : nullptr;
+        load_query<D>(a, tq, rowValid, head, g, qreg, qDma ? qlds : nullptr, q_dma, glds);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         wait_vmcnt<0>();
         lds_barrier();
