@@ -213,6 +213,22 @@ __global__ __launch_bounds__(PREP_THREADS) void prefill_prep_vec_kernel(PrefillP
     const uint32_t t = blockIdx.x, pos = uint32_t(p.start) + t;
     const uint32_t H = uint32_t(p.heads), KVH = uint32_t(p.kvHeads), rows = p.kvReady ? H : H + 2 * KVH;
     const int half = p.freqs ? p.rotaryDims / 2 : 0;
+    const int e0 = 8 * sub;
+    // a pass's rows: issued before the angles' sin/cos and the barrier for
+    // the first pass, so that their latency overlaps that work
+    auto load_pass = [&](uint32_t r0, float (&x)[UNROLL][8]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const uint32_t r = r0 + u * RPP;
+            if (r >= rows) continue;
+            if (r < H) load8<F32>(p.q, (size_t(t) * H + r) * p.qStride + e0, x[u]);
+            else if (r < H + KVH) load8<F32>(p.k, (size_t(t) * KVH + (r - H)) * D + e0, x[u]);
+            else load8<F32>(p.v, (size_t(t) * KVH + (r - H - KVH)) * D + e0, x[u]);
+        }
+    };
+    const uint32_t rFirst = firstRow + tid / LPR;
+    float x[UNROLL][8];
+    load_pass(rFirst, x);
     if (blockIdx.x == 0) zero_pad_rows(kh, vh, uint64_t(KVH) * T * D, uint32_t(D));
     if (tid < half) {
         const float fpos = float(pos);   // the reference's fp32 angle (LocalModel.hpp:2632)
@@ -224,7 +240,7 @@ __global__ __launch_bounds__(PREP_THREADS) void prefill_prep_vec_kernel(PrefillP
     }
     __syncthreads();
     // rotate-half partner lane and the sign of its term, per element slot
-    const int e0 = 8 * sub, shiftL = half / 8;
+    const int shiftL = half / 8;
     const bool lowHalf = e0 < half, highHalf = !lowHalf && e0 < 2 * half;
     const int partner = lowHalf ? lane + shiftL : (highHalf ? lane - shiftL : lane);
     float c8[8], s8[8];
@@ -238,16 +254,8 @@ __global__ __launch_bounds__(PREP_THREADS) void prefill_prep_vec_kernel(PrefillP
     }
 
     bool bad = false;   // an fp16 conversion out of range
-    for (uint32_t r0 = firstRow + tid / LPR; r0 < rows; r0 += UNROLL * RPP) {
-        float x[UNROLL][8];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            const uint32_t r = r0 + u * RPP;
-            if (r >= rows) continue;
-            if (r < H) load8<F32>(p.q, (size_t(t) * H + r) * p.qStride + e0, x[u]);
-            else if (r < H + KVH) load8<F32>(p.k, (size_t(t) * KVH + (r - H)) * D + e0, x[u]);
-            else load8<F32>(p.v, (size_t(t) * KVH + (r - H - KVH)) * D + e0, x[u]);
-        }
+    for (uint32_t r0 = rFirst; r0 < rows; r0 += UNROLL * RPP) {
+        if (r0 != rFirst) load_pass(r0, x);
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             const uint32_t r = r0 + u * RPP;
