@@ -138,16 +138,23 @@ __device__ __forceinline__ void chunk_gates(const DeltaRuleParams& p, uint64_t t
     head's record.
 */
 template <int KD, bool F32, bool SPLIT>
-__global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs a) {
+__global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs a) {
     static_assert(!(F32 && SPLIT), "the split form serves bf16 inputs");
     constexpr int PE = KD / 4;              // elements of a row per thread
     constexpr int EPL = F32 ? 4 : 8;        // elements per 16-byte load
     constexpr int KH = F32 ? KD + 1 : KD + 8;   // LDS row stride in elements
     using Raw = std::conditional_t<F32, float, __bf16>;
-    __shared__ __attribute__((aligned(16))) Raw ks[CH * KH];   // raw k rows
-    __shared__ __attribute__((aligned(16))) Raw qs[CH * KH];   // raw q rows
-    __shared__ float Am[CH * CS];
-    __shared__ float Tm[CH * CS];
+    // The raw q/k rows are dead once K K^T and Q K^T are in registers, and
+    // the masks and T are written only after that: they share one LDS pool,
+    // so that four workgroups fit a CU (bf16 inputs) instead of two
+    constexpr int KQB = (CH * KH * int(sizeof(Raw)) + 15) / 16 * 16;   // bytes of ks (and qs)
+    constexpr int AMB = (CH * CS * 4 + 15) / 16 * 16;                  // bytes of Am (and Tm)
+    constexpr int POOL = 2 * KQB > 2 * AMB ? 2 * KQB : 2 * AMB;
+    __shared__ __attribute__((aligned(16))) unsigned char pool[POOL];
+    Raw* ks = reinterpret_cast<Raw*>(pool);          // raw k rows
+    Raw* qs = reinterpret_cast<Raw*>(pool + KQB);    // raw q rows
+    float* Am = reinterpret_cast<float*>(pool);
+    float* Tm = reinterpret_cast<float*>(pool + AMB);
     __shared__ float Xs[4][16 * 17];
     __shared__ float nrm[2 * CH];           // kinv, qinv
     __shared__ float gsc[2 * CH];           // gc, beta of the current value head
@@ -207,11 +214,6 @@ __global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs
             nrm[CH + r] = qinv;
         }
     }
-    // T is zero above its diagonal blocks for every value head
-    for (int idx = tid; idx < CH * CH; idx += 256) {
-        const int i = idx / CH, j = idx % CH;
-        if ((j >> 4) > (i >> 4)) Tm[i * CS + j] = 0.0f;
-    }
     __syncthreads();
 
     // K K^T and Q K^T of the normalised rows: wave w owns rows 16w..16w+15
@@ -245,6 +247,12 @@ __global__ __launch_bounds__(256, F32 ? 1 : 2) void delta_solve_kernel(DeltaArgs
             kk[ct][r] = x[r] * (nrm[i] * nrm[j]);
             qk[ct][r] = y[r] * (nrm[CH + i] * nrm[j]);
         }
+    }
+    __syncthreads();   // the q/k rows are dead: Am and Tm take their LDS
+    // T is zero above its diagonal blocks for every value head
+    for (int idx = tid; idx < CH * CH; idx += 256) {
+        const int i = idx / CH, j = idx % CH;
+        if ((j >> 4) > (i >> 4)) Tm[i * CS + j] = 0.0f;
     }
 
     for (uint32_t m = 0; m < G; ++m) {
