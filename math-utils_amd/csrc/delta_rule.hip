@@ -105,6 +105,37 @@ __device__ __forceinline__ float raw_elem(const u32x4& r, int e) {
     return __uint_as_float((e & 1) ? (w & 0xFFFF0000u) : (w << 16));
 }
 
+/* fp32 -> bf16 high part and bf16 residual (round to nearest even): hi + lo
+   carries ~16 significant bits over fp32's whole exponent range */
+__device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
+    hi = __bf16(x);
+    lo = __bf16(x - float(hi));
+}
+/* the same for four values, two to a conversion instruction: the high
+   parts are widened back from the packed pair by a shift and a mask */
+__device__ __forceinline__ void split_bf16x4(const floatx4& x, bf16x4& hi, bf16x4& lo) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    u32x2 h, l;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        h[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{x[2 * i], x[2 * i + 1]}, b2));
+        const f2 r{x[2 * i] - __uint_as_float(h[i] << 16), x[2 * i + 1] - __uint_as_float(h[i] & 0xFFFF0000u)};
+        l[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, b2));
+    }
+    hi = __builtin_bit_cast(bf16x4, h);
+    lo = __builtin_bit_cast(bf16x4, l);
+}
+
+/* e^x for the solve's decays (x <= 0): the library expf where the record is
+   fp32, and the hardware 2^x (1 ulp) of x log2(e) where it is split into
+   bf16 parts (~16 significant bits), which cannot carry the difference */
+template <bool FAST>
+__device__ __forceinline__ float decay_exp(float x) {
+    if constexpr (FAST) return __builtin_amdgcn_exp2f(x * LOG2E);
+    else return expf(x);
+}
+
 /* the gates of tokens t0 .. t0+63 for value head h: lane = token; g is
    cumulated over the chunk (LocalModel.hpp:2820-2823 for the raw form) */
 __device__ __forceinline__ void chunk_gates(const DeltaRuleParams& p, uint64_t t0, uint32_t n, uint32_t h,
@@ -166,6 +197,7 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
     const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, c16 = lane & 15;
 
+    float gcEarly = 0.0f, btEarly = 0.0f;
     // rows: thread -> (row tid / 4, quarter tid % 4); l2 norms over the 4
     // threads of a row (LocalModel.hpp:2814-2818, l2normalise at :1380-1386)
     {
@@ -177,6 +209,9 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
             kr[i] = uint32_t(r) < n ? load_raw16<F32>(p.k, src + i * EPL, a.vec) : u32x4{0, 0, 0, 0};
             qr[i] = uint32_t(r) < n ? load_raw16<F32>(p.q, src + i * EPL, a.vec) : u32x4{0, 0, 0, 0};
         }
+        // the gates of value heads 0-3 of this key head, one wave each, while
+        // the rows are in flight (later heads load theirs in the loop)
+        if (uint32_t(w) < G) chunk_gates(p, t0, n, kh * G + w, lane, gcEarly, btEarly);
         float kss = 0.0f, qss = 0.0f;
 #pragma unroll
         for (int i = 0; i < PE / EPL; ++i)
@@ -258,9 +293,9 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
     for (uint32_t m = 0; m < G; ++m) {
         const uint32_t h = kh * G + m;
         float* rec = a.work + (size_t(h) * a.nChunks + chunk) * (SPLIT ? WORK_SPLIT : WORK);
-        if (w == 0) {
-            float gc, bt;
-            chunk_gates(p, t0, n, h, lane, gc, bt);
+        if (m < 4 ? uint32_t(w) == m : w == 0) {
+            float gc = gcEarly, bt = btEarly;
+            if (m >= 4) chunk_gates(p, t0, n, h, lane, gc, bt);
             gsc[lane] = gc;
             gsc[CH + lane] = bt;
         }
@@ -273,7 +308,7 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * w + 4 * g + r, j = 16 * ct + c16;
-                const float dec = j <= i ? expf(gsc[i] - gsc[j]) : 0.0f;
+                const float dec = j <= i ? decay_exp<SPLIT>(gsc[i] - gsc[j]) : 0.0f;
                 Am[i * CS + j] = j < i ? gsc[CH + i] * dec * kk[ct][r] : 0.0f;
                 if constexpr (SPLIT) qkv[ct][r] = dec * qk[ct][r];
                 else qkm[i * CH + j] = dec * qk[ct][r];
@@ -346,18 +381,13 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
                     const float* src = (m == 0 ? Tm : Am) + r * CS + 8 * b;
-                    u32x4 hi, lo;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float x0 = src[2 * e], x1 = src[2 * e + 1];
-                        const uint16_t h0 = float_to_bf16_bits(x0), h1 = float_to_bf16_bits(x1);
-                        const uint16_t l0 = float_to_bf16_bits(x0 - bf16_bits_to_float(h0));
-                        const uint16_t l1 = float_to_bf16_bits(x1 - bf16_bits_to_float(h1));
-                        hi[e] = uint32_t(h0) | (uint32_t(h1) << 16);
-                        lo[e] = uint32_t(l0) | (uint32_t(l1) << 16);
-                    }
-                    *reinterpret_cast<u32x4*>(out16 + (2 * m) * PMAT + dst) = hi;
-                    *reinterpret_cast<u32x4*>(out16 + (2 * m + 1) * PMAT + dst) = lo;
+                    bf16x4 h0, l0, h1, l1;
+                    split_bf16x4(floatx4{src[0], src[1], src[2], src[3]}, h0, l0);
+                    split_bf16x4(floatx4{src[4], src[5], src[6], src[7]}, h1, l1);
+                    *reinterpret_cast<bf16x8*>(out16 + (2 * m) * PMAT + dst) =
+                        __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+                    *reinterpret_cast<bf16x8*>(out16 + (2 * m + 1) * PMAT + dst) =
+                        __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
                 }
             }
             // per-row scalars of the scan: rows past the sequence's end have
@@ -368,10 +398,10 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
                 const int i = idx & (CH - 1), part = idx >> 6;
                 float x = 0.0f;
                 if (part == 0) x = gsc[CH + i];
-                else if (part == 1) x = expf(gsc[i]) * nrm[i];
-                else if (part == 2) x = expf(gsc[i]) * nrm[CH + i];
-                else if (part == 3) x = nrm[i] * expf(gLast - gsc[i]);
-                else if (part == 4) x = expf(gLast);
+                else if (part == 1) x = decay_exp<true>(gsc[i]) * nrm[i];
+                else if (part == 2) x = decay_exp<true>(gsc[i]) * nrm[CH + i];
+                else if (part == 3) x = nrm[i] * decay_exp<true>(gLast - gsc[i]);
+                else if (part == 4) x = decay_exp<true>(gLast);
                 sc[idx] = x;
             }
         }
@@ -576,12 +606,6 @@ __global__ __launch_bounds__(256) void delta_scan_f32_kernel(DeltaArgs a) {
 
 typedef __fp16 fp16x4v __attribute__((__vector_size__(4 * sizeof(__fp16))));
 
-/* fp32 -> bf16 high part and bf16 residual (round to nearest even): hi + lo
-   carries ~16 significant bits over fp32's whole exponent range */
-__device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
-    hi = __bf16(x);
-    lo = __bf16(x - float(hi));
-}
 
 /* ds_read_b64_tr_b16 pair: lane i of each 16-lane group receives column
    `base + i` of rows P0..P0+7 when lane L addresses row P0 + L/4 (and +4),
@@ -650,13 +674,7 @@ __global__ __launch_bounds__(256) void delta_scan_kernel(DeltaArgs a) {
     // C-layout tile (rows row0 + 4g + r, column c16) -> transposed split [col][row]
     auto put_t = [&](__bf16* dhi, __bf16* dlo, int stride, int row0, const floatx4& x) {
         bf16x4 hv, lv;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            __bf16 hi, lo;
-            split_bf16(x[r], hi, lo);
-            hv[r] = hi;
-            lv[r] = lo;
-        }
+        split_bf16x4(x, hv, lv);
         *reinterpret_cast<bf16x4*>(&dhi[c16 * stride + row0 + 4 * g]) = hv;
         *reinterpret_cast<bf16x4*>(&dlo[c16 * stride + row0 + 4 * g]) = lv;
     };
@@ -930,16 +948,18 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
     // partial chunk's end repeat its last row, whose beta is 0), the split
     // matrices and scalars of a record, the value rows
     const uint32_t rowBytes = uint32_t(p.keyHeads * KD * 2);
-    int kqRow[KI];
-    uint32_t kqCol[KI];
+    // (a row's byte offset, clamped by the uniform offset of the chunk's
+    // last row: one min and one add per DMA block)
+    uint32_t kqRowB[KI], kqCol[KI];
 #pragma unroll
     for (int j = 0; j < KI; ++j) {
-        kqRow[j] = RPI * (w * KI + j) + lane / KBLK;
-        kqCol[j] = kh * KD * 2 + 16 * ((lane % KBLK) ^ (kqRow[j] % KBLK));
+        const int row = RPI * (w * KI + j) + lane / KBLK;
+        kqRowB[j] = uint32_t(row) * rowBytes;
+        kqCol[j] = kh * KD * 2 + 16 * ((lane % KBLK) ^ (row % KBLK));
     }
     const uint32_t matOff = uint32_t(w * TI * 1024 + 16 * lane);
     const uint32_t vRowBytes = uint32_t(Hv * VD * 2);
-    const int vRow = 32 * w + lane / 2;
+    const uint32_t vRowB = uint32_t(32 * w + lane / 2) * vRowBytes + 16 * (lane & 1);
 
     // The next chunk's DMA is spread over the current chunk's phases, a block
     // or two between MFMAs: a wave that issues it all at once stalls on the
@@ -956,8 +976,7 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
                     static_cast<const uint8_t*>(p.v) + ((t0 * Hv + h) * VD + col0) * 2, chunk_rows(chunk), buf};
     };
     auto dma_rows_j = [&](const Next& nx, int j) __attribute__((always_inline)) {   // k and q block j
-        const uint32_t rr = uint32_t(kqRow[j]) < nx.n ? uint32_t(kqRow[j]) : nx.n - 1;
-        const uint32_t off = rr * rowBytes + kqCol[j];
+        const uint32_t off = min(kqRowB[j], (nx.n - 1) * rowBytes) + kqCol[j];
         dma_block(nx.k, off, ldsK + nx.buf * KBUF + (w * KI + j) * 1024);
         dma_block(nx.q, off, ldsQ + nx.buf * KBUF + (w * KI + j) * 1024);
     };
@@ -969,8 +988,7 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
     };
     auto dma_aux = [&](const Next& nx) __attribute__((always_inline)) {
         if (w < 2) {   // value block: 32 rows of 32 bytes per DMA block
-            const uint32_t rr = uint32_t(vRow) < nx.n ? uint32_t(vRow) : nx.n - 1;
-            dma_block(nx.v, rr * vRowBytes + 16 * (lane & 1), ldsA + nx.buf * ABUF + 1024 * w);
+            dma_block(nx.v, min(vRowB, (nx.n - 1) * vRowBytes + 16 * (lane & 1)), ldsA + nx.buf * ABUF + 1024 * w);
         } else {       // scalars
             dma_block(nx.rec + 4 * PMAT_BYTES, uint32_t(1024 * (w - 2) + 16 * lane),
                       ldsA + nx.buf * ABUF + 2048 + 1024 * (w - 2));
@@ -980,13 +998,7 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
     // C-layout tile (rows row0 + 4g + r, column c16) -> transposed split [col][row]
     auto put_t = [&](__bf16* dhi, __bf16* dlo, int stride, int row0, const floatx4& x) __attribute__((always_inline)) {
         bf16x4 hv, lv;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            __bf16 hi, lo;
-            split_bf16(x[r], hi, lo);
-            hv[r] = hi;
-            lv[r] = lo;
-        }
+        split_bf16x4(x, hv, lv);
         *reinterpret_cast<bf16x4*>(&dhi[c16 * stride + row0 + 4 * g]) = hv;
         *reinterpret_cast<bf16x4*>(&dlo[c16 * stride + row0 + 4 * g]) = lv;
     };
