@@ -989,7 +989,6 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                 if (i + AHEAD_PP < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
-            mask_scores(k0, s);
         };
         // P.V of the previous tile and S of this one as one pipeline: the
         // first K fragments are read during the last P.V products, so the
@@ -1034,11 +1033,11 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                 else if (i + AHEAD_PP < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
-            mask_scores(k0, s);
         };
         floatx16 s[NKB];
         half8 pk[NKB][2];
         bool haveP = false, haveS = false;
+        uint32_t sK0 = 0;   // the first key of the tile whose scores s holds
         // MFMA phase of tile j: P.V of tile j - 1 (V stage vs), S of tile j (K
         // stage KS). The wave runs it at a raised priority: the SIMD then
         // issues its LDS reads and MFMAs ahead of the partner wave's softmax
@@ -1047,6 +1046,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         auto mphase = [&](uint32_t j, auto KS, const _Float16* vs) __attribute__((always_inline)) {
             __builtin_amdgcn_s_setprio(3);
             haveS = active(j);
+            sK0 = kbeg + j * BN;
             // S starts at -base (the registers are free: P holds the last tile)
             const float nb = m == -INFINITY ? 0.0f : -m;
             if (haveP && haveS) {
@@ -1137,6 +1137,11 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         auto vphase = [&](auto hook) __attribute__((always_inline)) {
             __builtin_amdgcn_s_setprio(0);
             if (haveS) {
+                // the mask of a diagonal tile is applied here, beside the
+                // partner group's MFMAs, rather than after this wave's own
+                // products, where it waited for them and held up the
+                // interval (0.3% over the kernel)
+                mask_scores(sK0, s);
                 softmax_pp(s, pk, hook);
                 haveP = true;
                 haveS = false;
