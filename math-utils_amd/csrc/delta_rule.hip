@@ -177,7 +177,9 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
     using Raw = std::conditional_t<F32, float, __bf16>;
     // The raw q/k rows are dead once K K^T and Q K^T are in registers, and
     // the masks and T are written only after that: they share one LDS pool,
-    // so that four workgroups fit a CU (bf16 inputs) instead of two
+    // so that the LDS holds four workgroups per CU (bf16 inputs) instead of
+    // two; the registers then allow three (four, at 128 VGPRs, spilled and
+    // ran no faster)
     constexpr int KQB = (CH * KH * int(sizeof(Raw)) + 15) / 16 * 16;   // bytes of ks (and qs)
     constexpr int AMB = (CH * CS * 4 + 15) / 16 * 16;                  // bytes of Am (and Tm)
     constexpr int POOL = 2 * KQB > 2 * AMB ? 2 * KQB : 2 * AMB;
