@@ -967,7 +967,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                     }
             }
         };
-        auto scores_pp = [&](uint32_t k0, auto J, floatx16 (&s)[NKB]) __attribute__((always_inline)) {
+        auto scores_pp = [&](auto J, floatx16 (&s)[NKB]) __attribute__((always_inline)) {
             const _Float16* ks = kbuf(J);
             constexpr int N = NKB * DB;   // products: db outer, kb inner
             auto frag = [&](int i) __attribute__((always_inline)) {
@@ -993,9 +993,8 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         // P.V of the previous tile and S of this one as one pipeline: the
         // first K fragments are read during the last P.V products, so the
         // matrix core does not wait for LDS between the two products
-        auto pv_scores_pp = [&](const _Float16* vs, const half8 (&pk)[NKB][2], uint32_t k0, auto J,
-                                floatx16 (&s)[NKB], float nb, auto PRE,
-                                const half8& pre) __attribute__((always_inline)) {
+        auto pv_scores_pp = [&](const _Float16* vs, const half8 (&pk)[NKB][2], auto J, floatx16 (&s)[NKB],
+                                float nb, auto PRE, const half8& pre) __attribute__((always_inline)) {
             constexpr bool prefetched = decltype(PRE)::value;   // the first fragment is `pre`
             const _Float16* ks = kbuf(J);
             constexpr int NP = NKB * 2 * DT, N = NP + NKB * DB;
@@ -1040,11 +1039,6 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
         half8 pk[NKB][2];
         bool haveP = false, haveS = false;
         uint32_t sK0 = 0;   // the first key of the tile whose scores s holds
-        // MFMA phase of tile j: P.V of tile j - 1 (V stage vs), S of tile j (K
-        // stage KS). The wave runs it at a raised priority: the SIMD then
-        // issues its LDS reads and MFMAs ahead of the partner wave's softmax
-        // (without it the younger group's MFMA phase ran a third longer than
-        // the older group's, 3,380 against 2,770 cycles per interval)
         // Group 1 reads the first P.V fragment of its next MFMA phase at the
         // end of its softmax phase (that V tile is visible from the start of
         // the softmax phase), so the phase's first product does not wait for
@@ -1056,6 +1050,11 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
             const _Float16* a0 = vs + vaddr[0];   // fragment 0: dt 0, key block 0, first half
             preV = read_tr16x2(a0, a0 + 4 * D);
         };
+        // MFMA phase of tile j: P.V of tile j - 1 (V stage vs), S of tile j (K
+        // stage KS). The wave runs it at a raised priority: the SIMD then
+        // issues its LDS reads and MFMAs ahead of the partner wave's softmax
+        // (without it the younger group's MFMA phase ran a third longer than
+        // the older group's, 3,380 against 2,770 cycles per interval)
         auto mphase = [&](uint32_t j, auto KS, const _Float16* vs, auto PRE) __attribute__((always_inline)) {
             __builtin_amdgcn_s_setprio(3);
             haveS = active(j);
@@ -1063,7 +1062,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
             // S starts at -base (the registers are free: P holds the last tile)
             const float nb = m == -INFINITY ? 0.0f : -m;
             if (haveP && haveS) {
-                pv_scores_pp(vs, pk, kbeg + j * BN, KS, s, nb, PRE, preV);
+                pv_scores_pp(vs, pk, KS, s, nb, PRE, preV);
                 haveP = false;
                 return;
             }
@@ -1077,7 +1076,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void prefill_flash_
                 pv_pp(vs, pk);
                 haveP = false;
             } else if (haveS) {
-                scores_pp(kbeg + j * BN, KS, s);
+                scores_pp(KS, s);
             }
         };
         // The softmax of the ping-pong loop. The S accumulators start at
