@@ -11,8 +11,9 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 
-def gates(S, hv, seed):
-    g = -np.log1p(np.exp(O.fill_normal((S, hv), seed, "g").astype(np.float64))).astype(np.float32)
+def gates(S, hv, seed, decay_scale=1.0):
+    g = -np.log1p(np.exp(O.fill_normal((S, hv), seed, "g").astype(np.float64)))
+    g = (g * decay_scale).astype(np.float32)
     beta = (1.0 / (1.0 + np.exp(-O.fill_normal((S, hv), seed, "beta").astype(np.float64)))).astype(np.float32)
     return g, beta
 
@@ -25,7 +26,8 @@ def misaligned(t):
     return flat[1:].view(t.shape)
 
 
-def run_gdn(gpu, S, hk, hv, kd, vd, seed, dtype="f32", state0=None, raw_gates=False, unaligned=False):
+def run_gdn(gpu, S, hk, hv, kd, vd, seed, dtype="f32", state0=None, raw_gates=False, unaligned=False,
+            decay_scale=1.0):
     import torch
     if dtype == "bf16":
         qb, q = bf16_normal((S, hk, kd), seed, "q")
@@ -53,7 +55,7 @@ def run_gdn(gpu, S, hk, hv, kd, vd, seed, dtype="f32", state0=None, raw_gates=Fa
         gpu.gated_delta_rule(dq, dk, dv, state, out, a=dev_f32(a), b=dev_f32(b), a_log=dev_f32(alog),
                              dt_bias=dev_f32(dt))
     else:
-        g, beta = gates(S, hv, seed)
+        g, beta = gates(S, hv, seed, decay_scale)
         gpu.gated_delta_rule(dq, dk, dv, state, out, g=dev_f32(g), beta=dev_f32(beta))
     ref_out, ref_state = O.gated_delta_rule(q, k, v, g, beta, state=s0, nthreads=0)
     return ref_out, host(out), ref_state, host(state)
@@ -93,6 +95,26 @@ def test_raw_gates_and_initial_state(gpu):
     ro, go, rs, gs = run_gdn(gpu, 150, 2, 4, 128, 64, 7, state0=s0, raw_gates=True)
     assert_f32_parity(ro, go, "out raw gates")
     assert_f32_parity(rs, gs, "state raw gates")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_eight_value_heads_per_key_head(gpu, dtype):
+    """G = 8 value heads share each key head: the solve loads the first four
+    heads' gates beside the q/k rows and the rest inside its head loop"""
+    ro, go, rs, gs = run_gdn(gpu, 150, 2, 16, 128, 32, 21, dtype=dtype)
+    check = assert_f32_parity if dtype == "f32" else assert_bf16_parity
+    check(ro, go, f"out G=8 {dtype}")
+    check(rs, gs, f"state G=8 {dtype}")
+
+
+@pytest.mark.parametrize("scale", [0.02, 30.0])
+def test_bf16_weak_and_strong_decays(gpu, scale):
+    """log decays scaled to near 0 (the state barely forgets) and to ~-20 per
+    token (in-chunk decays underflow to 0): the split records' base-2
+    exponentials against the oracle's"""
+    ro, go, rs, gs = run_gdn(gpu, 200, 2, 4, 128, 64, 23, dtype="bf16", decay_scale=scale)
+    assert_bf16_parity(ro, go, f"out decay x{scale}")
+    assert_bf16_parity(rs, gs, f"state decay x{scale}")
 
 
 def test_key_dim_64(gpu):
