@@ -49,14 +49,13 @@ PEAK_HBM = 8000.0           # GB/s
 CPU_THREADS_CAP = 16        # the GPU box's CPU share for one GPU
 
 # HBM bytes per launch of prefill_flash_kernel<128, 8, 2, 128, true> on
-# rocprofv3 FETCH_SIZE and WRITE_SIZE passes, each scaled by what
-# the same counter reads for a 1 GiB device copy (fetch x2.000, write x1.000):
-# 182.1 MB read + 136.3 MB written (profiles/prefill_flash_kernel_cfg3_hbm_traffic.md).
-# Re-measure when the kernel changes.
+# rocprofv3 FETCH_SIZE and WRITE_SIZE passes (`--calibrate-copy
+# --workload prefill`), each scaled by what the same counter reads for a
+# 1 GiB device copy (fetch x2.000, write x1.000): 182.1 MB read + 136.3 MB
+# written. Re-measure when the kernel changes.
 PREFILL_FLASH_TRAFFIC = 318.4e6
 # HBM bytes per launch of decode_attention_kernel<128> on configs[3], measured
-# the same way: 1,240.4 MB read + 5.2 MB written
-# (profiles/decode_attention_kernel_cfg4_hbm_traffic.md)
+# the same way (`--workload decode`): 1,240.4 MB read + 5.2 MB written
 DECODE_ATTENTION_TRAFFIC = 1245.6e6
 
 
