@@ -30,8 +30,11 @@ HIP_FLAGS = [
 # per-source additions: the delta scan keeps its state accumulators in VGPRs
 # (the default AGPR form moved them through ~60 v_accvgpr instructions per
 # chunk; 1% faster without) and is scheduled by the iterative ILP strategy
-# (another 1%)
-SOURCE_FLAGS = {"delta_rule.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
+# (another 1%); the tiled fp32 attention keeps its scores and output
+# accumulators in VGPRs too (the AGPR form moved them through ~400 v_accvgpr
+# instructions per key tile for the softmax and the rescale)
+SOURCE_FLAGS = {"delta_rule.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+                "attention_f32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _run(cmd):

@@ -33,6 +33,7 @@ enum ScratchSlot {
     SLOT_GEMM_SPLIT,     // the K slices' partial tiles of a split GEMM
     SLOT_GEMM_A,         // a split into bf16 high parts and residuals for gemm_dma_kernel
     SLOT_MIXER_KV,       // fp32 k and v projections of a prefill mixer before their epilogue
+    SLOT_ATTN_PARTS,     // split records of the tiled fp32 attention
     SLOT_COUNT
 };
 

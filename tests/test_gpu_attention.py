@@ -110,3 +110,57 @@ def test_counters_track_transfers(gpu):
     assert c["launches"] >= 1 and c["hostToDeviceBytes"] >= q.nbytes + 2 * k.nbytes
     assert c["deviceToHostBytes"] == 4 * 2 * 32 * 4
     assert errors(np.zeros(1), np.zeros(1))["max_abs"] == 0
+
+
+# The tiled fp32 form (fp32 q and KV, dim 64 or 128, 16-byte aligned rows):
+# 128-token groups, 64-key tiles, key ranges split over workgroups whose
+# records a merge launch combines when the groups alone leave CUs idle.
+@pytest.mark.parametrize("count,start,H,KV,D,window,stride", [
+    (300, 0, 8, 2, 128, 0, 128),     # three token groups, split, causal imbalance
+    (200, 77, 4, 4, 64, 0, 64),      # history ending off a tile boundary, MHA
+    (260, 40, 8, 2, 64, 100, 72),    # a window inside the tile range, qStride > dim
+    (130, 500, 4, 1, 128, 33, 128),  # window 33, G = 4, a one-row second group
+    (1, 4999, 2, 1, 64, 0, 64),      # one token against 5000 keys: many splits
+    (33, 0, 2, 2, 128, 1, 128),      # window 1: every row sees only its own key
+    (64, 0, 3, 1, 128, 0, 132),      # one tile, no split
+])
+def test_tiled_fp32_shapes(gpu, count, start, H, KV, D, window, stride):
+    q = O.fill_normal((count, H, stride), 51, "q")
+    k = O.fill_normal((start + count, KV, D), 52, "k")
+    v = O.fill_normal((start + count, KV, D), 53, "v")
+    ref = O.attention(q, k, v, count, start, H, KV, D, stride, window)
+    say("tiled fp32", count, start, H, KV, D, window, stride)
+    got = gpu.attention(q, k, v, count, start, H, KV, D, stride, window)
+    assert_f32_parity(ref, got, f"tiled {count}/{start}/{D}/w{window}")
+
+
+def test_tiled_fp32_head_major_strides(gpu):
+    """the device form over an fp32 head-major cache (posStride = dim,
+    headStride = capacity * dim), split, and called twice on one buffer"""
+    cnt, start, H, KV, D, cap = 150, 90, 8, 2, 128, 256
+    q = O.fill_normal((cnt, H, D), 54, "q")
+    k = O.fill_normal((KV, cap, D), 55, "k")
+    v = O.fill_normal((KV, cap, D), 56, "v")
+    ref = O.attention_strided(q.reshape(-1), k, v, cnt, start, H, KV, D, D, D, cap * D)
+    import torch
+    out = torch.zeros((cnt, H, D), dtype=torch.float32, device="cuda")
+    dq, dk, dv = dev_f32(q), dev_f32(k), dev_f32(v)
+    for rep in range(2):
+        say("tiled fp32 head-major", rep)
+        gpu.attention_device(dq, dk, dv, out, cnt, start, H, KV, D, D, D, cap * D)
+        assert_f32_parity(ref.reshape(cnt, H, D), host(out), f"head-major {rep}")
+
+
+def test_tiled_fp32_unsplit_many_groups(gpu):
+    """2048 tokens x 32 heads: enough workgroups that no key range is split;
+    every head of 40 tokens (group edges, first, last) against the oracle"""
+    cnt, H, KV, D = 2048, 32, 8, 128
+    q = O.fill_normal((cnt, H, D), 57, "q")
+    k = O.fill_normal((cnt, KV, D), 58, "k")
+    v = O.fill_normal((cnt, KV, D), 59, "v")
+    rows = sorted({0, 1, 31, 32, 127, 128, 129, 255, 256, 1023, 1024, 2046, 2047} |
+                  set(range(3, 2048, 73)))
+    ref = O.attention_strided(q.reshape(-1), k, v, cnt, 0, H, KV, D, D, KV * D, D, rows=rows, nthreads=0)
+    say("tiled fp32 unsplit", cnt, H)
+    got = gpu.attention(q, k, v, cnt, 0, H, KV, D, D)
+    assert_f32_parity(ref, got[rows], "unsplit")
