@@ -48,6 +48,7 @@ Context::Context() {
         return;
     }
     name = props.name;
+    cus = props.multiProcessorCount;
     if (hipHostMalloc(reinterpret_cast<void**>(&rangeHost), RANGE_SLOTS * sizeof(uint32_t), hipHostMallocMapped) !=
             hipSuccess ||
         hipHostGetDevicePointer(reinterpret_cast<void**>(&rangeDev), rangeHost, 0) != hipSuccess) {

@@ -34,12 +34,14 @@ enum ScratchSlot {
     SLOT_GEMM_A,         // a split into bf16 high parts and residuals for gemm_dma_kernel
     SLOT_MIXER_KV,       // fp32 k and v projections of a prefill mixer before their epilogue
     SLOT_ATTN_PARTS,     // split records of the tiled fp32 attention
+    SLOT_DELTA_SEG,      // segment maps and start states of the two-level delta-rule scan
     SLOT_COUNT
 };
 
 struct Context {
     bool ok = false;
     std::string name;
+    int cus = 0;         // compute units of the device
     std::string error;
     std::recursive_mutex gate;
 

@@ -1181,6 +1181,399 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
             state[size_t(16 * (w + 4 * t) + 4 * g + r) * VD + col0 + c16] = sacc[t][r];
 }
 
+
+/*
+    The two-level scan for long sequences (keyDim = valueDim = 128, bf16
+    inputs on 16-byte boundaries). A chunk maps the state affinely,
+      S' = M_c S + N_c,  M_c = e^{gc_last} I - K_raw^T diag(kdk) T diag(beta gamma kinv) K_raw,
+    so a run of chunks maps it by S_end = A S_start + B, where B is the run
+    from a zero state and A the same run over the 128 columns of the identity
+    with zero values. Each value head's chunks are cut into P segments of L:
+      pass A  delta_seg_kernel<false>, per (head, segment < P - 1): B of the
+              segment and, from segment 1 on, its A (segment 0 starts from the
+              given state, so its B is segment 1's start);
+      join    delta_join_kernel, per (head, 16 columns): start(s + 1) =
+              A_s start(s) + B_s for s = 1 .. P - 2;
+      pass C  delta_seg_kernel<true>, per (head, segment): the segment's scan
+              from its start state with the outputs; the last segment writes
+              the final state.
+    The serial chain is 2 L chunk steps and P - 2 products instead of P L
+    chunk steps.
+
+    A workgroup takes all 128 value columns of its head (pass A: and the 128
+    identity columns), 16 per wave, so each wave owns whole columns of S and
+    no product needs another wave's results: the chunk's inputs arrive by DMA
+    into double buffers and one barrier per chunk hands them over. Every B
+    operand is built in registers from the wave's own accumulators, so the
+    contraction index of each product is ordered as they hold it: a 32-row
+    block of the contraction is two 16-row accumulator tiles, lane (column,
+    g) holding rows 4g .. 4g+3 of each, so B slot e < 4 is row 4g + e and slot
+    e >= 4 row 16 + 4g + e - 4; the A operand reads the same contraction
+    columns as two 8-byte pieces, and K^T comes from the row-major K buffer
+    through transposed reads of those rows.
+*/
+constexpr int SEG_D = 128;                   // key and value dim of the two-level scan
+constexpr int SEG_IMG = SEG_D * SEG_D;       // floats per state image
+
+struct SegArgs {
+    DeltaArgs d;
+    float* seg;          // per value head: 3 P state images
+    uint32_t P, L;       // segments, chunks per segment
+};
+
+/* image slots of a head: 0 the given state, 1 + s segment s's B (s <= P - 2),
+   P + s segment s's A (1 <= s <= P - 2, row-major), then the starts of
+   segments 2 .. P - 1 (segment 1 starts at B_0) */
+__host__ __device__ constexpr uint32_t slot_b(uint32_t s) { return 1 + s; }
+__host__ __device__ constexpr uint32_t slot_a(uint32_t P, uint32_t s) { return P + s; }
+__host__ __device__ constexpr uint32_t slot_start(uint32_t P, uint32_t s) { return s == 0 ? 0 : s == 1 ? 1 : 2 * P - 1 + s; }
+constexpr uint32_t SEG_SLOTS_PER_P = 3;
+
+/* fp32 accumulator tiles x (slots 0-3) and y (slots 4-7) as one B operand:
+   bf16 high parts and residuals */
+__device__ __forceinline__ void split_pair(const floatx4& x, const floatx4& y, bf16x8& hi, bf16x8& lo) {
+    bf16x4 hx, lx, hy, ly;
+    split_bf16x4(x, hx, lx);
+    split_bf16x4(y, hy, ly);
+    const u32x2 a = __builtin_bit_cast(u32x2, hx), b = __builtin_bit_cast(u32x2, hy);
+    const u32x2 c = __builtin_bit_cast(u32x2, lx), d = __builtin_bit_cast(u32x2, ly);
+    hi = __builtin_bit_cast(bf16x8, u32x4{a[0], a[1], b[0], b[1]});
+    lo = __builtin_bit_cast(bf16x8, u32x4{c[0], c[1], d[0], d[1]});
+}
+
+/* A operand from a swizzled [64][128] row buffer (16-byte block b of row r
+   at b ^ (r % 16)): row r, columns cc .. cc+3 and cc+16 .. cc+19 */
+__device__ __forceinline__ bf16x8 seg_rows(const __bf16* X, int r, int cc) {
+    const int s = r & 15, b = cc >> 3, o = cc & 7;
+    const u32x2 x = *reinterpret_cast<const u32x2*>(X + r * SEG_D + 8 * (b ^ s) + o);
+    const u32x2 y = *reinterpret_cast<const u32x2*>(X + r * SEG_D + 8 * ((b + 2) ^ s) + o);
+    return __builtin_bit_cast(bf16x8, u32x4{x[0], x[1], y[0], y[1]});
+}
+
+/* the same from a packed T / QKm matrix */
+__device__ __forceinline__ bf16x8 seg_mat(const __bf16* X, int r, int cc) {
+    const int b = cc >> 3, o = cc & 7;
+    const u32x2 x = *reinterpret_cast<const u32x2*>(X + pmat_offset(r, b) + o);
+    const u32x2 y = *reinterpret_cast<const u32x2*>(X + pmat_offset(r, b + 2) + o);
+    return __builtin_bit_cast(bf16x8, u32x4{x[0], x[1], y[0], y[1]});
+}
+
+template <bool OUT>
+__global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs sa) {
+    constexpr int KD = SEG_D, VD = SEG_D;
+    constexpr int NW = OUT ? 8 : 16;                   // waves
+    // 1 KB DMA blocks per chunk: k rows, q rows (pass C), T, QKm (pass C),
+    // the scalars, the value rows
+    constexpr int QB0 = 16, TB0 = OUT ? 32 : 16, MB0 = TB0 + 12, SB0 = OUT ? MB0 + 12 : MB0, VB0 = SB0 + 2;
+    constexpr int NBLK = VB0 + 16;
+    constexpr int PER = (NBLK + NW - 1) / NW;          // DMA blocks per wave
+    constexpr uint32_t KBUF = CH * KD * 2, TBUF = 2 * PMAT_BYTES, SBUF = 2048;
+    __shared__ __attribute__((aligned(16))) __bf16 Kb[2][CH * KD];
+    __shared__ __attribute__((aligned(16))) __bf16 Vb[2][CH * VD];
+    __shared__ __attribute__((aligned(16))) __bf16 Tb[2][2 * PMAT];
+    __shared__ __attribute__((aligned(16))) float Sb[2][512];
+    __shared__ __attribute__((aligned(16))) __bf16 Qb[OUT ? 2 : 1][OUT ? CH * KD : 8];
+    __shared__ __attribute__((aligned(16))) __bf16 Mb[OUT ? 2 : 1][OUT ? 2 * PMAT : 8];
+
+    const DeltaRuleParams& p = sa.d.p;
+    const uint32_t P = sa.P, L = sa.L, nChunks = sa.d.nChunks;
+    const uint32_t nSeg = OUT ? P : P - 1;
+    const uint32_t h = blockIdx.x / nSeg, sg = blockIdx.x % nSeg;
+    const uint32_t kh = uint32_t(h / (p.valueHeads / p.keyHeads));
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool hom = !OUT && w >= 8;                   // a wave of identity columns
+    const int cb = w & 7;                              // its 16-column block
+    const uint32_t c0 = sg * L, c1 = min(c0 + L, nChunks);
+    const size_t Hv = p.valueHeads;
+    float* const img = sa.seg + size_t(h) * SEG_SLOTS_PER_P * P * SEG_IMG;
+    // this lane's float4 of tile t in a state image: ((cb 8 + t) 64 + lane) 4
+    auto img_tile = [&](uint32_t slot, int t) -> float* {
+        return img + size_t(slot) * SEG_IMG + size_t((cb * 8 + t) * 64 + lane) * 4;
+    };
+
+    // S: tile t holds key rows 16 t + 4 g + r of column 16 cb + c16
+    floatx4 s[8];
+    if (OUT) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) s[t] = *reinterpret_cast<const floatx4*>(img_tile(slot_start(P, sg), t));
+    } else if (hom) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[t][r] = (16 * t + 4 * g + r == 16 * cb + c16) ? 1.0f : 0.0f;
+    } else if (sg == 0) {
+        const float* st = p.state + size_t(h) * KD * VD;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[t][r] = st[size_t(16 * t + 4 * g + r) * VD + 16 * cb + c16];
+            *reinterpret_cast<floatx4*>(img_tile(0, t)) = s[t];
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) s[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    // DMA: row blocks carry rows 4 j + lane / 16, 16-byte slot lane % 16
+    // holding the row's block slot ^ (row % 16); rows past a partial chunk's
+    // end repeat its last row (whose beta is 0)
+    const uint32_t rowBytes = uint32_t(p.keyHeads * KD * 2), vRowBytes = uint32_t(Hv * VD * 2);
+    const uint32_t ldsK = lds_address(Kb), ldsV = lds_address(Vb), ldsT = lds_address(Tb), ldsS = lds_address(Sb);
+    const uint32_t ldsQ = lds_address(Qb), ldsM = lds_address(Mb);
+    const uint32_t lr = uint32_t(lane >> 4), ls = uint32_t(lane & 15);
+    struct Src {
+        const uint8_t *k, *q, *v, *rec;
+        uint32_t n, buf;
+    };
+    auto src_of = [&](uint32_t chunk, uint32_t buf) __attribute__((always_inline)) {
+        const uint64_t t0 = uint64_t(chunk) * CH;
+        const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
+        return Src{static_cast<const uint8_t*>(p.k) + t0 * rowBytes + kh * KD * 2,
+                   static_cast<const uint8_t*>(p.q) + t0 * rowBytes + kh * KD * 2,
+                   static_cast<const uint8_t*>(p.v) + (t0 * Hv + h) * VD * 2,
+                   reinterpret_cast<const uint8_t*>(sa.d.work + (size_t(h) * nChunks + chunk) * WORK_SPLIT), n, buf};
+    };
+    auto row_off = [&](const Src& x, int j, uint32_t stride) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t row = 4 * uint32_t(j) + lr;
+        return min(row, x.n - 1) * stride + 16 * (ls ^ (row & 15));
+    };
+    auto dma_one = [&](const Src& x, int b) __attribute__((always_inline)) {
+        if (b < QB0) {
+            dma_block(x.k, row_off(x, b, rowBytes), ldsK + x.buf * KBUF + b * 1024);
+        } else if (OUT && b < TB0) {
+            dma_block(x.q, row_off(x, b - QB0, rowBytes), ldsQ + x.buf * KBUF + (b - QB0) * 1024);
+        } else if (b < MB0) {
+            dma_block(x.rec + (b - TB0) * 1024, 16 * uint32_t(lane), ldsT + x.buf * TBUF + (b - TB0) * 1024);
+        } else if (OUT && b < SB0) {
+            dma_block(x.rec + TBUF + (b - MB0) * 1024, 16 * uint32_t(lane), ldsM + x.buf * TBUF + (b - MB0) * 1024);
+        } else if (b < VB0) {
+            dma_block(x.rec + 2 * TBUF + (b - SB0) * 1024, 16 * uint32_t(lane), ldsS + x.buf * SBUF + (b - SB0) * 1024);
+        } else {
+            dma_block(x.v, row_off(x, b - VB0, vRowBytes), ldsV + x.buf * KBUF + (b - VB0) * 1024);
+        }
+    };
+    // the wave's blocks w, w + NW, ..., in three parts spread over a chunk
+    auto dma_part = [&](const Src& x, int part) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            if (i * 3 / PER != part) continue;
+            const int b = w + NW * i;
+            if (b < NBLK) dma_one(x, b);
+        }
+    };
+    {
+        const Src first = src_of(c0, 0);
+#pragma unroll
+        for (int part = 0; part < 3; ++part) dma_part(first, part);
+    }
+
+    for (uint32_t c = c0; c < c1; ++c) {
+        const uint32_t par = (c - c0) & 1;
+        // this chunk's inputs have landed; every read of the other buffers is done
+        wait_vmcnt_all();
+        __syncthreads();
+        // the lane coordinates pass through an empty asm each chunk, so that
+        // the LDS addresses built from them are computed in the phase that
+        // uses them instead of being held across the whole loop
+        int lv = lane;
+        asm volatile("" : "+v"(lv));
+        const int g = lv >> 4, c16 = lv & 15;
+        const bool more = c + 1 < c1;
+        const Src nx = src_of(more ? c + 1 : c, par ^ 1);
+        const __bf16* K = Kb[par];
+        const __bf16* V = Vb[par];
+        const __bf16* T = Tb[par];
+        const float* sc = Sb[par];
+        if (more) dma_part(nx, 0);
+
+        // R = K_raw S and, for the output, Q_raw S
+        floatx4 ra[4], qa[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ra[i] = qa[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            bf16x8 sh, sl;
+            split_pair(s[2 * j], s[2 * j + 1], sh, sl);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bf16x8 x = seg_rows(K, 16 * i + c16, 32 * j + 4 * g);
+                ra[i] = mfma_bf(x, sh, ra[i]);
+                ra[i] = mfma_bf(x, sl, ra[i]);
+                if constexpr (OUT) {
+                    const bf16x8 xq = seg_rows(Qb[par], 16 * i + c16, 32 * j + 4 * g);
+                    qa[i] = mfma_bf(xq, sh, qa[i]);
+                    qa[i] = mfma_bf(xq, sl, qa[i]);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);   // phases keep their own operands live
+        // R = beta (V - gamma kinv R)
+        floatx4 rv[4];
+        const int col = 16 * cb + c16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const floatx4 be = *reinterpret_cast<const floatx4*>(sc + 16 * i + 4 * g);
+            const floatx4 gk = *reinterpret_cast<const floatx4*>(sc + CH + 16 * i + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * i + 4 * g + r;
+                const float v = hom ? 0.0f : float(V[row * VD + 8 * ((col >> 3) ^ (row & 15)) + (col & 7)]);
+                rv[i][r] = be[r] * (v - gk[r] * ra[i][r]);
+            }
+        }
+        bf16x8 rh[2], rl[2];
+        split_pair(rv[0], rv[1], rh[0], rl[0]);
+        split_pair(rv[2], rv[3], rh[1], rl[1]);
+        if (more) dma_part(nx, 1);
+
+        __builtin_amdgcn_sched_barrier(0);
+        // U = T R (rows < 32 of T have no nonzero entry past column 31)
+        floatx4 u[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            u[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int jb = 0; jb < 2; ++jb) {
+                if (jb == 1 && i < 2) continue;
+                const bf16x8 th = seg_mat(T, 16 * i + c16, 32 * jb + 4 * g);
+                const bf16x8 tl = seg_mat(T + PMAT, 16 * i + c16, 32 * jb + 4 * g);
+                u[i] = mfma_bf(th, rh[jb], u[i]);
+                u[i] = mfma_bf(th, rl[jb], u[i]);
+                u[i] = mfma_bf(tl, rh[jb], u[i]);
+            }
+        }
+        // W = diag(kinv e^{gc_last - gc}) U
+        bf16x8 wh[2], wl[2];
+        {
+            floatx4 wv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wv[i] = *reinterpret_cast<const floatx4*>(sc + 3 * CH + 16 * i + 4 * g) * u[i];
+            split_pair(wv[0], wv[1], wh[0], wl[0]);
+            split_pair(wv[2], wv[3], wh[1], wl[1]);
+        }
+        if (more) dma_part(nx, 2);
+
+        __builtin_amdgcn_sched_barrier(0);
+        // O = gamma qinv (Q_raw S) + QKm U, before S moves on
+        if constexpr (OUT) {
+            bf16x8 uh[2], ul[2];
+            split_pair(u[0], u[1], uh[0], ul[0]);
+            split_pair(u[2], u[3], uh[1], ul[1]);
+            const __bf16* M = Mb[par];
+            const uint64_t t0 = uint64_t(c) * CH;
+            const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
+            float* ob = p.out + (t0 * Hv + h) * VD + col;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                floatx4 o = *reinterpret_cast<const floatx4*>(sc + 2 * CH + 16 * i + 4 * g) * qa[i];
+#pragma unroll
+                for (int jb = 0; jb < 2; ++jb) {
+                    if (jb == 1 && i < 2) continue;
+                    const bf16x8 mh = seg_mat(M, 16 * i + c16, 32 * jb + 4 * g);
+                    const bf16x8 ml = seg_mat(M + PMAT, 16 * i + c16, 32 * jb + 4 * g);
+                    o = mfma_bf(mh, uh[jb], o);
+                    o = mfma_bf(mh, ul[jb], o);
+                    o = mfma_bf(ml, uh[jb], o);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = uint32_t(16 * i + 4 * g + r);
+                    if (row < n) __builtin_nontemporal_store(o[r], ob + size_t(row) * Hv * VD);
+                }
+            }
+        }
+
+        __builtin_amdgcn_sched_barrier(0);
+        // S' = e^{gc_last} S + K_raw^T W: lane (c16, g) of a transposed read
+        // addresses row rb + c16 / 4, columns 16 t + 4 (c16 % 4) ..
+        const float eLast = sc[4 * CH];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[t][r] *= eLast;
+#pragma unroll
+            for (int ib = 0; ib < 2; ++ib) {
+                const int r0 = 32 * ib + 4 * g + (c16 >> 2), r1 = r0 + 16, kc = 16 * t + 4 * (c16 & 3);
+                const bf16x8 kt = tr_pair(K + r0 * KD + 8 * ((kc >> 3) ^ (r0 & 15)) + (kc & 7),
+                                          K + r1 * KD + 8 * ((kc >> 3) ^ (r1 & 15)) + (kc & 7));
+                s[t] = mfma_bf(kt, wh[ib], s[t]);
+                s[t] = mfma_bf(kt, wl[ib], s[t]);
+            }
+        }
+    }
+    wait_vmcnt_all();   // no DMA may still be landing when the LDS is released
+
+    if constexpr (OUT) {
+        if (sg == P - 1) {
+            float* st = p.state + size_t(h) * KD * VD;
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) st[size_t(16 * t + 4 * g + r) * VD + 16 * cb + c16] = s[t][r];
+        }
+    } else if (!hom) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) *reinterpret_cast<floatx4*>(img_tile(slot_b(sg), t)) = s[t];
+    } else if (sg >= 1) {
+        float* A = img + size_t(slot_a(P, sg)) * SEG_IMG;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) A[(16 * t + 4 * g + r) * SEG_D + 16 * cb + c16] = s[t][r];
+    }
+}
+
+/*
+    The join of the two-level scan, per (value head, 16 columns): start(s + 1)
+    = A_s start(s) + B_s for s = 1 .. P - 2, from start(1) = B_0. Wave w
+    computes tiles 2w and 2w + 1 (key rows 32 w ..), which are the 32-row
+    block w of the next product's contraction: it publishes their split in
+    LDS for the other waves.
+*/
+__global__ __launch_bounds__(256) void delta_join_kernel(SegArgs sa) {
+    const uint32_t P = sa.P;
+    const uint32_t h = blockIdx.x / 8, cb = blockIdx.x % 8;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const int w = tid >> 6;
+    __shared__ __attribute__((aligned(16))) u32x4 Bs[2][4][2][64];   // [buffer][block][hi, lo][lane]
+    float* const img = sa.seg + size_t(h) * SEG_SLOTS_PER_P * P * SEG_IMG;
+    auto tile = [&](uint32_t slot, int t) -> floatx4* {
+        return reinterpret_cast<floatx4*>(img + size_t(slot) * SEG_IMG + size_t((cb * 8 + t) * 64 + lane) * 4);
+    };
+    floatx4 x0 = *tile(slot_b(0), 2 * w), x1 = *tile(slot_b(0), 2 * w + 1);
+    for (uint32_t s = 1; s + 1 < P; ++s) {
+        const int buf = s & 1;
+        {
+            bf16x8 hi, lo;
+            split_pair(x0, x1, hi, lo);
+            Bs[buf][w][0][lane] = __builtin_bit_cast(u32x4, hi);
+            Bs[buf][w][1][lane] = __builtin_bit_cast(u32x4, lo);
+        }
+        __syncthreads();
+        x0 = *tile(slot_b(s), 2 * w);
+        x1 = *tile(slot_b(s), 2 * w + 1);
+        const float* A = img + size_t(slot_a(P, s)) * SEG_IMG;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bf16x8 bh = __builtin_bit_cast(bf16x8, Bs[buf][j][0][lane]);
+            const bf16x8 bl = __builtin_bit_cast(bf16x8, Bs[buf][j][1][lane]);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const float* row = A + (16 * (2 * w + tt) + c16) * SEG_D + 32 * j + 4 * g;
+                bf16x8 ah, al;
+                split_pair(*reinterpret_cast<const floatx4*>(row), *reinterpret_cast<const floatx4*>(row + 16), ah, al);
+                floatx4& acc = tt ? x1 : x0;
+                acc = mfma_bf(ah, bh, acc);
+                acc = mfma_bf(ah, bl, acc);
+                acc = mfma_bf(al, bh, acc);
+            }
+        }
+        *tile(slot_start(P, s + 1), 2 * w) = x0;
+        *tile(slot_start(P, s + 1), 2 * w + 1) = x1;
+    }
+}
+
 } // namespace
 
 bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream) {
@@ -1212,6 +1605,34 @@ bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream) {
 
     const dim3 sgrid(a.nChunks, unsigned(p.keyHeads));
     const dim3 grid{unsigned(p.valueHeads * (p.valueDim / NB))}, block{256};
+
+    // 128 x 128 heads over many chunks: the two-level scan, P segments per
+    // head so that pass C runs about one workgroup per CU, each segment at
+    // least 8 chunks long
+    uint32_t segP = 0, segL = 0;
+    if (dma && p.keyDim == SEG_D && p.valueDim == SEG_D && ctx.cus > 0) {
+        const uint64_t want = std::min<uint64_t>(16, uint64_t(ctx.cus) / p.valueHeads);
+        if (want >= 3 && a.nChunks >= 8 * want) {
+            segL = uint32_t((a.nChunks + want - 1) / want);
+            segP = (a.nChunks + segL - 1) / segL;
+        }
+    }
+    if (segP) {
+        SegArgs sa{a, nullptr, segP, segL};
+        sa.seg = static_cast<float*>(
+            ctx.grow(SLOT_DELTA_SEG, size_t(p.valueHeads) * SEG_SLOTS_PER_P * segP * SEG_IMG * sizeof(float)));
+        if (!sa.seg) return false;
+        const unsigned Hv = unsigned(p.valueHeads);
+        return ctx.launch("delta_solve_kernel", stream,
+                          [&] { hipLaunchKernelGGL((delta_solve_kernel<128, false, true>), sgrid, dim3(256), 0, stream, a); }) &&
+               ctx.launch("delta_seg_kernel<false>", stream,
+                          [&] { hipLaunchKernelGGL(delta_seg_kernel<false>, dim3(Hv * (segP - 1)), dim3(1024), 0, stream, sa); }) &&
+               (segP < 3 || ctx.launch("delta_join_kernel", stream, [&] {
+                    hipLaunchKernelGGL(delta_join_kernel, dim3(Hv * 8), dim3(256), 0, stream, sa);
+                })) &&
+               ctx.launch("delta_seg_kernel<true>", stream,
+                          [&] { hipLaunchKernelGGL(delta_seg_kernel<true>, dim3(Hv * segP), dim3(512), 0, stream, sa); });
+    }
 #define AIGPU_DELTA(KD)                                                                                        \
     if (p.keyDim == KD) {                                                                                      \
         if (!ctx.launch("delta_solve_kernel", stream, [&] {                                                    \

@@ -153,3 +153,68 @@ def test_cfg5_qwen3_next_16k(gpu):
     ro, go, rs, gs = run_gdn(gpu, 16384, 16, 32, 128, 128, 4, dtype="bf16")
     say("cfg5 out", assert_bf16_parity(ro, go, "cfg5 out"))
     say("cfg5 state", assert_bf16_parity(rs, gs, "cfg5 state"))
+
+
+def two_level_launches(fn):
+    """runs fn with launch profiling on; the number of pass-C launches of the
+    two-level scan it made"""
+    import aigpu
+    aigpu.profile(True)
+    aigpu.profile_reset()
+    try:
+        result = fn()
+        _, n = aigpu.profile_read("delta_seg_kernel<true>")
+    finally:
+        aigpu.profile(False)
+    return result, n
+
+
+# 128 x 128 heads over at least 8 chunks per segment take the two-level scan:
+# P = 256 CUs / value heads segments (at most 16), cut as evenly as whole chunks
+# allow; these shapes give P = 8 with L = 9 (segments 9 x 7 + 2 and a ragged
+# last chunk), P = 4 with L = 9 (9, 9, 9, 6), and P = 15 with L = 9
+@pytest.mark.parametrize("S,hk,hv", [(4100, 16, 32), (2085, 32, 64), (8292, 8, 16)])
+def test_bf16_two_level_scan(gpu, S, hk, hv):
+    s0 = O.fill_normal((hv, 128, 128), 31, "s0") * np.float32(0.1)
+    (ro, go, rs, gs), n = two_level_launches(
+        lambda: run_gdn(gpu, S, hk, hv, 128, 128, 31 + S, dtype="bf16", state0=s0))
+    assert n == 1, "the two-level scan did not run"
+    say(f"two-level S={S} hv={hv} out", assert_bf16_parity(ro, go, f"out two-level S={S}"))
+    say(f"two-level S={S} hv={hv} state", assert_bf16_parity(rs, gs, f"state two-level S={S}"))
+
+
+def test_bf16_two_level_scan_raw_gates(gpu):
+    (ro, go, rs, gs), n = two_level_launches(
+        lambda: run_gdn(gpu, 2085, 32, 64, 128, 128, 41, dtype="bf16", raw_gates=True))
+    assert n == 1, "the two-level scan did not run"
+    assert_bf16_parity(ro, go, "out two-level raw gates")
+    assert_bf16_parity(rs, gs, "state two-level raw gates")
+
+
+def test_bf16_two_level_continuation(gpu):
+    """4,100 tokens in one call (65 chunks, P = 4, L = 17) against two calls of
+    2,050 (33 chunks each, P = 4, L = 9) carrying the state: both take the
+    two-level scan, and the split, unaligned to a chunk, must agree"""
+    import torch
+    S, hk, hv = 4100, 32, 64
+    qb, _ = bf16_normal((S, hk, 128), 43, "q")
+    kb, _ = bf16_normal((S, hk, 128), 43, "k")
+    vb, _ = bf16_normal((S, hv, 128), 43, "v")
+    g, beta = gates(S, hv, 43)
+    s0 = O.fill_normal((hv, 128, 128), 43, "s0") * np.float32(0.1)
+
+    def run(lo, hi, state):
+        o = torch.zeros((hi - lo, hv, 128), dtype=torch.float32, device="cuda")
+        gpu.gated_delta_rule(dev_bf16(qb[lo:hi]), dev_bf16(kb[lo:hi]), dev_bf16(vb[lo:hi]), state, o,
+                             g=dev_f32(g[lo:hi]), beta=dev_f32(beta[lo:hi]))
+        return host(o)
+
+    say("two-level continuation")
+    whole_state = dev_f32(s0)
+    whole, n = two_level_launches(lambda: run(0, S, whole_state))
+    assert n == 1
+    split_state = dev_f32(s0)
+    parts, n = two_level_launches(lambda: [run(0, 2050, split_state), run(2050, S, split_state)])
+    assert n == 2
+    assert_bf16_parity(whole, np.concatenate(parts), "two-level continuation out")
+    assert_bf16_parity(host(whole_state), host(split_state), "two-level continuation state")
