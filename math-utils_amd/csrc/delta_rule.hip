@@ -1204,16 +1204,23 @@ __global__ __launch_bounds__(256) void delta_scan_dma_kernel(DeltaArgs a) {
     identity columns), 16 per wave, so each wave owns whole columns of S and
     no product needs another wave's results: the chunk's inputs arrive by DMA
     into double buffers and one barrier per chunk hands them over. Every B
-    operand is built in registers from the wave's own accumulators, so the
-    contraction index of each product is ordered as they hold it: a 32-row
-    block of the contraction is two 16-row accumulator tiles, lane (column,
-    g) holding rows 4g .. 4g+3 of each, so B slot e < 4 is row 4g + e and slot
-    e >= 4 row 16 + 4g + e - 4; the A operand reads the same contraction
-    columns as two 8-byte pieces, and K^T comes from the row-major K buffer
-    through transposed reads of those rows.
+    operand is built in registers from the wave's own accumulators. For that,
+    accumulator tile t (16 rows) holds the rows seg_row(t, m): lane (column,
+    g) register r holds row seg_row(t, 4g + r), so the two tiles 2j and 2j + 1
+    together hold rows 32j + 8g .. 32j + 8g + 7 in that lane, in order, which
+    is what a B operand's lane holds for the contraction block j. The state's
+    key rows and the chunk's token rows are both kept in this order; an A
+    operand then reads 16 contiguous bytes of a row, the rows of its M side
+    in the same order, and K^T's rows come from transposed reads of K whose
+    lanes address the column groups of seg_row.
 */
 constexpr int SEG_D = 128;                   // key and value dim of the two-level scan
 constexpr int SEG_IMG = SEG_D * SEG_D;       // floats per state image
+
+/* the row that position m (0..15) of accumulator tile t stands for */
+__host__ __device__ constexpr int seg_row(int t, int m) {
+    return 32 * (t >> 1) + 8 * (m >> 2) + 4 * (t & 1) + (m & 3);
+}
 
 struct SegArgs {
     DeltaArgs d;
@@ -1223,7 +1230,9 @@ struct SegArgs {
 
 /* image slots of a head: 0 the given state, 1 + s segment s's B (s <= P - 2),
    P + s segment s's A (1 <= s <= P - 2, row-major), then the starts of
-   segments 2 .. P - 1 (segment 1 starts at B_0) */
+   segments 2 .. P - 1 (segment 1 starts at B_0). A state image is the
+   accumulators as the waves hold them: float4 ((cb 8 + t) 64 + lane) is
+   tile t of column block cb. */
 __host__ __device__ constexpr uint32_t slot_b(uint32_t s) { return 1 + s; }
 __host__ __device__ constexpr uint32_t slot_a(uint32_t P, uint32_t s) { return P + s; }
 __host__ __device__ constexpr uint32_t slot_start(uint32_t P, uint32_t s) { return s == 0 ? 0 : s == 1 ? 1 : 2 * P - 1 + s; }
@@ -1241,32 +1250,9 @@ __device__ __forceinline__ void split_pair(const floatx4& x, const floatx4& y, b
     lo = __builtin_bit_cast(bf16x8, u32x4{c[0], c[1], d[0], d[1]});
 }
 
-/* A operand from a swizzled [64][128] row buffer (16-byte block b of row r
-   at b ^ (r % 16)): row r, columns cc .. cc+3 and cc+16 .. cc+19 */
-__device__ __forceinline__ bf16x8 seg_rows(const __bf16* X, int r, int cc) {
-    const int s = r & 15, b = cc >> 3, o = cc & 7;
-    const u32x2 x = *reinterpret_cast<const u32x2*>(X + r * SEG_D + 8 * (b ^ s) + o);
-    const u32x2 y = *reinterpret_cast<const u32x2*>(X + r * SEG_D + 8 * ((b + 2) ^ s) + o);
-    return __builtin_bit_cast(bf16x8, u32x4{x[0], x[1], y[0], y[1]});
-}
-
-/* the same from a packed T / QKm matrix */
-__device__ __forceinline__ bf16x8 seg_mat(const __bf16* X, int r, int cc) {
-    const int b = cc >> 3, o = cc & 7;
-    const u32x2 x = *reinterpret_cast<const u32x2*>(X + pmat_offset(r, b) + o);
-    const u32x2 y = *reinterpret_cast<const u32x2*>(X + pmat_offset(r, b + 2) + o);
-    return __builtin_bit_cast(bf16x8, u32x4{x[0], x[1], y[0], y[1]});
-}
-
 template <bool OUT>
 __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs sa) {
     constexpr int KD = SEG_D, VD = SEG_D;
-    constexpr int NW = OUT ? 8 : 16;                   // waves
-    // 1 KB DMA blocks per chunk: k rows, q rows (pass C), T, QKm (pass C),
-    // the scalars, the value rows
-    constexpr int QB0 = 16, TB0 = OUT ? 32 : 16, MB0 = TB0 + 12, SB0 = OUT ? MB0 + 12 : MB0, VB0 = SB0 + 2;
-    constexpr int NBLK = VB0 + 16;
-    constexpr int PER = (NBLK + NW - 1) / NW;          // DMA blocks per wave
     constexpr uint32_t KBUF = CH * KD * 2, TBUF = 2 * PMAT_BYTES, SBUF = 2048;
     __shared__ __attribute__((aligned(16))) __bf16 Kb[2][CH * KD];
     __shared__ __attribute__((aligned(16))) __bf16 Vb[2][CH * VD];
@@ -1284,44 +1270,48 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool hom = !OUT && w >= 8;                   // a wave of identity columns
     const int cb = w & 7;                              // its 16-column block
+    const int col = 16 * cb + c16;
     const uint32_t c0 = sg * L, c1 = min(c0 + L, nChunks);
     const size_t Hv = p.valueHeads;
     float* const img = sa.seg + size_t(h) * SEG_SLOTS_PER_P * P * SEG_IMG;
-    // this lane's float4 of tile t in a state image: ((cb 8 + t) 64 + lane) 4
-    auto img_tile = [&](uint32_t slot, int t) -> float* {
-        return img + size_t(slot) * SEG_IMG + size_t((cb * 8 + t) * 64 + lane) * 4;
+    auto img_tile = [&](uint32_t slot, int t) -> floatx4* {
+        return reinterpret_cast<floatx4*>(img + size_t(slot) * SEG_IMG + size_t((cb * 8 + t) * 64 + lane) * 4);
     };
 
-    // S: tile t holds key rows 16 t + 4 g + r of column 16 cb + c16
+    // S: tile t holds key rows seg_row(t, 4g + r) of column col
     floatx4 s[8];
     if (OUT) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) s[t] = *reinterpret_cast<const floatx4*>(img_tile(slot_start(P, sg), t));
+        for (int t = 0; t < 8; ++t) s[t] = *img_tile(slot_start(P, sg), t);
     } else if (hom) {
 #pragma unroll
         for (int t = 0; t < 8; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) s[t][r] = (16 * t + 4 * g + r == 16 * cb + c16) ? 1.0f : 0.0f;
+            for (int r = 0; r < 4; ++r) s[t][r] = seg_row(t, 4 * g + r) == col ? 1.0f : 0.0f;
     } else if (sg == 0) {
         const float* st = p.state + size_t(h) * KD * VD;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) s[t][r] = st[size_t(16 * t + 4 * g + r) * VD + 16 * cb + c16];
-            *reinterpret_cast<floatx4*>(img_tile(0, t)) = s[t];
+            for (int r = 0; r < 4; ++r) s[t][r] = st[size_t(seg_row(t, 4 * g + r)) * VD + col];
+            *img_tile(0, t) = s[t];
         }
     } else {
 #pragma unroll
         for (int t = 0; t < 8; ++t) s[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // DMA: row blocks carry rows 4 j + lane / 16, 16-byte slot lane % 16
-    // holding the row's block slot ^ (row % 16); rows past a partial chunk's
-    // end repeat its last row (whose beta is 0)
+    // DMA of a chunk, 1 KB blocks, the same kinds on every wave. Row blocks
+    // carry rows 4 j + lane / 16 with 16-byte slot lane % 16 holding the
+    // row's block slot ^ (row % 16); rows past a partial chunk's end repeat
+    // its last row (whose beta is 0). Pass C (8 waves): k and q blocks 2w,
+    // 2w + 1, value blocks 2w, 2w + 1, T and QKm blocks w (and w + 8 for
+    // w < 4), scalar block w < 2. Pass A (16 waves): k block w, value block w,
+    // T block w < 12, scalar block w - 12.
     const uint32_t rowBytes = uint32_t(p.keyHeads * KD * 2), vRowBytes = uint32_t(Hv * VD * 2);
     const uint32_t ldsK = lds_address(Kb), ldsV = lds_address(Vb), ldsT = lds_address(Tb), ldsS = lds_address(Sb);
     const uint32_t ldsQ = lds_address(Qb), ldsM = lds_address(Mb);
-    const uint32_t lr = uint32_t(lane >> 4), ls = uint32_t(lane & 15);
+    const uint32_t lr = uint32_t(lane >> 4), ls = uint32_t(lane & 15), l16 = 16 * uint32_t(lane);
     struct Src {
         const uint8_t *k, *q, *v, *rec;
         uint32_t n, buf;
@@ -1334,51 +1324,110 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
                    static_cast<const uint8_t*>(p.v) + (t0 * Hv + h) * VD * 2,
                    reinterpret_cast<const uint8_t*>(sa.d.work + (size_t(h) * nChunks + chunk) * WORK_SPLIT), n, buf};
     };
-    auto row_off = [&](const Src& x, int j, uint32_t stride) __attribute__((always_inline)) -> uint32_t {
-        const uint32_t row = 4 * uint32_t(j) + lr;
+    auto row_off = [&](const Src& x, uint32_t j, uint32_t stride) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t row = 4 * j + lr;
         return min(row, x.n - 1) * stride + 16 * (ls ^ (row & 15));
     };
-    auto dma_one = [&](const Src& x, int b) __attribute__((always_inline)) {
-        if (b < QB0) {
-            dma_block(x.k, row_off(x, b, rowBytes), ldsK + x.buf * KBUF + b * 1024);
-        } else if (OUT && b < TB0) {
-            dma_block(x.q, row_off(x, b - QB0, rowBytes), ldsQ + x.buf * KBUF + (b - QB0) * 1024);
-        } else if (b < MB0) {
-            dma_block(x.rec + (b - TB0) * 1024, 16 * uint32_t(lane), ldsT + x.buf * TBUF + (b - TB0) * 1024);
-        } else if (OUT && b < SB0) {
-            dma_block(x.rec + TBUF + (b - MB0) * 1024, 16 * uint32_t(lane), ldsM + x.buf * TBUF + (b - MB0) * 1024);
-        } else if (b < VB0) {
-            dma_block(x.rec + 2 * TBUF + (b - SB0) * 1024, 16 * uint32_t(lane), ldsS + x.buf * SBUF + (b - SB0) * 1024);
-        } else {
-            dma_block(x.v, row_off(x, b - VB0, vRowBytes), ldsV + x.buf * KBUF + (b - VB0) * 1024);
-        }
-    };
-    // the wave's blocks w, w + NW, ..., in three parts spread over a chunk
     auto dma_part = [&](const Src& x, int part) __attribute__((always_inline)) {
+        const uint32_t bk = x.buf * KBUF, bt = x.buf * TBUF;
+        if constexpr (OUT) {
+            if (part == 0) {
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            if (i * 3 / PER != part) continue;
-            const int b = w + NW * i;
-            if (b < NBLK) dma_one(x, b);
+                for (uint32_t e = 0; e < 2; ++e) {
+                    const uint32_t j = 2 * uint32_t(w) + e;
+                    const uint32_t off = row_off(x, j, rowBytes);
+                    dma_block(x.k, off, ldsK + bk + j * 1024);
+                    dma_block(x.q, off, ldsQ + bk + j * 1024);
+                }
+            } else if (part == 1) {
+                dma_block(x.rec + w * 1024, l16, ldsT + bt + w * 1024);
+                dma_block(x.rec + TBUF + w * 1024, l16, ldsM + bt + w * 1024);
+                if (w < 4) {
+                    dma_block(x.rec + (w + 8) * 1024, l16, ldsT + bt + (w + 8) * 1024);
+                    dma_block(x.rec + TBUF + (w + 8) * 1024, l16, ldsM + bt + (w + 8) * 1024);
+                }
+                if (w < 2) dma_block(x.rec + 2 * TBUF + w * 1024, l16, ldsS + x.buf * SBUF + w * 1024);
+            } else {
+#pragma unroll
+                for (uint32_t e = 0; e < 2; ++e) {
+                    const uint32_t j = 2 * uint32_t(w) + e;
+                    dma_block(x.v, row_off(x, j, vRowBytes), ldsV + bk + j * 1024);
+                }
+            }
+        } else {
+            if (part == 0) {
+                dma_block(x.k, row_off(x, uint32_t(w), rowBytes), ldsK + bk + w * 1024);
+            } else if (part == 1) {
+                if (w < 12) dma_block(x.rec + w * 1024, l16, ldsT + bt + w * 1024);
+                else if (w < 14) dma_block(x.rec + 2 * TBUF + (w - 12) * 1024, l16, ldsS + x.buf * SBUF + (w - 12) * 1024);
+            } else {
+                dma_block(x.v, row_off(x, uint32_t(w), vRowBytes), ldsV + bk + w * 1024);
+            }
         }
     };
     {
         const Src first = src_of(c0, 0);
-#pragma unroll
-        for (int part = 0; part < 3; ++part) dma_part(first, part);
+        dma_part(first, 0);
+        dma_part(first, 1);
+        dma_part(first, 2);
     }
+    const uint32_t oStride = uint32_t(Hv * VD * 4);      // bytes between output rows
+
+    // the lane's LDS byte offsets within a buffer; tiles i and i + 2 (token
+    // rows 32 apart) and the two halves of the token rows of K^T reads share
+    // a row's swizzle, so they differ by immediates
+    struct Offsets {
+        uint32_t k[2][4];    // k/q A operand: token row seg_row(i, c16), block 4j + g
+        uint32_t t[4][2];    // T/QKm A operand: token row seg_row(i, c16), block 4jb + g
+        uint32_t v[2][4];    // value of token row 8g + 4 (i & 1) + r, column col
+    };
+    auto offsets_of = [&](int gl, int cl) __attribute__((always_inline)) {
+        Offsets f;
+        const int cc = 16 * cb + cl;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = seg_row(i, cl);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f.k[i][j] = uint32_t(r * KD + 8 * ((4 * j + gl) ^ (r & 15))) * 2;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int row = 8 * gl + 4 * i + rr;
+                f.v[i][rr] = uint32_t(row * VD + 8 * ((cc >> 3) ^ (row & 15)) + (cc & 7)) * 2;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int jb = 0; jb < 2; ++jb)
+                f.t[i][jb] = (jb == 1 && i < 2) ? 0u : uint32_t(pmat_offset(seg_row(i, cl), 4 * jb + gl)) * 2;
+        return f;
+    };
+    // K^T: token row 8g + c16 / 4 (+ 4 for e = 1), key columns seg_row(t, 4 (c16 % 4)) ..
+    auto tr_off = [](int t, int e, int gl, int cl) __attribute__((always_inline)) -> uint32_t {
+        const int kc = seg_row(t, 4 * (cl & 3)), r = 8 * gl + (cl >> 2) + 4 * e;
+        return uint32_t(r * KD + 8 * ((kc >> 3) ^ (r & 15)) + (kc & 7)) * 2;
+    };
+    // pass C holds the offsets across the loop; pass A, at four waves per
+    // SIMD, has no registers for them and rebuilds them each chunk from the
+    // lane, which passes through an empty asm so that they are not hoisted
+    const Offsets held = offsets_of(g, c16);
+    uint32_t trOff[8][2];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) trOff[t][e] = tr_off(t, e, g, c16);
+    auto lds_at = [](const void* base, uint32_t bytes) __attribute__((always_inline)) {
+        return reinterpret_cast<const uint8_t*>(base) + bytes;
+    };
 
     for (uint32_t c = c0; c < c1; ++c) {
         const uint32_t par = (c - c0) & 1;
         // this chunk's inputs have landed; every read of the other buffers is done
         wait_vmcnt_all();
         __syncthreads();
-        // the lane coordinates pass through an empty asm each chunk, so that
-        // the LDS addresses built from them are computed in the phase that
-        // uses them instead of being held across the whole loop
         int lv = lane;
-        asm volatile("" : "+v"(lv));
-        const int g = lv >> 4, c16 = lv & 15;
+        if constexpr (!OUT) asm volatile("" : "+v"(lv));
+        const Offsets f = OUT ? held : offsets_of(lv >> 4, lv & 15);
         const bool more = c + 1 < c1;
         const Src nx = src_of(more ? c + 1 : c, par ^ 1);
         const __bf16* K = Kb[par];
@@ -1387,7 +1436,8 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
         const float* sc = Sb[par];
         if (more) dma_part(nx, 0);
 
-        // R = K_raw S and, for the output, Q_raw S
+        // R = K_raw S and, for the output, Q_raw S: A rows seg_row(i, c16),
+        // 16-byte block 4j + g
         floatx4 ra[4], qa[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) ra[i] = qa[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1397,28 +1447,29 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
             split_pair(s[2 * j], s[2 * j + 1], sh, sl);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const bf16x8 x = seg_rows(K, 16 * i + c16, 32 * j + 4 * g);
+                const uint32_t o = f.k[i & 1][j] + uint32_t(i >> 1) * 32 * KD * 2;
+                const bf16x8 x = *reinterpret_cast<const bf16x8*>(lds_at(K, o));
                 ra[i] = mfma_bf(x, sh, ra[i]);
                 ra[i] = mfma_bf(x, sl, ra[i]);
                 if constexpr (OUT) {
-                    const bf16x8 xq = seg_rows(Qb[par], 16 * i + c16, 32 * j + 4 * g);
+                    const bf16x8 xq = *reinterpret_cast<const bf16x8*>(lds_at(Qb[par], o));
                     qa[i] = mfma_bf(xq, sh, qa[i]);
                     qa[i] = mfma_bf(xq, sl, qa[i]);
                 }
             }
         }
         __builtin_amdgcn_sched_barrier(0);   // phases keep their own operands live
-        // R = beta (V - gamma kinv R)
+        // R = beta (V - gamma kinv R): tile i register r is token row
+        // seg_row(i, 4g + r) = b + r with b = 32 (i >> 1) + 4 (i & 1) + 8g
         floatx4 rv[4];
-        const int col = 16 * cb + c16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const floatx4 be = *reinterpret_cast<const floatx4*>(sc + 16 * i + 4 * g);
-            const floatx4 gk = *reinterpret_cast<const floatx4*>(sc + CH + 16 * i + 4 * g);
+            const int b = seg_row(i, 4 * g);
+            const floatx4 be = *reinterpret_cast<const floatx4*>(sc + b);
+            const floatx4 gk = *reinterpret_cast<const floatx4*>(sc + CH + b);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = 16 * i + 4 * g + r;
-                const float v = hom ? 0.0f : float(V[row * VD + 8 * ((col >> 3) ^ (row & 15)) + (col & 7)]);
+                const float v = hom ? 0.0f : float(*reinterpret_cast<const __bf16*>(lds_at(V, f.v[i & 1][r] + uint32_t(i >> 1) * 32 * VD * 2)));
                 rv[i][r] = be[r] * (v - gk[r] * ra[i][r]);
             }
         }
@@ -1426,9 +1477,9 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
         split_pair(rv[0], rv[1], rh[0], rl[0]);
         split_pair(rv[2], rv[3], rh[1], rl[1]);
         if (more) dma_part(nx, 1);
-
         __builtin_amdgcn_sched_barrier(0);
-        // U = T R (rows < 32 of T have no nonzero entry past column 31)
+
+        // U = T R (token rows < 32 have no nonzero T past column 31)
         floatx4 u[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -1436,8 +1487,8 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
 #pragma unroll
             for (int jb = 0; jb < 2; ++jb) {
                 if (jb == 1 && i < 2) continue;
-                const bf16x8 th = seg_mat(T, 16 * i + c16, 32 * jb + 4 * g);
-                const bf16x8 tl = seg_mat(T + PMAT, 16 * i + c16, 32 * jb + 4 * g);
+                const bf16x8 th = *reinterpret_cast<const bf16x8*>(lds_at(T, f.t[i][jb]));
+                const bf16x8 tl = *reinterpret_cast<const bf16x8*>(lds_at(T, f.t[i][jb] + PMAT_BYTES));
                 u[i] = mfma_bf(th, rh[jb], u[i]);
                 u[i] = mfma_bf(th, rl[jb], u[i]);
                 u[i] = mfma_bf(tl, rh[jb], u[i]);
@@ -1448,14 +1499,15 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
         {
             floatx4 wv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) wv[i] = *reinterpret_cast<const floatx4*>(sc + 3 * CH + 16 * i + 4 * g) * u[i];
+            for (int i = 0; i < 4; ++i) wv[i] = *reinterpret_cast<const floatx4*>(sc + 3 * CH + seg_row(i, 4 * g)) * u[i];
             split_pair(wv[0], wv[1], wh[0], wl[0]);
             split_pair(wv[2], wv[3], wh[1], wl[1]);
         }
         if (more) dma_part(nx, 2);
-
         __builtin_amdgcn_sched_barrier(0);
-        // O = gamma qinv (Q_raw S) + QKm U, before S moves on
+
+        // O = gamma qinv (Q_raw S) + QKm U, before S moves on; row b + r of
+        // the output leaves from a uniform row address plus the lane's offset
         if constexpr (OUT) {
             bf16x8 uh[2], ul[2];
             split_pair(u[0], u[1], uh[0], ul[0]);
@@ -1463,30 +1515,36 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
             const __bf16* M = Mb[par];
             const uint64_t t0 = uint64_t(c) * CH;
             const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
-            float* ob = p.out + (t0 * Hv + h) * VD + col;
+            uint8_t* const ob = reinterpret_cast<uint8_t*>(p.out + (t0 * Hv + h) * VD);
+            const uint32_t laneOff = uint32_t(8 * g) * oStride + uint32_t(col) * 4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                floatx4 o = *reinterpret_cast<const floatx4*>(sc + 2 * CH + 16 * i + 4 * g) * qa[i];
+                const int b0 = seg_row(i, 0);
+                floatx4 o = *reinterpret_cast<const floatx4*>(sc + 2 * CH + b0 + 8 * g) * qa[i];
 #pragma unroll
                 for (int jb = 0; jb < 2; ++jb) {
                     if (jb == 1 && i < 2) continue;
-                    const bf16x8 mh = seg_mat(M, 16 * i + c16, 32 * jb + 4 * g);
-                    const bf16x8 ml = seg_mat(M + PMAT, 16 * i + c16, 32 * jb + 4 * g);
+                    const bf16x8 mh = *reinterpret_cast<const bf16x8*>(lds_at(M, f.t[i][jb]));
+                    const bf16x8 ml = *reinterpret_cast<const bf16x8*>(lds_at(M, f.t[i][jb] + PMAT_BYTES));
                     o = mfma_bf(mh, uh[jb], o);
                     o = mfma_bf(mh, ul[jb], o);
                     o = mfma_bf(ml, uh[jb], o);
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const uint32_t row = uint32_t(16 * i + 4 * g + r);
-                    if (row < n) __builtin_nontemporal_store(o[r], ob + size_t(row) * Hv * VD);
+                    float* dst = reinterpret_cast<float*>(ob + size_t(b0 + r) * oStride + laneOff);
+                    if (n == CH || uint32_t(b0 + 8 * g + r) < n) __builtin_nontemporal_store(o[r], dst);
                 }
             }
         }
-
         __builtin_amdgcn_sched_barrier(0);
-        // S' = e^{gc_last} S + K_raw^T W: lane (c16, g) of a transposed read
-        // addresses row rb + c16 / 4, columns 16 t + 4 (c16 % 4) ..
+
+        // S' = e^{gc_last} S + K_raw^T W. The transposed read of 16 lanes
+        // (c16 = 4a + e) returns to lane m the 8-byte column group that lane
+        // 4k + m / 4 addressed, element m % 4, for rows k = 0..3: lane c16
+        // addresses token row 32 ib + 8g + c16 / 4 (and + 4), key columns
+        // seg_row(t, 4 (c16 % 4)) .. + 3, so lane m receives key row
+        // seg_row(t, m) over the token rows of the B operand's block ib
         const float eLast = sc[4 * CH];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -1494,9 +1552,11 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
             for (int r = 0; r < 4; ++r) s[t][r] *= eLast;
 #pragma unroll
             for (int ib = 0; ib < 2; ++ib) {
-                const int r0 = 32 * ib + 4 * g + (c16 >> 2), r1 = r0 + 16, kc = 16 * t + 4 * (c16 & 3);
-                const bf16x8 kt = tr_pair(K + r0 * KD + 8 * ((kc >> 3) ^ (r0 & 15)) + (kc & 7),
-                                          K + r1 * KD + 8 * ((kc >> 3) ^ (r1 & 15)) + (kc & 7));
+                const uint32_t ro = uint32_t(ib) * 32 * KD * 2;
+                const uint32_t o0 = OUT ? trOff[t][0] : tr_off(t, 0, lv >> 4, lv & 15);
+                const uint32_t o1 = OUT ? trOff[t][1] : tr_off(t, 1, lv >> 4, lv & 15);
+                const bf16x8 kt = tr_pair(reinterpret_cast<const __bf16*>(lds_at(K, o0 + ro)),
+                                          reinterpret_cast<const __bf16*>(lds_at(K, o1 + ro)));
                 s[t] = mfma_bf(kt, wh[ib], s[t]);
                 s[t] = mfma_bf(kt, wl[ib], s[t]);
             }
@@ -1510,26 +1570,27 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
 #pragma unroll
             for (int t = 0; t < 8; ++t)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) st[size_t(16 * t + 4 * g + r) * VD + 16 * cb + c16] = s[t][r];
+                for (int r = 0; r < 4; ++r) st[size_t(seg_row(t, 4 * g + r)) * VD + col] = s[t][r];
         }
     } else if (!hom) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) *reinterpret_cast<floatx4*>(img_tile(slot_b(sg), t)) = s[t];
+        for (int t = 0; t < 8; ++t) *img_tile(slot_b(sg), t) = s[t];
     } else if (sg >= 1) {
         float* A = img + size_t(slot_a(P, sg)) * SEG_IMG;
 #pragma unroll
         for (int t = 0; t < 8; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) A[(16 * t + 4 * g + r) * SEG_D + 16 * cb + c16] = s[t][r];
+            for (int r = 0; r < 4; ++r) A[seg_row(t, 4 * g + r) * SEG_D + col] = s[t][r];
     }
 }
 
 /*
     The join of the two-level scan, per (value head, 16 columns): start(s + 1)
     = A_s start(s) + B_s for s = 1 .. P - 2, from start(1) = B_0. Wave w
-    computes tiles 2w and 2w + 1 (key rows 32 w ..), which are the 32-row
-    block w of the next product's contraction: it publishes their split in
-    LDS for the other waves.
+    computes tiles 2w and 2w + 1, key rows 32 w .. 32 w + 31, which are the
+    32-row block w of the next product's contraction: it publishes their
+    split in LDS for the other waves. The next step's A rows and B tiles are
+    loaded while this step multiplies.
 */
 __global__ __launch_bounds__(256) void delta_join_kernel(SegArgs sa) {
     const uint32_t P = sa.P;
@@ -1541,7 +1602,27 @@ __global__ __launch_bounds__(256) void delta_join_kernel(SegArgs sa) {
     auto tile = [&](uint32_t slot, int t) -> floatx4* {
         return reinterpret_cast<floatx4*>(img + size_t(slot) * SEG_IMG + size_t((cb * 8 + t) * 64 + lane) * 4);
     };
+    // wave w's A rows of step s: seg_row(2w + tt, c16), contraction columns 32 j + 8 g .. + 7
+    struct Step {
+        floatx4 a[2][4][2];
+        floatx4 b[2];
+    };
+    auto load_step = [&](uint32_t s, Step& st) __attribute__((always_inline)) {
+        const float* A = img + size_t(slot_a(P, s)) * SEG_IMG;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float* row = A + seg_row(2 * w + tt, c16) * SEG_D + 32 * j + 8 * g;
+                st.a[tt][j][0] = *reinterpret_cast<const floatx4*>(row);
+                st.a[tt][j][1] = *reinterpret_cast<const floatx4*>(row + 4);
+            }
+        st.b[0] = *tile(slot_b(s), 2 * w);
+        st.b[1] = *tile(slot_b(s), 2 * w + 1);
+    };
     floatx4 x0 = *tile(slot_b(0), 2 * w), x1 = *tile(slot_b(0), 2 * w + 1);
+    Step cur;
+    if (P > 2) load_step(1, cur);
     for (uint32_t s = 1; s + 1 < P; ++s) {
         const int buf = s & 1;
         {
@@ -1551,18 +1632,18 @@ __global__ __launch_bounds__(256) void delta_join_kernel(SegArgs sa) {
             Bs[buf][w][1][lane] = __builtin_bit_cast(u32x4, lo);
         }
         __syncthreads();
-        x0 = *tile(slot_b(s), 2 * w);
-        x1 = *tile(slot_b(s), 2 * w + 1);
-        const float* A = img + size_t(slot_a(P, s)) * SEG_IMG;
+        Step nxt;
+        if (s + 2 < P) load_step(s + 1, nxt);
+        x0 = cur.b[0];
+        x1 = cur.b[1];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const bf16x8 bh = __builtin_bit_cast(bf16x8, Bs[buf][j][0][lane]);
             const bf16x8 bl = __builtin_bit_cast(bf16x8, Bs[buf][j][1][lane]);
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
-                const float* row = A + (16 * (2 * w + tt) + c16) * SEG_D + 32 * j + 4 * g;
                 bf16x8 ah, al;
-                split_pair(*reinterpret_cast<const floatx4*>(row), *reinterpret_cast<const floatx4*>(row + 16), ah, al);
+                split_pair(cur.a[tt][j][0], cur.a[tt][j][1], ah, al);
                 floatx4& acc = tt ? x1 : x0;
                 acc = mfma_bf(ah, bh, acc);
                 acc = mfma_bf(ah, bl, acc);
@@ -1571,6 +1652,7 @@ __global__ __launch_bounds__(256) void delta_join_kernel(SegArgs sa) {
         }
         *tile(slot_start(P, s + 1), 2 * w) = x0;
         *tile(slot_start(P, s + 1), 2 * w + 1) = x1;
+        cur = nxt;
     }
 }
 
