@@ -1251,8 +1251,11 @@ __device__ __forceinline__ void split_pair(const floatx4& x, const floatx4& y, b
 }
 
 template <bool OUT>
-__global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs sa) {
+__global__ __launch_bounds__(512, 1) void delta_seg_kernel(SegArgs sa) {
     constexpr int KD = SEG_D, VD = SEG_D;
+    // 16-column blocks per wave: pass C one of the 8 value blocks; pass A two
+    // of the 16 (waves 0-3 the value blocks, waves 4-7 the identity's)
+    constexpr int NCB = OUT ? 1 : 2;
     constexpr uint32_t KBUF = CH * KD * 2, TBUF = 2 * PMAT_BYTES, SBUF = 2048;
     __shared__ __attribute__((aligned(16))) __bf16 Kb[2][CH * KD];
     __shared__ __attribute__((aligned(16))) __bf16 Vb[2][CH * VD];
@@ -1268,46 +1271,48 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
     const uint32_t kh = uint32_t(h / (p.valueHeads / p.keyHeads));
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool hom = !OUT && w >= 8;                   // a wave of identity columns
-    const int cb = w & 7;                              // its 16-column block
-    const int col = 16 * cb + c16;
+    const bool hom = !OUT && w >= 4;                   // a wave of identity columns
+    // the wave's value (or identity) columns: block cbOf(b) of 8, column colOf(b)
+    auto cbOf = [&](int b) { return (NCB * w + b) & 7; };
+    auto colOf = [&](int b) { return 16 * cbOf(b) + c16; };
     const uint32_t c0 = sg * L, c1 = min(c0 + L, nChunks);
     const size_t Hv = p.valueHeads;
     float* const img = sa.seg + size_t(h) * SEG_SLOTS_PER_P * P * SEG_IMG;
-    auto img_tile = [&](uint32_t slot, int t) -> floatx4* {
-        return reinterpret_cast<floatx4*>(img + size_t(slot) * SEG_IMG + size_t((cb * 8 + t) * 64 + lane) * 4);
+    auto img_tile = [&](uint32_t slot, int b, int t) -> floatx4* {
+        return reinterpret_cast<floatx4*>(img + size_t(slot) * SEG_IMG + size_t((cbOf(b) * 8 + t) * 64 + lane) * 4);
     };
 
-    // S: tile t holds key rows seg_row(t, 4g + r) of column col
-    floatx4 s[8];
-    if (OUT) {
+    // S: tile t of block b holds key rows seg_row(t, 4g + r) of column colOf(b)
+    floatx4 s[NCB][8];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) s[t] = *img_tile(slot_start(P, sg), t);
-    } else if (hom) {
+    for (int b = 0; b < NCB; ++b) {
+        if (OUT) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
+            for (int t = 0; t < 8; ++t) s[b][t] = *img_tile(slot_start(P, sg), b, t);
+        } else if (hom) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) s[t][r] = seg_row(t, 4 * g + r) == col ? 1.0f : 0.0f;
-    } else if (sg == 0) {
-        const float* st = p.state + size_t(h) * KD * VD;
+            for (int t = 0; t < 8; ++t)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+                for (int r = 0; r < 4; ++r) s[b][t][r] = seg_row(t, 4 * g + r) == colOf(b) ? 1.0f : 0.0f;
+        } else if (sg == 0) {
+            const float* st = p.state + size_t(h) * KD * VD;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) s[t][r] = st[size_t(seg_row(t, 4 * g + r)) * VD + col];
-            *img_tile(0, t) = s[t];
+            for (int t = 0; t < 8; ++t) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[b][t][r] = st[size_t(seg_row(t, 4 * g + r)) * VD + colOf(b)];
+                *img_tile(0, b, t) = s[b][t];
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) s[b][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-    } else {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) s[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // DMA of a chunk, 1 KB blocks, the same kinds on every wave. Row blocks
-    // carry rows 4 j + lane / 16 with 16-byte slot lane % 16 holding the
-    // row's block slot ^ (row % 16); rows past a partial chunk's end repeat
-    // its last row (whose beta is 0). Pass C (8 waves): k and q blocks 2w,
-    // 2w + 1, value blocks 2w, 2w + 1, T and QKm blocks w (and w + 8 for
-    // w < 4), scalar block w < 2. Pass A (16 waves): k block w, value block w,
-    // T block w < 12, scalar block w - 12.
+    // DMA of a chunk in 1 KB blocks, the same kinds on every wave: k (and q)
+    // blocks 2w, 2w + 1, value blocks 2w, 2w + 1, T (and QKm) blocks w and,
+    // for w < 4, w + 8, scalar block w < 2. Row blocks carry rows 4 j + lane
+    // / 16 with 16-byte slot lane % 16 holding the row's block slot ^ (row %
+    // 16); rows past a partial chunk's end repeat its last row (whose beta is 0).
     const uint32_t rowBytes = uint32_t(p.keyHeads * KD * 2), vRowBytes = uint32_t(Hv * VD * 2);
     const uint32_t ldsK = lds_address(Kb), ldsV = lds_address(Vb), ldsT = lds_address(Tb), ldsS = lds_address(Sb);
     const uint32_t ldsQ = lds_address(Qb), ldsM = lds_address(Mb);
@@ -1330,38 +1335,27 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
     };
     auto dma_part = [&](const Src& x, int part) __attribute__((always_inline)) {
         const uint32_t bk = x.buf * KBUF, bt = x.buf * TBUF;
-        if constexpr (OUT) {
-            if (part == 0) {
+        if (part == 0) {
 #pragma unroll
-                for (uint32_t e = 0; e < 2; ++e) {
-                    const uint32_t j = 2 * uint32_t(w) + e;
-                    const uint32_t off = row_off(x, j, rowBytes);
-                    dma_block(x.k, off, ldsK + bk + j * 1024);
-                    dma_block(x.q, off, ldsQ + bk + j * 1024);
-                }
-            } else if (part == 1) {
-                dma_block(x.rec + w * 1024, l16, ldsT + bt + w * 1024);
-                dma_block(x.rec + TBUF + w * 1024, l16, ldsM + bt + w * 1024);
-                if (w < 4) {
-                    dma_block(x.rec + (w + 8) * 1024, l16, ldsT + bt + (w + 8) * 1024);
-                    dma_block(x.rec + TBUF + (w + 8) * 1024, l16, ldsM + bt + (w + 8) * 1024);
-                }
-                if (w < 2) dma_block(x.rec + 2 * TBUF + w * 1024, l16, ldsS + x.buf * SBUF + w * 1024);
-            } else {
-#pragma unroll
-                for (uint32_t e = 0; e < 2; ++e) {
-                    const uint32_t j = 2 * uint32_t(w) + e;
-                    dma_block(x.v, row_off(x, j, vRowBytes), ldsV + bk + j * 1024);
-                }
+            for (uint32_t e = 0; e < 2; ++e) {
+                const uint32_t j = 2 * uint32_t(w) + e;
+                const uint32_t off = row_off(x, j, rowBytes);
+                dma_block(x.k, off, ldsK + bk + j * 1024);
+                if constexpr (OUT) dma_block(x.q, off, ldsQ + bk + j * 1024);
             }
+        } else if (part == 1) {
+            dma_block(x.rec + w * 1024, l16, ldsT + bt + w * 1024);
+            if constexpr (OUT) dma_block(x.rec + TBUF + w * 1024, l16, ldsM + bt + w * 1024);
+            if (w < 4) {
+                dma_block(x.rec + (w + 8) * 1024, l16, ldsT + bt + (w + 8) * 1024);
+                if constexpr (OUT) dma_block(x.rec + TBUF + (w + 8) * 1024, l16, ldsM + bt + (w + 8) * 1024);
+            }
+            if (w < 2) dma_block(x.rec + 2 * TBUF + w * 1024, l16, ldsS + x.buf * SBUF + w * 1024);
         } else {
-            if (part == 0) {
-                dma_block(x.k, row_off(x, uint32_t(w), rowBytes), ldsK + bk + w * 1024);
-            } else if (part == 1) {
-                if (w < 12) dma_block(x.rec + w * 1024, l16, ldsT + bt + w * 1024);
-                else if (w < 14) dma_block(x.rec + 2 * TBUF + (w - 12) * 1024, l16, ldsS + x.buf * SBUF + (w - 12) * 1024);
-            } else {
-                dma_block(x.v, row_off(x, uint32_t(w), vRowBytes), ldsV + bk + w * 1024);
+#pragma unroll
+            for (uint32_t e = 0; e < 2; ++e) {
+                const uint32_t j = 2 * uint32_t(w) + e;
+                dma_block(x.v, row_off(x, j, vRowBytes), ldsV + bk + j * 1024);
             }
         }
     };
@@ -1373,49 +1367,40 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
     }
     const uint32_t oStride = uint32_t(Hv * VD * 4);      // bytes between output rows
 
-    // the lane's LDS byte offsets within a buffer; tiles i and i + 2 (token
-    // rows 32 apart) and the two halves of the token rows of K^T reads share
-    // a row's swizzle, so they differ by immediates
-    struct Offsets {
-        uint32_t k[2][4];    // k/q A operand: token row seg_row(i, c16), block 4j + g
-        uint32_t t[4][2];    // T/QKm A operand: token row seg_row(i, c16), block 4jb + g
-        uint32_t v[2][4];    // value of token row 8g + 4 (i & 1) + r, column col
-    };
-    auto offsets_of = [&](int gl, int cl) __attribute__((always_inline)) {
-        Offsets f;
-        const int cc = 16 * cb + cl;
+    // The lane's LDS byte offsets within a buffer, held across the loop.
+    // Tiles i and i + 2 (token rows 32 apart) and the two token-row blocks of
+    // a K^T read share a row's swizzle, so they differ by immediates.
+    uint32_t kOff[2][4];   // k/q A operand: token row seg_row(i, c16), block 4j + g
+    uint32_t tOff[4][2];   // T/QKm A operand: token row seg_row(i, c16), block 4jb + g
+    uint32_t vOff[NCB][2][4];   // value of token row 8g + 4 (i & 1) + r, column colOf(b)
+    uint32_t trOff[8][2];  // K^T: token row 8g + c16 / 4 (+ 4), key columns seg_row(t, 4 (c16 % 4)) ..
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int r = seg_row(i, cl);
+    for (int i = 0; i < 2; ++i) {
+        const int r = seg_row(i, c16);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) f.k[i][j] = uint32_t(r * KD + 8 * ((4 * j + gl) ^ (r & 15))) * 2;
+        for (int j = 0; j < 4; ++j) kOff[i][j] = uint32_t(r * KD + 8 * ((4 * j + g) ^ (r & 15))) * 2;
+#pragma unroll
+        for (int b = 0; b < NCB; ++b)
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
-                const int row = 8 * gl + 4 * i + rr;
-                f.v[i][rr] = uint32_t(row * VD + 8 * ((cc >> 3) ^ (row & 15)) + (cc & 7)) * 2;
+                const int row = 8 * g + 4 * i + rr, cc = colOf(b);
+                vOff[b][i][rr] = uint32_t(row * VD + 8 * ((cc >> 3) ^ (row & 15)) + (cc & 7)) * 2;
             }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb)
+            tOff[i][jb] = (jb == 1 && i < 2) ? 0u : uint32_t(pmat_offset(seg_row(i, c16), 4 * jb + g)) * 2;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int kc = seg_row(t, 4 * (c16 & 3));
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int r = 8 * g + (c16 >> 2) + 4 * e;
+            trOff[t][e] = uint32_t(r * KD + 8 * ((kc >> 3) ^ (r & 15)) + (kc & 7)) * 2;
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int jb = 0; jb < 2; ++jb)
-                f.t[i][jb] = (jb == 1 && i < 2) ? 0u : uint32_t(pmat_offset(seg_row(i, cl), 4 * jb + gl)) * 2;
-        return f;
-    };
-    // K^T: token row 8g + c16 / 4 (+ 4 for e = 1), key columns seg_row(t, 4 (c16 % 4)) ..
-    auto tr_off = [](int t, int e, int gl, int cl) __attribute__((always_inline)) -> uint32_t {
-        const int kc = seg_row(t, 4 * (cl & 3)), r = 8 * gl + (cl >> 2) + 4 * e;
-        return uint32_t(r * KD + 8 * ((kc >> 3) ^ (r & 15)) + (kc & 7)) * 2;
-    };
-    // pass C holds the offsets across the loop; pass A, at four waves per
-    // SIMD, has no registers for them and rebuilds them each chunk from the
-    // lane, which passes through an empty asm so that they are not hoisted
-    const Offsets held = offsets_of(g, c16);
-    uint32_t trOff[8][2];
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) trOff[t][e] = tr_off(t, e, g, c16);
+    }
     auto lds_at = [](const void* base, uint32_t bytes) __attribute__((always_inline)) {
         return reinterpret_cast<const uint8_t*>(base) + bytes;
     };
@@ -1425,9 +1410,6 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
         // this chunk's inputs have landed; every read of the other buffers is done
         wait_vmcnt_all();
         __syncthreads();
-        int lv = lane;
-        if constexpr (!OUT) asm volatile("" : "+v"(lv));
-        const Offsets f = OUT ? held : offsets_of(lv >> 4, lv & 15);
         const bool more = c + 1 < c1;
         const Src nx = src_of(more ? c + 1 : c, par ^ 1);
         const __bf16* K = Kb[par];
@@ -1437,86 +1419,104 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
         if (more) dma_part(nx, 0);
 
         // R = K_raw S and, for the output, Q_raw S: A rows seg_row(i, c16),
-        // 16-byte block 4j + g
-        floatx4 ra[4], qa[4];
+        // 16-byte block 4j + g; each A fragment serves the wave's blocks
+        floatx4 ra[NCB][4], qa[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ra[i] = qa[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < 4; ++i) {
+            qa[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int b = 0; b < NCB; ++b) ra[b][i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            bf16x8 sh, sl;
-            split_pair(s[2 * j], s[2 * j + 1], sh, sl);
+            bf16x8 sh[NCB], sl[NCB];
+#pragma unroll
+            for (int b = 0; b < NCB; ++b) split_pair(s[b][2 * j], s[b][2 * j + 1], sh[b], sl[b]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t o = f.k[i & 1][j] + uint32_t(i >> 1) * 32 * KD * 2;
+                const uint32_t o = kOff[i & 1][j] + uint32_t(i >> 1) * 32 * KD * 2;
                 const bf16x8 x = *reinterpret_cast<const bf16x8*>(lds_at(K, o));
-                ra[i] = mfma_bf(x, sh, ra[i]);
-                ra[i] = mfma_bf(x, sl, ra[i]);
+#pragma unroll
+                for (int b = 0; b < NCB; ++b) {
+                    ra[b][i] = mfma_bf(x, sh[b], ra[b][i]);
+                    ra[b][i] = mfma_bf(x, sl[b], ra[b][i]);
+                }
                 if constexpr (OUT) {
                     const bf16x8 xq = *reinterpret_cast<const bf16x8*>(lds_at(Qb[par], o));
-                    qa[i] = mfma_bf(xq, sh, qa[i]);
-                    qa[i] = mfma_bf(xq, sl, qa[i]);
+                    qa[i] = mfma_bf(xq, sh[0], qa[i]);
+                    qa[i] = mfma_bf(xq, sl[0], qa[i]);
                 }
             }
         }
         __builtin_amdgcn_sched_barrier(0);   // phases keep their own operands live
         // R = beta (V - gamma kinv R): tile i register r is token row
         // seg_row(i, 4g + r) = b + r with b = 32 (i >> 1) + 4 (i & 1) + 8g
-        floatx4 rv[4];
+        bf16x8 rh[NCB][2], rl[NCB][2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int b = seg_row(i, 4 * g);
-            const floatx4 be = *reinterpret_cast<const floatx4*>(sc + b);
-            const floatx4 gk = *reinterpret_cast<const floatx4*>(sc + CH + b);
+        for (int b = 0; b < NCB; ++b) {
+            floatx4 rv[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float v = hom ? 0.0f : float(*reinterpret_cast<const __bf16*>(lds_at(V, f.v[i & 1][r] + uint32_t(i >> 1) * 32 * VD * 2)));
-                rv[i][r] = be[r] * (v - gk[r] * ra[i][r]);
+            for (int i = 0; i < 4; ++i) {
+                const int rb = seg_row(i, 4 * g);
+                const floatx4 be = *reinterpret_cast<const floatx4*>(sc + rb);
+                const floatx4 gk = *reinterpret_cast<const floatx4*>(sc + CH + rb);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float v = hom ? 0.0f
+                                        : float(*reinterpret_cast<const __bf16*>(
+                                              lds_at(V, vOff[b][i & 1][r] + uint32_t(i >> 1) * 32 * VD * 2)));
+                    rv[i][r] = be[r] * (v - gk[r] * ra[b][i][r]);
+                }
             }
+            split_pair(rv[0], rv[1], rh[b][0], rl[b][0]);
+            split_pair(rv[2], rv[3], rh[b][1], rl[b][1]);
         }
-        bf16x8 rh[2], rl[2];
-        split_pair(rv[0], rv[1], rh[0], rl[0]);
-        split_pair(rv[2], rv[3], rh[1], rl[1]);
         if (more) dma_part(nx, 1);
         __builtin_amdgcn_sched_barrier(0);
 
         // U = T R (token rows < 32 have no nonzero T past column 31)
-        floatx4 u[4];
+        floatx4 u[NCB][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            u[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int b = 0; b < NCB; ++b) u[b][i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int jb = 0; jb < 2; ++jb) {
                 if (jb == 1 && i < 2) continue;
-                const bf16x8 th = *reinterpret_cast<const bf16x8*>(lds_at(T, f.t[i][jb]));
-                const bf16x8 tl = *reinterpret_cast<const bf16x8*>(lds_at(T, f.t[i][jb] + PMAT_BYTES));
-                u[i] = mfma_bf(th, rh[jb], u[i]);
-                u[i] = mfma_bf(th, rl[jb], u[i]);
-                u[i] = mfma_bf(tl, rh[jb], u[i]);
+                const bf16x8 th = *reinterpret_cast<const bf16x8*>(lds_at(T, tOff[i][jb]));
+                const bf16x8 tl = *reinterpret_cast<const bf16x8*>(lds_at(T, tOff[i][jb] + PMAT_BYTES));
+#pragma unroll
+                for (int b = 0; b < NCB; ++b) {
+                    u[b][i] = mfma_bf(th, rh[b][jb], u[b][i]);
+                    u[b][i] = mfma_bf(th, rl[b][jb], u[b][i]);
+                    u[b][i] = mfma_bf(tl, rh[b][jb], u[b][i]);
+                }
             }
         }
         // W = diag(kinv e^{gc_last - gc}) U
-        bf16x8 wh[2], wl[2];
-        {
+        bf16x8 wh[NCB][2], wl[NCB][2];
+#pragma unroll
+        for (int b = 0; b < NCB; ++b) {
             floatx4 wv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) wv[i] = *reinterpret_cast<const floatx4*>(sc + 3 * CH + seg_row(i, 4 * g)) * u[i];
-            split_pair(wv[0], wv[1], wh[0], wl[0]);
-            split_pair(wv[2], wv[3], wh[1], wl[1]);
+            for (int i = 0; i < 4; ++i) wv[i] = *reinterpret_cast<const floatx4*>(sc + 3 * CH + seg_row(i, 4 * g)) * u[b][i];
+            split_pair(wv[0], wv[1], wh[b][0], wl[b][0]);
+            split_pair(wv[2], wv[3], wh[b][1], wl[b][1]);
         }
         if (more) dma_part(nx, 2);
         __builtin_amdgcn_sched_barrier(0);
 
-        // O = gamma qinv (Q_raw S) + QKm U, before S moves on; row b + r of
+        // O = gamma qinv (Q_raw S) + QKm U, before S moves on; row b0 + r of
         // the output leaves from a uniform row address plus the lane's offset
         if constexpr (OUT) {
             bf16x8 uh[2], ul[2];
-            split_pair(u[0], u[1], uh[0], ul[0]);
-            split_pair(u[2], u[3], uh[1], ul[1]);
+            split_pair(u[0][0], u[0][1], uh[0], ul[0]);
+            split_pair(u[0][2], u[0][3], uh[1], ul[1]);
             const __bf16* M = Mb[par];
             const uint64_t t0 = uint64_t(c) * CH;
             const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
             uint8_t* const ob = reinterpret_cast<uint8_t*>(p.out + (t0 * Hv + h) * VD);
-            const uint32_t laneOff = uint32_t(8 * g) * oStride + uint32_t(col) * 4;
+            const uint32_t laneOff = uint32_t(8 * g) * oStride + uint32_t(colOf(0)) * 4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int b0 = seg_row(i, 0);
@@ -1524,8 +1524,8 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
 #pragma unroll
                 for (int jb = 0; jb < 2; ++jb) {
                     if (jb == 1 && i < 2) continue;
-                    const bf16x8 mh = *reinterpret_cast<const bf16x8*>(lds_at(M, f.t[i][jb]));
-                    const bf16x8 ml = *reinterpret_cast<const bf16x8*>(lds_at(M, f.t[i][jb] + PMAT_BYTES));
+                    const bf16x8 mh = *reinterpret_cast<const bf16x8*>(lds_at(M, tOff[i][jb]));
+                    const bf16x8 ml = *reinterpret_cast<const bf16x8*>(lds_at(M, tOff[i][jb] + PMAT_BYTES));
                     o = mfma_bf(mh, uh[jb], o);
                     o = mfma_bf(mh, ul[jb], o);
                     o = mfma_bf(ml, uh[jb], o);
@@ -1549,38 +1549,44 @@ __global__ __launch_bounds__(OUT ? 512 : 1024, 1) void delta_seg_kernel(SegArgs 
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) s[t][r] *= eLast;
+            for (int b = 0; b < NCB; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[b][t][r] *= eLast;
 #pragma unroll
             for (int ib = 0; ib < 2; ++ib) {
                 const uint32_t ro = uint32_t(ib) * 32 * KD * 2;
-                const uint32_t o0 = OUT ? trOff[t][0] : tr_off(t, 0, lv >> 4, lv & 15);
-                const uint32_t o1 = OUT ? trOff[t][1] : tr_off(t, 1, lv >> 4, lv & 15);
-                const bf16x8 kt = tr_pair(reinterpret_cast<const __bf16*>(lds_at(K, o0 + ro)),
-                                          reinterpret_cast<const __bf16*>(lds_at(K, o1 + ro)));
-                s[t] = mfma_bf(kt, wh[ib], s[t]);
-                s[t] = mfma_bf(kt, wl[ib], s[t]);
+                const bf16x8 kt = tr_pair(reinterpret_cast<const __bf16*>(lds_at(K, trOff[t][0] + ro)),
+                                          reinterpret_cast<const __bf16*>(lds_at(K, trOff[t][1] + ro)));
+#pragma unroll
+                for (int b = 0; b < NCB; ++b) {
+                    s[b][t] = mfma_bf(kt, wh[b][ib], s[b][t]);
+                    s[b][t] = mfma_bf(kt, wl[b][ib], s[b][t]);
+                }
             }
         }
     }
     wait_vmcnt_all();   // no DMA may still be landing when the LDS is released
 
-    if constexpr (OUT) {
-        if (sg == P - 1) {
-            float* st = p.state + size_t(h) * KD * VD;
+#pragma unroll
+    for (int b = 0; b < NCB; ++b) {
+        if constexpr (OUT) {
+            if (sg == P - 1) {
+                float* st = p.state + size_t(h) * KD * VD;
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) st[size_t(seg_row(t, 4 * g + r)) * VD + colOf(b)] = s[b][t][r];
+            }
+        } else if (!hom) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) *img_tile(slot_b(sg), b, t) = s[b][t];
+        } else if (sg >= 1) {
+            float* A = img + size_t(slot_a(P, sg)) * SEG_IMG;
 #pragma unroll
             for (int t = 0; t < 8; ++t)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) st[size_t(seg_row(t, 4 * g + r)) * VD + col] = s[t][r];
+                for (int r = 0; r < 4; ++r) A[seg_row(t, 4 * g + r) * SEG_D + colOf(b)] = s[b][t][r];
         }
-    } else if (!hom) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) *img_tile(slot_b(sg), t) = s[t];
-    } else if (sg >= 1) {
-        float* A = img + size_t(slot_a(P, sg)) * SEG_IMG;
-#pragma unroll
-        for (int t = 0; t < 8; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) A[seg_row(t, 4 * g + r) * SEG_D + col] = s[t][r];
     }
 }
 
@@ -1708,7 +1714,7 @@ bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream) {
         return ctx.launch("delta_solve_kernel", stream,
                           [&] { hipLaunchKernelGGL((delta_solve_kernel<128, false, true>), sgrid, dim3(256), 0, stream, a); }) &&
                ctx.launch("delta_seg_kernel<false>", stream,
-                          [&] { hipLaunchKernelGGL(delta_seg_kernel<false>, dim3(Hv * (segP - 1)), dim3(1024), 0, stream, sa); }) &&
+                          [&] { hipLaunchKernelGGL(delta_seg_kernel<false>, dim3(Hv * (segP - 1)), dim3(512), 0, stream, sa); }) &&
                (segP < 3 || ctx.launch("delta_join_kernel", stream, [&] {
                     hipLaunchKernelGGL(delta_join_kernel, dim3(Hv * 8), dim3(256), 0, stream, sa);
                 })) &&
