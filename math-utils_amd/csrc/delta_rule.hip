@@ -1599,8 +1599,11 @@ __global__ __launch_bounds__(512, 1) void delta_seg_kernel(SegArgs sa) {
     loaded while this step multiplies.
 */
 __global__ __launch_bounds__(256) void delta_join_kernel(SegArgs sa) {
-    const uint32_t P = sa.P;
-    const uint32_t h = blockIdx.x / 8, cb = blockIdx.x % 8;
+    const uint32_t P = sa.P, Hv = uint32_t(sa.d.p.valueHeads);
+    // a head's 8 workgroups read the same A and B images: with the heads a
+    // multiple of 8, they share blockIdx % 8 and so one XCD's L2
+    const uint32_t h = Hv % 8 == 0 ? blockIdx.x % Hv : blockIdx.x / 8;
+    const uint32_t cb = Hv % 8 == 0 ? blockIdx.x / Hv : blockIdx.x % 8;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
     const int w = tid >> 6;
     __shared__ __attribute__((aligned(16))) u32x4 Bs[2][4][2][64];   // [buffer][block][hi, lo][lane]
