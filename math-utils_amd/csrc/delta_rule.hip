@@ -50,8 +50,10 @@ constexpr int NS = NB + 1;
 constexpr int SC = 4 * CH;               // gc, beta, kinv, qinv per chunk
 constexpr int WORK = 2 * CH * CH + SC;   // floats per (head, chunk) record, fp32 form
 // the split form, laid out as the DMA scan's LDS image: T hi, T lo, QKm hi,
-// QKm lo, then 512 floats: beta, gamma kinv, gamma qinv, kinv exp(gc_last -
-// gc), exp(gc_last) (64 copies), zeros. T and QKm are lower triangular, so
+// QKm lo (left unwritten for the two-level scan, which forms QKm itself), then
+// 512 floats: beta, gamma kinv, gamma qinv, kinv exp(gc_last - gc),
+// exp(gc_last) (64 copies), a = gc log2(e) + log2(qinv), b = gc log2(e) -
+// log2(kinv), zeros. T and QKm are lower triangular, so
 // rows 0-31 keep only their first 32 columns (the scan's waves 0 and 1 read
 // no other k block): a packed bf16 matrix is rows 0-31 x 32 columns (16-byte
 // block b of row r at b ^ ((r >> 1 ^ r >> 3) & 3)) followed by rows 32-63 x
@@ -168,9 +170,10 @@ __device__ __forceinline__ void chunk_gates(const DeltaRuleParams& p, uint64_t t
     the decayed masks A and QKm and T = (I + A)^-1, written to that value
     head's record.
 */
-template <int KD, bool F32, bool SPLIT>
+template <int KD, bool F32, bool SPLIT, bool QKM = true>
 __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs a) {
     static_assert(!(F32 && SPLIT), "the split form serves bf16 inputs");
+    static_assert(QKM || SPLIT, "only the split form leaves QKm to the scan");
     constexpr int PE = KD / 4;              // elements of a row per thread
     constexpr int EPL = F32 ? 4 : 8;        // elements per 16-byte load
     constexpr int KH = F32 ? KD + 1 : KD + 8;   // LDS row stride in elements
@@ -273,8 +276,9 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
                 const bf16x8 kj = *reinterpret_cast<const bf16x8*>(&ks[(16 * ct + c16) * KH + 32 * kb + 8 * g]);
                 x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                     *reinterpret_cast<const bf16x8*>(&ks[(16 * w + c16) * KH + 32 * kb + 8 * g]), kj, x, 0, 0, 0);
-                y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    *reinterpret_cast<const bf16x8*>(&qs[(16 * w + c16) * KH + 32 * kb + 8 * g]), kj, y, 0, 0, 0);
+                if constexpr (QKM)
+                    y = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        *reinterpret_cast<const bf16x8*>(&qs[(16 * w + c16) * KH + 32 * kb + 8 * g]), kj, y, 0, 0, 0);
             }
         }
         const int j = 16 * ct + c16;
@@ -312,8 +316,11 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
                 const int i = 16 * w + 4 * g + r, j = 16 * ct + c16;
                 const float dec = j <= i ? decay_exp<SPLIT>(gsc[i] - gsc[j]) : 0.0f;
                 Am[i * CS + j] = j < i ? gsc[CH + i] * dec * kk[ct][r] : 0.0f;
-                if constexpr (SPLIT) qkv[ct][r] = dec * qk[ct][r];
-                else qkm[i * CH + j] = dec * qk[ct][r];
+                if constexpr (SPLIT) {
+                    if constexpr (QKM) qkv[ct][r] = dec * qk[ct][r];
+                } else {
+                    qkm[i * CH + j] = dec * qk[ct][r];
+                }
             }
         __syncthreads();
 
@@ -369,11 +376,14 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
         } else {
             // QKm into Am (free now that T is done), then both matrices split
             // into bf16 hi/lo rows, 16 bytes per store, in the scan's LDS image
+            // (without QKm, the two-level scan's form: T alone)
+            if constexpr (QKM) {
 #pragma unroll
-            for (int ct = 0; ct < 4; ++ct)
+                for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) Am[(16 * w + 4 * g + r) * CS + 16 * ct + c16] = qkv[ct][r];
-            __syncthreads();
+                    for (int r = 0; r < 4; ++r) Am[(16 * w + 4 * g + r) * CS + 16 * ct + c16] = qkv[ct][r];
+                __syncthreads();
+            }
             uint16_t* out16 = reinterpret_cast<uint16_t*>(rec);
 #pragma unroll
             for (int it = 0; it < 2; ++it) {
@@ -381,7 +391,7 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
                 if (r < 32 && b >= 4) continue;   // above the diagonal blocks: zero, not stored
                 const int dst = pmat_offset(r, b);
 #pragma unroll
-                for (int m = 0; m < 2; ++m) {
+                for (int m = 0; m < (QKM ? 2 : 1); ++m) {
                     const float* src = (m == 0 ? Tm : Am) + r * CS + 8 * b;
                     bf16x4 h0, l0, h1, l1;
                     split_bf16x4(floatx4{src[0], src[1], src[2], src[3]}, h0, l0);
@@ -404,6 +414,10 @@ __global__ __launch_bounds__(256, F32 ? 1 : 3) void delta_solve_kernel(DeltaArgs
                 else if (part == 2) x = decay_exp<true>(gsc[i]) * nrm[CH + i];
                 else if (part == 3) x = nrm[i] * decay_exp<true>(gLast - gsc[i]);
                 else if (part == 4) x = decay_exp<true>(gLast);
+                // the factors of QKm for a scan that forms it from the raw
+                // products: QKm_ij = (q_i.k_j) 2^(a_i - b_j), j <= i
+                else if (part == 5) x = gsc[i] * LOG2E + __builtin_amdgcn_logf(nrm[CH + i]);
+                else if (part == 6) x = gsc[i] * LOG2E - __builtin_amdgcn_logf(nrm[i]);
                 sc[idx] = x;
             }
         }
@@ -1262,7 +1276,9 @@ __global__ __launch_bounds__(512, 1) void delta_seg_kernel(SegArgs sa) {
     __shared__ __attribute__((aligned(16))) __bf16 Tb[2][2 * PMAT];
     __shared__ __attribute__((aligned(16))) float Sb[2][512];
     __shared__ __attribute__((aligned(16))) __bf16 Qb[OUT ? 2 : 1][OUT ? CH * KD : 8];
-    __shared__ __attribute__((aligned(16))) __bf16 Mb[OUT ? 2 : 1][OUT ? 2 * PMAT : 8];
+    // pass C: QKm's A operands for O, block p = (query tile i, key block jb)
+    // formed by wave p: [p][hi, lo][lane] 16 bytes
+    __shared__ __attribute__((aligned(16))) u32x4 Qm[OUT ? 6 : 1][2][64];
 
     const DeltaRuleParams& p = sa.d.p;
     const uint32_t P = sa.P, L = sa.L, nChunks = sa.d.nChunks;
@@ -1309,13 +1325,13 @@ __global__ __launch_bounds__(512, 1) void delta_seg_kernel(SegArgs sa) {
     }
 
     // DMA of a chunk in 1 KB blocks, the same kinds on every wave: k (and q)
-    // blocks 2w, 2w + 1, value blocks 2w, 2w + 1, T (and QKm) blocks w and,
-    // for w < 4, w + 8, scalar block w < 2. Row blocks carry rows 4 j + lane
+    // blocks 2w, 2w + 1, value blocks 2w, 2w + 1, T blocks w and, for w < 4,
+    // w + 8, scalar block w < 2. Row blocks carry rows 4 j + lane
     // / 16 with 16-byte slot lane % 16 holding the row's block slot ^ (row %
     // 16); rows past a partial chunk's end repeat its last row (whose beta is 0).
     const uint32_t rowBytes = uint32_t(p.keyHeads * KD * 2), vRowBytes = uint32_t(Hv * VD * 2);
     const uint32_t ldsK = lds_address(Kb), ldsV = lds_address(Vb), ldsT = lds_address(Tb), ldsS = lds_address(Sb);
-    const uint32_t ldsQ = lds_address(Qb), ldsM = lds_address(Mb);
+    const uint32_t ldsQ = lds_address(Qb);
     const uint32_t lr = uint32_t(lane >> 4), ls = uint32_t(lane & 15), l16 = 16 * uint32_t(lane);
     struct Src {
         const uint8_t *k, *q, *v, *rec;
@@ -1345,11 +1361,7 @@ __global__ __launch_bounds__(512, 1) void delta_seg_kernel(SegArgs sa) {
             }
         } else if (part == 1) {
             dma_block(x.rec + w * 1024, l16, ldsT + bt + w * 1024);
-            if constexpr (OUT) dma_block(x.rec + TBUF + w * 1024, l16, ldsM + bt + w * 1024);
-            if (w < 4) {
-                dma_block(x.rec + (w + 8) * 1024, l16, ldsT + bt + (w + 8) * 1024);
-                if constexpr (OUT) dma_block(x.rec + TBUF + (w + 8) * 1024, l16, ldsM + bt + (w + 8) * 1024);
-            }
+            if (w < 4) dma_block(x.rec + (w + 8) * 1024, l16, ldsT + bt + (w + 8) * 1024);
             if (w < 2) dma_block(x.rec + 2 * TBUF + w * 1024, l16, ldsS + x.buf * SBUF + w * 1024);
         } else {
 #pragma unroll
@@ -1419,8 +1431,14 @@ __global__ __launch_bounds__(512, 1) void delta_seg_kernel(SegArgs sa) {
         if (more) dma_part(nx, 0);
 
         // R = K_raw S and, for the output, Q_raw S: A rows seg_row(i, c16),
-        // 16-byte block 4j + g; each A fragment serves the wave's blocks
-        floatx4 ra[NCB][4], qa[4];
+        // 16-byte block 4j + g; each A fragment serves the wave's blocks. In
+        // pass C, wave w < 6 also forms block w = (query tile i, key block jb)
+        // of QKm from the same fragments: D(jt, i) = K_raw Q_raw^T over key
+        // tiles jt = 2jb, 2jb + 1 (exact bf16 products), whose lane (query
+        // seg_row(i, c16), g) holds the keys 32 jb + 8g .. + 7 that the A
+        // operand of QKm U needs in that lane.
+        constexpr int PI[6] = {0, 1, 2, 2, 3, 3}, PJB[6] = {0, 0, 0, 1, 0, 1};
+        floatx4 ra[NCB][4], qa[4], d0 = {0.0f, 0.0f, 0.0f, 0.0f}, d1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             qa[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1432,20 +1450,59 @@ __global__ __launch_bounds__(512, 1) void delta_seg_kernel(SegArgs sa) {
             bf16x8 sh[NCB], sl[NCB];
 #pragma unroll
             for (int b = 0; b < NCB; ++b) split_pair(s[b][2 * j], s[b][2 * j + 1], sh[b], sl[b]);
+            bf16x8 x[4], xq[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t o = kOff[i & 1][j] + uint32_t(i >> 1) * 32 * KD * 2;
-                const bf16x8 x = *reinterpret_cast<const bf16x8*>(lds_at(K, o));
+                x[i] = *reinterpret_cast<const bf16x8*>(lds_at(K, o));
+                if constexpr (OUT) xq[i] = *reinterpret_cast<const bf16x8*>(lds_at(Qb[par], o));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
 #pragma unroll
                 for (int b = 0; b < NCB; ++b) {
-                    ra[b][i] = mfma_bf(x, sh[b], ra[b][i]);
-                    ra[b][i] = mfma_bf(x, sl[b], ra[b][i]);
+                    ra[b][i] = mfma_bf(x[i], sh[b], ra[b][i]);
+                    ra[b][i] = mfma_bf(x[i], sl[b], ra[b][i]);
                 }
                 if constexpr (OUT) {
-                    const bf16x8 xq = *reinterpret_cast<const bf16x8*>(lds_at(Qb[par], o));
-                    qa[i] = mfma_bf(xq, sh[0], qa[i]);
-                    qa[i] = mfma_bf(xq, sl[0], qa[i]);
+                    qa[i] = mfma_bf(xq[i], sh[0], qa[i]);
+                    qa[i] = mfma_bf(xq[i], sl[0], qa[i]);
                 }
+            }
+            if constexpr (OUT) {
+#pragma unroll
+                for (int pb = 0; pb < 6; ++pb)
+                    if (pb == w) {
+                        d0 = mfma_bf(x[2 * PJB[pb]], xq[PI[pb]], d0);
+                        d1 = mfma_bf(x[2 * PJB[pb] + 1], xq[PI[pb]], d1);
+                    }
+            }
+        }
+        // QKm_ij = D_ji 2^(a_i - b_j) for keys j <= query i (the solve's
+        // factors a and b carry the decays and the inverse norms), split and
+        // published for every wave's output
+        if constexpr (OUT) {
+            if (w < 6) {
+#pragma unroll
+                for (int pb = 0; pb < 6; ++pb)
+                    if (pb == w) {
+                        const int i = PI[pb], jb = PJB[pb], qrow = seg_row(i, c16);
+                        const bool diag = (i >> 1) == jb;   // keys past the query are masked
+                        const float ai = sc[5 * CH + qrow];
+                        const floatx4 bj0 = *reinterpret_cast<const floatx4*>(sc + 6 * CH + 32 * jb + 8 * g);
+                        const floatx4 bj1 = *reinterpret_cast<const floatx4*>(sc + 6 * CH + 32 * jb + 8 * g + 4);
+                        floatx4 m0, m1;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int k0 = 32 * jb + 8 * g + e, k1 = k0 + 4;
+                            m0[e] = d0[e] * __builtin_amdgcn_exp2f(diag && k0 > qrow ? -INFINITY : ai - bj0[e]);
+                            m1[e] = d1[e] * __builtin_amdgcn_exp2f(diag && k1 > qrow ? -INFINITY : ai - bj1[e]);
+                        }
+                        bf16x8 mh, ml;
+                        split_pair(m0, m1, mh, ml);
+                        Qm[pb][0][lane] = __builtin_bit_cast(u32x4, mh);
+                        Qm[pb][1][lane] = __builtin_bit_cast(u32x4, ml);
+                    }
             }
         }
         __builtin_amdgcn_sched_barrier(0);   // phases keep their own operands live
@@ -1512,11 +1569,11 @@ __global__ __launch_bounds__(512, 1) void delta_seg_kernel(SegArgs sa) {
             bf16x8 uh[2], ul[2];
             split_pair(u[0][0], u[0][1], uh[0], ul[0]);
             split_pair(u[0][2], u[0][3], uh[1], ul[1]);
-            const __bf16* M = Mb[par];
             const uint64_t t0 = uint64_t(c) * CH;
             const uint32_t n = uint32_t(p.count - t0 < CH ? p.count - t0 : CH);
             uint8_t* const ob = reinterpret_cast<uint8_t*>(p.out + (t0 * Hv + h) * VD);
             const uint32_t laneOff = uint32_t(8 * g) * oStride + uint32_t(colOf(0)) * 4;
+            lds_barrier();   // every wave's QKm block is published
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int b0 = seg_row(i, 0);
@@ -1524,8 +1581,9 @@ __global__ __launch_bounds__(512, 1) void delta_seg_kernel(SegArgs sa) {
 #pragma unroll
                 for (int jb = 0; jb < 2; ++jb) {
                     if (jb == 1 && i < 2) continue;
-                    const bf16x8 mh = *reinterpret_cast<const bf16x8*>(lds_at(M, tOff[i][jb]));
-                    const bf16x8 ml = *reinterpret_cast<const bf16x8*>(lds_at(M, tOff[i][jb] + PMAT_BYTES));
+                    const int pb = i < 2 ? i : 2 * i - 2 + jb;
+                    const bf16x8 mh = __builtin_bit_cast(bf16x8, Qm[pb][0][lane]);
+                    const bf16x8 ml = __builtin_bit_cast(bf16x8, Qm[pb][1][lane]);
                     o = mfma_bf(mh, uh[jb], o);
                     o = mfma_bf(mh, ul[jb], o);
                     o = mfma_bf(ml, uh[jb], o);
@@ -1715,7 +1773,7 @@ bool launch_delta_rule(const DeltaRuleParams& p, hipStream_t stream) {
         if (!sa.seg) return false;
         const unsigned Hv = unsigned(p.valueHeads);
         return ctx.launch("delta_solve_kernel", stream,
-                          [&] { hipLaunchKernelGGL((delta_solve_kernel<128, false, true>), sgrid, dim3(256), 0, stream, a); }) &&
+                          [&] { hipLaunchKernelGGL((delta_solve_kernel<128, false, true, false>), sgrid, dim3(256), 0, stream, a); }) &&
                ctx.launch("delta_seg_kernel<false>", stream,
                           [&] { hipLaunchKernelGGL(delta_seg_kernel<false>, dim3(Hv * (segP - 1)), dim3(512), 0, stream, sa); }) &&
                (segP < 3 || ctx.launch("delta_join_kernel", stream, [&] {
