@@ -14,7 +14,8 @@
 // Every exponent is a difference gc_i - gc_j <= 0 or gc itself, so nothing
 // overflows however strongly the gates decay.
 //
-// Two launches:
+// The single-level form is two launches (the two-level scan for long 128 x
+// 128 heads, further down, replaces the second with three):
 //   delta_solve_kernel  parallel over (key head, chunk): l2 norms, KK^T, QK^T,
 //                       then per value head the decayed masks and
 //                       T = (I + A)^-1 (blocked: four 16 x 16 diagonal blocks
