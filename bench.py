@@ -57,6 +57,11 @@ PREFILL_FLASH_TRAFFIC = 318.4e6
 # HBM bytes per launch of decode_attention_kernel<128> on configs[3], measured
 # the same way (`--workload decode`): 1,240.4 MB read + 5.2 MB written
 DECODE_ATTENTION_TRAFFIC = 1245.6e6
+# HBM bytes per step of the two-level delta scan on configs[4] (pass A, the
+# join and pass C together; `--workload delta`, the same scaling): pass A
+# 340.0 MB read + 29.7 MB written, the join 27.3 + 12.6 MB, pass C 402.9 +
+# 278.6 MB
+DELTA_SCAN_TRAFFIC = 1091.1e6
 
 
 def parse():
@@ -499,7 +504,7 @@ def delta_workload(args, cpu):
         "recurrence_tflops": flops / (step_ms * 1e-3) / 1e12,
         "roofline": {"kernel": " + ".join(scan_kernels), "bound": "hbm",
                      "achieved": scan_bytes / (k_ms * 1e-3) / 1e9, "peak": PEAK_HBM, "unit": "GB/s",
-                     "frac": scan_bytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": None,
+                     "frac": scan_bytes / (k_ms * 1e-3) / 1e9 / PEAK_HBM, "traffic": DELTA_SCAN_TRAFFIC,
                      "kernel_ms": k_ms, "bytes_per_launch": scan_bytes,
                      "all_kernels_ms": launched_ms, "all_kernels_frac": nbytes / (launched_ms * 1e-3) / 1e9 / PEAK_HBM,
                      "bytes_per_step": nbytes},
