@@ -1689,9 +1689,10 @@ __global__ __launch_bounds__(256) void delta_join_kernel(SegArgs sa) {
         st.b[1] = *tile(slot_b(s), 2 * w + 1);
     };
     floatx4 x0 = *tile(slot_b(0), 2 * w), x1 = *tile(slot_b(0), 2 * w + 1);
-    Step cur;
-    if (P > 2) load_step(1, cur);
-    for (uint32_t s = 1; s + 1 < P; ++s) {
+    // steps s = 1 .. P - 2; step s's loads are issued two steps ahead into a
+    // ring of three named buffers (no copies, so nothing waits for them
+    // before their use), and the barrier waits only for LDS
+    auto step = [&](uint32_t s, const Step& cur, Step& fill) __attribute__((always_inline)) {
         const int buf = s & 1;
         {
             bf16x8 hi, lo;
@@ -1699,9 +1700,8 @@ __global__ __launch_bounds__(256) void delta_join_kernel(SegArgs sa) {
             Bs[buf][w][0][lane] = __builtin_bit_cast(u32x4, hi);
             Bs[buf][w][1][lane] = __builtin_bit_cast(u32x4, lo);
         }
-        __syncthreads();
-        Step nxt;
-        if (s + 2 < P) load_step(s + 1, nxt);
+        lds_barrier();
+        if (s + 2 <= P - 2) load_step(s + 2, fill);
         x0 = cur.b[0];
         x1 = cur.b[1];
 #pragma unroll
@@ -1720,7 +1720,14 @@ __global__ __launch_bounds__(256) void delta_join_kernel(SegArgs sa) {
         }
         *tile(slot_start(P, s + 1), 2 * w) = x0;
         *tile(slot_start(P, s + 1), 2 * w + 1) = x1;
-        cur = nxt;
+    };
+    Step r0, r1, r2;
+    if (P > 2) load_step(1, r0);
+    if (P > 3) load_step(2, r1);
+    for (uint32_t s = 1; s + 1 < P; s += 3) {
+        step(s, r0, r2);
+        if (s + 2 < P) step(s + 1, r1, r0);
+        if (s + 3 < P) step(s + 2, r2, r1);
     }
 }
 
