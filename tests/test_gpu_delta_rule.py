@@ -173,8 +173,11 @@ def two_level_launches(fn):
 # P = 256 CUs / value heads segments (at most 16), cut as evenly as whole chunks
 # allow; these shapes give P = 8 with L = 9 (segments 9 x 7 + 2 and a ragged
 # last chunk), P = 4 with L = 9 (9, 9, 9, 6), and P = 15 with L = 9, with two
-# value heads per key head, then four (P = 8) and one (P = 4)
-@pytest.mark.parametrize("S,hk,hv", [(4100, 16, 32), (2085, 32, 64), (8292, 8, 16), (4100, 8, 32), (2085, 64, 64)])
+# value heads per key head, then four (P = 8) and one (P = 4); 20 value heads
+# (P = 12, L = 10: a head count that is not a multiple of 8, so the join's
+# workgroups of a head do not share an XCD)
+@pytest.mark.parametrize("S,hk,hv", [(4100, 16, 32), (2085, 32, 64), (8292, 8, 16), (4100, 8, 32), (2085, 64, 64),
+                                     (7323, 10, 20)])
 def test_bf16_two_level_scan(gpu, S, hk, hv):
     s0 = O.fill_normal((hv, 128, 128), 31, "s0") * np.float32(0.1)
     (ro, go, rs, gs), n = two_level_launches(
