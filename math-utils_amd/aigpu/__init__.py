@@ -402,6 +402,39 @@ def gated_delta_rule(q, k, v, state, out, g=None, beta=None, a=None, b=None, a_l
     return out
 
 
+def gated_delta_rule_host(q, k, v, state, g=None, beta=None, a=None, b=None, a_log=None, dt_bias=None,
+                          normalize=True):
+    """Host form (aigpu_gated_delta_rule_host, the entry the reference's C++
+    mixer binds): q, k [count][keyHeads][keyDim] and v [count][valueHeads]
+    [valueDim] as numpy fp32 arrays or bf16 bit patterns (uint16); gates fp32;
+    state fp32 [valueHeads][keyDim][valueDim], updated in place. Returns out
+    [count][valueHeads][valueDim] fp32."""
+    import numpy as np
+
+    def host(x, dtype=np.float32):
+        return None if x is None else np.ascontiguousarray(x, dtype=dtype)
+
+    def addr(x):
+        return None if x is None else C.c_void_p(x.ctypes.data)
+
+    bf16 = np.asarray(q).dtype == np.uint16
+    in_type = np.uint16 if bf16 else np.float32
+    q, k, v = host(q, in_type), host(k, in_type), host(v, in_type)
+    g, beta, a, b, a_log, dt_bias = (host(x) for x in (g, beta, a, b, a_log, dt_bias))
+    if state.dtype != np.float32 or not state.flags["C_CONTIGUOUS"]:
+        raise TypeError("state must be a C-contiguous float32 array (updated in place)")
+    count, key_heads, key_dim = q.shape
+    _, value_heads, value_dim = v.shape
+    out = np.empty((count, value_heads, value_dim), np.float32)
+    args = AiGpuDeltaRule(q=addr(q), k=addr(k), v=addr(v), g=addr(g), beta=addr(beta), a=addr(a), b=addr(b),
+                          aLog=addr(a_log), dtBias=addr(dt_bias), state=addr(state), out=addr(out),
+                          inType=BF16 if bf16 else F32, normalize=1 if normalize else 0, chunk=64, count=count,
+                          keyHeads=key_heads, valueHeads=value_heads, keyDim=key_dim, valueDim=value_dim,
+                          stream=None)
+    _check(lib().aigpu_gated_delta_rule_host(C.byref(args)))
+    return out
+
+
 def gdn_conv(x, kernel, window, q, k, v, key_heads, value_heads, key_dim, value_dim, ba=None, z=None,
              a=None, b=None, stream=None):
     """Device form of gatedDeltaNetMixer's de-interleave + causalConvolution:

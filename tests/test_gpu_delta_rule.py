@@ -222,3 +222,33 @@ def test_bf16_two_level_continuation(gpu):
     assert n == 2
     assert_bf16_parity(whole, np.concatenate(parts), "two-level continuation out")
     assert_bf16_parity(host(whole_state), host(split_state), "two-level continuation state")
+
+
+@pytest.mark.parametrize("dtype,S,hk,hv", [("f32", 200, 2, 4), ("bf16", 4100, 16, 32)])
+def test_host_form(gpu, dtype, S, hk, hv):
+    """aigpu_gated_delta_rule_host, the entry the reference's mixer binds
+    (host arrays staged through the backend's scratch): the single-level fp32
+    scan, and the two-level scan for bf16 rows that the staging leaves on
+    16-byte boundaries"""
+    import aigpu
+    seed = 51 + S
+    if dtype == "bf16":
+        qb, q = bf16_normal((S, hk, 128), seed, "q")
+        kb, k = bf16_normal((S, hk, 128), seed, "k")
+        vb, v = bf16_normal((S, hv, 128), seed, "v")
+        args = (qb, kb, vb)
+    else:
+        q = O.fill_normal((S, hk, 128), seed, "q")
+        k = O.fill_normal((S, hk, 128), seed, "k")
+        v = O.fill_normal((S, hv, 128), seed, "v")
+        args = (q, k, v)
+    g, beta = gates(S, hv, seed)
+    s0 = O.fill_normal((hv, 128, 128), seed, "s0") * np.float32(0.1)
+    state = s0.copy()
+    say("delta rule host form", dict(S=S, hk=hk, hv=hv, dtype=dtype))
+    out, n = two_level_launches(lambda: aigpu.gated_delta_rule_host(*args, state, g=g, beta=beta))
+    assert n == (1 if dtype == "bf16" else 0)
+    ref_out, ref_state = O.gated_delta_rule(q, k, v, g, beta, state=s0, nthreads=0)
+    check = assert_f32_parity if dtype == "f32" else assert_bf16_parity
+    check(ref_out, out, f"host form out {dtype}")
+    check(ref_state, state, f"host form state {dtype}")
