@@ -384,6 +384,42 @@ def decode(q, k, v, out, key_cache, value_cache, positions, max_position, heads,
     return out
 
 
+def decode_host(q, k, v, key_cache, value_cache, positions, heads, kv_heads, dim, q_stride=None, q_norm=None,
+                k_norm=None, eps=1e-6, norm_offset=0.0, freqs=None, rotary_dims=0, window=0, capacity=None,
+                batch_stride=0, output_gate=False):
+    """Host form (aigpu_decode_attention_host): q [batch][heads][qStride], k,
+    v [batch][kvHeads][dim] as numpy fp32 arrays or bf16 bit patterns
+    (uint16), positions numpy uint32, norms and frequencies numpy fp32; the
+    caches stay device tensors. Returns out [batch][heads][dim] fp32."""
+    import numpy as np
+
+    def host(x, dtype=np.float32):
+        return None if x is None else np.ascontiguousarray(x, dtype=dtype)
+
+    def addr(x):
+        return None if x is None else C.c_void_p(x.ctypes.data)
+
+    for t, n in ((key_cache, "key_cache"), (value_cache, "value_cache")):
+        _need(t, n)
+    bf16 = np.asarray(q).dtype == np.uint16
+    in_type = np.uint16 if bf16 else np.float32
+    q, k, v = host(q, in_type), host(k, in_type), host(v, in_type)
+    positions = host(positions, np.uint32)
+    q_norm, k_norm, freqs = host(q_norm), host(k_norm), host(freqs)
+    batch = q.shape[0]
+    out = np.empty((batch, heads, dim), np.float32)
+    cap = capacity if capacity is not None else key_cache.shape[-2]
+    a = AiGpuDecode(q=addr(q), k=addr(k), v=addr(v), out=addr(out), keyCache=_ptr(key_cache),
+                    valueCache=_ptr(value_cache), positions=addr(positions), qNorm=addr(q_norm), kNorm=addr(k_norm),
+                    rotaryFrequencies=addr(freqs), epsilon=eps, normOffset=norm_offset,
+                    rotaryDims=rotary_dims if freqs is not None else 0, inType=BF16 if bf16 else F32,
+                    maxPosition=int(positions.max()), outputGate=1 if output_gate else 0, batch=batch, heads=heads,
+                    kvHeads=kv_heads, dim=dim, qStride=q_stride or dim, window=window, capacity=cap,
+                    batchStride=batch_stride, stream=None)
+    _check(lib().aigpu_decode_attention_host(C.byref(a)))
+    return out
+
+
 def gated_delta_rule(q, k, v, state, out, g=None, beta=None, a=None, b=None, a_log=None,
                      dt_bias=None, normalize=True, stream=None):
     """Device form of the gatedDeltaNetMixer recurrence; state updated in place."""

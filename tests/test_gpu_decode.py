@@ -158,3 +158,33 @@ def test_output_gate(gpu, lengths):
     kernel) and multi-chunk ones (merge kernel)"""
     ref, got = run_decode(gpu, lengths, 8, 2, 128, 91, q_stride=256, gate=True)
     assert_bf16_parity(ref, got, f"gate {lengths}")
+
+
+def test_host_form_matches_device_form(gpu):
+    """aigpu_decode_attention_host (host q/k/v, positions, norms, frequencies;
+    device caches) against the device form on the same inputs: the same
+    kernels run, so the outputs and both caches are bit-identical"""
+    import torch
+    lengths, H, KV, D, seed = [300, 1, 4096, 1500], 16, 8, 128, 61
+    B, cap = len(lengths), 4097
+    qb, _ = bf16_normal((B, H, D), seed, "q")
+    kb, _ = bf16_normal((B, KV, D), seed, "k")
+    vb, _ = bf16_normal((B, KV, D), seed, "v")
+    gq, gk = gammas(D, seed, "q_norm"), gammas(D, seed, "k_norm")
+    fr = O.rotary_frequencies(D, 1e6)
+    kc = np.zeros((B, KV, cap, D), np.uint16)
+    vc = np.zeros((B, KV, cap, D), np.uint16)
+    for b, L in enumerate(lengths):
+        kc[b, :, :L] = bf16_normal((KV, L, D), seed, f"k_cache{b}")[0]
+        vc[b, :, :L] = bf16_normal((KV, L, D), seed, f"v_cache{b}")[0]
+    pos = np.array(lengths, np.uint32)
+    say("decode host form", dict(B=B, H=H, KV=KV, D=D))
+    kd, vd = dev_bf16(kc), dev_bf16(vc)
+    out = torch.zeros((B, H, D), dtype=torch.float32, device="cuda")
+    gpu.decode(dev_bf16(qb), dev_bf16(kb), dev_bf16(vb), out, kd, vd, dev_u32(pos), max(lengths), H, KV, D,
+               q_norm=dev_f32(gq), k_norm=dev_f32(gk), freqs=dev_f32(fr), rotary_dims=D)
+    kh, vh = dev_bf16(kc), dev_bf16(vc)
+    got = gpu.decode_host(qb, kb, vb, kh, vh, pos, H, KV, D, q_norm=gq, k_norm=gk, freqs=fr, rotary_dims=D)
+    assert np.array_equal(got, host(out))
+    assert np.array_equal(host_bits(kh), host_bits(kd))
+    assert np.array_equal(host_bits(vh), host_bits(vd))
